@@ -1,0 +1,311 @@
+"""ctypes binding of the CPU oracle (oracle/liboracle.so).
+
+TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
+bench.py's CPU-baseline leg, always as the checker or the timed CPU
+baseline, never as a product path.  Function names follow the reference's
+(src/gemv.rs, src/talker.rs, src/code_predictor.rs, src/generate_new.rs).
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+import sys
+from typing import Optional
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_PKG = os.path.join(os.path.dirname(_HERE), "qora-tts-12hz-1.7b_amd")
+if _PKG not in sys.path:
+    sys.path.insert(0, _PKG)
+
+import qtts  # noqa: E402  (host weight containers and ctypes views)
+
+LIB_PATH = os.path.join(_HERE, "liboracle.so")
+_lib = None
+
+
+def _p(a):
+    return None if a is None else C.c_void_p(a.ctypes.data)
+
+
+def load():
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise RuntimeError(f"{LIB_PATH} is not built (make -C oracle)")
+    lib = C.CDLL(LIB_PATH)
+    vp, i32, u32 = C.c_void_p, C.c_int32, C.c_uint32
+    Q4P, TVP, PVP = C.POINTER(qtts.Q4View), C.POINTER(qtts.TalkerView), C.POINTER(qtts.PredictorView)
+    sig = {
+        "qor_available_parallelism": ([], i32),
+        "qor_f16_to_f32": ([C.c_uint16], C.c_float),
+        "qor_gemv": ([vp, Q4P, vp, i32], None),
+        "qor_gemm": ([vp, i32, Q4P, vp, i32], None),
+        "qor_embed_lookup": ([Q4P, i32, vp], None),
+        "qor_rms_norm_f16": ([vp, vp, i32, vp], None),
+        "qor_softmax_raw": ([vp, i32], None),
+        "qor_silu": ([C.c_float], C.c_float),
+        "qor_qk_norm": ([vp, i32, i32, vp], None),
+        "qor_build_rope_table": ([i32, i32, C.c_double, vp, vp], None),
+        "qor_rope_split": ([vp, i32, i32, i32, vp, vp], None),
+        "qor_kv_new": ([i32, i32, i32, i32], vp),
+        "qor_kv_free": ([vp], None),
+        "qor_kv_len": ([vp], i32),
+        "qor_kv_clear": ([vp], None),
+        "qor_kv_load": ([vp, vp, vp, i32], i32),
+        "qor_kv_store": ([vp, vp, vp], i32),
+        "qor_talker_new": ([TVP], vp),
+        "qor_talker_free": ([vp], None),
+        "qor_forward_with_embedding": ([vp, vp, vp, i32, vp, i32], i32),
+        "qor_prefill_talker_raw": ([vp, vp, i32, vp, vp, i32], i32),
+        "qor_apply_codec_head": ([vp, vp, vp, i32], None),
+        "qor_embed_codec_token": ([vp, u32, vp], None),
+        "qor_predictor_new": ([PVP], vp),
+        "qor_predictor_free": ([vp], None),
+        "qor_generate_acoustic_codes": ([vp, vp, vp, vp, vp, i32], i32),
+        "qor_get_acoustic_embeddings_sum": ([vp, vp, vp], None),
+        "qor_simple_rand": ([C.POINTER(C.c_uint64)], C.c_float),
+        "qor_argmax": ([vp, i32, C.POINTER(u32)], i32),
+        "qor_sample_token": ([vp, i32, C.POINTER(qtts.SamplerParams), vp, i32, C.POINTER(C.c_uint64),
+                              C.POINTER(u32)], i32),
+        "qor_generate_codes": ([vp, vp, vp, vp, vp, vp, i32, vp, i32, vp, C.POINTER(qtts.LoopParams), C.c_uint64,
+                                vp, C.POINTER(i32), i32], i32),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    _lib = lib
+    return lib
+
+
+class OracleError(RuntimeError):
+    def __init__(self, status: int):
+        self.status = status
+        super().__init__(f"oracle status {qtts.STATUS_NAMES[status]}")
+
+
+def _check(st: int):
+    if st != 0:
+        raise OracleError(st)
+
+
+def f32(a, n=None):
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    if n is not None:
+        assert a.size >= n
+    return a
+
+
+# --- src/gemv.rs ------------------------------------------------------------
+def gemv(x, w: "qtts.Q4Weight", nthreads: int = 0) -> np.ndarray:
+    x = f32(x, w.k)
+    y = np.empty(w.n, dtype=np.float32)
+    v = w.view()
+    load().qor_gemv(_p(x), C.byref(v), _p(y), nthreads)
+    return y
+
+
+def gemm(x, seq_len: int, w: "qtts.Q4Weight", nthreads: int = 0) -> np.ndarray:
+    x = f32(x, seq_len * w.k)
+    y = np.empty(seq_len * w.n, dtype=np.float32)
+    v = w.view()
+    load().qor_gemm(_p(x), seq_len, C.byref(v), _p(y), nthreads)
+    return y
+
+
+def embed_lookup(w: "qtts.Q4Weight", token: int) -> np.ndarray:
+    y = np.empty(w.n, dtype=np.float32)
+    v = w.view()
+    load().qor_embed_lookup(C.byref(v), token, _p(y))
+    return y
+
+
+def rms_norm_f16(x, gamma_f16_bits) -> np.ndarray:
+    x = f32(x)
+    g = np.ascontiguousarray(gamma_f16_bits, dtype=np.uint16)
+    y = np.empty_like(x)
+    load().qor_rms_norm_f16(_p(x), _p(g), x.size, _p(y))
+    return y
+
+
+def softmax_raw(s) -> np.ndarray:
+    s = f32(s).copy()
+    load().qor_softmax_raw(_p(s), s.size)
+    return s
+
+
+def silu(x: float) -> float:
+    return float(load().qor_silu(x))
+
+
+def qk_norm(data, num_heads: int, head_dim: int, gamma_f16_bits) -> np.ndarray:
+    d = f32(data).copy()
+    g = np.ascontiguousarray(gamma_f16_bits, dtype=np.uint16)
+    load().qor_qk_norm(_p(d), num_heads, head_dim, _p(g))
+    return d
+
+
+def build_rope_table(head_dim: int, max_pos: int, theta: float):
+    half = head_dim // 2
+    c = np.empty(max_pos * half, dtype=np.float32)
+    s = np.empty(max_pos * half, dtype=np.float32)
+    load().qor_build_rope_table(head_dim, max_pos, theta, _p(c), _p(s))
+    return c.reshape(max_pos, half), s.reshape(max_pos, half)
+
+
+def rope_split(data, num_heads: int, head_dim: int, pos: int, cos_t, sin_t) -> np.ndarray:
+    d = f32(data).copy()
+    load().qor_rope_split(_p(d), num_heads, head_dim, pos, _p(f32(cos_t)), _p(f32(sin_t)))
+    return d
+
+
+def f16_to_f32(h: int) -> float:
+    return float(load().qor_f16_to_f32(h))
+
+
+def available_parallelism() -> int:
+    return int(load().qor_available_parallelism())
+
+
+# --- src/generate_new.rs ----------------------------------------------------
+def simple_rand(state: int):
+    st = C.c_uint64(state)
+    r = load().qor_simple_rand(C.byref(st))
+    return float(r), int(st.value)
+
+
+def argmax(logits):
+    lg = f32(logits)
+    out = C.c_uint32(0)
+    _check(load().qor_argmax(_p(lg), lg.size, C.byref(out)))
+    return int(out.value)
+
+
+def sample_token(logits, temperature=0.8, top_k=50, repetition_penalty=1.05, prev_tokens=(0,) * 16, rng=0,
+                 greedy=False):
+    lg = f32(logits)
+    prev = np.ascontiguousarray(prev_tokens, dtype=np.uint32)
+    p = qtts.SamplerParams(temperature, top_k, repetition_penalty, 1 if greedy else 0)
+    st = C.c_uint64(rng)
+    tok = C.c_uint32(0)
+    _check(load().qor_sample_token(_p(lg), lg.size, C.byref(p), _p(prev), prev.size, C.byref(st), C.byref(tok)))
+    return int(tok.value), int(st.value)
+
+
+# --- KV, talker, predictor --------------------------------------------------
+class Kv:
+    def __init__(self, num_layers, num_kv_heads, head_dim, capacity):
+        self.shape = (num_layers, num_kv_heads, head_dim)
+        self.h = load().qor_kv_new(num_layers, num_kv_heads, head_dim, capacity)
+
+    def __len__(self):
+        return int(load().qor_kv_len(self.h))
+
+    def clear(self):
+        load().qor_kv_clear(self.h)
+
+    def load(self, k, v, length):
+        _check(load().qor_kv_load(self.h, _p(f32(k)), _p(f32(v)), length))
+
+    def store(self):
+        L, H, D = self.shape
+        n = len(self)
+        k = np.empty((L, n, H, D), dtype=np.float32)
+        v = np.empty_like(k)
+        _check(load().qor_kv_store(self.h, _p(k), _p(v)))
+        return k, v
+
+    def __del__(self):
+        try:
+            load().qor_kv_free(self.h)
+        except Exception:
+            pass
+
+
+class Talker:
+    def __init__(self, w: "qtts.TalkerWeights", nthreads: int = 0):
+        self.w, self.cfg, self.nthreads = w, w.cfg, nthreads
+        self._view = w.view()
+        self.h = load().qor_talker_new(C.byref(self._view))
+
+    def new_kv(self, capacity):
+        c = self.cfg
+        return Kv(c.layers, c.kv_heads, c.head_dim, capacity)
+
+    def forward_with_embedding(self, embedding, kv: Kv, position: int) -> np.ndarray:
+        e = f32(embedding, self.cfg.hidden)
+        out = np.empty(self.cfg.hidden + self.cfg.vocab, dtype=np.float32)
+        _check(load().qor_forward_with_embedding(self.h, _p(e), kv.h, position, _p(out), self.nthreads))
+        return out
+
+    def prefill_talker_raw(self, x, seq_len: int, kv: Kv) -> np.ndarray:
+        x = f32(x, seq_len * self.cfg.hidden)
+        out = np.empty(self.cfg.hidden, dtype=np.float32)
+        _check(load().qor_prefill_talker_raw(self.h, _p(x), seq_len, kv.h, _p(out), self.nthreads))
+        return out
+
+    def apply_codec_head(self, hidden) -> np.ndarray:
+        out = np.empty(self.cfg.vocab, dtype=np.float32)
+        load().qor_apply_codec_head(self.h, _p(f32(hidden)), _p(out), self.nthreads)
+        return out
+
+    def embed_codec_token(self, token: int) -> np.ndarray:
+        out = np.empty(self.cfg.hidden, dtype=np.float32)
+        load().qor_embed_codec_token(self.h, token, _p(out))
+        return out
+
+    def __del__(self):
+        try:
+            load().qor_talker_free(self.h)
+        except Exception:
+            pass
+
+
+class CodePredictor:
+    def __init__(self, w: "qtts.CodePredictorWeights", nthreads: int = 0):
+        self.w, self.cfg, self.nthreads = w, w.cfg, nthreads
+        self.num_groups, self.talker_hidden = w.num_groups, w.talker_hidden
+        self._view = w.view()
+        self.h = load().qor_predictor_new(C.byref(self._view))
+
+    def new_kv(self, capacity=16):
+        c = self.cfg
+        return Kv(c.layers, c.kv_heads, c.head_dim, capacity)
+
+    def generate_acoustic_codes(self, talker_hidden, semantic_embed, kv: Kv) -> np.ndarray:
+        codes = np.empty(self.num_groups, dtype=np.uint32)
+        _check(load().qor_generate_acoustic_codes(self.h, _p(f32(talker_hidden)), _p(f32(semantic_embed)), kv.h,
+                                                  _p(codes), self.nthreads))
+        return codes
+
+    def get_acoustic_embeddings_sum(self, codes) -> np.ndarray:
+        cs = np.ascontiguousarray(codes, dtype=np.uint32)
+        out = np.empty(self.talker_hidden, dtype=np.float32)
+        load().qor_get_acoustic_embeddings_sum(self.h, _p(cs), _p(out))
+        return out
+
+    def __del__(self):
+        try:
+            load().qor_predictor_free(self.h)
+        except Exception:
+            pass
+
+
+def generate_codes(talker: Talker, predictor: Optional[CodePredictor], talker_kv: Kv, predictor_kv: Optional[Kv],
+                   last_hidden, logits, position: int, trailing_text, tts_pad_embed, params: "qtts.LoopParams",
+                   seed: int, nthreads: int = 0) -> np.ndarray:
+    hidden = talker.cfg.hidden
+    tt = None if trailing_text is None else f32(trailing_text).reshape(-1, hidden)
+    tl = 0 if tt is None else tt.shape[0]
+    pad = None if tts_pad_embed is None else f32(tts_pad_embed)
+    codes = np.zeros((16, max(params.max_codes, 1)), dtype=np.uint32)
+    n = C.c_int32(0)
+    _check(load().qor_generate_codes(talker.h, predictor.h if predictor is not None else None, talker_kv.h,
+                                     predictor_kv.h if predictor_kv is not None else None, _p(f32(last_hidden)), _p(f32(logits)),
+                                     position, _p(tt), tl, _p(pad), C.byref(params), seed, _p(codes), C.byref(n),
+                                     nthreads))
+    return codes[:, : n.value].copy()

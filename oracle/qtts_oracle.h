@@ -1,0 +1,115 @@
+/*
+ * qtts_oracle.h — CPU restatement of the reference's per-code loop.
+ *
+ * TEST INFRASTRUCTURE ONLY.  This is the checker the parity tests compare
+ * the HIP library against, and the CPU baseline bench.py times.  Nothing in
+ * the product library links, loads or calls it.
+ *
+ * It restates the arithmetic ORDER of the reference Rust crate (qora-tts
+ * 0.1.0): the LUT GEMV with its k*n >= 4e6 split-K thread fan-out, sequential
+ * f32 sums, glibc expf/sqrtf, RoPE tables built in double and cast to float.
+ * Built with -O3 -ffp-contract=off (no -march), as rustc would compile the
+ * crate for the default x86-64 target: no FMA contraction, no reassociation.
+ */
+#ifndef QTTS_ORACLE_H
+#define QTTS_ORACLE_H
+
+#include <stdint.h>
+
+#include "../include/qtts.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* std::thread::available_parallelism(): affinity mask, capped by a cgroup
+ * CPU quota when one is set. */
+int32_t qor_available_parallelism(void);
+
+float qor_f16_to_f32(uint16_t h);
+
+/* --- src/gemv.rs ---------------------------------------------------------- */
+/* gemv_q4, src/gemv.rs:263-309.  nthreads = the value available_parallelism()
+ * would return (<= 0: detect); it only matters when k*n >= 4e6. */
+void qor_gemv(const float *input, const qtts_q4_view *w, float *out, int32_t nthreads);
+/* gemm_q4, src/gemv.rs:311-375 (row results do not depend on nthreads). */
+void qor_gemm(const float *x, int32_t seq_len, const qtts_q4_view *w, float *out, int32_t nthreads);
+/* embed_lookup_q4, src/gemv.rs:377-400. */
+void qor_embed_lookup(const qtts_q4_view *w, int32_t token_id, float *out);
+/* rms_norm_f16, src/gemv.rs:406-417. */
+void qor_rms_norm_f16(const float *x, const uint16_t *gamma, int32_t n, float *out);
+/* softmax_raw, src/gemv.rs:433-445. */
+void qor_softmax_raw(float *scores, int32_t n);
+/* silu, src/gemv.rs:447-451. */
+float qor_silu(float x);
+/* apply_qk_norm, src/talker.rs:86-99 (= src/code_predictor.rs:84-93). */
+void qor_qk_norm(float *data, int32_t num_heads, int32_t head_dim, const uint16_t *gamma);
+
+/* --- src/rope.rs ---------------------------------------------------------- */
+/* build_mrope_tables, src/rope.rs:11-41 (sections are contiguous, so this is
+ * also the predictor table of src/loader.rs:859-874). */
+void qor_build_rope_table(int32_t head_dim, int32_t max_pos, double theta, float *cos_table, float *sin_table);
+/* Split-half rotation at one position: apply_mrope_interleaved with
+ * position_ids = [p,p,p] (src/rope.rs:50-93) and apply_rope_split
+ * (src/code_predictor.rs:97-121). */
+void qor_rope_split(float *data, int32_t num_heads, int32_t head_dim, int32_t pos, const float *cos_table,
+                    const float *sin_table);
+
+/* --- KV cache: RawKvCache, src/gemv.rs:75-86 (token-major f32) ----------- */
+typedef struct qor_kv qor_kv;
+qor_kv *qor_kv_new(int32_t num_layers, int32_t num_kv_heads, int32_t head_dim, int32_t capacity);
+void qor_kv_free(qor_kv *kv);
+int32_t qor_kv_len(const qor_kv *kv);
+void qor_kv_clear(qor_kv *kv);
+/* k/v are [layer][len][kv_heads][head_dim]. */
+int32_t qor_kv_load(qor_kv *kv, const float *k, const float *v, int32_t len);
+int32_t qor_kv_store(const qor_kv *kv, float *k, float *v);
+
+/* --- src/talker.rs -------------------------------------------------------- */
+typedef struct qor_talker qor_talker;
+/* Keeps a copy of the view (the arrays it points to must outlive it) and
+ * builds the RoPE table, as load_talker does (src/loader.rs:768-775). */
+qor_talker *qor_talker_new(const qtts_talker_view *w);
+void qor_talker_free(qor_talker *t);
+/* forward_with_embedding, src/talker.rs:263-360.  out = [hidden ++ logits]. */
+int32_t qor_forward_with_embedding(const qor_talker *t, const float *embedding, qor_kv *kv, int32_t position,
+                                   float *out, int32_t nthreads);
+/* prefill_talker_raw, src/talker.rs:364-462. */
+int32_t qor_prefill_talker_raw(const qor_talker *t, const float *x, int32_t seq_len, qor_kv *kv,
+                               float *last_hidden, int32_t nthreads);
+/* apply_codec_head, src/talker.rs:627-629. */
+void qor_apply_codec_head(const qor_talker *t, const float *hidden, float *logits, int32_t nthreads);
+/* embed_codec_token, src/talker.rs:152-154. */
+void qor_embed_codec_token(const qor_talker *t, uint32_t token_id, float *out);
+
+/* --- src/code_predictor.rs ----------------------------------------------- */
+typedef struct qor_predictor qor_predictor;
+qor_predictor *qor_predictor_new(const qtts_predictor_view *w);
+void qor_predictor_free(qor_predictor *p);
+/* generate_acoustic_codes, src/code_predictor.rs:218-273. */
+int32_t qor_generate_acoustic_codes(const qor_predictor *p, const float *talker_hidden, const float *semantic_embed,
+                                    qor_kv *kv, uint32_t *codes, int32_t nthreads);
+/* get_acoustic_embeddings_sum, src/code_predictor.rs:280-293. */
+void qor_get_acoustic_embeddings_sum(const qor_predictor *p, const uint32_t *codes, float *out);
+
+/* --- src/generate_new.rs ------------------------------------------------- */
+/* simple_rand, src/generate_new.rs:17-22. */
+float qor_simple_rand(uint64_t *state);
+/* sample_argmax, src/code_predictor.rs:328-334: last index wins ties.
+ * Returns QTTS_ENAN where the reference panics. */
+int32_t qor_argmax(const float *logits, int32_t n, uint32_t *out);
+/* sample_token, src/generate_new.rs:329-391 (greedy: argmax after penalty). */
+int32_t qor_sample_token(const float *logits, int32_t vocab, const qtts_sampler *params, const uint32_t *prev_tokens,
+                         int32_t n_prev, uint64_t *rng, uint32_t *token);
+/* The frame loop of generate_speech, src/generate_new.rs:229-300. */
+int32_t qor_generate_codes(const qor_talker *t, const qor_predictor *p, qor_kv *talker_kv, qor_kv *predictor_kv,
+                           const float *last_hidden, const float *logits, int32_t position,
+                           const float *trailing_text, int32_t trailing_len, const float *tts_pad_embed,
+                           const qtts_loop_params *params, uint64_t seed, uint32_t *codes, int32_t *n_frames,
+                           int32_t nthreads);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QTTS_ORACLE_H */

@@ -1,0 +1,1236 @@
+// api.cpp — host runtime behind the C-ABI (include/qtts.h): contexts, weight
+// upload + repack, the device KV arena, and the enqueue sequences of the
+// talker step, the predictor frame and the frame loop (replayed as a HIP
+// graph).  Host code; every kernel it launches lives in kernels.hip.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstdlib>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../include/qtts.h"
+#include "../../include/qtts_synth.h"
+#include "internal.h"
+
+using namespace qtts;
+
+namespace {
+
+constexpr size_t kPartialFloats = (size_t)1 << 20;  // split-K partials
+constexpr int kCounters = 8192;
+constexpr size_t kAttnPartFloats = (size_t)4 << 20;
+constexpr int kAttnCounters = 1024;
+
+}  // namespace
+
+struct qtts_ctx {
+    int device = 0;
+    hipStream_t stream = nullptr;
+    std::string err;
+    float *partial = nullptr;
+    unsigned *counters = nullptr;
+    float *attn_part = nullptr;
+    unsigned *attn_counters = nullptr;
+    // staging for the stand-alone operators
+    float *d_in = nullptr;
+    size_t d_in_cap = 0;
+    float *d_out = nullptr;
+    size_t d_out_cap = 0;
+    uint32_t *d_small = nullptr;  // tokens, prev tokens, status, rng (256 B)
+};
+
+struct qtts_q4 {
+    qtts_ctx *ctx = nullptr;
+    DevQ4 d{};
+    void *mem = nullptr;
+    size_t bytes = 0;
+};
+
+struct qtts_kv {
+    qtts_ctx *ctx = nullptr;
+    int layers = 0, kvh = 0, hd = 0, cap = 0, len = 0;
+    float *k = nullptr, *v = nullptr;  // [layer][kvh][cap][hd]
+    float *layer_k(int l) const { return k + (size_t)l * kvh * cap * hd; }
+    float *layer_v(int l) const { return v + (size_t)l * kvh * cap * hd; }
+};
+
+namespace {
+
+struct DevLayer {
+    DevQ4 qkv{}, o{}, gu{}, down{};
+    uint16_t *q_norm = nullptr, *k_norm = nullptr, *in_g = nullptr, *post_g = nullptr;
+};
+
+struct Stack {  // shapes shared by the talker and predictor layer stacks
+    int layers = 0, hidden = 0, nq = 0, nkv = 0, hd = 0, inter = 0;
+    std::vector<DevLayer> L;
+    uint16_t *final_g = nullptr;
+    float *rope_cos = nullptr, *rope_sin = nullptr;
+    int rope_rows = 0;
+    int rope_skip_oob = 0;
+};
+
+qtts_status fail(qtts_ctx *c, qtts_status s, const std::string &m) {
+    if (c) c->err = m;
+    return s;
+}
+
+#define HIP_TRY(ctx, expr)                                                                   \
+    do {                                                                                     \
+        hipError_t e_ = (expr);                                                              \
+        if (e_ != hipSuccess)                                                                \
+            return fail((ctx), QTTS_EDEVICE, std::string(#expr) + ": " + hipGetErrorString(e_)); \
+    } while (0)
+
+#define QTTS_TRY(expr)                     \
+    do {                                   \
+        qtts_status s_ = (expr);           \
+        if (s_ != QTTS_OK) return s_;      \
+    } while (0)
+
+qtts_status check_launch(qtts_ctx *c, const char *what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(c, QTTS_EDEVICE, std::string(what) + ": " + hipGetErrorString(e));
+    return QTTS_OK;
+}
+
+// Owns device allocations of a model object.
+struct Owner {
+    std::vector<void *> ptrs;
+    ~Owner() {
+        for (void *p : ptrs) (void)hipFree(p);
+    }
+    template <class T>
+    qtts_status alloc(qtts_ctx *c, T **out, size_t count) {
+        void *p = nullptr;
+        hipError_t e = hipMalloc(&p, count * sizeof(T) > 0 ? count * sizeof(T) : 1);
+        if (e != hipSuccess) return fail(c, QTTS_ENOMEM, std::string("hipMalloc: ") + hipGetErrorString(e));
+        ptrs.push_back(p);
+        *out = reinterpret_cast<T *>(p);
+        return QTTS_OK;
+    }
+};
+
+qtts_status check_view(qtts_ctx *c, const qtts_q4_view *v, int K, int N, const char *name) {
+    if (!v || !v->packed || !v->scales) return fail(c, QTTS_EINVAL, std::string(name) + ": null weight");
+    if (v->k != K || v->n != N || N % 32 != 0 || K <= 0)
+        return fail(c, QTTS_ESHAPE, std::string(name) + ": shape " + std::to_string(v->k) + "x" +
+                                        std::to_string(v->n) + ", expected " + std::to_string(K) + "x" +
+                                        std::to_string(N));
+    return QTTS_OK;
+}
+
+qtts_status alloc_q4(qtts_ctx *c, Owner &own, int K, int N, DevQ4 *d) {
+    uint8_t *mem = nullptr;
+    const size_t wbytes = (size_t)K * N / 2, sbytes = (size_t)K * (N / 32) * 2;
+    QTTS_TRY(own.alloc(c, &mem, wbytes + sbytes));
+    d->wq = reinterpret_cast<const uint4 *>(mem);
+    d->ws = reinterpret_cast<const uint16_t *>(mem + wbytes);
+    d->K = K;
+    d->N = N;
+    return QTTS_OK;
+}
+
+// Uploads one reference-layout weight into columns [col0, col0+n) of d.
+qtts_status upload_part(qtts_ctx *c, const qtts_q4_view *v, const DevQ4 &d, int col0) {
+    const size_t pb = (size_t)v->k * v->n / 2, sb = (size_t)v->k * (v->n / 32) * 2;
+    uint8_t *stage = nullptr;
+    HIP_TRY(c, hipMalloc(&stage, pb + sb));
+    hipError_t e = hipMemcpyAsync(stage, v->packed, pb, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) e = hipMemcpyAsync(stage + pb, v->scales, sb, hipMemcpyHostToDevice, c->stream);
+    if (e == hipSuccess) {
+        launch_repack_q4(c->stream, stage, reinterpret_cast<const uint16_t *>(stage + pb), v->k, v->n, col0, d.N,
+                         const_cast<uint4 *>(d.wq), const_cast<uint16_t *>(d.ws));
+        e = hipGetLastError();
+    }
+    if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+    (void)hipFree(stage);
+    if (e != hipSuccess) return fail(c, QTTS_EDEVICE, std::string("weight upload: ") + hipGetErrorString(e));
+    return QTTS_OK;
+}
+
+template <class T>
+qtts_status upload_array(qtts_ctx *c, Owner &own, const T *src, size_t count, T **dst, const char *name) {
+    if (!src) return fail(c, QTTS_EINVAL, std::string(name) + ": null");
+    QTTS_TRY(own.alloc(c, dst, count));
+    HIP_TRY(c, hipMemcpy(*dst, src, count * sizeof(T), hipMemcpyHostToDevice));
+    return QTTS_OK;
+}
+
+// RoPE table exactly as build_mrope_tables (src/rope.rs:11-41) and the
+// predictor table (src/loader.rs:859-874): double pow/cos/sin, cast to float.
+qtts_status upload_rope(qtts_ctx *c, Owner &own, int head_dim, int rows, double theta, Stack *st) {
+    const int half = head_dim / 2;
+    std::vector<float> cs((size_t)rows * half), sn((size_t)rows * half);
+    for (int i = 0; i < half; i++) {
+        const double freq = 1.0 / std::pow(theta, (double)(2 * i) / (double)head_dim);
+        for (int pos = 0; pos < rows; pos++) {
+            const double angle = (double)pos * freq;
+            cs[(size_t)pos * half + i] = (float)std::cos(angle);
+            sn[(size_t)pos * half + i] = (float)std::sin(angle);
+        }
+    }
+    QTTS_TRY(upload_array(c, own, cs.data(), cs.size(), &st->rope_cos, "rope cos"));
+    QTTS_TRY(upload_array(c, own, sn.data(), sn.size(), &st->rope_sin, "rope sin"));
+    st->rope_rows = rows;
+    return QTTS_OK;
+}
+
+qtts_status upload_stack(qtts_ctx *c, Owner &own, int num_layers, const qtts_layer_view *layers, int hidden,
+                         int nq, int nkv, int hd, Stack *st) {
+    if (!layers || num_layers <= 0) return fail(c, QTTS_EINVAL, "no layers");
+    if (hd != 128) return fail(c, QTTS_ESHAPE, "head_dim must be 128");
+    if (nkv <= 0 || nq % nkv != 0 || nq / nkv > 4) return fail(c, QTTS_ESHAPE, "unsupported GQA grouping");
+    const int inter = layers[0].gate_proj.n;
+    st->layers = num_layers;
+    st->hidden = hidden;
+    st->nq = nq;
+    st->nkv = nkv;
+    st->hd = hd;
+    st->inter = inter;
+    st->L.resize(num_layers);
+    const int qd = nq * hd, kd = nkv * hd;
+    for (int l = 0; l < num_layers; l++) {
+        const qtts_layer_view &v = layers[l];
+        DevLayer &d = st->L[l];
+        QTTS_TRY(check_view(c, &v.q_proj, hidden, qd, "q_proj"));
+        QTTS_TRY(check_view(c, &v.k_proj, hidden, kd, "k_proj"));
+        QTTS_TRY(check_view(c, &v.v_proj, hidden, kd, "v_proj"));
+        QTTS_TRY(check_view(c, &v.o_proj, qd, hidden, "o_proj"));
+        QTTS_TRY(check_view(c, &v.gate_proj, hidden, inter, "gate_proj"));
+        QTTS_TRY(check_view(c, &v.up_proj, hidden, inter, "up_proj"));
+        QTTS_TRY(check_view(c, &v.down_proj, inter, hidden, "down_proj"));
+        // q|k|v and gate|up are concatenated along N: both splits fall on
+        // 32-column scale-group boundaries, so every column's K-sum is the
+        // reference's own.
+        QTTS_TRY(alloc_q4(c, own, hidden, qd + 2 * kd, &d.qkv));
+        QTTS_TRY(upload_part(c, &v.q_proj, d.qkv, 0));
+        QTTS_TRY(upload_part(c, &v.k_proj, d.qkv, qd));
+        QTTS_TRY(upload_part(c, &v.v_proj, d.qkv, qd + kd));
+        QTTS_TRY(alloc_q4(c, own, qd, hidden, &d.o));
+        QTTS_TRY(upload_part(c, &v.o_proj, d.o, 0));
+        QTTS_TRY(alloc_q4(c, own, hidden, 2 * inter, &d.gu));
+        QTTS_TRY(upload_part(c, &v.gate_proj, d.gu, 0));
+        QTTS_TRY(upload_part(c, &v.up_proj, d.gu, inter));
+        QTTS_TRY(alloc_q4(c, own, inter, hidden, &d.down));
+        QTTS_TRY(upload_part(c, &v.down_proj, d.down, 0));
+        QTTS_TRY(upload_array(c, own, v.q_norm, (size_t)hd, &d.q_norm, "q_norm"));
+        QTTS_TRY(upload_array(c, own, v.k_norm, (size_t)hd, &d.k_norm, "k_norm"));
+        QTTS_TRY(upload_array(c, own, v.input_norm_gamma, (size_t)hidden, &d.in_g, "input_norm_gamma"));
+        QTTS_TRY(upload_array(c, own, v.post_attn_norm_gamma, (size_t)hidden, &d.post_g, "post_attn_norm_gamma"));
+    }
+    return QTTS_OK;
+}
+
+GemvParams gemv_base(qtts_ctx *c, const DevQ4 &w, int M) {
+    GemvParams p{};
+    p.w = w;
+    p.M = M;
+    plan_gemv(w.K, w.N, M, &p.kc, &p.rpt);
+    p.partial = c->partial;
+    p.counters = c->counters;
+    return p;
+}
+
+qtts_status run_gemv(qtts_ctx *c, const GemvParams &p) {
+    if ((size_t)p.kc * p.M * p.w.N > kPartialFloats || p.w.N / 32 + 1 > kCounters)
+        return fail(c, QTTS_ESHAPE, "GEMV too large for the partial buffer");
+    if (p.M < 1 || p.M > kMaxM) return fail(c, QTTS_EINVAL, "GEMV rows per launch out of range");
+    launch_gemv(c->stream, p);
+    return check_launch(c, "k_gemv");
+}
+
+int attn_nsplit(int cap, int min_split) {
+    int n = (cap + kAttnMaxChunk - 1) / kAttnMaxChunk;
+    if (n < min_split) n = min_split;
+    return n;
+}
+
+// One layer stack over M rows: QKV (RMSNorm prologue; QK-norm, RoPE and KV
+// append epilogue) -> attention -> O (+residual) -> gate|up (RMSNorm
+// prologue, SiLU*up epilogue) -> down (+residual).  Positions and cache rows
+// come from d_pos/d_kvlen when given (graph replay), else the constants.
+qtts_status enqueue_layers(qtts_ctx *c, const Stack &st, qtts_kv *kv, float *x, float *q, float *attn, float *h,
+                           int M, const int *d_pos, int pos_const, const int *d_kvlen, int kvlen_const, int nsplit,
+                           const int *d_done) {
+    const int qd = st.nq * st.hd;
+    for (int l = 0; l < st.layers; l++) {
+        const DevLayer &Ly = st.L[l];
+        float *kc = kv->layer_k(l), *vc = kv->layer_v(l);
+        GemvParams p = gemv_base(c, Ly.qkv, M);
+        p.prologue = PRO_RMSNORM;
+        p.x = x;
+        p.ldx = st.hidden;
+        p.gamma = Ly.in_g;
+        p.epilogue = EPI_QKV;
+        p.y = q;
+        p.ldy = qd;
+        p.n_q_heads = st.nq;
+        p.n_kv_heads = st.nkv;
+        p.head_dim = st.hd;
+        p.q_norm = Ly.q_norm;
+        p.k_norm = Ly.k_norm;
+        p.rope_cos = st.rope_cos;
+        p.rope_sin = st.rope_sin;
+        p.rope_rows = st.rope_rows;
+        p.rope_skip_oob = st.rope_skip_oob;
+        p.kcache = kc;
+        p.vcache = vc;
+        p.kv_cap = kv->cap;
+        p.d_pos = d_pos;
+        p.pos_const = pos_const;
+        p.d_kvlen = d_kvlen;
+        p.kvlen_const = kvlen_const;
+        p.d_done = d_done;
+        QTTS_TRY(run_gemv(c, p));
+
+        AttnParams a{};
+        a.q = q;
+        a.ldq = qd;
+        a.kcache = kc;
+        a.vcache = vc;
+        a.kv_cap = kv->cap;
+        a.nq = st.nq;
+        a.nkv = st.nkv;
+        a.hd = st.hd;
+        a.d_kvlen = d_kvlen;
+        a.kvlen_const = kvlen_const;
+        a.nsplit = nsplit;
+        a.scale = 1.0f / sqrtf((float)st.hd);  // src/talker.rs:305
+        a.part = c->attn_part;
+        a.counters = c->attn_counters;
+        a.out = attn;
+        a.ldo = qd;
+        a.d_done = d_done;
+        if ((size_t)M * st.nq * nsplit * (st.hd + 2) > kAttnPartFloats || M * st.nkv > kAttnCounters)
+            return fail(c, QTTS_ESHAPE, "attention split buffer too small");
+        launch_attention(c->stream, a, M);
+        QTTS_TRY(check_launch(c, "k_attn"));
+
+        p = gemv_base(c, Ly.o, M);
+        p.prologue = PRO_PLAIN;
+        p.x = attn;
+        p.ldx = qd;
+        p.epilogue = EPI_RESID;
+        p.y = x;
+        p.ldy = st.hidden;
+        p.d_done = d_done;
+        QTTS_TRY(run_gemv(c, p));
+
+        p = gemv_base(c, Ly.gu, M);
+        p.prologue = PRO_RMSNORM;
+        p.x = x;
+        p.ldx = st.hidden;
+        p.gamma = Ly.post_g;
+        p.epilogue = EPI_SWIGLU;
+        p.y = h;
+        p.ldy = st.inter;
+        p.d_done = d_done;
+        QTTS_TRY(run_gemv(c, p));
+
+        p = gemv_base(c, Ly.down, M);
+        p.prologue = PRO_PLAIN;
+        p.x = h;
+        p.ldx = st.inter;
+        p.epilogue = EPI_RESID;
+        p.y = x;
+        p.ldy = st.hidden;
+        p.d_done = d_done;
+        QTTS_TRY(run_gemv(c, p));
+    }
+    return QTTS_OK;
+}
+
+qtts_status ensure_staging(qtts_ctx *c, size_t in_floats, size_t out_floats) {
+    if (in_floats > c->d_in_cap) {
+        if (c->d_in) (void)hipFree(c->d_in);
+        c->d_in = nullptr;
+        c->d_in_cap = 0;
+        HIP_TRY(c, hipMalloc(&c->d_in, in_floats * sizeof(float)));
+        c->d_in_cap = in_floats;
+    }
+    if (out_floats > c->d_out_cap) {
+        if (c->d_out) (void)hipFree(c->d_out);
+        c->d_out = nullptr;
+        c->d_out_cap = 0;
+        HIP_TRY(c, hipMalloc(&c->d_out, out_floats * sizeof(float)));
+        c->d_out_cap = out_floats;
+    }
+    return QTTS_OK;
+}
+
+qtts_status sync(qtts_ctx *c) {
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    return check_launch(c, "stream");
+}
+
+}  // namespace
+
+// ===========================================================================
+// Model objects
+// ===========================================================================
+struct qtts_talker {
+    qtts_ctx *ctx = nullptr;
+    Owner own;
+    Stack st;
+    int vocab = 0, max_pos = 0, nsplit = 16;
+    DevQ4 head{}, emb{};
+    float *x = nullptr, *q = nullptr, *attn = nullptr, *h = nullptr, *out = nullptr;
+    LoopState *state = nullptr;
+    // prefill work buffers
+    float *xp = nullptr, *qp = nullptr, *ap = nullptr, *hp = nullptr;
+    int prefill_cap = 0;
+    std::vector<void *> prefill_bufs;
+    // loop buffers
+    uint32_t *codes = nullptr;
+    size_t codes_cap = 0;
+    float *trailing = nullptr;
+    size_t trailing_cap = 0;
+    float *pad = nullptr;
+    ~qtts_talker() {
+        for (void *p : prefill_bufs) (void)hipFree(p);
+        if (codes) (void)hipFree(codes);
+        if (trailing) (void)hipFree(trailing);
+    }
+};
+
+struct qtts_predictor {
+    qtts_ctx *ctx = nullptr;
+    Owner own;
+    Stack st;
+    int talker_hidden = 0, groups = 0, vocab = 0, embed_dim = 0;
+    bool identity_proj = false;
+    DevQ4 in_proj{};
+    float *bias = nullptr;
+    DevQ4 emb[kMaxGroups]{};
+    DevQ4 heads[kMaxGroups]{};
+    float *in2 = nullptr;  // [2][talker_hidden]: talker hidden, semantic embedding
+    float *x2 = nullptr, *q2 = nullptr, *a2 = nullptr, *h2 = nullptr, *logits = nullptr;
+    uint32_t *codes = nullptr;  // [16]
+    int *status = nullptr;
+};
+
+// ===========================================================================
+// C-ABI
+// ===========================================================================
+extern "C" {
+
+const char *qtts_version(void) { return "qtts-mi355x 0.1.0 (gfx950)"; }
+
+qtts_status qtts_ctx_create(int32_t device, qtts_ctx **out) {
+    if (!out) return QTTS_EINVAL;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || n <= 0) return QTTS_EDEVICE;
+    if (device < 0 || device >= n) return QTTS_EINVAL;
+    qtts_ctx *c = new qtts_ctx();
+    c->device = device;
+    auto bad = [&](hipError_t e) {
+        if (e == hipSuccess) return false;
+        qtts_ctx_destroy(c);
+        return true;
+    };
+    if (bad(hipSetDevice(device))) return QTTS_EDEVICE;
+    if (bad(hipStreamCreateWithFlags(&c->stream, hipStreamNonBlocking))) return QTTS_EDEVICE;
+    if (bad(hipMalloc(&c->partial, kPartialFloats * sizeof(float)))) return QTTS_ENOMEM;
+    if (bad(hipMalloc(&c->counters, kCounters * sizeof(unsigned)))) return QTTS_ENOMEM;
+    if (bad(hipMalloc(&c->attn_part, kAttnPartFloats * sizeof(float)))) return QTTS_ENOMEM;
+    if (bad(hipMalloc(&c->attn_counters, kAttnCounters * sizeof(unsigned)))) return QTTS_ENOMEM;
+    if (bad(hipMalloc(&c->d_small, 256))) return QTTS_ENOMEM;
+    if (bad(hipMemset(c->counters, 0, kCounters * sizeof(unsigned)))) return QTTS_EDEVICE;
+    if (bad(hipMemset(c->attn_counters, 0, kAttnCounters * sizeof(unsigned)))) return QTTS_EDEVICE;
+    if (bad(hipDeviceSynchronize())) return QTTS_EDEVICE;
+    *out = c;
+    return QTTS_OK;
+}
+
+void qtts_ctx_destroy(qtts_ctx *c) {
+    if (!c) return;
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    (void)hipFree(c->partial);
+    (void)hipFree(c->counters);
+    (void)hipFree(c->attn_part);
+    (void)hipFree(c->attn_counters);
+    (void)hipFree(c->d_in);
+    (void)hipFree(c->d_out);
+    (void)hipFree(c->d_small);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    delete c;
+}
+
+const char *qtts_last_error(const qtts_ctx *c) { return c ? c->err.c_str() : "null context"; }
+
+void *qtts_ctx_stream(qtts_ctx *c) { return c ? (void *)c->stream : nullptr; }
+
+qtts_status qtts_ctx_synchronize(qtts_ctx *c) {
+    if (!c) return QTTS_EINVAL;
+    return sync(c);
+}
+
+// ---------------------------------------------------------------------------
+qtts_status qtts_q4_upload(qtts_ctx *c, const qtts_q4_view *v, qtts_q4 **out) {
+    if (!c || !v || !out) return QTTS_EINVAL;
+    *out = nullptr;
+    if (!v->packed || !v->scales) return fail(c, QTTS_EINVAL, "null weight arrays");
+    if (v->k <= 0 || v->n <= 0 || v->n % 32 != 0) return fail(c, QTTS_ESHAPE, "Q4 weight needs n % 32 == 0");
+    qtts_q4 *w = new qtts_q4();
+    w->ctx = c;
+    w->bytes = (size_t)v->k * v->n / 2 + (size_t)v->k * (v->n / 32) * 2;
+    if (hipMalloc(&w->mem, w->bytes) != hipSuccess) {
+        delete w;
+        return fail(c, QTTS_ENOMEM, "hipMalloc weight");
+    }
+    w->d.wq = reinterpret_cast<const uint4 *>(w->mem);
+    w->d.ws = reinterpret_cast<const uint16_t *>((uint8_t *)w->mem + (size_t)v->k * v->n / 2);
+    w->d.K = v->k;
+    w->d.N = v->n;
+    qtts_status s = upload_part(c, v, w->d, 0);
+    if (s != QTTS_OK) {
+        qtts_q4_free(w);
+        return s;
+    }
+    *out = w;
+    return QTTS_OK;
+}
+
+void qtts_q4_free(qtts_q4 *w) {
+    if (!w) return;
+    (void)hipFree(w->mem);
+    delete w;
+}
+
+size_t qtts_q4_bytes(const qtts_q4 *w) { return w ? w->bytes : 0; }
+
+qtts_status qtts_gemm_device(qtts_ctx *c, const qtts_q4 *w, const float *d_x, int32_t seq_len, float *d_out) {
+    if (!c || !w || !d_x || !d_out) return QTTS_EINVAL;
+    if (seq_len < 1) return fail(c, QTTS_EINVAL, "seq_len < 1");
+    for (int r0 = 0; r0 < seq_len; r0 += kMaxM) {
+        const int M = seq_len - r0 < kMaxM ? seq_len - r0 : kMaxM;
+        GemvParams p = gemv_base(c, w->d, M);
+        p.prologue = PRO_PLAIN;
+        p.x = d_x + (size_t)r0 * w->d.K;
+        p.ldx = w->d.K;
+        p.epilogue = EPI_STORE;
+        p.y = d_out + (size_t)r0 * w->d.N;
+        p.ldy = w->d.N;
+        QTTS_TRY(run_gemv(c, p));
+    }
+    return QTTS_OK;
+}
+
+qtts_status qtts_gemv_device(qtts_ctx *c, const qtts_q4 *w, const float *d_x, float *d_out) {
+    return qtts_gemm_device(c, w, d_x, 1, d_out);
+}
+
+qtts_status qtts_gemm(qtts_ctx *c, const qtts_q4 *w, const float *x, int32_t seq_len, float *out) {
+    if (!c || !w || !x || !out) return QTTS_EINVAL;
+    if (seq_len < 1) return fail(c, QTTS_EINVAL, "seq_len < 1");
+    const size_t nin = (size_t)seq_len * w->d.K, nout = (size_t)seq_len * w->d.N;
+    QTTS_TRY(ensure_staging(c, nin, nout));
+    HIP_TRY(c, hipMemcpyAsync(c->d_in, x, nin * sizeof(float), hipMemcpyHostToDevice, c->stream));
+    QTTS_TRY(qtts_gemm_device(c, w, c->d_in, seq_len, c->d_out));
+    HIP_TRY(c, hipMemcpyAsync(out, c->d_out, nout * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    return sync(c);
+}
+
+qtts_status qtts_gemv(qtts_ctx *c, const qtts_q4 *w, const float *input, float *output) {
+    return qtts_gemm(c, w, input, 1, output);
+}
+
+qtts_status qtts_embed_lookup(qtts_ctx *c, const qtts_q4 *w, int32_t token_id, float *out) {
+    if (!c || !w || !out) return QTTS_EINVAL;
+    if (token_id < 0 || token_id >= w->d.K) return fail(c, QTTS_ERANGE, "token id out of range");
+    QTTS_TRY(ensure_staging(c, 0, (size_t)w->d.N));
+    const uint32_t tok = (uint32_t)token_id;
+    HIP_TRY(c, hipMemcpyAsync(c->d_small, &tok, 4, hipMemcpyHostToDevice, c->stream));
+    launch_embed_row(c->stream, w->d, c->d_small, c->d_out, nullptr);
+    QTTS_TRY(check_launch(c, "k_embed_row"));
+    HIP_TRY(c, hipMemcpyAsync(out, c->d_out, (size_t)w->d.N * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    return sync(c);
+}
+
+// ---------------------------------------------------------------------------
+qtts_status qtts_kv_create(qtts_ctx *c, int32_t num_layers, int32_t num_kv_heads, int32_t head_dim, int32_t capacity,
+                           qtts_kv **out) {
+    if (!c || !out) return QTTS_EINVAL;
+    *out = nullptr;
+    if (num_layers <= 0 || num_kv_heads <= 0 || head_dim <= 0 || capacity <= 0)
+        return fail(c, QTTS_EINVAL, "kv dimensions must be positive");
+    qtts_kv *kv = new qtts_kv();
+    kv->ctx = c;
+    kv->layers = num_layers;
+    kv->kvh = num_kv_heads;
+    kv->hd = head_dim;
+    kv->cap = capacity;
+    const size_t bytes = (size_t)num_layers * num_kv_heads * capacity * head_dim * sizeof(float);
+    if (hipMalloc(&kv->k, bytes) != hipSuccess || hipMalloc(&kv->v, bytes) != hipSuccess) {
+        qtts_kv_free(kv);
+        return fail(c, QTTS_ENOMEM, "hipMalloc kv cache");
+    }
+    if (hipMemset(kv->k, 0, bytes) != hipSuccess || hipMemset(kv->v, 0, bytes) != hipSuccess) {
+        qtts_kv_free(kv);
+        return fail(c, QTTS_EDEVICE, "hipMemset kv cache");
+    }
+    *out = kv;
+    return QTTS_OK;
+}
+
+void qtts_kv_free(qtts_kv *kv) {
+    if (!kv) return;
+    (void)hipFree(kv->k);
+    (void)hipFree(kv->v);
+    delete kv;
+}
+
+int32_t qtts_kv_len(const qtts_kv *kv) { return kv ? kv->len : -1; }
+
+qtts_status qtts_kv_clear(qtts_kv *kv) {
+    if (!kv) return QTTS_EINVAL;
+    kv->len = 0;
+    return QTTS_OK;
+}
+
+qtts_status qtts_kv_load(qtts_kv *kv, const float *k, const float *v, int32_t len) {
+    if (!kv || !k || !v) return QTTS_EINVAL;
+    qtts_ctx *c = kv->ctx;
+    if (len < 0 || len > kv->cap) return fail(c, QTTS_ERANGE, "kv_load: len exceeds capacity");
+    const size_t row = (size_t)kv->kvh * kv->hd;
+    std::vector<float> tk((size_t)kv->kvh * kv->cap * kv->hd), tv(tk.size());
+    for (int l = 0; l < kv->layers; l++) {
+        const float *sk = k + (size_t)l * len * row, *sv = v + (size_t)l * len * row;
+        for (int t = 0; t < len; t++)
+            for (int hh = 0; hh < kv->kvh; hh++) {
+                std::memcpy(&tk[((size_t)hh * kv->cap + t) * kv->hd], sk + t * row + (size_t)hh * kv->hd,
+                            sizeof(float) * kv->hd);
+                std::memcpy(&tv[((size_t)hh * kv->cap + t) * kv->hd], sv + t * row + (size_t)hh * kv->hd,
+                            sizeof(float) * kv->hd);
+            }
+        HIP_TRY(c, hipMemcpy(kv->layer_k(l), tk.data(), tk.size() * sizeof(float), hipMemcpyHostToDevice));
+        HIP_TRY(c, hipMemcpy(kv->layer_v(l), tv.data(), tv.size() * sizeof(float), hipMemcpyHostToDevice));
+    }
+    kv->len = len;
+    return QTTS_OK;
+}
+
+qtts_status qtts_kv_store(const qtts_kv *kv, float *k, float *v) {
+    if (!kv || !k || !v) return QTTS_EINVAL;
+    qtts_ctx *c = kv->ctx;
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    const size_t row = (size_t)kv->kvh * kv->hd;
+    std::vector<float> tk((size_t)kv->kvh * kv->cap * kv->hd), tv(tk.size());
+    for (int l = 0; l < kv->layers; l++) {
+        HIP_TRY(c, hipMemcpy(tk.data(), kv->layer_k(l), tk.size() * sizeof(float), hipMemcpyDeviceToHost));
+        HIP_TRY(c, hipMemcpy(tv.data(), kv->layer_v(l), tv.size() * sizeof(float), hipMemcpyDeviceToHost));
+        float *dk = k + (size_t)l * kv->len * row, *dv = v + (size_t)l * kv->len * row;
+        for (int t = 0; t < kv->len; t++)
+            for (int hh = 0; hh < kv->kvh; hh++) {
+                std::memcpy(dk + t * row + (size_t)hh * kv->hd, &tk[((size_t)hh * kv->cap + t) * kv->hd],
+                            sizeof(float) * kv->hd);
+                std::memcpy(dv + t * row + (size_t)hh * kv->hd, &tv[((size_t)hh * kv->cap + t) * kv->hd],
+                            sizeof(float) * kv->hd);
+            }
+    }
+    return QTTS_OK;
+}
+
+// ---------------------------------------------------------------------------
+qtts_status qtts_talker_upload(qtts_ctx *c, const qtts_talker_view *v, qtts_talker **out) {
+    if (!c || !v || !out) return QTTS_EINVAL;
+    *out = nullptr;
+    qtts_talker *t = new qtts_talker();
+    t->ctx = c;
+    auto bail = [&](qtts_status s) {
+        delete t;
+        return s;
+    };
+    qtts_status s =
+        upload_stack(c, t->own, v->num_layers, v->layers, v->hidden_size, v->num_heads, v->num_kv_heads, v->head_dim, &t->st);
+    if (s != QTTS_OK) return bail(s);
+    const int hidden = v->hidden_size;
+    t->vocab = v->codec_head.n;
+    t->max_pos = v->max_position;
+    if ((s = check_view(c, &v->codec_head, hidden, t->vocab, "codec_head")) != QTTS_OK) return bail(s);
+    if ((s = check_view(c, &v->codec_embedding, v->codec_embedding.k, hidden, "codec_embedding")) != QTTS_OK)
+        return bail(s);
+    if (v->max_position <= 0) return bail(fail(c, QTTS_EINVAL, "max_position must be positive"));
+    if ((s = alloc_q4(c, t->own, hidden, t->vocab, &t->head)) != QTTS_OK) return bail(s);
+    if ((s = upload_part(c, &v->codec_head, t->head, 0)) != QTTS_OK) return bail(s);
+    if ((s = alloc_q4(c, t->own, v->codec_embedding.k, hidden, &t->emb)) != QTTS_OK) return bail(s);
+    if ((s = upload_part(c, &v->codec_embedding, t->emb, 0)) != QTTS_OK) return bail(s);
+    if ((s = upload_array(c, t->own, v->final_norm_gamma, (size_t)hidden, &t->st.final_g, "final_norm_gamma")) !=
+        QTTS_OK)
+        return bail(s);
+    if ((s = upload_rope(c, t->own, v->head_dim, v->max_position, v->rope_theta, &t->st)) != QTTS_OK) return bail(s);
+    t->st.rope_skip_oob = 0;
+    const int qd = t->st.nq * t->st.hd;
+    if ((s = t->own.alloc(c, &t->x, (size_t)hidden)) != QTTS_OK) return bail(s);
+    if ((s = t->own.alloc(c, &t->q, (size_t)qd)) != QTTS_OK) return bail(s);
+    if ((s = t->own.alloc(c, &t->attn, (size_t)qd)) != QTTS_OK) return bail(s);
+    if ((s = t->own.alloc(c, &t->h, (size_t)t->st.inter)) != QTTS_OK) return bail(s);
+    if ((s = t->own.alloc(c, &t->out, (size_t)hidden + t->vocab)) != QTTS_OK) return bail(s);
+    if ((s = t->own.alloc(c, &t->pad, (size_t)hidden)) != QTTS_OK) return bail(s);
+    if ((s = t->own.alloc(c, &t->state, 1)) != QTTS_OK) return bail(s);
+    if (hipMemset(t->state, 0, sizeof(LoopState)) != hipSuccess) return bail(fail(c, QTTS_EDEVICE, "memset"));
+    *out = t;
+    return QTTS_OK;
+}
+
+void qtts_talker_free(qtts_talker *t) {
+    if (!t) return;
+    (void)hipStreamSynchronize(t->ctx->stream);
+    delete t;
+}
+
+namespace {
+
+qtts_status check_kv(qtts_ctx *c, const Stack &st, const qtts_kv *kv) {
+    if (!kv) return fail(c, QTTS_EINVAL, "null kv cache");
+    if (kv->layers != st.layers || kv->kvh != st.nkv || kv->hd != st.hd)
+        return fail(c, QTTS_ESHAPE, "kv cache shape does not match the model");
+    return QTTS_OK;
+}
+
+qtts_status set_state(qtts_talker *t, int pos, int kvlen) {
+    const int v[2] = {pos, kvlen};
+    HIP_TRY(t->ctx, hipMemcpyAsync(t->state, v, sizeof(v), hipMemcpyHostToDevice, t->ctx->stream));
+    return QTTS_OK;
+}
+
+// forward_with_embedding on device buffers: t->x holds the input embedding;
+// hidden_out/logits_out receive [normed hidden] and [logits].
+qtts_status enqueue_talker_step(qtts_talker *t, qtts_kv *kv, float *hidden_out, float *logits_out, const int *d_done,
+                                int frame_step) {
+    qtts_ctx *c = t->ctx;
+    QTTS_TRY(enqueue_layers(c, t->st, kv, t->x, t->q, t->attn, t->h, 1, &t->state->pos, 0, &t->state->kvlen, 0,
+                            t->nsplit, d_done));
+    GemvParams p = gemv_base(c, t->head, 1);
+    p.prologue = PRO_RMSNORM;
+    p.x = t->x;
+    p.ldx = t->st.hidden;
+    p.gamma = t->st.final_g;
+    p.norm_out = hidden_out;
+    p.ldn = t->st.hidden;
+    p.epilogue = EPI_STORE;
+    p.y = logits_out;
+    p.ldy = t->vocab;
+    p.d_done = d_done;
+    QTTS_TRY(run_gemv(c, p));
+    launch_advance(c->stream, t->state, frame_step);
+    return check_launch(c, "k_advance");
+}
+
+}  // namespace
+
+qtts_status qtts_forward_with_embedding(qtts_talker *t, const float *embedding, qtts_kv *kv, int32_t position,
+                                        float *out) {
+    if (!t || !embedding || !out) return QTTS_EINVAL;
+    qtts_ctx *c = t->ctx;
+    QTTS_TRY(check_kv(c, t->st, kv));
+    if (position < 0 || position >= t->max_pos) return fail(c, QTTS_ERANGE, "position beyond the RoPE table");
+    if (kv->len + 1 > kv->cap) return fail(c, QTTS_ERANGE, "kv cache full");
+    t->nsplit = attn_nsplit(kv->cap, 16);
+    const int hidden = t->st.hidden;
+    HIP_TRY(c, hipMemcpyAsync(t->x, embedding, sizeof(float) * hidden, hipMemcpyHostToDevice, c->stream));
+    QTTS_TRY(set_state(t, position, kv->len));
+    QTTS_TRY(enqueue_talker_step(t, kv, t->out, t->out + hidden, nullptr, 0));
+    HIP_TRY(c, hipMemcpyAsync(out, t->out, sizeof(float) * (hidden + t->vocab), hipMemcpyDeviceToHost, c->stream));
+    QTTS_TRY(sync(c));
+    kv->len += 1;
+    return QTTS_OK;
+}
+
+qtts_status qtts_prefill_talker_raw(qtts_talker *t, const float *x, int32_t seq_len, qtts_kv *kv, float *last_hidden) {
+    if (!t || !x || !last_hidden) return QTTS_EINVAL;
+    qtts_ctx *c = t->ctx;
+    QTTS_TRY(check_kv(c, t->st, kv));
+    if (kv->len != 0) return fail(c, QTTS_ESTATE, "prefill needs an empty cache (src/talker.rs:405-408)");
+    if (seq_len < 1) return fail(c, QTTS_EINVAL, "seq_len < 1");
+    if (seq_len > kv->cap) return fail(c, QTTS_ERANGE, "prefill longer than the cache");
+    if (seq_len > t->max_pos) return fail(c, QTTS_ERANGE, "prefill longer than the RoPE table");
+    const Stack &st = t->st;
+    const int hidden = st.hidden, qd = st.nq * st.hd;
+    if (seq_len > t->prefill_cap) {
+        for (void *p : t->prefill_bufs) (void)hipFree(p);
+        t->prefill_bufs.clear();
+        t->prefill_cap = 0;
+        HIP_TRY(c, hipMalloc(&t->xp, sizeof(float) * seq_len * hidden));
+        t->prefill_bufs.push_back(t->xp);
+        HIP_TRY(c, hipMalloc(&t->qp, sizeof(float) * seq_len * qd));
+        t->prefill_bufs.push_back(t->qp);
+        HIP_TRY(c, hipMalloc(&t->ap, sizeof(float) * seq_len * qd));
+        t->prefill_bufs.push_back(t->ap);
+        HIP_TRY(c, hipMalloc(&t->hp, sizeof(float) * seq_len * st.inter));
+        t->prefill_bufs.push_back(t->hp);
+        t->prefill_cap = seq_len;
+    }
+    t->nsplit = attn_nsplit(kv->cap, 16);
+    HIP_TRY(c, hipMemcpyAsync(t->xp, x, sizeof(float) * seq_len * hidden, hipMemcpyHostToDevice, c->stream));
+    // Row chunks of up to kMaxM tokens, in order, layer by layer: a chunk's
+    // causal attention reads the K/V rows earlier chunks appended.
+    Stack one = st;
+    for (int l = 0; l < st.layers; l++) {
+        one.layers = 1;
+        one.L.assign(1, st.L[l]);
+        qtts_kv layer_kv = *kv;
+        layer_kv.layers = 1;
+        layer_kv.k = kv->layer_k(l);
+        layer_kv.v = kv->layer_v(l);
+        for (int r0 = 0; r0 < seq_len; r0 += kMaxM) {
+            const int M = seq_len - r0 < kMaxM ? seq_len - r0 : kMaxM;
+            QTTS_TRY(enqueue_layers(c, one, &layer_kv, t->xp + (size_t)r0 * hidden, t->qp + (size_t)r0 * qd,
+                                    t->ap + (size_t)r0 * qd, t->hp + (size_t)r0 * st.inter, M, nullptr, r0, nullptr,
+                                    r0, t->nsplit, nullptr));
+        }
+    }
+    // final norm of the last row (src/talker.rs:460-461) via the head GEMV's
+    // normalising prologue; the logits it also produces are discarded.
+    GemvParams p = gemv_base(c, t->head, 1);
+    p.prologue = PRO_RMSNORM;
+    p.x = t->xp;
+    p.ldx = hidden;
+    p.norm_src_row0 = seq_len - 1;
+    p.gamma = st.final_g;
+    p.norm_out = t->out;
+    p.ldn = hidden;
+    p.epilogue = EPI_STORE;
+    p.y = t->out + hidden;
+    p.ldy = t->vocab;
+    QTTS_TRY(run_gemv(c, p));
+    HIP_TRY(c, hipMemcpyAsync(last_hidden, t->out, sizeof(float) * hidden, hipMemcpyDeviceToHost, c->stream));
+    QTTS_TRY(sync(c));
+    kv->len = seq_len;
+    return QTTS_OK;
+}
+
+qtts_status qtts_apply_codec_head(qtts_talker *t, const float *hidden, float *logits) {
+    if (!t || !hidden || !logits) return QTTS_EINVAL;
+    qtts_ctx *c = t->ctx;
+    HIP_TRY(c, hipMemcpyAsync(t->x, hidden, sizeof(float) * t->st.hidden, hipMemcpyHostToDevice, c->stream));
+    GemvParams p = gemv_base(c, t->head, 1);
+    p.prologue = PRO_PLAIN;
+    p.x = t->x;
+    p.ldx = t->st.hidden;
+    p.epilogue = EPI_STORE;
+    p.y = t->out + t->st.hidden;
+    p.ldy = t->vocab;
+    QTTS_TRY(run_gemv(c, p));
+    HIP_TRY(c, hipMemcpyAsync(logits, t->out + t->st.hidden, sizeof(float) * t->vocab, hipMemcpyDeviceToHost,
+                              c->stream));
+    return sync(c);
+}
+
+qtts_status qtts_embed_codec_token(qtts_talker *t, uint32_t token_id, float *out) {
+    if (!t || !out) return QTTS_EINVAL;
+    qtts_ctx *c = t->ctx;
+    if (token_id >= (uint32_t)t->emb.K) return fail(c, QTTS_ERANGE, "token id out of range");
+    HIP_TRY(c, hipMemcpyAsync(c->d_small, &token_id, 4, hipMemcpyHostToDevice, c->stream));
+    launch_embed_row(c->stream, t->emb, c->d_small, t->out, nullptr);
+    QTTS_TRY(check_launch(c, "k_embed_row"));
+    HIP_TRY(c, hipMemcpyAsync(out, t->out, sizeof(float) * t->st.hidden, hipMemcpyDeviceToHost, c->stream));
+    return sync(c);
+}
+
+// ---------------------------------------------------------------------------
+qtts_status qtts_predictor_upload(qtts_ctx *c, const qtts_predictor_view *v, qtts_predictor **out) {
+    if (!c || !v || !out) return QTTS_EINVAL;
+    *out = nullptr;
+    if (v->num_groups <= 0 || v->num_groups > kMaxGroups) return fail(c, QTTS_ESHAPE, "num_groups must be 1..15");
+    if (!v->codec_embeddings || !v->lm_heads) return fail(c, QTTS_EINVAL, "null embeddings or heads");
+    qtts_predictor *p = new qtts_predictor();
+    p->ctx = c;
+    auto bail = [&](qtts_status s) {
+        delete p;
+        return s;
+    };
+    const int hidden = v->hidden_size;
+    qtts_status s =
+        upload_stack(c, p->own, v->num_layers, v->layers, hidden, v->num_heads, v->num_kv_heads, v->head_dim, &p->st);
+    if (s != QTTS_OK) return bail(s);
+    p->groups = v->num_groups;
+    p->embed_dim = v->codec_embeddings[0].n;
+    p->vocab = v->lm_heads[0].n;
+    p->identity_proj = v->input_proj.k == 0;
+    p->talker_hidden = p->identity_proj ? hidden : v->input_proj.k;
+    if (p->embed_dim != p->talker_hidden)
+        return bail(fail(c, QTTS_ESHAPE, "codec embedding width must equal the projection input"));
+    if (!p->identity_proj) {
+        if ((s = check_view(c, &v->input_proj, p->talker_hidden, hidden, "input_proj")) != QTTS_OK) return bail(s);
+        if ((s = alloc_q4(c, p->own, p->talker_hidden, hidden, &p->in_proj)) != QTTS_OK) return bail(s);
+        if ((s = upload_part(c, &v->input_proj, p->in_proj, 0)) != QTTS_OK) return bail(s);
+        if (v->input_proj_bias &&
+            (s = upload_array(c, p->own, v->input_proj_bias, (size_t)hidden, &p->bias, "input_proj_bias")) != QTTS_OK)
+            return bail(s);
+    }
+    for (int g = 0; g < p->groups; g++) {
+        const qtts_q4_view &e = v->codec_embeddings[g];
+        if ((s = check_view(c, &e, e.k, p->embed_dim, "codec_embeddings")) != QTTS_OK) return bail(s);
+        if ((s = alloc_q4(c, p->own, e.k, p->embed_dim, &p->emb[g])) != QTTS_OK) return bail(s);
+        if ((s = upload_part(c, &e, p->emb[g], 0)) != QTTS_OK) return bail(s);
+        const qtts_q4_view &h = v->lm_heads[g];
+        if ((s = check_view(c, &h, hidden, p->vocab, "lm_heads")) != QTTS_OK) return bail(s);
+        if ((s = alloc_q4(c, p->own, hidden, p->vocab, &p->heads[g])) != QTTS_OK) return bail(s);
+        if ((s = upload_part(c, &h, p->heads[g], 0)) != QTTS_OK) return bail(s);
+    }
+    if ((s = upload_array(c, p->own, v->final_norm_gamma, (size_t)hidden, &p->st.final_g, "final_norm_gamma")) !=
+        QTTS_OK)
+        return bail(s);
+    // Positions 0..num_groups occur (the cache restarts every frame); rows
+    // past max_position skip the rotation as src/code_predictor.rs:107 does.
+    int rows = p->groups + 2;
+    if (rows > v->max_position) rows = v->max_position;
+    if (rows < 1) return bail(fail(c, QTTS_EINVAL, "max_position must be positive"));
+    if ((s = upload_rope(c, p->own, v->head_dim, rows, v->rope_theta, &p->st)) != QTTS_OK) return bail(s);
+    p->st.rope_skip_oob = 1;
+    const int qd = p->st.nq * p->st.hd;
+    if ((s = p->own.alloc(c, &p->in2, 2 * (size_t)p->talker_hidden)) != QTTS_OK) return bail(s);
+    if ((s = p->own.alloc(c, &p->x2, 2 * (size_t)hidden)) != QTTS_OK) return bail(s);
+    if ((s = p->own.alloc(c, &p->q2, 2 * (size_t)qd)) != QTTS_OK) return bail(s);
+    if ((s = p->own.alloc(c, &p->a2, 2 * (size_t)qd)) != QTTS_OK) return bail(s);
+    if ((s = p->own.alloc(c, &p->h2, 2 * (size_t)p->st.inter)) != QTTS_OK) return bail(s);
+    if ((s = p->own.alloc(c, &p->logits, (size_t)p->vocab)) != QTTS_OK) return bail(s);
+    if ((s = p->own.alloc(c, &p->codes, 16)) != QTTS_OK) return bail(s);
+    if ((s = p->own.alloc(c, &p->status, 4)) != QTTS_OK) return bail(s);
+    *out = p;
+    return QTTS_OK;
+}
+
+void qtts_predictor_free(qtts_predictor *p) {
+    if (!p) return;
+    (void)hipStreamSynchronize(p->ctx->stream);
+    delete p;
+}
+
+namespace {
+
+// generate_acoustic_codes (src/code_predictor.rs:218-273) on device buffers:
+// p->in2 = [talker_hidden; semantic_embed]; the 15 codes go to codes_out.
+qtts_status enqueue_predictor(qtts_predictor *p, qtts_kv *kv, uint32_t *codes_out, int *status, const int *d_done) {
+    qtts_ctx *c = p->ctx;
+    const Stack &st = p->st;
+    const int hidden = st.hidden;
+    const int nsplit = attn_nsplit(kv->cap, 1);
+    // 1. project both prefill rows
+    if (p->identity_proj) {
+        HIP_TRY(c, hipMemcpyAsync(p->x2, p->in2, sizeof(float) * 2 * hidden, hipMemcpyDeviceToDevice, c->stream));
+    } else {
+        GemvParams g = gemv_base(c, p->in_proj, 2);
+        g.prologue = PRO_PLAIN;
+        g.x = p->in2;
+        g.ldx = p->talker_hidden;
+        g.epilogue = EPI_STORE;
+        g.y = p->x2;
+        g.ldy = hidden;
+        g.bias = p->bias;
+        g.d_done = d_done;
+        QTTS_TRY(run_gemv(c, g));
+    }
+    // 2. two-token prefill at positions 0, 1
+    QTTS_TRY(enqueue_layers(c, st, kv, p->x2, p->q2, p->a2, p->h2, 2, nullptr, 0, nullptr, 0, nsplit, d_done));
+    auto head = [&](int gi, int src_row) -> qtts_status {
+        GemvParams g = gemv_base(c, p->heads[gi], 1);
+        g.prologue = PRO_RMSNORM;
+        g.x = p->x2;
+        g.ldx = hidden;
+        g.norm_src_row0 = src_row;
+        g.gamma = st.final_g;
+        g.epilogue = EPI_STORE;
+        g.y = p->logits;
+        g.ldy = p->vocab;
+        g.fin = FIN_ARGMAX;
+        g.argmax_out = codes_out + gi;
+        g.status = status;
+        g.d_done = d_done;
+        return run_gemv(c, g);
+    };
+    QTTS_TRY(head(0, 1));
+    // 3. fourteen single-token decodes at cache offsets 2..15
+    for (int gi = 1; gi < p->groups; gi++) {
+        if (p->identity_proj) {
+            launch_embed_row(c->stream, p->emb[gi - 1], codes_out + gi - 1, p->x2, d_done);
+            QTTS_TRY(check_launch(c, "k_embed_row"));
+        } else {
+            GemvParams g = gemv_base(c, p->in_proj, 1);
+            g.prologue = PRO_EMBED;
+            g.emb = p->emb[gi - 1];
+            g.emb_token = codes_out + gi - 1;
+            g.epilogue = EPI_STORE;
+            g.y = p->x2;
+            g.ldy = hidden;
+            g.bias = p->bias;
+            g.d_done = d_done;
+            QTTS_TRY(run_gemv(c, g));
+        }
+        QTTS_TRY(enqueue_layers(c, st, kv, p->x2, p->q2, p->a2, p->h2, 1, nullptr, gi + 1, nullptr, gi + 1, nsplit,
+                                d_done));
+        QTTS_TRY(head(gi, 0));
+    }
+    return QTTS_OK;
+}
+
+}  // namespace
+
+qtts_status qtts_generate_acoustic_codes(qtts_predictor *p, const float *talker_hidden, const float *semantic_embed,
+                                         qtts_kv *kv, uint32_t *codes) {
+    if (!p || !talker_hidden || !semantic_embed || !codes) return QTTS_EINVAL;
+    qtts_ctx *c = p->ctx;
+    QTTS_TRY(check_kv(c, p->st, kv));
+    if (kv->cap < p->groups + 1) return fail(c, QTTS_ERANGE, "predictor cache needs num_groups+1 positions");
+    kv->len = 0;  // src/code_predictor.rs:227-231
+    const int th = p->talker_hidden;
+    HIP_TRY(c, hipMemcpyAsync(p->in2, talker_hidden, sizeof(float) * th, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(c, hipMemcpyAsync(p->in2 + th, semantic_embed, sizeof(float) * th, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(c, hipMemsetAsync(p->status, 0, sizeof(int), c->stream));
+    QTTS_TRY(enqueue_predictor(p, kv, p->codes, p->status, nullptr));
+    int status = 0;
+    HIP_TRY(c, hipMemcpyAsync(codes, p->codes, sizeof(uint32_t) * p->groups, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(c, hipMemcpyAsync(&status, p->status, sizeof(int), hipMemcpyDeviceToHost, c->stream));
+    QTTS_TRY(sync(c));
+    kv->len = p->groups + 1;
+    if (status != 0) return fail(c, (qtts_status)status, "NaN logits in the predictor (src/code_predictor.rs:331)");
+    return QTTS_OK;
+}
+
+qtts_status qtts_get_acoustic_embeddings_sum(qtts_predictor *p, const uint32_t *codes, float *out) {
+    if (!p || !codes || !out) return QTTS_EINVAL;
+    qtts_ctx *c = p->ctx;
+    for (int g = 0; g < p->groups; g++)
+        if (codes[g] >= (uint32_t)p->emb[g].K) return fail(c, QTTS_ERANGE, "code out of range");
+    uint32_t cur[16] = {0};
+    for (int g = 0; g < p->groups; g++) cur[1 + g] = codes[g];
+    QTTS_TRY(ensure_staging(c, 0, (size_t)p->embed_dim));
+    HIP_TRY(c, hipMemcpyAsync(p->codes, cur, sizeof(cur), hipMemcpyHostToDevice, c->stream));
+    EmbSumParams e{};
+    e.mode = 1;
+    for (int g = 0; g < p->groups; g++) e.group_emb[g] = p->emb[g];
+    e.num_groups = p->groups;
+    e.cur = p->codes;
+    e.out = c->d_out;
+    e.hidden = p->embed_dim;
+    launch_embed_sum(c->stream, e);
+    QTTS_TRY(check_launch(c, "k_embed_sum"));
+    HIP_TRY(c, hipMemcpyAsync(out, c->d_out, sizeof(float) * p->embed_dim, hipMemcpyDeviceToHost, c->stream));
+    return sync(c);
+}
+
+// ---------------------------------------------------------------------------
+qtts_status qtts_sample_token(qtts_ctx *c, const float *logits, int32_t vocab, const qtts_sampler *params,
+                              const uint32_t *prev_tokens, int32_t n_prev, uint64_t *rng, uint32_t *token) {
+    if (!c || !logits || !params || !rng || !token || (n_prev > 0 && !prev_tokens)) return QTTS_EINVAL;
+    if (vocab <= 0 || vocab > 32768) return fail(c, QTTS_ESHAPE, "vocab must be 1..32768");
+    if (n_prev < 0 || n_prev > 32) return fail(c, QTTS_EINVAL, "n_prev must be 0..32");
+    QTTS_TRY(ensure_staging(c, (size_t)vocab, 0));
+    // d_small layout: [0] token, [1] status, [2..3] rng, [4..35] prev tokens
+    uint32_t small[36] = {0};
+    std::memcpy(&small[2], rng, 8);
+    if (n_prev > 0) std::memcpy(&small[4], prev_tokens, sizeof(uint32_t) * n_prev);
+    HIP_TRY(c, hipMemcpyAsync(c->d_in, logits, sizeof(float) * vocab, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(c, hipMemcpyAsync(c->d_small, small, sizeof(small), hipMemcpyHostToDevice, c->stream));
+    SampleParams s{};
+    s.logits = c->d_in;
+    s.vocab = vocab;
+    s.temperature = params->temperature;
+    s.top_k = params->top_k;
+    s.penalty = params->repetition_penalty;
+    s.greedy = params->greedy;
+    s.prev = c->d_small + 4;
+    s.n_prev = n_prev;
+    s.rng = reinterpret_cast<uint64_t *>(c->d_small + 2);
+    s.token_out = c->d_small;
+    s.status = reinterpret_cast<int *>(c->d_small + 1);
+    launch_sample(c->stream, s);
+    QTTS_TRY(check_launch(c, "k_sample"));
+    HIP_TRY(c, hipMemcpyAsync(small, c->d_small, 16, hipMemcpyDeviceToHost, c->stream));
+    QTTS_TRY(sync(c));
+    *token = small[0];
+    std::memcpy(rng, &small[2], 8);
+    if (small[1] != 0) return fail(c, (qtts_status)small[1], "NaN in the sampler (src/generate_new.rs:365)");
+    return QTTS_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Frame loop
+// ---------------------------------------------------------------------------
+namespace {
+
+struct LoopCfg {
+    qtts_talker *t;
+    qtts_predictor *p;
+    qtts_kv *tkv, *pkv;
+    const qtts_loop_params *params;
+    int trailing_len;
+};
+
+// One frame of src/generate_new.rs:242-300 on the device.
+qtts_status enqueue_frame(const LoopCfg &L) {
+    qtts_talker *t = L.t;
+    qtts_ctx *c = t->ctx;
+    LoopState *S = t->state;
+    const int hidden = t->st.hidden;
+    const bool talker_only = L.params->talker_only || !L.p;
+    SampleParams s{};
+    s.logits = t->out + hidden;
+    s.vocab = t->vocab;
+    s.temperature = L.params->sampler.temperature;
+    s.top_k = L.params->sampler.top_k;
+    s.penalty = L.params->sampler.repetition_penalty;
+    s.greedy = L.params->sampler.greedy;
+    s.prev = S->prev;
+    s.n_prev = 16;
+    s.rng = &S->rng;
+    s.token_out = &S->cur[0];
+    s.status = &S->status;
+    s.done = &S->done;
+    s.stop_on_eos = L.params->stop_on_eos;
+    s.eos = L.params->codec_eos_id;
+    s.codes = t->codes;
+    s.frame = &S->frame;
+    s.max_codes = L.params->max_codes;
+    s.prev_out = &S->prev[0];
+    launch_sample(c->stream, s);
+    QTTS_TRY(check_launch(c, "k_sample"));
+    EmbSumParams e{};
+    e.mode = 0;
+    e.codec_emb = t->emb;
+    e.cur = S->cur;
+    e.trailing = t->trailing;
+    e.trailing_len = L.trailing_len;
+    e.pad = t->pad;
+    e.frame = &S->frame;
+    e.out = t->x;
+    e.hidden = hidden;
+    e.d_done = &S->done;
+    e.codes = t->codes;
+    e.max_codes = L.params->max_codes;
+    e.prev = S->prev;
+    float *hidden_out = t->out;
+    if (!talker_only) {
+        qtts_predictor *p = L.p;
+        launch_embed_row(c->stream, t->emb, &S->cur[0], p->in2 + p->talker_hidden, &S->done);
+        QTTS_TRY(check_launch(c, "k_embed_row"));
+        QTTS_TRY(enqueue_predictor(p, L.pkv, &S->cur[1], &S->status, &S->done));
+        for (int g = 0; g < p->groups; g++) e.group_emb[g] = p->emb[g];
+        e.num_groups = p->groups;
+        hidden_out = p->in2;  // next frame's predictor input row 0
+    }
+    launch_embed_sum(c->stream, e);
+    QTTS_TRY(check_launch(c, "k_embed_sum"));
+    return enqueue_talker_step(t, L.tkv, hidden_out, t->out + hidden, &S->done, 1);
+}
+
+}  // namespace
+
+qtts_status qtts_generate_codes(qtts_talker *t, qtts_predictor *p, qtts_kv *talker_kv, qtts_kv *predictor_kv,
+                                const float *last_hidden, const float *logits, int32_t position,
+                                const float *trailing_text, int32_t trailing_len, const float *tts_pad_embed,
+                                const qtts_loop_params *params, uint64_t seed, uint32_t *codes, int32_t *n_frames) {
+    if (!t || !last_hidden || !logits || !params || !codes || !n_frames) return QTTS_EINVAL;
+    qtts_ctx *c = t->ctx;
+    *n_frames = 0;
+    const bool talker_only = params->talker_only || !p;
+    if (!talker_only && (!predictor_kv || !tts_pad_embed || (trailing_len > 0 && !trailing_text)))
+        return fail(c, QTTS_EINVAL, "predictor loop needs a predictor cache, tts_pad_embed and trailing text");
+    if (trailing_len < 0) return fail(c, QTTS_EINVAL, "trailing_len < 0");
+    QTTS_TRY(check_kv(c, t->st, talker_kv));
+    if (!talker_only) {
+        QTTS_TRY(check_kv(c, p->st, predictor_kv));
+        if (predictor_kv->cap < p->groups + 1) return fail(c, QTTS_ERANGE, "predictor cache too small");
+        if (p->talker_hidden != t->st.hidden) return fail(c, QTTS_ESHAPE, "predictor input width != talker hidden");
+    }
+    const int max_codes = params->max_codes;
+    if (max_codes <= 0) return QTTS_OK;
+    if (position < 0 || position + max_codes > t->max_pos) return fail(c, QTTS_ERANGE, "positions beyond the RoPE table");
+    if (talker_kv->len + max_codes > talker_kv->cap) return fail(c, QTTS_ERANGE, "talker cache too small");
+    const int hidden = t->st.hidden;
+    t->nsplit = attn_nsplit(talker_kv->cap, 16);
+    // device buffers
+    const size_t ncodes = (size_t)16 * max_codes;
+    if (ncodes > t->codes_cap) {
+        if (t->codes) (void)hipFree(t->codes);
+        t->codes = nullptr;
+        t->codes_cap = 0;
+        HIP_TRY(c, hipMalloc(&t->codes, ncodes * sizeof(uint32_t)));
+        t->codes_cap = ncodes;
+    }
+    HIP_TRY(c, hipMemsetAsync(t->codes, 0, ncodes * sizeof(uint32_t), c->stream));
+    const size_t ntrail = (size_t)(trailing_len > 0 ? trailing_len : 1) * hidden;
+    if (ntrail > t->trailing_cap) {
+        if (t->trailing) (void)hipFree(t->trailing);
+        t->trailing = nullptr;
+        t->trailing_cap = 0;
+        HIP_TRY(c, hipMalloc(&t->trailing, ntrail * sizeof(float)));
+        t->trailing_cap = ntrail;
+    }
+    if (trailing_len > 0)
+        HIP_TRY(c, hipMemcpyAsync(t->trailing, trailing_text, sizeof(float) * trailing_len * hidden,
+                                  hipMemcpyHostToDevice, c->stream));
+    if (tts_pad_embed)
+        HIP_TRY(c, hipMemcpyAsync(t->pad, tts_pad_embed, sizeof(float) * hidden, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(c, hipMemcpyAsync(t->out + hidden, logits, sizeof(float) * t->vocab, hipMemcpyHostToDevice, c->stream));
+    if (!talker_only)
+        HIP_TRY(c, hipMemcpyAsync(p->in2, last_hidden, sizeof(float) * hidden, hipMemcpyHostToDevice, c->stream));
+    LoopState init{};
+    init.pos = position;
+    init.kvlen = talker_kv->len;
+    init.rng = seed;
+    HIP_TRY(c, hipMemcpyAsync(t->state, &init, sizeof(init), hipMemcpyHostToDevice, c->stream));
+    QTTS_TRY(sync(c));
+
+    LoopCfg L{t, talker_only ? nullptr : p, talker_kv, predictor_kv, params, trailing_len};
+    const bool use_graph = std::getenv("QTTS_NO_GRAPH") == nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    if (use_graph) {
+        HIP_TRY(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+        qtts_status s = enqueue_frame(L);
+        hipGraph_t g = nullptr;
+        hipError_t e = hipStreamEndCapture(c->stream, &g);
+        if (s != QTTS_OK) {
+            if (g) (void)hipGraphDestroy(g);
+            return s;
+        }
+        if (e != hipSuccess) return fail(c, QTTS_EDEVICE, std::string("graph capture: ") + hipGetErrorString(e));
+        graph = g;
+        e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        if (e != hipSuccess) {
+            (void)hipGraphDestroy(graph);
+            return fail(c, QTTS_EDEVICE, std::string("graph instantiate: ") + hipGetErrorString(e));
+        }
+    }
+    qtts_status rc = QTTS_OK;
+    const int batch = 16;
+    LoopState fin{};
+    for (int f0 = 0; f0 < max_codes && rc == QTTS_OK; f0 += batch) {
+        const int nb = max_codes - f0 < batch ? max_codes - f0 : batch;
+        for (int i = 0; i < nb && rc == QTTS_OK; i++) {
+            if (use_graph) {
+                hipError_t e = hipGraphLaunch(exec, c->stream);
+                if (e != hipSuccess) rc = fail(c, QTTS_EDEVICE, std::string("graph launch: ") + hipGetErrorString(e));
+            } else {
+                rc = enqueue_frame(L);
+            }
+        }
+        if (rc != QTTS_OK) break;
+        hipError_t e = hipMemcpyAsync(&fin, t->state, sizeof(fin), hipMemcpyDeviceToHost, c->stream);
+        if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+        if (e != hipSuccess) {
+            rc = fail(c, QTTS_EDEVICE, std::string("loop: ") + hipGetErrorString(e));
+            break;
+        }
+        if (fin.done) break;
+    }
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    QTTS_TRY(rc);
+    QTTS_TRY(sync(c));
+    HIP_TRY(c, hipMemcpy(codes, t->codes, ncodes * sizeof(uint32_t), hipMemcpyDeviceToHost));
+    *n_frames = fin.frame;
+    talker_kv->len += fin.frame;
+    if (!talker_only && fin.frame > 0) predictor_kv->len = p->groups + 1;
+    if (fin.status != 0) return fail(c, (qtts_status)fin.status, "NaN logits during generation");
+    return QTTS_OK;
+}
+
+}  // extern "C"

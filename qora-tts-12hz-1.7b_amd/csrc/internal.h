@@ -1,0 +1,178 @@
+// internal.h — device-side data layout and kernel parameter blocks shared by
+// the HIP kernels (kernels.hip) and the host runtime (api.cpp).
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace qtts {
+
+// Repacked Q4 weight ("panel-major").  The reference stores packed[k][n/2]
+// and scales[k][n/32] (src/gemv.rs:26-31).  On the device the 32 output
+// columns of one scale group form a panel; panel p holds, for every input row
+// k, the 16 packed bytes of columns [32p, 32p+32) (same nibble order as the
+// reference) followed in a separate array by that row's binary16 scale:
+//   wq[p*K + k] = packed[k][16p .. 16p+16)     (one 128-bit load)
+//   ws[p*K + k] = scales[k][p]
+// A wavefront reading 64 consecutive rows of one panel reads 1 KiB of
+// contiguous weights and 128 B of contiguous scales.  Total bytes are exactly
+// the reference's Weight::memory_bytes().
+struct DevQ4 {
+    const uint4 *wq;
+    const uint16_t *ws;
+    int K;  // input rows
+    int N;  // output columns (multiple of 32); panels = N / 32
+};
+
+constexpr int kGemvThreads = 256;
+constexpr int kMaxM = 4;          // rows per GEMV launch (prefill chunks)
+constexpr int kMaxGroups = 15;    // predictor code groups
+constexpr int kAttnThreads = 256;
+constexpr int kAttnMaxChunk = 256;  // positions per attention split block
+constexpr int kMaxHeadDim = 128;
+constexpr int kSampleThreads = 1024;
+
+enum Prologue : int {
+    PRO_PLAIN = 0,    // x[m][k] = x[m*ldx + k]
+    PRO_RMSNORM = 1,  // x[m][k] = rms_norm_f16(src row m, gamma)[k]
+    PRO_EMBED = 2,    // x[0][k] = embed_lookup(emb, *emb_token)[k]
+};
+
+enum Epilogue : int {
+    EPI_STORE = 0,   // y[m*ldy + j] = gemv (+ bias[j])
+    EPI_RESID = 1,   // y[m*ldy + j] += gemv
+    EPI_SWIGLU = 2,  // y[m*ldy + j] = silu(gate_j) * up_j; gate = cols [0,N/2), up = [N/2,N)
+    EPI_QKV = 3,     // per head: QK-norm + RoPE, q -> y, k/v -> KV cache
+};
+
+enum Final : int {
+    FIN_NONE = 0,
+    FIN_ARGMAX = 1,  // after all groups: argmax of y[0..N) -> *argmax_out
+};
+
+struct GemvParams {
+    DevQ4 w;
+    int M;
+    int kc;   // K chunks (blocks per panel)
+    int rpt;  // rows per thread per chunk; chunk = 256*rpt rows
+    int prologue, epilogue, fin;
+    // input
+    const float *x;
+    int ldx;
+    const uint16_t *gamma;  // PRO_RMSNORM
+    int norm_src_row0;      // PRO_RMSNORM: source row of output row 0 (m -> row0 + m)
+    float *norm_out;        // PRO_RMSNORM: optional, receives the normed rows
+    int ldn;
+    DevQ4 emb;                   // PRO_EMBED
+    const uint32_t *emb_token;   // PRO_EMBED: device token index
+    // output
+    float *y;
+    int ldy;
+    const float *bias;
+    // EPI_QKV
+    int n_q_heads, n_kv_heads, head_dim;
+    const uint16_t *q_norm, *k_norm;
+    const float *rope_cos, *rope_sin;
+    int rope_rows;
+    int rope_skip_oob;
+    float *kcache, *vcache;  // this layer: [kv_heads][cap][head_dim]
+    int kv_cap;
+    const int *d_pos;  // rope position of row m = (*d_pos or pos_const) + m
+    int pos_const;
+    const int *d_kvlen;  // cache row of row m = (*d_kvlen or kvlen_const) + m
+    int kvlen_const;
+    // FIN_ARGMAX
+    uint32_t *argmax_out;
+    int *status;  // set to QTTS_ENAN on NaN
+    // scratch
+    float *partial;      // [kc][M][N]
+    unsigned *counters;  // [groups + 1], zero between launches
+    const int *d_done;   // skip the launch when *d_done != 0
+};
+
+struct AttnParams {
+    const float *q;  // [M][nq*hd]
+    int ldq;
+    const float *kcache, *vcache;  // this layer: [nkv][cap][hd]
+    int kv_cap;
+    int nq, nkv, hd;
+    const int *d_kvlen;  // cache length before this step's rows were appended
+    int kvlen_const;
+    int nsplit;
+    float scale;
+    float *part;         // [M][nq][nsplit][hd + 2]
+    unsigned *counters;  // [M][nkv]
+    float *out;          // [M][nq*hd]
+    int ldo;
+    const int *d_done;
+};
+
+// Device-resident state of one generation loop (one per talker).
+struct LoopState {
+    int pos;           // talker RoPE position
+    int kvlen;         // talker cache length
+    int frame;         // frames produced
+    int done;          // EOS seen (stop_on_eos) or error
+    int status;        // qtts_status of the device side
+    int pad0;
+    uint64_t rng;      // simple_rand state
+    uint32_t prev[16]; // prev_tokens
+    uint32_t cur[16];  // codes of the current frame
+};
+
+struct SampleParams {
+    const float *logits;
+    int vocab;
+    float temperature;
+    int top_k;
+    float penalty;
+    int greedy;
+    const uint32_t *prev;
+    int n_prev;
+    uint64_t *rng;
+    uint32_t *token_out;
+    int *status;
+    // loop integration (all optional)
+    int *done;
+    int stop_on_eos;
+    uint32_t eos;
+    uint32_t *codes;  // codes[frame] of group 0
+    const int *frame;
+    int max_codes;
+    uint32_t *prev_out;  // prev_tokens[0] = token
+};
+
+struct EmbSumParams {
+    int mode;                     // 0: full next-step input, 1: acoustic sum only
+    DevQ4 codec_emb;              // talker codec_embedding
+    DevQ4 group_emb[kMaxGroups];  // predictor codec_embeddings
+    int num_groups;
+    const uint32_t *cur;  // cur[0] = code0, cur[1+g] = acoustic code g
+    const float *trailing;
+    int trailing_len;
+    const float *pad;
+    const int *frame;
+    float *out;       // combined embedding
+    int hidden;
+    const int *d_done;
+    // frame bookkeeping: codes[g][frame] = cur[g], prev[g] = cur[g] for g >= 1
+    uint32_t *codes;
+    int max_codes;
+    uint32_t *prev;
+};
+
+// Launchers (kernels.hip).
+void launch_gemv(hipStream_t st, const GemvParams &p);
+void launch_attention(hipStream_t st, const AttnParams &p, int M);
+void launch_sample(hipStream_t st, const SampleParams &p);
+void launch_embed_row(hipStream_t st, const DevQ4 &w, const uint32_t *d_token, float *out, const int *d_done);
+void launch_embed_sum(hipStream_t st, const EmbSumParams &p);
+void launch_advance(hipStream_t st, LoopState *s, int frame_step);
+void launch_repack_q4(hipStream_t st, const uint8_t *packed, const uint16_t *scales, int K, int N, int col0,
+                      int Ntot, uint4 *wq, uint16_t *ws);
+
+// GEMV launch plan for a [K -> N] weight at M rows.
+void plan_gemv(int K, int N, int M, int *kc, int *rpt);
+
+}  // namespace qtts

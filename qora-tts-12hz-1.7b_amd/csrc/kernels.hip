@@ -1,0 +1,886 @@
+// kernels.hip — gfx950 kernels of the per-code loop.
+//
+//  k_gemv      Q4 GEMV/GEMM-by-rows over the panel-major layout: 128-bit
+//              coalesced weight loads, f32 accumulate, deterministic split-K
+//              (partials summed in chunk order by the last block of each
+//              output group), with fused prologues (RMSNorm, embedding
+//              gather) and epilogues (bias, residual add, SiLU*up, QK-norm +
+//              RoPE + KV append, argmax).
+//  k_attn      split-K flash-decode GQA attention over the device KV cache.
+//  k_sample    sample_token on one workgroup (bit-exact order of sums).
+//  k_embed_*   Q4 row dequant gathers and the combined next-step embedding.
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <cmath>
+
+#include "../../include/qtts.h"
+#include "internal.h"
+
+namespace qtts {
+
+namespace {
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+// Sum over a 256-thread block; every thread gets the result.
+__device__ float block_sum_256(float v, float *scratch /* >= 4 */) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) scratch[wave] = v;
+    __syncthreads();
+    float t = 0.0f;
+#pragma unroll
+    for (int w = 0; w < 4; w++) t += scratch[w];
+    return t;
+}
+
+// One Q4 nibble contributes (scale*x) * (nib - 8) to its output column
+// (the reference's LUT entry, src/gemv.rs:239-256).
+template <int M>
+__device__ __forceinline__ void q4_accumulate(const uint4 wv, const float s, const float (&xv)[M],
+                                              float (&acc)[M][32]) {
+    float sx[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) sx[m] = s * xv[m];
+    const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+#pragma unroll
+        for (int b = 0; b < 8; b++) {
+            const float q = (float)((int)((wd[d] >> (4 * b)) & 15u) - 8);
+#pragma unroll
+            for (int m = 0; m < M; m++) acc[m][d * 8 + b] = fmaf(sx[m], q, acc[m][d * 8 + b]);
+        }
+    }
+}
+
+}  // namespace
+
+// ---------------------------------------------------------------------------
+// Q4 GEMV
+// ---------------------------------------------------------------------------
+template <int M, int RPT>
+__global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvParams P) {
+    if (P.d_done && *P.d_done) return;
+    __shared__ float red[kGemvThreads * 33];
+    __shared__ float part8[8 * 32];
+    __shared__ float ybuf[kMaxM * 128];
+    __shared__ float scratch[8];
+    __shared__ int s_last;
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int K = P.w.K, N = P.w.N;
+    const int p = blockIdx.x / P.kc;
+    const int c = blockIdx.x - p * P.kc;
+    const int k0 = c * (kGemvThreads * RPT);
+
+    // 1. weight rows of this chunk: one 128-bit load + one scale per row.
+    uint4 wv[RPT];
+    uint16_t sv[RPT];
+#pragma unroll
+    for (int i = 0; i < RPT; i++) {
+        const int k = k0 + tid + i * kGemvThreads;
+        if (k < K) {
+            wv[i] = P.w.wq[(size_t)p * K + k];
+            sv[i] = P.w.ws[(size_t)p * K + k];
+        } else {
+            wv[i] = make_uint4(0u, 0u, 0u, 0u);
+            sv[i] = 0;
+        }
+    }
+
+    // 2. input values of those rows.
+    float xv[RPT][M];
+    if (P.prologue == PRO_RMSNORM) {
+        // rms_norm_f16 (src/gemv.rs:406-417); each wave computes the full
+        // sum of squares itself, so no block barrier sits behind the loads.
+        float inv[M];
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            const float *src = P.x + (size_t)(P.norm_src_row0 + m) * P.ldx;
+            float ss = 0.0f;
+            for (int j = lane * 4; j < K; j += 256) {
+                const float4 v = *reinterpret_cast<const float4 *>(src + j);
+                ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
+            }
+            ss = wave_sum(ss);
+            inv[m] = 1.0f / sqrtf(ss / (float)K + 1e-6f);
+        }
+#pragma unroll
+        for (int i = 0; i < RPT; i++) {
+            const int k = k0 + tid + i * kGemvThreads;
+            if (k < K) {
+                const float g = f16_to_f32(P.gamma[k]);
+#pragma unroll
+                for (int m = 0; m < M; m++) {
+                    const float v = P.x[(size_t)(P.norm_src_row0 + m) * P.ldx + k] * inv[m] * g;
+                    xv[i][m] = v;
+                    if (P.norm_out && p == 0) P.norm_out[(size_t)m * P.ldn + k] = v;
+                }
+            } else {
+#pragma unroll
+                for (int m = 0; m < M; m++) xv[i][m] = 0.0f;
+            }
+        }
+    } else if (P.prologue == PRO_EMBED) {
+        // embed_lookup_q4 (src/gemv.rs:377-400) of row *emb_token.
+        const uint32_t tok = *P.emb_token;
+        const uint8_t *eb = reinterpret_cast<const uint8_t *>(P.emb.wq);
+#pragma unroll
+        for (int i = 0; i < RPT; i++) {
+            const int k = k0 + tid + i * kGemvThreads;
+            float v = 0.0f;
+            if (k < K && tok < (uint32_t)P.emb.K) {
+                const size_t row = (size_t)(k >> 5) * P.emb.K + tok;
+                const uint8_t byte = eb[row * 16 + ((k & 31) >> 1)];
+                const int nib = (k & 1) ? (byte >> 4) : (byte & 15);
+                v = f16_to_f32(P.emb.ws[row]) * (float)(nib - 8);
+            }
+#pragma unroll
+            for (int m = 0; m < M; m++) xv[i][m] = v;
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < RPT; i++) {
+            const int k = k0 + tid + i * kGemvThreads;
+#pragma unroll
+            for (int m = 0; m < M; m++) xv[i][m] = k < K ? P.x[(size_t)m * P.ldx + k] : 0.0f;
+        }
+    }
+
+    // 3. accumulate 32 columns per thread.
+    float acc[M][32];
+#pragma unroll
+    for (int m = 0; m < M; m++)
+#pragma unroll
+        for (int j = 0; j < 32; j++) acc[m][j] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < RPT; i++) q4_accumulate<M>(wv[i], f16_to_f32(sv[i]), xv[i], acc);
+
+    // 4. block reduction -> this chunk's partial for the panel's 32 columns.
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+#pragma unroll
+        for (int j = 0; j < 32; j++) red[tid * 33 + j] = acc[m][j];
+        __syncthreads();
+        {
+            const int col = tid & 31, part = tid >> 5;
+            float s = 0.0f;
+#pragma unroll 8
+            for (int r = 0; r < 32; r++) s += red[(part * 32 + r) * 33 + col];
+            part8[part * 32 + col] = s;
+        }
+        __syncthreads();
+        if (tid < 32) {
+            float s = 0.0f;
+#pragma unroll
+            for (int q = 0; q < 8; q++) s += part8[q * 32 + tid];
+            P.partial[((size_t)c * M + m) * N + p * 32 + tid] = s;
+        }
+    }
+
+    // 5. the last block of an output group sums the chunks in order.
+    int gp, group;
+    if (P.epilogue == EPI_SWIGLU) {
+        const int half = N / 64;
+        gp = 2;
+        group = p % half;
+    } else if (P.epilogue == EPI_QKV) {
+        gp = P.head_dim / 32;
+        group = p / gp;
+    } else {
+        gp = 1;
+        group = p;
+    }
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) s_last = atomicAdd(&P.counters[group], 1u) == (unsigned)(gp * P.kc - 1);
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    if (tid == 0) P.counters[group] = 0u;
+
+    const int gcols = gp * 32;
+    for (int idx = tid; idx < M * gcols; idx += kGemvThreads) {
+        const int m = idx / gcols, j = idx - m * gcols;
+        int col;
+        if (P.epilogue == EPI_SWIGLU)
+            col = (j < 32) ? group * 32 + j : N / 2 + group * 32 + (j - 32);
+        else
+            col = group * gcols + j;
+        float s = 0.0f;
+        for (int cc = 0; cc < P.kc; cc++) s += P.partial[((size_t)cc * M + m) * N + col];
+        ybuf[m * gcols + j] = s;
+    }
+    __syncthreads();
+
+    // 6. epilogue
+    if (P.epilogue == EPI_STORE) {
+        for (int idx = tid; idx < M * 32; idx += kGemvThreads) {
+            const int m = idx >> 5, j = idx & 31, col = group * 32 + j;
+            float v = ybuf[m * 32 + j];
+            if (P.bias) v += P.bias[col];
+            P.y[(size_t)m * P.ldy + col] = v;
+        }
+    } else if (P.epilogue == EPI_RESID) {
+        for (int idx = tid; idx < M * 32; idx += kGemvThreads) {
+            const int m = idx >> 5, j = idx & 31, col = group * 32 + j;
+            P.y[(size_t)m * P.ldy + col] += ybuf[m * 32 + j];
+        }
+    } else if (P.epilogue == EPI_SWIGLU) {
+        // silu(g) * u, src/talker.rs:342-345, silu = g / (1 + exp(-g)).
+        for (int idx = tid; idx < M * 32; idx += kGemvThreads) {
+            const int m = idx >> 5, j = idx & 31;
+            const float g = ybuf[m * 64 + j], u = ybuf[m * 64 + 32 + j];
+            P.y[(size_t)m * P.ldy + group * 32 + j] = (g / (1.0f + expf(-g))) * u;
+        }
+    } else if (P.epilogue == EPI_QKV) {
+        // apply_qk_norm (src/talker.rs:86-99) + split-half RoPE
+        // (src/rope.rs:79-92) + KV append (src/talker.rs:299-302).
+        const int hd = P.head_dim, half = hd / 2;
+        const int head = group;
+        const bool is_q = head < P.n_q_heads;
+        const bool is_k = !is_q && head < P.n_q_heads + P.n_kv_heads;
+        for (int m = 0; m < M; m++) {
+            const int pos = (P.d_pos ? *P.d_pos : P.pos_const) + m;
+            const int row = (P.d_kvlen ? *P.d_kvlen : P.kvlen_const) + m;
+            float *vals = ybuf + m * gcols;
+            if (is_q || is_k) {
+                const float v = tid < hd ? vals[tid] : 0.0f;
+                const float ss = block_sum_256(v * v, scratch);
+                const float inv = 1.0f / sqrtf(ss / (float)hd + 1e-6f);
+                const uint16_t *gam = is_q ? P.q_norm : P.k_norm;
+                float nv = 0.0f;
+                if (tid < hd) nv = v * inv * f16_to_f32(gam[tid]);
+                __syncthreads();
+                if (tid < hd) vals[tid] = nv;
+                __syncthreads();
+                const bool rotate = !(P.rope_skip_oob && pos >= P.rope_rows);
+                if (tid < half) {
+                    const float x1 = vals[tid], x2 = vals[tid + half];
+                    float o1 = x1, o2 = x2;
+                    if (rotate) {
+                        const float cs = P.rope_cos[(size_t)pos * half + tid];
+                        const float sn = P.rope_sin[(size_t)pos * half + tid];
+                        o1 = x1 * cs - x2 * sn;
+                        o2 = x2 * cs + x1 * sn;
+                    }
+                    if (is_q) {
+                        P.y[(size_t)m * P.ldy + head * hd + tid] = o1;
+                        P.y[(size_t)m * P.ldy + head * hd + tid + half] = o2;
+                    } else {
+                        const int kh = head - P.n_q_heads;
+                        float *dst = P.kcache + ((size_t)kh * P.kv_cap + row) * hd;
+                        dst[tid] = o1;
+                        dst[tid + half] = o2;
+                    }
+                }
+                __syncthreads();
+            } else {
+                const int vh = head - P.n_q_heads - P.n_kv_heads;
+                if (tid < hd) P.vcache[((size_t)vh * P.kv_cap + row) * hd + tid] = vals[tid];
+            }
+        }
+    }
+
+    // 7. kernel-wide final step
+    if (P.fin == FIN_ARGMAX) {
+        const int ngroups = N / 32;
+        __threadfence();
+        __syncthreads();
+        if (tid == 0) s_last = atomicAdd(&P.counters[ngroups], 1u) == (unsigned)(ngroups - 1);
+        __syncthreads();
+        if (!s_last) return;
+        __threadfence();
+        if (tid == 0) P.counters[ngroups] = 0u;
+        // sample_argmax (src/code_predictor.rs:328-334): last index of the max.
+        float bv = -INFINITY;
+        int bi = -1, nan = 0;
+        for (int i = tid; i < N; i += kGemvThreads) {
+            const float v = P.y[i];
+            if (v != v)
+                nan = 1;
+            else if (bi < 0 || v >= bv) {
+                bv = v;
+                bi = i;
+            }
+        }
+        __shared__ float sv_[kGemvThreads];
+        __shared__ int si_[kGemvThreads];
+        __shared__ int snan;
+        if (tid == 0) snan = 0;
+        __syncthreads();
+        if (nan) atomicOr(&snan, 1);
+        sv_[tid] = bv;
+        si_[tid] = bi;
+        __syncthreads();
+        for (int st = kGemvThreads / 2; st > 0; st >>= 1) {
+            if (tid < st) {
+                const float ov = sv_[tid + st];
+                const int oi = si_[tid + st];
+                if (oi >= 0 && (si_[tid] < 0 || ov > sv_[tid] || (ov == sv_[tid] && oi > si_[tid]))) {
+                    sv_[tid] = ov;
+                    si_[tid] = oi;
+                }
+            }
+            __syncthreads();
+        }
+        if (tid == 0) {
+            if (snan) {
+                *P.argmax_out = 0u;
+                if (P.status) *P.status = QTTS_ENAN;
+            } else {
+                *P.argmax_out = (uint32_t)(si_[0] < 0 ? 0 : si_[0]);
+            }
+        }
+    }
+}
+
+void plan_gemv(int K, int N, int M, int *kc, int *rpt) {
+    const int panels = N / 32;
+    int r = 1;
+    const int cands[3] = {4, 2, 1};
+    for (int ci = 0; ci < 3; ci++) {
+        r = cands[ci];
+        const int c = (K + kGemvThreads * r - 1) / (kGemvThreads * r);
+        if (panels * c >= 512) break;
+    }
+    (void)M;
+    *rpt = r;
+    *kc = (K + kGemvThreads * r - 1) / (kGemvThreads * r);
+}
+
+template <int M>
+static void launch_gemv_m(hipStream_t st, const GemvParams &p) {
+    const dim3 grid((unsigned)((p.w.N / 32) * p.kc));
+    switch (p.rpt) {
+        case 4: hipLaunchKernelGGL((k_gemv<M, 4>), grid, dim3(kGemvThreads), 0, st, p); break;
+        case 2: hipLaunchKernelGGL((k_gemv<M, 2>), grid, dim3(kGemvThreads), 0, st, p); break;
+        default: hipLaunchKernelGGL((k_gemv<M, 1>), grid, dim3(kGemvThreads), 0, st, p); break;
+    }
+}
+
+void launch_gemv(hipStream_t st, const GemvParams &p) {
+    switch (p.M) {
+        case 1: launch_gemv_m<1>(st, p); break;
+        case 2: launch_gemv_m<2>(st, p); break;
+        case 3: launch_gemv_m<3>(st, p); break;
+        default: launch_gemv_m<4>(st, p); break;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Attention: one block per (kv head, split, query row).  Both query heads of
+// a GQA group share the K/V reads.  Softmax partials (max, sum, unnormalised
+// P.V) are combined in split order by the last block of the kv head.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams P) {
+    if (P.d_done && *P.d_done) return;
+    constexpr int HD = 128;
+    constexpr int GMAX = 4;
+    __shared__ float qs[GMAX][HD];
+    __shared__ float sc[GMAX][kAttnMaxChunk];
+    __shared__ float pv[GMAX][HD];
+    __shared__ float mloc[GMAX], lloc[GMAX];
+    __shared__ int s_last;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int m = blockIdx.y;
+    const int kvh = blockIdx.x / P.nsplit, sp = blockIdx.x - kvh * P.nsplit;
+    const int G = P.nq / P.nkv;
+    const int L = (P.d_kvlen ? *P.d_kvlen : P.kvlen_const) + m + 1;
+    const int chunk = (L + P.nsplit - 1) / P.nsplit;
+    const int t0 = sp * chunk;
+    const int t1 = min(L, t0 + chunk);
+    const int nt = max(0, t1 - t0);
+
+    for (int idx = tid; idx < G * HD; idx += kAttnThreads) {
+        const int g = idx / HD, d = idx - g * HD;
+        qs[g][d] = P.q[(size_t)m * P.ldq + (size_t)(kvh * G + g) * HD + d];
+    }
+    __syncthreads();
+
+    const float *Kb = P.kcache + (size_t)kvh * P.kv_cap * HD;
+    const float *Vb = P.vcache + (size_t)kvh * P.kv_cap * HD;
+
+    // scores: 16 lanes per position, 8 dims per lane.
+    {
+        const int l16 = tid & 15, slot = tid >> 4;
+        for (int tt = slot; tt < nt; tt += kAttnThreads / 16) {
+            const float *kr = Kb + (size_t)(t0 + tt) * HD + l16 * 8;
+            const float4 a = *reinterpret_cast<const float4 *>(kr);
+            const float4 b = *reinterpret_cast<const float4 *>(kr + 4);
+            for (int g = 0; g < G; g++) {
+                const float *qq = &qs[g][l16 * 8];
+                float dot = qq[0] * a.x + qq[1] * a.y + qq[2] * a.z + qq[3] * a.w + qq[4] * b.x + qq[5] * b.y +
+                            qq[6] * b.z + qq[7] * b.w;
+                dot += __shfl_xor(dot, 8, 16);
+                dot += __shfl_xor(dot, 4, 16);
+                dot += __shfl_xor(dot, 2, 16);
+                dot += __shfl_xor(dot, 1, 16);
+                if (l16 == 0) sc[g][tt] = dot * P.scale;
+            }
+        }
+    }
+    __syncthreads();
+    // local softmax statistics, one wave per query head.
+    for (int g = wave; g < G; g += kAttnThreads / 64) {
+        float mx = -INFINITY;
+        for (int t = lane; t < nt; t += 64) mx = fmaxf(mx, sc[g][t]);
+        mx = wave_max(mx);
+        float l = 0.0f;
+        for (int t = lane; t < nt; t += 64) {
+            const float e = expf(sc[g][t] - mx);
+            sc[g][t] = e;
+            l += e;
+        }
+        l = wave_sum(l);
+        if (lane == 0) {
+            mloc[g] = nt > 0 ? mx : -INFINITY;
+            lloc[g] = l;
+        }
+    }
+    __syncthreads();
+    // P.V: thread (d, half) walks every other position.
+    {
+        const int d = tid & (HD - 1), hf = tid >> 7;
+        float acc[GMAX] = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int tt = hf; tt < nt; tt += 2) {
+            const float v = Vb[(size_t)(t0 + tt) * HD + d];
+            for (int g = 0; g < G; g++) acc[g] += sc[g][tt] * v;
+        }
+        if (hf == 1)
+            for (int g = 0; g < G; g++) pv[g][d] = acc[g];
+        __syncthreads();
+        if (hf == 0) {
+            for (int g = 0; g < G; g++) {
+                const int h = kvh * G + g;
+                float *dst = P.part + (((size_t)m * P.nq + h) * P.nsplit + sp) * (HD + 2);
+                dst[2 + d] = acc[g] + pv[g][d];
+                if (d == 0) {
+                    dst[0] = mloc[g];
+                    dst[1] = lloc[g];
+                }
+            }
+        }
+    }
+    __threadfence();
+    __syncthreads();
+    if (tid == 0) s_last = atomicAdd(&P.counters[m * P.nkv + kvh], 1u) == (unsigned)(P.nsplit - 1);
+    __syncthreads();
+    if (!s_last) return;
+    __threadfence();
+    if (tid == 0) P.counters[m * P.nkv + kvh] = 0u;
+    for (int idx = tid; idx < G * HD; idx += kAttnThreads) {
+        const int g = idx / HD, d = idx - g * HD;
+        const int h = kvh * G + g;
+        const float *base = P.part + ((size_t)m * P.nq + h) * P.nsplit * (HD + 2);
+        float mx = -INFINITY;
+        for (int s = 0; s < P.nsplit; s++) mx = fmaxf(mx, base[s * (HD + 2)]);
+        float o = 0.0f, l = 0.0f;
+        for (int s = 0; s < P.nsplit; s++) {
+            const float ms = base[s * (HD + 2)];
+            if (ms == -INFINITY) continue;
+            const float w = expf(ms - mx);
+            o += w * base[s * (HD + 2) + 2 + d];
+            l += w * base[s * (HD + 2) + 1];
+        }
+        P.out[(size_t)m * P.ldo + (size_t)h * HD + d] = o / l;
+    }
+}
+
+void launch_attention(hipStream_t st, const AttnParams &p, int M) {
+    hipLaunchKernelGGL(k_attn, dim3((unsigned)(p.nkv * p.nsplit), (unsigned)M), dim3(kAttnThreads), 0, st, p);
+}
+
+// ---------------------------------------------------------------------------
+// Sampler: sample_token (src/generate_new.rs:329-391) on one workgroup.  The
+// three order-dependent f32 sums (softmax denominator, top-k renormaliser,
+// cumulative sum) run sequentially in index order on one lane, as in the
+// reference; everything else is order-independent and runs in parallel.
+// exp is evaluated in double and rounded once to float (glibc's expf is
+// accurate to 0.502 ulp, so both agree except within ~0.002 ulp of a
+// rounding boundary).
+// ---------------------------------------------------------------------------
+namespace {
+
+// Exclusive scan over a 1024-thread block.
+__device__ int block_exscan_1024(int v, int *wsum /* >= 16 */, int *total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int x = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(x, off, 64);
+        if (lane >= off) x += y;
+    }
+    __syncthreads();
+    if (lane == 63) wsum[wave] = x;
+    __syncthreads();
+    int base = 0, tot = 0;
+    for (int w = 0; w < (int)(blockDim.x >> 6); w++) {
+        if (w < wave) base += wsum[w];
+        tot += wsum[w];
+    }
+    *total = tot;
+    return base + x - v;
+}
+
+__device__ __forceinline__ float simple_rand_dev(uint64_t *state) {
+    uint64_t s = *state;
+    s ^= s << 13;
+    s ^= s >> 7;
+    s ^= s << 17;
+    *state = s;
+    return (float)s / 18446744073709551616.0f;  // (u64::MAX as f32) == 2^64
+}
+
+}  // namespace
+
+__global__ __launch_bounds__(kSampleThreads) void k_sample(SampleParams P) {
+    if (P.done && *P.done) return;
+    extern __shared__ unsigned char smem_raw[];
+    float *s = reinterpret_cast<float *>(smem_raw);
+    int *list = reinterpret_cast<int *>(s + P.vocab);
+    __shared__ unsigned hist[256];
+    __shared__ int wsum[16];
+    __shared__ float fred[16];
+    __shared__ int ired[16];
+    __shared__ float s_max, s_sum;
+    __shared__ unsigned s_prefix, s_mask;
+    __shared__ int s_remaining, s_nan, s_count;
+    __shared__ uint32_t s_token;
+
+    const int V = P.vocab, tid = threadIdx.x, nthr = blockDim.x;
+    const int lane = tid & 63, wave = tid >> 6, nwaves = nthr >> 6;
+    for (int i = tid; i < V; i += nthr) s[i] = P.logits[i];
+    if (tid == 0) {
+        s_nan = 0;
+        s_token = 0;
+    }
+    __syncthreads();
+    if (tid == 0 && P.penalty != 1.0f) {
+        for (int j = 0; j < P.n_prev; j++) {
+            const uint32_t t = P.prev[j];
+            if (t < (uint32_t)V) {
+                if (s[t] > 0.0f)
+                    s[t] /= P.penalty;
+                else
+                    s[t] *= P.penalty;
+            }
+        }
+    }
+    __syncthreads();
+
+    if (P.greedy) {
+        // argmax with the last index winning ties (src/generate.rs:51-56).
+        float bv = -INFINITY;
+        int bi = -1, nan = 0;
+        for (int i = tid; i < V; i += nthr) {
+            const float v = s[i];
+            if (v != v)
+                nan = 1;
+            else if (bi < 0 || v >= bv) {
+                bv = v;
+                bi = i;
+            }
+        }
+        if (nan) atomicOr(&s_nan, 1);
+        for (int off = 32; off >= 1; off >>= 1) {
+            const float ov = __shfl_xor(bv, off, 64);
+            const int oi = __shfl_xor(bi, off, 64);
+            if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi > bi))) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        if (lane == 0) {
+            fred[wave] = bv;
+            ired[wave] = bi;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            float b = -INFINITY;
+            int ix = -1;
+            for (int w = 0; w < nwaves; w++) {
+                if (ired[w] >= 0 && (ix < 0 || fred[w] > b || (fred[w] == b && ired[w] > ix))) {
+                    b = fred[w];
+                    ix = ired[w];
+                }
+            }
+            s_token = ix < 0 ? 0u : (uint32_t)ix;
+        }
+        __syncthreads();
+    } else {
+        if (P.temperature != 1.0f)
+            for (int i = tid; i < V; i += nthr) s[i] /= P.temperature;
+        // max (fold with f32::max: NaN is ignored)
+        float mx = -INFINITY;
+        for (int i = tid; i < V; i += nthr) mx = fmaxf(mx, s[i]);
+        mx = wave_max(mx);
+        if (lane == 0) fred[wave] = mx;
+        __syncthreads();
+        if (tid == 0) {
+            float t = -INFINITY;
+            for (int w = 0; w < nwaves; w++) t = fmaxf(t, fred[w]);
+            s_max = t;
+        }
+        __syncthreads();
+        const float maxv = s_max;
+        for (int i = tid; i < V; i += nthr) s[i] = (float)exp((double)(s[i] - maxv));
+        __syncthreads();
+        if (tid == 0) {
+            float sum = 0.0f;
+            for (int i = 0; i < V; i++) sum += s[i];
+            s_sum = sum;
+        }
+        __syncthreads();
+        const float sum = s_sum;
+        for (int i = tid; i < V; i += nthr) s[i] = s[i] / sum;
+        __syncthreads();
+
+        const bool topk = P.top_k > 0 && P.top_k < V;
+        if (topk) {
+            // The stable descending sort keeps entry i iff
+            //   #{j: s_j > s_i} + #{j < i: s_j == s_i} < top_k.
+            // Find the top_k-th largest key by MSB-first radix select over
+            // the float bits (all values are >= 0, so bits order as values).
+            int nan = 0;
+            for (int i = tid; i < V; i += nthr)
+                if (s[i] != s[i]) nan = 1;
+            if (nan) atomicOr(&s_nan, 1);
+            if (tid == 0) {
+                s_prefix = 0u;
+                s_mask = 0u;
+                s_remaining = P.top_k;
+            }
+            __syncthreads();
+            if (!s_nan) {
+                for (int pass = 0; pass < 4; pass++) {
+                    const int shift = 24 - 8 * pass;
+                    for (int b = tid; b < 256; b += nthr) hist[b] = 0u;
+                    __syncthreads();
+                    const unsigned prefix = s_prefix, mask = s_mask;
+                    for (int i = tid; i < V; i += nthr) {
+                        const unsigned key = __float_as_uint(s[i]);
+                        if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+                    }
+                    __syncthreads();
+                    if (tid == 0) {
+                        int cum = 0, sel = 0;
+                        const int rem = s_remaining;
+                        for (int d = 255; d >= 0; d--) {
+                            if (cum + (int)hist[d] >= rem) {
+                                sel = d;
+                                break;
+                            }
+                            cum += (int)hist[d];
+                        }
+                        s_remaining = rem - cum;
+                        s_prefix = prefix | ((unsigned)sel << shift);
+                        s_mask = mask | (255u << shift);
+                    }
+                    __syncthreads();
+                }
+                const unsigned T = s_prefix;
+                const int need_eq = s_remaining;
+                // contiguous ownership keeps index order for the scans
+                const int per = (V + nthr - 1) / nthr;
+                const int i0 = min(V, tid * per), i1 = min(V, i0 + per);
+                int neq = 0;
+                for (int i = i0; i < i1; i++) neq += (__float_as_uint(s[i]) == T);
+                int tot;
+                int eq_rank = block_exscan_1024(neq, wsum, &tot);
+                int nkeep = 0;
+                unsigned keep_bits = 0u;  // per <= 32
+                for (int i = i0; i < i1; i++) {
+                    const unsigned key = __float_as_uint(s[i]);
+                    bool keep = key > T;
+                    if (key == T) {
+                        keep = eq_rank < need_eq;
+                        eq_rank++;
+                    }
+                    if (keep) {
+                        keep_bits |= 1u << (i - i0);
+                        nkeep++;
+                    }
+                }
+                __syncthreads();
+                int pos = block_exscan_1024(nkeep, wsum, &tot);
+                for (int i = i0; i < i1; i++)
+                    if (keep_bits & (1u << (i - i0))) list[pos++] = i;
+                if (tid == 0) s_count = tot;
+                __syncthreads();
+                if (tid == 0) {
+                    const int cnt = s_count;
+                    float sum2 = 0.0f;
+                    for (int j = 0; j < cnt; j++) sum2 += s[list[j]];
+                    const float r = simple_rand_dev(P.rng);
+                    float cumsum = 0.0f;
+                    uint32_t tok = 0u;
+                    for (int j = 0; j < cnt; j++) {
+                        const float pj = sum2 > 0.0f ? s[list[j]] / sum2 : s[list[j]];
+                        cumsum += pj;
+                        if (r < cumsum) {
+                            tok = (uint32_t)list[j];
+                            break;
+                        }
+                    }
+                    s_token = tok;
+                }
+            }
+            __syncthreads();
+        } else {
+            if (tid == 0) {
+                const float r = simple_rand_dev(P.rng);
+                float cumsum = 0.0f;
+                uint32_t tok = 0u;
+                for (int i = 0; i < V; i++) {
+                    cumsum += s[i];
+                    if (r < cumsum) {
+                        tok = (uint32_t)i;
+                        break;
+                    }
+                }
+                s_token = tok;
+            }
+            __syncthreads();
+        }
+    }
+
+    if (tid == 0) {
+        uint32_t tok = s_token;
+        if (s_nan) {
+            tok = 0u;
+            if (P.status) *P.status = QTTS_ENAN;
+            if (P.done) *P.done = 1;
+        } else if (P.done && P.stop_on_eos && tok == P.eos) {
+            *P.done = 1;
+        } else {
+            if (P.codes && P.frame) {
+                const int f = *P.frame;
+                if (f < P.max_codes) P.codes[f] = tok;
+            }
+            if (P.prev_out) P.prev_out[0] = tok;
+        }
+        *P.token_out = tok;
+    }
+}
+
+void launch_sample(hipStream_t st, const SampleParams &p) {
+    const size_t smem = (size_t)p.vocab * (sizeof(float) + sizeof(int));
+    hipLaunchKernelGGL(k_sample, dim3(1), dim3(kSampleThreads), smem, st, p);
+}
+
+// ---------------------------------------------------------------------------
+// Embedding gathers
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float q4_element(const DevQ4 &w, uint32_t row, int col) {
+    const size_t r = (size_t)(col >> 5) * w.K + row;
+    const uint8_t byte = reinterpret_cast<const uint8_t *>(w.wq)[r * 16 + ((col & 31) >> 1)];
+    const int nib = (col & 1) ? (byte >> 4) : (byte & 15);
+    return f16_to_f32(w.ws[r]) * (float)(nib - 8);
+}
+
+__global__ void k_embed_row(DevQ4 w, const uint32_t *tok, float *out, const int *d_done) {
+    if (d_done && *d_done) return;
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= w.N) return;
+    const uint32_t t = *tok;
+    out[j] = t < (uint32_t)w.K ? q4_element(w, t, j) : 0.0f;
+}
+
+void launch_embed_row(hipStream_t st, const DevQ4 &w, const uint32_t *d_token, float *out, const int *d_done) {
+    hipLaunchKernelGGL(k_embed_row, dim3((unsigned)((w.N + 255) / 256)), dim3(256), 0, st, w, d_token, out, d_done);
+}
+
+// Next talker input: codec_emb[code0] + sum_g group_emb[g][code_g] + text row
+// (src/generate_new.rs:270-286, src/code_predictor.rs:280-293), in the
+// reference's order of additions; the frame's codes are filed here too.
+__global__ void k_embed_sum(EmbSumParams P) {
+    if (P.d_done && *P.d_done) return;
+    const int j = blockIdx.x * blockDim.x + threadIdx.x;
+    const int frame = P.frame ? *P.frame : 0;
+    if (blockIdx.x == 0 && threadIdx.x < (unsigned)P.num_groups) {
+        const int g = threadIdx.x;
+        if (P.codes && frame < P.max_codes) P.codes[(size_t)(g + 1) * P.max_codes + frame] = P.cur[1 + g];
+        if (P.prev) P.prev[1 + g] = P.cur[1 + g];
+    }
+    if (j >= P.hidden) return;
+    if (P.mode == 1) {  // get_acoustic_embeddings_sum alone
+        float acc = 0.0f;
+        for (int g = 0; g < P.num_groups; g++) {
+            const uint32_t c = P.cur[1 + g];
+            acc += c < (uint32_t)P.group_emb[g].K ? q4_element(P.group_emb[g], c, j) : 0.0f;
+        }
+        P.out[j] = acc;
+        return;
+    }
+    const uint32_t c0 = P.cur[0];
+    float v = c0 < (uint32_t)P.codec_emb.K ? q4_element(P.codec_emb, c0, j) : 0.0f;
+    if (P.num_groups > 0) {
+        float acc = 0.0f;
+        for (int g = 0; g < P.num_groups; g++) {
+            const uint32_t c = P.cur[1 + g];
+            acc += c < (uint32_t)P.group_emb[g].K ? q4_element(P.group_emb[g], c, j) : 0.0f;
+        }
+        v += acc;
+        const float *text = frame < P.trailing_len ? P.trailing + (size_t)frame * P.hidden : P.pad;
+        v += text[j];
+    }
+    P.out[j] = v;
+}
+
+void launch_embed_sum(hipStream_t st, const EmbSumParams &p) {
+    hipLaunchKernelGGL(k_embed_sum, dim3((unsigned)((p.hidden + 255) / 256)), dim3(256), 0, st, p);
+}
+
+__global__ void k_advance(LoopState *s, int frame_step) {
+    if (s->done) return;
+    s->pos += 1;
+    s->kvlen += 1;
+    s->frame += frame_step;
+}
+
+void launch_advance(hipStream_t st, LoopState *s, int frame_step) {
+    hipLaunchKernelGGL(k_advance, dim3(1), dim3(1), 0, st, s, frame_step);
+}
+
+// ---------------------------------------------------------------------------
+// Upload-time repack: reference [K][N/2] + [K][N/32] -> panels [p0 + pl][K].
+// ---------------------------------------------------------------------------
+__global__ void k_repack(const uint8_t *packed, const uint16_t *scales, int K, int N, int p0, uint4 *wq,
+                         uint16_t *ws) {
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t panels = (size_t)(N / 32);
+    if (idx >= panels * (size_t)K) return;
+    const size_t pl = idx / (size_t)K, k = idx - pl * (size_t)K;
+    wq[((size_t)p0 + pl) * K + k] = *reinterpret_cast<const uint4 *>(packed + k * (size_t)(N / 2) + pl * 16);
+    ws[((size_t)p0 + pl) * K + k] = scales[k * panels + pl];
+}
+
+void launch_repack_q4(hipStream_t st, const uint8_t *packed, const uint16_t *scales, int K, int N, int col0,
+                      int Ntot, uint4 *wq, uint16_t *ws) {
+    (void)Ntot;
+    const size_t total = (size_t)(N / 32) * K;
+    hipLaunchKernelGGL(k_repack, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st, packed, scales, K, N,
+                       col0 / 32, wq, ws);
+}
+
+}  // namespace qtts

@@ -1,0 +1,626 @@
+"""Python mirror of the reference crate's per-code-loop API over the C-ABI.
+
+The reference (qora-tts 0.1.0, Rust) exposes its hot path as plain functions:
+``gemv``/``gemm`` (src/gemv.rs:148-162), ``forward_with_embedding``
+(src/talker.rs:263), ``prefill_talker_raw`` (src/talker.rs:364),
+``generate_acoustic_codes`` (src/code_predictor.rs:218), ``sample_token`` and
+the frame loop of ``generate_speech`` (src/generate_new.rs:191-391).  This
+module exposes the same names over ``lib/libqtts.so`` (include/qtts.h), plus
+the host-side weight containers in the reference layout and the seeded
+synthetic checkpoints used by the benchmark and tests.
+
+Everything here runs the HIP library; there is no CPU fallback.  Loading
+raises if the shared library has not been built.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import dataclasses
+import os
+from typing import List, Optional, Sequence
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "lib", "libqtts.so")
+
+QTTS_OK, QTTS_EINVAL, QTTS_ESHAPE, QTTS_ENOMEM, QTTS_EDEVICE, QTTS_ENAN, QTTS_ERANGE, QTTS_ESTATE = range(8)
+STATUS_NAMES = ["OK", "EINVAL", "ESHAPE", "ENOMEM", "EDEVICE", "ENAN", "ERANGE", "ESTATE"]
+
+# Special codec tokens, src/generate_new.rs:34-36.
+CODEC_PAD, CODEC_BOS, CODEC_EOS = 2148, 2149, 2150
+
+
+class QttsError(RuntimeError):
+    def __init__(self, status: int, message: str):
+        self.status = status
+        name = STATUS_NAMES[status] if 0 <= status < len(STATUS_NAMES) else str(status)
+        super().__init__(f"qtts {name}: {message}")
+
+
+# ---------------------------------------------------------------------------
+# ctypes mirror of include/qtts.h
+# ---------------------------------------------------------------------------
+class Q4View(C.Structure):
+    _fields_ = [("packed", C.c_void_p), ("scales", C.c_void_p), ("k", C.c_int32), ("n", C.c_int32)]
+
+
+class LayerView(C.Structure):
+    _fields_ = [(n, Q4View) for n in ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj")] + [
+        (n, C.c_void_p) for n in ("q_norm", "k_norm", "input_norm_gamma", "post_attn_norm_gamma")
+    ]
+
+
+class TalkerView(C.Structure):
+    _fields_ = [
+        ("num_layers", C.c_int32),
+        ("layers", C.POINTER(LayerView)),
+        ("codec_embedding", Q4View),
+        ("codec_head", Q4View),
+        ("final_norm_gamma", C.c_void_p),
+        ("hidden_size", C.c_int32),
+        ("num_heads", C.c_int32),
+        ("num_kv_heads", C.c_int32),
+        ("head_dim", C.c_int32),
+        ("rope_theta", C.c_double),
+        ("max_position", C.c_int32),
+    ]
+
+
+class PredictorView(C.Structure):
+    _fields_ = [
+        ("input_proj", Q4View),
+        ("input_proj_bias", C.c_void_p),
+        ("num_groups", C.c_int32),
+        ("codec_embeddings", C.POINTER(Q4View)),
+        ("num_layers", C.c_int32),
+        ("layers", C.POINTER(LayerView)),
+        ("lm_heads", C.POINTER(Q4View)),
+        ("final_norm_gamma", C.c_void_p),
+        ("hidden_size", C.c_int32),
+        ("num_heads", C.c_int32),
+        ("num_kv_heads", C.c_int32),
+        ("head_dim", C.c_int32),
+        ("rope_theta", C.c_double),
+        ("max_position", C.c_int32),
+    ]
+
+
+class SamplerParams(C.Structure):
+    _fields_ = [
+        ("temperature", C.c_float),
+        ("top_k", C.c_int32),
+        ("repetition_penalty", C.c_float),
+        ("greedy", C.c_int32),
+    ]
+
+
+class LoopParams(C.Structure):
+    _fields_ = [
+        ("max_codes", C.c_int32),
+        ("sampler", SamplerParams),
+        ("codec_eos_id", C.c_uint32),
+        ("stop_on_eos", C.c_int32),
+        ("talker_only", C.c_int32),
+    ]
+
+
+_lib = None
+
+
+def _ptr(a: Optional[np.ndarray]):
+    return None if a is None else C.c_void_p(a.ctypes.data)
+
+
+def load_library(path: str = LIB_PATH):
+    """Loads libqtts.so; raises if it is missing (no fallback path exists)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is not built; run __graft_entry__.build() first")
+    lib = C.CDLL(path)
+    vp, i32, u32, u64, f32p = C.c_void_p, C.c_int32, C.c_uint32, C.c_uint64, C.c_void_p
+    sig = {
+        "qtts_version": ([], C.c_char_p),
+        "qtts_ctx_create": ([i32, C.POINTER(vp)], i32),
+        "qtts_ctx_destroy": ([vp], None),
+        "qtts_last_error": ([vp], C.c_char_p),
+        "qtts_ctx_stream": ([vp], vp),
+        "qtts_ctx_synchronize": ([vp], i32),
+        "qtts_q4_upload": ([vp, C.POINTER(Q4View), C.POINTER(vp)], i32),
+        "qtts_q4_free": ([vp], None),
+        "qtts_q4_bytes": ([vp], C.c_size_t),
+        "qtts_gemv": ([vp, vp, f32p, f32p], i32),
+        "qtts_gemm": ([vp, vp, f32p, i32, f32p], i32),
+        "qtts_embed_lookup": ([vp, vp, i32, f32p], i32),
+        "qtts_gemv_device": ([vp, vp, vp, vp], i32),
+        "qtts_gemm_device": ([vp, vp, vp, i32, vp], i32),
+        "qtts_kv_create": ([vp, i32, i32, i32, i32, C.POINTER(vp)], i32),
+        "qtts_kv_free": ([vp], None),
+        "qtts_kv_len": ([vp], i32),
+        "qtts_kv_clear": ([vp], i32),
+        "qtts_kv_load": ([vp, f32p, f32p, i32], i32),
+        "qtts_kv_store": ([vp, f32p, f32p], i32),
+        "qtts_talker_upload": ([vp, C.POINTER(TalkerView), C.POINTER(vp)], i32),
+        "qtts_talker_free": ([vp], None),
+        "qtts_forward_with_embedding": ([vp, f32p, vp, i32, f32p], i32),
+        "qtts_prefill_talker_raw": ([vp, f32p, i32, vp, f32p], i32),
+        "qtts_apply_codec_head": ([vp, f32p, f32p], i32),
+        "qtts_embed_codec_token": ([vp, u32, f32p], i32),
+        "qtts_predictor_upload": ([vp, C.POINTER(PredictorView), C.POINTER(vp)], i32),
+        "qtts_predictor_free": ([vp], None),
+        "qtts_generate_acoustic_codes": ([vp, f32p, f32p, vp, vp], i32),
+        "qtts_get_acoustic_embeddings_sum": ([vp, vp, f32p], i32),
+        "qtts_sample_token": ([vp, f32p, i32, C.POINTER(SamplerParams), vp, i32, C.POINTER(u64), C.POINTER(u32)], i32),
+        "qtts_generate_codes": (
+            [vp, vp, vp, vp, f32p, f32p, i32, f32p, i32, f32p, C.POINTER(LoopParams), u64, vp, C.POINTER(i32)],
+            i32,
+        ),
+        "qtts_synth_u64": ([u64, u64, u64], u64),
+        "qtts_synth_q4": ([u64, u64, i32, i32, C.c_float, vp, vp], None),
+        "qtts_synth_normal_f32": ([u64, u64, C.c_int64, C.c_float, C.c_float, vp], None),
+        "qtts_synth_normal_f16": ([u64, u64, C.c_int64, C.c_float, C.c_float, vp], None),
+        "qtts_f32_to_f16": ([C.c_float], C.c_uint16),
+        "qtts_f16_to_f32": ([C.c_uint16], C.c_float),
+        "qtts_quantize_f32_to_q4": ([vp, i32, i32, vp, vp], None),
+    }
+    for name, (args, res) in sig.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = res
+    _lib = lib
+    return lib
+
+
+def exported_symbols() -> List[str]:
+    """Names the C-ABI headers declare (checked against the library)."""
+    return [
+        "qtts_version", "qtts_ctx_create", "qtts_ctx_destroy", "qtts_last_error", "qtts_ctx_stream",
+        "qtts_ctx_synchronize", "qtts_q4_upload", "qtts_q4_free", "qtts_q4_bytes", "qtts_gemv", "qtts_gemm",
+        "qtts_embed_lookup", "qtts_gemv_device", "qtts_gemm_device", "qtts_kv_create", "qtts_kv_free",
+        "qtts_kv_len", "qtts_kv_clear", "qtts_kv_load", "qtts_kv_store", "qtts_talker_upload", "qtts_talker_free",
+        "qtts_forward_with_embedding", "qtts_prefill_talker_raw", "qtts_apply_codec_head",
+        "qtts_embed_codec_token", "qtts_predictor_upload", "qtts_predictor_free", "qtts_generate_acoustic_codes",
+        "qtts_get_acoustic_embeddings_sum", "qtts_sample_token", "qtts_generate_codes", "qtts_synth_u64",
+        "qtts_synth_q4", "qtts_synth_normal_f32", "qtts_synth_normal_f16", "qtts_f32_to_f16", "qtts_f16_to_f32",
+        "qtts_quantize_f32_to_q4",
+    ]
+
+
+# ---------------------------------------------------------------------------
+# Host weights in the reference layout
+# ---------------------------------------------------------------------------
+def stream_id(name: str) -> int:
+    """Stable 64-bit id of a tensor name (FNV-1a) for the synthetic generator."""
+    h = 0xCBF29CE484222325
+    for b in name.encode():
+        h = ((h ^ b) * 0x100000001B3) & 0xFFFFFFFFFFFFFFFF
+    return h
+
+
+def synth_normal_f32(seed: int, name: str, count: int, mean: float = 0.0, std: float = 1.0) -> np.ndarray:
+    out = np.empty(count, dtype=np.float32)
+    load_library().qtts_synth_normal_f32(seed, stream_id(name), count, mean, std, _ptr(out))
+    return out
+
+
+def synth_normal_f16(seed: int, name: str, count: int, mean: float = 1.0, std: float = 0.1) -> np.ndarray:
+    out = np.empty(count, dtype=np.uint16)
+    load_library().qtts_synth_normal_f16(seed, stream_id(name), count, mean, std, _ptr(out))
+    return out
+
+
+class Q4Weight:
+    """Q4Weight (src/gemv.rs:26-31): packed [k][n/2] u8, scales [k][n/32] f16 bits."""
+
+    def __init__(self, packed: np.ndarray, scales: np.ndarray, k: int, n: int):
+        assert n % 32 == 0
+        self.packed = np.ascontiguousarray(packed, dtype=np.uint8).reshape(k, n // 2)
+        self.scales = np.ascontiguousarray(scales, dtype=np.uint16).reshape(k, n // 32)
+        self.k, self.n = k, n
+
+    @staticmethod
+    def synthetic(seed: int, name: str, k: int, n: int, scale_std: float = 0.02) -> "Q4Weight":
+        packed = np.empty((k, n // 2), dtype=np.uint8)
+        scales = np.empty((k, n // 32), dtype=np.uint16)
+        load_library().qtts_synth_q4(seed, stream_id(name), k, n, scale_std, _ptr(packed), _ptr(scales))
+        return Q4Weight(packed, scales, k, n)
+
+    @staticmethod
+    def quantize(data: np.ndarray) -> "Q4Weight":
+        """quantize_f32_to_q4 (src/gemv.rs:92-130)."""
+        data = np.ascontiguousarray(data, dtype=np.float32)
+        k, n = data.shape
+        packed = np.empty((k, n // 2), dtype=np.uint8)
+        scales = np.empty((k, n // 32), dtype=np.uint16)
+        load_library().qtts_quantize_f32_to_q4(_ptr(data), k, n, _ptr(packed), _ptr(scales))
+        return Q4Weight(packed, scales, k, n)
+
+    def nibbles(self) -> np.ndarray:
+        lo = self.packed & 0x0F
+        hi = self.packed >> 4
+        return np.stack([lo, hi], axis=-1).reshape(self.k, self.n)
+
+    def dequantize(self) -> np.ndarray:
+        """(nib - 8) * f32(scale), exactly as embed_lookup_q4 (src/gemv.rs:377-400)."""
+        s = self.scales.view(np.float16).astype(np.float32)
+        s = np.repeat(s, 32, axis=1)
+        return (self.nibbles().astype(np.int32) - 8).astype(np.float32) * s
+
+    def view(self) -> Q4View:
+        return Q4View(self.packed.ctypes.data, self.scales.ctypes.data, self.k, self.n)
+
+    @property
+    def memory_bytes(self) -> int:
+        return self.packed.size + 2 * self.scales.size
+
+
+@dataclasses.dataclass
+class StackConfig:
+    layers: int
+    hidden: int
+    heads: int
+    kv_heads: int
+    head_dim: int
+    inter: int
+    vocab: int
+    max_position: int
+    rope_theta: float = 1.0e6
+
+
+# The 1.7B shapes (src/config.rs:130-153, model/1.7B/config.json).
+TALKER_1P7B = StackConfig(layers=28, hidden=2048, heads=16, kv_heads=8, head_dim=128, inter=6144, vocab=3072,
+                          max_position=32768)
+PREDICTOR_1P7B = StackConfig(layers=5, hidden=1024, heads=16, kv_heads=8, head_dim=128, inter=3072, vocab=2048,
+                             max_position=65536)
+NUM_GROUPS = 15
+
+
+class LayerWeights:
+    """TalkerLayerWeights / PredictorLayerWeights (src/talker.rs:19-31)."""
+
+    def __init__(self, seed: int, prefix: str, cfg: StackConfig, scale_std: float = 0.02):
+        qd, kd = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+        w = lambda n, k, nn: Q4Weight.synthetic(seed, f"{prefix}.{n}", k, nn, scale_std)
+        self.q_proj = w("q_proj", cfg.hidden, qd)
+        self.k_proj = w("k_proj", cfg.hidden, kd)
+        self.v_proj = w("v_proj", cfg.hidden, kd)
+        self.o_proj = w("o_proj", qd, cfg.hidden)
+        self.gate_proj = w("gate_proj", cfg.hidden, cfg.inter)
+        self.up_proj = w("up_proj", cfg.hidden, cfg.inter)
+        self.down_proj = w("down_proj", cfg.inter, cfg.hidden)
+        self.q_norm = synth_normal_f16(seed, f"{prefix}.q_norm", cfg.head_dim)
+        self.k_norm = synth_normal_f16(seed, f"{prefix}.k_norm", cfg.head_dim)
+        self.input_norm_gamma = synth_normal_f16(seed, f"{prefix}.input_norm", cfg.hidden)
+        self.post_attn_norm_gamma = synth_normal_f16(seed, f"{prefix}.post_attn_norm", cfg.hidden)
+
+    def view(self) -> LayerView:
+        v = LayerView()
+        for n in ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj"):
+            setattr(v, n, getattr(self, n).view())
+        for n in ("q_norm", "k_norm", "input_norm_gamma", "post_attn_norm_gamma"):
+            setattr(v, n, getattr(self, n).ctypes.data)
+        return v
+
+    @property
+    def memory_bytes(self) -> int:
+        q4 = sum(getattr(self, n).memory_bytes for n in ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj",
+                                                         "up_proj", "down_proj"))
+        return q4 + 2 * (self.q_norm.size + self.k_norm.size + self.input_norm_gamma.size +
+                         self.post_attn_norm_gamma.size)
+
+
+class TalkerWeights:
+    """Decode-path part of TalkerWeights (src/talker.rs:33-56), random init."""
+
+    def __init__(self, seed: int, cfg: StackConfig = TALKER_1P7B, scale_std: float = 0.02):
+        self.cfg = cfg
+        self.layers = [LayerWeights(seed, f"talker.layers.{i}", cfg, scale_std) for i in range(cfg.layers)]
+        self.codec_embedding = Q4Weight.synthetic(seed, "talker.codec_embedding", cfg.vocab, cfg.hidden, scale_std)
+        self.codec_head = Q4Weight.synthetic(seed, "talker.codec_head", cfg.hidden, cfg.vocab, scale_std)
+        self.final_norm_gamma = synth_normal_f16(seed, "talker.final_norm", cfg.hidden)
+        self._keep = None
+
+    def view(self) -> TalkerView:
+        # Built once: the oracle keeps pointers into these ctypes arrays.
+        if self._keep is None:
+            arr = (LayerView * len(self.layers))(*[l.view() for l in self.layers])
+            c = self.cfg
+            v = TalkerView(len(self.layers), arr, self.codec_embedding.view(), self.codec_head.view(),
+                           self.final_norm_gamma.ctypes.data, c.hidden, c.heads, c.kv_heads, c.head_dim,
+                           c.rope_theta, c.max_position)
+            self._keep = (arr, v)
+        return self._keep[1]
+
+    @property
+    def memory_bytes(self) -> int:
+        return (sum(l.memory_bytes for l in self.layers) + self.codec_embedding.memory_bytes +
+                self.codec_head.memory_bytes + 2 * self.final_norm_gamma.size)
+
+
+class CodePredictorWeights:
+    """CodePredictorWeights (src/code_predictor.rs:28-46), random init."""
+
+    def __init__(self, seed: int, cfg: StackConfig = PREDICTOR_1P7B, talker_hidden: int = 2048,
+                 num_groups: int = NUM_GROUPS, scale_std: float = 0.02):
+        self.cfg = cfg
+        self.num_groups = num_groups
+        self.talker_hidden = talker_hidden
+        self.input_proj = Q4Weight.synthetic(seed, "cp.input_proj", talker_hidden, cfg.hidden, scale_std)
+        self.input_proj_bias = synth_normal_f32(seed, "cp.input_proj_bias", cfg.hidden, 0.0, 0.02)
+        self.codec_embeddings = [Q4Weight.synthetic(seed, f"cp.codec_embedding.{g}", cfg.vocab, talker_hidden,
+                                                    scale_std) for g in range(num_groups)]
+        self.layers = [LayerWeights(seed, f"cp.layers.{i}", cfg, scale_std) for i in range(cfg.layers)]
+        self.lm_heads = [Q4Weight.synthetic(seed, f"cp.lm_head.{g}", cfg.hidden, cfg.vocab, scale_std)
+                         for g in range(num_groups)]
+        self.final_norm_gamma = synth_normal_f16(seed, "cp.final_norm", cfg.hidden)
+        self._keep = None
+
+    def view(self) -> PredictorView:
+        # Built once: the oracle keeps pointers into these ctypes arrays.
+        if self._keep is None:
+            layers = (LayerView * len(self.layers))(*[l.view() for l in self.layers])
+            embs = (Q4View * self.num_groups)(*[e.view() for e in self.codec_embeddings])
+            heads = (Q4View * self.num_groups)(*[h.view() for h in self.lm_heads])
+            c = self.cfg
+            v = PredictorView(self.input_proj.view(), self.input_proj_bias.ctypes.data, self.num_groups, embs,
+                              len(self.layers), layers, heads, self.final_norm_gamma.ctypes.data, c.hidden,
+                              c.heads, c.kv_heads, c.head_dim, c.rope_theta, c.max_position)
+            self._keep = (layers, embs, heads, v)
+        return self._keep[3]
+
+    @property
+    def memory_bytes(self) -> int:
+        return (self.input_proj.memory_bytes + 4 * self.input_proj_bias.size +
+                sum(e.memory_bytes for e in self.codec_embeddings) + sum(l.memory_bytes for l in self.layers) +
+                sum(h.memory_bytes for h in self.lm_heads) + 2 * self.final_norm_gamma.size)
+
+
+# ---------------------------------------------------------------------------
+# Device objects
+# ---------------------------------------------------------------------------
+def _f32(a, n: Optional[int] = None) -> np.ndarray:
+    a = np.ascontiguousarray(a, dtype=np.float32)
+    if n is not None and a.size < n:
+        raise ValueError(f"expected at least {n} floats, got {a.size}")
+    return a
+
+
+class Context:
+    """One HIP device + stream (qtts_ctx)."""
+
+    def __init__(self, device: int = 0):
+        self.lib = load_library()
+        h = C.c_void_p()
+        st = self.lib.qtts_ctx_create(device, C.byref(h))
+        if st != QTTS_OK:
+            raise QttsError(st, f"qtts_ctx_create(device={device}) failed")
+        self.h = h
+
+    def check(self, st: int):
+        if st != QTTS_OK:
+            raise QttsError(st, self.lib.qtts_last_error(self.h).decode())
+
+    @property
+    def stream(self) -> int:
+        return self.lib.qtts_ctx_stream(self.h)
+
+    def synchronize(self):
+        self.check(self.lib.qtts_ctx_synchronize(self.h))
+
+    def close(self):
+        if self.h:
+            self.lib.qtts_ctx_destroy(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    # sample_token, src/generate_new.rs:329-391
+    def sample_token(self, logits, temperature=0.8, top_k=50, repetition_penalty=1.05, prev_tokens=(0,) * 16,
+                     rng: int = 0, greedy: bool = False):
+        """Returns (token, new_rng_state)."""
+        lg = _f32(logits)
+        prev = np.ascontiguousarray(prev_tokens, dtype=np.uint32)
+        p = SamplerParams(temperature, top_k, repetition_penalty, 1 if greedy else 0)
+        state = C.c_uint64(rng)
+        tok = C.c_uint32(0)
+        self.check(self.lib.qtts_sample_token(self.h, _ptr(lg), lg.size, C.byref(p), _ptr(prev), prev.size,
+                                              C.byref(state), C.byref(tok)))
+        return int(tok.value), int(state.value)
+
+
+class DeviceQ4:
+    """A Weight::Q4 resident in HBM with gemv/gemm/embed_lookup (src/gemv.rs:148-176)."""
+
+    def __init__(self, ctx: Context, w: Q4Weight):
+        self.ctx, self.k, self.n = ctx, w.k, w.n
+        h = C.c_void_p()
+        v = w.view()
+        ctx.check(ctx.lib.qtts_q4_upload(ctx.h, C.byref(v), C.byref(h)))
+        self.h = h
+
+    def gemv(self, x) -> np.ndarray:
+        x = _f32(x, self.k)
+        y = np.empty(self.n, dtype=np.float32)
+        self.ctx.check(self.ctx.lib.qtts_gemv(self.ctx.h, self.h, _ptr(x), _ptr(y)))
+        return y
+
+    def gemm(self, x, seq_len: int) -> np.ndarray:
+        x = _f32(x, seq_len * self.k)
+        y = np.empty(seq_len * self.n, dtype=np.float32)
+        self.ctx.check(self.ctx.lib.qtts_gemm(self.ctx.h, self.h, _ptr(x), seq_len, _ptr(y)))
+        return y
+
+    def embed_lookup(self, token: int) -> np.ndarray:
+        y = np.empty(self.n, dtype=np.float32)
+        self.ctx.check(self.ctx.lib.qtts_embed_lookup(self.ctx.h, self.h, int(token), _ptr(y)))
+        return y
+
+    def gemv_device(self, d_x: int, d_y: int):
+        self.ctx.check(self.ctx.lib.qtts_gemv_device(self.ctx.h, self.h, C.c_void_p(d_x), C.c_void_p(d_y)))
+
+    @property
+    def memory_bytes(self) -> int:
+        return int(self.ctx.lib.qtts_q4_bytes(self.h))
+
+    def __del__(self):
+        try:
+            self.ctx.lib.qtts_q4_free(self.h)
+        except Exception:
+            pass
+
+
+class KvCache:
+    """RawKvCache (src/gemv.rs:75-86) in HBM, fixed capacity."""
+
+    def __init__(self, ctx: Context, num_layers: int, num_kv_heads: int, head_dim: int, capacity: int):
+        self.ctx = ctx
+        self.shape = (num_layers, num_kv_heads, head_dim)
+        h = C.c_void_p()
+        ctx.check(ctx.lib.qtts_kv_create(ctx.h, num_layers, num_kv_heads, head_dim, capacity, C.byref(h)))
+        self.h = h
+
+    def __len__(self) -> int:
+        return int(self.ctx.lib.qtts_kv_len(self.h))
+
+    def clear(self):
+        self.ctx.check(self.ctx.lib.qtts_kv_clear(self.h))
+
+    def load(self, k: np.ndarray, v: np.ndarray, length: int):
+        """k, v: [layers][length][kv_heads][head_dim] float32."""
+        k, v = _f32(k), _f32(v)
+        self.ctx.check(self.ctx.lib.qtts_kv_load(self.h, _ptr(k), _ptr(v), length))
+
+    def store(self):
+        L, H, D = self.shape
+        n = len(self)
+        k = np.empty((L, n, H, D), dtype=np.float32)
+        v = np.empty_like(k)
+        self.ctx.check(self.ctx.lib.qtts_kv_store(self.h, _ptr(k), _ptr(v)))
+        return k, v
+
+    def __del__(self):
+        try:
+            self.ctx.lib.qtts_kv_free(self.h)
+        except Exception:
+            pass
+
+
+class Talker:
+    """TalkerWeights in HBM with the reference's talker functions."""
+
+    def __init__(self, ctx: Context, w: TalkerWeights):
+        self.ctx, self.cfg = ctx, w.cfg
+        h = C.c_void_p()
+        v = w.view()
+        ctx.check(ctx.lib.qtts_talker_upload(ctx.h, C.byref(v), C.byref(h)))
+        self.h = h
+
+    def new_kv(self, capacity: int) -> KvCache:
+        c = self.cfg
+        return KvCache(self.ctx, c.layers, c.kv_heads, c.head_dim, capacity)
+
+    # forward_with_embedding, src/talker.rs:263-360
+    def forward_with_embedding(self, embedding, kv: KvCache, position: int) -> np.ndarray:
+        e = _f32(embedding, self.cfg.hidden)
+        out = np.empty(self.cfg.hidden + self.cfg.vocab, dtype=np.float32)
+        self.ctx.check(self.ctx.lib.qtts_forward_with_embedding(self.h, _ptr(e), kv.h, position, _ptr(out)))
+        return out
+
+    # prefill_talker_raw, src/talker.rs:364-462
+    def prefill_talker_raw(self, x, seq_len: int, kv: KvCache) -> np.ndarray:
+        x = _f32(x, seq_len * self.cfg.hidden)
+        out = np.empty(self.cfg.hidden, dtype=np.float32)
+        self.ctx.check(self.ctx.lib.qtts_prefill_talker_raw(self.h, _ptr(x), seq_len, kv.h, _ptr(out)))
+        return out
+
+    # apply_codec_head, src/talker.rs:627-629
+    def apply_codec_head(self, hidden) -> np.ndarray:
+        hs = _f32(hidden, self.cfg.hidden)
+        out = np.empty(self.cfg.vocab, dtype=np.float32)
+        self.ctx.check(self.ctx.lib.qtts_apply_codec_head(self.h, _ptr(hs), _ptr(out)))
+        return out
+
+    # embed_codec_token, src/talker.rs:152-154
+    def embed_codec_token(self, token: int) -> np.ndarray:
+        out = np.empty(self.cfg.hidden, dtype=np.float32)
+        self.ctx.check(self.ctx.lib.qtts_embed_codec_token(self.h, int(token), _ptr(out)))
+        return out
+
+    def __del__(self):
+        try:
+            self.ctx.lib.qtts_talker_free(self.h)
+        except Exception:
+            pass
+
+
+class CodePredictor:
+    """CodePredictorWeights in HBM with generate_acoustic_codes."""
+
+    def __init__(self, ctx: Context, w: CodePredictorWeights):
+        self.ctx, self.cfg, self.num_groups = ctx, w.cfg, w.num_groups
+        self.talker_hidden = w.talker_hidden
+        h = C.c_void_p()
+        v = w.view()
+        ctx.check(ctx.lib.qtts_predictor_upload(ctx.h, C.byref(v), C.byref(h)))
+        self.h = h
+
+    def new_kv(self, capacity: int = 16) -> KvCache:
+        c = self.cfg
+        return KvCache(self.ctx, c.layers, c.kv_heads, c.head_dim, capacity)
+
+    # generate_acoustic_codes, src/code_predictor.rs:218-273
+    def generate_acoustic_codes(self, talker_hidden, semantic_embed, kv: KvCache) -> np.ndarray:
+        th = _f32(talker_hidden, self.talker_hidden)
+        se = _f32(semantic_embed, self.talker_hidden)
+        codes = np.empty(self.num_groups, dtype=np.uint32)
+        self.ctx.check(self.ctx.lib.qtts_generate_acoustic_codes(self.h, _ptr(th), _ptr(se), kv.h, _ptr(codes)))
+        return codes
+
+    # get_acoustic_embeddings_sum, src/code_predictor.rs:280-293
+    def get_acoustic_embeddings_sum(self, codes) -> np.ndarray:
+        cs = np.ascontiguousarray(codes, dtype=np.uint32)
+        out = np.empty(self.talker_hidden, dtype=np.float32)
+        self.ctx.check(self.ctx.lib.qtts_get_acoustic_embeddings_sum(self.h, _ptr(cs), _ptr(out)))
+        return out
+
+    def __del__(self):
+        try:
+            self.ctx.lib.qtts_predictor_free(self.h)
+        except Exception:
+            pass
+
+
+def loop_params(max_codes: int, temperature: float = 0.8, top_k: int = 50, repetition_penalty: float = 1.05,
+                greedy: bool = False, stop_on_eos: bool = True, talker_only: bool = False,
+                codec_eos_id: int = CODEC_EOS) -> LoopParams:
+    return LoopParams(max_codes, SamplerParams(temperature, top_k, repetition_penalty, 1 if greedy else 0),
+                      codec_eos_id, 1 if stop_on_eos else 0, 1 if talker_only else 0)
+
+
+def generate_codes(talker: Talker, predictor: Optional[CodePredictor], talker_kv: KvCache,
+                   predictor_kv: Optional[KvCache], last_hidden, logits, position: int,
+                   trailing_text: Optional[np.ndarray], tts_pad_embed: Optional[np.ndarray], params: LoopParams,
+                   seed: int) -> np.ndarray:
+    """The frame loop of generate_speech (src/generate_new.rs:229-300) on the
+    device.  Returns all_codes as [16][n_frames] uint32."""
+    ctx = talker.ctx
+    hidden = talker.cfg.hidden
+    lh = _f32(last_hidden, hidden)
+    lg = _f32(logits, talker.cfg.vocab)
+    tt = None if trailing_text is None else _f32(trailing_text).reshape(-1, hidden)
+    tl = 0 if tt is None else tt.shape[0]
+    pad = None if tts_pad_embed is None else _f32(tts_pad_embed, hidden)
+    codes = np.zeros((16, max(params.max_codes, 1)), dtype=np.uint32)
+    n = C.c_int32(0)
+    ctx.check(ctx.lib.qtts_generate_codes(talker.h, predictor.h if predictor is not None else None,
+                                          talker_kv.h, predictor_kv.h if predictor_kv is not None else None, _ptr(lh), _ptr(lg),
+                                          position, _ptr(tt), tl, _ptr(pad), C.byref(params), seed, _ptr(codes),
+                                          C.byref(n)))
+    return codes[:, : n.value].copy()

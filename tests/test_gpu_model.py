@@ -1,0 +1,193 @@
+"""GPU parity of the composite paths — talker decode step, talker prefill,
+predictor frame and the frame loop — against the oracle on the same seeded
+random-init weights and inputs.
+
+Bars: hidden states and logits within REL_TOL = 1e-3 relative (fp32
+accumulate); predictor codes and greedy loop codes identical.
+"""
+import time
+
+import numpy as np
+import pytest
+
+import qtts
+from oracle import oracle
+from shapes import FULL_PREDICTOR, FULL_TALKER, TINY_PREDICTOR, TINY_TALKER, rel_err
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def tiny(ctx):
+    tw = qtts.TalkerWeights(21, TINY_TALKER)
+    pw = qtts.CodePredictorWeights(21, TINY_PREDICTOR, talker_hidden=TINY_TALKER.hidden)
+    return tw, pw, qtts.Talker(ctx, tw), qtts.CodePredictor(ctx, pw), oracle.Talker(tw, 1), oracle.CodePredictor(pw, 1)
+
+
+@pytest.fixture(scope="module")
+def full(ctx):
+    t0 = time.time()
+    tw = qtts.TalkerWeights(1, FULL_TALKER)
+    pw = qtts.CodePredictorWeights(1, FULL_PREDICTOR, talker_hidden=FULL_TALKER.hidden)
+    print(f"synthetic 1.7B weights in {time.time() - t0:.1f}s", flush=True)
+    return tw, pw, qtts.Talker(ctx, tw), qtts.CodePredictor(ctx, pw), oracle.Talker(tw), oracle.CodePredictor(pw)
+
+
+def test_talker_steps_tiny(tiny):
+    tw, _, t, _, ot, _ = tiny
+    cfg = tw.cfg
+    kv, okv = t.new_kv(40), ot.new_kv(40)
+    for step in range(20):
+        emb = qtts.synth_normal_f32(22, f"tiny.emb.{step}", cfg.hidden)
+        got = t.forward_with_embedding(emb, kv, step + 3)
+        ref = ot.forward_with_embedding(emb, okv, step + 3)
+        assert rel_err(got[: cfg.hidden], ref[: cfg.hidden]) < REL_TOL
+        assert rel_err(got[cfg.hidden:], ref[cfg.hidden:]) < REL_TOL
+    assert len(kv) == len(okv) == 20
+    k, v = kv.store()
+    ok, ov = okv.store()
+    assert rel_err(k, ok) < REL_TOL and rel_err(v, ov) < REL_TOL
+
+
+def test_talker_step_full_prefilled_kv(full):
+    """Single talker decode step: 28 layers, KV pre-filled to 256 positions
+    with N(0,1), one N(0,1) embedding at position 256."""
+    tw, _, t, _, ot, _ = full
+    cfg = tw.cfg
+    L = 256
+    shape = (cfg.layers, L, cfg.kv_heads, cfg.head_dim)
+    k = qtts.synth_normal_f32(3, "kv.k", int(np.prod(shape))).reshape(shape)
+    v = qtts.synth_normal_f32(3, "kv.v", int(np.prod(shape))).reshape(shape)
+    kv, okv = t.new_kv(1024), ot.new_kv(1024)
+    kv.load(k, v, L)
+    okv.load(k, v, L)
+    emb = qtts.synth_normal_f32(3, "step.emb", cfg.hidden)
+    got = t.forward_with_embedding(emb, kv, L)
+    ref = ot.forward_with_embedding(emb, okv, L)
+    eh, el = rel_err(got[: cfg.hidden], ref[: cfg.hidden]), rel_err(got[cfg.hidden:], ref[cfg.hidden:])
+    print(f"full talker step: hidden rel err {eh:.2e}, logits rel err {el:.2e}")
+    assert eh < REL_TOL and el < REL_TOL
+    assert int(np.argmax(got[cfg.hidden:])) == int(np.argmax(ref[cfg.hidden:]))
+
+
+@pytest.mark.parametrize("seq_len", [1, 5, 13])
+def test_prefill_tiny(tiny, seq_len):
+    tw, _, t, _, ot, _ = tiny
+    cfg = tw.cfg
+    x = qtts.synth_normal_f32(23, f"prefill.{seq_len}", seq_len * cfg.hidden)
+    kv, okv = t.new_kv(32), ot.new_kv(32)
+    got = t.prefill_talker_raw(x, seq_len, kv)
+    ref = ot.prefill_talker_raw(x, seq_len, okv)
+    assert rel_err(got, ref) < REL_TOL
+    k, v = kv.store()
+    ok, ov = okv.store()
+    assert rel_err(k, ok) < REL_TOL and rel_err(v, ov) < REL_TOL
+    # a decode step continues from the prefilled cache
+    emb = qtts.synth_normal_f32(23, "prefill.next", cfg.hidden)
+    assert rel_err(t.forward_with_embedding(emb, kv, seq_len), ot.forward_with_embedding(emb, okv, seq_len)) < REL_TOL
+
+
+def test_prefill_nonempty_cache_rejected(tiny):
+    tw, _, t, _, _, _ = tiny
+    kv = t.new_kv(8)
+    t.forward_with_embedding(np.zeros(tw.cfg.hidden, np.float32), kv, 0)
+    with pytest.raises(qtts.QttsError) as e:
+        t.prefill_talker_raw(np.zeros(2 * tw.cfg.hidden, np.float32), 2, kv)
+    assert e.value.status == qtts.QTTS_ESTATE
+
+
+def test_prefill_full_64(full):
+    tw, _, t, _, ot, _ = full
+    x = qtts.synth_normal_f32(4, "prefill64", 64 * tw.cfg.hidden)
+    kv, okv = t.new_kv(128), ot.new_kv(128)
+    got = t.prefill_talker_raw(x, 64, kv)
+    ref = ot.prefill_talker_raw(x, 64, okv)
+    e = rel_err(got, ref)
+    print(f"prefill 64 rel err {e:.2e}")
+    assert e < REL_TOL
+
+
+def test_predictor_tiny(tiny):
+    tw, pw, t, p, ot, op = tiny
+    for i in range(6):
+        h = qtts.synth_normal_f32(24, f"ph.{i}", tw.cfg.hidden)
+        sem = ot.embed_codec_token(100 + i)
+        got = p.generate_acoustic_codes(h, sem, p.new_kv())
+        ref = op.generate_acoustic_codes(h, sem, op.new_kv())
+        assert np.array_equal(got, ref), (got, ref)
+        assert np.array_equal(p.get_acoustic_embeddings_sum(got), op.get_acoustic_embeddings_sum(ref))
+
+
+def test_predictor_full(full):
+    tw, pw, t, p, ot, op = full
+    for i in range(3):
+        h = qtts.synth_normal_f32(5, f"fph.{i}", tw.cfg.hidden)
+        sem = ot.embed_codec_token(7 + 300 * i)
+        got = p.generate_acoustic_codes(h, sem, p.new_kv())
+        ref = op.generate_acoustic_codes(h, sem, op.new_kv())
+        assert np.array_equal(got, ref), (got, ref)
+
+
+def _loop_inputs(tw, seed, trailing=3):
+    hidden = tw.cfg.hidden
+    last_hidden = qtts.synth_normal_f32(seed, "loop.h", hidden)
+    trailing_text = qtts.synth_normal_f32(seed, "loop.text", trailing * hidden, 0.0, 0.1).reshape(trailing, hidden)
+    pad = qtts.synth_normal_f32(seed, "loop.pad", hidden, 0.0, 0.1)
+    return last_hidden, trailing_text, pad
+
+
+@pytest.mark.parametrize("greedy", [True, False])
+def test_loop_tiny(tiny, greedy):
+    tw, pw, t, p, ot, op = tiny
+    last_hidden, text, pad = _loop_inputs(tw, 25)
+    frames = 64
+    params = qtts.loop_params(frames, greedy=greedy, stop_on_eos=False)
+    kv, okv = t.new_kv(96), ot.new_kv(96)
+    # start from a short prefill, as generate_speech does
+    x = qtts.synth_normal_f32(25, "loop.prefill", 10 * tw.cfg.hidden)
+    lh = t.prefill_talker_raw(x, 10, kv)
+    olh = ot.prefill_talker_raw(x, 10, okv)
+    logits = ot.apply_codec_head(olh)
+    got = qtts.generate_codes(t, p, kv, p.new_kv(), olh, logits, 10, text, pad, params, seed=777)
+    ref = oracle.generate_codes(ot, op, okv, op.new_kv(), olh, logits, 10, text, pad, params, seed=777)
+    assert got.shape == ref.shape == (16, frames)
+    assert np.array_equal(got, ref), np.argwhere(got != ref)[:5]
+    assert len(kv) == len(okv) == 10 + frames
+    assert rel_err(lh, olh) < REL_TOL
+
+
+def test_loop_tiny_talker_only_and_eos(tiny):
+    tw, _, t, _, ot, _ = tiny
+    hidden = tw.cfg.hidden
+    lh = qtts.synth_normal_f32(26, "eos.h", hidden)
+    logits = ot.apply_codec_head(lh)
+    params = qtts.loop_params(24, greedy=True, stop_on_eos=False, talker_only=True)
+    kv, okv = t.new_kv(32), ot.new_kv(32)
+    got = qtts.generate_codes(t, None, kv, None, lh, logits, 0, None, None, params, seed=1)
+    ref = oracle.generate_codes(ot, None, okv, None, lh, logits, 0, None, None, params, seed=1)
+    assert np.array_equal(got, ref)
+    # declare the 6th frame's code EOS: both stop before that frame
+    eos = int(ref[0, 5])
+    first = int(np.argmax(ref[0] == eos))
+    params = qtts.loop_params(24, greedy=True, stop_on_eos=True, talker_only=True, codec_eos_id=eos)
+    kv, okv = t.new_kv(32), ot.new_kv(32)
+    got = qtts.generate_codes(t, None, kv, None, lh, logits, 0, None, None, params, seed=1)
+    ref2 = oracle.generate_codes(ot, None, okv, None, lh, logits, 0, None, None, params, seed=1)
+    assert got.shape[1] == ref2.shape[1] == first
+    assert np.array_equal(got, ref2)
+    assert len(kv) == len(okv) == first
+
+
+def test_loop_full_greedy(full):
+    """Full 1.7B talker + predictor, greedy, 16 frames against the oracle."""
+    tw, pw, t, p, ot, op = full
+    last_hidden, text, pad = _loop_inputs(tw, 27)
+    logits = ot.apply_codec_head(last_hidden)
+    frames = 16
+    params = qtts.loop_params(frames, greedy=True, stop_on_eos=False)
+    kv, okv = t.new_kv(256), ot.new_kv(256)
+    got = qtts.generate_codes(t, p, kv, p.new_kv(), last_hidden, logits, 0, text, pad, params, seed=9)
+    ref = oracle.generate_codes(ot, op, okv, op.new_kv(), last_hidden, logits, 0, text, pad, params, seed=9)
+    assert np.array_equal(got, ref), np.argwhere(got != ref)[:5]
