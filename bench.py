@@ -1,0 +1,251 @@
+"""Benchmark: codes/s of the 1.7B talker + code-predictor per-code loop at
+batch 1 on one MI355X, with the Q4 GEMV's achieved HBM bandwidth and the
+oracle's codes/s on this host's CPU cores.
+
+Workload (one "step" = one code = one frame of generate_speech's loop,
+src/generate_new.rs:242-300): sample code 0 (top-k 50, T 0.8, repetition
+penalty 1.05), 15 predictor passes (5 layers, argmax heads), the embedding
+sum and one 28-layer talker step.  A 64-token random-embedding prompt is
+prefilled first (untimed); EOS is ignored so every run produces exactly
+--steps codes.  Weights are seeded random Q4 of the 1.7B shapes.
+
+Prints one JSON line.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+PKG = os.path.join(ROOT, "qora-tts-12hz-1.7b_amd")
+sys.path.insert(0, PKG)
+sys.path.insert(0, ROOT)
+
+import qtts  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+PROMPT = 64
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class Hip:
+    """The few HIP runtime calls the benchmark needs (events, buffers), from
+    the same libamdhip64 the library links."""
+
+    def __init__(self):
+        import ctypes as C
+
+        self.C = C
+        self.lib = C.CDLL("libamdhip64.so.7")
+
+    def _ok(self, rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed: {rc}")
+
+    def malloc(self, nbytes):
+        p = self.C.c_void_p()
+        self._ok(self.lib.hipMalloc(self.C.byref(p), self.C.c_size_t(nbytes)), "hipMalloc")
+        return p.value
+
+    def free(self, p):
+        self.lib.hipFree(self.C.c_void_p(p))
+
+    def h2d(self, dst, arr):
+        self._ok(self.lib.hipMemcpy(self.C.c_void_p(dst), self.C.c_void_p(arr.ctypes.data),
+                                    self.C.c_size_t(arr.nbytes), 1), "hipMemcpy")
+
+    def event(self):
+        e = self.C.c_void_p()
+        self._ok(self.lib.hipEventCreate(self.C.byref(e)), "hipEventCreate")
+        return e
+
+    def record(self, e, stream):
+        self._ok(self.lib.hipEventRecord(e, self.C.c_void_p(stream)), "hipEventRecord")
+
+    def elapsed_ms(self, a, b):
+        self._ok(self.lib.hipEventSynchronize(b), "hipEventSynchronize")
+        ms = self.C.c_float()
+        self._ok(self.lib.hipEventElapsedTime(self.C.byref(ms), a, b), "hipEventElapsedTime")
+        return ms.value
+
+
+def gemv_roofline(ctx, iters=256, copies=64):
+    """Average duration of the talker's gate|up Q4 GEMV shape (K=2048 ->
+    N=2*6144 in one launch) over `copies` distinct weights (a 0.9 GB working
+    set, larger than the 256 MB last-level cache), timed with HIP events on
+    the context's stream, the stream the kernels run on."""
+    K, N = 2048, 12288
+    hip = Hip()
+    ws = [qtts.DeviceQ4(ctx, qtts.Q4Weight.synthetic(99, f"roof.{i}", K, N)) for i in range(copies)]
+    dx, dy = hip.malloc(4 * K), hip.malloc(4 * N)
+    hip.h2d(dx, qtts.synth_normal_f32(99, "roof.x", K))
+    for i in range(copies):
+        ws[i].gemv_device(dx, dy)
+    ctx.synchronize()
+    start, end = hip.event(), hip.event()
+    hip.record(start, ctx.stream)
+    for i in range(iters):
+        ws[i % copies].gemv_device(dx, dy)
+    hip.record(end, ctx.stream)
+    avg_s = hip.elapsed_ms(start, end) / 1e3 / iters
+    hip.free(dx)
+    hip.free(dy)
+    algo_bytes = K * N // 2 + K * (N // 32) * 2 + 4 * K + 4 * N
+    achieved = algo_bytes / avg_s / 1e9
+    return {
+        "bound": "hbm",
+        "achieved": round(achieved, 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "traffic": read_traffic(),
+        "kernel": "k_gemv<1,4> (Q4 GEMV 2048->12288, talker gate|up)",
+        "algorithmic_bytes_per_launch": algo_bytes,
+        "avg_launch_us": round(avg_s * 1e6, 3),
+    }
+
+
+def copy_calibration(ctx, nbytes=512 << 20):
+    """One device-to-device copy of a known size: the plain copy kernel whose
+    FETCH_SIZE / WRITE_SIZE counters calibrate the GEMV's."""
+    hip = Hip()
+    a, b = hip.malloc(nbytes), hip.malloc(nbytes)
+    rc = hip.lib.hipMemcpyDtoD(hip.C.c_void_p(b), hip.C.c_void_p(a), hip.C.c_size_t(nbytes))
+    hip._ok(rc, "hipMemcpyDtoD")
+    hip._ok(hip.lib.hipDeviceSynchronize(), "hipDeviceSynchronize")
+    hip.free(a)
+    hip.free(b)
+    return nbytes
+
+
+def read_traffic():
+    """HBM bytes per launch of the roofline GEMV measured by the rocprofv3
+    counter runs (profiles/q4_gemv_2048x12288_counters.md), if present."""
+    path = os.path.join(ROOT, "profiles", "q4_gemv_2048x12288_counters.md")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            return int(float(line.split(":")[1]))
+    return None
+
+
+def cpu_baseline(tw, pw, gpu_kv, last_hidden, logits, text, pad, frames):
+    """The oracle's frame loop on this host, from the GPU's prefilled cache."""
+    from oracle import oracle
+
+    ot, op = oracle.Talker(tw), oracle.CodePredictor(pw)
+    okv = ot.new_kv(PROMPT + frames + 8)
+    k, v = gpu_kv.store()
+    okv.load(k, v, k.shape[1])
+    params = qtts.loop_params(frames, temperature=0.8, top_k=50, repetition_penalty=1.05, stop_on_eos=False)
+    t0 = time.perf_counter()
+    codes = oracle.generate_codes(ot, op, okv, op.new_kv(), last_hidden, logits, PROMPT, text, pad, params, seed=42)
+    dt = time.perf_counter() - t0
+    return {
+        "value": round(codes.shape[1] / dt, 4),
+        "unit": "codes/s",
+        "cores": oracle.available_parallelism(),
+        "kind": "port",
+        "sample": f"{codes.shape[1]} codes of the same loop from the same 64-token prefilled cache "
+                  f"(C oracle, -O3, split-K threads = cores when k*n >= 4e6, predictor single-threaded)",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--cpu-frames", type=int, default=12)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-roofline", action="store_true")
+    ap.add_argument("--roofline-only", action="store_true",
+                    help="only the GEMV timing and the copy-kernel calibration (for counter runs)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for {args.gpus}); the per-code loop at batch 1 is a serial "
+              f"chain and independent streams shard with no collectives", file=sys.stderr)
+        sys.exit(2)
+
+    if args.roofline_only:
+        ctx = qtts.Context(0)
+        roof = gemv_roofline(ctx)
+        copied = copy_calibration(ctx)
+        print(json.dumps({"roofline": roof, "copy_bytes": copied}), flush=True)
+        return
+
+    t0 = time.time()
+    tw = qtts.TalkerWeights(1, qtts.TALKER_1P7B)
+    pw = qtts.CodePredictorWeights(1, qtts.PREDICTOR_1P7B, talker_hidden=qtts.TALKER_1P7B.hidden)
+    log(f"synthetic weights {time.time() - t0:.1f}s")
+    ctx = qtts.Context(0)
+    talker, pred = qtts.Talker(ctx, tw), qtts.CodePredictor(ctx, pw)
+    log(f"uploaded {time.time() - t0:.1f}s")
+    hidden = tw.cfg.hidden
+    prompt = qtts.synth_normal_f32(2, "bench.prompt", PROMPT * hidden)
+    text = qtts.synth_normal_f32(2, "bench.text", 8 * hidden, 0.0, 0.1).reshape(8, hidden)
+    pad = qtts.synth_normal_f32(2, "bench.pad", hidden, 0.0, 0.1)
+    cap = PROMPT + max(args.steps, args.warmup) + 8
+
+    def prefill():
+        kv = talker.new_kv(cap)
+        lh = talker.prefill_talker_raw(prompt, PROMPT, kv)
+        return kv, lh, talker.apply_codec_head(lh)
+
+    params = lambda n: qtts.loop_params(n, temperature=0.8, top_k=50, repetition_penalty=1.05, stop_on_eos=False)
+    pkv = pred.new_kv()
+    if args.warmup > 0:
+        kv, lh, lg = prefill()
+        qtts.generate_codes(talker, pred, kv, pkv, lh, lg, PROMPT, text, pad, params(args.warmup), seed=41)
+        log(f"warmup {args.warmup} codes done")
+    kv, lh, lg = prefill()
+    ctx.synchronize()
+    t1 = time.perf_counter()
+    codes = qtts.generate_codes(talker, pred, kv, pkv, lh, lg, PROMPT, text, pad, params(args.steps), seed=42)
+    ctx.synchronize()
+    dt = time.perf_counter() - t1
+    assert codes.shape == (16, args.steps), codes.shape
+    cps = args.steps / dt
+    log(f"{args.steps} codes in {dt * 1e3:.1f} ms -> {cps:.1f} codes/s")
+
+    out = {
+        "metric": "codes/sec, 1.7B talker+predictor bs=1; Q4 GEMV HBM GB/s vs peak",
+        "value": round(cps, 3),
+        "unit": "codes/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(dt * 1e3 / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": "talker (28 layers, hidden 2048, 16/8 heads, SwiGLU 6144, vocab 3072) + code predictor "
+                        "(5 layers, hidden 1024, 15 argmax heads of 2048) per code, Q4 g=32 weights, batch 1",
+            "prompt_tokens": PROMPT,
+            "kv_len": [PROMPT + 1, PROMPT + args.steps],
+            "sampler": "top-k 50, temperature 0.8, repetition penalty 1.05",
+        },
+    }
+    if not args.no_roofline:
+        out["roofline"] = gemv_roofline(ctx)
+        log(f"roofline {out['roofline']}")
+    if not args.no_cpu:
+        lh_np, lg_np = lh, lg
+        kv_cpu, lh_np, lg_np = prefill()
+        out["cpu_baseline"] = cpu_baseline(tw, pw, kv_cpu, lh_np, lg_np, text, pad, args.cpu_frames)
+        log(f"cpu baseline {out['cpu_baseline']}")
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -25,6 +25,27 @@ __device__ __forceinline__ float f16_to_f32(uint16_t h) {
     return (float)__builtin_bit_cast(_Float16, h);
 }
 
+// Cross-workgroup traffic inside one kernel (split-K partials, softmax
+// partials, logits for a final argmax) goes through agent-scope atomic
+// loads/stores, which the gfx950 memory model performs at the device
+// coherence point.  That orders the handoff without an agent-scope fence,
+// whose L2 writeback + invalidate per workgroup costs more than the GEMV.
+__device__ __forceinline__ void st_dev(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float *p) {
+    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Waits until this workgroup's device-scope stores have completed, then
+// counts one arrival; returns the count before the increment.
+__device__ __forceinline__ unsigned arrive_dev(unsigned *ctr) {
+    return __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void reset_dev(unsigned *ctr) {
+    __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup"); }
+
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
     for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
@@ -192,7 +213,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvParams P) {
             float s = 0.0f;
 #pragma unroll
             for (int q = 0; q < 8; q++) s += part8[q * 32 + tid];
-            P.partial[((size_t)c * M + m) * N + p * 32 + tid] = s;
+            st_dev(&P.partial[((size_t)c * M + m) * N + p * 32 + tid], s);
         }
     }
 
@@ -209,13 +230,12 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvParams P) {
         gp = 1;
         group = p;
     }
-    __threadfence();
+    wait_stores();
     __syncthreads();
-    if (tid == 0) s_last = atomicAdd(&P.counters[group], 1u) == (unsigned)(gp * P.kc - 1);
+    if (tid == 0) s_last = arrive_dev(&P.counters[group]) == (unsigned)(gp * P.kc - 1);
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
-    if (tid == 0) P.counters[group] = 0u;
+    if (tid == 0) reset_dev(&P.counters[group]);
 
     const int gcols = gp * 32;
     for (int idx = tid; idx < M * gcols; idx += kGemvThreads) {
@@ -226,7 +246,7 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvParams P) {
         else
             col = group * gcols + j;
         float s = 0.0f;
-        for (int cc = 0; cc < P.kc; cc++) s += P.partial[((size_t)cc * M + m) * N + col];
+        for (int cc = 0; cc < P.kc; cc++) s += ld_dev(&P.partial[((size_t)cc * M + m) * N + col]);
         ybuf[m * gcols + j] = s;
     }
     __syncthreads();
@@ -237,7 +257,10 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvParams P) {
             const int m = idx >> 5, j = idx & 31, col = group * 32 + j;
             float v = ybuf[m * 32 + j];
             if (P.bias) v += P.bias[col];
-            P.y[(size_t)m * P.ldy + col] = v;
+            if (P.fin == FIN_ARGMAX)
+                st_dev(&P.y[(size_t)m * P.ldy + col], v);
+            else
+                P.y[(size_t)m * P.ldy + col] = v;
         }
     } else if (P.epilogue == EPI_RESID) {
         for (int idx = tid; idx < M * 32; idx += kGemvThreads) {
@@ -303,18 +326,17 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvParams P) {
     // 7. kernel-wide final step
     if (P.fin == FIN_ARGMAX) {
         const int ngroups = N / 32;
-        __threadfence();
+        wait_stores();
         __syncthreads();
-        if (tid == 0) s_last = atomicAdd(&P.counters[ngroups], 1u) == (unsigned)(ngroups - 1);
+        if (tid == 0) s_last = arrive_dev(&P.counters[ngroups]) == (unsigned)(ngroups - 1);
         __syncthreads();
         if (!s_last) return;
-        __threadfence();
-        if (tid == 0) P.counters[ngroups] = 0u;
+        if (tid == 0) reset_dev(&P.counters[ngroups]);
         // sample_argmax (src/code_predictor.rs:328-334): last index of the max.
         float bv = -INFINITY;
         int bi = -1, nan = 0;
         for (int i = tid; i < N; i += kGemvThreads) {
-            const float v = P.y[i];
+            const float v = ld_dev(&P.y[i]);
             if (v != v)
                 nan = 1;
             else if (bi < 0 || v >= bv) {
@@ -473,34 +495,33 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams P) {
             for (int g = 0; g < G; g++) {
                 const int h = kvh * G + g;
                 float *dst = P.part + (((size_t)m * P.nq + h) * P.nsplit + sp) * (HD + 2);
-                dst[2 + d] = acc[g] + pv[g][d];
+                st_dev(&dst[2 + d], acc[g] + pv[g][d]);
                 if (d == 0) {
-                    dst[0] = mloc[g];
-                    dst[1] = lloc[g];
+                    st_dev(&dst[0], mloc[g]);
+                    st_dev(&dst[1], lloc[g]);
                 }
             }
         }
     }
-    __threadfence();
+    wait_stores();
     __syncthreads();
-    if (tid == 0) s_last = atomicAdd(&P.counters[m * P.nkv + kvh], 1u) == (unsigned)(P.nsplit - 1);
+    if (tid == 0) s_last = arrive_dev(&P.counters[m * P.nkv + kvh]) == (unsigned)(P.nsplit - 1);
     __syncthreads();
     if (!s_last) return;
-    __threadfence();
-    if (tid == 0) P.counters[m * P.nkv + kvh] = 0u;
+    if (tid == 0) reset_dev(&P.counters[m * P.nkv + kvh]);
     for (int idx = tid; idx < G * HD; idx += kAttnThreads) {
         const int g = idx / HD, d = idx - g * HD;
         const int h = kvh * G + g;
         const float *base = P.part + ((size_t)m * P.nq + h) * P.nsplit * (HD + 2);
         float mx = -INFINITY;
-        for (int s = 0; s < P.nsplit; s++) mx = fmaxf(mx, base[s * (HD + 2)]);
+        for (int s = 0; s < P.nsplit; s++) mx = fmaxf(mx, ld_dev(&base[s * (HD + 2)]));
         float o = 0.0f, l = 0.0f;
         for (int s = 0; s < P.nsplit; s++) {
-            const float ms = base[s * (HD + 2)];
+            const float ms = ld_dev(&base[s * (HD + 2)]);
             if (ms == -INFINITY) continue;
             const float w = expf(ms - mx);
-            o += w * base[s * (HD + 2) + 2 + d];
-            l += w * base[s * (HD + 2) + 1];
+            o += w * ld_dev(&base[s * (HD + 2) + 2 + d]);
+            l += w * ld_dev(&base[s * (HD + 2) + 1]);
         }
         P.out[(size_t)m * P.ldo + (size_t)h * HD + d] = o / l;
     }
