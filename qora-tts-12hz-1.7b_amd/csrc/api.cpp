@@ -8,11 +8,14 @@
 #include <cstdio>
 #include <cstdlib>
 #include <cstring>
+#include <functional>
+#include <memory>
 #include <string>
 #include <vector>
 
 #include "../../include/qtts.h"
 #include "../../include/qtts_synth.h"
+#include "engine.h"
 #include "internal.h"
 
 using namespace qtts;
@@ -40,6 +43,14 @@ struct qtts_ctx {
     float *d_out = nullptr;
     size_t d_out_cap = 0;
     uint32_t *d_small = nullptr;  // tokens, prev tokens, status, rng (256 B)
+    // persistent-kernel engine
+    EngState *eng_state = nullptr;  // [2]
+    int *eng_done = nullptr;
+    int *eng_status = nullptr;
+    uint32_t eng_tag = 0;  // tag base of the last launch
+    int eng_grid = 0;
+    uint64_t *eng_trace = nullptr;  // QTTS_ENGINE_TRACE: per-op block timestamps
+    size_t eng_trace_cap = 0;
 };
 
 struct qtts_q4 {
@@ -369,6 +380,50 @@ qtts_status sync(qtts_ctx *c) {
 
 }  // namespace
 
+namespace qtts {
+
+struct TvRef {
+    tv_t *p = nullptr;
+    int tag = 0;
+    int ld = 0;       // row stride
+};
+
+// A program and its tagged-value arena.  Built twice: a sizing pass with null
+// pointers, then the real pass into an arena of the measured size.
+struct EngProgram {
+    std::vector<EngOp> ops;
+    EngOp *d_ops = nullptr;
+    tv_t *arena = nullptr;
+    size_t used = 0;
+    bool sizing = true;
+    int next_tag = 1;
+    int rot_next = 0;
+    int grid = 1;
+    ~EngProgram() {
+        if (d_ops) (void)hipFree(d_ops);
+        if (arena) (void)hipFree(arena);
+    }
+    void reset_build() {
+        ops.clear();
+        used = 0;
+        next_tag = 1;
+        rot_next = 0;
+    }
+    tv_t *tv(size_t n) {
+        const size_t off = used;
+        used += (n + 31) & ~size_t(31);
+        return sizing ? nullptr : arena + off;
+    }
+    int tag() { return next_tag++; }
+    void push(EngOp &op) {
+        op.rot = rot_next;
+        rot_next = (rot_next + op.ntasks) % grid;
+        ops.push_back(op);
+    }
+};
+
+}  // namespace qtts
+
 // ===========================================================================
 // Model objects
 // ===========================================================================
@@ -390,6 +445,10 @@ struct qtts_talker {
     float *trailing = nullptr;
     size_t trailing_cap = 0;
     float *pad = nullptr;
+    // engine programs (built lazily, cached per cache object)
+    std::unique_ptr<EngProgram> step_prog, frame_prog;
+    const qtts_kv *step_kv = nullptr;
+    std::string frame_key;
     ~qtts_talker() {
         for (void *p : prefill_bufs) (void)hipFree(p);
         if (codes) (void)hipFree(codes);
@@ -411,7 +470,396 @@ struct qtts_predictor {
     float *x2 = nullptr, *q2 = nullptr, *a2 = nullptr, *h2 = nullptr, *logits = nullptr;
     uint32_t *codes = nullptr;  // [16]
     int *status = nullptr;
+    std::unique_ptr<EngProgram> prog;
+    const qtts_kv *prog_kv = nullptr;
 };
+
+// ===========================================================================
+// Engine programs (host side of engine.hip)
+// ===========================================================================
+namespace {
+
+EngInput in_tv(const TvRef &r, int row) {
+    EngInput i{};
+    i.kind = EIN_TV;
+    i.tv = r.p ? r.p + (size_t)row * r.ld : nullptr;
+    i.tag = r.tag;
+    return i;
+}
+EngInput in_plain(const float *p) {
+    EngInput i{};
+    i.kind = EIN_PLAIN;
+    i.plain = p;
+    return i;
+}
+EngInput in_embed(const DevQ4 &emb, const TvRef &tok) {
+    EngInput i{};
+    i.kind = EIN_EMBED;
+    i.emb = emb;
+    i.tok_tv = tok.p;
+    i.tag = tok.tag;
+    return i;
+}
+
+struct GemvSpec {
+    int M = 1;
+    int epi = EEPI_STORE;
+    bool norm = false;
+    const uint16_t *gamma = nullptr;
+    EngInput in[kEngMaxM]{};
+    const float *bias = nullptr;
+    TvRef resid{};
+    int kc = 0;  // 0: choose
+    float *out_plain = nullptr;
+    float *norm_plain = nullptr;
+};
+
+TvRef add_gemv(EngProgram &P, const DevQ4 &w, const GemvSpec &sp) {
+    EngOp op{};
+    op.kind = EOP_GEMV;
+    EngGemv &g = op.gemv;
+    const int NP = sp.epi == EEPI_SWIGLU ? 2 : 1;
+    const int ngroups = w.N / (32 * NP);
+    const int Nout = sp.epi == EEPI_SWIGLU ? w.N / 2 : w.N;
+    int kc = sp.kc;
+    if (kc <= 0) {
+        kc = 256 / ngroups;
+        if (kc < 1) kc = 1;
+        if (kc > 4) kc = 4;
+    }
+    const int kmin = (w.K + kEngThreads * kEngRptMax - 1) / (kEngThreads * kEngRptMax);
+    if (kc < kmin) kc = kmin;
+    int kchunk = (w.K + kc - 1) / kc;
+    kchunk = (kchunk + kEngThreads - 1) / kEngThreads * kEngThreads;
+    kc = (w.K + kchunk - 1) / kchunk;
+    g.w = w;
+    g.M = sp.M;
+    g.kc = kc;
+    g.kchunk = kchunk;
+    g.epi = sp.epi;
+    g.norm = sp.norm ? 1 : 0;
+    g.gamma = sp.gamma;
+    for (int m = 0; m < kEngMaxM; m++) g.in[m] = sp.in[m];
+    g.bias = sp.bias;
+    g.resid = sp.resid.p;
+    g.resid_tag = sp.resid.tag;
+    g.ld_resid = sp.resid.ld;
+    g.out = P.tv((size_t)sp.M * Nout);
+    g.out_tag = P.tag();
+    g.ld_out = Nout;
+    g.out_plain = sp.out_plain;
+    g.ld_plain = Nout;
+    g.norm_plain = sp.norm_plain;
+    if (kc > 1) {
+        g.part = P.tv((size_t)(kc - 1) * sp.M * w.N);
+        g.part_tag = P.tag();
+    }
+    op.ntasks = ngroups * kc;
+    P.push(op);
+    return TvRef{g.out, g.out_tag, Nout};
+}
+
+TvRef add_attention(EngProgram &P, const Stack &st, int l, qtts_kv *kv, int M, const TvRef &qkv, bool from_state,
+                    int pos_const, int len_const, int nsplit) {
+    EngOp op{};
+    op.kind = EOP_ATTN;
+    EngAttn &a = op.attn;
+    a.qkv = qkv.p;
+    a.qkv_tag = qkv.tag;
+    a.ld_qkv = qkv.ld;
+    a.M = M;
+    a.nq = st.nq;
+    a.nkv = st.nkv;
+    a.hd = st.hd;
+    a.q_norm = st.L[l].q_norm;
+    a.k_norm = st.L[l].k_norm;
+    a.rope_cos = st.rope_cos;
+    a.rope_sin = st.rope_sin;
+    a.rope_rows = st.rope_rows;
+    a.rope_skip_oob = st.rope_skip_oob;
+    a.kcache = kv->layer_k(l);
+    a.vcache = kv->layer_v(l);
+    a.kv_cap = kv->cap;
+    a.from_state = from_state ? 1 : 0;
+    a.pos_const = pos_const;
+    a.len_const = len_const;
+    a.nsplit = nsplit;
+    a.scale = 1.0f / sqrtf((float)st.hd);  // src/talker.rs:305
+    const int qd = st.nq * st.hd;
+    TvRef out{};
+    if (nsplit > 1) {
+        a.part = P.tv((size_t)M * st.nq * nsplit * (st.hd + 2));
+        a.part_tag = P.tag();
+    } else {
+        a.out = P.tv((size_t)M * qd);
+        a.out_tag = P.tag();
+    }
+    op.ntasks = st.nkv * nsplit;
+    if (nsplit == 1) out = TvRef{a.out, a.out_tag, qd};
+    P.push(op);
+    if (nsplit > 1) {
+        EngOp cop{};
+        cop.kind = EOP_COMBINE;
+        EngCombine &cb = cop.comb;
+        cb.part = a.part;
+        cb.part_tag = a.part_tag;
+        cb.M = M;
+        cb.nq = st.nq;
+        cb.hd = st.hd;
+        cb.nsplit = nsplit;
+        cb.out = P.tv((size_t)M * qd);
+        cb.out_tag = P.tag();
+        cop.ntasks = M * st.nq;
+        P.push(cop);
+        out = TvRef{cb.out, cb.out_tag, qd};
+    }
+    return out;
+}
+
+// One transformer layer over M rows; returns the new residual stream.
+TvRef add_layer(EngProgram &P, const Stack &st, int l, qtts_kv *kv, int M, const TvRef &x, bool from_state,
+                int pos_const, int len_const, int nsplit) {
+    const DevLayer &L = st.L[l];
+    GemvSpec q;
+    q.M = M;
+    q.norm = true;
+    q.gamma = L.in_g;
+    for (int m = 0; m < M; m++) q.in[m] = in_tv(x, m);
+    const TvRef qkv = add_gemv(P, L.qkv, q);
+    const TvRef att = add_attention(P, st, l, kv, M, qkv, from_state, pos_const, len_const, nsplit);
+    GemvSpec o;
+    o.M = M;
+    for (int m = 0; m < M; m++) o.in[m] = in_tv(att, m);
+    o.epi = EEPI_RESID;
+    o.resid = x;
+    const TvRef xm = add_gemv(P, L.o, o);
+    GemvSpec gu;
+    gu.M = M;
+    gu.norm = true;
+    gu.gamma = L.post_g;
+    gu.epi = EEPI_SWIGLU;
+    for (int m = 0; m < M; m++) gu.in[m] = in_tv(xm, m);
+    const TvRef h = add_gemv(P, L.gu, gu);
+    GemvSpec dn;
+    dn.M = M;
+    dn.epi = EEPI_RESID;
+    dn.resid = xm;
+    for (int m = 0; m < M; m++) dn.in[m] = in_tv(h, m);
+    return add_gemv(P, L.down, dn);
+}
+
+TvRef add_argmax(EngProgram &P, const TvRef &logits, int n, int group) {
+    EngOp op{};
+    op.kind = EOP_ARGMAX;
+    op.ntasks = 1;
+    op.amax.logits = logits.p;
+    op.amax.logits_tag = logits.tag;
+    op.amax.n = n;
+    op.amax.code = P.tv(1);
+    op.amax.code_tag = P.tag();
+    op.amax.group = group;
+    P.push(op);
+    return TvRef{op.amax.code, op.amax.code_tag, 1};
+}
+
+TvRef add_embsum(EngProgram &P, int mode, const DevQ4 *codec_emb, const DevQ4 *group_emb, const TvRef *codes,
+                 int groups, const TvRef &tok, const float *trailing, int trailing_len, const float *pad, int hidden) {
+    EngOp op{};
+    op.kind = EOP_EMBSUM;
+    EngEmbSum &e = op.emb;
+    e.mode = mode;
+    if (codec_emb) e.codec_emb = *codec_emb;
+    e.num_groups = groups;
+    for (int g = 0; g < groups; g++) {
+        e.group_emb[g] = group_emb[g];
+        e.code[g] = codes[g].p;
+        e.code_tag[g] = codes[g].tag;
+    }
+    e.tok = tok.p;
+    e.tok_tag = tok.tag;
+    e.trailing = trailing;
+    e.trailing_len = trailing_len;
+    e.pad = pad;
+    e.hidden = hidden;
+    e.out = P.tv((size_t)hidden);
+    e.out_tag = P.tag();
+    op.ntasks = (hidden + kEngThreads - 1) / kEngThreads;
+    P.push(op);
+    return TvRef{e.out, e.out_tag, hidden};
+}
+
+}  // namespace
+
+// ===========================================================================
+// Engine launches
+// ===========================================================================
+namespace {
+
+bool engine_enabled() {
+    const char *e = std::getenv("QTTS_ENGINE");
+    return !(e && std::strcmp(e, "ops") == 0);
+}
+
+qtts_status eng_init(qtts_ctx *c) {
+    if (c->eng_state) return QTTS_OK;
+    HIP_TRY(c, hipMalloc(&c->eng_state, 2 * sizeof(EngState)));
+    HIP_TRY(c, hipMalloc(&c->eng_done, 2 * sizeof(int)));
+    c->eng_status = c->eng_done + 1;
+    HIP_TRY(c, hipMemset(c->eng_done, 0, 2 * sizeof(int)));
+    c->eng_grid = engine_max_grid();
+    if (c->eng_grid <= 0) return fail(c, QTTS_EDEVICE, "engine kernel cannot be resident on this device");
+    c->eng_tag = 0;
+    return QTTS_OK;
+}
+
+using BuildFn = std::function<qtts_status(EngProgram &)>;
+
+qtts_status eng_build(qtts_ctx *c, EngProgram &P, const BuildFn &fn) {
+    P.grid = c->eng_grid;
+    P.sizing = true;
+    P.reset_build();
+    QTTS_TRY(fn(P));
+    const size_t need = P.used;
+    if (P.arena) (void)hipFree(P.arena);
+    if (P.d_ops) (void)hipFree(P.d_ops);
+    P.arena = nullptr;
+    P.d_ops = nullptr;
+    HIP_TRY(c, hipMalloc(&P.arena, (need ? need : 1) * sizeof(tv_t)));
+    HIP_TRY(c, hipMemset(P.arena, 0, (need ? need : 1) * sizeof(tv_t)));
+    P.sizing = false;
+    P.reset_build();
+    QTTS_TRY(fn(P));
+    if ((uint32_t)P.next_tag >= kTagStride) return fail(c, QTTS_ESHAPE, "engine program has too many tagged outputs");
+    HIP_TRY(c, hipMalloc(&P.d_ops, P.ops.size() * sizeof(EngOp)));
+    HIP_TRY(c, hipMemcpy(P.d_ops, P.ops.data(), P.ops.size() * sizeof(EngOp), hipMemcpyHostToDevice));
+    return QTTS_OK;
+}
+
+// Resets the abort word, status and both state copies.
+qtts_status eng_reset(qtts_ctx *c, int pos, int kvlen, uint64_t rng) {
+    EngState s[2];
+    for (auto &x : s) {
+        x.pos = pos;
+        x.kvlen = kvlen;
+        x.frame = 0;
+        x.pad = 0;
+        x.rng = rng;
+    }
+    HIP_TRY(c, hipMemcpyAsync(c->eng_state, s, sizeof(s), hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(c, hipMemsetAsync(c->eng_done, 0, 2 * sizeof(int), c->stream));
+    return QTTS_OK;
+}
+
+qtts_status eng_launch(qtts_ctx *c, EngProgram &P, int st_in, uint32_t *codes, int max_codes) {
+    if (c->eng_tag > 0xFFFFFFFFu - 2 * kTagStride) {
+        // Tags are about to wrap: restart them above zero-filled arenas.
+        HIP_TRY(c, hipStreamSynchronize(c->stream));
+        return fail(c, QTTS_ESTATE, "engine tag space exhausted; recreate the context");
+    }
+    c->eng_tag += kTagStride;
+    EngArgs a{};
+    a.ops = P.d_ops;
+    a.nops = (int)P.ops.size();
+    a.tag_base = c->eng_tag;
+    a.st_in = c->eng_state + st_in;
+    a.st_out = c->eng_state + (st_in ^ 1);
+    a.done = c->eng_done;
+    a.status = c->eng_status;
+    a.codes = codes;
+    a.max_codes = max_codes;
+    // QTTS_ENGINE_TRACE=<file>: each launch synchronizes and appends
+    // {nops, grid, kind[nops], ntasks[nops], u64 stamps[nops][grid][kTraceSlots]}.
+    const char *trace_path = std::getenv("QTTS_ENGINE_TRACE");
+    const size_t trace_n = (size_t)a.nops * P.grid * kTraceSlots;
+    if (trace_path && *trace_path) {
+        if (c->eng_trace_cap < trace_n) {
+            if (c->eng_trace) (void)hipFree(c->eng_trace);
+            c->eng_trace = nullptr;
+            c->eng_trace_cap = 0;
+            HIP_TRY(c, hipMalloc(&c->eng_trace, trace_n * sizeof(uint64_t)));
+            c->eng_trace_cap = trace_n;
+        }
+        HIP_TRY(c, hipMemsetAsync(c->eng_trace, 0, trace_n * sizeof(uint64_t), c->stream));
+        a.trace = c->eng_trace;
+    }
+    hipError_t e = launch_engine(c->stream, a, P.grid);
+    if (e != hipSuccess) return fail(c, QTTS_EDEVICE, std::string("engine launch: ") + hipGetErrorString(e));
+    if (a.trace) {
+        std::vector<uint64_t> h(trace_n);
+        HIP_TRY(c, hipMemcpyAsync(h.data(), a.trace, trace_n * sizeof(uint64_t), hipMemcpyDeviceToHost, c->stream));
+        HIP_TRY(c, hipStreamSynchronize(c->stream));
+        if (FILE *f = std::fopen(trace_path, "ab")) {
+            const int32_t hdr[2] = {a.nops, P.grid};
+            std::fwrite(hdr, sizeof(hdr), 1, f);
+            for (const EngOp &op : P.ops) std::fwrite(&op.kind, sizeof(int32_t), 1, f);
+            for (const EngOp &op : P.ops) std::fwrite(&op.ntasks, sizeof(int32_t), 1, f);
+            std::fwrite(h.data(), sizeof(uint64_t), trace_n, f);
+            std::fclose(f);
+        }
+    }
+    return QTTS_OK;
+}
+
+qtts_status eng_status_check(qtts_ctx *c, const char *what) {
+    int st[2] = {0, 0};
+    HIP_TRY(c, hipMemcpy(st, c->eng_done, sizeof(st), hipMemcpyDeviceToHost));
+    if (st[1] == QTTS_ENAN) return fail(c, QTTS_ENAN, std::string(what) + ": NaN logits (the reference panics)");
+    if (st[1] != 0) return fail(c, (qtts_status)st[1], std::string(what) + ": engine wait timed out");
+    return QTTS_OK;
+}
+
+// Talker attention splits: chunks of at most 256 positions, ~128 typical.
+int eng_talker_nsplit(int cap) {
+    int n = (cap + 127) / 128;
+    if (n < 1) n = 1;
+    if (n > kEngMaxSplit) n = kEngMaxSplit;
+    return n;
+}
+bool eng_talker_fits(int cap) { return (cap + kEngMaxSplit - 1) / kEngMaxSplit <= 256; }
+
+qtts_status build_predictor_passes(EngProgram &P, qtts_predictor *p, qtts_kv *kv, const EngInput &row0,
+                                   const EngInput &row1, TvRef *codes) {
+    const Stack &st = p->st;
+    GemvSpec ip;
+    ip.M = 2;
+    ip.in[0] = row0;
+    ip.in[1] = row1;
+    ip.bias = p->bias;
+    TvRef x = add_gemv(P, p->in_proj, ip);
+    for (int l = 0; l < st.layers; l++) x = add_layer(P, st, l, kv, 2, x, false, 0, 0, 1);
+    GemvSpec hd;
+    hd.norm = true;
+    hd.gamma = st.final_g;
+    hd.in[0] = in_tv(x, 1);
+    TvRef lg = add_gemv(P, p->heads[0], hd);
+    codes[0] = add_argmax(P, lg, p->vocab, 1);
+    for (int g = 1; g < p->groups; g++) {
+        GemvSpec e;
+        e.in[0] = in_embed(p->emb[g - 1], codes[g - 1]);
+        e.bias = p->bias;
+        x = add_gemv(P, p->in_proj, e);
+        for (int l = 0; l < st.layers; l++) x = add_layer(P, st, l, kv, 1, x, false, g + 1, g + 1, 1);
+        hd.in[0] = in_tv(x, 0);
+        lg = add_gemv(P, p->heads[g], hd);
+        codes[g] = add_argmax(P, lg, p->vocab, g + 1);
+    }
+    return QTTS_OK;
+}
+
+qtts_status build_talker_layers_and_head(EngProgram &P, qtts_talker *t, qtts_kv *kv, TvRef x, int nsplit) {
+    for (int l = 0; l < t->st.layers; l++) x = add_layer(P, t->st, l, kv, 1, x, true, 0, 0, nsplit);
+    GemvSpec h;
+    h.norm = true;
+    h.gamma = t->st.final_g;
+    h.in[0] = in_tv(x, 0);
+    h.kc = 1;
+    h.out_plain = t->out + t->st.hidden;  // logits, read by the next frame's sampler
+    h.norm_plain = t->out;                // normed hidden, read by the next predictor frame
+    add_gemv(P, t->head, h);
+    return QTTS_OK;
+}
+
+}  // namespace
 
 // ===========================================================================
 // C-ABI
@@ -457,6 +905,9 @@ void qtts_ctx_destroy(qtts_ctx *c) {
     (void)hipFree(c->d_in);
     (void)hipFree(c->d_out);
     (void)hipFree(c->d_small);
+    (void)hipFree(c->eng_state);
+    (void)hipFree(c->eng_done);
+    (void)hipFree(c->eng_trace);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
 }
@@ -731,8 +1182,28 @@ qtts_status qtts_forward_with_embedding(qtts_talker *t, const float *embedding, 
     QTTS_TRY(check_kv(c, t->st, kv));
     if (position < 0 || position >= t->max_pos) return fail(c, QTTS_ERANGE, "position beyond the RoPE table");
     if (kv->len + 1 > kv->cap) return fail(c, QTTS_ERANGE, "kv cache full");
-    t->nsplit = attn_nsplit(kv->cap, 16);
     const int hidden = t->st.hidden;
+    if (engine_enabled() && eng_talker_fits(kv->cap)) {
+        QTTS_TRY(eng_init(c));
+        if (!t->step_prog || t->step_kv != kv) {
+            t->step_prog.reset(new EngProgram());
+            const int nsplit = eng_talker_nsplit(kv->cap);
+            QTTS_TRY(eng_build(c, *t->step_prog, [&](EngProgram &P) {
+                TvRef x = add_embsum(P, 2, nullptr, nullptr, nullptr, 0, TvRef{}, nullptr, 0, t->x, hidden);
+                return build_talker_layers_and_head(P, t, kv, x, nsplit);
+            }));
+            t->step_kv = kv;
+        }
+        HIP_TRY(c, hipMemcpyAsync(t->x, embedding, sizeof(float) * hidden, hipMemcpyHostToDevice, c->stream));
+        QTTS_TRY(eng_reset(c, position, kv->len, 0));
+        QTTS_TRY(eng_launch(c, *t->step_prog, 0, c->d_small, 1));
+        HIP_TRY(c, hipMemcpyAsync(out, t->out, sizeof(float) * (hidden + t->vocab), hipMemcpyDeviceToHost, c->stream));
+        QTTS_TRY(sync(c));
+        QTTS_TRY(eng_status_check(c, "forward_with_embedding"));
+        kv->len += 1;
+        return QTTS_OK;
+    }
+    t->nsplit = attn_nsplit(kv->cap, 16);
     HIP_TRY(c, hipMemcpyAsync(t->x, embedding, sizeof(float) * hidden, hipMemcpyHostToDevice, c->stream));
     QTTS_TRY(set_state(t, position, kv->len));
     QTTS_TRY(enqueue_talker_step(t, kv, t->out, t->out + hidden, nullptr, 0));
@@ -982,6 +1453,26 @@ qtts_status qtts_generate_acoustic_codes(qtts_predictor *p, const float *talker_
     const int th = p->talker_hidden;
     HIP_TRY(c, hipMemcpyAsync(p->in2, talker_hidden, sizeof(float) * th, hipMemcpyHostToDevice, c->stream));
     HIP_TRY(c, hipMemcpyAsync(p->in2 + th, semantic_embed, sizeof(float) * th, hipMemcpyHostToDevice, c->stream));
+    if (engine_enabled() && !p->identity_proj) {
+        QTTS_TRY(eng_init(c));
+        if (!p->prog || p->prog_kv != kv) {
+            p->prog.reset(new EngProgram());
+            QTTS_TRY(eng_build(c, *p->prog, [&](EngProgram &P) {
+                TvRef codes[kMaxGroups];
+                return build_predictor_passes(P, p, kv, in_plain(p->in2), in_plain(p->in2 + th), codes);
+            }));
+            p->prog_kv = kv;
+        }
+        QTTS_TRY(eng_reset(c, 0, 0, 0));
+        QTTS_TRY(eng_launch(c, *p->prog, 0, p->codes, 1));
+        uint32_t all[16];
+        HIP_TRY(c, hipMemcpyAsync(all, p->codes, sizeof(all), hipMemcpyDeviceToHost, c->stream));
+        QTTS_TRY(sync(c));
+        QTTS_TRY(eng_status_check(c, "generate_acoustic_codes"));
+        for (int g = 0; g < p->groups; g++) codes[g] = all[1 + g];
+        kv->len = p->groups + 1;
+        return QTTS_OK;
+    }
     HIP_TRY(c, hipMemsetAsync(p->status, 0, sizeof(int), c->stream));
     QTTS_TRY(enqueue_predictor(p, kv, p->codes, p->status, nullptr));
     int status = 0;
@@ -1177,6 +1668,81 @@ qtts_status qtts_generate_codes(qtts_talker *t, qtts_predictor *p, qtts_kv *talk
     init.rng = seed;
     HIP_TRY(c, hipMemcpyAsync(t->state, &init, sizeof(init), hipMemcpyHostToDevice, c->stream));
     QTTS_TRY(sync(c));
+
+    if (engine_enabled() && eng_talker_fits(talker_kv->cap) && (talker_only || !p->identity_proj) &&
+        t->vocab <= 4096) {
+        QTTS_TRY(eng_init(c));
+        char key[256];
+        std::snprintf(key, sizeof(key), "%p %p %p %d %d %g %d %g %d %u %d %d %p %p", (void *)talker_kv,
+                      (void *)predictor_kv, (void *)(talker_only ? nullptr : p), max_codes, trailing_len,
+                      params->sampler.temperature, params->sampler.top_k, params->sampler.repetition_penalty,
+                      params->sampler.greedy, params->codec_eos_id, params->stop_on_eos, (int)talker_only,
+                      (void *)t->trailing, (void *)t->codes);
+        if (!t->frame_prog || t->frame_key != key) {
+            t->frame_prog.reset(new EngProgram());
+            const int nsplit = eng_talker_nsplit(talker_kv->cap);
+            QTTS_TRY(eng_build(c, *t->frame_prog, [&](EngProgram &P) {
+                EngOp op{};
+                op.kind = EOP_SAMPLE;
+                op.ntasks = 1;
+                EngSample &sm = op.samp;
+                sm.logits = t->out + hidden;
+                sm.vocab = t->vocab;
+                sm.temperature = params->sampler.temperature;
+                sm.top_k = params->sampler.top_k;
+                sm.penalty = params->sampler.repetition_penalty;
+                sm.greedy = params->sampler.greedy;
+                sm.stop_on_eos = params->stop_on_eos;
+                sm.eos = params->codec_eos_id;
+                sm.num_prev = 16;
+                sm.tok = P.tv(1);
+                sm.tok_tag = P.tag();
+                P.push(op);
+                const TvRef tok{sm.tok, sm.tok_tag, 1};
+                TvRef x;
+                if (!talker_only) {
+                    TvRef codes[kMaxGroups];
+                    QTTS_TRY(build_predictor_passes(P, p, predictor_kv, in_plain(t->out), in_embed(t->emb, tok), codes));
+                    x = add_embsum(P, 0, &t->emb, p->emb, codes, p->groups, tok, t->trailing, trailing_len, t->pad,
+                                   hidden);
+                } else {
+                    x = add_embsum(P, 1, &t->emb, nullptr, nullptr, 0, tok, nullptr, 0, nullptr, hidden);
+                }
+                return build_talker_layers_and_head(P, t, talker_kv, x, nsplit);
+            }));
+            t->frame_key = key;
+        }
+        // t->out holds [last_hidden | logits] for the first frame's sampler
+        // and predictor input.
+        HIP_TRY(c, hipMemcpyAsync(t->out, last_hidden, sizeof(float) * hidden, hipMemcpyHostToDevice, c->stream));
+        QTTS_TRY(eng_reset(c, position, talker_kv->len, seed));
+        qtts_status rc = QTTS_OK;
+        const int batch = 16;
+        int done = 0;
+        for (int f0 = 0; f0 < max_codes && rc == QTTS_OK && !done; f0 += batch) {
+            const int nb = max_codes - f0 < batch ? max_codes - f0 : batch;
+            for (int i = 0; i < nb && rc == QTTS_OK; i++) rc = eng_launch(c, *t->frame_prog, (f0 + i) & 1, t->codes, max_codes);
+            if (rc != QTTS_OK) break;
+            if (params->stop_on_eos && f0 + nb < max_codes) {
+                int d = 0;
+                hipError_t e = hipMemcpyAsync(&d, c->eng_done, sizeof(int), hipMemcpyDeviceToHost, c->stream);
+                if (e == hipSuccess) e = hipStreamSynchronize(c->stream);
+                if (e != hipSuccess) rc = fail(c, QTTS_EDEVICE, std::string("loop: ") + hipGetErrorString(e));
+                done = d;
+            }
+        }
+        QTTS_TRY(rc);
+        QTTS_TRY(sync(c));
+        QTTS_TRY(eng_status_check(c, "generate_codes"));
+        EngState fin[2];
+        HIP_TRY(c, hipMemcpy(fin, c->eng_state, sizeof(fin), hipMemcpyDeviceToHost));
+        HIP_TRY(c, hipMemcpy(codes, t->codes, ncodes * sizeof(uint32_t), hipMemcpyDeviceToHost));
+        const int nf = fin[0].frame > fin[1].frame ? fin[0].frame : fin[1].frame;
+        *n_frames = nf;
+        talker_kv->len += nf;
+        if (!talker_only && nf > 0) predictor_kv->len = p->groups + 1;
+        return QTTS_OK;
+    }
 
     LoopCfg L{t, talker_only ? nullptr : p, talker_kv, predictor_kv, params, trailing_len};
     const bool use_graph = std::getenv("QTTS_NO_GRAPH") == nullptr;

@@ -1,0 +1,97 @@
+// device_common.h — small device helpers shared by the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+#include "internal.h"
+
+namespace qtts {
+
+// Global-address-space view of a pointer.  Pointers read out of structs in
+// memory are generic to the compiler, and generic (flat) accesses count
+// against both vmcnt and lgkmcnt: every later LDS or scalar-load wait would
+// then also wait for outstanding HBM loads.  Accesses through glb() are
+// global_load/global_store.
+template <typename T>
+__device__ __forceinline__ __attribute__((address_space(1))) T *glb(T *p) {
+    return (__attribute__((address_space(1))) T *)p;
+}
+
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
+
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+// Cross-workgroup traffic inside one kernel goes through agent-scope atomic
+// loads/stores, which the gfx950 memory model performs at the device
+// coherence point (sc1).  That orders a handoff without an agent-scope
+// fence, whose L2 writeback + invalidate per workgroup costs more than a
+// small GEMV.
+__device__ __forceinline__ void st_dev(float *p, float v) {
+    __hip_atomic_store(glb(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float *p) {
+    return __hip_atomic_load(glb(const_cast<float *>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev_u32(uint32_t *p, uint32_t v) {
+    __hip_atomic_store(glb(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t ld_dev_u32(const uint32_t *p) {
+    return __hip_atomic_load(glb(const_cast<uint32_t *>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ int ld_dev_i32(const int *p) {
+    return __hip_atomic_load(glb(const_cast<int *>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev_i32(int *p, int v) {
+    __hip_atomic_store(glb(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t ld_dev_u64(const uint64_t *p) {
+    return __hip_atomic_load(glb(const_cast<uint64_t *>(p)), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void st_dev_u64(uint64_t *p, uint64_t v) {
+    __hip_atomic_store(glb(p), v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Counts one arrival; returns the count before the increment.
+__device__ __forceinline__ unsigned arrive_dev(unsigned *ctr) {
+    return __hip_atomic_fetch_add(glb(ctr), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void reset_dev(unsigned *ctr) {
+    __hip_atomic_store(glb(ctr), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Waits until this wave's earlier memory operations have completed.
+__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup"); }
+
+// xorshift64 (13, 7, 17) and (state as f32) / (u64::MAX as f32), both
+// conversions rounding to nearest (src/generate_new.rs:17-22).
+__device__ __forceinline__ float simple_rand_dev(uint64_t *state) {
+    uint64_t s = *state;
+    s ^= s << 13;
+    s ^= s >> 7;
+    s ^= s << 17;
+    *state = s;
+    return (float)s / 18446744073709551616.0f;
+}
+
+// Element (row, col) of a panel-major Q4 weight: f32(scale) * (nib - 8),
+// the product embed_lookup_q4 forms (src/gemv.rs:388-396); exact.
+__device__ __forceinline__ float q4_element(const DevQ4 &w, uint32_t row, int col) {
+    const size_t r = (size_t)(col >> 5) * w.K + row;
+    const uint8_t byte = glb(reinterpret_cast<const uint8_t *>(w.wq))[r * 16 + ((col & 31) >> 1)];
+    const int nib = (col & 1) ? (byte >> 4) : (byte & 15);
+    return f16_to_f32(glb(w.ws)[r]) * (float)(nib - 8);
+}
+
+}  // namespace qtts

@@ -1,0 +1,178 @@
+// engine.h — the persistent dataflow kernel that runs one frame of the
+// per-code loop (or one talker step, or one predictor frame) in a single
+// cooperative launch.
+//
+// A program is a list of ops (GEMV, attention, combine, argmax, sampler,
+// embedding sum), each split into tasks.  Every block walks the ops in order
+// and takes the tasks t with (t + rotation) % gridDim == blockIdx.  Values
+// that cross blocks are "tagged": a 64-bit word holding the float bits and a
+// 32-bit tag naming the op instance that wrote it.  A consumer spins on the
+// words it needs until their tags match, so a dependency costs one device
+// store + one device load (no grid barrier), and a block that has no task in
+// an op moves on and issues the next op's weight loads while it waits.
+//
+// Deadlock freedom: tasks only wait on values of earlier ops, or (split-K
+// owners) on the non-owner chunks of the same op, which come first in task
+// order.  Every spin is bounded and also polls a shared abort word, so an
+// error or EOS drains the grid.
+#pragma once
+
+#include "internal.h"
+
+namespace qtts {
+
+using tv_t = uint64_t;  // float bits | tag << 32
+
+constexpr int kEngThreads = 256;
+constexpr int kEngRptMax = 8;  // rows per thread of one GEMV task (K chunk <= 2048)
+constexpr int kEngMaxM = 2;    // rows per GEMV (the predictor's 2-token prefill)
+constexpr uint32_t kTagStride = 8192;  // tags reserved per launch
+constexpr int kEngMaxSplit = 32;
+constexpr int kEngSmemFloats = 10240;
+
+enum EngOpKind : int { EOP_GEMV = 1, EOP_ATTN = 2, EOP_COMBINE = 3, EOP_ARGMAX = 4, EOP_SAMPLE = 5, EOP_EMBSUM = 6 };
+enum EngIn : int { EIN_TV = 0, EIN_PLAIN = 1, EIN_EMBED = 2 };
+enum EngEpi : int { EEPI_STORE = 0, EEPI_RESID = 1, EEPI_SWIGLU = 2 };
+
+struct EngInput {
+    int kind;
+    int tag;              // EIN_TV: tag of tv; EIN_EMBED: tag of tok_tv
+    const tv_t *tv;       // EIN_TV: the row (K values)
+    const float *plain;   // EIN_PLAIN: the row, written by an earlier launch or the host
+    DevQ4 emb;            // EIN_EMBED: x = emb row at the token
+    const tv_t *tok_tv;   // EIN_EMBED: the token (integer in the value bits)
+};
+
+struct EngGemv {
+    DevQ4 w;
+    int M;       // rows (1 or 2)
+    int kc;      // K chunks; chunk 0 owns the epilogue
+    int kchunk;  // rows per chunk (multiple of 256, <= 256 * kEngRptMax)
+    int epi;
+    int norm;    // RMSNorm the input rows (rms_norm_f16)
+    const uint16_t *gamma;
+    EngInput in[kEngMaxM];
+    const float *bias;
+    const tv_t *resid;  // EEPI_RESID: y = resid + gemv
+    int resid_tag, ld_resid;
+    tv_t *out;
+    int out_tag, ld_out;
+    float *out_plain;  // optional plain copy of the output (read by a later launch)
+    int ld_plain;
+    float *norm_plain;  // optional: the normed input row M-1 (kc must be 1)
+    tv_t *part;         // split-K partials [kc-1][M][N]
+    int part_tag;
+};
+
+struct EngAttn {
+    const tv_t *qkv;  // [M][ld_qkv]: q (nq*hd) | k (nkv*hd) | v (nkv*hd), before QK-norm/RoPE
+    int qkv_tag, ld_qkv;
+    int M, nq, nkv, hd;
+    const uint16_t *q_norm, *k_norm;
+    const float *rope_cos, *rope_sin;
+    int rope_rows, rope_skip_oob;
+    float *kcache, *vcache;  // this layer [nkv][cap][hd]
+    int kv_cap;
+    int from_state;          // position / cache length from the frame state (talker)
+    int pos_const, len_const;
+    int nsplit;
+    float scale;
+    tv_t *part;  // nsplit > 1: [M][nq][nsplit][hd + 2]
+    int part_tag;
+    tv_t *out;   // nsplit == 1: [M][nq*hd]
+    int out_tag;
+};
+
+struct EngCombine {
+    const tv_t *part;
+    int part_tag;
+    int M, nq, hd, nsplit;
+    tv_t *out;
+    int out_tag;
+};
+
+struct EngArgmax {
+    const tv_t *logits;
+    int logits_tag, n;
+    tv_t *code;  // one tagged integer
+    int code_tag;
+    int group;   // codes row this code is filed under
+};
+
+struct EngSample {
+    const float *logits;  // plain, from the previous launch (or the host)
+    int vocab;
+    float temperature;
+    int top_k;
+    float penalty;
+    int greedy;
+    int stop_on_eos;
+    uint32_t eos;
+    int num_prev;  // prev_tokens entries (16)
+    tv_t *tok;
+    int tok_tag;
+};
+
+struct EngEmbSum {
+    int mode;  // 0: codec_emb[tok] + sum_g group_emb[g][code_g] + text; 1: codec_emb[tok] only;
+               // 2: copy the plain row `pad` (a host input)
+    DevQ4 codec_emb;
+    DevQ4 group_emb[kMaxGroups];
+    const tv_t *code[kMaxGroups];
+    int code_tag[kMaxGroups];
+    int num_groups;
+    const tv_t *tok;
+    int tok_tag;
+    const float *trailing;
+    int trailing_len;
+    const float *pad;
+    int hidden;
+    tv_t *out;
+    int out_tag;
+};
+
+struct EngOp {
+    int kind;
+    int ntasks;
+    int rot;  // task rotation across blocks
+    int pad;
+    union {
+        EngGemv gemv;
+        EngAttn attn;
+        EngCombine comb;
+        EngArgmax amax;
+        EngSample samp;
+        EngEmbSum emb;
+    };
+};
+
+// Frame state, double-buffered across launches: a launch reads one copy and
+// its sampler writes the other.
+struct EngState {
+    int pos;    // talker RoPE position
+    int kvlen;  // talker cache length
+    int frame;  // frames produced
+    int pad;
+    uint64_t rng;
+};
+
+struct EngArgs {
+    const EngOp *ops;
+    int nops;
+    uint32_t tag_base;
+    const EngState *st_in;
+    EngState *st_out;
+    int *done;    // abort word: EOS, error or timeout
+    int *status;  // qtts_status of the device side
+    uint32_t *codes;  // [16][max_codes]
+    int max_codes;
+    uint64_t *trace;  // optional [nops][grid][kTraceSlots]: wall clock at 0 start, 1 end, 2..7 inside a task;
+                      // shader clock at 8 start, 9 end
+};
+
+constexpr int kTraceSlots = 10;
+
+hipError_t launch_engine(hipStream_t st, const EngArgs &a, int grid);
+int engine_max_grid();
+
+}  // namespace qtts

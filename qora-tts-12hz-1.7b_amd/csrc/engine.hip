@@ -1,0 +1,1102 @@
+// engine.hip — persistent dataflow kernel for the per-code loop (see engine.h).
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+
+#include "../../include/qtts.h"
+#include "device_common.h"
+#include "engine.h"
+
+namespace qtts {
+
+namespace {
+
+constexpr uint32_t kSpinLimit = 1u << 23;
+
+// Per-thread wait bookkeeping.  A thread that sees the abort word, or spins
+// past the limit, marks itself bad and keeps executing the task with zeros
+// (so every block barrier is still reached); the block leaves at the end of
+// the task.
+struct Ctl {
+    int *done;
+    int *status;
+    uint32_t spins;
+    bool bad;
+    uint64_t *tr;  // trace slots of this (op, block), or null
+};
+
+// Trace stamp k (2..7) of the current task, thread 0 only.
+__device__ __forceinline__ void stamp(const Ctl &c, int k) {
+    if (c.tr && threadIdx.x == 0) glb(c.tr)[k] = wall_clock64();
+}
+
+__device__ __forceinline__ void fail_dev(Ctl &c, int code) {
+    st_dev_i32(c.status, code);
+    st_dev_i32(c.done, 1);
+    c.bad = true;
+}
+
+__device__ __forceinline__ bool must_stop(Ctl &c) {
+    if (c.bad) return true;
+    if ((++c.spins & 127u) == 0u) {
+        if (ld_dev_i32(c.done)) {
+            c.bad = true;
+            return true;
+        }
+        if (c.spins > kSpinLimit) {
+            fail_dev(c, QTTS_EDEVICE);
+            return true;
+        }
+    }
+    return false;
+}
+
+__device__ __forceinline__ float wait_tv(const tv_t *p, uint32_t tag, Ctl &c) {
+    uint64_t v = ld_dev_u64(p);
+    while ((uint32_t)(v >> 32) != tag) {
+        if (must_stop(c)) return 0.0f;
+        __builtin_amdgcn_s_sleep(1);
+        v = ld_dev_u64(p);
+    }
+    return __uint_as_float((uint32_t)v);
+}
+
+// Waits for `count` (<= N) words base[i*stride]: all loads are issued
+// before any tag is checked, then only the stale ones are re-read.
+template <int N>
+__device__ __forceinline__ void wait_strided(const tv_t *base, size_t stride, int count, uint32_t tag, float (&out)[N],
+                                             Ctl &c) {
+    uint64_t v[N];
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = i < count ? ld_dev_u64(base + i * stride) : ((uint64_t)tag << 32);
+    for (;;) {
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < N; i++) ok &= ((uint32_t)(v[i] >> 32) == tag);
+        if (ok || must_stop(c)) break;
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int i = 0; i < N; i++) v[i] = i < count ? ld_dev_u64(base + i * stride) : v[i];
+    }
+#pragma unroll
+    for (int i = 0; i < N; i++) out[i] = __uint_as_float((uint32_t)v[i]);
+}
+
+// Same for a list of words with their own tags.
+template <int N>
+__device__ __forceinline__ void wait_list(const tv_t *const (&p)[N], const uint32_t (&tag)[N], int count,
+                                          float (&out)[N], Ctl &c) {
+    uint64_t v[N];
+#pragma unroll
+    for (int i = 0; i < N; i++) v[i] = i < count ? ld_dev_u64(p[i]) : ((uint64_t)tag[i] << 32);
+    for (;;) {
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < N; i++) ok &= ((uint32_t)(v[i] >> 32) == tag[i]);
+        if (ok || must_stop(c)) break;
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int i = 0; i < N; i++) v[i] = i < count ? ld_dev_u64(p[i]) : v[i];
+    }
+#pragma unroll
+    for (int i = 0; i < N; i++) out[i] = __uint_as_float((uint32_t)v[i]);
+}
+
+__device__ __forceinline__ uint32_t wait_tv_u32(const tv_t *p, uint32_t tag, Ctl &c) {
+    return __float_as_uint(wait_tv(p, tag, c));
+}
+
+__device__ __forceinline__ void put_tv(tv_t *p, float x, uint32_t tag) {
+    st_dev_u64(p, ((uint64_t)tag << 32) | (uint64_t)__float_as_uint(x));
+}
+
+__device__ __forceinline__ void put_tv_u32(tv_t *p, uint32_t x, uint32_t tag) {
+    st_dev_u64(p, ((uint64_t)tag << 32) | (uint64_t)x);
+}
+
+// Sum over the 256-thread block, fixed order; every thread gets the result.
+__device__ __forceinline__ float block_sum(float v, float *scr) {
+    v = wave_sum(v);
+    __syncthreads();
+    if ((threadIdx.x & 63) == 0) scr[threadIdx.x >> 6] = v;
+    __syncthreads();
+    const float t = (scr[0] + scr[1]) + (scr[2] + scr[3]);
+    __syncthreads();
+    return t;
+}
+
+// ---------------------------------------------------------------------------
+// GEMV task: NP panels (1, or gate+up for SwiGLU) x one K chunk x M rows.
+// Same arithmetic as k_gemv: acc += (scale * x) * (nib - 8), f32.
+// ---------------------------------------------------------------------------
+template <int M, int NP>
+__device__ __forceinline__ int eng_gemv(const EngGemv &g, int task, uint32_t tb, Ctl &c, float *smem) {
+    float *red = smem;                     // [256][33]
+    float *part8 = red + kEngThreads * 33;  // [8][32]
+    float *ybuf = part8 + 8 * 32;           // [NP][M][32]
+    float *scr = ybuf + NP * M * 32;        // [8]
+    const int tid = threadIdx.x;
+    const int N = g.w.N, K = g.w.K;
+    const int ngroups = NP == 2 ? N / 64 : N / 32;
+    const int nonowner = ngroups * (g.kc - 1);
+    int group, ch;
+    if (task < nonowner) {
+        group = task % ngroups;
+        ch = 1 + task / ngroups;
+    } else {
+        group = task - nonowner;
+        ch = 0;
+    }
+    const int k0 = ch * g.kchunk;
+    const int k1 = min(K, k0 + g.kchunk);
+    int panel[NP];
+    panel[0] = group;
+    if (NP == 2) panel[NP - 1] = group + ngroups;
+
+    // 1. this chunk's weight rows: issued before any input wait.
+    uint4 wv[NP][kEngRptMax];
+    uint32_t sv[NP][kEngRptMax];
+#pragma unroll
+    for (int i = 0; i < kEngRptMax; i++) {
+        const int k = k0 + tid + i * kEngThreads;
+#pragma unroll
+        for (int pp = 0; pp < NP; pp++) {
+            if (k < k1) {
+                const u32x4 t = glb(reinterpret_cast<const u32x4 *>(g.w.wq))[(size_t)panel[pp] * K + k];
+                wv[pp][i] = make_uint4(t.x, t.y, t.z, t.w);
+                sv[pp][i] = glb(g.w.ws)[(size_t)panel[pp] * K + k];
+            } else {
+                wv[pp][i] = make_uint4(0u, 0u, 0u, 0u);
+                sv[pp][i] = 0u;
+            }
+        }
+    }
+
+    // RMSNorm gamma of the same rows, and the owner's epilogue operands
+    // (bias; the residual, tag-checked when used): loaded before any wait.
+    uint16_t gam[kEngRptMax];
+#pragma unroll
+    for (int i = 0; i < kEngRptMax; i++) {
+        const int k = k0 + tid + i * kEngThreads;
+        gam[i] = (g.norm && k < k1) ? glb(g.gamma)[k] : (uint16_t)0;
+    }
+    const bool epi_lane = ch == 0 && NP == 1 && tid < M * 32;
+    float e_bias = 0.0f;
+    uint64_t e_res = 0;
+    if (epi_lane) {
+        const int m = tid >> 5, col = group * 32 + (tid & 31);
+        if (g.bias) e_bias = glb(g.bias)[col];
+        if (g.epi == EEPI_RESID) e_res = ld_dev_u64(&g.resid[(size_t)m * g.ld_resid + col]);
+    }
+
+    stamp(c, 2);
+    // 2. inputs of this thread's rows.
+    stamp(c, 3);
+    float xv[kEngRptMax][M];
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+        const EngInput &in = g.in[m];
+        if (in.kind == EIN_TV && g.norm) {
+            // rms_norm_f16 (src/gemv.rs:406-417) over the full row.
+            float keep[kEngRptMax];
+#pragma unroll
+            for (int i = 0; i < kEngRptMax; i++) keep[i] = 0.0f;
+            const int nj = K > tid ? (K - tid + kEngThreads - 1) / kEngThreads : 0;  // <= kEngRptMax (K <= 2048)
+            const int j0 = k0 / kEngThreads;
+            float row[kEngRptMax];
+            wait_strided<kEngRptMax>(in.tv + tid, kEngThreads, nj, tb + in.tag, row, c);
+            float ss = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kEngRptMax; j++) {
+                if (j >= nj) continue;
+                ss += row[j] * row[j];
+#pragma unroll
+                for (int i = 0; i < kEngRptMax; i++)
+                    if (j - j0 == i) keep[i] = row[j];
+            }
+            ss = block_sum(ss, scr);
+            const float inv = 1.0f / sqrtf(ss / (float)K + 1e-6f);
+#pragma unroll
+            for (int i = 0; i < kEngRptMax; i++) {
+                const int k = k0 + tid + i * kEngThreads;
+                xv[i][m] = k < k1 ? keep[i] * inv * f16_to_f32(gam[i]) : 0.0f;
+                if (g.norm_plain && m == M - 1 && group == 0 && ch == 0 && k < k1) st_dev(&g.norm_plain[k], xv[i][m]);
+            }
+        } else if (in.kind == EIN_TV) {
+            const int cnt = k1 > k0 + tid ? (k1 - k0 - tid + kEngThreads - 1) / kEngThreads : 0;
+            float row[kEngRptMax];
+            wait_strided<kEngRptMax>(in.tv + k0 + tid, kEngThreads, cnt, tb + in.tag, row, c);
+#pragma unroll
+            for (int i = 0; i < kEngRptMax; i++) xv[i][m] = i < cnt ? row[i] : 0.0f;
+        } else if (in.kind == EIN_PLAIN) {
+#pragma unroll
+            for (int i = 0; i < kEngRptMax; i++) {
+                const int k = k0 + tid + i * kEngThreads;
+                xv[i][m] = k < k1 ? ld_dev(&in.plain[k]) : 0.0f;
+            }
+        } else {
+            // embed_lookup_q4 (src/gemv.rs:377-400) of the tagged token's row.
+            const uint32_t tok = wait_tv_u32(in.tok_tv, tb + in.tag, c);
+#pragma unroll
+            for (int i = 0; i < kEngRptMax; i++) {
+                const int k = k0 + tid + i * kEngThreads;
+                xv[i][m] = (k < k1 && tok < (uint32_t)in.emb.K) ? q4_element(in.emb, tok, k) : 0.0f;
+            }
+        }
+    }
+
+    stamp(c, 4);
+    // 3. accumulate 32 columns per panel.
+    float acc[NP][M][32];
+#pragma unroll
+    for (int pp = 0; pp < NP; pp++)
+#pragma unroll
+        for (int m = 0; m < M; m++)
+#pragma unroll
+            for (int j = 0; j < 32; j++) acc[pp][m][j] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kEngRptMax; i++) {
+        if (k0 + tid + i * kEngThreads >= k1) continue;
+#pragma unroll
+        for (int pp = 0; pp < NP; pp++) {
+            const float s = f16_to_f32((uint16_t)sv[pp][i]);
+            float sx[M];
+#pragma unroll
+            for (int m = 0; m < M; m++) sx[m] = s * xv[i][m];
+            const uint32_t wd[4] = {wv[pp][i].x, wv[pp][i].y, wv[pp][i].z, wv[pp][i].w};
+#pragma unroll
+            for (int d = 0; d < 4; d++) {
+#pragma unroll
+                for (int b = 0; b < 8; b++) {
+                    const float q = (float)((int)((wd[d] >> (4 * b)) & 15u) - 8);
+#pragma unroll
+                    for (int m = 0; m < M; m++) acc[pp][m][d * 8 + b] = fmaf(sx[m], q, acc[pp][m][d * 8 + b]);
+                }
+            }
+        }
+    }
+
+    stamp(c, 5);
+    // 4. block reduction -> ybuf[pp][m][32].
+#pragma unroll
+    for (int pp = 0; pp < NP; pp++) {
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+#pragma unroll
+            for (int j = 0; j < 32; j++) red[tid * 33 + j] = acc[pp][m][j];
+            __syncthreads();
+            {
+                const int col = tid & 31, prt = tid >> 5;
+                float s = 0.0f;
+#pragma unroll 8
+                for (int r = 0; r < 32; r++) s += red[(prt * 32 + r) * 33 + col];
+                part8[prt * 32 + col] = s;
+            }
+            __syncthreads();
+            if (tid < 32) {
+                float s = 0.0f;
+#pragma unroll
+                for (int q = 0; q < 8; q++) s += part8[q * 32 + tid];
+                ybuf[(pp * M + m) * 32 + tid] = s;
+            }
+        }
+    }
+    __syncthreads();
+
+    stamp(c, 6);
+    // 5. split-K: non-owners publish partials; the owner adds them in order.
+    if (ch > 0) {
+        for (int idx = tid; idx < NP * M * 32; idx += kEngThreads) {
+            const int pp = idx / (M * 32), m = (idx / 32) % M, j = idx & 31;
+            put_tv(&g.part[((size_t)(ch - 1) * M + m) * N + panel[pp] * 32 + j], ybuf[idx], tb + g.part_tag);
+        }
+        return -1;
+    }
+    if (g.kc > 1) {
+        for (int idx = tid; idx < NP * M * 32; idx += kEngThreads) {
+            const int pp = idx / (M * 32), m = (idx / 32) % M, j = idx & 31;
+            float pv4[4];
+            wait_strided<4>(&g.part[(size_t)m * N + panel[pp] * 32 + j], (size_t)M * N, g.kc - 1, tb + g.part_tag, pv4, c);
+            float s = ybuf[idx];
+#pragma unroll
+            for (int cc = 0; cc < 4; cc++)
+                if (cc < g.kc - 1) s += pv4[cc];
+            ybuf[idx] = s;
+        }
+        __syncthreads();
+    }
+
+    // 6. epilogue
+    if (NP == 2) {
+        // silu(g) * u, src/talker.rs:342-345
+        for (int idx = tid; idx < M * 32; idx += kEngThreads) {
+            const int m = idx >> 5, j = idx & 31;
+            const float gt = ybuf[m * 32 + j], up = ybuf[(M + m) * 32 + j];
+            const float h = (gt / (1.0f + expf(-gt))) * up;
+            put_tv(&g.out[(size_t)m * g.ld_out + group * 32 + j], h, tb + g.out_tag);
+        }
+    } else if (epi_lane) {
+        const int m = tid >> 5, j = tid & 31, col = group * 32 + j;
+        float v = ybuf[m * 32 + j];
+        if (g.bias) v += e_bias;
+        if (g.epi == EEPI_RESID) {
+            const float r = (uint32_t)(e_res >> 32) == tb + g.resid_tag
+                                ? __uint_as_float((uint32_t)e_res)
+                                : wait_tv(&g.resid[(size_t)m * g.ld_resid + col], tb + g.resid_tag, c);
+            v = r + v;
+        }
+        put_tv(&g.out[(size_t)m * g.ld_out + col], v, tb + g.out_tag);
+        if (g.out_plain) st_dev(&g.out_plain[(size_t)m * g.ld_plain + col], v);
+    }
+    stamp(c, 7);
+    return group;
+}
+
+// ---------------------------------------------------------------------------
+// Attention task: one kv head x one split of positions, M query rows.
+// QK-norm (src/talker.rs:86-99) and split-half RoPE (src/rope.rs:79-92) of the
+// raw q/k, K/V append (src/talker.rs:299-302), then softmax(q.K^T*scale).V
+// over the split (src/talker.rs:304-331), causal across the M new rows.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int eng_attn(const EngAttn &a, int task, uint32_t tb, const EngState &st, Ctl &c, float *smem) {
+    constexpr int HD = 128, HALF = 64, CH = 256;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int G = a.nq / a.nkv;
+    const int M = a.M;
+    const int kvh = task / a.nsplit, sp = task - kvh * a.nsplit;
+    const int base = a.from_state ? st.kvlen : a.len_const;
+    const int pos0 = a.from_state ? st.pos : a.pos_const;
+    const int Lt = base + M;
+    const int chunk = (Lt + a.nsplit - 1) / a.nsplit;
+    const int t0 = sp * chunk, t1 = min(Lt, t0 + chunk);
+    const int nt = max(0, t1 - t0);
+    float *qs = smem;                 // [M][G][HD]
+    float *kn = qs + kEngMaxM * 4 * HD;  // [M][HD]
+    float *vn = kn + kEngMaxM * HD;      // [M][HD]
+    float *sc = vn + kEngMaxM * HD;      // [M*G][CH]
+    float *pv = sc + kEngMaxM * 4 * CH;  // [M*G][HD]
+    float *ml = pv + kEngMaxM * 4 * HD;  // [M*G][2]
+
+    // 1. raw q (G heads), k, v of this kv head for the M rows
+    stamp(c, 2);
+    const int per = (G + 2) * HD;
+    {
+        constexpr int NB = kEngMaxM * 6 * HD / kEngThreads;  // M <= 2, G <= 4
+        const tv_t *ptr[NB];
+        uint32_t tg[NB];
+        float val[NB];
+        int cnt = 0;
+#pragma unroll
+        for (int i = 0; i < NB; i++) {
+            const int idx = tid + i * kEngThreads;
+            tg[i] = tb + a.qkv_tag;
+            ptr[i] = a.qkv;
+            if (idx < M * per) {
+                const int m = idx / per, r = idx - m * per, prt = r / HD, d = r - prt * HD;
+                int src;
+                if (prt < G)
+                    src = (kvh * G + prt) * HD + d;
+                else if (prt == G)
+                    src = a.nq * HD + kvh * HD + d;
+                else
+                    src = (a.nq + a.nkv) * HD + kvh * HD + d;
+                ptr[i] = &a.qkv[(size_t)m * a.ld_qkv + src];
+                cnt = i + 1;
+            }
+        }
+        wait_list<NB>(ptr, tg, cnt, val, c);
+#pragma unroll
+        for (int i = 0; i < NB; i++) {
+            const int idx = tid + i * kEngThreads;
+            if (idx >= M * per) continue;
+            const int m = idx / per, r = idx - m * per, prt = r / HD, d = r - prt * HD;
+            if (prt < G)
+                qs[(m * G + prt) * HD + d] = val[i];
+            else if (prt == G)
+                kn[m * HD + d] = val[i];
+            else
+                vn[m * HD + d] = val[i];
+        }
+    }
+    __syncthreads();
+    stamp(c, 3);
+    // 2. QK-norm + RoPE, one wave per 128-vector
+    for (int vi = wave; vi < M * (G + 1); vi += kEngThreads / 64) {
+        const int m = vi / (G + 1), r = vi - m * (G + 1);
+        float *vec = r < G ? &qs[(m * G + r) * HD] : &kn[m * HD];
+        const uint16_t *gam = r < G ? a.q_norm : a.k_norm;
+        const float x1 = vec[lane], x2 = vec[lane + HALF];
+        const float ss = wave_sum(x1 * x1 + x2 * x2);
+        const float inv = 1.0f / sqrtf(ss / (float)HD + 1e-6f);
+        const float n1 = x1 * inv * f16_to_f32(glb(gam)[lane]);
+        const float n2 = x2 * inv * f16_to_f32(glb(gam)[lane + HALF]);
+        const int pos = pos0 + m;
+        float o1 = n1, o2 = n2;
+        if (!(a.rope_skip_oob && pos >= a.rope_rows)) {
+            const float cs = glb(a.rope_cos)[(size_t)pos * HALF + lane], sn = glb(a.rope_sin)[(size_t)pos * HALF + lane];
+            o1 = n1 * cs - n2 * sn;
+            o2 = n2 * cs + n1 * sn;
+        }
+        vec[lane] = o1;
+        vec[lane + HALF] = o2;
+    }
+    __syncthreads();
+    stamp(c, 4);
+    // 3. append the new rows that fall in this split
+    float *Kb = a.kcache + (size_t)kvh * a.kv_cap * HD;
+    float *Vb = a.vcache + (size_t)kvh * a.kv_cap * HD;
+    for (int idx = tid; idx < M * HD; idx += kEngThreads) {
+        const int m = idx / HD, d = idx - m * HD, t = base + m;
+        if (t >= t0 && t < t1) {
+            st_dev(&Kb[(size_t)t * HD + d], kn[m * HD + d]);
+            st_dev(&Vb[(size_t)t * HD + d], vn[m * HD + d]);
+        }
+    }
+    stamp(c, 5);
+    // 4. scores: 16 lanes per position, 8 dims per lane
+    {
+        const int l16 = tid & 15, slot = tid >> 4;
+        constexpr int UNR = 4;
+        for (int tb0 = slot; tb0 < nt; tb0 += UNR * (kEngThreads / 16)) {
+            uint64_t raw[UNR][4];
+#pragma unroll
+            for (int u = 0; u < UNR; u++) {
+                const int t = t0 + tb0 + u * (kEngThreads / 16);
+                if (tb0 + u * (kEngThreads / 16) < nt && t < base) {
+                    const uint64_t *src = reinterpret_cast<const uint64_t *>(&Kb[(size_t)t * HD + l16 * 8]);
+#pragma unroll
+                    for (int e = 0; e < 4; e++) raw[u][e] = ld_dev_u64(src + e);
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < UNR; u++) {
+            const int tt = tb0 + u * (kEngThreads / 16);
+            if (tt >= nt) continue;
+            const int t = t0 + tt;
+            float kr[8];
+            if (t < base) {
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    kr[2 * e] = __uint_as_float((uint32_t)raw[u][e]);
+                    kr[2 * e + 1] = __uint_as_float((uint32_t)(raw[u][e] >> 32));
+                }
+            } else {
+#pragma unroll
+                for (int e = 0; e < 8; e++) kr[e] = kn[(t - base) * HD + l16 * 8 + e];
+            }
+            for (int m = 0; m < M; m++) {
+                for (int g = 0; g < G; g++) {
+                    const float *qq = &qs[(m * G + g) * HD + l16 * 8];
+                    float dot = 0.0f;
+#pragma unroll
+                    for (int e = 0; e < 8; e++) dot += qq[e] * kr[e];
+                    dot += __shfl_xor(dot, 8, 16);
+                    dot += __shfl_xor(dot, 4, 16);
+                    dot += __shfl_xor(dot, 2, 16);
+                    dot += __shfl_xor(dot, 1, 16);
+                    if (l16 == 0) sc[(m * G + g) * CH + tt] = (t <= base + m) ? dot * a.scale : -INFINITY;
+                }
+            }
+            }
+        }
+    }
+    __syncthreads();
+    stamp(c, 6);
+    // 5. local softmax statistics, one wave per (row, head)
+    for (int pi = wave; pi < M * G; pi += kEngThreads / 64) {
+        float mx = -INFINITY;
+        for (int t = lane; t < nt; t += 64) mx = fmaxf(mx, sc[pi * CH + t]);
+        mx = wave_max(mx);
+        float l = 0.0f;
+        for (int t = lane; t < nt; t += 64) {
+            const float s = sc[pi * CH + t];
+            const float e = (mx == -INFINITY) ? 0.0f : expf(s - mx);
+            sc[pi * CH + t] = e;
+            l += e;
+        }
+        l = wave_sum(l);
+        if (lane == 0) {
+            ml[pi * 2] = mx;
+            ml[pi * 2 + 1] = l;
+        }
+    }
+    __syncthreads();
+    stamp(c, 7);
+    // 6. P.V: thread (d, half) walks every other position; V read once per (d)
+    {
+        const int d = tid & (HD - 1), hf = tid >> 7;
+        float acc[kEngMaxM * 4];
+#pragma unroll
+        for (int i = 0; i < kEngMaxM * 4; i++) acc[i] = 0.0f;
+        const int npi = M * G;
+        constexpr int VU = 8;
+        for (int tb0 = hf; tb0 < nt; tb0 += 2 * VU) {
+            float vv[VU];
+#pragma unroll
+            for (int u = 0; u < VU; u++) {
+                const int tt = tb0 + 2 * u, t = t0 + tt;
+                vv[u] = 0.0f;
+                if (tt < nt) vv[u] = t < base ? ld_dev(&Vb[(size_t)t * HD + d]) : vn[(t - base) * HD + d];
+            }
+#pragma unroll
+            for (int u = 0; u < VU; u++) {
+                const int tt = tb0 + 2 * u;
+                if (tt >= nt) continue;
+#pragma unroll
+                for (int pi = 0; pi < kEngMaxM * 4; pi++)
+                    if (pi < npi) acc[pi] += sc[pi * CH + tt] * vv[u];
+            }
+        }
+        if (hf == 1) {
+#pragma unroll
+            for (int pi = 0; pi < kEngMaxM * 4; pi++)
+                if (pi < npi) pv[pi * HD + d] = acc[pi];
+        }
+        __syncthreads();
+        // K/V appends complete before the outputs that publish this step
+        wait_stores();
+        __syncthreads();
+        if (hf == 0) {
+#pragma unroll
+            for (int pi = 0; pi < kEngMaxM * 4; pi++) {
+                if (pi >= npi) continue;
+                const int m = pi / G, g = pi - m * G, h = kvh * G + g;
+                const float o = acc[pi] + pv[pi * HD + d];
+                if (a.nsplit == 1) {
+                    const float l = ml[pi * 2 + 1];
+                    put_tv(&a.out[(size_t)m * a.nq * HD + h * HD + d], o / l, tb + a.out_tag);
+                } else {
+                    tv_t *dst = a.part + (((size_t)m * a.nq + h) * a.nsplit + sp) * (HD + 2);
+                    put_tv(&dst[2 + d], o, tb + a.part_tag);
+                    if (d == 0) {
+                        put_tv(&dst[0], ml[pi * 2], tb + a.part_tag);
+                        put_tv(&dst[1], ml[pi * 2 + 1], tb + a.part_tag);
+                    }
+                }
+            }
+        }
+    }
+    return task;
+}
+
+// Combine the splits of one (row, query head): flash-decode merge.
+__device__ __forceinline__ int eng_combine(const EngCombine &cb, int task, uint32_t tb, Ctl &c) {
+    constexpr int HD = 128;
+    const int m = task / cb.nq, h = task - m * cb.nq;
+    const int d = threadIdx.x;
+    if (d >= HD) return task;
+    const tv_t *base = cb.part + ((size_t)m * cb.nq + h) * cb.nsplit * (HD + 2);
+    float ms[kEngMaxSplit], ls[kEngMaxSplit], os[kEngMaxSplit];
+    wait_strided<kEngMaxSplit>(base, HD + 2, cb.nsplit, tb + cb.part_tag, ms, c);
+    wait_strided<kEngMaxSplit>(base + 1, HD + 2, cb.nsplit, tb + cb.part_tag, ls, c);
+    wait_strided<kEngMaxSplit>(base + 2 + d, HD + 2, cb.nsplit, tb + cb.part_tag, os, c);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int s = 0; s < kEngMaxSplit; s++)
+        if (s < cb.nsplit) mx = fmaxf(mx, ms[s]);
+    float o = 0.0f, l = 0.0f;
+#pragma unroll
+    for (int s = 0; s < kEngMaxSplit; s++) {
+        if (s >= cb.nsplit || ms[s] == -INFINITY) continue;
+        const float w = expf(ms[s] - mx);
+        o += w * os[s];
+        l += w * ls[s];
+    }
+    put_tv(&cb.out[(size_t)m * cb.nq * HD + h * HD + d], o / l, tb + cb.out_tag);
+    return task;
+}
+
+// sample_argmax (src/code_predictor.rs:328-334): last index of the maximum.
+__device__ __forceinline__ void eng_argmax(const EngArgmax &a, uint32_t tb, const EngState &st, Ctl &c, uint32_t *codes,
+                           int max_codes, float *smem) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float bv = -INFINITY;
+    int bi = -1, nan = 0;
+    constexpr int NA = 16;  // n <= 4096
+    float vals[NA];
+    const int cnt = a.n > tid ? (a.n - tid + kEngThreads - 1) / kEngThreads : 0;
+    wait_strided<NA>(a.logits + tid, kEngThreads, cnt, tb + a.logits_tag, vals, c);
+#pragma unroll
+    for (int k = 0; k < NA; k++) {
+        if (k >= cnt) continue;
+        const int i = tid + k * kEngThreads;
+        const float v = vals[k];
+        if (v != v)
+            nan = 1;
+        else if (bi < 0 || v >= bv) {
+            bv = v;
+            bi = i;
+        }
+    }
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(bv, off, 64);
+        const int oi = __shfl_xor(bi, off, 64);
+        if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi > bi))) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    int *si = reinterpret_cast<int *>(smem);
+    float *sv = smem + 8;
+    const int anynan = __syncthreads_or(nan);
+    if (lane == 0) {
+        sv[wave] = bv;
+        si[wave] = bi;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        float b = -INFINITY;
+        int ix = -1;
+        for (int w = 0; w < kEngThreads / 64; w++)
+            if (si[w] >= 0 && (ix < 0 || sv[w] > b || (sv[w] == b && si[w] > ix))) {
+                b = sv[w];
+                ix = si[w];
+            }
+        uint32_t code = ix < 0 ? 0u : (uint32_t)ix;
+        if (anynan) {
+            code = 0u;
+            fail_dev(c, QTTS_ENAN);
+        }
+        if (st.frame < max_codes) st_dev_u32(&codes[(size_t)a.group * max_codes + st.frame], code);
+        put_tv_u32(a.code, code, tb + a.code_tag);
+    }
+    __syncthreads();
+}
+
+// f32 sum of s[0..n) in index order by one thread (the order the reference
+// sums in).  The LDS reads are issued 32 at a time so the add chain, not the
+// read latency, sets the pace.  s is 16-byte aligned.
+__device__ __forceinline__ float seq_sum(const float *s, int n) {
+    float sum = 0.0f;
+    int i = 0;
+    for (; i + 32 <= n; i += 32) {
+        float4 v[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) v[q] = *reinterpret_cast<const float4 *>(&s[i + 4 * q]);
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            sum += v[q].x;
+            sum += v[q].y;
+            sum += v[q].z;
+            sum += v[q].w;
+        }
+    }
+    for (; i < n; i++) sum += s[i];
+    return sum;
+}
+
+// First index j with r < p[0] + ... + p[j] (f32, summed in index order), or
+// -1; one thread, reads batched like seq_sum.
+__device__ __forceinline__ int seq_find(const float *p, int n, float r) {
+    float cum = 0.0f;
+    int i = 0;
+    for (; i + 32 <= n; i += 32) {
+        float4 v[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) v[q] = *reinterpret_cast<const float4 *>(&p[i + 4 * q]);
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            cum += v[q].x;
+            if (r < cum) return i + 4 * q;
+            cum += v[q].y;
+            if (r < cum) return i + 4 * q + 1;
+            cum += v[q].z;
+            if (r < cum) return i + 4 * q + 2;
+            cum += v[q].w;
+            if (r < cum) return i + 4 * q + 3;
+        }
+    }
+    for (; i < n; i++) {
+        cum += p[i];
+        if (r < cum) return i;
+    }
+    return -1;
+}
+
+// Exclusive scan over the 256-thread block.
+__device__ int block_exscan(int v, int *wsum, int *total) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    int x = v;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int y = __shfl_up(x, off, 64);
+        if (lane >= off) x += y;
+    }
+    __syncthreads();
+    if (lane == 63) wsum[wave] = x;
+    __syncthreads();
+    int base = 0, tot = 0;
+    for (int w = 0; w < kEngThreads / 64; w++) {
+        if (w < wave) base += wsum[w];
+        tot += wsum[w];
+    }
+    *total = tot;
+    __syncthreads();
+    return base + x - v;
+}
+
+// sample_token (src/generate_new.rs:329-391), same schedule as k_sample:
+// the three order-dependent f32 sums on one lane in index order, the rest
+// in parallel; the stable top-k by radix select over the float bits.
+__device__ __forceinline__ void eng_sample(const EngSample &P, uint32_t tb, const EngState &st, EngState *st_out, Ctl &c,
+                           uint32_t *codes, int max_codes, float *smem) {
+    const int V = P.vocab, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float *s = smem;
+    int *list = reinterpret_cast<int *>(s + V);
+    unsigned *hist = reinterpret_cast<unsigned *>(list + V);
+    int *wsum = reinterpret_cast<int *>(hist + 256);
+    float *fred = reinterpret_cast<float *>(wsum + 8);
+    int *ired = reinterpret_cast<int *>(fred + 8);
+    int *misc = ired + 8;  // [0] prefix [1] mask [2] remaining [3] nan [4] token [5] count
+    float *fmisc = reinterpret_cast<float *>(misc + 8);  // [0] max [1] sum
+    uint64_t rng = st.rng;
+
+    {
+        constexpr int NS = 16;  // V <= 4096
+        float lv[NS];
+#pragma unroll
+        for (int k = 0; k < NS; k++) {
+            const int i = tid + k * kEngThreads;
+            lv[k] = i < V ? ld_dev(&P.logits[i]) : 0.0f;
+        }
+#pragma unroll
+        for (int k = 0; k < NS; k++) {
+            const int i = tid + k * kEngThreads;
+            if (i < V) s[i] = lv[k];
+        }
+    }
+    if (tid == 0) {
+        misc[3] = 0;
+        misc[4] = 0;
+    }
+    __syncthreads();
+    // prev_tokens = the previous frame's 16 codes (zeros before the first)
+    uint32_t *prev = reinterpret_cast<uint32_t *>(misc + 16);
+    if (tid < P.num_prev) prev[tid] = st.frame > 0 ? ld_dev_u32(&codes[(size_t)tid * max_codes + st.frame - 1]) : 0u;
+    __syncthreads();
+    if (tid == 0 && P.penalty != 1.0f) {
+        for (int j = 0; j < P.num_prev; j++) {
+            const uint32_t t = prev[j];
+            if (t < (uint32_t)V) {
+                if (s[t] > 0.0f)
+                    s[t] /= P.penalty;
+                else
+                    s[t] *= P.penalty;
+            }
+        }
+    }
+    __syncthreads();
+    if (P.greedy) {
+        float bv = -INFINITY;
+        int bi = -1, nan = 0;
+        for (int i = tid; i < V; i += kEngThreads) {
+            const float v = s[i];
+            if (v != v)
+                nan = 1;
+            else if (bi < 0 || v >= bv) {
+                bv = v;
+                bi = i;
+            }
+        }
+        for (int off = 32; off >= 1; off >>= 1) {
+            const float ov = __shfl_xor(bv, off, 64);
+            const int oi = __shfl_xor(bi, off, 64);
+            if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi > bi))) {
+                bv = ov;
+                bi = oi;
+            }
+        }
+        const int anynan = __syncthreads_or(nan);
+        if (lane == 0) {
+            fred[wave] = bv;
+            ired[wave] = bi;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            float b = -INFINITY;
+            int ix = -1;
+            for (int w = 0; w < kEngThreads / 64; w++)
+                if (ired[w] >= 0 && (ix < 0 || fred[w] > b || (fred[w] == b && ired[w] > ix))) {
+                    b = fred[w];
+                    ix = ired[w];
+                }
+            misc[4] = ix < 0 ? 0 : ix;
+            misc[3] = anynan;
+        }
+        __syncthreads();
+    } else {
+        if (P.temperature != 1.0f)
+            for (int i = tid; i < V; i += kEngThreads) s[i] /= P.temperature;
+        float mx = -INFINITY;
+        for (int i = tid; i < V; i += kEngThreads) mx = fmaxf(mx, s[i]);
+        mx = wave_max(mx);
+        __syncthreads();
+        if (lane == 0) fred[wave] = mx;
+        __syncthreads();
+        if (tid == 0) {
+            float t = -INFINITY;
+            for (int w = 0; w < kEngThreads / 64; w++) t = fmaxf(t, fred[w]);
+            fmisc[0] = t;
+        }
+        __syncthreads();
+        const float maxv = fmisc[0];
+        for (int i = tid; i < V; i += kEngThreads) s[i] = (float)exp((double)(s[i] - maxv));
+        __syncthreads();
+        if (tid == 0) fmisc[1] = seq_sum(s, V);
+        __syncthreads();
+        const float sum = fmisc[1];
+        for (int i = tid; i < V; i += kEngThreads) s[i] = s[i] / sum;
+        __syncthreads();
+        if (P.top_k > 0 && P.top_k < V) {
+            int nan = 0;
+            for (int i = tid; i < V; i += kEngThreads)
+                if (s[i] != s[i]) nan = 1;
+            const int anynan = __syncthreads_or(nan);
+            if (tid == 0) {
+                misc[0] = 0;
+                misc[1] = 0;
+                misc[2] = P.top_k;
+                misc[3] = anynan;
+            }
+            __syncthreads();
+            if (!anynan) {
+                for (int pass = 0; pass < 4; pass++) {
+                    const int shift = 24 - 8 * pass;
+                    for (int b = tid; b < 256; b += kEngThreads) hist[b] = 0u;
+                    __syncthreads();
+                    const unsigned prefix = (unsigned)misc[0], mask = (unsigned)misc[1];
+                    for (int i = tid; i < V; i += kEngThreads) {
+                        const unsigned key = __float_as_uint(s[i]);
+                        if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+                    }
+                    __syncthreads();
+                    if (wave == 0) {
+                        // digits in descending order: lane l holds 255-4l .. 252-4l
+                        const int rem = misc[2];
+                        int h[4], loc = 0;
+#pragma unroll
+                        for (int q = 0; q < 4; q++) {
+                            h[q] = (int)hist[255 - 4 * lane - q];
+                            loc += h[q];
+                        }
+                        int incl = loc;
+#pragma unroll
+                        for (int off = 1; off < 64; off <<= 1) {
+                            const int y = __shfl_up(incl, off, 64);
+                            if (lane >= off) incl += y;
+                        }
+                        const int excl = incl - loc;
+                        // the first lane whose range reaches rem holds the digit
+                        const bool mine = excl < rem && incl >= rem;
+                        if (mine) {
+                            int cum = excl, sel = 255 - 4 * lane - 3;
+#pragma unroll
+                            for (int q = 0; q < 4; q++) {
+                                if (cum + h[q] >= rem) {
+                                    sel = 255 - 4 * lane - q;
+                                    break;
+                                }
+                                cum += h[q];
+                            }
+                            misc[2] = rem - cum;
+                            misc[0] = (int)(prefix | ((unsigned)sel << shift));
+                            misc[1] = (int)(mask | (255u << shift));
+                        }
+                    }
+                    __syncthreads();
+                }
+                const unsigned T = (unsigned)misc[0];
+                const int need_eq = misc[2];
+                const int per = (V + kEngThreads - 1) / kEngThreads;
+                const int i0 = min(V, tid * per), i1 = min(V, i0 + per);
+                int neq = 0;
+                for (int i = i0; i < i1; i++) neq += (__float_as_uint(s[i]) == T);
+                int tot;
+                int eq_rank = block_exscan(neq, wsum, &tot);
+                int nkeep = 0;
+                unsigned keep_bits = 0u;
+                for (int i = i0; i < i1; i++) {
+                    const unsigned key = __float_as_uint(s[i]);
+                    bool keep = key > T;
+                    if (key == T) {
+                        keep = eq_rank < need_eq;
+                        eq_rank++;
+                    }
+                    if (keep) {
+                        keep_bits |= 1u << (i - i0);
+                        nkeep++;
+                    }
+                }
+                int pos = block_exscan(nkeep, wsum, &tot);
+                for (int i = i0; i < i1; i++)
+                    if (keep_bits & (1u << (i - i0))) list[pos++] = i;
+                __syncthreads();
+                // compact the kept probabilities, in index order, into s[0..tot)
+                constexpr int NS = 16;  // V <= 4096
+                float kv[NS];
+#pragma unroll
+                for (int k = 0; k < NS; k++) {
+                    const int j = tid + k * kEngThreads;
+                    kv[k] = j < tot ? s[list[j]] : 0.0f;
+                }
+                __syncthreads();
+#pragma unroll
+                for (int k = 0; k < NS; k++) {
+                    const int j = tid + k * kEngThreads;
+                    if (j < tot) s[j] = kv[k];
+                }
+                __syncthreads();
+                if (tid == 0) fmisc[1] = seq_sum(s, tot);
+                __syncthreads();
+                const float sum2 = fmisc[1];
+                if (sum2 > 0.0f)
+                    for (int j = tid; j < tot; j += kEngThreads) s[j] = s[j] / sum2;
+                __syncthreads();
+                if (tid == 0) {
+                    const float r = simple_rand_dev(&rng);
+                    const int j = seq_find(s, tot, r);
+                    misc[4] = j < 0 ? 0 : list[j];
+                }
+            }
+            __syncthreads();
+        } else {
+            if (tid == 0) {
+                const float r = simple_rand_dev(&rng);
+                const int j = seq_find(s, V, r);
+                misc[4] = j < 0 ? 0 : j;
+            }
+            __syncthreads();
+        }
+    }
+    if (tid == 0) {
+        uint32_t tok = (uint32_t)misc[4];
+        EngState next = st;
+        next.rng = rng;
+        if (misc[3]) {
+            fail_dev(c, QTTS_ENAN);
+        } else if (P.stop_on_eos && tok == P.eos) {
+            st_dev_i32(c.done, 1);  // EOS: the rest of this frame is abandoned
+        } else {
+            if (st.frame < max_codes) st_dev_u32(&codes[st.frame], tok);
+            next.pos = st.pos + 1;
+            next.kvlen = st.kvlen + 1;
+            next.frame = st.frame + 1;
+            put_tv_u32(P.tok, tok, tb + P.tok_tag);
+        }
+        st_dev_i32(&st_out->pos, next.pos);
+        st_dev_i32(&st_out->kvlen, next.kvlen);
+        st_dev_i32(&st_out->frame, next.frame);
+        st_dev_u64(&st_out->rng, next.rng);
+    }
+    __syncthreads();
+}
+
+// Next talker input (src/generate_new.rs:270-286), 256 columns per task.
+__device__ __forceinline__ int eng_embsum(const EngEmbSum &E, int task, uint32_t tb, const EngState &st, Ctl &c) {
+    const int j = task * kEngThreads + threadIdx.x;
+    if (E.mode == 2) {  // publish a plain row (host input) as a tagged vector
+        if (j < E.hidden) put_tv(&E.out[j], ld_dev(&E.pad[j]), tb + E.out_tag);
+        return task;
+    }
+    const uint32_t tok = wait_tv_u32(E.tok, tb + E.tok_tag, c);
+    if (j >= E.hidden) return task;
+    float v = tok < (uint32_t)E.codec_emb.K ? q4_element(E.codec_emb, tok, j) : 0.0f;
+    if (E.mode == 0) {
+        const tv_t *ptr[kMaxGroups];
+        uint32_t tg[kMaxGroups];
+        float cv[kMaxGroups];
+#pragma unroll
+        for (int g = 0; g < kMaxGroups; g++) {
+            ptr[g] = g < E.num_groups ? E.code[g] : E.tok;
+            tg[g] = tb + (g < E.num_groups ? E.code_tag[g] : E.tok_tag);
+        }
+        wait_list<kMaxGroups>(ptr, tg, E.num_groups, cv, c);
+        float acc = 0.0f;
+#pragma unroll
+        for (int g = 0; g < kMaxGroups; g++) {
+            if (g >= E.num_groups) continue;
+            const uint32_t cg = __float_as_uint(cv[g]);
+            acc += cg < (uint32_t)E.group_emb[g].K ? q4_element(E.group_emb[g], cg, j) : 0.0f;
+        }
+        v += acc;
+        const float *text = st.frame < E.trailing_len ? E.trailing + (size_t)st.frame * E.hidden : E.pad;
+        v += ld_dev(&text[j]);
+    }
+    put_tv(&E.out[j], v, tb + E.out_tag);
+    return task;
+}
+
+}  // namespace
+
+__global__ __launch_bounds__(kEngThreads) void k_engine(EngArgs A) {
+    __shared__ __align__(16) float smem[kEngSmemFloats];
+    if (ld_dev_i32(A.done)) return;
+    Ctl c{A.done, A.status, 0u, false, nullptr};
+    EngState st;
+    st.pos = ld_dev_i32(&A.st_in->pos);
+    st.kvlen = ld_dev_i32(&A.st_in->kvlen);
+    st.frame = ld_dev_i32(&A.st_in->frame);
+    st.pad = 0;
+    st.rng = ld_dev_u64(&A.st_in->rng);
+    const int G = gridDim.x;
+    for (int oi = 0; oi < A.nops; oi++) {
+        const EngOp &op = A.ops[oi];
+        int t = ((int)blockIdx.x - op.rot) % G;
+        if (t < 0) t += G;
+        uint64_t *tr = (A.trace && t < op.ntasks) ? A.trace + ((size_t)oi * G + blockIdx.x) * kTraceSlots : nullptr;
+        c.tr = tr;
+        if (tr && threadIdx.x == 0) {
+            glb(tr)[0] = wall_clock64();
+            glb(tr)[8] = clock64();
+        }
+        for (; t < op.ntasks; t += G) {
+            int fi = -1;  // flag this task sets, if any
+            switch (op.kind) {
+                case EOP_GEMV: {
+                    const EngGemv &g = op.gemv;
+                    if (g.M == 1) {
+                        if (g.epi == EEPI_SWIGLU)
+                            fi = eng_gemv<1, 2>(g, t, A.tag_base, c, smem);
+                        else
+                            fi = eng_gemv<1, 1>(g, t, A.tag_base, c, smem);
+                    } else {
+                        if (g.epi == EEPI_SWIGLU)
+                            fi = eng_gemv<2, 2>(g, t, A.tag_base, c, smem);
+                        else
+                            fi = eng_gemv<2, 1>(g, t, A.tag_base, c, smem);
+                    }
+                    break;
+                }
+                case EOP_ATTN: fi = eng_attn(op.attn, t, A.tag_base, st, c, smem); break;
+                case EOP_COMBINE: fi = eng_combine(op.comb, t, A.tag_base, c); break;
+                case EOP_ARGMAX: eng_argmax(op.amax, A.tag_base, st, c, A.codes, A.max_codes, smem); break;
+                case EOP_SAMPLE: eng_sample(op.samp, A.tag_base, st, A.st_out, c, A.codes, A.max_codes, smem); break;
+                case EOP_EMBSUM: fi = eng_embsum(op.emb, t, A.tag_base, st, c); break;
+                default: break;
+            }
+            (void)fi;
+            if (__syncthreads_or(c.bad ? 1 : 0)) return;
+        }
+        if (tr && threadIdx.x == 0) {
+            glb(tr)[1] = wall_clock64();
+            glb(tr)[9] = clock64();
+        }
+    }
+}
+
+hipError_t launch_engine(hipStream_t st, const EngArgs &a, int grid) {
+    EngArgs args = a;
+    void *kargs[] = {&args};
+    return hipLaunchCooperativeKernel((const void *)k_engine, dim3((unsigned)grid), dim3(kEngThreads), kargs, 0, st);
+}
+
+int engine_max_grid() {
+    int dev = 0, ncu = 0, per = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 0;
+    if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, (const void *)k_engine, kEngThreads, 0) != hipSuccess)
+        return 0;
+    return ncu * (per < 1 ? 0 : 1);
+}
+
+}  // namespace qtts

@@ -15,48 +15,12 @@
 #include <cmath>
 
 #include "../../include/qtts.h"
+#include "device_common.h"
 #include "internal.h"
 
 namespace qtts {
 
 namespace {
-
-__device__ __forceinline__ float f16_to_f32(uint16_t h) {
-    return (float)__builtin_bit_cast(_Float16, h);
-}
-
-// Cross-workgroup traffic inside one kernel (split-K partials, softmax
-// partials, logits for a final argmax) goes through agent-scope atomic
-// loads/stores, which the gfx950 memory model performs at the device
-// coherence point.  That orders the handoff without an agent-scope fence,
-// whose L2 writeback + invalidate per workgroup costs more than the GEMV.
-__device__ __forceinline__ void st_dev(float *p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ float ld_dev(const float *p) {
-    return __hip_atomic_load(const_cast<float *>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-// Waits until this workgroup's device-scope stores have completed, then
-// counts one arrival; returns the count before the increment.
-__device__ __forceinline__ unsigned arrive_dev(unsigned *ctr) {
-    return __hip_atomic_fetch_add(ctr, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void reset_dev(unsigned *ctr) {
-    __hip_atomic_store(ctr, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup"); }
-
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
-    return v;
-}
-
-__device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
-}
 
 // Sum over a 256-thread block; every thread gets the result.
 __device__ float block_sum_256(float v, float *scratch /* >= 4 */) {
@@ -563,15 +527,6 @@ __device__ int block_exscan_1024(int v, int *wsum /* >= 16 */, int *total) {
     return base + x - v;
 }
 
-__device__ __forceinline__ float simple_rand_dev(uint64_t *state) {
-    uint64_t s = *state;
-    s ^= s << 13;
-    s ^= s >> 7;
-    s ^= s << 17;
-    *state = s;
-    return (float)s / 18446744073709551616.0f;  // (u64::MAX as f32) == 2^64
-}
-
 }  // namespace
 
 __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleParams P) {
@@ -812,13 +767,6 @@ void launch_sample(hipStream_t st, const SampleParams &p) {
 // ---------------------------------------------------------------------------
 // Embedding gathers
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float q4_element(const DevQ4 &w, uint32_t row, int col) {
-    const size_t r = (size_t)(col >> 5) * w.K + row;
-    const uint8_t byte = reinterpret_cast<const uint8_t *>(w.wq)[r * 16 + ((col & 31) >> 1)];
-    const int nib = (col & 1) ? (byte >> 4) : (byte & 15);
-    return f16_to_f32(w.ws[r]) * (float)(nib - 8);
-}
-
 __global__ void k_embed_row(DevQ4 w, const uint32_t *tok, float *out, const int *d_done) {
     if (d_done && *d_done) return;
     const int j = blockIdx.x * blockDim.x + threadIdx.x;
