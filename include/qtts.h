@@ -129,6 +129,9 @@ typedef struct qtts_predictor qtts_predictor;
 
 /* Creates a context on HIP device `device` with its own stream. */
 qtts_status qtts_ctx_create(int32_t device, qtts_ctx **out);
+/* Releases the caller's handle.  Weights, caches and models made from the
+ * context keep it alive until they are freed, in any order; the context must
+ * not be used for new calls after this. */
 void qtts_ctx_destroy(qtts_ctx *ctx);
 /* Message of the last failed call on this context ("" if none). */
 const char *qtts_last_error(const qtts_ctx *ctx);

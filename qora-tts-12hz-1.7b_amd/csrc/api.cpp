@@ -7,6 +7,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
+#include <atomic>
 #include <cstring>
 #include <functional>
 #include <memory>
@@ -51,7 +52,37 @@ struct qtts_ctx {
     int eng_grid = 0;
     uint64_t *eng_trace = nullptr;  // QTTS_ENGINE_TRACE: per-op block timestamps
     size_t eng_trace_cap = 0;
+    // The context and every object made from it hold one reference each, so
+    // objects may be freed after qtts_ctx_destroy (e.g. in any order at
+    // interpreter shutdown).
+    std::atomic<int> refs{1};
 };
+
+namespace {
+
+qtts_ctx *ctx_retain(qtts_ctx *c) {
+    c->refs.fetch_add(1);
+    return c;
+}
+
+void ctx_release(qtts_ctx *c) {
+    if (c->refs.fetch_sub(1) != 1) return;
+    if (c->stream) (void)hipStreamSynchronize(c->stream);
+    (void)hipFree(c->partial);
+    (void)hipFree(c->counters);
+    (void)hipFree(c->attn_part);
+    (void)hipFree(c->attn_counters);
+    (void)hipFree(c->d_in);
+    (void)hipFree(c->d_out);
+    (void)hipFree(c->d_small);
+    (void)hipFree(c->eng_state);
+    (void)hipFree(c->eng_done);
+    (void)hipFree(c->eng_trace);
+    if (c->stream) (void)hipStreamDestroy(c->stream);
+    delete c;
+}
+
+}  // namespace
 
 struct qtts_q4 {
     qtts_ctx *ctx = nullptr;
@@ -60,8 +91,13 @@ struct qtts_q4 {
     size_t bytes = 0;
 };
 
+// Serial numbers identify caches and predictors in the engine's program
+// caches: a freed object's host address can be reused by the next one.
+static std::atomic<uint64_t> g_serial{0};
+
 struct qtts_kv {
     qtts_ctx *ctx = nullptr;
+    uint64_t serial = ++g_serial;
     int layers = 0, kvh = 0, hd = 0, cap = 0, len = 0;
     float *k = nullptr, *v = nullptr;  // [layer][kvh][cap][hd]
     float *layer_k(int l) const { return k + (size_t)l * kvh * cap * hd; }
@@ -447,7 +483,7 @@ struct qtts_talker {
     float *pad = nullptr;
     // engine programs (built lazily, cached per cache object)
     std::unique_ptr<EngProgram> step_prog, frame_prog;
-    const qtts_kv *step_kv = nullptr;
+    uint64_t step_kv = 0;  // serial of the cache step_prog was built for
     std::string frame_key;
     ~qtts_talker() {
         for (void *p : prefill_bufs) (void)hipFree(p);
@@ -458,6 +494,7 @@ struct qtts_talker {
 
 struct qtts_predictor {
     qtts_ctx *ctx = nullptr;
+    uint64_t serial = ++g_serial;
     Owner own;
     Stack st;
     int talker_hidden = 0, groups = 0, vocab = 0, embed_dim = 0;
@@ -471,7 +508,7 @@ struct qtts_predictor {
     uint32_t *codes = nullptr;  // [16]
     int *status = nullptr;
     std::unique_ptr<EngProgram> prog;
-    const qtts_kv *prog_kv = nullptr;
+    uint64_t prog_kv = 0;  // serial of the cache prog was built for
 };
 
 // ===========================================================================
@@ -521,12 +558,9 @@ TvRef add_gemv(EngProgram &P, const DevQ4 &w, const GemvSpec &sp) {
     const int NP = sp.epi == EEPI_SWIGLU ? 2 : 1;
     const int ngroups = w.N / (32 * NP);
     const int Nout = sp.epi == EEPI_SWIGLU ? w.N / 2 : w.N;
-    int kc = sp.kc;
-    if (kc <= 0) {
-        kc = 256 / ngroups;
-        if (kc < 1) kc = 1;
-        if (kc > 4) kc = 4;
-    }
+    // One K chunk per group where the rows fit one task: a split-K owner
+    // waits a cross-block round trip for its partials.
+    int kc = sp.kc > 0 ? sp.kc : 1;
     const int kmin = (w.K + kEngThreads * kEngRptMax - 1) / (kEngThreads * kEngRptMax);
     if (kc < kmin) kc = kmin;
     int kchunk = (w.K + kc - 1) / kc;
@@ -898,18 +932,7 @@ qtts_status qtts_ctx_create(int32_t device, qtts_ctx **out) {
 void qtts_ctx_destroy(qtts_ctx *c) {
     if (!c) return;
     if (c->stream) (void)hipStreamSynchronize(c->stream);
-    (void)hipFree(c->partial);
-    (void)hipFree(c->counters);
-    (void)hipFree(c->attn_part);
-    (void)hipFree(c->attn_counters);
-    (void)hipFree(c->d_in);
-    (void)hipFree(c->d_out);
-    (void)hipFree(c->d_small);
-    (void)hipFree(c->eng_state);
-    (void)hipFree(c->eng_done);
-    (void)hipFree(c->eng_trace);
-    if (c->stream) (void)hipStreamDestroy(c->stream);
-    delete c;
+    ctx_release(c);
 }
 
 const char *qtts_last_error(const qtts_ctx *c) { return c ? c->err.c_str() : "null context"; }
@@ -928,7 +951,7 @@ qtts_status qtts_q4_upload(qtts_ctx *c, const qtts_q4_view *v, qtts_q4 **out) {
     if (!v->packed || !v->scales) return fail(c, QTTS_EINVAL, "null weight arrays");
     if (v->k <= 0 || v->n <= 0 || v->n % 32 != 0) return fail(c, QTTS_ESHAPE, "Q4 weight needs n % 32 == 0");
     qtts_q4 *w = new qtts_q4();
-    w->ctx = c;
+    w->ctx = ctx_retain(c);
     w->bytes = (size_t)v->k * v->n / 2 + (size_t)v->k * (v->n / 32) * 2;
     if (hipMalloc(&w->mem, w->bytes) != hipSuccess) {
         delete w;
@@ -949,8 +972,11 @@ qtts_status qtts_q4_upload(qtts_ctx *c, const qtts_q4_view *v, qtts_q4 **out) {
 
 void qtts_q4_free(qtts_q4 *w) {
     if (!w) return;
+    qtts_ctx *c = w->ctx;
+    if (c && c->stream) (void)hipStreamSynchronize(c->stream);
     (void)hipFree(w->mem);
     delete w;
+    if (c) ctx_release(c);
 }
 
 size_t qtts_q4_bytes(const qtts_q4 *w) { return w ? w->bytes : 0; }
@@ -1011,7 +1037,7 @@ qtts_status qtts_kv_create(qtts_ctx *c, int32_t num_layers, int32_t num_kv_heads
     if (num_layers <= 0 || num_kv_heads <= 0 || head_dim <= 0 || capacity <= 0)
         return fail(c, QTTS_EINVAL, "kv dimensions must be positive");
     qtts_kv *kv = new qtts_kv();
-    kv->ctx = c;
+    kv->ctx = ctx_retain(c);
     kv->layers = num_layers;
     kv->kvh = num_kv_heads;
     kv->hd = head_dim;
@@ -1031,9 +1057,12 @@ qtts_status qtts_kv_create(qtts_ctx *c, int32_t num_layers, int32_t num_kv_heads
 
 void qtts_kv_free(qtts_kv *kv) {
     if (!kv) return;
+    qtts_ctx *c = kv->ctx;
+    if (c && c->stream) (void)hipStreamSynchronize(c->stream);
     (void)hipFree(kv->k);
     (void)hipFree(kv->v);
     delete kv;
+    if (c) ctx_release(c);
 }
 
 int32_t qtts_kv_len(const qtts_kv *kv) { return kv ? kv->len : -1; }
@@ -1092,7 +1121,7 @@ qtts_status qtts_talker_upload(qtts_ctx *c, const qtts_talker_view *v, qtts_talk
     if (!c || !v || !out) return QTTS_EINVAL;
     *out = nullptr;
     qtts_talker *t = new qtts_talker();
-    t->ctx = c;
+    t->ctx = ctx_retain(c);
     auto bail = [&](qtts_status s) {
         delete t;
         return s;
@@ -1131,8 +1160,10 @@ qtts_status qtts_talker_upload(qtts_ctx *c, const qtts_talker_view *v, qtts_talk
 
 void qtts_talker_free(qtts_talker *t) {
     if (!t) return;
-    (void)hipStreamSynchronize(t->ctx->stream);
+    qtts_ctx *c = t->ctx;
+    if (c) (void)hipStreamSynchronize(c->stream);
     delete t;
+    if (c) ctx_release(c);
 }
 
 namespace {
@@ -1185,14 +1216,14 @@ qtts_status qtts_forward_with_embedding(qtts_talker *t, const float *embedding, 
     const int hidden = t->st.hidden;
     if (engine_enabled() && eng_talker_fits(kv->cap)) {
         QTTS_TRY(eng_init(c));
-        if (!t->step_prog || t->step_kv != kv) {
+        if (!t->step_prog || t->step_kv != kv->serial) {
             t->step_prog.reset(new EngProgram());
             const int nsplit = eng_talker_nsplit(kv->cap);
             QTTS_TRY(eng_build(c, *t->step_prog, [&](EngProgram &P) {
                 TvRef x = add_embsum(P, 2, nullptr, nullptr, nullptr, 0, TvRef{}, nullptr, 0, t->x, hidden);
                 return build_talker_layers_and_head(P, t, kv, x, nsplit);
             }));
-            t->step_kv = kv;
+            t->step_kv = kv->serial;
         }
         HIP_TRY(c, hipMemcpyAsync(t->x, embedding, sizeof(float) * hidden, hipMemcpyHostToDevice, c->stream));
         QTTS_TRY(eng_reset(c, position, kv->len, 0));
@@ -1311,7 +1342,7 @@ qtts_status qtts_predictor_upload(qtts_ctx *c, const qtts_predictor_view *v, qtt
     if (v->num_groups <= 0 || v->num_groups > kMaxGroups) return fail(c, QTTS_ESHAPE, "num_groups must be 1..15");
     if (!v->codec_embeddings || !v->lm_heads) return fail(c, QTTS_EINVAL, "null embeddings or heads");
     qtts_predictor *p = new qtts_predictor();
-    p->ctx = c;
+    p->ctx = ctx_retain(c);
     auto bail = [&](qtts_status s) {
         delete p;
         return s;
@@ -1370,8 +1401,10 @@ qtts_status qtts_predictor_upload(qtts_ctx *c, const qtts_predictor_view *v, qtt
 
 void qtts_predictor_free(qtts_predictor *p) {
     if (!p) return;
-    (void)hipStreamSynchronize(p->ctx->stream);
+    qtts_ctx *c = p->ctx;
+    if (c) (void)hipStreamSynchronize(c->stream);
     delete p;
+    if (c) ctx_release(c);
 }
 
 namespace {
@@ -1455,13 +1488,13 @@ qtts_status qtts_generate_acoustic_codes(qtts_predictor *p, const float *talker_
     HIP_TRY(c, hipMemcpyAsync(p->in2 + th, semantic_embed, sizeof(float) * th, hipMemcpyHostToDevice, c->stream));
     if (engine_enabled() && !p->identity_proj) {
         QTTS_TRY(eng_init(c));
-        if (!p->prog || p->prog_kv != kv) {
+        if (!p->prog || p->prog_kv != kv->serial) {
             p->prog.reset(new EngProgram());
             QTTS_TRY(eng_build(c, *p->prog, [&](EngProgram &P) {
                 TvRef codes[kMaxGroups];
                 return build_predictor_passes(P, p, kv, in_plain(p->in2), in_plain(p->in2 + th), codes);
             }));
-            p->prog_kv = kv;
+            p->prog_kv = kv->serial;
         }
         QTTS_TRY(eng_reset(c, 0, 0, 0));
         QTTS_TRY(eng_launch(c, *p->prog, 0, p->codes, 1));
@@ -1673,8 +1706,9 @@ qtts_status qtts_generate_codes(qtts_talker *t, qtts_predictor *p, qtts_kv *talk
         t->vocab <= 4096) {
         QTTS_TRY(eng_init(c));
         char key[256];
-        std::snprintf(key, sizeof(key), "%p %p %p %d %d %g %d %g %d %u %d %d %p %p", (void *)talker_kv,
-                      (void *)predictor_kv, (void *)(talker_only ? nullptr : p), max_codes, trailing_len,
+        std::snprintf(key, sizeof(key), "%llu %llu %llu %d %d %g %d %g %d %u %d %d %p %p",
+                      (unsigned long long)talker_kv->serial, (unsigned long long)(predictor_kv ? predictor_kv->serial : 0),
+                      (unsigned long long)(talker_only ? 0 : p->serial), max_codes, trailing_len,
                       params->sampler.temperature, params->sampler.top_k, params->sampler.repetition_penalty,
                       params->sampler.greedy, params->codec_eos_id, params->stop_on_eos, (int)talker_only,
                       (void *)t->trailing, (void *)t->codes);

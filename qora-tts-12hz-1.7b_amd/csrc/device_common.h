@@ -21,18 +21,53 @@ __device__ __forceinline__ __attribute__((address_space(1))) T *glb(T *p) {
 
 typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
+// Read-only (constant address space) view, for op descriptors: loads through
+// it are scalar loads (lgkmcnt), which do not wait behind outstanding vector
+// loads the way a vector load of a descriptor field would (vmcnt retires in
+// order).
+#define KCONST __attribute__((address_space(4)))
+
 __device__ __forceinline__ float f16_to_f32(uint16_t h) { return (float)__builtin_bit_cast(_Float16, h); }
 
-__device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+// Lane exchange within rows of 16 lanes through DPP (a VALU operand
+// modifier: no LDS round trip, unlike __shfl_xor's ds_bpermute).
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141;  // lane i <- 7-i within each 8
+constexpr int kDppMirror = 0x140;      // lane i <- 15-i within each 16
+
+// Sum over each row of 16 lanes; every lane of the row gets it.
+__device__ __forceinline__ float row16_sum(float v) {
+    v += dpp<kDppXor1>(v);
+    v += dpp<kDppXor2>(v);
+    v += dpp<kDppHalfMirror>(v);
+    v += dpp<kDppMirror>(v);
     return v;
+}
+__device__ __forceinline__ float row16_max(float v) {
+    v = fmaxf(v, dpp<kDppXor1>(v));
+    v = fmaxf(v, dpp<kDppXor2>(v));
+    v = fmaxf(v, dpp<kDppHalfMirror>(v));
+    v = fmaxf(v, dpp<kDppMirror>(v));
+    return v;
+}
+__device__ __forceinline__ float lane_f(float v, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+// Sum / max over the 64-lane wave; every lane gets the result.
+__device__ __forceinline__ float wave_sum(float v) {
+    v = row16_sum(v);
+    return (lane_f(v, 0) + lane_f(v, 16)) + (lane_f(v, 32) + lane_f(v, 48));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
-    return v;
+    v = row16_max(v);
+    return fmaxf(fmaxf(lane_f(v, 0), lane_f(v, 16)), fmaxf(lane_f(v, 32), lane_f(v, 48)));
 }
 
 // Cross-workgroup traffic inside one kernel goes through agent-scope atomic
@@ -87,7 +122,8 @@ __device__ __forceinline__ float simple_rand_dev(uint64_t *state) {
 
 // Element (row, col) of a panel-major Q4 weight: f32(scale) * (nib - 8),
 // the product embed_lookup_q4 forms (src/gemv.rs:388-396); exact.
-__device__ __forceinline__ float q4_element(const DevQ4 &w, uint32_t row, int col) {
+template <typename Q4>
+__device__ __forceinline__ float q4_element(const Q4 &w, uint32_t row, int col) {
     const size_t r = (size_t)(col >> 5) * w.K + row;
     const uint8_t byte = glb(reinterpret_cast<const uint8_t *>(w.wq))[r * 16 + ((col & 31) >> 1)];
     const int nib = (col & 1) ? (byte >> 4) : (byte & 15);

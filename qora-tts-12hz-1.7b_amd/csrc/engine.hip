@@ -130,7 +130,7 @@ __device__ __forceinline__ float block_sum(float v, float *scr) {
 // Same arithmetic as k_gemv: acc += (scale * x) * (nib - 8), f32.
 // ---------------------------------------------------------------------------
 template <int M, int NP>
-__device__ __forceinline__ int eng_gemv(const EngGemv &g, int task, uint32_t tb, Ctl &c, float *smem) {
+__device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint32_t tb, Ctl &c, float *smem) {
     float *red = smem;                     // [256][33]
     float *part8 = red + kEngThreads * 33;  // [8][32]
     float *ybuf = part8 + 8 * 32;           // [NP][M][32]
@@ -153,33 +153,32 @@ __device__ __forceinline__ int eng_gemv(const EngGemv &g, int task, uint32_t tb,
     panel[0] = group;
     if (NP == 2) panel[NP - 1] = group + ngroups;
 
-    // 1. this chunk's weight rows: issued before any input wait.
-    uint4 wv[NP][kEngRptMax];
+    // 1. this chunk's weight rows, issued back to back before any input
+    //    wait: row iterations are wave-uniform (nit), a thread past the
+    //    chunk's last row re-reads that row (its input is zero), and the raw
+    //    scale/gamma bits stay opaque until the accumulation, so no load
+    //    result is needed (and waited for) while the others are issued.
+    const int nit = (k1 - k0 + kEngThreads - 1) / kEngThreads;  // <= kEngRptMax
+    u32x4 wv[NP][kEngRptMax];
     uint32_t sv[NP][kEngRptMax];
+    uint32_t gam[kEngRptMax];
 #pragma unroll
     for (int i = 0; i < kEngRptMax; i++) {
-        const int k = k0 + tid + i * kEngThreads;
+        const int k = min(k0 + tid + i * kEngThreads, k1 - 1);
 #pragma unroll
         for (int pp = 0; pp < NP; pp++) {
-            if (k < k1) {
-                const u32x4 t = glb(reinterpret_cast<const u32x4 *>(g.w.wq))[(size_t)panel[pp] * K + k];
-                wv[pp][i] = make_uint4(t.x, t.y, t.z, t.w);
-                sv[pp][i] = glb(g.w.ws)[(size_t)panel[pp] * K + k];
-            } else {
-                wv[pp][i] = make_uint4(0u, 0u, 0u, 0u);
-                sv[pp][i] = 0u;
+            wv[pp][i] = (u32x4){0u, 0u, 0u, 0u};
+            sv[pp][i] = 0u;
+            if (i < nit) {
+                wv[pp][i] = __builtin_nontemporal_load(glb(reinterpret_cast<const u32x4 *>(g.w.wq)) + (size_t)panel[pp] * K + k);
+                sv[pp][i] = __builtin_nontemporal_load(glb(g.w.ws) + (size_t)panel[pp] * K + k);
             }
         }
+        gam[i] = 0u;
+        if (g.norm && i < nit) gam[i] = glb(g.gamma)[k];
     }
-
-    // RMSNorm gamma of the same rows, and the owner's epilogue operands
-    // (bias; the residual, tag-checked when used): loaded before any wait.
-    uint16_t gam[kEngRptMax];
-#pragma unroll
-    for (int i = 0; i < kEngRptMax; i++) {
-        const int k = k0 + tid + i * kEngThreads;
-        gam[i] = (g.norm && k < k1) ? glb(g.gamma)[k] : (uint16_t)0;
-    }
+    // The owner's epilogue operands (bias; the residual, tag-checked when
+    // used), also loaded before any wait.
     const bool epi_lane = ch == 0 && NP == 1 && tid < M * 32;
     float e_bias = 0.0f;
     uint64_t e_res = 0;
@@ -195,9 +194,11 @@ __device__ __forceinline__ int eng_gemv(const EngGemv &g, int task, uint32_t tb,
     float xv[kEngRptMax][M];
 #pragma unroll
     for (int m = 0; m < M; m++) {
-        const EngInput &in = g.in[m];
+        const KCONST EngInput &in = g.in[m];
         if (in.kind == EIN_TV && g.norm) {
             // rms_norm_f16 (src/gemv.rs:406-417) over the full row.
+#pragma unroll
+            for (int i = 0; i < kEngRptMax; i++) asm volatile("" : "+v"(gam[i]));
             float keep[kEngRptMax];
 #pragma unroll
             for (int i = 0; i < kEngRptMax; i++) keep[i] = 0.0f;
@@ -219,7 +220,7 @@ __device__ __forceinline__ int eng_gemv(const EngGemv &g, int task, uint32_t tb,
 #pragma unroll
             for (int i = 0; i < kEngRptMax; i++) {
                 const int k = k0 + tid + i * kEngThreads;
-                xv[i][m] = k < k1 ? keep[i] * inv * f16_to_f32(gam[i]) : 0.0f;
+                xv[i][m] = k < k1 ? keep[i] * inv * f16_to_f32((uint16_t)gam[i]) : 0.0f;
                 if (g.norm_plain && m == M - 1 && group == 0 && ch == 0 && k < k1) st_dev(&g.norm_plain[k], xv[i][m]);
             }
         } else if (in.kind == EIN_TV) {
@@ -254,16 +255,21 @@ __device__ __forceinline__ int eng_gemv(const EngGemv &g, int task, uint32_t tb,
         for (int m = 0; m < M; m++)
 #pragma unroll
             for (int j = 0; j < 32; j++) acc[pp][m][j] = 0.0f;
+    // weights and scales are consumed only from here on
+#pragma unroll
+    for (int i = 0; i < kEngRptMax; i++)
+#pragma unroll
+        for (int pp = 0; pp < NP; pp++) asm volatile("" : "+v"(sv[pp][i]), "+v"(wv[pp][i]));
 #pragma unroll
     for (int i = 0; i < kEngRptMax; i++) {
-        if (k0 + tid + i * kEngThreads >= k1) continue;
+        if (i >= nit) continue;  // uniform; rows past k1 carry a zero input
 #pragma unroll
         for (int pp = 0; pp < NP; pp++) {
             const float s = f16_to_f32((uint16_t)sv[pp][i]);
             float sx[M];
 #pragma unroll
             for (int m = 0; m < M; m++) sx[m] = s * xv[i][m];
-            const uint32_t wd[4] = {wv[pp][i].x, wv[pp][i].y, wv[pp][i].z, wv[pp][i].w};
+            const uint32_t wd[4] = {wv[pp][i].x, wv[pp][i].y, wv[pp][i].z, wv[pp][i].w};  // 32 nibbles
 #pragma unroll
             for (int d = 0; d < 4; d++) {
 #pragma unroll
@@ -358,27 +364,105 @@ __device__ __forceinline__ int eng_gemv(const EngGemv &g, int task, uint32_t tb,
 // raw q/k, K/V append (src/talker.rs:299-302), then softmax(q.K^T*scale).V
 // over the split (src/talker.rs:304-331), causal across the M new rows.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ int eng_attn(const EngAttn &a, int task, uint32_t tb, const EngState &st, Ctl &c, float *smem) {
+template <int NPI>
+__device__ __forceinline__ int eng_attn_t(const KCONST EngAttn &a, int task, uint32_t tb, const EngState &st, Ctl &c,
+                                          float *smem) {
     constexpr int HD = 128, HALF = 64, CH = 256;
+    constexpr int KJ = 8;    // positions per thread held in registers for the scores (16 lanes each)
+    constexpr int VJ = 64;   // positions per thread held in registers for P.V (two parities)
+    constexpr int PB = 128;  // positions per register batch (= 16 * KJ = 2 * VJ); splits are <= 128 long
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int G = a.nq / a.nkv;
     const int M = a.M;
+    const int npi = M * G;  // (row, head) pairs, <= NPI
     const int kvh = task / a.nsplit, sp = task - kvh * a.nsplit;
     const int base = a.from_state ? st.kvlen : a.len_const;
     const int pos0 = a.from_state ? st.pos : a.pos_const;
     const int Lt = base + M;
     const int chunk = (Lt + a.nsplit - 1) / a.nsplit;
     const int t0 = sp * chunk, t1 = min(Lt, t0 + chunk);
-    const int nt = max(0, t1 - t0);
-    float *qs = smem;                 // [M][G][HD]
+    const int nt = max(0, t1 - t0);      // <= CH
+    float *qs = smem;                    // [M][G][HD]
     float *kn = qs + kEngMaxM * 4 * HD;  // [M][HD]
     float *vn = kn + kEngMaxM * HD;      // [M][HD]
-    float *sc = vn + kEngMaxM * HD;      // [M*G][CH]
-    float *pv = sc + kEngMaxM * 4 * CH;  // [M*G][HD]
-    float *ml = pv + kEngMaxM * 4 * HD;  // [M*G][2]
+    float *sc = vn + kEngMaxM * HD;      // [NPI][CH] scores
+    float *pt = sc + kEngMaxM * 4 * CH;  // [CH][NPI] probabilities (position-major)
+    float *pv = pt + kEngMaxM * 4 * CH;  // [NPI][HD]
+    float *ml = pv + kEngMaxM * 4 * HD;  // [NPI][2]
+    float *Kb = a.kcache + (size_t)kvh * a.kv_cap * HD;
+    float *Vb = a.vcache + (size_t)kvh * a.kv_cap * HD;
+    const int l16 = tid & 15, slot = tid >> 4;    // scores: 16 lanes per position, 8 dims per lane
+    const int d = tid & (HD - 1), hf = tid >> 7;  // P.V: one dim, every other position
+
+    // Cached rows [0, base) for the register batch starting at position b0,
+    // read device-coherently (the rows may have been written on another
+    // XCD).  from_state: the rows were written by earlier launches, so the
+    // loads may be issued before this step's inputs arrive; otherwise (rows
+    // appended earlier in this launch) they are issued after the inputs.
+    // Positions past the split read as zero.
+    uint64_t kr[KJ][4];
+    float vr[VJ];
+    auto load_k = [&](int b0) {
+#pragma unroll
+        for (int j = 0; j < KJ; j++) {
+            const int tt = b0 + slot + 16 * j, t = t0 + tt;
+#pragma unroll
+            for (int e = 0; e < 4; e++) kr[j][e] = 0;
+            if (tt < nt && t < base) {
+                const uint64_t *src = reinterpret_cast<const uint64_t *>(Kb + (size_t)t * HD + l16 * 8);
+#pragma unroll
+                for (int e = 0; e < 4; e++) kr[j][e] = ld_dev_u64(src + e);
+            }
+        }
+    };
+    auto load_v = [&](int b0) {
+#pragma unroll
+        for (int u = 0; u < VJ; u++) {
+            const int tt = b0 + hf + 2 * u, t = t0 + tt;
+            vr[u] = (tt < nt && t < base) ? ld_dev(&Vb[(size_t)t * HD + d]) : 0.0f;
+        }
+    };
+    // the M new rows of the batch come from LDS
+    auto patch_k = [&](int b0) {
+#pragma unroll
+        for (int j = 0; j < KJ; j++) {
+            const int tt = b0 + slot + 16 * j, t = t0 + tt;
+            if (tt < nt && t >= base) {
+                const float *src = &kn[(t - base) * HD + l16 * 8];
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    kr[j][e] = (uint64_t)__float_as_uint(src[2 * e]) | ((uint64_t)__float_as_uint(src[2 * e + 1]) << 32);
+            }
+        }
+    };
+    auto patch_v = [&](int b0) {
+#pragma unroll
+        for (int u = 0; u < VJ; u++) {
+            const int tt = b0 + hf + 2 * u, t = t0 + tt;  // wave-uniform
+            if (tt < nt && t >= base) vr[u] = vn[(t - base) * HD + d];
+        }
+    };
+
+    // 0. inputs that do not depend on this step: norm gammas, RoPE rows, and
+    //    (from_state) the first batch of cached K/V.
+    const float gq1 = f16_to_f32(glb(a.q_norm)[lane]), gq2 = f16_to_f32(glb(a.q_norm)[lane + HALF]);
+    const float gk1 = f16_to_f32(glb(a.k_norm)[lane]), gk2 = f16_to_f32(glb(a.k_norm)[lane + HALF]);
+    float rcs[kEngMaxM], rsn[kEngMaxM];
+    bool rok[kEngMaxM];
+#pragma unroll
+    for (int m = 0; m < kEngMaxM; m++) {
+        const int pos = pos0 + m;
+        rok[m] = m < M && !(a.rope_skip_oob && pos >= a.rope_rows);
+        rcs[m] = rok[m] ? glb(a.rope_cos)[(size_t)pos * HALF + lane] : 1.0f;
+        rsn[m] = rok[m] ? glb(a.rope_sin)[(size_t)pos * HALF + lane] : 0.0f;
+    }
+    if (a.from_state) {
+        load_k(0);
+        load_v(0);
+    }
+    stamp(c, 2);
 
     // 1. raw q (G heads), k, v of this kv head for the M rows
-    stamp(c, 2);
     const int per = (G + 2) * HD;
     {
         constexpr int NB = kEngMaxM * 6 * HD / kEngThreads;  // M <= 2, G <= 4
@@ -392,126 +476,115 @@ __device__ __forceinline__ int eng_attn(const EngAttn &a, int task, uint32_t tb,
             tg[i] = tb + a.qkv_tag;
             ptr[i] = a.qkv;
             if (idx < M * per) {
-                const int m = idx / per, r = idx - m * per, prt = r / HD, d = r - prt * HD;
+                const int m = idx / per, r = idx - m * per, prt = r / HD, dd = r - prt * HD;
                 int src;
                 if (prt < G)
-                    src = (kvh * G + prt) * HD + d;
+                    src = (kvh * G + prt) * HD + dd;
                 else if (prt == G)
-                    src = a.nq * HD + kvh * HD + d;
+                    src = a.nq * HD + kvh * HD + dd;
                 else
-                    src = (a.nq + a.nkv) * HD + kvh * HD + d;
+                    src = (a.nq + a.nkv) * HD + kvh * HD + dd;
                 ptr[i] = &a.qkv[(size_t)m * a.ld_qkv + src];
                 cnt = i + 1;
             }
         }
         wait_list<NB>(ptr, tg, cnt, val, c);
+        if (!a.from_state) {
+            load_k(0);
+            load_v(0);
+        }
 #pragma unroll
         for (int i = 0; i < NB; i++) {
             const int idx = tid + i * kEngThreads;
             if (idx >= M * per) continue;
-            const int m = idx / per, r = idx - m * per, prt = r / HD, d = r - prt * HD;
+            const int m = idx / per, r = idx - m * per, prt = r / HD, dd = r - prt * HD;
             if (prt < G)
-                qs[(m * G + prt) * HD + d] = val[i];
+                qs[(m * G + prt) * HD + dd] = val[i];
             else if (prt == G)
-                kn[m * HD + d] = val[i];
+                kn[m * HD + dd] = val[i];
             else
-                vn[m * HD + d] = val[i];
+                vn[m * HD + dd] = val[i];
         }
     }
     __syncthreads();
     stamp(c, 3);
-    // 2. QK-norm + RoPE, one wave per 128-vector
+    // 2. QK-norm (src/talker.rs:86-99) + split-half RoPE (src/rope.rs:79-92), one wave per vector
     for (int vi = wave; vi < M * (G + 1); vi += kEngThreads / 64) {
         const int m = vi / (G + 1), r = vi - m * (G + 1);
         float *vec = r < G ? &qs[(m * G + r) * HD] : &kn[m * HD];
-        const uint16_t *gam = r < G ? a.q_norm : a.k_norm;
         const float x1 = vec[lane], x2 = vec[lane + HALF];
         const float ss = wave_sum(x1 * x1 + x2 * x2);
         const float inv = 1.0f / sqrtf(ss / (float)HD + 1e-6f);
-        const float n1 = x1 * inv * f16_to_f32(glb(gam)[lane]);
-        const float n2 = x2 * inv * f16_to_f32(glb(gam)[lane + HALF]);
-        const int pos = pos0 + m;
-        float o1 = n1, o2 = n2;
-        if (!(a.rope_skip_oob && pos >= a.rope_rows)) {
-            const float cs = glb(a.rope_cos)[(size_t)pos * HALF + lane], sn = glb(a.rope_sin)[(size_t)pos * HALF + lane];
-            o1 = n1 * cs - n2 * sn;
-            o2 = n2 * cs + n1 * sn;
-        }
-        vec[lane] = o1;
-        vec[lane + HALF] = o2;
+        const float n1 = x1 * inv * (r < G ? gq1 : gk1);
+        const float n2 = x2 * inv * (r < G ? gq2 : gk2);
+        const float cs = m == 0 ? rcs[0] : rcs[kEngMaxM - 1], sn = m == 0 ? rsn[0] : rsn[kEngMaxM - 1];
+        const bool rp = m == 0 ? rok[0] : rok[kEngMaxM - 1];
+        vec[lane] = rp ? n1 * cs - n2 * sn : n1;
+        vec[lane + HALF] = rp ? n2 * cs + n1 * sn : n2;
     }
     __syncthreads();
     stamp(c, 4);
-    // 3. append the new rows that fall in this split
-    float *Kb = a.kcache + (size_t)kvh * a.kv_cap * HD;
-    float *Vb = a.vcache + (size_t)kvh * a.kv_cap * HD;
+    // 3. append the new rows that fall in this split (src/talker.rs:299-302)
     for (int idx = tid; idx < M * HD; idx += kEngThreads) {
-        const int m = idx / HD, d = idx - m * HD, t = base + m;
+        const int m = idx / HD, dd = idx - m * HD, t = base + m;
         if (t >= t0 && t < t1) {
-            st_dev(&Kb[(size_t)t * HD + d], kn[m * HD + d]);
-            st_dev(&Vb[(size_t)t * HD + d], vn[m * HD + d]);
+            st_dev(&Kb[(size_t)t * HD + dd], kn[m * HD + dd]);
+            st_dev(&Vb[(size_t)t * HD + dd], vn[m * HD + dd]);
         }
     }
+    // q of this lane's 8 dims, per (row, head)
+    float q8[NPI][8];
+#pragma unroll
+    for (int pi = 0; pi < NPI; pi++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) q8[pi][e] = pi < npi ? qs[pi * HD + l16 * 8 + e] : 0.0f;
     stamp(c, 5);
-    // 4. scores: 16 lanes per position, 8 dims per lane
-    {
-        const int l16 = tid & 15, slot = tid >> 4;
-        constexpr int UNR = 4;
-        for (int tb0 = slot; tb0 < nt; tb0 += UNR * (kEngThreads / 16)) {
-            uint64_t raw[UNR][4];
+    // 4. scores q.K^T * scale, causal across the M new rows (src/talker.rs:304-318)
+    for (int b0 = 0; b0 < nt; b0 += PB) {
+        if (b0 > 0) load_k(b0);
+        patch_k(b0);
 #pragma unroll
-            for (int u = 0; u < UNR; u++) {
-                const int t = t0 + tb0 + u * (kEngThreads / 16);
-                if (tb0 + u * (kEngThreads / 16) < nt && t < base) {
-                    const uint64_t *src = reinterpret_cast<const uint64_t *>(&Kb[(size_t)t * HD + l16 * 8]);
+        for (int j = 0; j < KJ; j++) {
+            const int tt = b0 + slot + 16 * j, t = t0 + tt;
+            float k8[8];
 #pragma unroll
-                    for (int e = 0; e < 4; e++) raw[u][e] = ld_dev_u64(src + e);
-                }
+            for (int e = 0; e < 4; e++) {
+                k8[2 * e] = __uint_as_float((uint32_t)kr[j][e]);
+                k8[2 * e + 1] = __uint_as_float((uint32_t)(kr[j][e] >> 32));
             }
 #pragma unroll
-            for (int u = 0; u < UNR; u++) {
-            const int tt = tb0 + u * (kEngThreads / 16);
-            if (tt >= nt) continue;
-            const int t = t0 + tt;
-            float kr[8];
-            if (t < base) {
+            for (int pi = 0; pi < NPI; pi++) {
+                float dot = 0.0f;
 #pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    kr[2 * e] = __uint_as_float((uint32_t)raw[u][e]);
-                    kr[2 * e + 1] = __uint_as_float((uint32_t)(raw[u][e] >> 32));
-                }
-            } else {
-#pragma unroll
-                for (int e = 0; e < 8; e++) kr[e] = kn[(t - base) * HD + l16 * 8 + e];
-            }
-            for (int m = 0; m < M; m++) {
-                for (int g = 0; g < G; g++) {
-                    const float *qq = &qs[(m * G + g) * HD + l16 * 8];
-                    float dot = 0.0f;
-#pragma unroll
-                    for (int e = 0; e < 8; e++) dot += qq[e] * kr[e];
-                    dot += __shfl_xor(dot, 8, 16);
-                    dot += __shfl_xor(dot, 4, 16);
-                    dot += __shfl_xor(dot, 2, 16);
-                    dot += __shfl_xor(dot, 1, 16);
-                    if (l16 == 0) sc[(m * G + g) * CH + tt] = (t <= base + m) ? dot * a.scale : -INFINITY;
-                }
-            }
+                for (int e = 0; e < 8; e++) dot += q8[pi][e] * k8[e];
+                dot = row16_sum(dot);
+                const int m = pi / G;
+                if (l16 == 0 && pi < npi && tt < min(nt, b0 + PB))
+                    sc[pi * CH + tt] = (t <= base + m) ? dot * a.scale : -INFINITY;
             }
         }
     }
     __syncthreads();
     stamp(c, 6);
-    // 5. local softmax statistics, one wave per (row, head)
-    for (int pi = wave; pi < M * G; pi += kEngThreads / 64) {
+    // 5. local softmax statistics, one wave per (row, head) (src/talker.rs:319-326);
+    //    the probabilities go to pt position-major, zero past the split.
+    const int ntp = (nt + PB - 1) / PB * PB;
+    for (int pi = wave; pi < NPI; pi += kEngThreads / 64) {
+        if (pi >= npi) {
+            for (int t = lane; t < ntp; t += 64) pt[t * NPI + pi] = 0.0f;
+            continue;
+        }
         float mx = -INFINITY;
         for (int t = lane; t < nt; t += 64) mx = fmaxf(mx, sc[pi * CH + t]);
         mx = wave_max(mx);
         float l = 0.0f;
-        for (int t = lane; t < nt; t += 64) {
-            const float s = sc[pi * CH + t];
-            const float e = (mx == -INFINITY) ? 0.0f : expf(s - mx);
-            sc[pi * CH + t] = e;
+        for (int t = lane; t < ntp; t += 64) {
+            float e = 0.0f;
+            if (t < nt) {
+                const float s = sc[pi * CH + t];
+                e = (mx == -INFINITY) ? 0.0f : expf(s - mx);
+            }
+            pt[t * NPI + pi] = e;
             l += e;
         }
         l = wave_sum(l);
@@ -522,43 +595,48 @@ __device__ __forceinline__ int eng_attn(const EngAttn &a, int task, uint32_t tb,
     }
     __syncthreads();
     stamp(c, 7);
-    // 6. P.V: thread (d, half) walks every other position; V read once per (d)
+    // 6. P.V (src/talker.rs:327-331): thread (d, parity) over its positions
     {
-        const int d = tid & (HD - 1), hf = tid >> 7;
-        float acc[kEngMaxM * 4];
+        float acc[NPI];
 #pragma unroll
-        for (int i = 0; i < kEngMaxM * 4; i++) acc[i] = 0.0f;
-        const int npi = M * G;
-        constexpr int VU = 8;
-        for (int tb0 = hf; tb0 < nt; tb0 += 2 * VU) {
-            float vv[VU];
+        for (int pi = 0; pi < NPI; pi++) acc[pi] = 0.0f;
+        for (int b0 = 0; b0 < nt; b0 += PB) {
+            if (b0 > 0 || nt > PB) load_v(b0);  // a single-batch split reuses the early loads
+            patch_v(b0);
 #pragma unroll
-            for (int u = 0; u < VU; u++) {
-                const int tt = tb0 + 2 * u, t = t0 + tt;
-                vv[u] = 0.0f;
-                if (tt < nt) vv[u] = t < base ? ld_dev(&Vb[(size_t)t * HD + d]) : vn[(t - base) * HD + d];
-            }
+            for (int u = 0; u < VJ; u++) {
+                const int tt = b0 + hf + 2 * u;
+                float p[NPI];
+                if (NPI == 2) {
+                    const float2 q = *reinterpret_cast<const float2 *>(&pt[tt * NPI]);
+                    p[0] = q.x;
+                    p[NPI - 1] = q.y;
+                } else {
 #pragma unroll
-            for (int u = 0; u < VU; u++) {
-                const int tt = tb0 + 2 * u;
-                if (tt >= nt) continue;
+                    for (int h4 = 0; h4 < NPI / 4; h4++) {
+                        const float4 q = *reinterpret_cast<const float4 *>(&pt[tt * NPI + 4 * h4]);
+                        p[4 * h4] = q.x;
+                        p[4 * h4 + 1] = q.y;
+                        p[4 * h4 + 2] = q.z;
+                        p[4 * h4 + 3] = q.w;
+                    }
+                }
 #pragma unroll
-                for (int pi = 0; pi < kEngMaxM * 4; pi++)
-                    if (pi < npi) acc[pi] += sc[pi * CH + tt] * vv[u];
+                for (int pi = 0; pi < NPI; pi++) acc[pi] += p[pi] * vr[u];
             }
         }
         if (hf == 1) {
 #pragma unroll
-            for (int pi = 0; pi < kEngMaxM * 4; pi++)
-                if (pi < npi) pv[pi * HD + d] = acc[pi];
+            for (int pi = 0; pi < NPI; pi++) pv[pi * HD + d] = acc[pi];
         }
-        __syncthreads();
-        // K/V appends complete before the outputs that publish this step
-        wait_stores();
+        // Rows appended in this launch are read by later steps of the same
+        // launch: their stores complete before the outputs that order those
+        // steps.  Rows of a from_state step are only read by later launches.
+        if (!a.from_state) wait_stores();
         __syncthreads();
         if (hf == 0) {
 #pragma unroll
-            for (int pi = 0; pi < kEngMaxM * 4; pi++) {
+            for (int pi = 0; pi < NPI; pi++) {
                 if (pi >= npi) continue;
                 const int m = pi / G, g = pi - m * G, h = kvh * G + g;
                 const float o = acc[pi] + pv[pi * HD + d];
@@ -579,8 +657,16 @@ __device__ __forceinline__ int eng_attn(const EngAttn &a, int task, uint32_t tb,
     return task;
 }
 
+__device__ __forceinline__ int eng_attn(const KCONST EngAttn &a, int task, uint32_t tb, const EngState &st, Ctl &c,
+                                        float *smem) {
+    const int npi = a.M * (a.nq / a.nkv);
+    if (npi <= 2) return eng_attn_t<2>(a, task, tb, st, c, smem);
+    if (npi <= 4) return eng_attn_t<4>(a, task, tb, st, c, smem);
+    return eng_attn_t<8>(a, task, tb, st, c, smem);
+}
+
 // Combine the splits of one (row, query head): flash-decode merge.
-__device__ __forceinline__ int eng_combine(const EngCombine &cb, int task, uint32_t tb, Ctl &c) {
+__device__ __forceinline__ int eng_combine(const KCONST EngCombine &cb, int task, uint32_t tb, Ctl &c) {
     constexpr int HD = 128;
     const int m = task / cb.nq, h = task - m * cb.nq;
     const int d = threadIdx.x;
@@ -607,7 +693,7 @@ __device__ __forceinline__ int eng_combine(const EngCombine &cb, int task, uint3
 }
 
 // sample_argmax (src/code_predictor.rs:328-334): last index of the maximum.
-__device__ __forceinline__ void eng_argmax(const EngArgmax &a, uint32_t tb, const EngState &st, Ctl &c, uint32_t *codes,
+__device__ __forceinline__ void eng_argmax(const KCONST EngArgmax &a, uint32_t tb, const EngState &st, Ctl &c, uint32_t *codes,
                            int max_codes, float *smem) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float bv = -INFINITY;
@@ -738,7 +824,7 @@ __device__ int block_exscan(int v, int *wsum, int *total) {
 // sample_token (src/generate_new.rs:329-391), same schedule as k_sample:
 // the three order-dependent f32 sums on one lane in index order, the rest
 // in parallel; the stable top-k by radix select over the float bits.
-__device__ __forceinline__ void eng_sample(const EngSample &P, uint32_t tb, const EngState &st, EngState *st_out, Ctl &c,
+__device__ __forceinline__ void eng_sample(const KCONST EngSample &P, uint32_t tb, const EngState &st, EngState *st_out, Ctl &c,
                            uint32_t *codes, int max_codes, float *smem) {
     const int V = P.vocab, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float *s = smem;
@@ -992,7 +1078,7 @@ __device__ __forceinline__ void eng_sample(const EngSample &P, uint32_t tb, cons
 }
 
 // Next talker input (src/generate_new.rs:270-286), 256 columns per task.
-__device__ __forceinline__ int eng_embsum(const EngEmbSum &E, int task, uint32_t tb, const EngState &st, Ctl &c) {
+__device__ __forceinline__ int eng_embsum(const KCONST EngEmbSum &E, int task, uint32_t tb, const EngState &st, Ctl &c) {
     const int j = task * kEngThreads + threadIdx.x;
     if (E.mode == 2) {  // publish a plain row (host input) as a tagged vector
         if (j < E.hidden) put_tv(&E.out[j], ld_dev(&E.pad[j]), tb + E.out_tag);
@@ -1040,7 +1126,7 @@ __global__ __launch_bounds__(kEngThreads) void k_engine(EngArgs A) {
     st.rng = ld_dev_u64(&A.st_in->rng);
     const int G = gridDim.x;
     for (int oi = 0; oi < A.nops; oi++) {
-        const EngOp &op = A.ops[oi];
+        const KCONST EngOp &op = ((const KCONST EngOp *)A.ops)[oi];
         int t = ((int)blockIdx.x - op.rot) % G;
         if (t < 0) t += G;
         uint64_t *tr = (A.trace && t < op.ntasks) ? A.trace + ((size_t)oi * G + blockIdx.x) * kTraceSlots : nullptr;
@@ -1053,7 +1139,7 @@ __global__ __launch_bounds__(kEngThreads) void k_engine(EngArgs A) {
             int fi = -1;  // flag this task sets, if any
             switch (op.kind) {
                 case EOP_GEMV: {
-                    const EngGemv &g = op.gemv;
+                    const KCONST EngGemv &g = op.gemv;
                     if (g.M == 1) {
                         if (g.epi == EEPI_SWIGLU)
                             fi = eng_gemv<1, 2>(g, t, A.tag_base, c, smem);
