@@ -39,6 +39,20 @@ constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
 constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141;  // lane i <- 7-i within each 8
 constexpr int kDppMirror = 0x140;      // lane i <- 15-i within each 16
+constexpr int kDppRowShl4 = 0x104;     // lane i <- i+4 within each 16
+constexpr int kDppRowShl8 = 0x108;     // lane i <- i+8
+constexpr int kDppRowShr4 = 0x114;     // lane i <- i-4
+constexpr int kDppRowShr8 = 0x118;     // lane i <- i-8
+
+// dpp<A>(v) on lanes where `pick`, dpp<B>(v) elsewhere.  Both are computed
+// by every lane: a DPP read from a lane that is inactive (as it would be if
+// the compiler turned the choice into a branch) returns nothing.
+template <int A, int B>
+__device__ __forceinline__ float dpp_pick(bool pick, float v) {
+    float ra = dpp<A>(v), rb = dpp<B>(v);
+    asm volatile("" : "+v"(ra), "+v"(rb));
+    return pick ? ra : rb;
+}
 
 // Sum over each row of 16 lanes; every lane of the row gets it.
 __device__ __forceinline__ float row16_sum(float v) {

@@ -131,9 +131,8 @@ __device__ __forceinline__ float block_sum(float v, float *scr) {
 // ---------------------------------------------------------------------------
 template <int M, int NP>
 __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint32_t tb, Ctl &c, float *smem) {
-    float *red = smem;                     // [256][33]
-    float *part8 = red + kEngThreads * 33;  // [8][32]
-    float *ybuf = part8 + 8 * 32;           // [NP][M][32]
+    float *red = smem;                         // [NP][M][16 rows][32]
+    float *ybuf = red + NP * M * 16 * 32;      // [NP][M][32]
     float *scr = ybuf + NP * M * 32;        // [8]
     const int tid = threadIdx.x;
     const int N = g.w.N, K = g.w.K;
@@ -260,6 +259,14 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
     for (int i = 0; i < kEngRptMax; i++)
 #pragma unroll
         for (int pp = 0; pp < NP; pp++) asm volatile("" : "+v"(sv[pp][i]), "+v"(wv[pp][i]));
+    // Each term is (scale * x) * nib - 8 * (scale * x): the nibbles are
+    // split into bytes and converted with one v_cvt_f32_ubyteN each, and the
+    // offset is applied once per column from the running sum of scale * x.
+    float sxsum[NP][M];
+#pragma unroll
+    for (int pp = 0; pp < NP; pp++)
+#pragma unroll
+        for (int m = 0; m < M; m++) sxsum[pp][m] = 0.0f;
 #pragma unroll
     for (int i = 0; i < kEngRptMax; i++) {
         if (i >= nit) continue;  // uniform; rows past k1 carry a zero input
@@ -268,46 +275,85 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
             const float s = f16_to_f32((uint16_t)sv[pp][i]);
             float sx[M];
 #pragma unroll
-            for (int m = 0; m < M; m++) sx[m] = s * xv[i][m];
+            for (int m = 0; m < M; m++) {
+                sx[m] = s * xv[i][m];
+                sxsum[pp][m] += sx[m];
+            }
             const uint32_t wd[4] = {wv[pp][i].x, wv[pp][i].y, wv[pp][i].z, wv[pp][i].w};  // 32 nibbles
 #pragma unroll
             for (int d = 0; d < 4; d++) {
+                const uint32_t lo = wd[d] & 0x0F0F0F0Fu;          // nibbles 0, 2, 4, 6
+                const uint32_t hi = (wd[d] >> 4) & 0x0F0F0F0Fu;   // nibbles 1, 3, 5, 7
 #pragma unroll
-                for (int b = 0; b < 8; b++) {
-                    const float q = (float)((int)((wd[d] >> (4 * b)) & 15u) - 8);
+                for (int b = 0; b < 4; b++) {
+                    const float q0 = (float)((lo >> (8 * b)) & 0xFFu), q1 = (float)((hi >> (8 * b)) & 0xFFu);
 #pragma unroll
-                    for (int m = 0; m < M; m++) acc[pp][m][d * 8 + b] = fmaf(sx[m], q, acc[pp][m][d * 8 + b]);
+                    for (int m = 0; m < M; m++) {
+                        acc[pp][m][d * 8 + 2 * b] = fmaf(sx[m], q0, acc[pp][m][d * 8 + 2 * b]);
+                        acc[pp][m][d * 8 + 2 * b + 1] = fmaf(sx[m], q1, acc[pp][m][d * 8 + 2 * b + 1]);
+                    }
                 }
             }
         }
     }
+#pragma unroll
+    for (int pp = 0; pp < NP; pp++)
+#pragma unroll
+        for (int m = 0; m < M; m++)
+#pragma unroll
+            for (int j = 0; j < 32; j++) acc[pp][m][j] = fmaf(-8.0f, sxsum[pp][m], acc[pp][m][j]);
 
     stamp(c, 5);
-    // 4. block reduction -> ybuf[pp][m][32].
+    // 4. block reduction -> ybuf[pp][m][32].  Four DPP exchange stages
+    //    within each row of 16 lanes halve the column set per stage (lane
+    //    bit s keeps the lower or upper half and receives the partner's copy
+    //    of it), leaving each lane two column sums over its row; the 16 rows
+    //    of the block are then added through LDS.
+    {
+        const int r16 = tid & 15, row = tid >> 4;
+        const bool b0 = r16 & 1, b1 = r16 & 2, b2 = r16 & 4, b3 = r16 & 8;
+        const int colbase = (b0 ? 16 : 0) + (b1 ? 8 : 0) + (b2 ? 4 : 0) + (b3 ? 2 : 0);
 #pragma unroll
-    for (int pp = 0; pp < NP; pp++) {
+        for (int pp = 0; pp < NP; pp++) {
 #pragma unroll
-        for (int m = 0; m < M; m++) {
+            for (int m = 0; m < M; m++) {
+                float v16[16], v8[8], v4[4], v2[2];
 #pragma unroll
-            for (int j = 0; j < 32; j++) red[tid * 33 + j] = acc[pp][m][j];
-            __syncthreads();
-            {
-                const int col = tid & 31, prt = tid >> 5;
-                float s = 0.0f;
-#pragma unroll 8
-                for (int r = 0; r < 32; r++) s += red[(prt * 32 + r) * 33 + col];
-                part8[prt * 32 + col] = s;
-            }
-            __syncthreads();
-            if (tid < 32) {
-                float s = 0.0f;
+                for (int j = 0; j < 16; j++) {
+                    const float keep = b0 ? acc[pp][m][j + 16] : acc[pp][m][j];
+                    const float send = b0 ? acc[pp][m][j] : acc[pp][m][j + 16];
+                    v16[j] = keep + dpp<kDppXor1>(send);
+                }
 #pragma unroll
-                for (int q = 0; q < 8; q++) s += part8[q * 32 + tid];
-                ybuf[(pp * M + m) * 32 + tid] = s;
+                for (int j = 0; j < 8; j++) {
+                    const float keep = b1 ? v16[j + 8] : v16[j], send = b1 ? v16[j] : v16[j + 8];
+                    v8[j] = keep + dpp<kDppXor2>(send);
+                }
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const float keep = b2 ? v8[j + 4] : v8[j], send = b2 ? v8[j] : v8[j + 4];
+                    v4[j] = keep + dpp_pick<kDppRowShr4, kDppRowShl4>(b2, send);
+                }
+#pragma unroll
+                for (int j = 0; j < 2; j++) {
+                    const float keep = b3 ? v4[j + 2] : v4[j], send = b3 ? v4[j] : v4[j + 2];
+                    v2[j] = keep + dpp_pick<kDppRowShr8, kDppRowShl8>(b3, send);
+                }
+                float *dst = &red[((pp * M + m) * 16 + row) * 32 + colbase];
+                dst[0] = v2[0];
+                dst[1] = v2[1];
             }
         }
+        __syncthreads();
+        if (tid < NP * M * 32) {
+            const int pm = tid >> 5, col = tid & 31;
+            float s = 0.0f;
+#pragma unroll
+            for (int r = 0; r < 16; r++) s += red[(pm * 16 + r) * 32 + col];
+            ybuf[pm * 32 + col] = s;
+        }
+        __syncthreads();
     }
-    __syncthreads();
 
     stamp(c, 6);
     // 5. split-K: non-owners publish partials; the owner adds them in order.
