@@ -73,6 +73,12 @@ __device__ __forceinline__ float lane_f(float v, int l) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
+// v[l] + v[l ^ 32] on every lane (v_permlane32_swap).
+__device__ __forceinline__ float halves_sum(float v) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Sum / max over the 64-lane wave; every lane gets the result.
 __device__ __forceinline__ float wave_sum(float v) {
     v = row16_sum(v);

@@ -415,8 +415,8 @@ __device__ __forceinline__ int eng_attn_t(const KCONST EngAttn &a, int task, uin
                                           float *smem) {
     constexpr int HD = 128, HALF = 64, CH = 256;
     constexpr int KJ = 8;    // positions per thread held in registers for the scores (16 lanes each)
-    constexpr int VJ = 64;   // positions per thread held in registers for P.V (two parities)
-    constexpr int PB = 128;  // positions per register batch (= 16 * KJ = 2 * VJ); splits are <= 128 long
+    constexpr int VJ = 16;   // positions per thread held in registers for P.V (8 groups of 32 lanes)
+    constexpr int PB = 128;  // positions per register batch (= 16 * KJ = 8 * VJ); splits are <= 128 long
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int G = a.nq / a.nkv;
     const int M = a.M;
@@ -433,39 +433,46 @@ __device__ __forceinline__ int eng_attn_t(const KCONST EngAttn &a, int task, uin
     float *vn = kn + kEngMaxM * HD;      // [M][HD]
     float *sc = vn + kEngMaxM * HD;      // [NPI][CH] scores
     float *pt = sc + kEngMaxM * 4 * CH;  // [CH][NPI] probabilities (position-major)
-    float *pv = pt + kEngMaxM * 4 * CH;  // [NPI][HD]
-    float *ml = pv + kEngMaxM * 4 * HD;  // [NPI][2]
+    float *ml = pt + kEngMaxM * 4 * CH;  // [NPI][2]
+    float *pvb = ml + 16;                // [4 waves][NPI][HD] P.V partials
     float *Kb = a.kcache + (size_t)kvh * a.kv_cap * HD;
     float *Vb = a.vcache + (size_t)kvh * a.kv_cap * HD;
-    const int l16 = tid & 15, slot = tid >> 4;    // scores: 16 lanes per position, 8 dims per lane
-    const int d = tid & (HD - 1), hf = tid >> 7;  // P.V: one dim, every other position
+    const int l16 = tid & 15, slot = tid >> 4;  // scores: 16 lanes per position, 8 dims per lane
+    const int d4 = tid & 31, r8 = tid >> 5;     // P.V: 4 dims, every 8th position
 
-    // Cached rows [0, base) for the register batch starting at position b0,
-    // read device-coherently (the rows may have been written on another
-    // XCD).  from_state: the rows were written by earlier launches, so the
-    // loads may be issued before this step's inputs arrive; otherwise (rows
-    // appended earlier in this launch) they are issued after the inputs.
-    // Positions past the split read as zero.
-    uint64_t kr[KJ][4];
-    float vr[VJ];
+    // Cached rows [0, base) for the register batch starting at position b0.
+    // from_state: the rows were written by earlier launches, so plain loads
+    // see them and may be issued before this step's inputs arrive.
+    // Otherwise (rows appended earlier in this launch, possibly on another
+    // XCD) they are read device-coherently after the inputs.  Positions past
+    // the split read as zero.
+    u32x4 kr[KJ][2];
+    u32x4 vr[VJ];
+    const u32x4 z4 = (u32x4){0u, 0u, 0u, 0u};
+    auto load16 = [&](const float *p) -> u32x4 {
+        if (a.from_state) return glb(reinterpret_cast<const u32x4 *>(p))[0];
+        const uint64_t *q = reinterpret_cast<const uint64_t *>(p);
+        const uint64_t e0 = ld_dev_u64(q), e1 = ld_dev_u64(q + 1);
+        return (u32x4){(uint32_t)e0, (uint32_t)(e0 >> 32), (uint32_t)e1, (uint32_t)(e1 >> 32)};
+    };
     auto load_k = [&](int b0) {
 #pragma unroll
         for (int j = 0; j < KJ; j++) {
             const int tt = b0 + slot + 16 * j, t = t0 + tt;
-#pragma unroll
-            for (int e = 0; e < 4; e++) kr[j][e] = 0;
+            kr[j][0] = kr[j][1] = z4;
             if (tt < nt && t < base) {
-                const uint64_t *src = reinterpret_cast<const uint64_t *>(Kb + (size_t)t * HD + l16 * 8);
-#pragma unroll
-                for (int e = 0; e < 4; e++) kr[j][e] = ld_dev_u64(src + e);
+                const float *src = Kb + (size_t)t * HD + l16 * 8;
+                kr[j][0] = load16(src);
+                kr[j][1] = load16(src + 4);
             }
         }
     };
     auto load_v = [&](int b0) {
 #pragma unroll
         for (int u = 0; u < VJ; u++) {
-            const int tt = b0 + hf + 2 * u, t = t0 + tt;
-            vr[u] = (tt < nt && t < base) ? ld_dev(&Vb[(size_t)t * HD + d]) : 0.0f;
+            const int tt = b0 + r8 + 8 * u, t = t0 + tt;
+            vr[u] = z4;
+            if (tt < nt && t < base) vr[u] = load16(Vb + (size_t)t * HD + 4 * d4);
         }
     };
     // the M new rows of the batch come from LDS
@@ -474,18 +481,16 @@ __device__ __forceinline__ int eng_attn_t(const KCONST EngAttn &a, int task, uin
         for (int j = 0; j < KJ; j++) {
             const int tt = b0 + slot + 16 * j, t = t0 + tt;
             if (tt < nt && t >= base) {
-                const float *src = &kn[(t - base) * HD + l16 * 8];
-#pragma unroll
-                for (int e = 0; e < 4; e++)
-                    kr[j][e] = (uint64_t)__float_as_uint(src[2 * e]) | ((uint64_t)__float_as_uint(src[2 * e + 1]) << 32);
+                kr[j][0] = *reinterpret_cast<const u32x4 *>(&kn[(t - base) * HD + l16 * 8]);
+                kr[j][1] = *reinterpret_cast<const u32x4 *>(&kn[(t - base) * HD + l16 * 8 + 4]);
             }
         }
     };
     auto patch_v = [&](int b0) {
 #pragma unroll
         for (int u = 0; u < VJ; u++) {
-            const int tt = b0 + hf + 2 * u, t = t0 + tt;  // wave-uniform
-            if (tt < nt && t >= base) vr[u] = vn[(t - base) * HD + d];
+            const int tt = b0 + r8 + 8 * u, t = t0 + tt;
+            if (tt < nt && t >= base) vr[u] = *reinterpret_cast<const u32x4 *>(&vn[(t - base) * HD + 4 * d4]);
         }
     };
 
@@ -592,12 +597,9 @@ __device__ __forceinline__ int eng_attn_t(const KCONST EngAttn &a, int task, uin
 #pragma unroll
         for (int j = 0; j < KJ; j++) {
             const int tt = b0 + slot + 16 * j, t = t0 + tt;
-            float k8[8];
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                k8[2 * e] = __uint_as_float((uint32_t)kr[j][e]);
-                k8[2 * e + 1] = __uint_as_float((uint32_t)(kr[j][e] >> 32));
-            }
+            const float k8[8] = {__uint_as_float(kr[j][0].x), __uint_as_float(kr[j][0].y), __uint_as_float(kr[j][0].z),
+                                 __uint_as_float(kr[j][0].w), __uint_as_float(kr[j][1].x), __uint_as_float(kr[j][1].y),
+                                 __uint_as_float(kr[j][1].z), __uint_as_float(kr[j][1].w)};
 #pragma unroll
             for (int pi = 0; pi < NPI; pi++) {
                 float dot = 0.0f;
@@ -641,17 +643,21 @@ __device__ __forceinline__ int eng_attn_t(const KCONST EngAttn &a, int task, uin
     }
     __syncthreads();
     stamp(c, 7);
-    // 6. P.V (src/talker.rs:327-331): thread (d, parity) over its positions
+    // 6. P.V (src/talker.rs:327-331): thread (4 dims, position group) over
+    //    its positions; the 8 groups are added by a lane swap across the
+    //    wave halves and then through LDS.
     {
-        float acc[NPI];
+        float acc[NPI][4];
 #pragma unroll
-        for (int pi = 0; pi < NPI; pi++) acc[pi] = 0.0f;
+        for (int pi = 0; pi < NPI; pi++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[pi][e] = 0.0f;
         for (int b0 = 0; b0 < nt; b0 += PB) {
             if (b0 > 0 || nt > PB) load_v(b0);  // a single-batch split reuses the early loads
             patch_v(b0);
 #pragma unroll
             for (int u = 0; u < VJ; u++) {
-                const int tt = b0 + hf + 2 * u;
+                const int tt = b0 + r8 + 8 * u;
                 float p[NPI];
                 if (NPI == 2) {
                     const float2 q = *reinterpret_cast<const float2 *>(&pt[tt * NPI]);
@@ -667,35 +673,43 @@ __device__ __forceinline__ int eng_attn_t(const KCONST EngAttn &a, int task, uin
                         p[4 * h4 + 3] = q.w;
                     }
                 }
+                const float v[4] = {__uint_as_float(vr[u].x), __uint_as_float(vr[u].y), __uint_as_float(vr[u].z),
+                                    __uint_as_float(vr[u].w)};
 #pragma unroll
-                for (int pi = 0; pi < NPI; pi++) acc[pi] += p[pi] * vr[u];
+                for (int pi = 0; pi < NPI; pi++)
+#pragma unroll
+                    for (int e = 0; e < 4; e++) acc[pi][e] += p[pi] * v[e];
             }
         }
-        if (hf == 1) {
 #pragma unroll
-            for (int pi = 0; pi < NPI; pi++) pv[pi * HD + d] = acc[pi];
+        for (int pi = 0; pi < NPI; pi++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[pi][e] = halves_sum(acc[pi][e]);
+        if (lane < 32) {
+#pragma unroll
+            for (int pi = 0; pi < NPI; pi++)
+                *reinterpret_cast<float4 *>(&pvb[(wave * NPI + pi) * HD + 4 * d4]) =
+                    make_float4(acc[pi][0], acc[pi][1], acc[pi][2], acc[pi][3]);
         }
         // Rows appended in this launch are read by later steps of the same
         // launch: their stores complete before the outputs that order those
         // steps.  Rows of a from_state step are only read by later launches.
         if (!a.from_state) wait_stores();
         __syncthreads();
-        if (hf == 0) {
-#pragma unroll
-            for (int pi = 0; pi < NPI; pi++) {
-                if (pi >= npi) continue;
-                const int m = pi / G, g = pi - m * G, h = kvh * G + g;
-                const float o = acc[pi] + pv[pi * HD + d];
-                if (a.nsplit == 1) {
-                    const float l = ml[pi * 2 + 1];
-                    put_tv(&a.out[(size_t)m * a.nq * HD + h * HD + d], o / l, tb + a.out_tag);
-                } else {
-                    tv_t *dst = a.part + (((size_t)m * a.nq + h) * a.nsplit + sp) * (HD + 2);
-                    put_tv(&dst[2 + d], o, tb + a.part_tag);
-                    if (d == 0) {
-                        put_tv(&dst[0], ml[pi * 2], tb + a.part_tag);
-                        put_tv(&dst[1], ml[pi * 2 + 1], tb + a.part_tag);
-                    }
+        for (int idx = tid; idx < npi * HD; idx += kEngThreads) {
+            const int pi = idx / HD, d = idx - pi * HD;
+            const int m = pi / G, g = pi - m * G, h = kvh * G + g;
+            const float o = (pvb[(0 * NPI + pi) * HD + d] + pvb[(1 * NPI + pi) * HD + d]) +
+                            (pvb[(2 * NPI + pi) * HD + d] + pvb[(3 * NPI + pi) * HD + d]);
+            if (a.nsplit == 1) {
+                const float l = ml[pi * 2 + 1];
+                put_tv(&a.out[(size_t)m * a.nq * HD + h * HD + d], o / l, tb + a.out_tag);
+            } else {
+                tv_t *dst = a.part + (((size_t)m * a.nq + h) * a.nsplit + sp) * (HD + 2);
+                put_tv(&dst[2 + d], o, tb + a.part_tag);
+                if (d == 0) {
+                    put_tv(&dst[0], ml[pi * 2], tb + a.part_tag);
+                    put_tv(&dst[1], ml[pi * 2 + 1], tb + a.part_tag);
                 }
             }
         }
