@@ -140,6 +140,86 @@ __device__ __forceinline__ float simple_rand_dev(uint64_t *state) {
     return (float)s / 18446744073709551616.0f;
 }
 
+// acc[m][c] += sx[m] * nib_c for the 32 nibbles of one panel row (nib_c in
+// 0..15; the caller subtracts 8 * sum(sx) per column once).  The nibbles are
+// split into bytes so each converts with one v_cvt_f32_ubyteN.
+template <int M>
+__device__ __forceinline__ void q4_fma_row(const u32x4 w, const float (&sx)[M], float (&acc)[M][32]) {
+    const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int d = 0; d < 4; d++) {
+        const uint32_t lo = wd[d] & 0x0F0F0F0Fu;         // nibbles 0, 2, 4, 6
+        const uint32_t hi = (wd[d] >> 4) & 0x0F0F0F0Fu;  // nibbles 1, 3, 5, 7
+#pragma unroll
+        for (int b = 0; b < 4; b++) {
+            const float q0 = (float)((lo >> (8 * b)) & 0xFFu), q1 = (float)((hi >> (8 * b)) & 0xFFu);
+#pragma unroll
+            for (int m = 0; m < M; m++) {
+                acc[m][d * 8 + 2 * b] = fmaf(sx[m], q0, acc[m][d * 8 + 2 * b]);
+                acc[m][d * 8 + 2 * b + 1] = fmaf(sx[m], q1, acc[m][d * 8 + 2 * b + 1]);
+            }
+        }
+    }
+}
+
+// Column sums of a 256-thread block's acc[32], step one: four DPP exchange
+// stages within each row of 16 lanes halve the column set per stage (lane
+// bit s keeps the lower or upper half and receives the partner's copy of
+// it), leaving each lane two column sums over its row, stored to
+// red[row][32] (row = tid / 16).  After a barrier, red[0..15][c] summed over
+// the rows is column c.
+__device__ __forceinline__ void dpp_reduce32(const float (&acc)[32], float *red) {
+    const int tid = threadIdx.x, r16 = tid & 15, row = tid >> 4;
+    const bool b0 = r16 & 1, b1 = r16 & 2, b2 = r16 & 4, b3 = r16 & 8;
+    const int colbase = (b0 ? 16 : 0) + (b1 ? 8 : 0) + (b2 ? 4 : 0) + (b3 ? 2 : 0);
+    float v16[16], v8[8], v4[4], v2[2];
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const float keep = b0 ? acc[j + 16] : acc[j], send = b0 ? acc[j] : acc[j + 16];
+        v16[j] = keep + dpp<kDppXor1>(send);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const float keep = b1 ? v16[j + 8] : v16[j], send = b1 ? v16[j] : v16[j + 8];
+        v8[j] = keep + dpp<kDppXor2>(send);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const float keep = b2 ? v8[j + 4] : v8[j], send = b2 ? v8[j] : v8[j + 4];
+        v4[j] = keep + dpp_pick<kDppRowShr4, kDppRowShl4>(b2, send);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; j++) {
+        const float keep = b3 ? v4[j + 2] : v4[j], send = b3 ? v4[j] : v4[j + 2];
+        v2[j] = keep + dpp_pick<kDppRowShr8, kDppRowShl8>(b3, send);
+    }
+    red[row * 32 + colbase] = v2[0];
+    red[row * 32 + colbase + 1] = v2[1];
+}
+
+// out[i] = element (row, col0 + i * stride) of a panel-major Q4 weight for
+// columns < ncol, else 0 (row < w.K).  All loads are issued before any is
+// used, as in embed_lookup_q4 (src/gemv.rs:377-400) per element.
+template <int N, typename Q4>
+__device__ __forceinline__ void q4_gather(const Q4 &w, uint32_t row, int col0, int stride, int ncol, float (&out)[N]) {
+    uint32_t by[N], sc[N];
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        const int col = min(col0 + i * stride, ncol - 1);
+        const size_t r = (size_t)(col >> 5) * w.K + row;
+        by[i] = glb(reinterpret_cast<const uint8_t *>(w.wq))[r * 16 + ((col & 31) >> 1)];
+        sc[i] = glb(w.ws)[r];
+    }
+#pragma unroll
+    for (int i = 0; i < N; i++) asm volatile("" : "+v"(by[i]), "+v"(sc[i]));
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        const int col = col0 + i * stride;
+        const int nib = (col & 1) ? (int)(by[i] >> 4) : (int)(by[i] & 15u);
+        out[i] = col < ncol ? f16_to_f32((uint16_t)sc[i]) * (float)(nib - 8) : 0.0f;
+    }
+}
+
 // Element (row, col) of a panel-major Q4 weight: f32(scale) * (nib - 8),
 // the product embed_lookup_q4 forms (src/gemv.rs:388-396); exact.
 template <typename Q4>

@@ -237,11 +237,12 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
         } else {
             // embed_lookup_q4 (src/gemv.rs:377-400) of the tagged token's row.
             const uint32_t tok = wait_tv_u32(in.tok_tv, tb + in.tag, c);
+            float ev[kEngRptMax];
 #pragma unroll
-            for (int i = 0; i < kEngRptMax; i++) {
-                const int k = k0 + tid + i * kEngThreads;
-                xv[i][m] = (k < k1 && tok < (uint32_t)in.emb.K) ? q4_element(in.emb, tok, k) : 0.0f;
-            }
+            for (int i = 0; i < kEngRptMax; i++) ev[i] = 0.0f;
+            if (tok < (uint32_t)in.emb.K) q4_gather<kEngRptMax>(in.emb, tok, k0 + tid, kEngThreads, k1, ev);
+#pragma unroll
+            for (int i = 0; i < kEngRptMax; i++) xv[i][m] = ev[i];
         }
     }
 
@@ -259,9 +260,8 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
     for (int i = 0; i < kEngRptMax; i++)
 #pragma unroll
         for (int pp = 0; pp < NP; pp++) asm volatile("" : "+v"(sv[pp][i]), "+v"(wv[pp][i]));
-    // Each term is (scale * x) * nib - 8 * (scale * x): the nibbles are
-    // split into bytes and converted with one v_cvt_f32_ubyteN each, and the
-    // offset is applied once per column from the running sum of scale * x.
+    // Each term is (scale * x) * nib - 8 * (scale * x): the offset is applied
+    // once per column from the running sum of scale * x.
     float sxsum[NP][M];
 #pragma unroll
     for (int pp = 0; pp < NP; pp++)
@@ -279,21 +279,7 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
                 sx[m] = s * xv[i][m];
                 sxsum[pp][m] += sx[m];
             }
-            const uint32_t wd[4] = {wv[pp][i].x, wv[pp][i].y, wv[pp][i].z, wv[pp][i].w};  // 32 nibbles
-#pragma unroll
-            for (int d = 0; d < 4; d++) {
-                const uint32_t lo = wd[d] & 0x0F0F0F0Fu;          // nibbles 0, 2, 4, 6
-                const uint32_t hi = (wd[d] >> 4) & 0x0F0F0F0Fu;   // nibbles 1, 3, 5, 7
-#pragma unroll
-                for (int b = 0; b < 4; b++) {
-                    const float q0 = (float)((lo >> (8 * b)) & 0xFFu), q1 = (float)((hi >> (8 * b)) & 0xFFu);
-#pragma unroll
-                    for (int m = 0; m < M; m++) {
-                        acc[pp][m][d * 8 + 2 * b] = fmaf(sx[m], q0, acc[pp][m][d * 8 + 2 * b]);
-                        acc[pp][m][d * 8 + 2 * b + 1] = fmaf(sx[m], q1, acc[pp][m][d * 8 + 2 * b + 1]);
-                    }
-                }
-            }
+            q4_fma_row<M>(wv[pp][i], sx, acc[pp]);
         }
     }
 #pragma unroll
@@ -304,56 +290,20 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
             for (int j = 0; j < 32; j++) acc[pp][m][j] = fmaf(-8.0f, sxsum[pp][m], acc[pp][m][j]);
 
     stamp(c, 5);
-    // 4. block reduction -> ybuf[pp][m][32].  Four DPP exchange stages
-    //    within each row of 16 lanes halve the column set per stage (lane
-    //    bit s keeps the lower or upper half and receives the partner's copy
-    //    of it), leaving each lane two column sums over its row; the 16 rows
-    //    of the block are then added through LDS.
-    {
-        const int r16 = tid & 15, row = tid >> 4;
-        const bool b0 = r16 & 1, b1 = r16 & 2, b2 = r16 & 4, b3 = r16 & 8;
-        const int colbase = (b0 ? 16 : 0) + (b1 ? 8 : 0) + (b2 ? 4 : 0) + (b3 ? 2 : 0);
+    // 4. block reduction -> ybuf[pp][m][32] (DPP row stage, then 16 rows through LDS).
 #pragma unroll
-        for (int pp = 0; pp < NP; pp++) {
+    for (int pp = 0; pp < NP; pp++)
 #pragma unroll
-            for (int m = 0; m < M; m++) {
-                float v16[16], v8[8], v4[4], v2[2];
+        for (int m = 0; m < M; m++) dpp_reduce32(acc[pp][m], &red[(pp * M + m) * 16 * 32]);
+    __syncthreads();
+    if (tid < NP * M * 32) {
+        const int pm = tid >> 5, col = tid & 31;
+        float s = 0.0f;
 #pragma unroll
-                for (int j = 0; j < 16; j++) {
-                    const float keep = b0 ? acc[pp][m][j + 16] : acc[pp][m][j];
-                    const float send = b0 ? acc[pp][m][j] : acc[pp][m][j + 16];
-                    v16[j] = keep + dpp<kDppXor1>(send);
-                }
-#pragma unroll
-                for (int j = 0; j < 8; j++) {
-                    const float keep = b1 ? v16[j + 8] : v16[j], send = b1 ? v16[j] : v16[j + 8];
-                    v8[j] = keep + dpp<kDppXor2>(send);
-                }
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const float keep = b2 ? v8[j + 4] : v8[j], send = b2 ? v8[j] : v8[j + 4];
-                    v4[j] = keep + dpp_pick<kDppRowShr4, kDppRowShl4>(b2, send);
-                }
-#pragma unroll
-                for (int j = 0; j < 2; j++) {
-                    const float keep = b3 ? v4[j + 2] : v4[j], send = b3 ? v4[j] : v4[j + 2];
-                    v2[j] = keep + dpp_pick<kDppRowShr8, kDppRowShl8>(b3, send);
-                }
-                float *dst = &red[((pp * M + m) * 16 + row) * 32 + colbase];
-                dst[0] = v2[0];
-                dst[1] = v2[1];
-            }
-        }
-        __syncthreads();
-        if (tid < NP * M * 32) {
-            const int pm = tid >> 5, col = tid & 31;
-            float s = 0.0f;
-#pragma unroll
-            for (int r = 0; r < 16; r++) s += red[(pm * 16 + r) * 32 + col];
-            ybuf[pm * 32 + col] = s;
-        }
-        __syncthreads();
+        for (int r = 0; r < 16; r++) s += red[(pm * 16 + r) * 32 + col];
+        ybuf[pm * 32 + col] = s;
     }
+    __syncthreads();
 
     stamp(c, 6);
     // 5. split-K: non-owners publish partials; the owner adds them in order.
@@ -410,13 +360,15 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
 // raw q/k, K/V append (src/talker.rs:299-302), then softmax(q.K^T*scale).V
 // over the split (src/talker.rs:304-331), causal across the M new rows.
 // ---------------------------------------------------------------------------
-template <int NPI>
+// NPI: (row, head) pairs rounded up; KJ: positions per thread held in
+// registers for the scores (16 lanes each) -- a register batch covers
+// PB = 16 * KJ positions (talker splits are <= 128 long, predictor steps <= 32).
+template <int NPI, int KJ>
 __device__ __forceinline__ int eng_attn_t(const KCONST EngAttn &a, int task, uint32_t tb, const EngState &st, Ctl &c,
                                           float *smem) {
     constexpr int HD = 128, HALF = 64, CH = 256;
-    constexpr int KJ = 8;    // positions per thread held in registers for the scores (16 lanes each)
-    constexpr int VJ = 16;   // positions per thread held in registers for P.V (8 groups of 32 lanes)
-    constexpr int PB = 128;  // positions per register batch (= 16 * KJ = 8 * VJ); splits are <= 128 long
+    constexpr int VJ = 2 * KJ;     // positions per thread for P.V (8 groups of 32 lanes)
+    constexpr int PB = 16 * KJ;    // positions per register batch
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int G = a.nq / a.nkv;
     const int M = a.M;
@@ -616,7 +568,7 @@ __device__ __forceinline__ int eng_attn_t(const KCONST EngAttn &a, int task, uin
     stamp(c, 6);
     // 5. local softmax statistics, one wave per (row, head) (src/talker.rs:319-326);
     //    the probabilities go to pt position-major, zero past the split.
-    const int ntp = (nt + PB - 1) / PB * PB;
+    const int ntp = (nt + PB - 1) / PB * PB;  // P.V reads whole batches
     for (int pi = wave; pi < NPI; pi += kEngThreads / 64) {
         if (pi >= npi) {
             for (int t = lane; t < ntp; t += 64) pt[t * NPI + pi] = 0.0f;
@@ -720,9 +672,11 @@ __device__ __forceinline__ int eng_attn_t(const KCONST EngAttn &a, int task, uin
 __device__ __forceinline__ int eng_attn(const KCONST EngAttn &a, int task, uint32_t tb, const EngState &st, Ctl &c,
                                         float *smem) {
     const int npi = a.M * (a.nq / a.nkv);
-    if (npi <= 2) return eng_attn_t<2>(a, task, tb, st, c, smem);
-    if (npi <= 4) return eng_attn_t<4>(a, task, tb, st, c, smem);
-    return eng_attn_t<8>(a, task, tb, st, c, smem);
+    const int Lt = (a.from_state ? st.kvlen : a.len_const) + a.M;
+    const bool small = (Lt + a.nsplit - 1) / a.nsplit <= 32;
+    if (npi <= 2) return small ? eng_attn_t<2, 2>(a, task, tb, st, c, smem) : eng_attn_t<2, 8>(a, task, tb, st, c, smem);
+    if (npi <= 4) return small ? eng_attn_t<4, 2>(a, task, tb, st, c, smem) : eng_attn_t<4, 8>(a, task, tb, st, c, smem);
+    return small ? eng_attn_t<8, 2>(a, task, tb, st, c, smem) : eng_attn_t<8, 8>(a, task, tb, st, c, smem);
 }
 
 // Combine the splits of one (row, query head): flash-decode merge.

@@ -35,25 +35,6 @@ __device__ float block_sum_256(float v, float *scratch /* >= 4 */) {
     return t;
 }
 
-// One Q4 nibble contributes (scale*x) * (nib - 8) to its output column
-// (the reference's LUT entry, src/gemv.rs:239-256).
-template <int M>
-__device__ __forceinline__ void q4_accumulate(const uint4 wv, const float s, const float (&xv)[M],
-                                              float (&acc)[M][32]) {
-    float sx[M];
-#pragma unroll
-    for (int m = 0; m < M; m++) sx[m] = s * xv[m];
-    const uint32_t wd[4] = {wv.x, wv.y, wv.z, wv.w};
-#pragma unroll
-    for (int d = 0; d < 4; d++) {
-#pragma unroll
-        for (int b = 0; b < 8; b++) {
-            const float q = (float)((int)((wd[d] >> (4 * b)) & 15u) - 8);
-#pragma unroll
-            for (int m = 0; m < M; m++) acc[m][d * 8 + b] = fmaf(sx[m], q, acc[m][d * 8 + b]);
-        }
-    }
-}
 
 }  // namespace
 
@@ -63,8 +44,7 @@ __device__ __forceinline__ void q4_accumulate(const uint4 wv, const float s, con
 template <int M, int RPT>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvParams P) {
     if (P.d_done && *P.d_done) return;
-    __shared__ float red[kGemvThreads * 33];
-    __shared__ float part8[8 * 32];
+    __shared__ float red[kMaxM * 16 * 32];
     __shared__ float ybuf[kMaxM * 128];
     __shared__ float scratch[8];
     __shared__ int s_last;
@@ -76,19 +56,19 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvParams P) {
     const int c = blockIdx.x - p * P.kc;
     const int k0 = c * (kGemvThreads * RPT);
 
-    // 1. weight rows of this chunk: one 128-bit load + one scale per row.
-    uint4 wv[RPT];
-    uint16_t sv[RPT];
+    // 1. weight rows of this chunk: one 128-bit load + one scale per row,
+    //    issued back to back with no branch between them.  A thread past the
+    //    last row (only in the last chunk) re-reads that row, and its input
+    //    is zero; the raw scale bits stay opaque until the accumulation so
+    //    that no load result is waited for while the others are issued.
+    const int nit = min(RPT, (K - k0 + kGemvThreads - 1) / kGemvThreads);
+    u32x4 wv[RPT];
+    uint32_t sv[RPT];
 #pragma unroll
     for (int i = 0; i < RPT; i++) {
-        const int k = k0 + tid + i * kGemvThreads;
-        if (k < K) {
-            wv[i] = P.w.wq[(size_t)p * K + k];
-            sv[i] = P.w.ws[(size_t)p * K + k];
-        } else {
-            wv[i] = make_uint4(0u, 0u, 0u, 0u);
-            sv[i] = 0;
-        }
+        const int k = min(k0 + tid + i * kGemvThreads, K - 1);
+        wv[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(P.w.wq) + (size_t)p * K + k);
+        sv[i] = __builtin_nontemporal_load(P.w.ws + (size_t)p * K + k);
     }
 
     // 2. input values of those rows.
@@ -127,20 +107,14 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvParams P) {
     } else if (P.prologue == PRO_EMBED) {
         // embed_lookup_q4 (src/gemv.rs:377-400) of row *emb_token.
         const uint32_t tok = *P.emb_token;
-        const uint8_t *eb = reinterpret_cast<const uint8_t *>(P.emb.wq);
+        float ev[RPT];
 #pragma unroll
-        for (int i = 0; i < RPT; i++) {
-            const int k = k0 + tid + i * kGemvThreads;
-            float v = 0.0f;
-            if (k < K && tok < (uint32_t)P.emb.K) {
-                const size_t row = (size_t)(k >> 5) * P.emb.K + tok;
-                const uint8_t byte = eb[row * 16 + ((k & 31) >> 1)];
-                const int nib = (k & 1) ? (byte >> 4) : (byte & 15);
-                v = f16_to_f32(P.emb.ws[row]) * (float)(nib - 8);
-            }
+        for (int i = 0; i < RPT; i++) ev[i] = 0.0f;
+        if (tok < (uint32_t)P.emb.K) q4_gather<RPT>(P.emb, tok, k0 + tid, kGemvThreads, K, ev);
 #pragma unroll
-            for (int m = 0; m < M; m++) xv[i][m] = v;
-        }
+        for (int i = 0; i < RPT; i++)
+#pragma unroll
+            for (int m = 0; m < M; m++) xv[i][m] = ev[i];
     } else {
 #pragma unroll
         for (int i = 0; i < RPT; i++) {
@@ -150,35 +124,45 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvParams P) {
         }
     }
 
-    // 3. accumulate 32 columns per thread.
+    // 3. accumulate 32 columns per thread: (scale * x) * nib, minus
+    //    8 * sum(scale * x) per column.
     float acc[M][32];
+    float sxsum[M];
+#pragma unroll
+    for (int m = 0; m < M; m++) {
+        sxsum[m] = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 32; j++) acc[m][j] = 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < RPT; i++) asm volatile("" : "+v"(sv[i]), "+v"(wv[i]));
+#pragma unroll
+    for (int i = 0; i < RPT; i++) {
+        if (i >= nit) continue;
+        const float s = f16_to_f32((uint16_t)sv[i]);
+        float sx[M];
+#pragma unroll
+        for (int m = 0; m < M; m++) {
+            sx[m] = s * xv[i][m];
+            sxsum[m] += sx[m];
+        }
+        q4_fma_row<M>(wv[i], sx, acc);
+    }
 #pragma unroll
     for (int m = 0; m < M; m++)
 #pragma unroll
-        for (int j = 0; j < 32; j++) acc[m][j] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < RPT; i++) q4_accumulate<M>(wv[i], f16_to_f32(sv[i]), xv[i], acc);
+        for (int j = 0; j < 32; j++) acc[m][j] = fmaf(-8.0f, sxsum[m], acc[m][j]);
 
     // 4. block reduction -> this chunk's partial for the panel's 32 columns.
 #pragma unroll
-    for (int m = 0; m < M; m++) {
+    for (int m = 0; m < M; m++) dpp_reduce32(acc[m], &red[m * 16 * 32]);
+    __syncthreads();
+    if (tid < M * 32) {
+        const int m = tid >> 5, col = tid & 31;
+        float s = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 32; j++) red[tid * 33 + j] = acc[m][j];
-        __syncthreads();
-        {
-            const int col = tid & 31, part = tid >> 5;
-            float s = 0.0f;
-#pragma unroll 8
-            for (int r = 0; r < 32; r++) s += red[(part * 32 + r) * 33 + col];
-            part8[part * 32 + col] = s;
-        }
-        __syncthreads();
-        if (tid < 32) {
-            float s = 0.0f;
-#pragma unroll
-            for (int q = 0; q < 8; q++) s += part8[q * 32 + tid];
-            st_dev(&P.partial[((size_t)c * M + m) * N + p * 32 + tid], s);
-        }
+        for (int r = 0; r < 16; r++) s += red[(m * 16 + r) * 32 + col];
+        st_dev(&P.partial[((size_t)c * M + m) * N + p * 32 + col], s);
     }
 
     // 5. the last block of an output group sums the chunks in order.
