@@ -1,5 +1,6 @@
 """Benchmark: codes/s of the 1.7B talker + code-predictor per-code loop at
-batch 1 on one MI355X, with the Q4 GEMV's achieved HBM bandwidth and the
+batch 1 on one MI355X, with the achieved bandwidth of the kernel the loop
+runs (k_engine, one launch per code), the stand-alone Q4 GEMV's, and the
 oracle's codes/s on this host's CPU cores.
 
 Workload (one "step" = one code = one frame of generate_speech's loop,
@@ -75,6 +76,48 @@ class Hip:
         return ms.value
 
 
+def q4_bytes(k, n):
+    """Bytes of a K x N Q4 weight: packed nibbles + one f16 scale per 32 columns."""
+    return k * n // 2 + k * (n // 32) * 2
+
+
+def frame_bytes(tc, pc, groups, kv_len):
+    """Algorithmic bytes one engine launch (one code) moves: every weight it
+    applies once (talker layers + codec head, the predictor's input
+    projection, 5 layers and one head per pass), the talker K/V rows it reads
+    at kv_len positions and writes once, and the predictor's K/V rows."""
+    def layer(c):
+        qd, kd = c.heads * c.head_dim, c.kv_heads * c.head_dim
+        return (q4_bytes(c.hidden, qd + 2 * kd) + q4_bytes(qd, c.hidden) + q4_bytes(c.hidden, 2 * c.inter)
+                + q4_bytes(c.inter, c.hidden) + 4 * c.hidden + 4 * c.head_dim)
+    talker = tc.layers * layer(tc) + q4_bytes(tc.hidden, tc.vocab) + 2 * tc.hidden
+    kv_row = tc.kv_heads * tc.head_dim * 4
+    talker_kv = tc.layers * 2 * kv_row * (kv_len + 1)
+    pred_pass = q4_bytes(tc.hidden, pc.hidden) + pc.layers * layer(pc) + q4_bytes(pc.hidden, pc.vocab)
+    pred_kv = sum(pc.layers * 2 * pc.kv_heads * pc.head_dim * 4 * (g + 2) for g in range(groups))
+    return talker + talker_kv + groups * pred_pass + pred_kv
+
+
+def engine_roofline(frames, gpu_s, kv_len_mean):
+    """k_engine, the kernel the loop runs (one launch per code): algorithmic
+    bytes per launch over the average launch duration from HIP events on the
+    context's stream around the timed region."""
+    per = frame_bytes(qtts.TALKER_1P7B, qtts.PREDICTOR_1P7B, qtts.NUM_GROUPS, kv_len_mean)
+    avg_s = gpu_s / frames
+    achieved = per / avg_s / 1e9
+    return {
+        "bound": "hbm",
+        "achieved": round(achieved, 1),
+        "peak": HBM_PEAK_GBS,
+        "unit": "GB/s",
+        "frac": round(achieved / HBM_PEAK_GBS, 4),
+        "traffic": read_traffic("k_engine_frame_counters.md"),
+        "kernel": "k_engine (one cooperative launch per code: sampler, 15 predictor passes, talker step)",
+        "algorithmic_bytes_per_launch": per,
+        "avg_launch_us": round(avg_s * 1e6, 2),
+    }
+
+
 def gemv_roofline(ctx, iters=256, copies=64):
     """Average duration of the talker's gate|up Q4 GEMV shape (K=2048 ->
     N=2*6144 in one launch) over `copies` distinct weights (a 0.9 GB working
@@ -104,8 +147,8 @@ def gemv_roofline(ctx, iters=256, copies=64):
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
-        "traffic": read_traffic(),
-        "kernel": "k_gemv<1,4> (Q4 GEMV 2048->12288, talker gate|up)",
+        "traffic": read_traffic("q4_gemv_2048x12288_counters.md"),
+        "kernel": "k_gemv<1,4> (stand-alone Q4 GEMV 2048->12288, talker gate|up, launch gaps included)",
         "algorithmic_bytes_per_launch": algo_bytes,
         "avg_launch_us": round(avg_s * 1e6, 3),
     }
@@ -124,10 +167,10 @@ def copy_calibration(ctx, nbytes=512 << 20):
     return nbytes
 
 
-def read_traffic():
-    """HBM bytes per launch of the roofline GEMV measured by the rocprofv3
-    counter runs (profiles/q4_gemv_2048x12288_counters.md), if present."""
-    path = os.path.join(ROOT, "profiles", "q4_gemv_2048x12288_counters.md")
+def read_traffic(name):
+    """HBM bytes per launch measured by the rocprofv3 counter runs
+    (profiles/<name>), if present."""
+    path = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(path):
         return None
     for line in open(path):
@@ -165,7 +208,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--cpu-frames", type=int, default=12)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-roofline", action="store_true")
+    ap.add_argument("--no-roofline", action="store_true", help="skip the stand-alone GEMV timing")
     ap.add_argument("--roofline-only", action="store_true",
                     help="only the GEMV timing and the copy-kernel calibration (for counter runs)")
     args = ap.parse_args()
@@ -206,11 +249,16 @@ def main():
         qtts.generate_codes(talker, pred, kv, pkv, lh, lg, PROMPT, text, pad, params(args.warmup), seed=41)
         log(f"warmup {args.warmup} codes done")
     kv, lh, lg = prefill()
+    hip = Hip()
+    ev0, ev1 = hip.event(), hip.event()
     ctx.synchronize()
     t1 = time.perf_counter()
+    hip.record(ev0, ctx.stream)
     codes = qtts.generate_codes(talker, pred, kv, pkv, lh, lg, PROMPT, text, pad, params(args.steps), seed=42)
+    hip.record(ev1, ctx.stream)
     ctx.synchronize()
     dt = time.perf_counter() - t1
+    gpu_s = hip.elapsed_ms(ev0, ev1) / 1e3
     assert codes.shape == (16, args.steps), codes.shape
     cps = args.steps / dt
     log(f"{args.steps} codes in {dt * 1e3:.1f} ms -> {cps:.1f} codes/s")
@@ -236,9 +284,11 @@ def main():
             "sampler": "top-k 50, temperature 0.8, repetition penalty 1.05",
         },
     }
+    out["roofline"] = engine_roofline(args.steps, gpu_s, PROMPT + (args.steps - 1) / 2)
+    log(f"roofline {out['roofline']}")
     if not args.no_roofline:
-        out["roofline"] = gemv_roofline(ctx)
-        log(f"roofline {out['roofline']}")
+        out["gemv"] = gemv_roofline(ctx)
+        log(f"stand-alone gemv {out['gemv']}")
     if not args.no_cpu:
         lh_np, lg_np = lh, lg
         kv_cpu, lh_np, lg_np = prefill()
