@@ -148,8 +148,11 @@ __device__ __forceinline__ void q4_fma_row(const u32x4 w, const float (&sx)[M], 
     const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
 #pragma unroll
     for (int d = 0; d < 4; d++) {
-        const uint32_t lo = wd[d] & 0x0F0F0F0Fu;         // nibbles 0, 2, 4, 6
-        const uint32_t hi = (wd[d] >> 4) & 0x0F0F0F0Fu;  // nibbles 1, 3, 5, 7
+        uint32_t lo = wd[d] & 0x0F0F0F0Fu;         // nibbles 0, 2, 4, 6
+        uint32_t hi = (wd[d] >> 4) & 0x0F0F0F0Fu;  // nibbles 1, 3, 5, 7
+        // opaque to the compiler, which would otherwise fold the byte
+        // conversions back into per-nibble bit-field extracts
+        asm volatile("" : "+v"(lo), "+v"(hi));
 #pragma unroll
         for (int b = 0; b < 4; b++) {
             const float q0 = (float)((lo >> (8 * b)) & 0xFFu), q1 = (float)((hi >> (8 * b)) & 0xFFu);

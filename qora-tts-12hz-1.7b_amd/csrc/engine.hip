@@ -114,26 +114,14 @@ __device__ __forceinline__ void put_tv_u32(tv_t *p, uint32_t x, uint32_t tag) {
     st_dev_u64(p, ((uint64_t)tag << 32) | (uint64_t)x);
 }
 
-// Sum over the 256-thread block, fixed order; every thread gets the result.
-__device__ __forceinline__ float block_sum(float v, float *scr) {
-    v = wave_sum(v);
-    __syncthreads();
-    if ((threadIdx.x & 63) == 0) scr[threadIdx.x >> 6] = v;
-    __syncthreads();
-    const float t = (scr[0] + scr[1]) + (scr[2] + scr[3]);
-    __syncthreads();
-    return t;
-}
-
 // ---------------------------------------------------------------------------
 // GEMV task: NP panels (1, or gate+up for SwiGLU) x one K chunk x M rows.
 // Same arithmetic as k_gemv: acc += (scale * x) * (nib - 8), f32.
 // ---------------------------------------------------------------------------
 template <int M, int NP>
 __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint32_t tb, Ctl &c, float *smem) {
-    float *red = smem;                         // [NP][M][16 rows][32]
-    float *ybuf = red + NP * M * 16 * 32;      // [NP][M][32]
-    float *scr = ybuf + NP * M * 32;        // [8]
+    float *red = smem;                     // [NP][M][16 rows][32]
+    float *scr = red + NP * M * 16 * 32;   // [M][4] block-sum partials
     const int tid = threadIdx.x;
     const int N = g.w.N, K = g.w.K;
     const int ngroups = NP == 2 ? N / 64 : N / 32;
@@ -176,21 +164,19 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
         gam[i] = 0u;
         if (g.norm && i < nit) gam[i] = glb(g.gamma)[k];
     }
-    // The owner's epilogue operands (bias; the residual, tag-checked when
-    // used), also loaded before any wait.
+    // The owner's bias, also loaded before any wait.
     const bool epi_lane = ch == 0 && NP == 1 && tid < M * 32;
     float e_bias = 0.0f;
     uint64_t e_res = 0;
-    if (epi_lane) {
-        const int m = tid >> 5, col = group * 32 + (tid & 31);
-        if (g.bias) e_bias = glb(g.bias)[col];
-        if (g.epi == EEPI_RESID) e_res = ld_dev_u64(&g.resid[(size_t)m * g.ld_resid + col]);
-    }
+    if (epi_lane && g.bias) e_bias = glb(g.bias)[group * 32 + (tid & 31)];
 
     stamp(c, 2);
     // 2. inputs of this thread's rows.
     stamp(c, 3);
     float xv[kEngRptMax][M];
+    float ssq[M];  // this thread's share of the row's sum of squares (norm only)
+#pragma unroll
+    for (int m = 0; m < M; m++) ssq[m] = 0.0f;
 #pragma unroll
     for (int m = 0; m < M; m++) {
         const KCONST EngInput &in = g.in[m];
@@ -214,13 +200,14 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
                 for (int i = 0; i < kEngRptMax; i++)
                     if (j - j0 == i) keep[i] = row[j];
             }
-            ss = block_sum(ss, scr);
-            const float inv = 1.0f / sqrtf(ss / (float)K + 1e-6f);
+            // The row is accumulated as x * gamma and the sums are scaled by
+            // 1 / rms once the block's sum of squares is known (after the
+            // reduction barrier), so no barrier sits before the accumulation.
+            ssq[m] = ss;
 #pragma unroll
             for (int i = 0; i < kEngRptMax; i++) {
                 const int k = k0 + tid + i * kEngThreads;
-                xv[i][m] = k < k1 ? keep[i] * inv * f16_to_f32((uint16_t)gam[i]) : 0.0f;
-                if (g.norm_plain && m == M - 1 && group == 0 && ch == 0 && k < k1) st_dev(&g.norm_plain[k], xv[i][m]);
+                xv[i][m] = k < k1 ? keep[i] * f16_to_f32((uint16_t)gam[i]) : 0.0f;
             }
         } else if (in.kind == EIN_TV) {
             const int cnt = k1 > k0 + tid ? (k1 - k0 - tid + kEngThreads - 1) / kEngThreads : 0;
@@ -246,6 +233,11 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
         }
     }
 
+    // The residual is older than the input in the dependency chain, so it is
+    // ready now; its load flies during the accumulation.
+    if (epi_lane && g.epi == EEPI_RESID)
+        e_res = ld_dev_u64(&g.resid[(size_t)(tid >> 5) * g.ld_resid + group * 32 + (tid & 31)]);
+    asm volatile("" ::: "memory");  // keep the load here (not sunk to its use)
     stamp(c, 4);
     // 3. accumulate 32 columns per panel.
     float acc[NP][M][32];
@@ -290,66 +282,90 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
             for (int j = 0; j < 32; j++) acc[pp][m][j] = fmaf(-8.0f, sxsum[pp][m], acc[pp][m][j]);
 
     stamp(c, 5);
-    // 4. block reduction -> ybuf[pp][m][32] (DPP row stage, then 16 rows through LDS).
+    // 4. block reduction (DPP row stage, then 16 rows through LDS).  Thread
+    //    (m, j) < M * 32 ends with column j of row m of every panel, so the
+    //    split-K exchange and the epilogue stay in its registers.
 #pragma unroll
     for (int pp = 0; pp < NP; pp++)
 #pragma unroll
         for (int m = 0; m < M; m++) dpp_reduce32(acc[pp][m], &red[(pp * M + m) * 16 * 32]);
-    __syncthreads();
-    if (tid < NP * M * 32) {
-        const int pm = tid >> 5, col = tid & 31;
-        float s = 0.0f;
+    if (g.norm) {
 #pragma unroll
-        for (int r = 0; r < 16; r++) s += red[(pm * 16 + r) * 32 + col];
-        ybuf[pm * 32 + col] = s;
+        for (int m = 0; m < M; m++) {
+            const float w = wave_sum(ssq[m]);
+            if ((tid & 63) == 0) scr[4 * m + (tid >> 6)] = w;
+        }
     }
     __syncthreads();
-
     stamp(c, 6);
-    // 5. split-K: non-owners publish partials; the owner adds them in order.
-    if (ch > 0) {
-        for (int idx = tid; idx < NP * M * 32; idx += kEngThreads) {
-            const int pp = idx / (M * 32), m = (idx / 32) % M, j = idx & 31;
-            put_tv(&g.part[((size_t)(ch - 1) * M + m) * N + panel[pp] * 32 + j], ybuf[idx], tb + g.part_tag);
-        }
-        return -1;
-    }
-    if (g.kc > 1) {
-        for (int idx = tid; idx < NP * M * 32; idx += kEngThreads) {
-            const int pp = idx / (M * 32), m = (idx / 32) % M, j = idx & 31;
-            float pv4[4];
-            wait_strided<4>(&g.part[(size_t)m * N + panel[pp] * 32 + j], (size_t)M * N, g.kc - 1, tb + g.part_tag, pv4, c);
-            float s = ybuf[idx];
+    float inv[M];  // 1 / rms of each input row (rms_norm_f16, src/gemv.rs:406-417)
 #pragma unroll
-            for (int cc = 0; cc < 4; cc++)
-                if (cc < g.kc - 1) s += pv4[cc];
-            ybuf[idx] = s;
+    for (int m = 0; m < M; m++)
+        inv[m] = g.norm ? 1.0f / sqrtf(((scr[4 * m] + scr[4 * m + 1]) + (scr[4 * m + 2] + scr[4 * m + 3])) / (float)K + 1e-6f)
+                        : 1.0f;
+    if (g.norm_plain && group == 0 && ch == 0) {
+        // the normed last row, for a later launch
+#pragma unroll
+        for (int i = 0; i < kEngRptMax; i++) {
+            const int k = k0 + tid + i * kEngThreads;
+            if (i < nit && k < k1) st_dev(&g.norm_plain[k], xv[i][M - 1] * inv[M - 1]);
         }
-        __syncthreads();
     }
-
-    // 6. epilogue
-    if (NP == 2) {
-        // silu(g) * u, src/talker.rs:342-345
-        for (int idx = tid; idx < M * 32; idx += kEngThreads) {
-            const int m = idx >> 5, j = idx & 31;
-            const float gt = ybuf[m * 32 + j], up = ybuf[(M + m) * 32 + j];
-            const float h = (gt / (1.0f + expf(-gt))) * up;
-            put_tv(&g.out[(size_t)m * g.ld_out + group * 32 + j], h, tb + g.out_tag);
+    if (tid < M * 32) {
+        const int m = tid >> 5, j = tid & 31;
+        float y[NP];
+#pragma unroll
+        for (int pp = 0; pp < NP; pp++) {
+            float r16[16];
+#pragma unroll
+            for (int r = 0; r < 16; r++) r16[r] = red[((pp * M + m) * 16 + r) * 32 + j];
+#pragma unroll
+            for (int w = 8; w >= 1; w >>= 1)
+#pragma unroll
+                for (int r = 0; r < w; r++) r16[r] += r16[r + w];
+            y[pp] = r16[0];
         }
-    } else if (epi_lane) {
-        const int m = tid >> 5, j = tid & 31, col = group * 32 + j;
-        float v = ybuf[m * 32 + j];
-        if (g.bias) v += e_bias;
-        if (g.epi == EEPI_RESID) {
-            const float r = (uint32_t)(e_res >> 32) == tb + g.resid_tag
-                                ? __uint_as_float((uint32_t)e_res)
-                                : wait_tv(&g.resid[(size_t)m * g.ld_resid + col], tb + g.resid_tag, c);
-            v = r + v;
+        // 5. split-K: non-owners publish partials; the owner adds them in order.
+        if (ch > 0) {
+#pragma unroll
+            for (int pp = 0; pp < NP; pp++)
+                put_tv(&g.part[((size_t)(ch - 1) * M + m) * N + panel[pp] * 32 + j], y[pp], tb + g.part_tag);
+            return -1;
         }
-        put_tv(&g.out[(size_t)m * g.ld_out + col], v, tb + g.out_tag);
-        if (g.out_plain) st_dev(&g.out_plain[(size_t)m * g.ld_plain + col], v);
+        if (g.kc > 1) {
+#pragma unroll
+            for (int pp = 0; pp < NP; pp++) {
+                float pv4[4];
+                wait_strided<4>(&g.part[(size_t)m * N + panel[pp] * 32 + j], (size_t)M * N, g.kc - 1, tb + g.part_tag, pv4, c);
+#pragma unroll
+                for (int cc = 0; cc < 4; cc++)
+                    if (cc < g.kc - 1) y[pp] += pv4[cc];
+            }
+        }
+        if (g.norm) {
+#pragma unroll
+            for (int pp = 0; pp < NP; pp++) y[pp] *= inv[m];
+        }
+        // 6. epilogue
+        if (NP == 2) {
+            // silu(g) * u, src/talker.rs:342-345
+            const float gt = y[0], up = y[NP - 1];
+            put_tv(&g.out[(size_t)m * g.ld_out + group * 32 + j], (gt / (1.0f + expf(-gt))) * up, tb + g.out_tag);
+        } else {
+            const int col = group * 32 + j;
+            float v = y[0];
+            if (g.bias) v += e_bias;
+            if (g.epi == EEPI_RESID) {
+                const float r = (uint32_t)(e_res >> 32) == tb + g.resid_tag
+                                    ? __uint_as_float((uint32_t)e_res)
+                                    : wait_tv(&g.resid[(size_t)m * g.ld_resid + col], tb + g.resid_tag, c);
+                v = r + v;
+            }
+            put_tv(&g.out[(size_t)m * g.ld_out + col], v, tb + g.out_tag);
+            if (g.out_plain) st_dev(&g.out_plain[(size_t)m * g.ld_plain + col], v);
+        }
     }
+    if (ch > 0) return -1;
     stamp(c, 7);
     return group;
 }
@@ -1130,7 +1146,10 @@ __device__ __forceinline__ int eng_embsum(const KCONST EngEmbSum &E, int task, u
 
 __global__ __launch_bounds__(kEngThreads) void k_engine(EngArgs A) {
     __shared__ __align__(16) float smem[kEngSmemFloats];
+    __shared__ int s_bad;  // set by a thread that saw the abort word or timed out
     if (ld_dev_i32(A.done)) return;
+    if (threadIdx.x == 0) s_bad = 0;
+    __syncthreads();
     Ctl c{A.done, A.status, 0u, false, nullptr};
     EngState st;
     st.pos = ld_dev_i32(&A.st_in->pos);
@@ -1175,7 +1194,11 @@ __global__ __launch_bounds__(kEngThreads) void k_engine(EngArgs A) {
                 default: break;
             }
             (void)fi;
-            if (__syncthreads_or(c.bad ? 1 : 0)) return;
+            // One barrier between tasks: LDS is reused by the next task, and
+            // the block leaves together once any thread has seen an abort.
+            if (c.bad) s_bad = 1;
+            __syncthreads();
+            if (s_bad) return;
         }
         if (tr && threadIdx.x == 0) {
             glb(tr)[1] = wall_clock64();
