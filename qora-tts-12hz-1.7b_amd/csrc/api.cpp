@@ -52,6 +52,7 @@ struct qtts_ctx {
     int eng_grid = 0;
     uint64_t *eng_trace = nullptr;  // QTTS_ENGINE_TRACE: per-op block timestamps
     size_t eng_trace_cap = 0;
+    long long eng_launches = 0;
     // The context and every object made from it hold one reference each, so
     // objects may be freed after qtts_ctx_destroy (e.g. in any order at
     // interpreter shutdown).
@@ -801,11 +802,15 @@ qtts_status eng_launch(qtts_ctx *c, EngProgram &P, int st_in, uint32_t *codes, i
     a.status = c->eng_status;
     a.codes = codes;
     a.max_codes = max_codes;
-    // QTTS_ENGINE_TRACE=<file>: each launch synchronizes and appends
+    // QTTS_ENGINE_TRACE=<file>: each launch (from the QTTS_ENGINE_TRACE_FROM-th
+    // of this context on) synchronizes and appends
     // {nops, grid, kind[nops], ntasks[nops], u64 stamps[nops][grid][kTraceSlots]}.
     const char *trace_path = std::getenv("QTTS_ENGINE_TRACE");
+    const char *trace_from = std::getenv("QTTS_ENGINE_TRACE_FROM");
     const size_t trace_n = (size_t)a.nops * P.grid * kTraceSlots;
-    if (trace_path && *trace_path) {
+    const bool trace_this = trace_path && *trace_path && c->eng_launches >= (trace_from ? std::atoll(trace_from) : 0);
+    c->eng_launches++;
+    if (trace_this) {
         if (c->eng_trace_cap < trace_n) {
             if (c->eng_trace) (void)hipFree(c->eng_trace);
             c->eng_trace = nullptr;
@@ -842,9 +847,11 @@ qtts_status eng_status_check(qtts_ctx *c, const char *what) {
     return QTTS_OK;
 }
 
-// Talker attention splits: chunks of at most 256 positions, ~128 typical.
+// Talker attention splits of ~32 positions: a split's K/V rows (1 KB per
+// position) stream into one CU at ~25-30 GB/s, so short splits keep the
+// attention step near its hand-off latency at long contexts.
 int eng_talker_nsplit(int cap) {
-    int n = (cap + 127) / 128;
+    int n = (cap + 31) / 32;
     if (n < 1) n = 1;
     if (n > kEngMaxSplit) n = kEngMaxSplit;
     return n;

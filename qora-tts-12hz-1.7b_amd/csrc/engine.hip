@@ -695,30 +695,45 @@ __device__ __forceinline__ int eng_attn(const KCONST EngAttn &a, int task, uint3
     return small ? eng_attn_t<8, 2>(a, task, tb, st, c, smem) : eng_attn_t<8, 8>(a, task, tb, st, c, smem);
 }
 
-// Combine the splits of one (row, query head): flash-decode merge.
-__device__ __forceinline__ int eng_combine(const KCONST EngCombine &cb, int task, uint32_t tb, Ctl &c) {
+// Combine the splits of one (row, query head): flash-decode merge.  Threads
+// 0..127 load their dim of every split's P.V while threads 128.. load the
+// splits' (max, sum): one round trip for all of it.
+__device__ __forceinline__ int eng_combine(const KCONST EngCombine &cb, int task, uint32_t tb, Ctl &c, float *smem) {
     constexpr int HD = 128;
     const int m = task / cb.nq, h = task - m * cb.nq;
-    const int d = threadIdx.x;
-    if (d >= HD) return task;
-    const tv_t *base = cb.part + ((size_t)m * cb.nq + h) * cb.nsplit * (HD + 2);
-    float ms[kEngMaxSplit], ls[kEngMaxSplit], os[kEngMaxSplit];
-    wait_strided<kEngMaxSplit>(base, HD + 2, cb.nsplit, tb + cb.part_tag, ms, c);
-    wait_strided<kEngMaxSplit>(base + 1, HD + 2, cb.nsplit, tb + cb.part_tag, ls, c);
-    wait_strided<kEngMaxSplit>(base + 2 + d, HD + 2, cb.nsplit, tb + cb.part_tag, os, c);
-    float mx = -INFINITY;
-#pragma unroll
-    for (int s = 0; s < kEngMaxSplit; s++)
-        if (s < cb.nsplit) mx = fmaxf(mx, ms[s]);
-    float o = 0.0f, l = 0.0f;
-#pragma unroll
-    for (int s = 0; s < kEngMaxSplit; s++) {
-        if (s >= cb.nsplit || ms[s] == -INFINITY) continue;
-        const float w = expf(ms[s] - mx);
-        o += w * os[s];
-        l += w * ls[s];
+    const int tid = threadIdx.x;
+    const int ns = cb.nsplit;
+    const tv_t *base = cb.part + ((size_t)m * cb.nq + h) * ns * (HD + 2);
+    float *sm = smem;                   // [kEngMaxSplit] split max
+    float *sl = smem + kEngMaxSplit;    // [kEngMaxSplit] split sum
+    float os[kEngMaxSplit];
+    if (tid < HD) {
+        wait_strided<kEngMaxSplit>(base + 2 + tid, HD + 2, ns, tb + cb.part_tag, os, c);
+    } else if (tid - HD < ns) {
+        const int sp = tid - HD;
+        const tv_t *ptr[2] = {base + (size_t)sp * (HD + 2), base + (size_t)sp * (HD + 2) + 1};
+        const uint32_t tg[2] = {tb + cb.part_tag, tb + cb.part_tag};
+        float ml[2];
+        wait_list<2>(ptr, tg, 2, ml, c);
+        sm[sp] = ml[0];
+        sl[sp] = ml[1];
     }
-    put_tv(&cb.out[(size_t)m * cb.nq * HD + h * HD + d], o / l, tb + cb.out_tag);
+    __syncthreads();
+    if (tid < HD) {
+        float mx = -INFINITY;
+#pragma unroll
+        for (int sp = 0; sp < kEngMaxSplit; sp++)
+            if (sp < ns) mx = fmaxf(mx, sm[sp]);
+        float o = 0.0f, l = 0.0f;
+#pragma unroll
+        for (int sp = 0; sp < kEngMaxSplit; sp++) {
+            if (sp >= ns || sm[sp] == -INFINITY) continue;
+            const float w = expf(sm[sp] - mx);
+            o += w * os[sp];
+            l += w * sl[sp];
+        }
+        put_tv(&cb.out[(size_t)m * cb.nq * HD + h * HD + tid], o / l, tb + cb.out_tag);
+    }
     return task;
 }
 
@@ -1187,7 +1202,7 @@ __global__ __launch_bounds__(kEngThreads) void k_engine(EngArgs A) {
                     break;
                 }
                 case EOP_ATTN: fi = eng_attn(op.attn, t, A.tag_base, st, c, smem); break;
-                case EOP_COMBINE: fi = eng_combine(op.comb, t, A.tag_base, c); break;
+                case EOP_COMBINE: fi = eng_combine(op.comb, t, A.tag_base, c, smem); break;
                 case EOP_ARGMAX: eng_argmax(op.amax, A.tag_base, st, c, A.codes, A.max_codes, smem); break;
                 case EOP_SAMPLE: eng_sample(op.samp, A.tag_base, st, A.st_out, c, A.codes, A.max_codes, smem); break;
                 case EOP_EMBSUM: fi = eng_embsum(op.emb, t, A.tag_base, st, c); break;
