@@ -436,11 +436,13 @@ struct EngProgram {
     int next_tag = 1;
     int rot_next = 0;
     int grid = 1;
+    const char *err = nullptr;  // set when an op cannot be expressed
     ~EngProgram() {
         if (d_ops) (void)hipFree(d_ops);
         if (arena) (void)hipFree(arena);
     }
     void reset_build() {
+        err = nullptr;
         ops.clear();
         used = 0;
         next_tag = 1;
@@ -556,21 +558,26 @@ TvRef add_gemv(EngProgram &P, const DevQ4 &w, const GemvSpec &sp) {
     EngOp op{};
     op.kind = EOP_GEMV;
     EngGemv &g = op.gemv;
-    const int NP = sp.epi == EEPI_SWIGLU ? 2 : 1;
-    const int ngroups = w.N / (32 * NP);
     const int Nout = sp.epi == EEPI_SWIGLU ? w.N / 2 : w.N;
-    // One K chunk per group where the rows fit one task: a split-K owner
-    // waits a cross-block round trip for its partials.
+    // Tasks of whole 32-column panels (the kernel's GEMV slice width).
+    const int NP = sp.epi == EEPI_SWIGLU ? 2 : 1;
+    const int C = 32;
+    const int rpt = eng_rows_per_thread(C, NP);
+    if (Nout % 32 != 0 || (sp.norm && w.K > kEngThreads * kEngNormRows)) P.err = "engine GEMV shape not supported";
+    // One K chunk where the rows fit one task: a split-K owner waits a
+    // cross-block round trip for its partials.
     int kc = sp.kc > 0 ? sp.kc : 1;
-    const int kmin = (w.K + kEngThreads * kEngRptMax - 1) / (kEngThreads * kEngRptMax);
+    const int kmin = (w.K + kEngThreads * rpt - 1) / (kEngThreads * rpt);
     if (kc < kmin) kc = kmin;
     int kchunk = (w.K + kc - 1) / kc;
     kchunk = (kchunk + kEngThreads - 1) / kEngThreads * kEngThreads;
     kc = (w.K + kchunk - 1) / kchunk;
+    if (sp.norm && kc != 1) P.err = "engine GEMV shape not supported";
     g.w = w;
     g.M = sp.M;
     g.kc = kc;
     g.kchunk = kchunk;
+    g.cols = C;
     g.epi = sp.epi;
     g.norm = sp.norm ? 1 : 0;
     g.gamma = sp.gamma;
@@ -589,7 +596,7 @@ TvRef add_gemv(EngProgram &P, const DevQ4 &w, const GemvSpec &sp) {
         g.part = P.tv((size_t)(kc - 1) * sp.M * w.N);
         g.part_tag = P.tag();
     }
-    op.ntasks = ngroups * kc;
+    op.ntasks = (Nout / C) * kc;
     P.push(op);
     return TvRef{g.out, g.out_tag, Nout};
 }
@@ -754,6 +761,7 @@ qtts_status eng_build(qtts_ctx *c, EngProgram &P, const BuildFn &fn) {
     P.sizing = true;
     P.reset_build();
     QTTS_TRY(fn(P));
+    if (P.err) return fail(c, QTTS_ESHAPE, P.err);
     const size_t need = P.used;
     if (P.arena) (void)hipFree(P.arena);
     if (P.d_ops) (void)hipFree(P.d_ops);

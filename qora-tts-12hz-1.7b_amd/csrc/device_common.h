@@ -140,64 +140,132 @@ __device__ __forceinline__ float simple_rand_dev(uint64_t *state) {
     return (float)s / 18446744073709551616.0f;
 }
 
-// acc[m][c] += sx[m] * nib_c for the 32 nibbles of one panel row (nib_c in
-// 0..15; the caller subtracts 8 * sum(sx) per column once).  The nibbles are
-// split into bytes so each converts with one v_cvt_f32_ubyteN.
-template <int M>
-__device__ __forceinline__ void q4_fma_row(const u32x4 w, const float (&sx)[M], float (&acc)[M][32]) {
-    const uint32_t wd[4] = {w.x, w.y, w.z, w.w};
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+
+// Dwords per row of a panel slice of C columns (C = 4: 16 bits in dword 0).
+template <int C>
+constexpr int q4_slice_dwords() {
+    return C >= 8 ? C / 8 : 1;
+}
+
+// One row of a C-column slice (`row` points at the slice's bytes inside a
+// 16-byte panel row), loaded with one non-temporal load of C / 2 bytes.
+template <int C>
+__device__ __forceinline__ void q4_slice_load(const uint8_t *row, uint32_t (&wd)[q4_slice_dwords<C>()]) {
+    if constexpr (C == 32) {
+        const u32x4 v = __builtin_nontemporal_load(glb(reinterpret_cast<const u32x4 *>(row)));
+        wd[0] = v.x;
+        wd[1] = v.y;
+        wd[2] = v.z;
+        wd[3] = v.w;
+    } else if constexpr (C == 16) {
+        const u32x2 v = __builtin_nontemporal_load(glb(reinterpret_cast<const u32x2 *>(row)));
+        wd[0] = v.x;
+        wd[1] = v.y;
+    } else if constexpr (C == 8) {
+        wd[0] = __builtin_nontemporal_load(glb(reinterpret_cast<const uint32_t *>(row)));
+    } else {
+        wd[0] = __builtin_nontemporal_load(glb(reinterpret_cast<const uint16_t *>(row)));
+    }
+}
+
+// acc[m][c] += sx[m] * nib_c over one row of a C-column slice (nibble c at
+// bits 4 * (c % 8) of dword c / 8; the caller subtracts 8 * sum(sx) per
+// column once), given sa = sx * 2^24 and sb = sx * 2^20, both exact.  Two
+// nibbles at a time are masked into the halves of a register, where they
+// read as f16 denormals: n * 2^-24 from bits 0-3 of a half, n * 2^-20 from
+// bits 4-7.  v_fma_mix_f32 converts a half exactly, so every term is
+// sx * n rounded once, the same sums as fmaf(sx, (float)n, acc), in 13 VALU
+// operations per 8 nibbles (a shift, 4 masks, 8 FMAs).
+template <int M, int C>
+__device__ __forceinline__ void q4_mix_row(const uint32_t (&wd)[q4_slice_dwords<C>()], const float (&sa)[M],
+                                           const float (&sb)[M], float (&acc)[M][C]) {
 #pragma unroll
-    for (int d = 0; d < 4; d++) {
-        uint32_t lo = wd[d] & 0x0F0F0F0Fu;         // nibbles 0, 2, 4, 6
-        uint32_t hi = (wd[d] >> 4) & 0x0F0F0F0Fu;  // nibbles 1, 3, 5, 7
-        // opaque to the compiler, which would otherwise fold the byte
-        // conversions back into per-nibble bit-field extracts
-        asm volatile("" : "+v"(lo), "+v"(hi));
+    for (int d = 0; d < q4_slice_dwords<C>(); d++) {
+        const uint32_t w = wd[d], w8 = w >> 8;
+        const f16x2 h0 = __builtin_bit_cast(f16x2, w & 0x000F000Fu);   // nibbles 0, 4
+        const f16x2 h1 = __builtin_bit_cast(f16x2, w & 0x00F000F0u);   // nibbles 1, 5
+        const f16x2 h2 = __builtin_bit_cast(f16x2, w8 & 0x000F000Fu);  // nibbles 2, 6
+        const f16x2 h3 = __builtin_bit_cast(f16x2, w8 & 0x00F000F0u);  // nibbles 3, 7
 #pragma unroll
-        for (int b = 0; b < 4; b++) {
-            const float q0 = (float)((lo >> (8 * b)) & 0xFFu), q1 = (float)((hi >> (8 * b)) & 0xFFu);
-#pragma unroll
-            for (int m = 0; m < M; m++) {
-                acc[m][d * 8 + 2 * b] = fmaf(sx[m], q0, acc[m][d * 8 + 2 * b]);
-                acc[m][d * 8 + 2 * b + 1] = fmaf(sx[m], q1, acc[m][d * 8 + 2 * b + 1]);
+        for (int m = 0; m < M; m++) {
+            float *a = &acc[m][8 * d];
+            a[0] = fmaf(sa[m], (float)h0.x, a[0]);
+            a[1] = fmaf(sb[m], (float)h1.x, a[1]);
+            a[2] = fmaf(sa[m], (float)h2.x, a[2]);
+            a[3] = fmaf(sb[m], (float)h3.x, a[3]);
+            if constexpr (C >= 8) {
+                a[4] = fmaf(sa[m], (float)h0.y, a[4]);
+                a[5] = fmaf(sb[m], (float)h1.y, a[5]);
+                a[6] = fmaf(sa[m], (float)h2.y, a[6]);
+                a[7] = fmaf(sb[m], (float)h3.y, a[7]);
             }
         }
     }
 }
 
-// Column sums of a 256-thread block's acc[32], step one: four DPP exchange
-// stages within each row of 16 lanes halve the column set per stage (lane
-// bit s keeps the lower or upper half and receives the partner's copy of
-// it), leaving each lane two column sums over its row, stored to
-// red[row][32] (row = tid / 16).  After a barrier, red[0..15][c] summed over
-// the rows is column c.
-__device__ __forceinline__ void dpp_reduce32(const float (&acc)[32], float *red) {
-    const int tid = threadIdx.x, r16 = tid & 15, row = tid >> 4;
+// Lane exchange of DPP stage S (partner lane = lane ^ (1 << S)) within rows
+// of 16 lanes; `bit` is this lane's bit S.
+template <int S>
+__device__ __forceinline__ float dpp_xchg(bool bit, float v) {
+    if constexpr (S == 0) return dpp<kDppXor1>(v);
+    else if constexpr (S == 1) return dpp<kDppXor2>(v);
+    else if constexpr (S == 2) return dpp_pick<kDppRowShr4, kDppRowShl4>(bit, v);
+    else return dpp_pick<kDppRowShr8, kDppRowShl8>(bit, v);
+}
+
+// One stage over the N values v[0..N): with N > 1 the set is halved (lanes
+// with `bit` keep the upper half and receive the partner's copy of it),
+// otherwise the partner's value is added.
+template <int N, int S, int C>
+__device__ __forceinline__ void dpp_stage(float (&v)[C], bool bit) {
+    if constexpr (N > 1) {
+#pragma unroll
+        for (int j = 0; j < N / 2; j++) {
+            const float keep = bit ? v[j + N / 2] : v[j], send = bit ? v[j] : v[j + N / 2];
+            v[j] = keep + dpp_xchg<S>(bit, send);
+        }
+    } else {
+        v[0] += dpp_xchg<S>(bit, v[0]);
+    }
+}
+
+// v summed over the four 16-lane rows of the wave, on every lane (for its
+// position in the row): rows (0 + 1) and (2 + 3) by v_permlane16_swap, then
+// the two halves by v_permlane32_swap.
+__device__ __forceinline__ float rows4_sum(float v) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
+// Column sums of a 256-thread block's acc[C] (C = 32, 16, 8 or 4), step
+// one: four DPP stages within each row of 16 lanes leave every lane with
+// max(C / 16, 1) column sums over its row, the rows of a wave are added by
+// lane swaps, and lanes 0-15 store the wave's sums to red[wave][C] (lanes
+// holding the same column store the same value).  After a barrier,
+// red[0..3][c] summed over the waves is column c.
+template <int C>
+__device__ __forceinline__ void dpp_reduce(const float (&acc)[C], float *red) {
+    const int tid = threadIdx.x, r16 = tid & 15, wave = tid >> 6;
     const bool b0 = r16 & 1, b1 = r16 & 2, b2 = r16 & 4, b3 = r16 & 8;
-    const int colbase = (b0 ? 16 : 0) + (b1 ? 8 : 0) + (b2 ? 4 : 0) + (b3 ? 2 : 0);
-    float v16[16], v8[8], v4[4], v2[2];
+    float v[C];
 #pragma unroll
-    for (int j = 0; j < 16; j++) {
-        const float keep = b0 ? acc[j + 16] : acc[j], send = b0 ? acc[j] : acc[j + 16];
-        v16[j] = keep + dpp<kDppXor1>(send);
-    }
+    for (int j = 0; j < C; j++) v[j] = acc[j];
+    dpp_stage<C, 0>(v, b0);
+    dpp_stage<(C / 2 > 1 ? C / 2 : 1), 1>(v, b1);
+    dpp_stage<(C / 4 > 1 ? C / 4 : 1), 2>(v, b2);
+    dpp_stage<(C / 8 > 1 ? C / 8 : 1), 3>(v, b3);
+    constexpr int NV = C / 16 > 1 ? C / 16 : 1;
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const float keep = b1 ? v16[j + 8] : v16[j], send = b1 ? v16[j] : v16[j + 8];
-        v8[j] = keep + dpp<kDppXor2>(send);
-    }
+    for (int j = 0; j < NV; j++) v[j] = rows4_sum(v[j]);
+    const int col = (b0 ? C / 2 : 0) + (b1 ? C / 4 : 0) + (C >= 8 && b2 ? C / 8 : 0) + (C >= 16 && b3 ? C / 16 : 0);
+    if ((tid & 63) < 16) {
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const float keep = b2 ? v8[j + 4] : v8[j], send = b2 ? v8[j] : v8[j + 4];
-        v4[j] = keep + dpp_pick<kDppRowShr4, kDppRowShl4>(b2, send);
+        for (int j = 0; j < NV; j++) red[wave * C + col + j] = v[j];
     }
-#pragma unroll
-    for (int j = 0; j < 2; j++) {
-        const float keep = b3 ? v4[j + 2] : v4[j], send = b3 ? v4[j] : v4[j + 2];
-        v2[j] = keep + dpp_pick<kDppRowShr8, kDppRowShl8>(b3, send);
-    }
-    red[row * 32 + colbase] = v2[0];
-    red[row * 32 + colbase + 1] = v2[1];
 }
 
 // out[i] = element (row, col0 + i * stride) of a panel-major Q4 weight for

@@ -24,7 +24,11 @@ namespace qtts {
 using tv_t = uint64_t;  // float bits | tag << 32
 
 constexpr int kEngThreads = 256;
-constexpr int kEngRptMax = 8;  // rows per thread of one GEMV task (K chunk <= 2048)
+// Rows per thread of a GEMV task over a slice of `cols` columns of `np`
+// panels (the K chunk is at most 256 times this): a task's weights stay in
+// registers from issue to use, cols / 8 dwords per row (one for 4 columns).
+constexpr int eng_rows_per_thread(int cols, int np) { return np == 2 || cols == 32 ? 8 : cols == 4 ? 16 : 24; }
+constexpr int kEngNormRows = 8;  // an RMSNorm input row has <= 256 * 8 values
 constexpr int kEngMaxM = 2;    // rows per GEMV (the predictor's 2-token prefill)
 constexpr uint32_t kTagStride = 8192;  // tags reserved per launch
 constexpr int kEngMaxSplit = 32;
@@ -47,7 +51,9 @@ struct EngGemv {
     DevQ4 w;
     int M;       // rows (1 or 2)
     int kc;      // K chunks; chunk 0 owns the epilogue
-    int kchunk;  // rows per chunk (multiple of 256, <= 256 * kEngRptMax)
+    int kchunk;  // rows per chunk (multiple of 256, <= 256 * eng_rows_per_thread(cols, panels))
+    int cols;    // output columns per task: 32, 16, 8 or 4 (a slice of a 32-column panel);
+                 // 32 or 16 for SwiGLU
     int epi;
     int norm;    // RMSNorm the input rows (rms_norm_f16)
     const uint16_t *gamma;

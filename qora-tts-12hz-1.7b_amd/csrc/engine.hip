@@ -115,65 +115,84 @@ __device__ __forceinline__ void put_tv_u32(tv_t *p, uint32_t x, uint32_t tag) {
 }
 
 // ---------------------------------------------------------------------------
-// GEMV task: NP panels (1, or gate+up for SwiGLU) x one K chunk x M rows.
-// Same arithmetic as k_gemv: acc += (scale * x) * (nib - 8), f32.
+// GEMV task: a slice of C output columns (C = 32, 16, 8 or 4 of a 32-column
+// panel; for SwiGLU the same slice of the gate and the up panel) x one K
+// chunk x M rows.  The host picks the narrowest slice that keeps the op
+// within one task per block, so every GEMV spreads over the whole grid.
+// Same arithmetic as k_gemv: acc += (scale * x) * nib - 8 * (scale * x), f32.
 // ---------------------------------------------------------------------------
-template <int M, int NP>
+template <int M, int NP, int C, int R>
 __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint32_t tb, Ctl &c, float *smem) {
-    float *red = smem;                     // [NP][M][16 rows][32]
-    float *scr = red + NP * M * 16 * 32;   // [M][4] block-sum partials
+    constexpr int DW = q4_slice_dwords<C>();
+    float *red = smem;                  // [NP][M][4 waves][C]
+    float *scr = red + NP * M * 4 * C;  // [M][4] block-sum partials
     const int tid = threadIdx.x;
     const int N = g.w.N, K = g.w.K;
-    const int ngroups = NP == 2 ? N / 64 : N / 32;
-    const int nonowner = ngroups * (g.kc - 1);
-    int group, ch;
+    const int Nout = N / NP;
+    const int P = Nout / 32;          // panels per half
+    const int per_chunk = Nout / C;   // tasks per K chunk
+    const int nonowner = per_chunk * (g.kc - 1);
+    int tt, ch;
     if (task < nonowner) {
-        group = task % ngroups;
-        ch = 1 + task / ngroups;
+        tt = task % per_chunk;
+        ch = 1 + task / per_chunk;
     } else {
-        group = task - nonowner;
+        tt = task - nonowner;
         ch = 0;
     }
+    // Slice-major: the slices of panel p are tasks p, p + P, ..., which run
+    // on blocks P apart -- one XCD when P % 8 == 0 (blocks are dealt to the
+    // 8 XCDs round-robin) -- so a panel's rows are fetched into one L2.
+    const int p = tt % P, sl = tt / P;
+    const int col0 = p * 32 + sl * C;  // first output column of the slice
     const int k0 = ch * g.kchunk;
     const int k1 = min(K, k0 + g.kchunk);
     int panel[NP];
-    panel[0] = group;
-    if (NP == 2) panel[NP - 1] = group + ngroups;
+    panel[0] = p;
+    if (NP == 2) panel[NP - 1] = p + P;
 
     // 1. this chunk's weight rows, issued back to back before any input
     //    wait: row iterations are wave-uniform (nit), a thread past the
     //    chunk's last row re-reads that row (its input is zero), and the raw
     //    scale/gamma bits stay opaque until the accumulation, so no load
     //    result is needed (and waited for) while the others are issued.
-    const int nit = (k1 - k0 + kEngThreads - 1) / kEngThreads;  // <= kEngRptMax
-    u32x4 wv[NP][kEngRptMax];
-    uint32_t sv[NP][kEngRptMax];
-    uint32_t gam[kEngRptMax];
+    const int nit = (k1 - k0 + kEngThreads - 1) / kEngThreads;  // <= R
+    const uint8_t *wq = reinterpret_cast<const uint8_t *>(g.w.wq) + sl * (C / 2);
+    uint32_t wv[NP][R][DW];
+    uint32_t sv[NP][R];
+    uint32_t gam[R];
 #pragma unroll
-    for (int i = 0; i < kEngRptMax; i++) {
+    for (int i = 0; i < R; i++) {
         const int k = min(k0 + tid + i * kEngThreads, k1 - 1);
 #pragma unroll
         for (int pp = 0; pp < NP; pp++) {
-            wv[pp][i] = (u32x4){0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int d = 0; d < DW; d++) wv[pp][i][d] = 0u;
             sv[pp][i] = 0u;
             if (i < nit) {
-                wv[pp][i] = __builtin_nontemporal_load(glb(reinterpret_cast<const u32x4 *>(g.w.wq)) + (size_t)panel[pp] * K + k);
+                q4_slice_load<C>(wq + ((size_t)panel[pp] * K + k) * 16, wv[pp][i]);
                 sv[pp][i] = __builtin_nontemporal_load(glb(g.w.ws) + (size_t)panel[pp] * K + k);
             }
         }
         gam[i] = 0u;
         if (g.norm && i < nit) gam[i] = glb(g.gamma)[k];
     }
-    // The owner's bias, also loaded before any wait.
-    const bool epi_lane = ch == 0 && NP == 1 && tid < M * 32;
+    // The owner's bias and residual, also loaded before any wait.  The
+    // residual is older than the input in the dependency chain and usually
+    // complete by now (its tag is checked in the epilogue, which re-reads
+    // it if not); loaded here, it does not sit in the queue behind the
+    // input polls.
+    const bool epi_lane = ch == 0 && NP == 1 && tid < M * C;
     float e_bias = 0.0f;
     uint64_t e_res = 0;
-    if (epi_lane && g.bias) e_bias = glb(g.bias)[group * 32 + (tid & 31)];
+    if (epi_lane && g.bias) e_bias = glb(g.bias)[col0 + (tid % C)];
+    if (epi_lane && g.epi == EEPI_RESID)
+        e_res = ld_dev_u64(&g.resid[(size_t)(tid / C) * g.ld_resid + col0 + (tid % C)]);
 
     stamp(c, 2);
     // 2. inputs of this thread's rows.
     stamp(c, 3);
-    float xv[kEngRptMax][M];
+    float xv[R][M];
     float ssq[M];  // this thread's share of the row's sum of squares (norm only)
 #pragma unroll
     for (int m = 0; m < M; m++) ssq[m] = 0.0f;
@@ -181,97 +200,102 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
     for (int m = 0; m < M; m++) {
         const KCONST EngInput &in = g.in[m];
         if (in.kind == EIN_TV && g.norm) {
-            // rms_norm_f16 (src/gemv.rs:406-417) over the full row.
+            // rms_norm_f16 (src/gemv.rs:406-417) over the full row, which is
+            // this task's chunk (the host keeps normed GEMVs in one chunk of
+            // <= 256 * kEngNormRows rows).
+            constexpr int NR = R < kEngNormRows ? R : kEngNormRows;
 #pragma unroll
-            for (int i = 0; i < kEngRptMax; i++) asm volatile("" : "+v"(gam[i]));
-            float keep[kEngRptMax];
-#pragma unroll
-            for (int i = 0; i < kEngRptMax; i++) keep[i] = 0.0f;
-            const int nj = K > tid ? (K - tid + kEngThreads - 1) / kEngThreads : 0;  // <= kEngRptMax (K <= 2048)
-            const int j0 = k0 / kEngThreads;
-            float row[kEngRptMax];
-            wait_strided<kEngRptMax>(in.tv + tid, kEngThreads, nj, tb + in.tag, row, c);
+            for (int i = 0; i < R; i++) asm volatile("" : "+v"(gam[i]));
+            const int nj = K > tid ? (K - tid + kEngThreads - 1) / kEngThreads : 0;  // <= NR
+            float row[NR];
+            wait_strided<NR>(in.tv + tid, kEngThreads, nj, tb + in.tag, row, c);
             float ss = 0.0f;
 #pragma unroll
-            for (int j = 0; j < kEngRptMax; j++) {
-                if (j >= nj) continue;
-                ss += row[j] * row[j];
-#pragma unroll
-                for (int i = 0; i < kEngRptMax; i++)
-                    if (j - j0 == i) keep[i] = row[j];
-            }
+            for (int j = 0; j < NR; j++)
+                if (j < nj) ss += row[j] * row[j];
             // The row is accumulated as x * gamma and the sums are scaled by
             // 1 / rms once the block's sum of squares is known (after the
             // reduction barrier), so no barrier sits before the accumulation.
             ssq[m] = ss;
 #pragma unroll
-            for (int i = 0; i < kEngRptMax; i++) {
-                const int k = k0 + tid + i * kEngThreads;
-                xv[i][m] = k < k1 ? keep[i] * f16_to_f32((uint16_t)gam[i]) : 0.0f;
-            }
+            for (int i = 0; i < R; i++) xv[i][m] = i < NR && i < nj ? row[i < NR ? i : 0] * f16_to_f32((uint16_t)gam[i]) : 0.0f;
         } else if (in.kind == EIN_TV) {
             const int cnt = k1 > k0 + tid ? (k1 - k0 - tid + kEngThreads - 1) / kEngThreads : 0;
-            float row[kEngRptMax];
-            wait_strided<kEngRptMax>(in.tv + k0 + tid, kEngThreads, cnt, tb + in.tag, row, c);
+            float row[R];
+            wait_strided<R>(in.tv + k0 + tid, kEngThreads, cnt, tb + in.tag, row, c);
 #pragma unroll
-            for (int i = 0; i < kEngRptMax; i++) xv[i][m] = i < cnt ? row[i] : 0.0f;
+            for (int i = 0; i < R; i++) xv[i][m] = i < cnt ? row[i] : 0.0f;
         } else if (in.kind == EIN_PLAIN) {
 #pragma unroll
-            for (int i = 0; i < kEngRptMax; i++) {
+            for (int i = 0; i < R; i++) {
                 const int k = k0 + tid + i * kEngThreads;
                 xv[i][m] = k < k1 ? ld_dev(&in.plain[k]) : 0.0f;
             }
         } else {
             // embed_lookup_q4 (src/gemv.rs:377-400) of the tagged token's row.
             const uint32_t tok = wait_tv_u32(in.tok_tv, tb + in.tag, c);
-            float ev[kEngRptMax];
+            float ev[R];
 #pragma unroll
-            for (int i = 0; i < kEngRptMax; i++) ev[i] = 0.0f;
-            if (tok < (uint32_t)in.emb.K) q4_gather<kEngRptMax>(in.emb, tok, k0 + tid, kEngThreads, k1, ev);
+            for (int i = 0; i < R; i++) ev[i] = 0.0f;
+            if (tok < (uint32_t)in.emb.K) q4_gather<R>(in.emb, tok, k0 + tid, kEngThreads, k1, ev);
 #pragma unroll
-            for (int i = 0; i < kEngRptMax; i++) xv[i][m] = ev[i];
+            for (int i = 0; i < R; i++) xv[i][m] = ev[i];
         }
     }
 
-    // The residual is older than the input in the dependency chain, so it is
-    // ready now; its load flies during the accumulation.
-    if (epi_lane && g.epi == EEPI_RESID)
-        e_res = ld_dev_u64(&g.resid[(size_t)(tid >> 5) * g.ld_resid + group * 32 + (tid & 31)]);
-    asm volatile("" ::: "memory");  // keep the load here (not sunk to its use)
+    // Every input value is final here: one wait, not one per row of the
+    // accumulation below.
+#pragma unroll
+    for (int i = 0; i < R; i++)
+#pragma unroll
+        for (int m = 0; m < M; m++) asm volatile("" : "+v"(xv[i][m]));
+    // A residual read before it was complete (a block that ran ahead) is
+    // read again now; the load flies during the accumulation.
+    if (epi_lane && g.epi == EEPI_RESID && (uint32_t)(e_res >> 32) != tb + g.resid_tag)
+        e_res = ld_dev_u64(&g.resid[(size_t)(tid / C) * g.ld_resid + col0 + (tid % C)]);
     stamp(c, 4);
-    // 3. accumulate 32 columns per panel.
-    float acc[NP][M][32];
+    // 3. accumulate the slice's columns per panel.
+    float acc[NP][M][C];
 #pragma unroll
     for (int pp = 0; pp < NP; pp++)
 #pragma unroll
         for (int m = 0; m < M; m++)
 #pragma unroll
-            for (int j = 0; j < 32; j++) acc[pp][m][j] = 0.0f;
+            for (int j = 0; j < C; j++) acc[pp][m][j] = 0.0f;
     // weights and scales are consumed only from here on
 #pragma unroll
-    for (int i = 0; i < kEngRptMax; i++)
+    for (int i = 0; i < R; i++)
 #pragma unroll
-        for (int pp = 0; pp < NP; pp++) asm volatile("" : "+v"(sv[pp][i]), "+v"(wv[pp][i]));
+        for (int pp = 0; pp < NP; pp++) {
+            asm volatile("" : "+v"(sv[pp][i]));
+#pragma unroll
+            for (int d = 0; d < DW; d++) asm volatile("" : "+v"(wv[pp][i][d]));
+        }
     // Each term is (scale * x) * nib - 8 * (scale * x): the offset is applied
-    // once per column from the running sum of scale * x.
+    // once per column from the running sum of scale * x, kept (like the
+    // products' operands) scaled by 2^24.
     float sxsum[NP][M];
 #pragma unroll
     for (int pp = 0; pp < NP; pp++)
 #pragma unroll
         for (int m = 0; m < M; m++) sxsum[pp][m] = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kEngRptMax; i++) {
+    for (int i = 0; i < R; i++) {
         if (i >= nit) continue;  // uniform; rows past k1 carry a zero input
+        float xa[M];
+#pragma unroll
+        for (int m = 0; m < M; m++) xa[m] = xv[i][m] * 16777216.0f;
 #pragma unroll
         for (int pp = 0; pp < NP; pp++) {
             const float s = f16_to_f32((uint16_t)sv[pp][i]);
-            float sx[M];
+            float sa[M], sb[M];
 #pragma unroll
             for (int m = 0; m < M; m++) {
-                sx[m] = s * xv[i][m];
-                sxsum[pp][m] += sx[m];
+                sa[m] = s * xa[m];
+                sb[m] = sa[m] * 0.0625f;
+                sxsum[pp][m] += sa[m];
             }
-            q4_fma_row<M>(wv[pp][i], sx, acc[pp]);
+            q4_mix_row<M, C>(wv[pp][i], sa, sb, acc[pp]);
         }
     }
 #pragma unroll
@@ -279,16 +303,17 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
 #pragma unroll
         for (int m = 0; m < M; m++)
 #pragma unroll
-            for (int j = 0; j < 32; j++) acc[pp][m][j] = fmaf(-8.0f, sxsum[pp][m], acc[pp][m][j]);
+            for (int j = 0; j < C; j++) acc[pp][m][j] = fmaf(-0x1p-21f, sxsum[pp][m], acc[pp][m][j]);
 
     stamp(c, 5);
-    // 4. block reduction (DPP row stage, then 16 rows through LDS).  Thread
-    //    (m, j) < M * 32 ends with column j of row m of every panel, so the
-    //    split-K exchange and the epilogue stay in its registers.
+    // 4. block reduction (lane exchanges within each wave, then 4 waves
+    //    through LDS).  Thread (m, j) < M * C ends with column j of row m of
+    //    every panel, so the split-K exchange and the epilogue stay in its
+    //    registers.
 #pragma unroll
     for (int pp = 0; pp < NP; pp++)
 #pragma unroll
-        for (int m = 0; m < M; m++) dpp_reduce32(acc[pp][m], &red[(pp * M + m) * 16 * 32]);
+        for (int m = 0; m < M; m++) dpp_reduce<C>(acc[pp][m], &red[(pp * M + m) * 4 * C]);
     if (g.norm) {
 #pragma unroll
         for (int m = 0; m < M; m++) {
@@ -303,40 +328,35 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
     for (int m = 0; m < M; m++)
         inv[m] = g.norm ? 1.0f / sqrtf(((scr[4 * m] + scr[4 * m + 1]) + (scr[4 * m + 2] + scr[4 * m + 3])) / (float)K + 1e-6f)
                         : 1.0f;
-    if (g.norm_plain && group == 0 && ch == 0) {
+    if (g.norm_plain && tt == 0 && ch == 0) {
         // the normed last row, for a later launch
 #pragma unroll
-        for (int i = 0; i < kEngRptMax; i++) {
+        for (int i = 0; i < R; i++) {
             const int k = k0 + tid + i * kEngThreads;
             if (i < nit && k < k1) st_dev(&g.norm_plain[k], xv[i][M - 1] * inv[M - 1]);
         }
     }
-    if (tid < M * 32) {
-        const int m = tid >> 5, j = tid & 31;
+    if (tid < M * C) {
+        const int m = tid / C, j = tid % C;
+        const int col = col0 + j;
         float y[NP];
 #pragma unroll
         for (int pp = 0; pp < NP; pp++) {
-            float r16[16];
-#pragma unroll
-            for (int r = 0; r < 16; r++) r16[r] = red[((pp * M + m) * 16 + r) * 32 + j];
-#pragma unroll
-            for (int w = 8; w >= 1; w >>= 1)
-#pragma unroll
-                for (int r = 0; r < w; r++) r16[r] += r16[r + w];
-            y[pp] = r16[0];
+            const float *rw = &red[(pp * M + m) * 4 * C + j];
+            y[pp] = (rw[0] + rw[C]) + (rw[2 * C] + rw[3 * C]);
         }
         // 5. split-K: non-owners publish partials; the owner adds them in order.
         if (ch > 0) {
 #pragma unroll
             for (int pp = 0; pp < NP; pp++)
-                put_tv(&g.part[((size_t)(ch - 1) * M + m) * N + panel[pp] * 32 + j], y[pp], tb + g.part_tag);
+                put_tv(&g.part[((size_t)(ch - 1) * M + m) * N + pp * Nout + col], y[pp], tb + g.part_tag);
             return -1;
         }
         if (g.kc > 1) {
 #pragma unroll
             for (int pp = 0; pp < NP; pp++) {
                 float pv4[4];
-                wait_strided<4>(&g.part[(size_t)m * N + panel[pp] * 32 + j], (size_t)M * N, g.kc - 1, tb + g.part_tag, pv4, c);
+                wait_strided<4>(&g.part[(size_t)m * N + pp * Nout + col], (size_t)M * N, g.kc - 1, tb + g.part_tag, pv4, c);
 #pragma unroll
                 for (int cc = 0; cc < 4; cc++)
                     if (cc < g.kc - 1) y[pp] += pv4[cc];
@@ -350,9 +370,8 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
         if (NP == 2) {
             // silu(g) * u, src/talker.rs:342-345
             const float gt = y[0], up = y[NP - 1];
-            put_tv(&g.out[(size_t)m * g.ld_out + group * 32 + j], (gt / (1.0f + expf(-gt))) * up, tb + g.out_tag);
+            put_tv(&g.out[(size_t)m * g.ld_out + col], (gt / (1.0f + expf(-gt))) * up, tb + g.out_tag);
         } else {
-            const int col = group * 32 + j;
             float v = y[0];
             if (g.bias) v += e_bias;
             if (g.epi == EEPI_RESID) {
@@ -367,7 +386,16 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
     }
     if (ch > 0) return -1;
     stamp(c, 7);
-    return group;
+    return col0;
+}
+
+template <int M, int NP>
+__device__ __forceinline__ int eng_gemv_cols(const KCONST EngGemv &g, int task, uint32_t tb, Ctl &c, float *smem) {
+    // Whole 32-column panels: narrower slices spread an op over more blocks
+    // but leave fewer blocks idle to run ahead into the next op (issuing its
+    // weight loads early), which costs more than the shorter accumulation
+    // saves on this loop.
+    return eng_gemv<M, NP, 32, eng_rows_per_thread(32, NP)>(g, task, tb, c, smem);
 }
 
 // ---------------------------------------------------------------------------
@@ -1190,14 +1218,14 @@ __global__ __launch_bounds__(kEngThreads) void k_engine(EngArgs A) {
                     const KCONST EngGemv &g = op.gemv;
                     if (g.M == 1) {
                         if (g.epi == EEPI_SWIGLU)
-                            fi = eng_gemv<1, 2>(g, t, A.tag_base, c, smem);
+                            fi = eng_gemv_cols<1, 2>(g, t, A.tag_base, c, smem);
                         else
-                            fi = eng_gemv<1, 1>(g, t, A.tag_base, c, smem);
+                            fi = eng_gemv_cols<1, 1>(g, t, A.tag_base, c, smem);
                     } else {
                         if (g.epi == EEPI_SWIGLU)
-                            fi = eng_gemv<2, 2>(g, t, A.tag_base, c, smem);
+                            fi = eng_gemv_cols<2, 2>(g, t, A.tag_base, c, smem);
                         else
-                            fi = eng_gemv<2, 1>(g, t, A.tag_base, c, smem);
+                            fi = eng_gemv_cols<2, 1>(g, t, A.tag_base, c, smem);
                     }
                     break;
                 }

@@ -44,7 +44,7 @@ __device__ float block_sum_256(float v, float *scratch /* >= 4 */) {
 template <int M, int RPT>
 __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvParams P) {
     if (P.d_done && *P.d_done) return;
-    __shared__ float red[kMaxM * 16 * 32];
+    __shared__ float red[kMaxM * 4 * 32];
     __shared__ float ybuf[kMaxM * 128];
     __shared__ float scratch[8];
     __shared__ int s_last;
@@ -140,28 +140,31 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvParams P) {
     for (int i = 0; i < RPT; i++) {
         if (i >= nit) continue;
         const float s = f16_to_f32((uint16_t)sv[i]);
-        float sx[M];
+        // sa = (scale * x) * 2^24, sb = (scale * x) * 2^20 (exact scalings;
+        // the sums carry sum(scale * x) * 2^24)
+        float sa[M], sb[M];
 #pragma unroll
         for (int m = 0; m < M; m++) {
-            sx[m] = s * xv[i][m];
-            sxsum[m] += sx[m];
+            sa[m] = s * (xv[i][m] * 16777216.0f);
+            sb[m] = sa[m] * 0.0625f;
+            sxsum[m] += sa[m];
         }
-        q4_fma_row<M>(wv[i], sx, acc);
+        const uint32_t wd[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+        q4_mix_row<M, 32>(wd, sa, sb, acc);
     }
 #pragma unroll
     for (int m = 0; m < M; m++)
 #pragma unroll
-        for (int j = 0; j < 32; j++) acc[m][j] = fmaf(-8.0f, sxsum[m], acc[m][j]);
+        for (int j = 0; j < 32; j++) acc[m][j] = fmaf(-0x1p-21f, sxsum[m], acc[m][j]);  // -8 * sum(scale * x)
 
     // 4. block reduction -> this chunk's partial for the panel's 32 columns.
 #pragma unroll
-    for (int m = 0; m < M; m++) dpp_reduce32(acc[m], &red[m * 16 * 32]);
+    for (int m = 0; m < M; m++) dpp_reduce<32>(acc[m], &red[m * 4 * 32]);
     __syncthreads();
     if (tid < M * 32) {
         const int m = tid >> 5, col = tid & 31;
-        float s = 0.0f;
-#pragma unroll
-        for (int r = 0; r < 16; r++) s += red[(m * 16 + r) * 32 + col];
+        const float *rw = &red[m * 4 * 32 + col];
+        const float s = (rw[0] + rw[32]) + (rw[64] + rw[96]);
         st_dev(&P.partial[((size_t)c * M + m) * N + p * 32 + col], s);
     }
 
