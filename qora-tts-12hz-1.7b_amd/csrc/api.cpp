@@ -437,12 +437,23 @@ struct EngProgram {
     int rot_next = 0;
     int grid = 1;
     const char *err = nullptr;  // set when an op cannot be expressed
+    // Rotation plan: ops pushed while `rot_record` is set append their
+    // rotation to it; while `rot_plan` is set they take theirs from it in
+    // order (a repeated sequence of ops then lands on the same blocks).
+    std::vector<int> *rot_record = nullptr;
+    const std::vector<int> *rot_plan = nullptr;
+    size_t plan_pos = 0;
+    std::vector<int> lds_owner;  // block -> layer whose K/V rows it keeps in LDS (-1: none)
     ~EngProgram() {
         if (d_ops) (void)hipFree(d_ops);
         if (arena) (void)hipFree(arena);
     }
     void reset_build() {
         err = nullptr;
+        rot_record = nullptr;
+        rot_plan = nullptr;
+        plan_pos = 0;
+        lds_owner.assign((size_t)grid, -1);
         ops.clear();
         used = 0;
         next_tag = 1;
@@ -454,10 +465,25 @@ struct EngProgram {
         return sizing ? nullptr : arena + off;
     }
     int tag() { return next_tag++; }
+    // The rotation the next op gets (from the plan, else the running one).
+    int next_rot() const { return rot_plan && plan_pos < rot_plan->size() ? (*rot_plan)[plan_pos] : rot_next; }
     void push(EngOp &op) {
-        op.rot = rot_next;
-        rot_next = (rot_next + op.ntasks) % grid;
+        op.rot = next_rot();
+        if (rot_plan) plan_pos++;
+        if (rot_record) rot_record->push_back(op.rot);
+        rot_next = (op.rot + op.ntasks) % grid;
         ops.push_back(op);
+    }
+    // Blocks rot .. rot+n-1 keep layer l's K/V rows in LDS: true if they
+    // are free (and are claimed) or already layer l's.
+    bool claim_lds(int rot, int n, int l) {
+        if (n > grid) return false;
+        for (int i = 0; i < n; i++) {
+            const int o = lds_owner[(size_t)((rot + i) % grid)];
+            if (o != -1 && o != l) return false;
+        }
+        for (int i = 0; i < n; i++) lds_owner[(size_t)((rot + i) % grid)] = l;
+        return true;
     }
 };
 
@@ -626,6 +652,12 @@ TvRef add_attention(EngProgram &P, const Stack &st, int l, qtts_kv *kv, int M, c
     a.pos_const = pos_const;
     a.len_const = len_const;
     a.nsplit = nsplit;
+    // A short in-launch cache (the predictor) stays in the LDS of the blocks
+    // that run this layer's steps, when those blocks serve no other layer
+    // (the caller repeats each step's rotations).
+    const bool lds_kv = !from_state && nsplit == 1 && st.hd == 128 && M * (st.nq / st.nkv) <= 4 &&
+                        kv->cap <= kEngLdsKvPos && P.claim_lds(P.next_rot(), st.nkv, l);
+    a.lds_kv = lds_kv ? 1 : 0;
     a.scale = 1.0f / sqrtf((float)st.hd);  // src/talker.rs:305
     const int qd = st.nq * st.hd;
     TvRef out{};
@@ -869,6 +901,10 @@ bool eng_talker_fits(int cap) { return (cap + kEngMaxSplit - 1) / kEngMaxSplit <
 qtts_status build_predictor_passes(EngProgram &P, qtts_predictor *p, qtts_kv *kv, const EngInput &row0,
                                    const EngInput &row1, TvRef *codes) {
     const Stack &st = p->st;
+    // Every pass repeats the first pass's rotations, so a layer's attention
+    // runs on the same blocks in all passes (its K/V rows stay in their LDS).
+    std::vector<int> rots;
+    P.rot_record = &rots;
     GemvSpec ip;
     ip.M = 2;
     ip.in[0] = row0;
@@ -882,7 +918,10 @@ qtts_status build_predictor_passes(EngProgram &P, qtts_predictor *p, qtts_kv *kv
     hd.in[0] = in_tv(x, 1);
     TvRef lg = add_gemv(P, p->heads[0], hd);
     codes[0] = add_argmax(P, lg, p->vocab, 1);
+    P.rot_record = nullptr;
     for (int g = 1; g < p->groups; g++) {
+        P.rot_plan = &rots;
+        P.plan_pos = 0;
         GemvSpec e;
         e.in[0] = in_embed(p->emb[g - 1], codes[g - 1]);
         e.bias = p->bias;
@@ -891,6 +930,7 @@ qtts_status build_predictor_passes(EngProgram &P, qtts_predictor *p, qtts_kv *kv
         hd.in[0] = in_tv(x, 0);
         lg = add_gemv(P, p->heads[g], hd);
         codes[g] = add_argmax(P, lg, p->vocab, g + 1);
+        P.rot_plan = nullptr;
     }
     return QTTS_OK;
 }

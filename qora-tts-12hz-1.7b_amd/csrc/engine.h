@@ -33,6 +33,7 @@ constexpr int kEngMaxM = 2;    // rows per GEMV (the predictor's 2-token prefill
 constexpr uint32_t kTagStride = 8192;  // tags reserved per launch
 constexpr int kEngMaxSplit = 32;
 constexpr int kEngSmemFloats = 10240;
+constexpr int kEngLdsKvPos = 32;  // positions of an LDS-resident K/V cache (one kv head)
 
 enum EngOpKind : int { EOP_GEMV = 1, EOP_ATTN = 2, EOP_COMBINE = 3, EOP_ARGMAX = 4, EOP_SAMPLE = 5, EOP_EMBSUM = 6 };
 enum EngIn : int { EIN_TV = 0, EIN_PLAIN = 1, EIN_EMBED = 2 };
@@ -82,6 +83,9 @@ struct EngAttn {
     int from_state;          // position / cache length from the frame state (talker)
     int pos_const, len_const;
     int nsplit;
+    int lds_kv;              // cached rows of this launch live in the block's LDS: every step
+                             // of this layer runs task h on the same block (the host pins the
+                             // rotation), which keeps kv head h's rows [0, len) there
     float scale;
     tv_t *part;  // nsplit > 1: [M][nq][nsplit][hd + 2]
     int part_tag;

@@ -713,8 +713,159 @@ __device__ __forceinline__ int eng_attn_t(const KCONST EngAttn &a, int task, uin
     return task;
 }
 
+// ---------------------------------------------------------------------------
+// Short in-launch attention (the predictor: <= 32 positions, one kv head
+// per task).  Every step of a layer runs task h on the same block, so the
+// rows of kv head h appended by earlier steps of this launch are in that
+// block's LDS (lds_kv), and one wave per (row, q head) works without a block
+// barrier.  Lane l holds dims 2l, 2l+1 of every vector; RoPE pairs
+// (d, d+64) sit 32 lanes apart (v_permlane32_swap).  Scores are reduced over
+// the wave by lane exchanges, softmax runs across lanes (one position each)
+// and P.V takes the probabilities by readlane.  Same arithmetic as
+// eng_attn_t: QK-norm (src/talker.rs:86-99), split-half RoPE
+// (src/rope.rs:79-92), softmax(q.K^T*scale).V with the sum divided out at
+// the end (src/talker.rs:304-331), causal across the M new rows.  The rows
+// are also written to the device cache, for the host.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ int eng_attn_lean(const KCONST EngAttn &a, int task, uint32_t tb, Ctl &c, float *smem,
+                                             float *kvl) {
+    constexpr int HD = 128, HALF = 64, NP = kEngLdsKvPos;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches below
+    const int G = a.nq / a.nkv;
+    const int M = a.M;
+    if (wave >= M * G) return task;
+    const int m = wave / G, gq = wave - m * G, kvh = task, h = kvh * G + gq;
+    const int base = a.len_const, pos0 = a.pos_const;
+    const int nvis = base + m + 1;  // positions row m attends to
+    const int d0 = 2 * lane;        // this lane's dims d0, d0 + 1
+    const int i0 = d0 & (HALF - 1);  // their RoPE table index
+    float *Kl = kvl + d0, *Vl = kvl + NP * HD + d0;  // row t of this lane: Kl[t * HD]
+
+    // 0. step-independent inputs: gammas, RoPE rows
+    const uint32_t gqb = glb(reinterpret_cast<const uint32_t *>(a.q_norm))[lane];
+    const uint32_t gkb = glb(reinterpret_cast<const uint32_t *>(a.k_norm))[lane];
+    float rc[kEngMaxM][2], rs[kEngMaxM][2];
+#pragma unroll
+    for (int r = 0; r < kEngMaxM; r++) {
+        const int pos = pos0 + r;
+        rc[r][0] = rc[r][1] = 1.0f;
+        rs[r][0] = rs[r][1] = 0.0f;
+        if (r < M && !(a.rope_skip_oob && pos >= a.rope_rows)) {
+            const uint64_t cb = glb(reinterpret_cast<const uint64_t *>(a.rope_cos + (size_t)pos * HALF + i0))[0];
+            const uint64_t sb = glb(reinterpret_cast<const uint64_t *>(a.rope_sin + (size_t)pos * HALF + i0))[0];
+            rc[r][0] = __uint_as_float((uint32_t)cb);
+            rc[r][1] = __uint_as_float((uint32_t)(cb >> 32));
+            rs[r][0] = __uint_as_float((uint32_t)sb);
+            rs[r][1] = __uint_as_float((uint32_t)(sb >> 32));
+        }
+    }
+    stamp(c, 2);
+
+    // 1. raw q of (row m, head h), k and v of the M new rows
+    constexpr int NW = 2 + 4 * kEngMaxM;
+    const tv_t *ptr[NW];
+    uint32_t tg[NW];
+    float val[NW];
+    const size_t qoff = (size_t)h * HD + d0, koff = (size_t)(a.nq + kvh) * HD + d0,
+                 voff = (size_t)(a.nq + a.nkv + kvh) * HD + d0;
+#pragma unroll
+    for (int i = 0; i < NW; i++) {
+        tg[i] = tb + a.qkv_tag;
+        ptr[i] = a.qkv;
+    }
+    ptr[0] = &a.qkv[(size_t)m * a.ld_qkv + qoff];
+    ptr[1] = ptr[0] + 1;
+#pragma unroll
+    for (int r = 0; r < kEngMaxM; r++) {
+        if (r >= M) continue;
+        ptr[2 + 4 * r] = &a.qkv[(size_t)r * a.ld_qkv + koff];
+        ptr[3 + 4 * r] = ptr[2 + 4 * r] + 1;
+        ptr[4 + 4 * r] = &a.qkv[(size_t)r * a.ld_qkv + voff];
+        ptr[5 + 4 * r] = ptr[4 + 4 * r] + 1;
+    }
+    wait_list<NW>(ptr, tg, 2 + 4 * M, val, c);
+    stamp(c, 3);
+
+    // 2. QK-norm + RoPE of q and of the new k rows
+    const float gq0 = f16_to_f32((uint16_t)gqb), gq1 = f16_to_f32((uint16_t)(gqb >> 16));
+    const float gk0 = f16_to_f32((uint16_t)gkb), gk1 = f16_to_f32((uint16_t)(gkb >> 16));
+    // the first half (dims < 64) rotates as x c - x' s, the second as x c + x' s
+    const float sgn = lane < 32 ? -1.0f : 1.0f;
+    auto norm_rope = [&](float x0, float x1, float g0, float g1, int r, float &o0, float &o1) {
+        const float inv = 1.0f / sqrtf(wave_sum(x0 * x0 + x1 * x1) / (float)HD + 1e-6f);
+        const float n0 = x0 * inv * g0, n1 = x1 * inv * g1;
+        const auto p0 = __builtin_amdgcn_permlane32_swap(__float_as_uint(n0), __float_as_uint(n0), false, false);
+        const auto p1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(n1), __float_as_uint(n1), false, false);
+        // the value 32 lanes away: lanes < 32 get it in [1], lanes >= 32 in [0]
+        const float q0 = __uint_as_float(lane < 32 ? p0[1] : p0[0]), q1 = __uint_as_float(lane < 32 ? p1[1] : p1[0]);
+        const int ri = r == 0 ? 0 : kEngMaxM - 1;
+        o0 = n0 * rc[ri][0] + sgn * (q0 * rs[ri][0]);
+        o1 = n1 * rc[ri][1] + sgn * (q1 * rs[ri][1]);
+    };
+    float qn0, qn1;
+    norm_rope(val[0], val[1], gq0, gq1, m, qn0, qn1);
+    // 3. append the new rows (src/talker.rs:299-302) to the block's LDS,
+    //    where this step reads them too (every wave of the task writes the
+    //    same values before reading), and to the device cache
+#pragma unroll
+    for (int r = 0; r < kEngMaxM; r++) {
+        if (r >= M) continue;
+        float k0, k1;
+        norm_rope(val[2 + 4 * r], val[3 + 4 * r], gk0, gk1, r, k0, k1);
+        const float v0 = val[4 + 4 * r], v1 = val[5 + 4 * r];
+        const int t = base + r;
+        *reinterpret_cast<float2 *>(&Kl[t * HD]) = make_float2(k0, k1);
+        *reinterpret_cast<float2 *>(&Vl[t * HD]) = make_float2(v0, v1);
+        st_dev_u64(reinterpret_cast<uint64_t *>(a.kcache + ((size_t)kvh * a.kv_cap + t) * HD + d0),
+                   ((uint64_t)__float_as_uint(k1) << 32) | __float_as_uint(k0));
+        st_dev_u64(reinterpret_cast<uint64_t *>(a.vcache + ((size_t)kvh * a.kv_cap + t) * HD + d0),
+                   ((uint64_t)__float_as_uint(v1) << 32) | __float_as_uint(v0));
+    }
+    stamp(c, 4);
+
+    // 4. scores over positions t < nvis, reduced over the wave into
+    //    red[wave][t]
+    //    (all NP rows are read at once, so the reads are not serialised
+    //    behind branches; columns past nvis hold stale or uninitialised rows
+    //    and are masked in the softmax -- the reduction keeps columns apart)
+    float2 kr[NP];
+#pragma unroll
+    for (int t = 0; t < NP; t++) kr[t] = *reinterpret_cast<const float2 *>(&Kl[t * HD]);
+    float part[NP];
+#pragma unroll
+    for (int t = 0; t < NP; t++) part[t] = qn0 * kr[t].x + qn1 * kr[t].y;
+    float *red = smem;  // [4 waves][NP]
+    dpp_reduce<NP>(part, red);
+    // 5. softmax across lanes, position t on lane t
+    const float sc = lane < nvis ? red[wave * NP + lane] * a.scale : -INFINITY;
+    const float mx = wave_max(sc);
+    const float e = lane < nvis ? expf(sc - mx) : 0.0f;
+    const float l = wave_sum(e);
+    stamp(c, 5);
+    // 6. P.V
+    float2 vr[NP];
+#pragma unroll
+    for (int t = 0; t < NP; t++) vr[t] = *reinterpret_cast<const float2 *>(&Vl[t * HD]);
+    float o0 = 0.0f, o1 = 0.0f;
+#pragma unroll
+    for (int t = 0; t < NP; t++) {
+        if (t < nvis) {  // uniform
+            const float pt = lane_f(e, t);
+            o0 += pt * vr[t].x;
+            o1 += pt * vr[t].y;
+        }
+    }
+    tv_t *dst = &a.out[(size_t)m * a.nq * HD + (size_t)h * HD + d0];
+    put_tv(dst, o0 / l, tb + a.out_tag);
+    put_tv(dst + 1, o1 / l, tb + a.out_tag);
+    stamp(c, 6);
+    return task;
+}
+
 __device__ __forceinline__ int eng_attn(const KCONST EngAttn &a, int task, uint32_t tb, const EngState &st, Ctl &c,
-                                        float *smem) {
+                                        float *smem, float *kvl) {
+    if (a.lds_kv) return eng_attn_lean(a, task, tb, c, smem, kvl);
     const int npi = a.M * (a.nq / a.nkv);
     const int Lt = (a.from_state ? st.kvlen : a.len_const) + a.M;
     const bool small = (Lt + a.nsplit - 1) / a.nsplit <= 32;
@@ -1189,6 +1340,7 @@ __device__ __forceinline__ int eng_embsum(const KCONST EngEmbSum &E, int task, u
 
 __global__ __launch_bounds__(kEngThreads) void k_engine(EngArgs A) {
     __shared__ __align__(16) float smem[kEngSmemFloats];
+    __shared__ __align__(16) float kvl[2 * kEngLdsKvPos * 128];  // lds_kv attention: this block's K/V rows
     __shared__ int s_bad;  // set by a thread that saw the abort word or timed out
     if (ld_dev_i32(A.done)) return;
     if (threadIdx.x == 0) s_bad = 0;
@@ -1229,7 +1381,7 @@ __global__ __launch_bounds__(kEngThreads) void k_engine(EngArgs A) {
                     }
                     break;
                 }
-                case EOP_ATTN: fi = eng_attn(op.attn, t, A.tag_base, st, c, smem); break;
+                case EOP_ATTN: fi = eng_attn(op.attn, t, A.tag_base, st, c, smem, kvl); break;
                 case EOP_COMBINE: fi = eng_combine(op.comb, t, A.tag_base, c, smem); break;
                 case EOP_ARGMAX: eng_argmax(op.amax, A.tag_base, st, c, A.codes, A.max_codes, smem); break;
                 case EOP_SAMPLE: eng_sample(op.samp, A.tag_base, st, A.st_out, c, A.codes, A.max_codes, smem); break;

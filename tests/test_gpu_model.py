@@ -120,6 +120,25 @@ def test_predictor_tiny(tiny):
         assert np.array_equal(p.get_acoustic_embeddings_sum(got), op.get_acoustic_embeddings_sum(ref))
 
 
+@pytest.mark.parametrize("capacity", [16, 40])
+def test_predictor_cache_paths(tiny, capacity):
+    """Both predictor attention paths: cached rows kept in the LDS of the
+    blocks that run the layer (capacity <= 32) and rows read back from the
+    device cache (larger capacity).  Codes match, and so does the cache the
+    call leaves for the host."""
+    tw, pw, t, p, ot, op = tiny
+    for i in range(3):
+        h = qtts.synth_normal_f32(31, f"pc.{i}", tw.cfg.hidden)
+        sem = ot.embed_codec_token(50 + i)
+        kv, okv = p.new_kv(capacity), op.new_kv(capacity)
+        got = p.generate_acoustic_codes(h, sem, kv)
+        ref = op.generate_acoustic_codes(h, sem, okv)
+        assert np.array_equal(got, ref), (got, ref)
+        (gk, gv), (rk, rv) = kv.store(), okv.store()
+        assert gk.shape == rk.shape
+        assert rel_err(gk, rk) < REL_TOL and rel_err(gv, rv) < REL_TOL
+
+
 def test_predictor_full(full):
     tw, pw, t, p, ot, op = full
     for i in range(3):
