@@ -53,6 +53,11 @@ struct qtts_ctx {
     uint64_t *eng_trace = nullptr;  // QTTS_ENGINE_TRACE: per-op block timestamps
     size_t eng_trace_cap = 0;
     long long eng_launches = 0;
+    // MFMA GEMM scratch: the rows split into binary16 hi/lo, and K-chunk partials
+    _Float16 *mfma_x = nullptr;
+    size_t mfma_x_cap = 0;
+    float *mfma_part = nullptr;
+    size_t mfma_part_cap = 0;
     // The context and every object made from it hold one reference each, so
     // objects may be freed after qtts_ctx_destroy (e.g. in any order at
     // interpreter shutdown).
@@ -79,6 +84,8 @@ void ctx_release(qtts_ctx *c) {
     (void)hipFree(c->eng_state);
     (void)hipFree(c->eng_done);
     (void)hipFree(c->eng_trace);
+    (void)hipFree(c->mfma_x);
+    (void)hipFree(c->mfma_part);
     if (c->stream) (void)hipStreamDestroy(c->stream);
     delete c;
 }
@@ -90,6 +97,8 @@ struct qtts_q4 {
     DevQ4 d{};
     void *mem = nullptr;
     size_t bytes = 0;
+    DevQ4Mfma m{};  // MFMA operand copy, made by the first GEMM of >= 8 rows
+    void *mfma_mem = nullptr;
 };
 
 // Serial numbers identify caches and predictors in the engine's program
@@ -289,6 +298,70 @@ qtts_status run_gemv(qtts_ctx *c, const GemvParams &p) {
     if (p.M < 1 || p.M > kMaxM) return fail(c, QTTS_EINVAL, "GEMV rows per launch out of range");
     launch_gemv(c->stream, p);
     return check_launch(c, "k_gemv");
+}
+
+// The MFMA operand copy of a panel-major weight (one allocation at *mem).
+qtts_status make_mfma_copy(qtts_ctx *c, const DevQ4 &w, void **mem, DevQ4Mfma *m) {
+    if (w.K % 16 != 0 || w.N % 32 != 0) return fail(c, QTTS_ESHAPE, "MFMA GEMM needs K % 16 == 0 and N % 32 == 0");
+    const size_t nw = (size_t)(w.N / 32) * (w.K / 16) * 64, ns = (size_t)(w.N / 32) * w.K;
+    const size_t bytes = nw * 4 + 2 * ns * 2;
+    HIP_TRY(c, hipMalloc(mem, bytes));
+    m->wm = reinterpret_cast<uint32_t *>(*mem);
+    m->sa = reinterpret_cast<uint16_t *>((uint8_t *)*mem + nw * 4);
+    m->sb = m->sa + ns;
+    m->K = w.K;
+    m->N = w.N;
+    launch_repack_mfma(c->stream, w, const_cast<uint32_t *>(m->wm), const_cast<uint16_t *>(m->sa),
+                       const_cast<uint16_t *>(m->sb));
+    return check_launch(c, "k_repack_mfma");
+}
+
+template <class T>
+qtts_status grow(qtts_ctx *c, T **buf, size_t *cap, size_t need) {
+    if (*cap >= need) return QTTS_OK;
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    (void)hipFree(*buf);
+    *buf = nullptr;
+    *cap = 0;
+    HIP_TRY(c, hipMalloc(buf, need * sizeof(T)));
+    *cap = need;
+    return QTTS_OK;
+}
+
+// y[m] (+)= x[m] . W (+ bias) for M rows on the matrix cores (csrc/mfma.hip),
+// 64 rows per pass: split the rows into binary16 hi/lo, one block per
+// (panel, K chunk) with chunks sized to give ~2 blocks per CU, then sum the
+// chunks.
+qtts_status run_gemm_mfma(qtts_ctx *c, const DevQ4Mfma &w, const float *x, int M, int ldx, float *y, int ldy,
+                          const float *bias, bool accumulate) {
+    const int K = w.K, N = w.N, Ks = K / 16, panels = N / 32;
+    for (int r0 = 0; r0 < M; r0 += 64) {
+        const int Mc = M - r0 < 64 ? M - r0 : 64;
+        const int mt = Mc > 32 ? 2 : 1, Mpad = 32 * mt;
+        int kc = (512 + panels - 1) / panels;
+        if (kc > Ks / 16) kc = Ks / 16;  // >= 4 steps per wave
+        if (kc < 1) kc = 1;
+        int steps = (Ks + kc - 1) / kc;
+        steps = (steps + 3) / 4 * 4;
+        kc = (Ks + steps - 1) / steps;
+        QTTS_TRY(grow(c, &c->mfma_x, &c->mfma_x_cap, (size_t)2 * Mpad * K));
+        QTTS_TRY(grow(c, &c->mfma_part, &c->mfma_part_cap, (size_t)kc * Mpad * N));
+        _Float16 *xh = c->mfma_x, *xl = c->mfma_x + (size_t)Mpad * K;
+        launch_split_x(c->stream, x + (size_t)r0 * ldx, Mc, ldx, K, Mpad, xh, xl);
+        QTTS_TRY(check_launch(c, "k_split_x"));
+        GemmMfmaParams p{};
+        p.w = w;
+        p.xh = xh;
+        p.xl = xl;
+        p.steps = steps;
+        p.part = c->mfma_part;
+        launch_gemm_mfma(c->stream, p, mt, kc);
+        QTTS_TRY(check_launch(c, "k_gemm_mfma"));
+        launch_gemm_reduce(c->stream, c->mfma_part, kc, Mc, Mpad, N, bias, y + (size_t)r0 * ldy, ldy,
+                           accumulate ? 1 : 0);
+        QTTS_TRY(check_launch(c, "k_gemm_reduce"));
+    }
+    return QTTS_OK;
 }
 
 int attn_nsplit(int cap, int min_split) {
@@ -1030,6 +1103,7 @@ void qtts_q4_free(qtts_q4 *w) {
     qtts_ctx *c = w->ctx;
     if (c && c->stream) (void)hipStreamSynchronize(c->stream);
     (void)hipFree(w->mem);
+    (void)hipFree(w->mfma_mem);
     delete w;
     if (c) ctx_release(c);
 }
@@ -1039,6 +1113,11 @@ size_t qtts_q4_bytes(const qtts_q4 *w) { return w ? w->bytes : 0; }
 qtts_status qtts_gemm_device(qtts_ctx *c, const qtts_q4 *w, const float *d_x, int32_t seq_len, float *d_out) {
     if (!c || !w || !d_x || !d_out) return QTTS_EINVAL;
     if (seq_len < 1) return fail(c, QTTS_EINVAL, "seq_len < 1");
+    if (seq_len >= kMfmaMinRows && w->d.K % 16 == 0) {
+        qtts_q4 *mw = const_cast<qtts_q4 *>(w);
+        if (!mw->mfma_mem) QTTS_TRY(make_mfma_copy(c, w->d, &mw->mfma_mem, &mw->m));
+        return run_gemm_mfma(c, w->m, d_x, seq_len, w->d.K, d_out, w->d.N, nullptr, false);
+    }
     for (int r0 = 0; r0 < seq_len; r0 += kMaxM) {
         const int M = seq_len - r0 < kMaxM ? seq_len - r0 : kMaxM;
         GemvParams p = gemv_base(c, w->d, M);

@@ -25,8 +25,30 @@ struct DevQ4 {
     int N;  // output columns (multiple of 32); panels = N / 32
 };
 
+// The same weight in the MFMA B-operand order (csrc/mfma.hip), made on
+// first use by a GEMM of >= 8 rows:
+//   wm[(p * K/16 + s) * 64 + l]: panel p, 16-row step s, lane l: column
+//     32p + l%32, rows 16s + 8(l/32) + i (i < 8), nibble i at bits
+//     4*(i/2) + 16*(i%2) -- rows 2j and 2j+1 are the two halves of
+//     (word >> 4j) & 0x000F000F;
+//   sa[p*K + k], sb[p*K + k]: the row's binary16 scale split exactly into
+//     its top 7 and low 4 significand bits (s = sa + sb).
+struct DevQ4Mfma {
+    const uint32_t *wm;
+    const uint16_t *sa, *sb;
+    int K, N;
+};
+
+struct GemmMfmaParams {
+    DevQ4Mfma w;
+    const _Float16 *xh, *xl;  // [32 * MT][K]: the rows split into binary16 hi + lo
+    int steps;                // 16-row steps per K chunk (a multiple of 4)
+    float *part;              // [kc][32 * MT][N]
+};
+
 constexpr int kGemvThreads = 256;
 constexpr int kMaxM = 4;          // rows per GEMV launch (prefill chunks)
+constexpr int kMfmaMinRows = 8;   // GEMMs of at least this many rows run on the matrix cores
 constexpr int kMaxGroups = 15;    // predictor code groups
 constexpr int kAttnThreads = 256;
 constexpr int kAttnMaxChunk = 256;  // positions per attention split block
@@ -167,6 +189,11 @@ void launch_gemv(hipStream_t st, const GemvParams &p);
 void launch_attention(hipStream_t st, const AttnParams &p, int M);
 void launch_sample(hipStream_t st, const SampleParams &p);
 void launch_embed_row(hipStream_t st, const DevQ4 &w, const uint32_t *d_token, float *out, const int *d_done);
+void launch_repack_mfma(hipStream_t st, const DevQ4 &w, uint32_t *wm, uint16_t *sa, uint16_t *sb);
+void launch_split_x(hipStream_t st, const float *x, int M, int ldx, int K, int Mpad, _Float16 *xh, _Float16 *xl);
+void launch_gemm_mfma(hipStream_t st, const GemmMfmaParams &p, int mt, int kc);
+void launch_gemm_reduce(hipStream_t st, const float *part, int kc, int M, int Mpad, int N, const float *bias, float *y,
+                        int ldy, int accumulate);
 void launch_embed_sum(hipStream_t st, const EmbSumParams &p);
 void launch_advance(hipStream_t st, LoopState *s, int frame_step);
 void launch_repack_q4(hipStream_t st, const uint8_t *packed, const uint16_t *scales, int K, int N, int col0,

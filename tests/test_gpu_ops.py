@@ -76,6 +76,44 @@ def test_gemm_rows(ctx, rows):
     assert rel_err(y, ref) < GEMV_TIGHT
 
 
+@pytest.mark.parametrize("K,N", GEMV_SHAPES)
+@pytest.mark.parametrize("rows", [8, 33, 64, 100])
+def test_gemm_mfma_config1_shapes(ctx, K, N, rows):
+    """GEMMs of >= 8 rows run on the matrix cores (binary16 hi/lo operands,
+    f32 accumulation): within GEMV_TIGHT of the oracle and of float64."""
+    w = qtts.Q4Weight.synthetic(15, f"mfma.{K}x{N}", K, N)
+    x = qtts.synth_normal_f32(15, f"mfma.x.{K}.{rows}", rows * K)
+    d = qtts.DeviceQ4(ctx, w)
+    y = d.gemm(x, rows).reshape(rows, N)
+    ref = oracle.gemm(x, rows, w, nthreads=1).reshape(rows, N)
+    exact = x.reshape(rows, K).astype(np.float64) @ w.dequantize().astype(np.float64)
+    e1, e2 = rel_err(y, ref), rel_err(y, exact)
+    print(f"{rows}x{K}->{N}: rel err vs oracle {e1:.2e}, vs f64 {e2:.2e}")
+    assert e1 < GEMV_TIGHT and e2 < GEMV_TIGHT
+    # every row on its own, not just the largest
+    for m in (0, rows // 2, rows - 1):
+        assert rel_err(y[m], exact[m]) < GEMV_TIGHT
+
+
+def test_gemm_mfma_one_hot_rows_are_dequantized_rows(ctx):
+    """With one-hot rows each output row is one weight row, bit for bit: the
+    scale split s = sa + sb and the binary16 products are exact, including
+    binary16 subnormal and zero scales."""
+    K, N, rows = 2048, 4096, 16
+    w = qtts.Q4Weight.synthetic(16, "mfma.onehot", K, N)
+    w.scales[3, :8] = np.array([1, 2, 3, 0x3FF, 0x200, 0, 0x7B, 0x3FF], dtype=np.uint16)
+    w.scales[700, 5] = 0
+    d = qtts.DeviceQ4(ctx, w)
+    deq = w.dequantize()
+    ks = [0, 3, 700, 2047, 5, 17, 1024, 1500, 9, 3, 700, 64, 65, 2000, 1, 999]
+    x = np.zeros((rows, K), dtype=np.float32)
+    for m, k in enumerate(ks):
+        x[m, k] = 1.0
+    y = d.gemm(x.reshape(-1), rows).reshape(rows, N)
+    for m, k in enumerate(ks):
+        assert np.array_equal(y[m], deq[k]), f"row {m} (k = {k})"
+
+
 def test_gemv_linearity(ctx):
     """gemv(a*x1 + x2) == a*gemv(x1) + gemv(x2) to f32 accuracy."""
     K, N = 6144, 2048
