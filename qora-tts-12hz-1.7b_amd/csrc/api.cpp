@@ -7,6 +7,7 @@
 #include <cmath>
 #include <cstdio>
 #include <cstdlib>
+#include <algorithm>
 #include <atomic>
 #include <cstring>
 #include <functional>
@@ -99,6 +100,7 @@ struct qtts_q4 {
     size_t bytes = 0;
     DevQ4Mfma m{};  // MFMA operand copy, made by the first GEMM of >= 8 rows
     void *mfma_mem = nullptr;
+    int mfma_state = 0;  // 0 not tried, 1 made, -1 the weight stays on the VALU path
 };
 
 // Serial numbers identify caches and predictors in the engine's program
@@ -301,19 +303,36 @@ qtts_status run_gemv(qtts_ctx *c, const GemvParams &p) {
 }
 
 // The MFMA operand copy of a panel-major weight (one allocation at *mem).
-qtts_status make_mfma_copy(qtts_ctx *c, const DevQ4 &w, void **mem, DevQ4Mfma *m) {
-    if (w.K % 16 != 0 || w.N % 32 != 0) return fail(c, QTTS_ESHAPE, "MFMA GEMM needs K % 16 == 0 and N % 32 == 0");
+// *ok is false (and *mem null) for a weight the matrix-core path cannot take
+// exactly: a shape off the 16 x 32 grid, K above the row prologue's limit,
+// or a scale above 8188 in magnitude.  Synchronises the stream.
+qtts_status make_mfma_copy(qtts_ctx *c, const DevQ4 &w, void **mem, DevQ4Mfma *m, bool *ok) {
+    *mem = nullptr;
+    *ok = false;
+    if (w.K % 16 != 0 || w.N % 32 != 0 || w.K > kMfmaRowsMaxK) return QTTS_OK;
     const size_t nw = (size_t)(w.N / 32) * (w.K / 16) * 64, ns = (size_t)(w.N / 32) * w.K;
-    const size_t bytes = nw * 4 + 2 * ns * 2;
-    HIP_TRY(c, hipMalloc(mem, bytes));
+    const size_t flag_off = (nw * 4 + 2 * ns * 2 + 255) / 256 * 256;
+    HIP_TRY(c, hipMalloc(mem, flag_off + 256));
     m->wm = reinterpret_cast<uint32_t *>(*mem);
     m->sa = reinterpret_cast<uint16_t *>((uint8_t *)*mem + nw * 4);
     m->sb = m->sa + ns;
     m->K = w.K;
     m->N = w.N;
+    int *flag = reinterpret_cast<int *>((uint8_t *)*mem + flag_off);
+    HIP_TRY(c, hipMemsetAsync(flag, 0, sizeof(int), c->stream));
     launch_repack_mfma(c->stream, w, const_cast<uint32_t *>(m->wm), const_cast<uint16_t *>(m->sa),
-                       const_cast<uint16_t *>(m->sb));
-    return check_launch(c, "k_repack_mfma");
+                       const_cast<uint16_t *>(m->sb), flag);
+    QTTS_TRY(check_launch(c, "k_repack_mfma"));
+    int too_large = 0;
+    HIP_TRY(c, hipMemcpyAsync(&too_large, flag, sizeof(int), hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(c, hipStreamSynchronize(c->stream));
+    if (too_large) {
+        (void)hipFree(*mem);
+        *mem = nullptr;
+        return QTTS_OK;
+    }
+    *ok = true;
+    return QTTS_OK;
 }
 
 template <class T>
@@ -328,38 +347,53 @@ qtts_status grow(qtts_ctx *c, T **buf, size_t *cap, size_t need) {
     return QTTS_OK;
 }
 
-// y[m] (+)= x[m] . W (+ bias) for M rows on the matrix cores (csrc/mfma.hip),
-// 64 rows per pass: split the rows into binary16 hi/lo, one block per
-// (panel, K chunk) with chunks sized to give ~2 blocks per CU, then sum the
-// chunks.
-qtts_status run_gemm_mfma(qtts_ctx *c, const DevQ4Mfma &w, const float *x, int M, int ldx, float *y, int ldy,
-                          const float *bias, bool accumulate) {
+// y[m] (+)= f(x[m]) . W (+ bias) for M rows on the matrix cores
+// (csrc/mfma.hip), f the row prologue (MfmaRowsMode), 64 rows per pass: the
+// prologue and binary16 split, then one block per (panel, K chunk) of
+// 4 * sw 16-row steps, and the last block of a panel sums its chunks.  sw is
+// 8 (each wave keeps 8 steps of operand loads in flight; measured fastest at
+// every talker shape, 64 rows) unless K is short.
+qtts_status run_gemm_mfma(qtts_ctx *c, const DevQ4Mfma &w, const float *x, int M, int ldx, int mode,
+                          const uint16_t *gamma, float *y, int ldy, const float *bias, bool accumulate) {
     const int K = w.K, N = w.N, Ks = K / 16, panels = N / 32;
+    if (K % 16 || N % 32 || K > kMfmaRowsMaxK || (mode == MFMA_ROWS_RMSNORM && (K % 4 || ldx % 4)))
+        return fail(c, QTTS_ESHAPE, "MFMA GEMM: unsupported shape");
+    if (panels > kCounters) return fail(c, QTTS_ESHAPE, "MFMA GEMM: more panels than counters");
+    int sw = 8;
+    while (sw > 1 && 4 * (sw / 2) >= Ks) sw /= 2;
+    const int kc = (Ks + 4 * sw - 1) / (4 * sw);
     for (int r0 = 0; r0 < M; r0 += 64) {
         const int Mc = M - r0 < 64 ? M - r0 : 64;
         const int mt = Mc > 32 ? 2 : 1, Mpad = 32 * mt;
-        int kc = (512 + panels - 1) / panels;
-        if (kc > Ks / 16) kc = Ks / 16;  // >= 4 steps per wave
-        if (kc < 1) kc = 1;
-        int steps = (Ks + kc - 1) / kc;
-        steps = (steps + 3) / 4 * 4;
-        kc = (Ks + steps - 1) / steps;
-        QTTS_TRY(grow(c, &c->mfma_x, &c->mfma_x_cap, (size_t)2 * Mpad * K));
-        QTTS_TRY(grow(c, &c->mfma_part, &c->mfma_part_cap, (size_t)kc * Mpad * N));
-        _Float16 *xh = c->mfma_x, *xl = c->mfma_x + (size_t)Mpad * K;
-        launch_split_x(c->stream, x + (size_t)r0 * ldx, Mc, ldx, K, Mpad, xh, xl);
-        QTTS_TRY(check_launch(c, "k_split_x"));
+        QTTS_TRY(grow(c, &c->mfma_x, &c->mfma_x_cap, (size_t)2 * 64 * K + 2 * 64));
+        if (kc > 1) QTTS_TRY(grow(c, &c->mfma_part, &c->mfma_part_cap, (size_t)kc * Mpad * N));
+        MfmaRowsParams r{};
+        r.x = x + (size_t)r0 * ldx;
+        r.ldx = ldx;
+        r.K = K;
+        r.M = Mc;
+        r.Mpad = Mpad;
+        r.mode = mode;
+        r.gamma = gamma;
+        r.xh = c->mfma_x;
+        r.xl = c->mfma_x + (size_t)Mpad * K;
+        r.rexp = reinterpret_cast<int *>(c->mfma_x + (size_t)2 * 64 * K);
+        launch_mfma_rows(c->stream, r);
+        QTTS_TRY(check_launch(c, "k_mfma_rows"));
         GemmMfmaParams p{};
         p.w = w;
-        p.xh = xh;
-        p.xl = xl;
-        p.steps = steps;
+        p.xh = r.xh;
+        p.xl = r.xl;
+        p.rexp = r.rexp;
+        p.M = Mc;
         p.part = c->mfma_part;
-        launch_gemm_mfma(c->stream, p, mt, kc);
+        p.counters = c->counters;
+        p.bias = bias;
+        p.y = y + (size_t)r0 * ldy;
+        p.ldy = ldy;
+        p.accumulate = accumulate ? 1 : 0;
+        launch_gemm_mfma(c->stream, p, mt, sw, kc);
         QTTS_TRY(check_launch(c, "k_gemm_mfma"));
-        launch_gemm_reduce(c->stream, c->mfma_part, kc, Mc, Mpad, N, bias, y + (size_t)r0 * ldy, ldy,
-                           accumulate ? 1 : 0);
-        QTTS_TRY(check_launch(c, "k_gemm_reduce"));
     }
     return QTTS_OK;
 }
@@ -574,9 +608,13 @@ struct qtts_talker {
     float *x = nullptr, *q = nullptr, *attn = nullptr, *h = nullptr, *out = nullptr;
     LoopState *state = nullptr;
     // prefill work buffers
-    float *xp = nullptr, *qp = nullptr, *ap = nullptr, *hp = nullptr;
+    float *xp = nullptr, *qp = nullptr, *ap = nullptr, *hp = nullptr, *rawp = nullptr;
     int prefill_cap = 0;
     std::vector<void *> prefill_bufs;
+    // MFMA operand copies of the layer weights (qkv, o, gu, down per layer),
+    // made by the first prefill of >= kMfmaMinRows rows
+    std::vector<DevQ4Mfma> mfma;
+    int mfma_state = 0;  // 0 not tried, 1 made, -1 some weight cannot use the matrix cores
     // loop buffers
     uint32_t *codes = nullptr;
     size_t codes_cap = 0;
@@ -1113,10 +1151,16 @@ size_t qtts_q4_bytes(const qtts_q4 *w) { return w ? w->bytes : 0; }
 qtts_status qtts_gemm_device(qtts_ctx *c, const qtts_q4 *w, const float *d_x, int32_t seq_len, float *d_out) {
     if (!c || !w || !d_x || !d_out) return QTTS_EINVAL;
     if (seq_len < 1) return fail(c, QTTS_EINVAL, "seq_len < 1");
-    if (seq_len >= kMfmaMinRows && w->d.K % 16 == 0) {
+    if (seq_len >= kMfmaMinRows) {
         qtts_q4 *mw = const_cast<qtts_q4 *>(w);
-        if (!mw->mfma_mem) QTTS_TRY(make_mfma_copy(c, w->d, &mw->mfma_mem, &mw->m));
-        return run_gemm_mfma(c, w->m, d_x, seq_len, w->d.K, d_out, w->d.N, nullptr, false);
+        if (mw->mfma_state == 0) {
+            bool ok = false;
+            QTTS_TRY(make_mfma_copy(c, w->d, &mw->mfma_mem, &mw->m, &ok));
+            mw->mfma_state = ok ? 1 : -1;
+        }
+        if (mw->mfma_state == 1)
+            return run_gemm_mfma(c, w->m, d_x, seq_len, w->d.K, MFMA_ROWS_PLAIN, nullptr, d_out, w->d.N, nullptr,
+                                 false);
     }
     for (int r0 = 0; r0 < seq_len; r0 += kMaxM) {
         const int M = seq_len - r0 < kMaxM ? seq_len - r0 : kMaxM;
@@ -1378,6 +1422,132 @@ qtts_status qtts_forward_with_embedding(qtts_talker *t, const float *embedding, 
     return QTTS_OK;
 }
 
+// Prefill layers on the GEMV path: row chunks of up to kMaxM tokens, in
+// order, layer by layer (a chunk's causal attention reads the K/V rows that
+// earlier chunks appended).
+static qtts_status prefill_layers_rows(qtts_talker *t, qtts_kv *kv, int seq_len) {
+    qtts_ctx *c = t->ctx;
+    const Stack &st = t->st;
+    const int hidden = st.hidden, qd = st.nq * st.hd;
+    Stack one = st;
+    for (int l = 0; l < st.layers; l++) {
+        one.layers = 1;
+        one.L.assign(1, st.L[l]);
+        qtts_kv layer_kv = *kv;
+        layer_kv.layers = 1;
+        layer_kv.k = kv->layer_k(l);
+        layer_kv.v = kv->layer_v(l);
+        for (int r0 = 0; r0 < seq_len; r0 += kMaxM) {
+            const int M = seq_len - r0 < kMaxM ? seq_len - r0 : kMaxM;
+            QTTS_TRY(enqueue_layers(c, one, &layer_kv, t->xp + (size_t)r0 * hidden, t->qp + (size_t)r0 * qd,
+                                    t->ap + (size_t)r0 * qd, t->hp + (size_t)r0 * st.inter, M, nullptr, r0, nullptr,
+                                    r0, t->nsplit, nullptr));
+        }
+    }
+    return QTTS_OK;
+}
+
+// The MFMA operand copies of every layer weight; t->mfma_state -1 (and no
+// copies kept) when any weight cannot take the matrix-core path.
+static qtts_status make_talker_mfma(qtts_talker *t) {
+    qtts_ctx *c = t->ctx;
+    std::vector<DevQ4Mfma> copies;
+    std::vector<void *> mems;
+    bool all = true;
+    for (const DevLayer &Ly : t->st.L) {
+        for (const DevQ4 *w : {&Ly.qkv, &Ly.o, &Ly.gu, &Ly.down}) {
+            DevQ4Mfma m{};
+            void *mem = nullptr;
+            bool ok = false;
+            const qtts_status s = make_mfma_copy(c, *w, &mem, &m, &ok);
+            if (s != QTTS_OK || !ok) {
+                for (void *p : mems) (void)hipFree(p);
+                if (s != QTTS_OK) return s;
+                all = false;
+                break;
+            }
+            mems.push_back(mem);
+            copies.push_back(m);
+        }
+        if (!all) break;
+    }
+    if (!all) {
+        t->mfma_state = -1;
+        return QTTS_OK;
+    }
+    for (void *p : mems) t->own.ptrs.push_back(p);
+    t->mfma = std::move(copies);
+    t->mfma_state = 1;
+    return QTTS_OK;
+}
+
+// Prefill layers on the matrix cores (csrc/mfma.hip), all rows at once per
+// layer: QKV (RMSNorm prologue) -> QK-norm, RoPE, KV append -> causal
+// attention (row r sees positions 0..r) -> O (+residual) -> gate|up (RMSNorm
+// prologue) -> down (SiLU*up prologue, +residual); src/talker.rs:364-462.
+static qtts_status prefill_layers_mfma(qtts_talker *t, qtts_kv *kv, int seq_len) {
+    qtts_ctx *c = t->ctx;
+    const Stack &st = t->st;
+    const int hidden = st.hidden, qd = st.nq * st.hd, nqkv = qd + 2 * st.nkv * st.hd;
+    int attn_rows = (int)(kAttnPartFloats / ((size_t)st.nq * t->nsplit * (st.hd + 2)));
+    if (attn_rows > kAttnCounters / st.nkv) attn_rows = kAttnCounters / st.nkv;
+    if (attn_rows < 1) return fail(c, QTTS_ESHAPE, "attention split buffer too small");
+    for (int l = 0; l < st.layers; l++) {
+        const DevLayer &Ly = st.L[l];
+        const DevQ4Mfma *W = &t->mfma[(size_t)4 * l];
+        float *kc = kv->layer_k(l), *vc = kv->layer_v(l);
+        QTTS_TRY(run_gemm_mfma(c, W[0], t->xp, seq_len, hidden, MFMA_ROWS_RMSNORM, Ly.in_g, t->rawp, nqkv, nullptr,
+                               false));
+        QkvRowsParams q{};
+        q.raw = t->rawp;
+        q.ldr = nqkv;
+        q.M = seq_len;
+        q.n_q_heads = st.nq;
+        q.n_kv_heads = st.nkv;
+        q.head_dim = st.hd;
+        q.q_norm = Ly.q_norm;
+        q.k_norm = Ly.k_norm;
+        q.rope_cos = st.rope_cos;
+        q.rope_sin = st.rope_sin;
+        q.rope_rows = st.rope_rows;
+        q.rope_skip_oob = st.rope_skip_oob;
+        q.q = t->qp;
+        q.ldq = qd;
+        q.kcache = kc;
+        q.vcache = vc;
+        q.kv_cap = kv->cap;
+        launch_qkv_rows(c->stream, q);
+        QTTS_TRY(check_launch(c, "k_qkv_rows"));
+        for (int r0 = 0; r0 < seq_len; r0 += attn_rows) {
+            const int M = seq_len - r0 < attn_rows ? seq_len - r0 : attn_rows;
+            AttnParams a{};
+            a.q = t->qp + (size_t)r0 * qd;
+            a.ldq = qd;
+            a.kcache = kc;
+            a.vcache = vc;
+            a.kv_cap = kv->cap;
+            a.nq = st.nq;
+            a.nkv = st.nkv;
+            a.hd = st.hd;
+            a.kvlen_const = r0;
+            a.nsplit = t->nsplit;
+            a.scale = 1.0f / sqrtf((float)st.hd);  // src/talker.rs:305
+            a.part = c->attn_part;
+            a.counters = c->attn_counters;
+            a.out = t->ap + (size_t)r0 * qd;
+            a.ldo = qd;
+            launch_attention(c->stream, a, M);
+            QTTS_TRY(check_launch(c, "k_attn"));
+        }
+        QTTS_TRY(run_gemm_mfma(c, W[1], t->ap, seq_len, qd, MFMA_ROWS_PLAIN, nullptr, t->xp, hidden, nullptr, true));
+        QTTS_TRY(run_gemm_mfma(c, W[2], t->xp, seq_len, hidden, MFMA_ROWS_RMSNORM, Ly.post_g, t->rawp, 2 * st.inter,
+                               nullptr, false));
+        QTTS_TRY(run_gemm_mfma(c, W[3], t->rawp, seq_len, 2 * st.inter, MFMA_ROWS_SWIGLU, nullptr, t->xp, hidden,
+                               nullptr, true));
+    }
+    return QTTS_OK;
+}
+
 qtts_status qtts_prefill_talker_raw(qtts_talker *t, const float *x, int32_t seq_len, qtts_kv *kv, float *last_hidden) {
     if (!t || !x || !last_hidden) return QTTS_EINVAL;
     qtts_ctx *c = t->ctx;
@@ -1400,26 +1570,18 @@ qtts_status qtts_prefill_talker_raw(qtts_talker *t, const float *x, int32_t seq_
         t->prefill_bufs.push_back(t->ap);
         HIP_TRY(c, hipMalloc(&t->hp, sizeof(float) * seq_len * st.inter));
         t->prefill_bufs.push_back(t->hp);
+        const size_t raw_cols = std::max((size_t)qd + 2 * st.nkv * st.hd, (size_t)2 * st.inter);
+        HIP_TRY(c, hipMalloc(&t->rawp, sizeof(float) * seq_len * raw_cols));
+        t->prefill_bufs.push_back(t->rawp);
         t->prefill_cap = seq_len;
     }
     t->nsplit = attn_nsplit(kv->cap, 16);
     HIP_TRY(c, hipMemcpyAsync(t->xp, x, sizeof(float) * seq_len * hidden, hipMemcpyHostToDevice, c->stream));
-    // Row chunks of up to kMaxM tokens, in order, layer by layer: a chunk's
-    // causal attention reads the K/V rows earlier chunks appended.
-    Stack one = st;
-    for (int l = 0; l < st.layers; l++) {
-        one.layers = 1;
-        one.L.assign(1, st.L[l]);
-        qtts_kv layer_kv = *kv;
-        layer_kv.layers = 1;
-        layer_kv.k = kv->layer_k(l);
-        layer_kv.v = kv->layer_v(l);
-        for (int r0 = 0; r0 < seq_len; r0 += kMaxM) {
-            const int M = seq_len - r0 < kMaxM ? seq_len - r0 : kMaxM;
-            QTTS_TRY(enqueue_layers(c, one, &layer_kv, t->xp + (size_t)r0 * hidden, t->qp + (size_t)r0 * qd,
-                                    t->ap + (size_t)r0 * qd, t->hp + (size_t)r0 * st.inter, M, nullptr, r0, nullptr,
-                                    r0, t->nsplit, nullptr));
-        }
+    if (seq_len >= kMfmaMinRows && t->mfma_state == 0) QTTS_TRY(make_talker_mfma(t));
+    if (seq_len >= kMfmaMinRows && t->mfma_state == 1) {
+        QTTS_TRY(prefill_layers_mfma(t, kv, seq_len));
+    } else {
+        QTTS_TRY(prefill_layers_rows(t, kv, seq_len));
     }
     // final norm of the last row (src/talker.rs:460-461) via the head GEMV's
     // normalising prologue; the logits it also produces are discarded.

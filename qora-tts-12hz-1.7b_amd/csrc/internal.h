@@ -39,11 +39,44 @@ struct DevQ4Mfma {
     int K, N;
 };
 
+// Row prologues of the MFMA GEMM's input split.
+enum MfmaRowsMode { MFMA_ROWS_PLAIN = 0, MFMA_ROWS_RMSNORM = 1, MFMA_ROWS_SWIGLU = 2 };
+constexpr int kMfmaRowsMaxK = 8192;
+
+struct MfmaRowsParams {
+    const float *x;  // row m at x + m * ldx (SWIGLU: gate [0, K), up [K, 2K))
+    int ldx, K, M, Mpad, mode;
+    const uint16_t *gamma;  // RMSNORM weight (binary16 bits)
+    _Float16 *xh, *xl;      // [Mpad / 32][K / 16][64][8], the MFMA A-operand order
+    int *rexp;              // [Mpad] row exponents
+};
+
+// apply_qk_norm + RoPE + KV append over M rows of a fused QKV projection
+// (the EPI_QKV epilogue of the GEMV, as a kernel of its own).
+struct QkvRowsParams {
+    const float *raw;  // row m at raw + m * ldr: [q heads | k heads | v heads] x head_dim
+    int ldr, M;
+    int n_q_heads, n_kv_heads, head_dim;
+    const uint16_t *q_norm, *k_norm;
+    const float *rope_cos, *rope_sin;
+    int rope_rows, rope_skip_oob;
+    float *q;  // [M][n_q_heads * head_dim], ldq
+    int ldq;
+    float *kcache, *vcache;  // [n_kv_heads][kv_cap][head_dim]
+    int kv_cap;
+    int pos0, row0;  // RoPE position and cache row of row 0
+};
+
 struct GemmMfmaParams {
     DevQ4Mfma w;
-    const _Float16 *xh, *xl;  // [32 * MT][K]: the rows split into binary16 hi + lo
-    int steps;                // 16-row steps per K chunk (a multiple of 4)
-    float *part;              // [kc][32 * MT][N]
+    const _Float16 *xh, *xl;  // the scaled rows split into binary16 hi + lo (MfmaRowsParams order)
+    const int *rexp;          // [32 * MT]: row m was scaled by 2^rexp[m]
+    int M;                    // rows of this pass (<= 32 * MT)
+    float *part;              // [kc][32 * MT][N] when kc > 1
+    unsigned *counters;       // [N / 32], zero between launches
+    const float *bias;        // optional
+    float *y;                 // y[m * ldy + n] (+)= result
+    int ldy, accumulate;
 };
 
 constexpr int kGemvThreads = 256;
@@ -189,11 +222,10 @@ void launch_gemv(hipStream_t st, const GemvParams &p);
 void launch_attention(hipStream_t st, const AttnParams &p, int M);
 void launch_sample(hipStream_t st, const SampleParams &p);
 void launch_embed_row(hipStream_t st, const DevQ4 &w, const uint32_t *d_token, float *out, const int *d_done);
-void launch_repack_mfma(hipStream_t st, const DevQ4 &w, uint32_t *wm, uint16_t *sa, uint16_t *sb);
-void launch_split_x(hipStream_t st, const float *x, int M, int ldx, int K, int Mpad, _Float16 *xh, _Float16 *xl);
-void launch_gemm_mfma(hipStream_t st, const GemmMfmaParams &p, int mt, int kc);
-void launch_gemm_reduce(hipStream_t st, const float *part, int kc, int M, int Mpad, int N, const float *bias, float *y,
-                        int ldy, int accumulate);
+void launch_repack_mfma(hipStream_t st, const DevQ4 &w, uint32_t *wm, uint16_t *sa, uint16_t *sb, int *too_large);
+void launch_mfma_rows(hipStream_t st, const MfmaRowsParams &p);
+void launch_qkv_rows(hipStream_t st, const QkvRowsParams &p);
+void launch_gemm_mfma(hipStream_t st, const GemmMfmaParams &p, int mt, int sw, int kc);
 void launch_embed_sum(hipStream_t st, const EmbSumParams &p);
 void launch_advance(hipStream_t st, LoopState *s, int frame_step);
 void launch_repack_q4(hipStream_t st, const uint8_t *packed, const uint16_t *scales, int K, int N, int col0,

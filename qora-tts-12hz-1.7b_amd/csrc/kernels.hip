@@ -359,6 +359,56 @@ void launch_gemv(hipStream_t st, const GemvParams &p) {
     }
 }
 
+// apply_qk_norm (src/talker.rs:86-99) + split-half RoPE (src/rope.rs:79-92)
+// + KV append (src/talker.rs:299-302) of one (head, row) per block, with the
+// expressions of the GEMV's EPI_QKV epilogue.
+__global__ __launch_bounds__(256) void k_qkv_rows(QkvRowsParams P) {
+    __shared__ float vals[256];
+    __shared__ float scratch[8];
+    const int head = blockIdx.x, m = blockIdx.y, tid = threadIdx.x;
+    const int hd = P.head_dim, half = hd / 2;
+    const bool is_q = head < P.n_q_heads;
+    const bool is_k = !is_q && head < P.n_q_heads + P.n_kv_heads;
+    const int pos = P.pos0 + m, row = P.row0 + m;
+    const float *src = P.raw + (size_t)m * P.ldr + (size_t)head * hd;
+    if (is_q || is_k) {
+        const float v = tid < hd ? src[tid] : 0.0f;
+        const float ss = block_sum_256(v * v, scratch);
+        const float inv = 1.0f / sqrtf(ss / (float)hd + 1e-6f);
+        const uint16_t *gam = is_q ? P.q_norm : P.k_norm;
+        if (tid < hd) vals[tid] = v * inv * f16_to_f32(gam[tid]);
+        __syncthreads();
+        const bool rotate = !(P.rope_skip_oob && pos >= P.rope_rows);
+        if (tid < half) {
+            const float x1 = vals[tid], x2 = vals[tid + half];
+            float o1 = x1, o2 = x2;
+            if (rotate) {
+                const float cs = P.rope_cos[(size_t)pos * half + tid];
+                const float sn = P.rope_sin[(size_t)pos * half + tid];
+                o1 = x1 * cs - x2 * sn;
+                o2 = x2 * cs + x1 * sn;
+            }
+            float *dst;
+            if (is_q) {
+                dst = P.q + (size_t)m * P.ldq + (size_t)head * hd;
+            } else {
+                const int kh = head - P.n_q_heads;
+                dst = P.kcache + ((size_t)kh * P.kv_cap + row) * hd;
+            }
+            dst[tid] = o1;
+            dst[tid + half] = o2;
+        }
+    } else {
+        const int vh = head - P.n_q_heads - P.n_kv_heads;
+        if (tid < hd) P.vcache[((size_t)vh * P.kv_cap + row) * hd + tid] = src[tid];
+    }
+}
+
+void launch_qkv_rows(hipStream_t st, const QkvRowsParams &p) {
+    hipLaunchKernelGGL(k_qkv_rows, dim3((unsigned)(p.n_q_heads + 2 * p.n_kv_heads), (unsigned)p.M), dim3(256), 0, st,
+                       p);
+}
+
 // ---------------------------------------------------------------------------
 // Attention: one block per (kv head, split, query row).  Both query heads of
 // a GQA group share the K/V reads.  Softmax partials (max, sum, unnormalised

@@ -72,12 +72,15 @@ def test_talker_step_full_prefilled_kv(full):
     assert int(np.argmax(got[cfg.hidden:])) == int(np.argmax(ref[cfg.hidden:]))
 
 
-@pytest.mark.parametrize("seq_len", [1, 5, 13])
+@pytest.mark.parametrize("seq_len", [1, 5, 13, 70])
 def test_prefill_tiny(tiny, seq_len):
+    """Below 8 rows the prefill runs on the GEMV path, from 8 rows on the
+    matrix cores (70 rows: two 64-row GEMM passes)."""
     tw, _, t, _, ot, _ = tiny
     cfg = tw.cfg
     x = qtts.synth_normal_f32(23, f"prefill.{seq_len}", seq_len * cfg.hidden)
-    kv, okv = t.new_kv(32), ot.new_kv(32)
+    cap = max(32, seq_len + 8)
+    kv, okv = t.new_kv(cap), ot.new_kv(cap)
     got = t.prefill_talker_raw(x, seq_len, kv)
     ref = ot.prefill_talker_raw(x, seq_len, okv)
     assert rel_err(got, ref) < REL_TOL

@@ -114,6 +114,37 @@ def test_gemm_mfma_one_hot_rows_are_dequantized_rows(ctx):
         assert np.array_equal(y[m], deq[k]), f"row {m} (k = {k})"
 
 
+def test_gemm_mfma_row_magnitudes(ctx):
+    """Rows from 1e-6 to 1e6 in magnitude (beyond binary16's range without the
+    per-row power-of-two scaling) keep f32-level accuracy row by row, and
+    repeated calls are bit-identical (chunk partials summed in order)."""
+    K, N, rows = 2048, 2048, 40
+    w = qtts.Q4Weight.synthetic(17, "mfma.mag", K, N)
+    x = qtts.synth_normal_f32(17, "mfma.mag.x", rows * K).reshape(rows, K)
+    x = (x * (10.0 ** (np.arange(rows) % 13 - 6))[:, None]).astype(np.float32)
+    x[7, :] = 0.0  # an all-zero row
+    d = qtts.DeviceQ4(ctx, w)
+    y = d.gemm(x.reshape(-1), rows).reshape(rows, N)
+    exact = x.astype(np.float64) @ w.dequantize().astype(np.float64)
+    assert np.all(y[7] == 0.0)
+    for m in range(rows):
+        if m != 7:
+            assert rel_err(y[m], exact[m]) < GEMV_TIGHT, f"row {m}"
+    assert np.array_equal(y, d.gemm(x.reshape(-1), rows).reshape(rows, N))
+
+
+def test_gemm_large_scales_stay_exact(ctx):
+    """A weight with a scale above 8188 (whose binary16 products sa * q could
+    overflow) is not given to the matrix cores; the result still matches."""
+    K, N, rows = 1024, 512, 16
+    w = qtts.Q4Weight.synthetic(18, "mfma.big", K, N)
+    w.scales[5, 3] = 0x7400  # 16384
+    x = qtts.synth_normal_f32(18, "mfma.big.x", rows * K)
+    y = qtts.DeviceQ4(ctx, w).gemm(x, rows).reshape(rows, N)
+    exact = x.reshape(rows, K).astype(np.float64) @ w.dequantize().astype(np.float64)
+    assert rel_err(y, exact) < GEMV_TIGHT
+
+
 def test_gemv_linearity(ctx):
     """gemv(a*x1 + x2) == a*gemv(x1) + gemv(x2) to f32 accuracy."""
     K, N = 6144, 2048
