@@ -356,8 +356,8 @@ qtts_status grow(qtts_ctx *c, T **buf, size_t *cap, size_t need) {
 qtts_status run_gemm_mfma(qtts_ctx *c, const DevQ4Mfma &w, const float *x, int M, int ldx, int mode,
                           const uint16_t *gamma, float *y, int ldy, const float *bias, bool accumulate) {
     const int K = w.K, N = w.N, Ks = K / 16, panels = N / 32;
-    if (K % 16 || N % 32 || K > kMfmaRowsMaxK || (mode == MFMA_ROWS_RMSNORM && (K % 4 || ldx % 4)))
-        return fail(c, QTTS_ESHAPE, "MFMA GEMM: unsupported shape");
+    if (K % 16 || N % 32 || K > kMfmaRowsMaxK || ldx % 4 || ((uintptr_t)x & 15))
+        return fail(c, QTTS_ESHAPE, "MFMA GEMM: unsupported shape or unaligned rows");
     if (panels > kCounters) return fail(c, QTTS_ESHAPE, "MFMA GEMM: more panels than counters");
     int sw = 8;
     while (sw > 1 && 4 * (sw / 2) >= Ks) sw /= 2;
@@ -1151,7 +1151,7 @@ size_t qtts_q4_bytes(const qtts_q4 *w) { return w ? w->bytes : 0; }
 qtts_status qtts_gemm_device(qtts_ctx *c, const qtts_q4 *w, const float *d_x, int32_t seq_len, float *d_out) {
     if (!c || !w || !d_x || !d_out) return QTTS_EINVAL;
     if (seq_len < 1) return fail(c, QTTS_EINVAL, "seq_len < 1");
-    if (seq_len >= kMfmaMinRows) {
+    if (seq_len >= kMfmaMinRows && ((uintptr_t)d_x & 15) == 0) {
         qtts_q4 *mw = const_cast<qtts_q4 *>(w);
         if (mw->mfma_state == 0) {
             bool ok = false;
@@ -1489,7 +1489,10 @@ static qtts_status prefill_layers_mfma(qtts_talker *t, qtts_kv *kv, int seq_len)
     qtts_ctx *c = t->ctx;
     const Stack &st = t->st;
     const int hidden = st.hidden, qd = st.nq * st.hd, nqkv = qd + 2 * st.nkv * st.hd;
-    int attn_rows = (int)(kAttnPartFloats / ((size_t)st.nq * t->nsplit * (st.hd + 2)));
+    // one attention split per kAttnMaxChunk positions of the prefill (the
+    // decode-sized split count would give thousands of tiny blocks)
+    const int nsplit = attn_nsplit(seq_len, 1);
+    int attn_rows = (int)(kAttnPartFloats / ((size_t)st.nq * nsplit * (st.hd + 2)));
     if (attn_rows > kAttnCounters / st.nkv) attn_rows = kAttnCounters / st.nkv;
     if (attn_rows < 1) return fail(c, QTTS_ESHAPE, "attention split buffer too small");
     for (int l = 0; l < st.layers; l++) {
@@ -1530,7 +1533,7 @@ static qtts_status prefill_layers_mfma(qtts_talker *t, qtts_kv *kv, int seq_len)
             a.nkv = st.nkv;
             a.hd = st.hd;
             a.kvlen_const = r0;
-            a.nsplit = t->nsplit;
+            a.nsplit = nsplit;
             a.scale = 1.0f / sqrtf((float)st.hd);  // src/talker.rs:305
             a.part = c->attn_part;
             a.counters = c->attn_counters;

@@ -72,16 +72,16 @@ __global__ void k_repack_mfma(DevQ4 w, uint32_t *wm, uint16_t *sa, uint16_t *sb,
 // xh and xl are stored in the MFMA A-operand order -- [M-tile][16-row step]
 // [lane][8] -- so that each wave's operand load of a step is one contiguous
 // KiB.
+template <int G>  // 8-value groups per thread: K <= 2048 * G
 __global__ __launch_bounds__(256) void k_mfma_rows(MfmaRowsParams P) {
-    __shared__ float vbuf[kMfmaRowsMaxK];
-    __shared__ float red[4];
+    __shared__ float red[2][4];
     const int m = blockIdx.x, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const int K = P.K, Ks = K / 16;
+    const int K = P.K, Ks = K / 16, ng = K / 8;
     // 8-value group g = k / 8 of row m goes to the A-operand slot of lane
     // (m % 32) + 32 (g % 2) in step g / 2 of M-tile m / 32
     const size_t tile = (size_t)(m >> 5) * Ks * 64 + (m & 31);
     if (m >= P.M) {
-        for (int g = tid; g < K / 8; g += 256) {
+        for (int g = tid; g < ng; g += 256) {
             const size_t o = (tile + (size_t)(g >> 1) * 64 + 32 * (g & 1)) * 8;
             *reinterpret_cast<half8 *>(P.xh + o) = (half8){};
             *reinterpret_cast<half8 *>(P.xl + o) = (half8){};
@@ -90,38 +90,59 @@ __global__ __launch_bounds__(256) void k_mfma_rows(MfmaRowsParams P) {
         return;
     }
     const float *src = P.x + (size_t)m * P.ldx;
-    float inv = 1.0f;
-    if (P.mode == MFMA_ROWS_RMSNORM) {
-        float ss = 0.0f;
-        for (int j = tid * 4; j < K; j += 1024) {
-            const float4 v = *reinterpret_cast<const float4 *>(src + j);
-            ss += v.x * v.x + v.y * v.y + v.z * v.z + v.w * v.w;
-        }
-        ss = wave_sum(ss);
-        if (lane == 0) red[wave] = ss;
-        __syncthreads();
-        ss = (red[0] + red[1]) + (red[2] + red[3]);
-        inv = 1.0f / sqrtf(ss / (float)K + 1e-6f);
-        __syncthreads();
-    }
-    float mx = 0.0f;
-    for (int k = tid; k < K; k += 256) {
-        float v;
-        if (P.mode == MFMA_ROWS_RMSNORM) {
-            v = src[k] * inv * f16_to_f32(P.gamma[k]);
-        } else if (P.mode == MFMA_ROWS_SWIGLU) {
-            const float g = src[k], u = src[K + k];
-            v = (g / (1.0f + expf(-g))) * u;
+    float v[G][8];
+    // 1. the row's values (all loads first), and the RMSNorm sum of squares
+    float ss = 0.0f;
+#pragma unroll
+    for (int j = 0; j < G; j++) {
+        const int g = tid + 256 * j;
+        if (g < ng) {
+            const float4 a = *reinterpret_cast<const float4 *>(src + 8 * g);
+            const float4 b = *reinterpret_cast<const float4 *>(src + 8 * g + 4);
+            v[j][0] = a.x, v[j][1] = a.y, v[j][2] = a.z, v[j][3] = a.w;
+            v[j][4] = b.x, v[j][5] = b.y, v[j][6] = b.z, v[j][7] = b.w;
+            if (P.mode == MFMA_ROWS_SWIGLU) {
+                const float4 c = *reinterpret_cast<const float4 *>(src + K + 8 * g);
+                const float4 d = *reinterpret_cast<const float4 *>(src + K + 8 * g + 4);
+                const float u[8] = {c.x, c.y, c.z, c.w, d.x, d.y, d.z, d.w};
+#pragma unroll
+                for (int i = 0; i < 8; i++) v[j][i] = (v[j][i] / (1.0f + expf(-v[j][i]))) * u[i];
+            }
         } else {
-            v = src[k];
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[j][i] = 0.0f;
         }
-        vbuf[k] = v;
-        mx = fmaxf(mx, fabsf(v));  // NaN entries drop out here and stay NaN below
+#pragma unroll
+        for (int i = 0; i < 8; i++) ss += v[j][i] * v[j][i];
     }
+    if (P.mode == MFMA_ROWS_RMSNORM) {
+        ss = wave_sum(ss);
+        if (lane == 0) red[0][wave] = ss;
+        __syncthreads();
+        ss = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
+        const float inv = 1.0f / sqrtf(ss / (float)K + 1e-6f);
+#pragma unroll
+        for (int j = 0; j < G; j++) {
+            const int g = tid + 256 * j;
+            if (g < ng) {
+                const uint4 gw = *reinterpret_cast<const uint4 *>(P.gamma + 8 * g);
+                const uint32_t gp[4] = {gw.x, gw.y, gw.z, gw.w};
+#pragma unroll
+                for (int i = 0; i < 8; i++)
+                    v[j][i] = v[j][i] * inv * f16_to_f32((uint16_t)(gp[i / 2] >> (16 * (i & 1))));
+            }
+        }
+    }
+    // 2. the row exponent
+    float mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < G; j++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) mx = fmaxf(mx, fabsf(v[j][i]));  // NaN entries drop out here and stay NaN below
     mx = wave_max(mx);
-    if (lane == 0) red[wave] = mx;
+    if (lane == 0) red[1][wave] = mx;
     __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    mx = fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3]));
     int e = 0;
     if (mx > 0.0f && mx < INFINITY) {
         int E;
@@ -129,13 +150,17 @@ __global__ __launch_bounds__(256) void k_mfma_rows(MfmaRowsParams P) {
         e = min(15 - E, 126);
     }
     if (tid == 0) P.rexp[m] = e;
-    for (int g = tid; g < K / 8; g += 256) {
+    // 3. the binary16 hi + lo split
+#pragma unroll
+    for (int j = 0; j < G; j++) {
+        const int g = tid + 256 * j;
+        if (g >= ng) continue;
         half8 h, l;
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            const float v = ldexpf(vbuf[8 * g + i], e);
-            h[i] = (_Float16)v;
-            l[i] = (_Float16)(v - (float)h[i]);
+            const float s = ldexpf(v[j][i], e);
+            h[i] = (_Float16)s;
+            l[i] = (_Float16)(s - (float)h[i]);
         }
         const size_t o = (tile + (size_t)(g >> 1) * 64 + 32 * (g & 1)) * 8;
         *reinterpret_cast<half8 *>(P.xh + o) = h;
@@ -289,7 +314,13 @@ void launch_repack_mfma(hipStream_t st, const DevQ4 &w, uint32_t *wm, uint16_t *
 }
 
 void launch_mfma_rows(hipStream_t st, const MfmaRowsParams &p) {
-    hipLaunchKernelGGL(k_mfma_rows, dim3((unsigned)p.Mpad), dim3(256), 0, st, p);
+    const int g = (p.K / 8 + 255) / 256;
+    if (g <= 1)
+        hipLaunchKernelGGL(k_mfma_rows<1>, dim3((unsigned)p.Mpad), dim3(256), 0, st, p);
+    else if (g == 2)
+        hipLaunchKernelGGL(k_mfma_rows<2>, dim3((unsigned)p.Mpad), dim3(256), 0, st, p);
+    else
+        hipLaunchKernelGGL(k_mfma_rows<4>, dim3((unsigned)p.Mpad), dim3(256), 0, st, p);
 }
 
 template <int MT>
