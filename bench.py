@@ -28,6 +28,7 @@ sys.path.insert(0, ROOT)
 import qtts  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0  # dense binary16 MFMA
 PROMPT = 64
 
 
@@ -151,6 +152,42 @@ def gemv_roofline(ctx, iters=256, copies=64):
         "kernel": "k_gemv<1,4> (stand-alone Q4 GEMV 2048->12288, talker gate|up, launch gaps included)",
         "algorithmic_bytes_per_launch": algo_bytes,
         "avg_launch_us": round(avg_s * 1e6, 3),
+    }
+
+
+def mfma_gemm_roofline(ctx, rows=64, iters=128, copies=32):
+    """The talker prefill's gate|up projection (K=2048 -> N=2*6144) for 64
+    rows on the matrix cores (qtts_gemm: row split + k_gemm_mfma), averaged
+    over `copies` distinct weights with HIP events on the context's stream.
+    Algorithmic work is 2*M*K*N flops; the kernel issues three binary16
+    MFMAs per product term (hi/lo operands) to stay at f32 accuracy."""
+    K, N = 2048, 12288
+    hip = Hip()
+    ws = [qtts.DeviceQ4(ctx, qtts.Q4Weight.synthetic(98, f"mfma.{i}", K, N)) for i in range(copies)]
+    dx, dy = hip.malloc(4 * K * rows), hip.malloc(4 * N * rows)
+    hip.h2d(dx, qtts.synth_normal_f32(98, "mfma.x", K * rows))
+    for i in range(copies):
+        ws[i].gemm_device(dx, rows, dy)
+    ctx.synchronize()
+    start, end = hip.event(), hip.event()
+    hip.record(start, ctx.stream)
+    for i in range(iters):
+        ws[i % copies].gemm_device(dx, rows, dy)
+    hip.record(end, ctx.stream)
+    avg_s = hip.elapsed_ms(start, end) / 1e3 / iters
+    hip.free(dx)
+    hip.free(dy)
+    flops = 2.0 * rows * K * N
+    achieved = flops / avg_s / 1e12
+    return {
+        "bound": "mfma",
+        "achieved": round(achieved, 2),
+        "peak": MFMA_F16_PEAK_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4),
+        "kernel": "k_mfma_rows + k_gemm_mfma<2,8> (Q4 GEMM 64x2048 -> 12288, talker gate|up at prefill)",
+        "weight_GBps": round((K * N // 2 + K * (N // 32) * 4) / avg_s / 1e9, 1),
+        "avg_call_us": round(avg_s * 1e6, 2),
     }
 
 
@@ -289,6 +326,18 @@ def main():
     if not args.no_roofline:
         out["gemv"] = gemv_roofline(ctx)
         log(f"stand-alone gemv {out['gemv']}")
+        # the 64-token prompt prefill (matrix-core path), HIP events
+        ctx.synchronize()
+        hip.record(ev0, ctx.stream)
+        for _ in range(5):
+            prefill()
+        hip.record(ev1, ctx.stream)
+        ctx.synchronize()
+        pf_s = hip.elapsed_ms(ev0, ev1) / 1e3 / 5
+        out["prefill"] = {"tokens": PROMPT, "ms": round(pf_s * 1e3, 3), "tokens_per_s": round(PROMPT / pf_s, 1),
+                          "timing": "HIP events around 5 prefill_talker_raw calls, host copies included",
+                          "gemm": mfma_gemm_roofline(ctx)}
+        log(f"prefill {out['prefill']}")
     if not args.no_cpu:
         lh_np, lg_np = lh, lg
         kv_cpu, lh_np, lg_np = prefill()

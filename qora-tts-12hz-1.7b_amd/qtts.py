@@ -465,6 +465,10 @@ class DeviceQ4:
     def gemv_device(self, d_x: int, d_y: int):
         self.ctx.check(self.ctx.lib.qtts_gemv_device(self.ctx.h, self.h, C.c_void_p(d_x), C.c_void_p(d_y)))
 
+    def gemm_device(self, d_x: int, seq_len: int, d_y: int):
+        """gemm over device buffers (x: seq_len rows of K, y: seq_len rows of N)."""
+        self.ctx.check(self.ctx.lib.qtts_gemm_device(self.ctx.h, self.h, C.c_void_p(d_x), seq_len, C.c_void_p(d_y)))
+
     @property
     def memory_bytes(self) -> int:
         return int(self.ctx.lib.qtts_q4_bytes(self.h))
