@@ -78,6 +78,10 @@ typedef struct qtts_talker_view {
     int32_t head_dim;     /* 128 */
     double rope_theta;    /* 1e6 */
     int32_t max_position; /* RoPE table length, 32768 (src/config.rs:142) */
+    /* Optional [max_position][head_dim/2] cos/sin tables (a model file's,
+     * src/save.rs:84-85); NULL: built from rope_theta (src/rope.rs:11-41). */
+    const float *rope_cos;
+    const float *rope_sin;
 } qtts_talker_view;
 
 /* CodePredictorWeights, src/code_predictor.rs:28-46. */
@@ -96,6 +100,10 @@ typedef struct qtts_predictor_view {
     int32_t head_dim;     /* 128 */
     double rope_theta;    /* 1e6 */
     int32_t max_position; /* RoPE table length, 65536 (src/loader.rs:862) */
+    /* Optional [max_position][head_dim/2] cos/sin tables (a model file's,
+     * src/save.rs:135-136); NULL: built from rope_theta (src/loader.rs:396-408). */
+    const float *rope_cos;
+    const float *rope_sin;
 } qtts_predictor_view;
 
 /* sample_token parameters, src/generate_new.rs:38-45,329-391. */

@@ -510,7 +510,12 @@ qor_talker *qor_talker_new(const qtts_talker_view *w) {
     t->st.max_pos = w->max_position;
     t->st.rope_cos = (float *)xcalloc((size_t)w->max_position * half, sizeof(float));
     t->st.rope_sin = (float *)xcalloc((size_t)w->max_position * half, sizeof(float));
-    qor_build_rope_table(w->head_dim, w->max_position, w->rope_theta, t->st.rope_cos, t->st.rope_sin);
+    if (w->rope_cos && w->rope_sin) { /* a model file's tables (src/save.rs:84-85) */
+        memcpy(t->st.rope_cos, w->rope_cos, (size_t)w->max_position * half * sizeof(float));
+        memcpy(t->st.rope_sin, w->rope_sin, (size_t)w->max_position * half * sizeof(float));
+    } else {
+        qor_build_rope_table(w->head_dim, w->max_position, w->rope_theta, t->st.rope_cos, t->st.rope_sin);
+    }
     t->st.rope_skip_oob = 0;
     return t;
 }
@@ -586,7 +591,12 @@ qor_predictor *qor_predictor_new(const qtts_predictor_view *w) {
     p->st.max_pos = rows;
     p->st.rope_cos = (float *)xcalloc((size_t)rows * half, sizeof(float));
     p->st.rope_sin = (float *)xcalloc((size_t)rows * half, sizeof(float));
-    qor_build_rope_table(w->head_dim, rows, w->rope_theta, p->st.rope_cos, p->st.rope_sin);
+    if (w->rope_cos && w->rope_sin) { /* a model file's tables (src/save.rs:135-136) */
+        memcpy(p->st.rope_cos, w->rope_cos, (size_t)rows * half * sizeof(float));
+        memcpy(p->st.rope_sin, w->rope_sin, (size_t)rows * half * sizeof(float));
+    } else {
+        qor_build_rope_table(w->head_dim, rows, w->rope_theta, p->st.rope_cos, p->st.rope_sin);
+    }
     p->st.rope_skip_oob = 1;
     return p;
 }

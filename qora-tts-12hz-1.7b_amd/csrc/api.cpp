@@ -221,8 +221,18 @@ qtts_status upload_array(qtts_ctx *c, Owner &own, const T *src, size_t count, T 
 
 // RoPE table exactly as build_mrope_tables (src/rope.rs:11-41) and the
 // predictor table (src/loader.rs:859-874): double pow/cos/sin, cast to float.
-qtts_status upload_rope(qtts_ctx *c, Owner &own, int head_dim, int rows, double theta, Stack *st) {
+// The first `rows` rows of the RoPE tables: the caller's (cos_in/sin_in,
+// e.g. a model file's) or built from theta.
+qtts_status upload_rope(qtts_ctx *c, Owner &own, int head_dim, int rows, double theta, const float *cos_in,
+                        const float *sin_in, Stack *st) {
     const int half = head_dim / 2;
+    if ((cos_in == nullptr) != (sin_in == nullptr)) return fail(c, QTTS_EINVAL, "RoPE tables: give both or neither");
+    if (cos_in) {
+        QTTS_TRY(upload_array(c, own, cos_in, (size_t)rows * half, &st->rope_cos, "rope cos"));
+        QTTS_TRY(upload_array(c, own, sin_in, (size_t)rows * half, &st->rope_sin, "rope sin"));
+        st->rope_rows = rows;
+        return QTTS_OK;
+    }
     std::vector<float> cs((size_t)rows * half), sn((size_t)rows * half);
     for (int i = 0; i < half; i++) {
         const double freq = 1.0 / std::pow(theta, (double)(2 * i) / (double)head_dim);
@@ -1321,7 +1331,7 @@ qtts_status qtts_talker_upload(qtts_ctx *c, const qtts_talker_view *v, qtts_talk
     if ((s = upload_array(c, t->own, v->final_norm_gamma, (size_t)hidden, &t->st.final_g, "final_norm_gamma")) !=
         QTTS_OK)
         return bail(s);
-    if ((s = upload_rope(c, t->own, v->head_dim, v->max_position, v->rope_theta, &t->st)) != QTTS_OK) return bail(s);
+    if ((s = upload_rope(c, t->own, v->head_dim, v->max_position, v->rope_theta, v->rope_cos, v->rope_sin, &t->st)) != QTTS_OK) return bail(s);
     t->st.rope_skip_oob = 0;
     const int qd = t->st.nq * t->st.hd;
     if ((s = t->own.alloc(c, &t->x, (size_t)hidden)) != QTTS_OK) return bail(s);
@@ -1683,7 +1693,7 @@ qtts_status qtts_predictor_upload(qtts_ctx *c, const qtts_predictor_view *v, qtt
     int rows = p->groups + 2;
     if (rows > v->max_position) rows = v->max_position;
     if (rows < 1) return bail(fail(c, QTTS_EINVAL, "max_position must be positive"));
-    if ((s = upload_rope(c, p->own, v->head_dim, rows, v->rope_theta, &p->st)) != QTTS_OK) return bail(s);
+    if ((s = upload_rope(c, p->own, v->head_dim, rows, v->rope_theta, v->rope_cos, v->rope_sin, &p->st)) != QTTS_OK) return bail(s);
     p->st.rope_skip_oob = 1;
     const int qd = p->st.nq * p->st.hd;
     if ((s = p->own.alloc(c, &p->in2, 2 * (size_t)p->talker_hidden)) != QTTS_OK) return bail(s);

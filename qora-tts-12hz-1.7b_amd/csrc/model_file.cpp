@@ -1,0 +1,388 @@
+// model_file.cpp — .qora-tts reader (load_model, src/save.rs:262-298).
+//
+// Sections are read in the order save_model writes them (src/save.rs:23-46):
+// talker (load_talker, src/save.rs:300-351), code predictor (load_predictor,
+// src/save.rs:353-409), speech decoder (load_decoder_weights,
+// src/save.rs:447-546).  Each array is read into its own host vector, so the
+// views are naturally aligned whatever the array's offset in the file.  Every
+// element count is checked against the bytes left in the file before anything
+// is allocated.
+#include "../../include/qtts_file.h"
+
+#include <cerrno>
+#include <cstdio>
+#include <cstring>
+#include <deque>
+#include <new>
+#include <string>
+#include <vector>
+
+namespace {
+
+thread_local std::string g_error;
+
+struct FileReader {
+    FILE *f = nullptr;
+    int64_t pos = 0, size = 0;
+    std::string err;
+
+    bool fail(const std::string &m) {
+        if (err.empty()) err = m + " (at byte " + std::to_string(pos) + ")";
+        return false;
+    }
+    bool bytes(void *dst, size_t n, const char *what) {
+        if ((int64_t)n > size - pos) return fail(std::string("truncated file reading ") + what);
+        if (n && fread(dst, 1, n, f) != n) return fail(std::string("read error in ") + what);
+        pos += (int64_t)n;
+        return true;
+    }
+    bool skip(int64_t n, const char *what) {
+        if (n < 0 || n > size - pos) return fail(std::string("truncated file skipping ") + what);
+        if (fseeko(f, (off_t)n, SEEK_CUR) != 0) return fail(std::string("seek error in ") + what);
+        pos += n;
+        return true;
+    }
+    bool u8(uint8_t *v, const char *what) { return bytes(v, 1, what); }
+    bool u32(uint32_t *v, const char *what) {
+        uint8_t b[4];
+        if (!bytes(b, 4, what)) return false;
+        *v = (uint32_t)b[0] | (uint32_t)b[1] << 8 | (uint32_t)b[2] << 16 | (uint32_t)b[3] << 24;
+        return true;
+    }
+    bool u64(uint64_t *v, const char *what) {
+        uint8_t b[8];
+        if (!bytes(b, 8, what)) return false;
+        *v = 0;
+        for (int i = 7; i >= 0; i--) *v = *v << 8 | b[i];
+        return true;
+    }
+    // A u32 count or dimension that must fit in int32.
+    bool dim(int32_t *v, const char *what) {
+        uint32_t u;
+        if (!u32(&u, what)) return false;
+        if (u > 0x7FFFFFFFu) return fail(std::string(what) + " out of range");
+        *v = (int32_t)u;
+        return true;
+    }
+    // u64 element count of `elem`-byte elements, bounded by the bytes left.
+    bool count(uint64_t *n, size_t elem, const char *what) {
+        if (!u64(n, what)) return false;
+        if (*n > (uint64_t)(size - pos) / elem) return fail(std::string(what) + ": length beyond the end of the file");
+        return true;
+    }
+};
+
+}  // namespace
+
+struct qtts_model_file {
+    std::deque<std::vector<uint8_t>> u8s;
+    std::deque<std::vector<uint16_t>> u16s;
+    std::deque<std::vector<float>> f32s;
+    std::vector<qtts_layer_view> talker_layers, predictor_layers;
+    std::vector<qtts_q4_view> codec_embeddings, lm_heads;
+    qtts_talker_view talker{};
+    qtts_predictor_view predictor{};
+    qtts_text_view text{};
+    qtts_file_info info{};
+
+    // write_f16_vec_io / read_f16_vec_io (src/gemv.rs:577-583,611-619)
+    bool f16_vec(FileReader &r, const uint16_t **out, uint64_t *len, const char *what) {
+        if (!r.count(len, 2, what)) return false;
+        u16s.emplace_back((size_t)*len);
+        std::vector<uint16_t> &v = u16s.back();
+        uint8_t *raw = reinterpret_cast<uint8_t *>(v.data());
+        if (!r.bytes(raw, (size_t)*len * 2, what)) return false;
+        for (size_t i = 0; i < v.size(); i++) v[i] = (uint16_t)(raw[2 * i] | raw[2 * i + 1] << 8);
+        *out = v.data();
+        return true;
+    }
+    // write_f32_vec_io / read_f32_vec_io (src/gemv.rs:585-591,621-629)
+    bool f32_vec(FileReader &r, const float **out, uint64_t *len, const char *what) {
+        if (!r.count(len, 4, what)) return false;
+        f32s.emplace_back((size_t)*len);
+        std::vector<float> &v = f32s.back();
+        uint8_t *raw = reinterpret_cast<uint8_t *>(v.data());
+        if (!r.bytes(raw, (size_t)*len * 4, what)) return false;
+        for (size_t i = 0; i < v.size(); i++) {
+            const uint32_t b = (uint32_t)raw[4 * i] | (uint32_t)raw[4 * i + 1] << 8 | (uint32_t)raw[4 * i + 2] << 16 |
+                               (uint32_t)raw[4 * i + 3] << 24;
+            std::memcpy(&v[i], &b, 4);
+        }
+        *out = v.data();
+        return true;
+    }
+    bool skip_f32_vec(FileReader &r, const char *what) {
+        uint64_t n;
+        return r.count(&n, 4, what) && r.skip((int64_t)n * 4, what);
+    }
+    // read_weight_io with format 1 (src/gemv.rs:639-650): u64 k, u64 n,
+    // u64-counted packed bytes, u64-counted binary16 scales.
+    bool q4(FileReader &r, qtts_q4_view *w, const std::string &name) {
+        uint64_t k, n, plen, slen;
+        const char *what = name.c_str();
+        if (!r.u64(&k, what) || !r.u64(&n, what)) return false;
+        if (k == 0 || n == 0 || n % 32 != 0 || k > 0x7FFFFFFF || n > 0x7FFFFFFF)
+            return r.fail(name + ": shape " + std::to_string(k) + "x" + std::to_string(n) +
+                          " (n must be a positive multiple of 32)");
+        if (!r.count(&plen, 1, what)) return false;
+        if (plen != k * n / 2) return r.fail(name + ": packed length " + std::to_string(plen) + " != k*n/2");
+        u8s.emplace_back((size_t)plen);
+        if (!r.bytes(u8s.back().data(), (size_t)plen, what)) return false;
+        const uint16_t *sc;
+        if (!f16_vec(r, &sc, &slen, what)) return false;
+        if (slen != k * n / 32) return r.fail(name + ": scale count " + std::to_string(slen) + " != k*n/32");
+        w->packed = u8s.back().data();
+        w->scales = sc;
+        w->k = (int32_t)k;
+        w->n = (int32_t)n;
+        return true;
+    }
+    bool gamma(FileReader &r, const uint16_t **out, uint64_t want, const std::string &name) {
+        uint64_t len;
+        if (!f16_vec(r, out, &len, name.c_str())) return false;
+        if (want && len != want)
+            return r.fail(name + ": length " + std::to_string(len) + ", expected " + std::to_string(want));
+        return true;
+    }
+    // TalkerLayerWeights / PredictorLayerWeights field order (src/save.rs:61-72).
+    bool layer(FileReader &r, qtts_layer_view *L, int32_t hidden, int32_t head_dim, const std::string &p) {
+        return q4(r, &L->q_proj, p + ".q_proj") && q4(r, &L->k_proj, p + ".k_proj") &&
+               q4(r, &L->v_proj, p + ".v_proj") && q4(r, &L->o_proj, p + ".o_proj") &&
+               gamma(r, &L->q_norm, (uint64_t)head_dim, p + ".q_norm") &&
+               gamma(r, &L->k_norm, (uint64_t)head_dim, p + ".k_norm") &&
+               q4(r, &L->gate_proj, p + ".gate_proj") && q4(r, &L->up_proj, p + ".up_proj") &&
+               q4(r, &L->down_proj, p + ".down_proj") &&
+               gamma(r, &L->input_norm_gamma, (uint64_t)hidden, p + ".input_norm") &&
+               gamma(r, &L->post_attn_norm_gamma, (uint64_t)hidden, p + ".post_attn_norm");
+    }
+    // The two RoPE tables of a section: equal lengths, whole rows of head_dim/2.
+    bool rope(FileReader &r, int32_t head_dim, const float **cs, const float **sn, int32_t *rows, const char *what) {
+        uint64_t lc, ls;
+        if (!f32_vec(r, cs, &lc, what) || !f32_vec(r, sn, &ls, what)) return false;
+        const uint64_t half = (uint64_t)head_dim / 2;
+        if (head_dim <= 0 || head_dim % 2 || lc != ls || lc == 0 || lc % half || lc / half > 0x7FFFFFFF)
+            return r.fail(std::string(what) + ": cos/sin tables of " + std::to_string(lc) + "/" + std::to_string(ls) +
+                          " values for head_dim " + std::to_string(head_dim));
+        *rows = (int32_t)(lc / half);
+        return true;
+    }
+
+    // load_talker, src/save.rs:300-351
+    bool read_talker(FileReader &r) {
+        qtts_talker_view &t = talker;
+        int32_t layers, text_hidden, sec;
+        if (!r.dim(&layers, "talker num_layers") || !r.dim(&t.hidden_size, "talker hidden_size") ||
+            !r.dim(&text_hidden, "talker text_hidden_size") || !r.dim(&t.num_heads, "talker num_heads") ||
+            !r.dim(&t.num_kv_heads, "talker num_kv_heads") || !r.dim(&t.head_dim, "talker head_dim") ||
+            !r.dim(&info.talker_num_kv_groups, "talker num_kv_groups") || !r.dim(&sec, "mrope_section length"))
+            return false;
+        if (sec > 8) return r.fail("mrope_section longer than 8");
+        info.mrope_sections = sec;
+        for (int i = 0; i < sec; i++)
+            if (!r.dim(&info.mrope_section[i], "mrope_section")) return false;
+        talker_layers.resize((size_t)layers);
+        for (int32_t l = 0; l < layers; l++)
+            if (!layer(r, &talker_layers[(size_t)l], t.hidden_size, t.head_dim, "talker.layers." + std::to_string(l)))
+                return false;
+        uint64_t len;
+        if (!q4(r, &t.codec_embedding, "talker.codec_embedding") || !q4(r, &text.text_embedding, "talker.text_embedding") ||
+            !q4(r, &text.text_proj_fc1, "talker.text_proj_fc1") ||
+            !f32_vec(r, &text.text_proj_fc1_bias, &len, "talker.text_proj_fc1_bias"))
+            return false;
+        if (len != (uint64_t)text.text_proj_fc1.n) return r.fail("talker.text_proj_fc1_bias: length mismatch");
+        if (!q4(r, &text.text_proj_fc2, "talker.text_proj_fc2") ||
+            !f32_vec(r, &text.text_proj_fc2_bias, &len, "talker.text_proj_fc2_bias"))
+            return false;
+        if (len != (uint64_t)text.text_proj_fc2.n) return r.fail("talker.text_proj_fc2_bias: length mismatch");
+        if (!q4(r, &t.codec_head, "talker.codec_head") ||
+            !gamma(r, &t.final_norm_gamma, (uint64_t)t.hidden_size, "talker.final_norm") ||
+            !rope(r, t.head_dim, &t.rope_cos, &t.rope_sin, &t.max_position, "talker rope tables"))
+            return false;
+        text.text_hidden_size = text_hidden;
+        t.num_layers = layers;
+        t.layers = talker_layers.data();
+        t.rope_theta = 0.0;  // the file's tables are used
+        return true;
+    }
+
+    // load_predictor, src/save.rs:353-409
+    bool read_predictor(FileReader &r) {
+        qtts_predictor_view &p = predictor;
+        int32_t layers, groups, heads_lm;
+        uint8_t has_proj;
+        if (!r.dim(&layers, "predictor num_layers") || !r.dim(&p.hidden_size, "predictor hidden_size") ||
+            !r.dim(&p.num_heads, "predictor num_heads") || !r.dim(&p.num_kv_heads, "predictor num_kv_heads") ||
+            !r.dim(&p.head_dim, "predictor head_dim") ||
+            !r.dim(&info.predictor_num_kv_groups, "predictor num_kv_groups") || !r.u8(&has_proj, "has_proj"))
+            return false;
+        // any flag other than 1 means "no projection" (src/save.rs:366-370)
+        info.predictor_has_input_proj = has_proj == 1;
+        if (has_proj == 1) {
+            uint64_t len;
+            if (!q4(r, &p.input_proj, "predictor.input_proj") ||
+                !f32_vec(r, &p.input_proj_bias, &len, "predictor.input_proj_bias"))
+                return false;
+            if (len != (uint64_t)p.input_proj.n) return r.fail("predictor.input_proj_bias: length mismatch");
+        }
+        if (!r.dim(&groups, "predictor codec embedding count")) return false;
+        codec_embeddings.resize((size_t)groups);
+        for (int32_t g = 0; g < groups; g++)
+            if (!q4(r, &codec_embeddings[(size_t)g], "predictor.codec_embeddings." + std::to_string(g))) return false;
+        predictor_layers.resize((size_t)layers);
+        for (int32_t l = 0; l < layers; l++)
+            if (!layer(r, &predictor_layers[(size_t)l], p.hidden_size, p.head_dim,
+                       "predictor.layers." + std::to_string(l)))
+                return false;
+        if (!r.dim(&heads_lm, "predictor lm head count")) return false;
+        lm_heads.resize((size_t)heads_lm);
+        for (int32_t g = 0; g < heads_lm; g++)
+            if (!q4(r, &lm_heads[(size_t)g], "predictor.lm_heads." + std::to_string(g))) return false;
+        if (!gamma(r, &p.final_norm_gamma, (uint64_t)p.hidden_size, "predictor.final_norm") ||
+            !rope(r, p.head_dim, &p.rope_cos, &p.rope_sin, &p.max_position, "predictor rope tables"))
+            return false;
+        p.num_groups = groups;
+        p.codec_embeddings = codec_embeddings.data();
+        p.num_layers = layers;
+        p.layers = predictor_layers.data();
+        p.lm_heads = lm_heads.data();
+        p.rope_theta = 0.0;
+        return true;
+    }
+
+    // load_conv1d / load_conv_t1d / load_dw_conv (src/save.rs:411-445):
+    // `dims` u32 fields, then weight and bias.
+    bool skip_conv(FileReader &r, int dims, const char *what) {
+        for (int i = 0; i < dims; i++) {
+            int32_t d;
+            if (!r.dim(&d, what)) return false;
+        }
+        return skip_f32_vec(r, what) && skip_f32_vec(r, what);
+    }
+    bool skip_vecs(FileReader &r, int n, const char *what) {
+        for (int i = 0; i < n; i++)
+            if (!skip_f32_vec(r, what)) return false;
+        return true;
+    }
+
+    // load_decoder_weights, src/save.rs:447-546: walked, not read.
+    bool walk_decoder(FileReader &r) {
+        qtts_file_info &d = info;
+        if (!r.dim(&d.decoder_hidden_size, "decoder hidden_size") || !r.dim(&d.decoder_num_heads, "decoder num_heads") ||
+            !r.dim(&d.decoder_head_dim, "decoder head_dim") ||
+            !r.dim(&d.decoder_intermediate_size, "decoder intermediate_size") ||
+            !r.dim(&d.decoder_sliding_window, "decoder sliding_window") ||
+            !r.dim(&d.decoder_codebook_dim, "decoder codebook_dim"))
+            return false;
+        if (!skip_vecs(r, 2, "decoder first codebook") || !r.dim(&d.decoder_rest_codebooks, "decoder codebook count") ||
+            !skip_vecs(r, d.decoder_rest_codebooks, "decoder codebooks") ||
+            !skip_vecs(r, 1, "decoder rest_output_proj") || !skip_conv(r, 6, "decoder pre_conv") ||
+            !skip_vecs(r, 2, "decoder tf_input") || !r.dim(&d.decoder_layers, "decoder layer count"))
+            return false;
+        for (int32_t l = 0; l < d.decoder_layers; l++)
+            if (!skip_vecs(r, 11, "decoder transformer layer")) return false;
+        if (!skip_vecs(r, 3, "decoder tf_norm/output") || !r.dim(&d.decoder_upsample_stages, "decoder upsample count"))
+            return false;
+        for (int32_t u = 0; u < d.decoder_upsample_stages; u++) {
+            int32_t ch;
+            if (!r.dim(&ch, "upsample channels") || !skip_conv(r, 5, "upsample conv_t") ||
+                !skip_conv(r, 3, "upsample dw_conv") || !skip_vecs(r, 7, "upsample stage"))
+                return false;
+        }
+        if (!skip_conv(r, 6, "vocos_init") || !r.dim(&d.decoder_vocos_blocks, "vocos block count")) return false;
+        for (int32_t b = 0; b < d.decoder_vocos_blocks; b++) {
+            int32_t nres;
+            if (!skip_vecs(r, 2, "vocos pre_snake") || !skip_conv(r, 5, "vocos upsample") ||
+                !r.dim(&nres, "vocos residual count"))
+                return false;
+            for (int32_t i = 0; i < nres; i++)
+                if (!skip_vecs(r, 2, "vocos act1") || !skip_conv(r, 6, "vocos conv1") ||
+                    !skip_vecs(r, 2, "vocos act2") || !skip_conv(r, 6, "vocos conv2"))
+                    return false;
+        }
+        return skip_vecs(r, 2, "final snake") && skip_conv(r, 6, "output_conv") && skip_vecs(r, 2, "decoder rope");
+    }
+};
+
+extern "C" {
+
+qtts_status qtts_model_file_open(const char *path, qtts_model_file **out) {
+    g_error.clear();
+    if (!path || !out) {
+        g_error = "null argument";
+        return QTTS_EINVAL;
+    }
+    *out = nullptr;
+    FileReader r;
+    r.f = fopen(path, "rb");
+    if (!r.f) {
+        g_error = std::string(path) + ": " + std::strerror(errno);
+        return QTTS_EINVAL;
+    }
+    qtts_status st = QTTS_OK;
+    qtts_model_file *m = nullptr;
+    try {
+        m = new qtts_model_file();
+        if (fseeko(r.f, 0, SEEK_END) != 0 || (r.size = (int64_t)ftello(r.f)) < 0 || fseeko(r.f, 0, SEEK_SET) != 0) {
+            r.fail("cannot size the file");
+        } else {
+            m->info.file_bytes = r.size;
+            // header: magic, version, format (src/save.rs:266-277)
+            char magic[4];
+            uint32_t version = 0;
+            uint8_t format = 0;
+            if (r.bytes(magic, 4, "magic") && std::memcmp(magic, "QTTS", 4) != 0) r.fail("invalid magic (expected QTTS)");
+            if (r.err.empty() && r.u32(&version, "version") && version != 1)
+                r.fail("version " + std::to_string(version) + ", expected 1");
+            if (r.err.empty() && r.u8(&format, "format")) {
+                m->info.version = version;
+                m->info.format_id = format;
+                if (format == 0) {
+                    r.fail("format 0 (f16 weights) is not supported: the loop runs Q4 weights");
+                    st = QTTS_ESHAPE;
+                } else if (format != 1) {
+                    r.fail("unknown weight format " + std::to_string(format));
+                }
+            }
+            if (r.err.empty()) {
+                m->info.talker_offset = r.pos;
+                if (m->read_talker(r)) {
+                    m->info.predictor_offset = r.pos;
+                    if (m->read_predictor(r)) {
+                        m->info.decoder_offset = r.pos;
+                        if (m->walk_decoder(r)) {
+                            m->info.decoder_end = r.pos;
+                            m->info.trailing_bytes = r.size - r.pos;
+                        }
+                    }
+                }
+            }
+            if (r.err.empty() && m->predictor.num_groups != (int32_t)m->lm_heads.size()) {
+                r.fail("predictor has " + std::to_string(m->predictor.num_groups) + " codec embeddings and " +
+                       std::to_string(m->lm_heads.size()) + " heads");
+                st = QTTS_ESHAPE;
+            }
+        }
+    } catch (const std::bad_alloc &) {
+        r.err = "out of host memory";
+        st = QTTS_ENOMEM;
+    }
+    fclose(r.f);
+    if (!r.err.empty()) {
+        delete m;
+        g_error = std::string(path) + ": " + r.err;
+        return st == QTTS_OK ? QTTS_EINVAL : st;
+    }
+    *out = m;
+    return QTTS_OK;
+}
+
+const char *qtts_model_file_error(void) { return g_error.c_str(); }
+
+void qtts_model_file_close(qtts_model_file *f) { delete f; }
+
+const qtts_talker_view *qtts_model_file_talker(const qtts_model_file *f) { return f ? &f->talker : nullptr; }
+const qtts_predictor_view *qtts_model_file_predictor(const qtts_model_file *f) { return f ? &f->predictor : nullptr; }
+const qtts_text_view *qtts_model_file_text(const qtts_model_file *f) { return f ? &f->text : nullptr; }
+const qtts_file_info *qtts_model_file_info(const qtts_model_file *f) { return f ? &f->info : nullptr; }
+
+}  // extern "C"

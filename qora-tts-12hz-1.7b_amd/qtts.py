@@ -65,6 +65,8 @@ class TalkerView(C.Structure):
         ("head_dim", C.c_int32),
         ("rope_theta", C.c_double),
         ("max_position", C.c_int32),
+        ("rope_cos", C.c_void_p),
+        ("rope_sin", C.c_void_p),
     ]
 
 
@@ -84,7 +86,36 @@ class PredictorView(C.Structure):
         ("head_dim", C.c_int32),
         ("rope_theta", C.c_double),
         ("max_position", C.c_int32),
+        ("rope_cos", C.c_void_p),
+        ("rope_sin", C.c_void_p),
     ]
+
+
+class TextView(C.Structure):
+    _fields_ = [
+        ("text_embedding", Q4View),
+        ("text_proj_fc1", Q4View),
+        ("text_proj_fc1_bias", C.c_void_p),
+        ("text_proj_fc2", Q4View),
+        ("text_proj_fc2_bias", C.c_void_p),
+        ("text_hidden_size", C.c_int32),
+    ]
+
+
+class FileInfo(C.Structure):
+    _fields_ = [
+        ("version", C.c_uint32),
+        ("format_id", C.c_uint32),
+        ("talker_num_kv_groups", C.c_int32),
+        ("predictor_num_kv_groups", C.c_int32),
+        ("mrope_sections", C.c_int32),
+        ("mrope_section", C.c_int32 * 8),
+        ("predictor_has_input_proj", C.c_int32),
+    ] + [(n, C.c_int32) for n in (
+        "decoder_hidden_size", "decoder_num_heads", "decoder_head_dim", "decoder_intermediate_size",
+        "decoder_sliding_window", "decoder_codebook_dim", "decoder_rest_codebooks", "decoder_layers",
+        "decoder_upsample_stages", "decoder_vocos_blocks")] + [(n, C.c_int64) for n in (
+        "talker_offset", "predictor_offset", "decoder_offset", "decoder_end", "file_bytes", "trailing_bytes")]
 
 
 class SamplerParams(C.Structure):
@@ -165,6 +196,13 @@ def load_library(path: str = LIB_PATH):
         "qtts_f32_to_f16": ([C.c_float], C.c_uint16),
         "qtts_f16_to_f32": ([C.c_uint16], C.c_float),
         "qtts_quantize_f32_to_q4": ([vp, i32, i32, vp, vp], None),
+        "qtts_model_file_open": ([C.c_char_p, C.POINTER(vp)], i32),
+        "qtts_model_file_error": ([], C.c_char_p),
+        "qtts_model_file_close": ([vp], None),
+        "qtts_model_file_talker": ([vp], C.POINTER(TalkerView)),
+        "qtts_model_file_predictor": ([vp], C.POINTER(PredictorView)),
+        "qtts_model_file_text": ([vp], C.POINTER(TextView)),
+        "qtts_model_file_info": ([vp], C.POINTER(FileInfo)),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -185,7 +223,8 @@ def exported_symbols() -> List[str]:
         "qtts_embed_codec_token", "qtts_predictor_upload", "qtts_predictor_free", "qtts_generate_acoustic_codes",
         "qtts_get_acoustic_embeddings_sum", "qtts_sample_token", "qtts_generate_codes", "qtts_synth_u64",
         "qtts_synth_q4", "qtts_synth_normal_f32", "qtts_synth_normal_f16", "qtts_f32_to_f16", "qtts_f16_to_f32",
-        "qtts_quantize_f32_to_q4",
+        "qtts_quantize_f32_to_q4", "qtts_model_file_open", "qtts_model_file_error", "qtts_model_file_close",
+        "qtts_model_file_talker", "qtts_model_file_predictor", "qtts_model_file_text", "qtts_model_file_info",
     ]
 
 
@@ -386,6 +425,64 @@ def _f32(a, n: Optional[int] = None) -> np.ndarray:
     if n is not None and a.size < n:
         raise ValueError(f"expected at least {n} floats, got {a.size}")
     return a
+
+
+# ---------------------------------------------------------------------------
+# .qora-tts model files (load_model, src/save.rs:262-298)
+# ---------------------------------------------------------------------------
+def q4_from_view(v: Q4View) -> Q4Weight:
+    """A host copy of a Q4 view's arrays."""
+    packed = np.ctypeslib.as_array(C.cast(v.packed, C.POINTER(C.c_uint8)), (v.k * v.n // 2,)).copy()
+    scales = np.ctypeslib.as_array(C.cast(v.scales, C.POINTER(C.c_uint16)), (v.k * v.n // 32,)).copy()
+    return Q4Weight(packed, scales, v.k, v.n)
+
+
+class _FileStack:
+    """A talker or predictor section of an open model file, usable wherever
+    TalkerWeights / CodePredictorWeights are (it has .cfg and .view())."""
+
+    def __init__(self, owner, view, cfg, **extra):
+        self._owner, self._view, self.cfg = owner, view, cfg
+        self.__dict__.update(extra)
+
+    def view(self):
+        return self._view
+
+
+class ModelFile:
+    """An opened .qora-tts file: .talker, .predictor (upload-ready views with
+    the file's RoPE tables), .text (the prompt-assembly weights) and .info."""
+
+    def __init__(self, path: str):
+        lib = load_library()
+        h = C.c_void_p()
+        rc = lib.qtts_model_file_open(os.fsencode(path), C.byref(h))
+        if rc != QTTS_OK:
+            raise QttsError(rc, lib.qtts_model_file_error().decode())
+        self.h, self._lib = h, lib
+        tv = lib.qtts_model_file_talker(h).contents
+        pv = lib.qtts_model_file_predictor(h).contents
+        self.info = lib.qtts_model_file_info(h).contents
+        self.text = lib.qtts_model_file_text(h).contents
+        l0 = tv.layers[0]
+        tcfg = StackConfig(layers=tv.num_layers, hidden=tv.hidden_size, heads=tv.num_heads,
+                           kv_heads=tv.num_kv_heads, head_dim=tv.head_dim, inter=l0.gate_proj.n,
+                           vocab=tv.codec_head.n, max_position=tv.max_position, rope_theta=0.0)
+        p0 = pv.layers[0]
+        pcfg = StackConfig(layers=pv.num_layers, hidden=pv.hidden_size, heads=pv.num_heads,
+                           kv_heads=pv.num_kv_heads, head_dim=pv.head_dim, inter=p0.gate_proj.n,
+                           vocab=pv.lm_heads[0].n, max_position=pv.max_position, rope_theta=0.0)
+        self.talker = _FileStack(self, tv, tcfg)
+        self.predictor = _FileStack(self, pv, pcfg, num_groups=pv.num_groups,
+                                    talker_hidden=pv.codec_embeddings[0].n)
+
+    def close(self):
+        if getattr(self, "h", None):
+            self._lib.qtts_model_file_close(self.h)
+            self.h = None
+
+    def __del__(self):
+        self.close()
 
 
 class Context:
