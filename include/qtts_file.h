@@ -11,12 +11,11 @@
  * Q4 weight as u64 k, u64 n, u64-counted packed bytes [k][n/2] and u64-counted
  * binary16 scales [k][n/32] (write_weight_io, src/gemv.rs:558-575).
  *
- * qtts_model_file_open reads the talker and predictor sections into host
- * memory and hands them out as the views qtts_talker_upload and
- * qtts_predictor_upload take (include/qtts.h), with the file's RoPE tables.
- * The speech decoder section is walked to check its structure and its
- * configuration is reported; its tensors are not read.  All views stay valid
- * until qtts_model_file_close.
+ * qtts_model_file_open reads the talker, predictor and speech decoder
+ * sections into host memory and hands them out as the views
+ * qtts_talker_upload, qtts_predictor_upload (include/qtts.h) and
+ * qtts_decoder_upload (include/qtts_decoder.h) take, with the file's RoPE
+ * tables.  All views stay valid until qtts_model_file_close.
  */
 #ifndef QTTS_FILE_H
 #define QTTS_FILE_H
@@ -24,6 +23,7 @@
 #include <stdint.h>
 
 #include "qtts.h"
+#include "qtts_decoder.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -73,6 +73,7 @@ const qtts_talker_view *qtts_model_file_talker(const qtts_model_file *f);
 const qtts_predictor_view *qtts_model_file_predictor(const qtts_model_file *f);
 const qtts_text_view *qtts_model_file_text(const qtts_model_file *f);
 const qtts_file_info *qtts_model_file_info(const qtts_model_file *f);
+const qtts_decoder_view *qtts_model_file_decoder(const qtts_model_file *f);
 
 #ifdef __cplusplus
 }

@@ -68,6 +68,9 @@ def load():
         "qor_generate_acoustic_codes": ([vp, vp, vp, vp, vp, i32], i32),
         "qor_get_acoustic_embeddings_sum": ([vp, vp, vp], None),
         "qor_simple_rand": ([C.POINTER(C.c_uint64)], C.c_float),
+        "qor_decoder_num_samples": ([C.POINTER(qtts.DecoderView), i32], C.c_int64),
+        "qor_decode_to_audio": ([C.POINTER(qtts.DecoderView), vp, i32, i32, vp, C.c_int64, C.POINTER(C.c_int64), i32],
+                                i32),
         "qor_argmax": ([vp, i32, C.POINTER(u32)], i32),
         "qor_sample_token": ([vp, i32, C.POINTER(qtts.SamplerParams), vp, i32, C.POINTER(C.c_uint64),
                               C.POINTER(u32)], i32),
@@ -309,3 +312,17 @@ def generate_codes(talker: Talker, predictor: Optional[CodePredictor], talker_kv
                                      position, _p(tt), tl, _p(pad), C.byref(params), seed, _p(codes), C.byref(n),
                                      nthreads))
     return codes[:, : n.value].copy()
+
+
+def decode_to_audio(w, codes, nthreads: int = 0) -> np.ndarray:
+    """decode_to_audio (src/decoder.rs:394-509) of codes [groups][frames] with
+    the decoder weights w (anything with .view() -> DecoderView)."""
+    codes = np.ascontiguousarray(codes, dtype=np.uint32)
+    frames = codes.shape[1]
+    view = w.view()
+    n_out = int(load().qor_decoder_num_samples(C.byref(view), frames))
+    out = np.empty(max(1, n_out), dtype=np.float32)
+    n = C.c_int64()
+    _check(load().qor_decode_to_audio(C.byref(view), _p(codes), frames, frames, _p(out), out.size, C.byref(n),
+                                      nthreads))
+    return out[: n.value]

@@ -17,6 +17,7 @@
 #include <stdint.h>
 
 #include "../include/qtts.h"
+#include "../include/qtts_decoder.h"
 
 #ifdef __cplusplus
 extern "C" {
@@ -107,6 +108,14 @@ int32_t qor_generate_codes(const qor_talker *t, const qor_predictor *p, qor_kv *
                            const float *trailing_text, int32_t trailing_len, const float *tts_pad_embed,
                            const qtts_loop_params *params, uint64_t seed, uint32_t *codes, int32_t *n_frames,
                            int32_t nthreads);
+
+/* --- src/decoder.rs, src/conv.rs (qtts_oracle_decoder.c) ---------------- */
+/* Samples decode_to_audio returns for `frames` frames. */
+int64_t qor_decoder_num_samples(const qtts_decoder_view *w, int32_t frames);
+/* decode_to_audio, src/decoder.rs:394-509; codes[g * ld + t].  QTTS_ERANGE
+ * for a code past the codebook or too small an output buffer. */
+int32_t qor_decode_to_audio(const qtts_decoder_view *w, const uint32_t *codes, int32_t frames, int32_t ld,
+                            float *audio, int64_t capacity, int64_t *n_samples, int32_t nthreads);
 
 #ifdef __cplusplus
 }

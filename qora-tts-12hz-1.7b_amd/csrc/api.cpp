@@ -16,6 +16,7 @@
 #include <vector>
 
 #include "../../include/qtts.h"
+#include "../../include/qtts_decoder.h"
 #include "../../include/qtts_synth.h"
 #include "engine.h"
 #include "internal.h"
@@ -2140,6 +2141,524 @@ qtts_status qtts_generate_codes(qtts_talker *t, qtts_predictor *p, qtts_kv *talk
     if (!talker_only && fin.frame > 0) predictor_kv->len = p->groups + 1;
     if (fin.status != 0) return fail(c, (qtts_status)fin.status, "NaN logits during generation");
     return QTTS_OK;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Speech decoder: decode_to_audio (src/decoder.rs:394-509) on the device.
+// The weights keep the reference's layouts; every projection and convolution
+// is one k_dec_gemm launch (csrc/decoder.hip).
+// ---------------------------------------------------------------------------
+struct qtts_decoder {
+    qtts_ctx *ctx = nullptr;
+    Owner own;
+    qtts_decoder_view w{};  // device pointers
+    std::vector<qtts_dec_layer_view> layers;
+    std::vector<qtts_upsample_view> upsample;
+    std::vector<qtts_vocos_block_view> blocks;
+    std::vector<std::vector<qtts_vocos_residual_view>> residuals;
+    const float **rest_dev = nullptr;  // device array of the rest codebooks
+    int *status = nullptr;
+    // work buffers, grown on demand
+    std::vector<float *> bufs;
+    std::vector<size_t> caps;
+    uint32_t *codes = nullptr;
+    size_t codes_cap = 0;
+    float *audio = nullptr;
+    size_t audio_cap = 0;
+    ~qtts_decoder() {
+        for (float *b : bufs) (void)hipFree(b);
+        if (codes) (void)hipFree(codes);
+        if (audio) (void)hipFree(audio);
+    }
+};
+
+namespace {
+
+qtts_status dec_up(qtts_ctx *c, Owner &own, const float *src, size_t n, const float **dst, const char *name) {
+    float *d = nullptr;
+    QTTS_TRY(upload_array(c, own, src, n, &d, name));
+    *dst = d;
+    return QTTS_OK;
+}
+
+// A convolution's weights: [out][in][k] (causal), [in][out][k] (transposed)
+// or [ch][k] (depthwise) -- the same element count but for depthwise.
+qtts_status dec_conv(qtts_ctx *c, Owner &own, const qtts_conv_view &v, bool depthwise, qtts_conv_view *d,
+                     const char *name) {
+    if (v.in_channels <= 0 || v.out_channels <= 0 || v.kernel_size <= 0)
+        return fail(c, QTTS_ESHAPE, std::string(name) + ": empty convolution");
+    *d = v;
+    const size_t wn = depthwise ? (size_t)v.out_channels * v.kernel_size
+                                : (size_t)v.in_channels * v.out_channels * v.kernel_size;
+    QTTS_TRY(dec_up(c, own, v.weight, wn, &d->weight, name));
+    return dec_up(c, own, v.bias, (size_t)v.out_channels, &d->bias, name);
+}
+
+qtts_status dec_check_transposed(qtts_ctx *c, const qtts_conv_view &v, int in_ch, const char *name) {
+    if (v.in_channels != in_ch || v.stride <= 0 || v.padding != 0 || v.kernel_size < v.stride ||
+        v.kernel_size % v.stride != 0)
+        return fail(c, QTTS_ESHAPE, std::string(name) +
+                                        ": transposed convolution needs in_channels to match, padding 0 and a "
+                                        "kernel that is a multiple of the stride");
+    return QTTS_OK;
+}
+
+float *dec_buf(qtts_decoder *d, size_t i, size_t n, qtts_status *st) {
+    if (d->bufs.size() <= i) {
+        d->bufs.resize(i + 1, nullptr);
+        d->caps.resize(i + 1, 0);
+    }
+    if (d->caps[i] < n) {
+        (void)hipStreamSynchronize(d->ctx->stream);
+        (void)hipFree(d->bufs[i]);
+        d->bufs[i] = nullptr;
+        d->caps[i] = 0;
+        if (hipMalloc(&d->bufs[i], n * sizeof(float)) != hipSuccess) {
+            *st = fail(d->ctx, QTTS_ENOMEM, "decoder work buffer");
+            return nullptr;
+        }
+        d->caps[i] = n;
+    }
+    return d->bufs[i];
+}
+
+int64_t dec_len_after(const qtts_conv_view &v, int64_t len) {
+    const int64_t full = (len - 1) * v.stride - 2 * v.padding + v.kernel_size;
+    const int64_t crop = v.kernel_size - v.stride;
+    return crop > 0 ? full - crop : full;
+}
+
+DecGemmParams dec_gemm_base(int M, int N, int K) {
+    DecGemmParams p{};
+    p.M = M;
+    p.N = N;
+    p.K = K;
+    p.epi = DEC_EPI_STORE;
+    return p;
+}
+
+// Y(m = row, n) = X[rows][K] . W[K][N] with X token-major: the transformer's
+// and ConvNeXt's projections.  Output at c[m * scm + n * scn].
+qtts_status dec_linear(qtts_decoder *d, const float *x, long long sxm, long long sxk, int rows, const float *w, int K,
+                       int N, const float *bias_n, float *c, long long scm, long long scn, int epi,
+                       const float *scale_n = nullptr, const float *resid = nullptr, int act = DEC_ACT_NONE) {
+    DecGemmParams p = dec_gemm_base(rows, N, K);
+    p.a_mode = DEC_A_STRIDED;
+    p.a = x;
+    p.sam = sxm;
+    p.sak = sxk;
+    p.a_kfast = sxk == 1;
+    p.b_mode = DEC_B_STRIDED;
+    p.b = w;
+    p.sbk = N;
+    p.sbn = 1;
+    p.bias_n = bias_n;
+    p.act = act;
+    p.epi = epi;
+    p.c = c;
+    p.scm = scm;
+    p.scn = scn;
+    p.scale_n = scale_n;
+    p.resid = resid;
+    launch_dec_gemm(d->ctx->stream, p);
+    return check_launch(d->ctx, "k_dec_gemm");
+}
+
+// Causal convolution (causal_conv1d, src/conv.rs:114-184) of x [in][len]
+// into c [out][len].
+qtts_status dec_causal(qtts_decoder *d, const qtts_conv_view &v, const float *x, int len, float *c, int epi,
+                       const float *resid = nullptr) {
+    DecGemmParams p = dec_gemm_base(v.out_channels, len, v.in_channels * v.kernel_size);
+    p.a_mode = DEC_A_STRIDED;
+    p.a = v.weight;
+    p.sam = (long long)v.in_channels * v.kernel_size;
+    p.sak = 1;
+    p.a_kfast = 1;
+    p.b_mode = DEC_B_CONV;
+    p.b = x;
+    p.ksize = v.kernel_size;
+    p.dilation = v.dilation;
+    p.in_len = len;
+    p.bias_m = v.bias;
+    p.epi = epi;
+    p.c = c;
+    p.scm = len;
+    p.scn = 1;
+    p.resid = resid;
+    launch_dec_gemm(d->ctx->stream, p);
+    return check_launch(d->ctx, "k_dec_gemm");
+}
+
+// conv_transpose1d + the causal right crop (src/conv.rs:198-268,
+// src/decoder.rs:430-444): one launch per output phase r, out[o = q*s + r].
+qtts_status dec_transposed(qtts_decoder *d, const qtts_conv_view &v, const float *x, int len, float *c) {
+    const int J = v.kernel_size / v.stride, out_len = len * v.stride;
+    for (int r = 0; r < v.stride; r++) {
+        DecGemmParams p = dec_gemm_base(v.out_channels, len, v.in_channels * J);
+        p.a_mode = DEC_A_CONVT;
+        p.a = v.weight;
+        p.a_kfast = 0;
+        p.b_mode = DEC_B_CONVT;
+        p.b = x;
+        p.ksize = v.kernel_size;
+        p.taps = J;
+        p.stride = v.stride;
+        p.phase = r;
+        p.in_len = len;
+        p.bias_m = v.bias;
+        p.c = c;
+        p.scm = out_len;
+        p.scn = 1;
+        p.out_stride = v.stride;
+        launch_dec_gemm(d->ctx->stream, p);
+        QTTS_TRY(check_launch(d->ctx, "k_dec_gemm"));
+    }
+    return QTTS_OK;
+}
+
+qtts_status dec_decode(qtts_decoder *d, const uint32_t *d_codes, int T, int ld, float *d_audio, int64_t capacity,
+                       int64_t *n_samples) {
+    qtts_ctx *c = d->ctx;
+    const qtts_decoder_view &w = d->w;
+    hipStream_t st = c->stream;
+    *n_samples = 0;
+    if (T <= 0) return QTTS_OK;
+    const int64_t need = qtts_decoder_num_samples(d, T);
+    if (need > capacity) return fail(c, QTTS_ERANGE, "audio buffer smaller than the decoded length");
+    const int cd = w.codebook_dim, vq = w.vq_dim, lat = w.pre_conv.out_channels, hid = w.hidden_size;
+    const int ad = w.num_heads * w.head_dim, inter = w.intermediate_size;
+    // the largest channel-first signal and ConvNeXt inner activation
+    size_t big = std::max((size_t)lat, (size_t)vq) * T, inner_max = 0;
+    int64_t len = T;
+    for (const auto &u : d->upsample) {
+        len = len * u.conv_t.stride;
+        big = std::max(big, (size_t)u.channels * len);
+        inner_max = std::max(inner_max, (size_t)u.inner_dim * len);
+    }
+    big = std::max(big, (size_t)w.vocos_init.out_channels * len);
+    for (const auto &b : d->blocks) {
+        len = len * b.upsample.stride;
+        big = std::max(big, (size_t)b.upsample.out_channels * len);
+    }
+    qtts_status s = QTTS_OK;
+    float *S0 = dec_buf(d, 0, big, &s), *S1 = dec_buf(d, 1, big, &s), *S2 = dec_buf(d, 2, big, &s);
+    float *S3 = dec_buf(d, 3, big, &s);
+    float *E0 = dec_buf(d, 4, (size_t)T * cd, &s), *ES = dec_buf(d, 5, (size_t)T * cd, &s);
+    float *X = dec_buf(d, 6, (size_t)T * hid, &s), *XN = dec_buf(d, 7, (size_t)T * hid, &s);
+    float *Q = dec_buf(d, 8, (size_t)T * ad, &s), *K = dec_buf(d, 9, (size_t)T * ad, &s);
+    float *V = dec_buf(d, 10, (size_t)T * ad, &s), *AO = dec_buf(d, 11, (size_t)T * ad, &s);
+    float *G = dec_buf(d, 12, (size_t)T * inter, &s), *U = dec_buf(d, 13, (size_t)T * inter, &s);
+    float *P1 = dec_buf(d, 14, std::max<size_t>(inner_max, 1), &s);
+    if (s != QTTS_OK) return s;
+
+    // 1. codebook lookup -> S0 [vq][T] (src/decoder.rs:142-189)
+    DecGatherParams g{};
+    g.codes = d_codes;
+    g.ld = ld;
+    g.cd = cd;
+    g.cb_size = w.codebook_size;
+    g.num_rest = w.num_rest;
+    g.first = w.first_codebook;
+    g.rest = d->rest_dev;
+    g.e0 = E0;
+    g.es = ES;
+    g.status = d->status;
+    launch_dec_gather(st, g, T);
+    QTTS_TRY(check_launch(c, "k_dec_gather"));
+    QTTS_TRY(dec_linear(d, E0, cd, 1, T, w.first_output_proj, cd, vq, nullptr, S0, 1, T, DEC_EPI_STORE));
+    QTTS_TRY(dec_linear(d, ES, cd, 1, T, w.rest_output_proj, cd, vq, nullptr, S0, 1, T, DEC_EPI_ACCUM));
+    // 2. pre-conv -> S1 [lat][T]
+    QTTS_TRY(dec_causal(d, w.pre_conv, S0, T, S1, DEC_EPI_STORE));
+    // 3. transformer (src/decoder.rs:195-330) -> S0 [lat][T]
+    QTTS_TRY(dec_linear(d, S1, 1, T, T, w.tf_input_w, lat, hid, w.tf_input_b, X, hid, 1, DEC_EPI_STORE));
+    DecAttnParams a{};
+    a.q = Q;
+    a.k = K;
+    a.v = V;
+    a.out = AO;
+    a.T = T;
+    a.heads = w.num_heads;
+    a.hd = w.head_dim;
+    a.window = w.sliding_window;
+    a.scale = 1.0f / sqrtf((float)w.head_dim);
+    for (const auto &L : d->layers) {
+        launch_dec_rmsnorm(st, X, L.input_norm, T, hid, 1e-5f, XN);
+        QTTS_TRY(check_launch(c, "k_dec_rmsnorm"));
+        QTTS_TRY(dec_linear(d, XN, hid, 1, T, L.q_proj, hid, ad, nullptr, Q, ad, 1, DEC_EPI_STORE));
+        QTTS_TRY(dec_linear(d, XN, hid, 1, T, L.k_proj, hid, ad, nullptr, K, ad, 1, DEC_EPI_STORE));
+        QTTS_TRY(dec_linear(d, XN, hid, 1, T, L.v_proj, hid, ad, nullptr, V, ad, 1, DEC_EPI_STORE));
+        launch_dec_rope(st, Q, K, T, w.num_heads, w.head_dim, w.rope_cos, w.rope_sin, w.rope_rows);
+        QTTS_TRY(check_launch(c, "k_dec_rope"));
+        launch_dec_attn(st, a);
+        QTTS_TRY(check_launch(c, "k_dec_attn"));
+        QTTS_TRY(dec_linear(d, AO, ad, 1, T, L.o_proj, ad, hid, nullptr, X, hid, 1, DEC_EPI_SCALED_RESID,
+                            L.attn_scale));
+        launch_dec_rmsnorm(st, X, L.post_attn_norm, T, hid, 1e-5f, XN);
+        QTTS_TRY(check_launch(c, "k_dec_rmsnorm"));
+        QTTS_TRY(dec_linear(d, XN, hid, 1, T, L.gate_proj, hid, inter, nullptr, G, inter, 1, DEC_EPI_STORE));
+        QTTS_TRY(dec_linear(d, XN, hid, 1, T, L.up_proj, hid, inter, nullptr, U, inter, 1, DEC_EPI_STORE));
+        launch_dec_swiglu(st, G, U, (size_t)T * inter, G);
+        QTTS_TRY(check_launch(c, "k_dec_swiglu"));
+        QTTS_TRY(dec_linear(d, G, inter, 1, T, L.down_proj, inter, hid, nullptr, X, hid, 1, DEC_EPI_SCALED_RESID,
+                            L.mlp_scale));
+    }
+    launch_dec_rmsnorm(st, X, w.tf_norm, T, hid, 1e-5f, XN);
+    QTTS_TRY(check_launch(c, "k_dec_rmsnorm"));
+    QTTS_TRY(dec_linear(d, XN, hid, 1, T, w.tf_output_w, hid, lat, w.tf_output_b, S0, 1, T, DEC_EPI_STORE));
+    // 4. upsample: transposed conv + ConvNeXt (src/decoder.rs:336-388, 424-448)
+    float *const pool[4] = {S0, S1, S2, S3};
+    auto other = [&](const float *a, const float *b = nullptr, const float *c3 = nullptr) {
+        for (float *p : pool)
+            if (p != a && p != b && p != c3) return p;
+        return (float *)nullptr;
+    };
+    float *sig = S0;
+    int L = T;
+    for (const auto &u : d->upsample) {
+        float *up = other(sig), *dw = other(sig, up), *nrm = other(sig, up, dw);
+        QTTS_TRY(dec_transposed(d, u.conv_t, sig, L, up));
+        L *= u.conv_t.stride;
+        launch_dec_dwconv(st, up, u.dw_conv.weight, u.dw_conv.bias, u.channels, L, u.dw_conv.kernel_size, dw);
+        QTTS_TRY(check_launch(c, "k_dec_dwconv"));
+        launch_dec_lnorm(st, dw, u.norm_w, u.norm_b, u.channels, L, 1e-5f, nrm);
+        QTTS_TRY(check_launch(c, "k_dec_lnorm"));
+        QTTS_TRY(dec_linear(d, nrm, 1, L, L, u.pw1_w, u.channels, u.inner_dim, u.pw1_b, P1, u.inner_dim, 1,
+                            DEC_EPI_STORE, nullptr, nullptr, DEC_ACT_GELU));
+        // out = residual + gamma * pw2 (the residual is the stage input `up`)
+        QTTS_TRY(dec_linear(d, P1, u.inner_dim, 1, L, u.pw2_w, u.inner_dim, u.channels, u.pw2_b, dw, 1, L,
+                            DEC_EPI_RESID_IN, u.gamma, up));
+        sig = dw;
+    }
+    // 5. Vocos (src/decoder.rs:450-495)
+    {
+        float *o = other(sig);
+        QTTS_TRY(dec_causal(d, w.vocos_init, sig, L, o, DEC_EPI_STORE));
+        sig = o;
+    }
+    for (const auto &b : d->blocks) {
+        const int cin = b.upsample.in_channels, cout = b.upsample.out_channels;
+        float *t1 = other(sig), *nxt = other(sig, t1);
+        launch_dec_snake(st, sig, b.pre_snake_alpha, b.pre_snake_beta, cin, L, t1);
+        QTTS_TRY(check_launch(c, "k_dec_snake"));
+        QTTS_TRY(dec_transposed(d, b.upsample, t1, L, nxt));
+        L *= b.upsample.stride;
+        sig = nxt;
+        float *t2 = other(sig, t1);
+        for (int r = 0; r < b.num_residuals; r++) {
+            const qtts_vocos_residual_view &rv = b.residuals[r];
+            launch_dec_snake(st, sig, rv.act1_alpha, rv.act1_beta, cout, L, t1);
+            QTTS_TRY(check_launch(c, "k_dec_snake"));
+            QTTS_TRY(dec_causal(d, rv.conv1, t1, L, t2, DEC_EPI_STORE));
+            launch_dec_snake(st, t2, rv.act2_alpha, rv.act2_beta, cout, L, t1);
+            QTTS_TRY(check_launch(c, "k_dec_snake"));
+            // signal = conv2 + residual, in place (each output reads its own residual first)
+            QTTS_TRY(dec_causal(d, rv.conv2, t1, L, sig, DEC_EPI_RESID_IN, sig));
+        }
+    }
+    float *t1 = other(sig);
+    // 6. final SnakeBeta, output conv, clamp to [-1, 1]
+    launch_dec_snake(st, sig, w.final_snake_alpha, w.final_snake_beta, w.output_conv.in_channels, L, t1);
+    QTTS_TRY(check_launch(c, "k_dec_snake"));
+    QTTS_TRY(dec_causal(d, w.output_conv, t1, L, d_audio, DEC_EPI_CLAMP));
+    *n_samples = (int64_t)L * w.output_conv.out_channels;
+    return QTTS_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+qtts_status qtts_decoder_upload(qtts_ctx *c, const qtts_decoder_view *v, qtts_decoder **out) {
+    if (!c || !v || !out) return QTTS_EINVAL;
+    *out = nullptr;
+    qtts_decoder *d = new qtts_decoder();
+    d->ctx = ctx_retain(c);
+    auto bail = [&](qtts_status s) {
+        delete d;
+        ctx_release(c);
+        return s;
+    };
+    Owner &o = d->own;
+    qtts_decoder_view &w = d->w;
+    w = *v;
+    const int cd = v->codebook_dim, vq = v->vq_dim, hid = v->hidden_size, ad = v->num_heads * v->head_dim;
+    const int inter = v->intermediate_size, lat = v->pre_conv.out_channels;
+    if (cd <= 0 || vq <= 0 || hid <= 0 || v->num_heads <= 0 || v->head_dim <= 0 || v->head_dim % 2 || inter <= 0 ||
+        v->codebook_size <= 0 || v->num_rest < 0 || v->sliding_window <= 0 || v->num_layers < 0 ||
+        v->rope_rows < 0)
+        return bail(fail(c, QTTS_ESHAPE, "decoder: bad configuration"));
+    if (v->head_dim > kDecMaxHeadDim || v->sliding_window > kDecMaxWindow)
+        return bail(fail(c, QTTS_ESHAPE, "decoder: head_dim or sliding_window above the attention kernel's limit"));
+    if (v->pre_conv.in_channels != vq) return bail(fail(c, QTTS_ESHAPE, "decoder: pre_conv input != vq_dim"));
+    qtts_status s;
+    auto up = [&](const float *src, size_t n, const float **dst, const char *name) {
+        return dec_up(c, o, src, n, dst, name);
+    };
+    const size_t cbn = (size_t)v->codebook_size * cd;
+    if ((s = up(v->first_codebook, cbn, &w.first_codebook, "first_codebook")) != QTTS_OK ||
+        (s = up(v->first_output_proj, (size_t)cd * vq, &w.first_output_proj, "first_output_proj")) != QTTS_OK ||
+        (s = up(v->rest_output_proj, (size_t)cd * vq, &w.rest_output_proj, "rest_output_proj")) != QTTS_OK)
+        return bail(s);
+    std::vector<const float *> rest((size_t)std::max(v->num_rest, 1), nullptr);
+    for (int g = 0; g < v->num_rest; g++)
+        if (!v->rest_codebooks || (s = up(v->rest_codebooks[g], cbn, &rest[g], "rest_codebook")) != QTTS_OK)
+            return bail(s != QTTS_OK ? s : fail(c, QTTS_EINVAL, "rest_codebooks: null"));
+    if ((s = o.alloc(c, &d->rest_dev, rest.size())) != QTTS_OK) return bail(s);
+    if (hipMemcpy(d->rest_dev, rest.data(), rest.size() * sizeof(float *), hipMemcpyHostToDevice) != hipSuccess)
+        return bail(fail(c, QTTS_EDEVICE, "hipMemcpy"));
+    w.rest_codebooks = nullptr;
+    if ((s = dec_conv(c, o, v->pre_conv, false, &w.pre_conv, "pre_conv")) != QTTS_OK) return bail(s);
+    if ((s = up(v->tf_input_w, (size_t)lat * hid, &w.tf_input_w, "tf_input_w")) != QTTS_OK ||
+        (s = up(v->tf_input_b, (size_t)hid, &w.tf_input_b, "tf_input_b")) != QTTS_OK ||
+        (s = up(v->tf_norm, (size_t)hid, &w.tf_norm, "tf_norm")) != QTTS_OK ||
+        (s = up(v->tf_output_w, (size_t)hid * lat, &w.tf_output_w, "tf_output_w")) != QTTS_OK ||
+        (s = up(v->tf_output_b, (size_t)lat, &w.tf_output_b, "tf_output_b")) != QTTS_OK)
+        return bail(s);
+    for (int l = 0; l < v->num_layers; l++) {
+        const qtts_dec_layer_view &L = v->layers[l];
+        qtts_dec_layer_view D{};
+        if ((s = up(L.q_proj, (size_t)hid * ad, &D.q_proj, "q_proj")) != QTTS_OK ||
+            (s = up(L.k_proj, (size_t)hid * ad, &D.k_proj, "k_proj")) != QTTS_OK ||
+            (s = up(L.v_proj, (size_t)hid * ad, &D.v_proj, "v_proj")) != QTTS_OK ||
+            (s = up(L.o_proj, (size_t)ad * hid, &D.o_proj, "o_proj")) != QTTS_OK ||
+            (s = up(L.gate_proj, (size_t)hid * inter, &D.gate_proj, "gate_proj")) != QTTS_OK ||
+            (s = up(L.up_proj, (size_t)hid * inter, &D.up_proj, "up_proj")) != QTTS_OK ||
+            (s = up(L.down_proj, (size_t)inter * hid, &D.down_proj, "down_proj")) != QTTS_OK ||
+            (s = up(L.input_norm, (size_t)hid, &D.input_norm, "input_norm")) != QTTS_OK ||
+            (s = up(L.post_attn_norm, (size_t)hid, &D.post_attn_norm, "post_attn_norm")) != QTTS_OK ||
+            (s = up(L.attn_scale, (size_t)hid, &D.attn_scale, "attn_scale")) != QTTS_OK ||
+            (s = up(L.mlp_scale, (size_t)hid, &D.mlp_scale, "mlp_scale")) != QTTS_OK)
+            return bail(s);
+        d->layers.push_back(D);
+    }
+    w.layers = nullptr;
+    int ch = lat;
+    for (int i = 0; i < v->num_upsample; i++) {
+        const qtts_upsample_view &U = v->upsample[i];
+        qtts_upsample_view D = U;
+        if (U.channels != ch || U.conv_t.out_channels != ch || U.dw_conv.out_channels != ch || U.inner_dim <= 0)
+            return bail(fail(c, QTTS_ESHAPE, "decoder: upsample stage channels do not chain"));
+        if ((s = dec_check_transposed(c, U.conv_t, ch, "upsample conv_t")) != QTTS_OK) return bail(s);
+        if ((s = dec_conv(c, o, U.conv_t, false, &D.conv_t, "upsample conv_t")) != QTTS_OK ||
+            (s = dec_conv(c, o, U.dw_conv, true, &D.dw_conv, "upsample dw_conv")) != QTTS_OK ||
+            (s = up(U.norm_w, (size_t)ch, &D.norm_w, "norm_w")) != QTTS_OK ||
+            (s = up(U.norm_b, (size_t)ch, &D.norm_b, "norm_b")) != QTTS_OK ||
+            (s = up(U.pw1_w, (size_t)ch * U.inner_dim, &D.pw1_w, "pw1_w")) != QTTS_OK ||
+            (s = up(U.pw1_b, (size_t)U.inner_dim, &D.pw1_b, "pw1_b")) != QTTS_OK ||
+            (s = up(U.pw2_w, (size_t)U.inner_dim * ch, &D.pw2_w, "pw2_w")) != QTTS_OK ||
+            (s = up(U.pw2_b, (size_t)ch, &D.pw2_b, "pw2_b")) != QTTS_OK ||
+            (s = up(U.gamma, (size_t)ch, &D.gamma, "gamma")) != QTTS_OK)
+            return bail(s);
+        d->upsample.push_back(D);
+    }
+    w.upsample = nullptr;
+    if (v->vocos_init.in_channels != ch) return bail(fail(c, QTTS_ESHAPE, "decoder: vocos_init input channels"));
+    if ((s = dec_conv(c, o, v->vocos_init, false, &w.vocos_init, "vocos_init")) != QTTS_OK) return bail(s);
+    ch = v->vocos_init.out_channels;
+    d->residuals.resize((size_t)std::max(v->num_vocos_blocks, 0));
+    for (int b = 0; b < v->num_vocos_blocks; b++) {
+        const qtts_vocos_block_view &B = v->vocos_blocks[b];
+        qtts_vocos_block_view D = B;
+        if ((s = dec_check_transposed(c, B.upsample, ch, "vocos upsample")) != QTTS_OK) return bail(s);
+        if ((s = up(B.pre_snake_alpha, (size_t)ch, &D.pre_snake_alpha, "pre_snake_alpha")) != QTTS_OK ||
+            (s = up(B.pre_snake_beta, (size_t)ch, &D.pre_snake_beta, "pre_snake_beta")) != QTTS_OK ||
+            (s = dec_conv(c, o, B.upsample, false, &D.upsample, "vocos upsample")) != QTTS_OK)
+            return bail(s);
+        ch = B.upsample.out_channels;
+        for (int r = 0; r < B.num_residuals; r++) {
+            const qtts_vocos_residual_view &R = B.residuals[r];
+            qtts_vocos_residual_view E = R;
+            if (R.conv1.in_channels != ch || R.conv1.out_channels != ch || R.conv2.in_channels != ch ||
+                R.conv2.out_channels != ch)
+                return bail(fail(c, QTTS_ESHAPE, "decoder: residual convolutions must keep the channels"));
+            if ((s = up(R.act1_alpha, (size_t)ch, &E.act1_alpha, "act1_alpha")) != QTTS_OK ||
+                (s = up(R.act1_beta, (size_t)ch, &E.act1_beta, "act1_beta")) != QTTS_OK ||
+                (s = up(R.act2_alpha, (size_t)ch, &E.act2_alpha, "act2_alpha")) != QTTS_OK ||
+                (s = up(R.act2_beta, (size_t)ch, &E.act2_beta, "act2_beta")) != QTTS_OK ||
+                (s = dec_conv(c, o, R.conv1, false, &E.conv1, "residual conv1")) != QTTS_OK ||
+                (s = dec_conv(c, o, R.conv2, false, &E.conv2, "residual conv2")) != QTTS_OK)
+                return bail(s);
+            d->residuals[b].push_back(E);
+        }
+        D.residuals = d->residuals[b].data();
+        d->blocks.push_back(D);
+    }
+    w.vocos_blocks = nullptr;
+    if (v->output_conv.in_channels != ch) return bail(fail(c, QTTS_ESHAPE, "decoder: output_conv input channels"));
+    if ((s = up(v->final_snake_alpha, (size_t)ch, &w.final_snake_alpha, "final_snake_alpha")) != QTTS_OK ||
+        (s = up(v->final_snake_beta, (size_t)ch, &w.final_snake_beta, "final_snake_beta")) != QTTS_OK ||
+        (s = dec_conv(c, o, v->output_conv, false, &w.output_conv, "output_conv")) != QTTS_OK)
+        return bail(s);
+    const size_t rn = (size_t)v->rope_rows * (v->head_dim / 2);
+    if (rn) {
+        if ((s = up(v->rope_cos, rn, &w.rope_cos, "rope_cos")) != QTTS_OK ||
+            (s = up(v->rope_sin, rn, &w.rope_sin, "rope_sin")) != QTTS_OK)
+            return bail(s);
+    }
+    if ((s = o.alloc(c, &d->status, 1)) != QTTS_OK) return bail(s);
+    if (hipMemset(d->status, 0, sizeof(int)) != hipSuccess) return bail(fail(c, QTTS_EDEVICE, "hipMemset"));
+    *out = d;
+    return QTTS_OK;
+}
+
+void qtts_decoder_free(qtts_decoder *d) {
+    if (!d) return;
+    qtts_ctx *c = d->ctx;
+    if (c) (void)hipStreamSynchronize(c->stream);
+    delete d;
+    if (c) ctx_release(c);
+}
+
+int64_t qtts_decoder_num_samples(const qtts_decoder *d, int32_t frames) {
+    if (!d || frames <= 0) return 0;
+    int64_t len = frames;
+    for (const auto &u : d->upsample) len = dec_len_after(u.conv_t, len);
+    for (const auto &b : d->blocks) len = dec_len_after(b.upsample, len);
+    return len * d->w.output_conv.out_channels;
+}
+
+qtts_status qtts_decode_to_audio_device(qtts_decoder *d, const uint32_t *d_codes, int32_t frames, int32_t ld,
+                                        float *d_audio, int64_t capacity, int64_t *n_samples) {
+    if (!d || !n_samples || (frames > 0 && (!d_codes || !d_audio || ld < frames))) return QTTS_EINVAL;
+    return dec_decode(d, d_codes, frames, ld, d_audio, capacity, n_samples);
+}
+
+qtts_status qtts_decode_to_audio(qtts_decoder *d, const uint32_t *codes, int32_t frames, int32_t ld, float *audio,
+                                 int64_t capacity, int64_t *n_samples) {
+    if (!d || !n_samples || (frames > 0 && (!codes || !audio || ld < frames))) return QTTS_EINVAL;
+    qtts_ctx *c = d->ctx;
+    *n_samples = 0;
+    if (frames <= 0) return QTTS_OK;
+    const int groups = d->w.num_rest + 1;
+    for (int g = 0; g < groups; g++)
+        for (int t = 0; t < frames; t++)
+            if (codes[(size_t)g * ld + t] >= (uint32_t)d->w.codebook_size)
+                return fail(c, QTTS_ERANGE, "code beyond the codebook");
+    const int64_t need = qtts_decoder_num_samples(d, frames);
+    if (need > capacity) return fail(c, QTTS_ERANGE, "audio buffer smaller than the decoded length");
+    const size_t ncodes = (size_t)groups * frames;
+    if (d->codes_cap < ncodes) {
+        (void)hipFree(d->codes);
+        d->codes = nullptr;
+        d->codes_cap = 0;
+        HIP_TRY(c, hipMalloc(&d->codes, ncodes * sizeof(uint32_t)));
+        d->codes_cap = ncodes;
+    }
+    if (d->audio_cap < (size_t)need) {
+        (void)hipFree(d->audio);
+        d->audio = nullptr;
+        d->audio_cap = 0;
+        HIP_TRY(c, hipMalloc(&d->audio, (size_t)need * sizeof(float)));
+        d->audio_cap = (size_t)need;
+    }
+    for (int g = 0; g < groups; g++)
+        HIP_TRY(c, hipMemcpyAsync(d->codes + (size_t)g * frames, codes + (size_t)g * ld, frames * sizeof(uint32_t),
+                                  hipMemcpyHostToDevice, c->stream));
+    QTTS_TRY(dec_decode(d, d->codes, frames, frames, d->audio, need, n_samples));
+    HIP_TRY(c, hipMemcpyAsync(audio, d->audio, (size_t)*n_samples * sizeof(float), hipMemcpyDeviceToHost, c->stream));
+    return sync(c);
 }
 
 }  // extern "C"

@@ -1,0 +1,315 @@
+// decoder.hip — the speech decoder's kernels (decode_to_audio,
+// src/decoder.rs:394-509), all f32 like the reference.
+//
+//  k_dec_gather   codebook rows of every frame: group 0's, and the sum of
+//                 the other groups' in group order (src/decoder.rs:142-189)
+//  k_dec_gemm     one f32 tile GEMM for every projection and convolution:
+//                 64 x 64 output tiles, 16-deep K slices staged in LDS, 4 x 4
+//                 outputs per thread; operands are strided views or gathers
+//                 (a causal convolution's shifted input rows; one output
+//                 phase of a transposed convolution), with fused epilogues
+//  k_dec_rmsnorm  rms_norm_f32 per frame (src/decoder.rs:515-525)
+//  k_dec_rope     apply_rope_split_half of q and k (src/decoder.rs:556-578)
+//  k_dec_attn     causal sliding-window attention, one wave per (frame, head)
+//  k_dec_swiglu   silu(gate) * up
+//  k_dec_dwconv   causal depthwise convolution (src/conv.rs:280-345)
+//  k_dec_lnorm    channel-first LayerNorm per time step, channels summed in
+//                 order (src/decoder.rs:580-602)
+//  k_dec_snake    SnakeBeta (src/conv.rs:347-400)
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+
+#include "device_common.h"
+#include "internal.h"
+
+namespace qtts {
+
+namespace {
+
+constexpr int TM = 64, TN = 64, TK = 16;
+
+__global__ void k_dec_gather(DecGatherParams P) {
+    const int t = blockIdx.x, cd = P.cd;
+    for (int d = threadIdx.x; d < cd; d += blockDim.x) {
+        uint32_t c0 = P.codes[t];
+        if (c0 >= (uint32_t)P.cb_size) {
+            if (d == 0) atomicOr(P.status, 1);
+            c0 = 0;
+        }
+        P.e0[(size_t)t * cd + d] = P.first[(size_t)c0 * cd + d];
+        float s = 0.0f;
+        for (int g = 0; g < P.num_rest; g++) {
+            uint32_t c = P.codes[(size_t)(g + 1) * P.ld + t];
+            if (c >= (uint32_t)P.cb_size) {
+                if (d == 0) atomicOr(P.status, 1);
+                c = 0;
+            }
+            s += P.rest[g][(size_t)c * cd + d];
+        }
+        P.es[(size_t)t * cd + d] = s;
+    }
+}
+
+// A(m, k) and B(k, n) of the GEMM.
+__device__ __forceinline__ float dec_a(const DecGemmParams &P, int m, int k) {
+    if (m >= P.M || k >= P.K) return 0.0f;
+    if (P.a_mode == DEC_A_STRIDED) return P.a[(size_t)m * P.sam + (size_t)k * P.sak];
+    // DEC_A_CONVT: W[ci][m][phase + j * stride], k = ci * J + j
+    const int ci = k / P.taps, j = k - ci * P.taps;
+    return P.a[((size_t)ci * P.M + m) * P.ksize + P.phase + j * P.stride];
+}
+
+__device__ __forceinline__ float dec_b(const DecGemmParams &P, int k, int n) {
+    if (k >= P.K || n >= P.N) return 0.0f;
+    if (P.b_mode == DEC_B_STRIDED) return P.b[(size_t)k * P.sbk + (size_t)n * P.sbn];
+    if (P.b_mode == DEC_B_CONV) {
+        // causal convolution: x[ci][n + tap * dilation - (ksize - 1) * dilation]
+        const int ci = k / P.ksize, tap = k - ci * P.ksize;
+        const int p = n + (tap - (P.ksize - 1)) * P.dilation;
+        return p >= 0 ? P.b[(size_t)ci * P.in_len + p] : 0.0f;
+    }
+    // DEC_B_CONVT: x[ci][n - j], k = ci * J + j
+    const int ci = k / P.taps, j = k - ci * P.taps;
+    const int p = n - j;
+    return (p >= 0 && p < P.in_len) ? P.b[(size_t)ci * P.in_len + p] : 0.0f;
+}
+
+__device__ __forceinline__ float dec_gelu(float x) { return x * 0.5f * (1.0f + tanhf(x * 0.7071067811865476f)); }
+
+__global__ __launch_bounds__(256) void k_dec_gemm(DecGemmParams P) {
+    __shared__ float As[TK][TM + 4];
+    __shared__ float Bs[TK][TN + 4];
+    const int tid = threadIdx.x;
+    const int m0 = blockIdx.y * TM, n0 = blockIdx.x * TN;
+    const int tm = (tid >> 4) * 4, tn = (tid & 15) * 4;
+    float acc[4][4] = {};
+    for (int k0 = 0; k0 < P.K; k0 += TK) {
+        // 1024 A and 1024 B values per slice, 4 per thread; consecutive
+        // threads take consecutive addresses of the operand's fast index
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int e = tid + 256 * i;
+            int mm, kk;
+            if (P.a_kfast) {
+                kk = e & (TK - 1);
+                mm = e >> 4;
+            } else {
+                mm = e & (TM - 1);
+                kk = e >> 6;
+            }
+            As[kk][mm] = dec_a(P, m0 + mm, k0 + kk);
+            const int nn = e & (TN - 1), kb = e >> 6;
+            Bs[kb][nn] = dec_b(P, k0 + kb, n0 + nn);
+        }
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < TK; kk++) {
+            const float4 a = *reinterpret_cast<const float4 *>(&As[kk][tm]);
+            const float4 b = *reinterpret_cast<const float4 *>(&Bs[kk][tn]);
+            const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+#pragma unroll
+                for (int j = 0; j < 4; j++) acc[i][j] += av[i] * bv[j];
+        }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int m = m0 + tm + i;
+        if (m >= P.M) continue;
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int n = n0 + tn + j;
+            if (n >= P.N) continue;
+            float v = acc[i][j];
+            if (P.bias_m) v += P.bias_m[m];
+            if (P.bias_n) v += P.bias_n[n];
+            if (P.act == DEC_ACT_GELU) v = dec_gelu(v);
+            const int col = P.out_stride ? n * P.out_stride + P.phase : n;
+            float *dst = P.c + (size_t)m * P.scm + (size_t)col * P.scn;
+            switch (P.epi) {
+                case DEC_EPI_STORE: *dst = v; break;
+                case DEC_EPI_ACCUM: *dst += v; break;
+                case DEC_EPI_SCALED_RESID: *dst += P.scale_n[n] * v; break;
+                case DEC_EPI_RESID_IN:
+                    *dst = P.resid[(size_t)m * P.scm + (size_t)col * P.scn] + (P.scale_n ? P.scale_n[n] * v : v);
+                    break;
+                default: *dst = v < -1.0f ? -1.0f : (v > 1.0f ? 1.0f : v); break;  // DEC_EPI_CLAMP (NaN stays)
+            }
+        }
+    }
+}
+
+// rms_norm_f32 of each of `rows` rows of n values: one block per row.
+__global__ __launch_bounds__(256) void k_dec_rmsnorm(const float *x, const float *gamma, int n, float eps, float *out) {
+    __shared__ float red[4];
+    const float *r = x + (size_t)blockIdx.x * n;
+    float ss = 0.0f;
+    for (int i = threadIdx.x; i < n; i += 256) ss += r[i] * r[i];
+    ss = wave_sum(ss);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    ss = (red[0] + red[1]) + (red[2] + red[3]);
+    const float inv = 1.0f / sqrtf(ss / (float)n + eps);
+    for (int i = threadIdx.x; i < n; i += 256) out[(size_t)blockIdx.x * n + i] = r[i] * inv * gamma[i];
+}
+
+// Split-half rotation of q and k at position = frame; no rotation past the
+// table.  One thread per (frame, head, pair).
+__global__ void k_dec_rope(float *q, float *k, int T, int heads, int hd, const float *cs, const float *sn, int rows) {
+    const int half = hd / 2;
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (size_t)T * heads * half) return;
+    const int i = (int)(idx % half), h = (int)(idx / half % heads), t = (int)(idx / half / heads);
+    if (t >= rows) return;
+    const float c = cs[(size_t)t * half + i], s = sn[(size_t)t * half + i];
+    float *qb = q + (size_t)t * heads * hd + (size_t)h * hd, *kb = k + (size_t)t * heads * hd + (size_t)h * hd;
+    float x0 = qb[i], x1 = qb[half + i];
+    qb[i] = x0 * c - x1 * s;
+    qb[half + i] = x1 * c + x0 * s;
+    x0 = kb[i], x1 = kb[half + i];
+    kb[i] = x0 * c - x1 * s;
+    kb[half + i] = x1 * c + x0 * s;
+}
+
+// Causal sliding-window attention (src/decoder.rs:248-275): one wave per
+// (frame t, head h); scores over positions max(0, t+1-window) .. t, softmax,
+// then out[d] = sum over positions in order of p * v[d] (lane = d).
+__global__ __launch_bounds__(256) void k_dec_attn(DecAttnParams P) {
+    __shared__ float ps[4][kDecMaxWindow];
+    __shared__ float qs[4][kDecMaxHeadDim];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int pair = blockIdx.x * 4 + wave;
+    const bool valid = pair < P.T * P.heads;  // wave-uniform; every wave reaches both barriers
+    const int t = valid ? pair / P.heads : 0, h = valid ? pair - t * P.heads : 0;
+    const int ad = P.heads * P.hd;
+    const int start = t + 1 > P.window ? t + 1 - P.window : 0, n = t + 1 - start;
+    if (valid)
+        for (int d = lane; d < P.hd; d += 64) qs[wave][d] = P.q[(size_t)t * ad + (size_t)h * P.hd + d];
+    __syncthreads();
+    float inv = 0.0f;
+    if (valid) {
+        float mx = -INFINITY;
+        for (int s = lane; s < n; s += 64) {
+            const float *k = P.k + (size_t)(start + s) * ad + (size_t)h * P.hd;
+            float dot = 0.0f;
+            for (int d = 0; d < P.hd; d++) dot += qs[wave][d] * k[d];
+            dot *= P.scale;
+            ps[wave][s] = dot;
+            mx = fmaxf(mx, dot);
+        }
+        mx = wave_max(mx);
+        float sum = 0.0f;
+        for (int s = lane; s < n; s += 64) {
+            const float e = expf(ps[wave][s] - mx);
+            ps[wave][s] = e;
+            sum += e;
+        }
+        inv = 1.0f / wave_sum(sum);
+    }
+    __syncthreads();
+    if (valid)
+        for (int d = lane; d < P.hd; d += 64) {
+            float o = 0.0f;
+            for (int s = 0; s < n; s++) o += (ps[wave][s] * inv) * P.v[(size_t)(start + s) * ad + (size_t)h * P.hd + d];
+            P.out[(size_t)t * ad + (size_t)h * P.hd + d] = o;
+        }
+}
+
+__global__ void k_dec_swiglu(const float *g, const float *u, size_t n, float *out) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
+}
+
+// Causal depthwise convolution (padding kernel_size - 1), channel-first.
+__global__ void k_dec_dwconv(const float *x, const float *w, const float *b, int ch, int len, int ks, float *out) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)ch * len) return;
+    const int c = (int)(i / len), o = (int)(i - (size_t)c * len);
+    float s = b[c];
+    for (int k = 0; k < ks; k++) {
+        const int p = o + k - (ks - 1);
+        if (p >= 0) s += x[(size_t)c * len + p] * w[(size_t)c * ks + k];
+    }
+    out[i] = s;
+}
+
+// LayerNorm across channels at each time step (one thread per step; the
+// channel sums run in channel order).
+__global__ void k_dec_lnorm(const float *x, const float *g, const float *b, int ch, int len, float eps, float *out) {
+    const int t = blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= len) return;
+    float mean = 0.0f;
+    for (int c = 0; c < ch; c++) mean += x[(size_t)c * len + t];
+    mean /= (float)ch;
+    float var = 0.0f;
+    for (int c = 0; c < ch; c++) {
+        const float d = x[(size_t)c * len + t] - mean;
+        var += d * d;
+    }
+    const float inv = 1.0f / sqrtf(var / (float)ch + eps);
+    for (int c = 0; c < ch; c++) out[(size_t)c * len + t] = (x[(size_t)c * len + t] - mean) * inv * g[c] + b[c];
+}
+
+// x + exp(-beta) * sin(exp(alpha) * x)^2 per channel, channel-first.
+__global__ void k_dec_snake(const float *x, const float *alpha, const float *beta, int ch, int len, float *out) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (size_t)ch * len) return;
+    const int c = (int)(i / len);
+    const float a = expf(alpha[c]), inv_b = expf(-beta[c]);
+    const float v = x[i], s = sinf(a * v);
+    out[i] = v + inv_b * s * s;
+}
+
+unsigned blocks_for(size_t n, unsigned per) { return (unsigned)((n + per - 1) / per); }
+
+}  // namespace
+
+void launch_dec_gather(hipStream_t st, const DecGatherParams &p, int frames) {
+    hipLaunchKernelGGL(k_dec_gather, dim3((unsigned)frames), dim3(256), 0, st, p);
+}
+
+void launch_dec_gemm(hipStream_t st, const DecGemmParams &p) {
+    const dim3 grid(blocks_for((size_t)p.N, TN), blocks_for((size_t)p.M, TM));
+    hipLaunchKernelGGL(k_dec_gemm, grid, dim3(256), 0, st, p);
+}
+
+void launch_dec_rmsnorm(hipStream_t st, const float *x, const float *gamma, int rows, int n, float eps, float *out) {
+    hipLaunchKernelGGL(k_dec_rmsnorm, dim3((unsigned)rows), dim3(256), 0, st, x, gamma, n, eps, out);
+}
+
+void launch_dec_rope(hipStream_t st, float *q, float *k, int T, int heads, int hd, const float *cs, const float *sn,
+                     int rows) {
+    const size_t n = (size_t)T * heads * (hd / 2);
+    hipLaunchKernelGGL(k_dec_rope, dim3(blocks_for(n, 256)), dim3(256), 0, st, q, k, T, heads, hd, cs, sn, rows);
+}
+
+void launch_dec_attn(hipStream_t st, const DecAttnParams &p) {
+    hipLaunchKernelGGL(k_dec_attn, dim3(blocks_for((size_t)p.T * p.heads, 4)), dim3(256), 0, st, p);
+}
+
+void launch_dec_swiglu(hipStream_t st, const float *g, const float *u, size_t n, float *out) {
+    hipLaunchKernelGGL(k_dec_swiglu, dim3(blocks_for(n, 256)), dim3(256), 0, st, g, u, n, out);
+}
+
+void launch_dec_dwconv(hipStream_t st, const float *x, const float *w, const float *b, int ch, int len, int ks,
+                       float *out) {
+    hipLaunchKernelGGL(k_dec_dwconv, dim3(blocks_for((size_t)ch * len, 256)), dim3(256), 0, st, x, w, b, ch, len, ks,
+                       out);
+}
+
+void launch_dec_lnorm(hipStream_t st, const float *x, const float *g, const float *b, int ch, int len, float eps,
+                      float *out) {
+    hipLaunchKernelGGL(k_dec_lnorm, dim3(blocks_for((size_t)len, 256)), dim3(256), 0, st, x, g, b, ch, len, eps, out);
+}
+
+void launch_dec_snake(hipStream_t st, const float *x, const float *alpha, const float *beta, int ch, int len,
+                      float *out) {
+    hipLaunchKernelGGL(k_dec_snake, dim3(blocks_for((size_t)ch * len, 256)), dim3(256), 0, st, x, alpha, beta, ch,
+                       len, out);
+}
+
+}  // namespace qtts

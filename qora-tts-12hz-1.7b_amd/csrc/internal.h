@@ -67,6 +67,52 @@ struct QkvRowsParams {
     int pos0, row0;  // RoPE position and cache row of row 0
 };
 
+// ---- speech decoder (csrc/decoder.hip) ----
+constexpr int kDecMaxWindow = 512;   // sliding window of the decoder attention
+constexpr int kDecMaxHeadDim = 256;
+
+struct DecGatherParams {
+    const uint32_t *codes;  // [groups][ld]
+    int ld, cd, cb_size, num_rest;
+    const float *first;          // [cb_size][cd]
+    const float *const *rest;    // device array of num_rest codebook pointers
+    float *e0, *es;              // [T][cd]
+    int *status;                 // set to 1 for a code >= cb_size
+};
+
+enum DecAMode { DEC_A_STRIDED = 0, DEC_A_CONVT = 1 };
+enum DecBMode { DEC_B_STRIDED = 0, DEC_B_CONV = 1, DEC_B_CONVT = 2 };
+enum DecAct { DEC_ACT_NONE = 0, DEC_ACT_GELU = 1 };
+enum DecEpi { DEC_EPI_STORE = 0, DEC_EPI_ACCUM = 1, DEC_EPI_SCALED_RESID = 2, DEC_EPI_RESID_IN = 3, DEC_EPI_CLAMP = 4 };
+
+// C(m, n) (epi)= act(sum_k A(m, k) B(k, n) + bias), C(m, n) at
+// c[m * scm + col * scn] with col = n, or n * out_stride + phase when
+// out_stride != 0 (one output phase of a transposed convolution).
+struct DecGemmParams {
+    int M, N, K;
+    int a_mode, b_mode, a_kfast;
+    const float *a;
+    long long sam, sak;  // DEC_A_STRIDED
+    const float *b;
+    long long sbk, sbn;  // DEC_B_STRIDED
+    int ksize, dilation, in_len;  // DEC_B_CONV: causal taps; DEC_*_CONVT: kernel size, input length
+    int taps, stride, phase;      // DEC_*_CONVT: taps per phase (ksize / stride), stride, output phase
+    const float *bias_m, *bias_n;
+    int act, epi;
+    float *c;
+    long long scm, scn;
+    int out_stride;
+    const float *scale_n;  // DEC_EPI_SCALED_RESID / DEC_EPI_RESID_IN
+    const float *resid;    // DEC_EPI_RESID_IN (same addressing as c)
+};
+
+struct DecAttnParams {
+    const float *q, *k, *v;  // [T][heads * hd]
+    float *out;
+    int T, heads, hd, window;
+    float scale;
+};
+
 struct GemmMfmaParams {
     DevQ4Mfma w;
     const _Float16 *xh, *xl;  // the scaled rows split into binary16 hi + lo (MfmaRowsParams order)
@@ -225,6 +271,19 @@ void launch_embed_row(hipStream_t st, const DevQ4 &w, const uint32_t *d_token, f
 void launch_repack_mfma(hipStream_t st, const DevQ4 &w, uint32_t *wm, uint16_t *sa, uint16_t *sb, int *too_large);
 void launch_mfma_rows(hipStream_t st, const MfmaRowsParams &p);
 void launch_qkv_rows(hipStream_t st, const QkvRowsParams &p);
+void launch_dec_gather(hipStream_t st, const DecGatherParams &p, int frames);
+void launch_dec_gemm(hipStream_t st, const DecGemmParams &p);
+void launch_dec_rmsnorm(hipStream_t st, const float *x, const float *gamma, int rows, int n, float eps, float *out);
+void launch_dec_rope(hipStream_t st, float *q, float *k, int T, int heads, int hd, const float *cs, const float *sn,
+                     int rows);
+void launch_dec_attn(hipStream_t st, const DecAttnParams &p);
+void launch_dec_swiglu(hipStream_t st, const float *g, const float *u, size_t n, float *out);
+void launch_dec_dwconv(hipStream_t st, const float *x, const float *w, const float *b, int ch, int len, int ks,
+                       float *out);
+void launch_dec_lnorm(hipStream_t st, const float *x, const float *g, const float *b, int ch, int len, float eps,
+                      float *out);
+void launch_dec_snake(hipStream_t st, const float *x, const float *alpha, const float *beta, int ch, int len,
+                      float *out);
 void launch_gemm_mfma(hipStream_t st, const GemmMfmaParams &p, int mt, int sw, int kc);
 void launch_embed_sum(hipStream_t st, const EmbSumParams &p);
 void launch_advance(hipStream_t st, LoopState *s, int frame_step);

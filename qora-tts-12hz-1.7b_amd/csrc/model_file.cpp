@@ -8,6 +8,7 @@
 // element count is checked against the bytes left in the file before anything
 // is allocated.
 #include "../../include/qtts_file.h"
+#include "../../include/qtts_decoder.h"
 
 #include <cerrno>
 #include <cstdio>
@@ -34,12 +35,6 @@ struct FileReader {
         if ((int64_t)n > size - pos) return fail(std::string("truncated file reading ") + what);
         if (n && fread(dst, 1, n, f) != n) return fail(std::string("read error in ") + what);
         pos += (int64_t)n;
-        return true;
-    }
-    bool skip(int64_t n, const char *what) {
-        if (n < 0 || n > size - pos) return fail(std::string("truncated file skipping ") + what);
-        if (fseeko(f, (off_t)n, SEEK_CUR) != 0) return fail(std::string("seek error in ") + what);
-        pos += n;
         return true;
     }
     bool u8(uint8_t *v, const char *what) { return bytes(v, 1, what); }
@@ -110,10 +105,6 @@ struct qtts_model_file {
         }
         *out = v.data();
         return true;
-    }
-    bool skip_f32_vec(FileReader &r, const char *what) {
-        uint64_t n;
-        return r.count(&n, 4, what) && r.skip((int64_t)n * 4, what);
     }
     // read_weight_io with format 1 (src/gemv.rs:639-650): u64 k, u64 n,
     // u64-counted packed bytes, u64-counted binary16 scales.
@@ -249,57 +240,162 @@ struct qtts_model_file {
         return true;
     }
 
-    // load_conv1d / load_conv_t1d / load_dw_conv (src/save.rs:411-445):
-    // `dims` u32 fields, then weight and bias.
-    bool skip_conv(FileReader &r, int dims, const char *what) {
-        for (int i = 0; i < dims; i++) {
-            int32_t d;
-            if (!r.dim(&d, what)) return false;
-        }
-        return skip_f32_vec(r, what) && skip_f32_vec(r, what);
-    }
-    bool skip_vecs(FileReader &r, int n, const char *what) {
-        for (int i = 0; i < n; i++)
-            if (!skip_f32_vec(r, what)) return false;
+    // An f32 array of exactly `want` values (0: any length, returned in *len).
+    bool vec(FileReader &r, const float **out, uint64_t want, const std::string &name, uint64_t *len = nullptr) {
+        uint64_t n;
+        if (!f32_vec(r, out, &n, name.c_str())) return false;
+        if (want && n != want)
+            return r.fail(name + ": length " + std::to_string(n) + ", expected " + std::to_string(want));
+        if (len) *len = n;
         return true;
     }
+    // load_conv1d (6 dims), load_conv_t1d (5), load_dw_conv (3), src/save.rs:411-445.
+    bool conv(FileReader &r, qtts_conv_view *c, int kind, const std::string &name) {
+        int32_t dims[6] = {0, 0, 0, 1, 0, 1};
+        const int nd = kind == 0 ? 6 : (kind == 1 ? 5 : 3);
+        for (int i = 0; i < nd; i++)
+            if (!r.dim(&dims[i], name.c_str())) return false;
+        if (kind == 2) {  // channels, kernel_size, padding
+            c->in_channels = c->out_channels = dims[0];
+            c->kernel_size = dims[1];
+            c->padding = dims[2];
+            c->stride = c->dilation = 1;
+        } else {
+            c->in_channels = dims[0];
+            c->out_channels = dims[1];
+            c->kernel_size = dims[2];
+            c->stride = dims[3];
+            c->padding = dims[4];
+            c->dilation = kind == 0 ? dims[5] : 1;
+        }
+        const uint64_t wn = kind == 2 ? (uint64_t)c->out_channels * c->kernel_size
+                                      : (uint64_t)c->in_channels * c->out_channels * c->kernel_size;
+        return vec(r, &c->weight, wn, name + ".weight") && vec(r, &c->bias, (uint64_t)c->out_channels, name + ".bias");
+    }
 
-    // load_decoder_weights, src/save.rs:447-546: walked, not read.
-    bool walk_decoder(FileReader &r) {
+    std::vector<const float *> rest_codebooks;
+    std::vector<qtts_dec_layer_view> dec_layers;
+    std::vector<qtts_upsample_view> dec_upsample;
+    std::vector<qtts_vocos_block_view> dec_blocks;
+    std::deque<std::vector<qtts_vocos_residual_view>> dec_residuals;
+    qtts_decoder_view decoder{};
+
+    // load_decoder_weights, src/save.rs:447-546.
+    bool read_decoder(FileReader &r) {
         qtts_file_info &d = info;
+        qtts_decoder_view &w = decoder;
         if (!r.dim(&d.decoder_hidden_size, "decoder hidden_size") || !r.dim(&d.decoder_num_heads, "decoder num_heads") ||
             !r.dim(&d.decoder_head_dim, "decoder head_dim") ||
             !r.dim(&d.decoder_intermediate_size, "decoder intermediate_size") ||
             !r.dim(&d.decoder_sliding_window, "decoder sliding_window") ||
             !r.dim(&d.decoder_codebook_dim, "decoder codebook_dim"))
             return false;
-        if (!skip_vecs(r, 2, "decoder first codebook") || !r.dim(&d.decoder_rest_codebooks, "decoder codebook count") ||
-            !skip_vecs(r, d.decoder_rest_codebooks, "decoder codebooks") ||
-            !skip_vecs(r, 1, "decoder rest_output_proj") || !skip_conv(r, 6, "decoder pre_conv") ||
-            !skip_vecs(r, 2, "decoder tf_input") || !r.dim(&d.decoder_layers, "decoder layer count"))
+        w.hidden_size = d.decoder_hidden_size;
+        w.num_heads = d.decoder_num_heads;
+        w.head_dim = d.decoder_head_dim;
+        w.intermediate_size = d.decoder_intermediate_size;
+        w.sliding_window = d.decoder_sliding_window;
+        w.codebook_dim = d.decoder_codebook_dim;
+        const uint64_t cd = (uint64_t)w.codebook_dim, hid = (uint64_t)w.hidden_size;
+        const uint64_t ad = (uint64_t)w.num_heads * w.head_dim, inter = (uint64_t)w.intermediate_size;
+        if (cd == 0 || hid == 0 || ad == 0) return r.fail("decoder: zero dimension");
+        uint64_t n;
+        if (!vec(r, &w.first_codebook, 0, "decoder.first_codebook", &n)) return false;
+        if (n % cd) return r.fail("decoder.first_codebook: not whole rows of codebook_dim");
+        w.codebook_size = (int32_t)(n / cd);
+        if (!vec(r, &w.first_output_proj, 0, "decoder.first_output_proj", &n)) return false;
+        if (n % cd) return r.fail("decoder.first_output_proj: not whole rows of codebook_dim");
+        w.vq_dim = (int32_t)(n / cd);
+        if (!r.dim(&d.decoder_rest_codebooks, "decoder codebook count")) return false;
+        w.num_rest = d.decoder_rest_codebooks;
+        rest_codebooks.resize((size_t)w.num_rest);
+        for (int32_t g = 0; g < w.num_rest; g++)
+            if (!vec(r, &rest_codebooks[(size_t)g], (uint64_t)w.codebook_size * cd,
+                     "decoder.rest_codebooks." + std::to_string(g)))
+                return false;
+        w.rest_codebooks = rest_codebooks.data();
+        if (!vec(r, &w.rest_output_proj, cd * (uint64_t)w.vq_dim, "decoder.rest_output_proj") ||
+            !conv(r, &w.pre_conv, 0, "decoder.pre_conv"))
             return false;
-        for (int32_t l = 0; l < d.decoder_layers; l++)
-            if (!skip_vecs(r, 11, "decoder transformer layer")) return false;
-        if (!skip_vecs(r, 3, "decoder tf_norm/output") || !r.dim(&d.decoder_upsample_stages, "decoder upsample count"))
+        const uint64_t lat = (uint64_t)w.pre_conv.out_channels;
+        if (!vec(r, &w.tf_input_w, lat * hid, "decoder.tf_input_w") || !vec(r, &w.tf_input_b, hid, "decoder.tf_input_b") ||
+            !r.dim(&d.decoder_layers, "decoder layer count"))
             return false;
-        for (int32_t u = 0; u < d.decoder_upsample_stages; u++) {
-            int32_t ch;
-            if (!r.dim(&ch, "upsample channels") || !skip_conv(r, 5, "upsample conv_t") ||
-                !skip_conv(r, 3, "upsample dw_conv") || !skip_vecs(r, 7, "upsample stage"))
+        w.num_layers = d.decoder_layers;
+        dec_layers.resize((size_t)w.num_layers);
+        for (int32_t l = 0; l < w.num_layers; l++) {
+            qtts_dec_layer_view &L = dec_layers[(size_t)l];
+            const std::string p = "decoder.layers." + std::to_string(l);
+            if (!vec(r, &L.q_proj, hid * ad, p + ".q_proj") || !vec(r, &L.k_proj, hid * ad, p + ".k_proj") ||
+                !vec(r, &L.v_proj, hid * ad, p + ".v_proj") || !vec(r, &L.o_proj, ad * hid, p + ".o_proj") ||
+                !vec(r, &L.gate_proj, hid * inter, p + ".gate_proj") || !vec(r, &L.up_proj, hid * inter, p + ".up_proj") ||
+                !vec(r, &L.down_proj, inter * hid, p + ".down_proj") || !vec(r, &L.input_norm, hid, p + ".input_norm") ||
+                !vec(r, &L.post_attn_norm, hid, p + ".post_attn_norm") ||
+                !vec(r, &L.attn_scale, hid, p + ".attn_scale") || !vec(r, &L.mlp_scale, hid, p + ".mlp_scale"))
                 return false;
         }
-        if (!skip_conv(r, 6, "vocos_init") || !r.dim(&d.decoder_vocos_blocks, "vocos block count")) return false;
-        for (int32_t b = 0; b < d.decoder_vocos_blocks; b++) {
+        w.layers = dec_layers.data();
+        if (!vec(r, &w.tf_norm, hid, "decoder.tf_norm") || !vec(r, &w.tf_output_w, hid * lat, "decoder.tf_output_w") ||
+            !vec(r, &w.tf_output_b, lat, "decoder.tf_output_b") ||
+            !r.dim(&d.decoder_upsample_stages, "decoder upsample count"))
+            return false;
+        w.num_upsample = d.decoder_upsample_stages;
+        dec_upsample.resize((size_t)w.num_upsample);
+        for (int32_t u = 0; u < w.num_upsample; u++) {
+            qtts_upsample_view &U = dec_upsample[(size_t)u];
+            const std::string p = "decoder.upsample." + std::to_string(u);
+            if (!r.dim(&U.channels, "upsample channels") || !conv(r, &U.conv_t, 1, p + ".conv_t") ||
+                !conv(r, &U.dw_conv, 2, p + ".dw_conv"))
+                return false;
+            const uint64_t ch = (uint64_t)U.channels;
+            uint64_t inner;
+            if (!vec(r, &U.norm_w, ch, p + ".norm_w") || !vec(r, &U.norm_b, ch, p + ".norm_b") ||
+                !vec(r, &U.pw1_w, 0, p + ".pw1_w", &n) || !vec(r, &U.pw1_b, 0, p + ".pw1_b", &inner))
+                return false;
+            if (inner == 0 || n != ch * inner) return r.fail(p + ".pw1_w: length is not channels x inner");
+            U.inner_dim = (int32_t)inner;
+            if (!vec(r, &U.pw2_w, inner * ch, p + ".pw2_w") || !vec(r, &U.pw2_b, ch, p + ".pw2_b") ||
+                !vec(r, &U.gamma, ch, p + ".gamma"))
+                return false;
+        }
+        w.upsample = dec_upsample.data();
+        if (!conv(r, &w.vocos_init, 0, "decoder.vocos_init") || !r.dim(&d.decoder_vocos_blocks, "vocos block count"))
+            return false;
+        w.num_vocos_blocks = d.decoder_vocos_blocks;
+        dec_blocks.resize((size_t)w.num_vocos_blocks);
+        for (int32_t b = 0; b < w.num_vocos_blocks; b++) {
+            qtts_vocos_block_view &B = dec_blocks[(size_t)b];
+            const std::string p = "decoder.vocos." + std::to_string(b);
+            uint64_t na;
             int32_t nres;
-            if (!skip_vecs(r, 2, "vocos pre_snake") || !skip_conv(r, 5, "vocos upsample") ||
+            if (!vec(r, &B.pre_snake_alpha, 0, p + ".pre_snake_alpha", &na) ||
+                !vec(r, &B.pre_snake_beta, na, p + ".pre_snake_beta") || !conv(r, &B.upsample, 1, p + ".upsample") ||
                 !r.dim(&nres, "vocos residual count"))
                 return false;
-            for (int32_t i = 0; i < nres; i++)
-                if (!skip_vecs(r, 2, "vocos act1") || !skip_conv(r, 6, "vocos conv1") ||
-                    !skip_vecs(r, 2, "vocos act2") || !skip_conv(r, 6, "vocos conv2"))
+            dec_residuals.emplace_back((size_t)nres);
+            std::vector<qtts_vocos_residual_view> &res = dec_residuals.back();
+            for (int32_t i = 0; i < nres; i++) {
+                qtts_vocos_residual_view &R = res[(size_t)i];
+                const std::string q = p + ".residuals." + std::to_string(i);
+                if (!vec(r, &R.act1_alpha, 0, q + ".act1_alpha", &na) || !vec(r, &R.act1_beta, na, q + ".act1_beta") ||
+                    !conv(r, &R.conv1, 0, q + ".conv1") || !vec(r, &R.act2_alpha, 0, q + ".act2_alpha", &na) ||
+                    !vec(r, &R.act2_beta, na, q + ".act2_beta") || !conv(r, &R.conv2, 0, q + ".conv2"))
                     return false;
+            }
+            B.num_residuals = nres;
+            B.residuals = res.data();
         }
-        return skip_vecs(r, 2, "final snake") && skip_conv(r, 6, "output_conv") && skip_vecs(r, 2, "decoder rope");
+        w.vocos_blocks = dec_blocks.data();
+        uint64_t na, nc;
+        if (!vec(r, &w.final_snake_alpha, 0, "decoder.final_snake_alpha", &na) ||
+            !vec(r, &w.final_snake_beta, na, "decoder.final_snake_beta") ||
+            !conv(r, &w.output_conv, 0, "decoder.output_conv") || !vec(r, &w.rope_cos, 0, "decoder.rope_cos", &nc) ||
+            !vec(r, &w.rope_sin, nc, "decoder.rope_sin"))
+            return false;
+        const uint64_t half = (uint64_t)w.head_dim / 2;
+        if (half == 0 || nc % half) return r.fail("decoder rope tables: not whole rows of head_dim/2");
+        w.rope_rows = (int32_t)(nc / half);
+        return true;
     }
 };
 
@@ -349,7 +445,7 @@ qtts_status qtts_model_file_open(const char *path, qtts_model_file **out) {
                     m->info.predictor_offset = r.pos;
                     if (m->read_predictor(r)) {
                         m->info.decoder_offset = r.pos;
-                        if (m->walk_decoder(r)) {
+                        if (m->read_decoder(r)) {
                             m->info.decoder_end = r.pos;
                             m->info.trailing_bytes = r.size - r.pos;
                         }
@@ -384,5 +480,6 @@ const qtts_talker_view *qtts_model_file_talker(const qtts_model_file *f) { retur
 const qtts_predictor_view *qtts_model_file_predictor(const qtts_model_file *f) { return f ? &f->predictor : nullptr; }
 const qtts_text_view *qtts_model_file_text(const qtts_model_file *f) { return f ? &f->text : nullptr; }
 const qtts_file_info *qtts_model_file_info(const qtts_model_file *f) { return f ? &f->info : nullptr; }
+const qtts_decoder_view *qtts_model_file_decoder(const qtts_model_file *f) { return f ? &f->decoder : nullptr; }
 
 }  // extern "C"

@@ -91,6 +91,45 @@ class PredictorView(C.Structure):
     ]
 
 
+class ConvView(C.Structure):
+    _fields_ = [("weight", C.c_void_p), ("bias", C.c_void_p)] + [
+        (n, C.c_int32) for n in ("in_channels", "out_channels", "kernel_size", "stride", "padding", "dilation")]
+
+
+class DecLayerView(C.Structure):
+    _fields_ = [(n, C.c_void_p) for n in ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj",
+                                          "down_proj", "input_norm", "post_attn_norm", "attn_scale", "mlp_scale")]
+
+
+class UpsampleView(C.Structure):
+    _fields_ = [("channels", C.c_int32), ("inner_dim", C.c_int32), ("conv_t", ConvView), ("dw_conv", ConvView)] + [
+        (n, C.c_void_p) for n in ("norm_w", "norm_b", "pw1_w", "pw1_b", "pw2_w", "pw2_b", "gamma")]
+
+
+class VocosResidualView(C.Structure):
+    _fields_ = [("act1_alpha", C.c_void_p), ("act1_beta", C.c_void_p), ("conv1", ConvView),
+                ("act2_alpha", C.c_void_p), ("act2_beta", C.c_void_p), ("conv2", ConvView)]
+
+
+class VocosBlockView(C.Structure):
+    _fields_ = [("pre_snake_alpha", C.c_void_p), ("pre_snake_beta", C.c_void_p), ("upsample", ConvView),
+                ("num_residuals", C.c_int32), ("residuals", C.POINTER(VocosResidualView))]
+
+
+class DecoderView(C.Structure):
+    _fields_ = [(n, C.c_int32) for n in ("hidden_size", "num_heads", "head_dim", "intermediate_size",
+                                         "sliding_window", "codebook_dim", "codebook_size", "vq_dim")] + [
+        ("first_codebook", C.c_void_p), ("first_output_proj", C.c_void_p), ("num_rest", C.c_int32),
+        ("rest_codebooks", C.POINTER(C.c_void_p)), ("rest_output_proj", C.c_void_p), ("pre_conv", ConvView),
+        ("tf_input_w", C.c_void_p), ("tf_input_b", C.c_void_p), ("num_layers", C.c_int32),
+        ("layers", C.POINTER(DecLayerView)), ("tf_norm", C.c_void_p), ("tf_output_w", C.c_void_p),
+        ("tf_output_b", C.c_void_p), ("num_upsample", C.c_int32), ("upsample", C.POINTER(UpsampleView)),
+        ("vocos_init", ConvView), ("num_vocos_blocks", C.c_int32), ("vocos_blocks", C.POINTER(VocosBlockView)),
+        ("final_snake_alpha", C.c_void_p), ("final_snake_beta", C.c_void_p), ("output_conv", ConvView),
+        ("rope_cos", C.c_void_p), ("rope_sin", C.c_void_p), ("rope_rows", C.c_int32),
+    ]
+
+
 class TextView(C.Structure):
     _fields_ = [
         ("text_embedding", Q4View),
@@ -203,6 +242,12 @@ def load_library(path: str = LIB_PATH):
         "qtts_model_file_predictor": ([vp], C.POINTER(PredictorView)),
         "qtts_model_file_text": ([vp], C.POINTER(TextView)),
         "qtts_model_file_info": ([vp], C.POINTER(FileInfo)),
+        "qtts_model_file_decoder": ([vp], C.POINTER(DecoderView)),
+        "qtts_decoder_upload": ([vp, C.POINTER(DecoderView), C.POINTER(vp)], i32),
+        "qtts_decoder_free": ([vp], None),
+        "qtts_decoder_num_samples": ([vp, i32], C.c_int64),
+        "qtts_decode_to_audio": ([vp, vp, i32, i32, f32p, C.c_int64, C.POINTER(C.c_int64)], i32),
+        "qtts_decode_to_audio_device": ([vp, vp, i32, i32, vp, C.c_int64, C.POINTER(C.c_int64)], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -225,6 +270,8 @@ def exported_symbols() -> List[str]:
         "qtts_synth_q4", "qtts_synth_normal_f32", "qtts_synth_normal_f16", "qtts_f32_to_f16", "qtts_f16_to_f32",
         "qtts_quantize_f32_to_q4", "qtts_model_file_open", "qtts_model_file_error", "qtts_model_file_close",
         "qtts_model_file_talker", "qtts_model_file_predictor", "qtts_model_file_text", "qtts_model_file_info",
+        "qtts_model_file_decoder", "qtts_decoder_upload", "qtts_decoder_free", "qtts_decoder_num_samples",
+        "qtts_decode_to_audio", "qtts_decode_to_audio_device",
     ]
 
 
@@ -428,6 +475,211 @@ def _f32(a, n: Optional[int] = None) -> np.ndarray:
 
 
 # ---------------------------------------------------------------------------
+# Speech decoder weights (SpeechDecoderWeights, src/decoder.rs:22-65)
+# ---------------------------------------------------------------------------
+@dataclasses.dataclass
+class DecoderConfig:
+    hidden: int = 512
+    heads: int = 16
+    head_dim: int = 64
+    inter: int = 1024
+    window: int = 72
+    codebook_dim: int = 256
+    codebook_size: int = 2048
+    vq_dim: int = 512
+    latent: int = 1024
+    num_rest: int = 15
+    layers: int = 8
+    upsample: tuple = (2, 2)  # ConvNeXt stage strides (transposed kernel = stride)
+    convnext_kernel: int = 7
+    convnext_mult: int = 4
+    vocos_channels: int = 1536
+    vocos: tuple = ((1536, 768, 16, 8), (768, 384, 10, 5), (384, 192, 8, 4), (192, 96, 6, 3))  # in, out, k, stride
+    dilations: tuple = (1, 3, 9)
+    res_kernel: int = 7
+    out_kernel: int = 7
+    rope_rows: int = 8000
+    rope_theta: float = 10000.0
+
+
+# The 12 Hz tokenizer's decoder (src/loader.rs:503-718).
+DECODER_1P7B = DecoderConfig()
+
+
+class DecoderWeights:
+    """Random-init SpeechDecoderWeights of a DecoderConfig (weights scaled by
+    1/sqrt(fan-in) so the signal keeps its size through the stack)."""
+
+    def __init__(self, seed: int, cfg: DecoderConfig = DECODER_1P7B):
+        self.cfg = c = cfg
+        self.seed = seed
+        self._arrays = []
+        n = lambda name, count, std, mean=0.0: self._keep(synth_normal_f32(seed, f"dec.{name}", count, mean, std))
+        cd, vq, lat, hid = c.codebook_dim, c.vq_dim, c.latent, c.hidden
+        ad = c.heads * c.head_dim
+        self.first_codebook = n("cb0", c.codebook_size * cd, 0.5)
+        self.first_output_proj = n("cb0.proj", cd * vq, cd ** -0.5)
+        self.rest_codebooks = [n(f"cb{g + 1}", c.codebook_size * cd, 0.5 / 4) for g in range(c.num_rest)]
+        self.rest_output_proj = n("cbr.proj", cd * vq, cd ** -0.5)
+        self.convs = {}
+        self.pre_conv = self._conv("pre_conv", vq, lat, 3, 1, 0, 1)
+        self.tf_input_w = n("tf.in.w", lat * hid, lat ** -0.5)
+        self.tf_input_b = n("tf.in.b", hid, 0.02)
+        self.layers = []
+        for i in range(c.layers):
+            p = f"tf.{i}"
+            self.layers.append(dict(
+                q_proj=n(p + ".q", hid * ad, hid ** -0.5), k_proj=n(p + ".k", hid * ad, hid ** -0.5),
+                v_proj=n(p + ".v", hid * ad, hid ** -0.5), o_proj=n(p + ".o", ad * hid, ad ** -0.5),
+                gate_proj=n(p + ".g", hid * c.inter, hid ** -0.5), up_proj=n(p + ".u", hid * c.inter, hid ** -0.5),
+                down_proj=n(p + ".d", c.inter * hid, c.inter ** -0.5),
+                input_norm=n(p + ".n1", hid, 0.1, 1.0), post_attn_norm=n(p + ".n2", hid, 0.1, 1.0),
+                attn_scale=n(p + ".s1", hid, 0.02, 0.1), mlp_scale=n(p + ".s2", hid, 0.02, 0.1)))
+        self.tf_norm = n("tf.norm", hid, 0.1, 1.0)
+        self.tf_output_w = n("tf.out.w", hid * lat, hid ** -0.5)
+        self.tf_output_b = n("tf.out.b", lat, 0.02)
+        self.upsample = []
+        for i, s in enumerate(c.upsample):
+            p = f"up.{i}"
+            inner = lat * c.convnext_mult
+            self.upsample.append(dict(
+                conv_t=self._conv(p + ".ct", lat, lat, s, s, 0, 1, transposed=True),
+                dw_conv=self._dw(p + ".dw", lat, c.convnext_kernel),
+                norm_w=n(p + ".nw", lat, 0.1, 1.0), norm_b=n(p + ".nb", lat, 0.02),
+                pw1_w=n(p + ".p1w", lat * inner, lat ** -0.5), pw1_b=n(p + ".p1b", inner, 0.02),
+                pw2_w=n(p + ".p2w", inner * lat, inner ** -0.5), pw2_b=n(p + ".p2b", lat, 0.02),
+                gamma=n(p + ".g", lat, 0.02, 0.1), inner=inner))
+        self.vocos_init = self._conv("vocos.init", lat, c.vocos_channels, 7, 1, 0, 1)
+        self.blocks = []
+        for b, (cin, cout, k, s) in enumerate(c.vocos):
+            p = f"vocos.{b}"
+            res = []
+            for r, d in enumerate(c.dilations):
+                q = f"{p}.r{r}"
+                res.append(dict(act1_alpha=n(q + ".a1", cout, 0.1), act1_beta=n(q + ".b1", cout, 0.1),
+                                conv1=self._conv(q + ".c1", cout, cout, c.res_kernel, 1, 0, d),
+                                act2_alpha=n(q + ".a2", cout, 0.1), act2_beta=n(q + ".b2", cout, 0.1),
+                                conv2=self._conv(q + ".c2", cout, cout, 1, 1, 0, 1, gain=0.5)))
+            self.blocks.append(dict(pre_snake_alpha=n(p + ".sa", cin, 0.1), pre_snake_beta=n(p + ".sb", cin, 0.1),
+                                    upsample=self._conv(p + ".up", cin, cout, k, s, 0, 1, transposed=True),
+                                    residuals=res))
+        last = c.vocos[-1][1] if c.vocos else c.vocos_channels
+        self.final_snake_alpha = n("final.a", last, 0.1)
+        self.final_snake_beta = n("final.b", last, 0.1)
+        self.output_conv = self._conv("out", last, 1, c.out_kernel, 1, 0, 1, gain=0.05)
+        half = c.head_dim // 2
+        freq = 1.0 / c.rope_theta ** (np.arange(half, dtype=np.float64) * 2 / c.head_dim)
+        ang = np.arange(c.rope_rows, dtype=np.float64)[:, None] * freq[None, :]
+        self.rope_cos = self._keep(np.cos(ang).astype(np.float32).reshape(-1))
+        self.rope_sin = self._keep(np.sin(ang).astype(np.float32).reshape(-1))
+        self._view = None
+
+    def _keep(self, a):
+        a = np.ascontiguousarray(a, dtype=np.float32)
+        self._arrays.append(a)
+        return a
+
+    def _conv(self, name, cin, cout, k, stride, pad, dil, transposed=False, gain=1.0):
+        """Conv1dWeight [out][in][k] or ConvTranspose1dWeight [in][out][k]."""
+        fan = cin * (max(1, k // stride) if transposed else k)
+        w = self._keep(synth_normal_f32(self.seed, f"dec.{name}.w", cin * cout * k, 0.0, gain * fan ** -0.5))
+        b = self._keep(synth_normal_f32(self.seed, f"dec.{name}.b", cout, 0.0, 0.02))
+        return dict(weight=w, bias=b, in_channels=cin, out_channels=cout, kernel_size=k, stride=stride,
+                    padding=pad, dilation=dil)
+
+    def _dw(self, name, ch, k):
+        w = self._keep(synth_normal_f32(self.seed, f"dec.{name}.w", ch * k, 0.0, k ** -0.5))
+        b = self._keep(synth_normal_f32(self.seed, f"dec.{name}.b", ch, 0.0, 0.02))
+        return dict(weight=w, bias=b, in_channels=ch, out_channels=ch, kernel_size=k, stride=1,
+                    padding=(k - 1) // 2, dilation=1)
+
+    @staticmethod
+    def _cv(d) -> ConvView:
+        return ConvView(d["weight"].ctypes.data, d["bias"].ctypes.data, d["in_channels"], d["out_channels"],
+                        d["kernel_size"], d["stride"], d["padding"], d["dilation"])
+
+    def view(self) -> DecoderView:
+        if self._view is not None:
+            return self._view[0]
+        c = self.cfg
+        ptr = lambda a: a.ctypes.data
+        rest = (C.c_void_p * c.num_rest)(*[ptr(a) for a in self.rest_codebooks])
+        layers = (DecLayerView * len(self.layers))(*[DecLayerView(*[ptr(L[n]) for n, _ in DecLayerView._fields_])
+                                                      for L in self.layers])
+        ups = (UpsampleView * len(self.upsample))(*[UpsampleView(
+            u["conv_t"]["in_channels"], u["inner"], self._cv(u["conv_t"]), self._cv(u["dw_conv"]),
+            *[ptr(u[n]) for n in ("norm_w", "norm_b", "pw1_w", "pw1_b", "pw2_w", "pw2_b", "gamma")])
+            for u in self.upsample])
+        res_arrays = []
+        blocks = []
+        for b in self.blocks:
+            ra = (VocosResidualView * len(b["residuals"]))(*[VocosResidualView(
+                ptr(r["act1_alpha"]), ptr(r["act1_beta"]), self._cv(r["conv1"]), ptr(r["act2_alpha"]),
+                ptr(r["act2_beta"]), self._cv(r["conv2"])) for r in b["residuals"]])
+            res_arrays.append(ra)
+            blocks.append(VocosBlockView(ptr(b["pre_snake_alpha"]), ptr(b["pre_snake_beta"]),
+                                         self._cv(b["upsample"]), len(b["residuals"]), ra))
+        barr = (VocosBlockView * len(blocks))(*blocks)
+        v = DecoderView(c.hidden, c.heads, c.head_dim, c.inter, c.window, c.codebook_dim, c.codebook_size, c.vq_dim,
+                        ptr(self.first_codebook), ptr(self.first_output_proj), c.num_rest, rest,
+                        ptr(self.rest_output_proj), self._cv(self.pre_conv), ptr(self.tf_input_w),
+                        ptr(self.tf_input_b), len(self.layers), layers, ptr(self.tf_norm), ptr(self.tf_output_w),
+                        ptr(self.tf_output_b), len(self.upsample), ups, self._cv(self.vocos_init), len(blocks), barr,
+                        ptr(self.final_snake_alpha), ptr(self.final_snake_beta), self._cv(self.output_conv),
+                        ptr(self.rope_cos), ptr(self.rope_sin), c.rope_rows)
+        self._view = (v, rest, layers, ups, res_arrays, barr)
+        return v
+
+    def synthetic_codes(self, seed: int, frames: int) -> np.ndarray:
+        """[num_rest + 1][frames] codes below codebook_size."""
+        raw = np.empty(frames * (self.cfg.num_rest + 1), dtype=np.float32)
+        load_library().qtts_synth_normal_f32(seed, stream_id("dec.codes"), raw.size, 0.0, 1.0, _ptr(raw))
+        u = (np.abs(raw.astype(np.float64)) * 1e6).astype(np.int64) % self.cfg.codebook_size
+        return u.astype(np.uint32).reshape(self.cfg.num_rest + 1, frames)
+
+
+class SpeechDecoder:
+    """SpeechDecoderWeights in HBM with decode_to_audio."""
+
+    def __init__(self, ctx: "Context", w):
+        self.ctx, self.cfg = ctx, getattr(w, "cfg", None)
+        h = C.c_void_p()
+        self._view = w.view()
+        ctx.check(ctx.lib.qtts_decoder_upload(ctx.h, C.byref(self._view), C.byref(h)))
+        self.h = h
+
+    def num_samples(self, frames: int) -> int:
+        return int(self.ctx.lib.qtts_decoder_num_samples(self.h, frames))
+
+    # decode_to_audio, src/decoder.rs:394-509
+    def decode_to_audio(self, codes) -> np.ndarray:
+        codes = np.ascontiguousarray(codes, dtype=np.uint32)
+        groups, frames = codes.shape
+        out = np.empty(max(1, self.num_samples(frames)), dtype=np.float32)
+        n = C.c_int64()
+        self.ctx.check(self.ctx.lib.qtts_decode_to_audio(self.h, _ptr(codes), frames, frames, _ptr(out), out.size,
+                                                         C.byref(n)))
+        return out[: n.value]
+
+    def decode_to_audio_device(self, d_codes: int, frames: int, ld: int, d_audio: int, capacity: int) -> int:
+        n = C.c_int64()
+        self.ctx.check(self.ctx.lib.qtts_decode_to_audio_device(self.h, C.c_void_p(d_codes), frames, ld,
+                                                                C.c_void_p(d_audio), capacity, C.byref(n)))
+        return n.value
+
+    def close(self):
+        if getattr(self, "h", None):
+            self.ctx.lib.qtts_decoder_free(self.h)
+            self.h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+# ---------------------------------------------------------------------------
 # .qora-tts model files (load_model, src/save.rs:262-298)
 # ---------------------------------------------------------------------------
 def q4_from_view(v: Q4View) -> Q4Weight:
@@ -472,6 +724,8 @@ class ModelFile:
         pcfg = StackConfig(layers=pv.num_layers, hidden=pv.hidden_size, heads=pv.num_heads,
                            kv_heads=pv.num_kv_heads, head_dim=pv.head_dim, inter=p0.gate_proj.n,
                            vocab=pv.lm_heads[0].n, max_position=pv.max_position, rope_theta=0.0)
+        dv = lib.qtts_model_file_decoder(h).contents
+        self.decoder = _FileStack(self, dv, None)
         self.talker = _FileStack(self, tv, tcfg)
         self.predictor = _FileStack(self, pv, pcfg, num_groups=pv.num_groups,
                                     talker_hidden=pv.codec_embeddings[0].n)

@@ -2,8 +2,7 @@
 save_model (src/save.rs:23-46): the talker section (src/save.rs:48-89), the
 code predictor section (src/save.rs:91-137) and the speech decoder section
 (src/save.rs:168-257), with the array encodings of src/gemv.rs:558-597
-(u64 element count, then little-endian elements).  The decoder tensors are
-small random arrays: the reader only walks that section."""
+(u64 element count, then little-endian elements)."""
 import struct
 
 import numpy as np
@@ -71,70 +70,82 @@ def _layer(o, L):  # src/save.rs:61-72
     o.f16v(L.post_attn_norm_gamma)
 
 
-def _conv(o, rng, dims, wlen, blen):
+def _conv(o, c, kind):
+    """save_conv1d (kind 0), save_conv_t1d (1), save_dw_conv (2), src/save.rs:139-166."""
+    if kind == 2:
+        dims = (c["out_channels"], c["kernel_size"], c["padding"])
+    else:
+        dims = (c["in_channels"], c["out_channels"], c["kernel_size"], c["stride"], c["padding"])
+        if kind == 0:
+            dims += (c["dilation"],)
     for d in dims:
         o.u32(d)
-    o.f32v(rng.standard_normal(wlen).astype(np.float32))
-    o.f32v(rng.standard_normal(blen).astype(np.float32))
+    o.f32v(c["weight"])
+    o.f32v(c["bias"])
 
 
-def _decoder(o, rng, layers=2, rest=3, upsample=2, blocks=2, residuals=2):
-    """A small speech decoder section in the order of src/save.rs:168-257."""
-    vec = lambda n: o.f32v(rng.standard_normal(n).astype(np.float32))
-    cfg = dict(hidden=64, heads=2, head_dim=32, inter=128, window=72, cb_dim=16)
-    for v in cfg.values():
+def _decoder(o, dw):
+    """save_decoder, src/save.rs:168-257, from a qtts.DecoderWeights."""
+    c = dw.cfg
+    for v in (c.hidden, c.heads, c.head_dim, c.inter, c.window, c.codebook_dim):
         o.u32(v)
-    vec(32 * 16)  # first_codebook
-    vec(16 * 64)  # first_output_proj
-    o.u32(rest)
-    for _ in range(rest):
-        vec(32 * 16)
-    vec(16 * 64)  # rest_output_proj
-    _conv(o, rng, (64, 64, 3, 1, 1, 1), 64 * 64 * 3, 64)  # pre_conv
-    vec(64 * 64)
-    vec(64)
-    o.u32(layers)
-    for _ in range(layers):
-        for n in (64 * 64,) * 4 + (64 * 128,) * 3 + (64,) * 4:
-            vec(n)
-    vec(64)
-    vec(64 * 64)
-    vec(64)
-    o.u32(upsample)
-    for _ in range(upsample):
-        o.u32(64)
-        _conv(o, rng, (64, 64, 2, 2, 0), 64 * 64 * 2, 64)  # conv_t
-        _conv(o, rng, (64, 7, 3), 64 * 7, 64)  # dw_conv
-        for n in (64, 64, 64 * 256, 256, 256 * 64, 64, 64):
-            vec(n)
-    _conv(o, rng, (64, 96, 7, 1, 3, 1), 64 * 96 * 7, 96)  # vocos_init
-    o.u32(blocks)
-    for _ in range(blocks):
-        vec(96)
-        vec(96)
-        _conv(o, rng, (96, 48, 4, 2, 1), 96 * 48 * 4, 48)
-        o.u32(residuals)
-        for _ in range(residuals):
-            vec(48)
-            vec(48)
-            _conv(o, rng, (48, 48, 7, 1, 3, 1), 48 * 48 * 7, 48)
-            vec(48)
-            vec(48)
-            _conv(o, rng, (48, 48, 1, 1, 0, 1), 48 * 48, 48)
-    vec(48)
-    vec(48)
-    _conv(o, rng, (48, 1, 7, 1, 3, 1), 48 * 7, 1)
-    vec(100 * 16)  # rope tables
-    vec(100 * 16)
-    return dict(cfg, layers=layers, rest=rest, upsample=upsample, blocks=blocks)
+    o.f32v(dw.first_codebook)
+    o.f32v(dw.first_output_proj)
+    o.u32(len(dw.rest_codebooks))
+    for cb in dw.rest_codebooks:
+        o.f32v(cb)
+    o.f32v(dw.rest_output_proj)
+    _conv(o, dw.pre_conv, 0)
+    o.f32v(dw.tf_input_w)
+    o.f32v(dw.tf_input_b)
+    o.u32(len(dw.layers))
+    for L in dw.layers:
+        for n in ("q_proj", "k_proj", "v_proj", "o_proj", "gate_proj", "up_proj", "down_proj", "input_norm",
+                  "post_attn_norm", "attn_scale", "mlp_scale"):
+            o.f32v(L[n])
+    o.f32v(dw.tf_norm)
+    o.f32v(dw.tf_output_w)
+    o.f32v(dw.tf_output_b)
+    o.u32(len(dw.upsample))
+    for u in dw.upsample:
+        o.u32(u["conv_t"]["out_channels"])
+        _conv(o, u["conv_t"], 1)
+        _conv(o, u["dw_conv"], 2)
+        for n in ("norm_w", "norm_b", "pw1_w", "pw1_b", "pw2_w", "pw2_b", "gamma"):
+            o.f32v(u[n])
+    _conv(o, dw.vocos_init, 0)
+    o.u32(len(dw.blocks))
+    for b in dw.blocks:
+        o.f32v(b["pre_snake_alpha"])
+        o.f32v(b["pre_snake_beta"])
+        _conv(o, b["upsample"], 1)
+        o.u32(len(b["residuals"]))
+        for r in b["residuals"]:
+            o.f32v(r["act1_alpha"])
+            o.f32v(r["act1_beta"])
+            _conv(o, r["conv1"], 0)
+            o.f32v(r["act2_alpha"])
+            o.f32v(r["act2_beta"])
+            _conv(o, r["conv2"], 0)
+    o.f32v(dw.final_snake_alpha)
+    o.f32v(dw.final_snake_beta)
+    _conv(o, dw.output_conv, 0)
+    o.f32v(dw.rope_cos)
+    o.f32v(dw.rope_sin)
 
 
-def write_model(path, tw, pw, text, talker_rope, predictor_rope, *, magic=b"QTTS", version=1, format_id=1,
-                mrope_section=(24, 20, 20), has_proj_flag=1, trailing=b"", lm_heads=None):
+# A small decoder for the reader's tests.
+SMALL_DECODER = qtts.DecoderConfig(hidden=64, heads=4, head_dim=16, inter=128, window=8, codebook_dim=32,
+                                   codebook_size=64, vq_dim=64, latent=128, num_rest=3, layers=2, upsample=(2,),
+                                   vocos_channels=96, vocos=((96, 48, 4, 2), (48, 24, 6, 3)), rope_rows=64)
+
+
+def write_model(path, tw, pw, text, talker_rope, predictor_rope, *, decoder=None, magic=b"QTTS", version=1,
+                format_id=1, mrope_section=(24, 20, 20), has_proj_flag=1, trailing=b"", lm_heads=None):
     """Writes tw (TalkerWeights), pw (CodePredictorWeights) and text
-    (TextWeights) with the given (cos, sin) RoPE tables, then a synthetic
-    decoder section and `trailing` bytes.  Returns the section offsets and
-    the decoder configuration."""
+    (TextWeights) with the given (cos, sin) RoPE tables, then the decoder
+    (a qtts.DecoderWeights; default a small random one) and `trailing`
+    bytes.  Returns the section offsets and the decoder weights."""
     o = _Out()
     o.raw(magic)
     o.u32(version)
@@ -181,7 +192,9 @@ def write_model(path, tw, pw, text, talker_rope, predictor_rope, *, magic=b"QTTS
     o.f32v(predictor_rope[0])
     o.f32v(predictor_rope[1])
     meta["decoder_offset"] = o.size
-    meta["decoder"] = _decoder(o, np.random.default_rng(5))
+    dw = decoder if decoder is not None else qtts.DecoderWeights(5, SMALL_DECODER)
+    _decoder(o, dw)
+    meta["decoder"] = dw
     meta["decoder_end"] = o.size
     o.raw(trailing)
     meta["file_bytes"] = o.size

@@ -14,7 +14,7 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def declared_symbols():
     names = set()
-    for h in ("qtts.h", "qtts_synth.h", "qtts_file.h"):
+    for h in ("qtts.h", "qtts_synth.h", "qtts_file.h", "qtts_decoder.h"):
         text = open(os.path.join(ROOT, "include", h)).read()
         text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
         names.update(re.findall(r"\b(qtts_[a-z0-9_]+)\s*\(", text))

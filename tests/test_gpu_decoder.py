@@ -1,0 +1,111 @@
+"""GPU parity of the speech decoder (decode_to_audio, src/decoder.rs:394-509)
+against the oracle's restatement: a small decoder (every stage, the
+transformer's sliding window exceeded) over several lengths, the 1.7B model's
+decoder at full size, the strided-codes device entry point, a decoder read
+from a .qora-tts file, and the error cases.
+
+Bar: audio within REL_TOL = 1e-3 of the oracle's (max abs difference over
+max abs sample, f32 sums in a different order over ~40 dependent stages);
+lengths exact."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import qtts
+from bench import Hip
+from oracle import oracle
+from qtts_file_writer import SMALL_DECODER, TextWeights, write_model
+from shapes import TINY_PREDICTOR, TINY_TALKER, rel_err
+
+pytestmark = pytest.mark.gpu
+REL_TOL = 1e-3
+
+
+@pytest.fixture(scope="module")
+def small(ctx):
+    w = qtts.DecoderWeights(7, SMALL_DECODER)
+    return w, qtts.SpeechDecoder(ctx, w)
+
+
+@pytest.mark.parametrize("frames", [1, 5, 40])
+def test_small_decoder_matches_oracle(small, frames):
+    w, dec = small
+    codes = w.synthetic_codes(100 + frames, frames)
+    got = dec.decode_to_audio(codes)
+    ref = oracle.decode_to_audio(w, codes)
+    assert got.shape == ref.shape == (dec.num_samples(frames),)
+    e = rel_err(got, ref)
+    print(f"small decoder, {frames} frames: {got.size} samples, rel err {e:.2e}")
+    assert e < REL_TOL
+
+
+def test_full_decoder_matches_oracle(ctx):
+    w = qtts.DecoderWeights(9)
+    dec = qtts.SpeechDecoder(ctx, w)
+    codes = w.synthetic_codes(11, 3)
+    got = dec.decode_to_audio(codes)
+    ref = oracle.decode_to_audio(w, codes)
+    assert got.shape == ref.shape == (3 * 1920,)
+    e = rel_err(got, ref)
+    print(f"1.7B decoder, 3 frames: rel err {e:.2e}, audio std {np.std(ref):.3f}")
+    assert e < REL_TOL
+
+
+def test_device_entry_point_with_strided_codes(ctx, small):
+    """codes[g * ld + t] with ld > frames, device buffers in and out."""
+    w, dec = small
+    frames, ld = 9, 16
+    codes = w.synthetic_codes(55, frames)
+    padded = np.full((codes.shape[0], ld), 0xFFFFFFFF, dtype=np.uint32)  # out-of-range filler past `frames`
+    padded[:, :frames] = codes
+    hip = Hip()
+    n = dec.num_samples(frames)
+    dc, da = hip.malloc(padded.nbytes), hip.malloc(4 * n)
+    hip.h2d(dc, padded)
+    got_n = dec.decode_to_audio_device(dc, frames, ld, da, n)
+    ctx.synchronize()
+    out = np.empty(n, dtype=np.float32)
+    hip._ok(hip.lib.hipMemcpy(out.ctypes.data_as(C.c_void_p), C.c_void_p(da), C.c_size_t(4 * n), 2), "hipMemcpy")
+    hip.free(dc)
+    hip.free(da)
+    assert got_n == n
+    assert np.array_equal(out, dec.decode_to_audio(codes))
+
+
+def test_decoder_errors(ctx, small):
+    w, dec = small
+    assert dec.decode_to_audio(np.zeros((SMALL_DECODER.num_rest + 1, 0), np.uint32)).size == 0
+    bad = w.synthetic_codes(3, 4)
+    bad[2, 1] = SMALL_DECODER.codebook_size
+    with pytest.raises(qtts.QttsError) as e:
+        dec.decode_to_audio(bad)
+    assert e.value.status == qtts.QTTS_ERANGE
+    with pytest.raises(qtts.QttsError) as e:  # output buffer one sample short
+        hip = Hip()
+        n = dec.num_samples(4)
+        dc, da = hip.malloc(4 * 4 * (SMALL_DECODER.num_rest + 1)), hip.malloc(4 * n)
+        try:
+            dec.decode_to_audio_device(dc, 4, 4, da, n - 1)
+        finally:
+            hip.free(dc)
+            hip.free(da)
+    assert e.value.status == qtts.QTTS_ERANGE
+
+
+def test_decoder_from_file(ctx, tmp_path):
+    """A decoder read from a .qora-tts file decodes the same bits as the
+    weights it was written from."""
+    tw = qtts.TalkerWeights(47, TINY_TALKER)
+    pw = qtts.CodePredictorWeights(47, TINY_PREDICTOR, talker_hidden=TINY_TALKER.hidden)
+    text = TextWeights(47, text_vocab=96, text_hidden=64, hidden=TINY_TALKER.hidden)
+    trope = oracle.build_rope_table(TINY_TALKER.head_dim, TINY_TALKER.max_position, TINY_TALKER.rope_theta)
+    prope = oracle.build_rope_table(TINY_PREDICTOR.head_dim, 64, TINY_PREDICTOR.rope_theta)
+    dw = qtts.DecoderWeights(48, SMALL_DECODER)
+    path = str(tmp_path / "dec.qora-tts")
+    write_model(path, tw, pw, text, trope, prope, decoder=dw)
+    f = qtts.ModelFile(path)
+    codes = dw.synthetic_codes(49, 20)
+    a = qtts.SpeechDecoder(ctx, f.decoder).decode_to_audio(codes)
+    b = qtts.SpeechDecoder(ctx, dw).decode_to_audio(codes)
+    assert np.array_equal(a, b)

@@ -70,12 +70,12 @@ def test_round_trip(tmp_path, model):
     assert info.trailing_bytes == len(b"speaker encoder bytes")
     assert list(info.mrope_section[: info.mrope_sections]) == [24, 20, 20]
     assert info.talker_num_kv_groups == TINY_TALKER.heads // TINY_TALKER.kv_heads
-    d = meta["decoder"]
+    dc = meta["decoder"].cfg
     assert (info.decoder_hidden_size, info.decoder_num_heads, info.decoder_head_dim, info.decoder_intermediate_size,
-            info.decoder_sliding_window, info.decoder_codebook_dim) == (d["hidden"], d["heads"], d["head_dim"],
-                                                                        d["inter"], d["window"], d["cb_dim"])
+            info.decoder_sliding_window, info.decoder_codebook_dim) == (dc.hidden, dc.heads, dc.head_dim, dc.inter,
+                                                                        dc.window, dc.codebook_dim)
     assert (info.decoder_layers, info.decoder_rest_codebooks, info.decoder_upsample_stages,
-            info.decoder_vocos_blocks) == (d["layers"], d["rest"], d["upsample"], d["blocks"])
+            info.decoder_vocos_blocks) == (dc.layers, dc.num_rest, len(dc.upsample), len(dc.vocos))
     # talker
     assert (tv.num_layers, tv.hidden_size, tv.num_heads, tv.num_kv_heads, tv.head_dim) == (
         TINY_TALKER.layers, TINY_TALKER.hidden, TINY_TALKER.heads, TINY_TALKER.kv_heads, TINY_TALKER.head_dim)
@@ -110,6 +110,31 @@ def test_round_trip(tmp_path, model):
         _same_layer(pv.layers[l], pw.layers[l], TINY_PREDICTOR)
     assert f.predictor.talker_hidden == TINY_TALKER.hidden and f.predictor.num_groups == pw.num_groups
     f.close()
+
+
+def test_decoder_round_trip(tmp_path, model):
+    """The decoder section reads back as a view of the same arrays, and the
+    oracle decodes identical audio from it."""
+    path, meta = _write(tmp_path, model)
+    dw = meta["decoder"]
+    f = qtts.ModelFile(path)
+    dv = f.decoder.view()
+    c = dw.cfg
+    assert (dv.hidden_size, dv.num_heads, dv.head_dim, dv.intermediate_size, dv.sliding_window, dv.codebook_dim,
+            dv.codebook_size, dv.vq_dim, dv.num_rest, dv.num_layers, dv.num_upsample, dv.num_vocos_blocks,
+            dv.rope_rows) == (c.hidden, c.heads, c.head_dim, c.inter, c.window, c.codebook_dim, c.codebook_size,
+                              c.vq_dim, c.num_rest, c.layers, len(c.upsample), len(c.vocos), c.rope_rows)
+    import ctypes as C
+
+    assert np.array_equal(_arr(dv.rest_codebooks[1], C.c_float, dw.rest_codebooks[1].size), dw.rest_codebooks[1])
+    r = dv.vocos_blocks[1].residuals[2].conv1
+    ref = dw.blocks[1]["residuals"][2]["conv1"]
+    assert (r.in_channels, r.out_channels, r.kernel_size, r.dilation) == (
+        ref["in_channels"], ref["out_channels"], ref["kernel_size"], ref["dilation"])
+    assert np.array_equal(_arr(r.weight, C.c_float, ref["weight"].size), ref["weight"])
+    assert dv.upsample[0].inner_dim == dw.upsample[0]["inner"]
+    codes = dw.synthetic_codes(6, 12)
+    assert np.array_equal(oracle.decode_to_audio(f.decoder, codes), oracle.decode_to_audio(dw, codes))
 
 
 def test_oracle_from_file_matches_weights(tmp_path, model):
