@@ -29,6 +29,7 @@ import qtts  # noqa: E402
 
 HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0  # dense binary16 MFMA
+FP32_PEAK_TFLOPS = 157.3  # dense f32 MFMA
 PROMPT = 64
 
 
@@ -191,6 +192,75 @@ def mfma_gemm_roofline(ctx, rows=64, iters=128, copies=32):
     }
 
 
+def decoder_flops(c, frames):
+    """Algorithmic multiply-adds x 2 of decode_to_audio at `frames` frames
+    (projections, convolutions with their valid taps, attention)."""
+    T, f = frames, 0
+    ad = c.heads * c.head_dim
+    f += 2 * T * c.codebook_dim * c.vq_dim * 2                       # two codebook projections
+    f += 2 * T * c.vq_dim * c.latent * 3                             # pre-conv, kernel 3
+    f += 2 * T * c.latent * c.hidden * 2                             # transformer in/out projections
+    win = sum(min(t + 1, c.window) for t in range(T))
+    f += c.layers * (2 * T * c.hidden * ad * 4 + 2 * T * c.hidden * c.inter * 3 + 2 * 2 * win * ad)
+    L = T
+    for s in c.upsample:
+        f += 2 * c.latent * c.latent * L * s                          # transposed conv, kernel = stride
+        L *= s
+        inner = c.latent * c.convnext_mult
+        f += 2 * L * (c.latent * c.convnext_kernel + 2 * c.latent * inner)
+    f += 2 * c.latent * c.vocos_channels * 7 * L
+    for (cin, cout, k, s) in c.vocos:
+        f += 2 * cin * cout * k * L                                   # each input sample meets every tap once
+        L *= s
+        f += len(c.dilations) * 2 * L * (cout * cout * c.res_kernel + cout * cout)
+    f += 2 * L * c.vocos[-1][1] * c.out_kernel
+    return f
+
+
+def decoder_measure(ctx, frames, cpu_frames=2, reps=3):
+    """decode_to_audio of `frames` frames of the 1.7B decoder (random
+    weights), codes and audio resident in HBM, HIP events on the context's
+    stream; and the oracle's decode of a short sample on the host cores."""
+    w = qtts.DecoderWeights(9)
+    dec = qtts.SpeechDecoder(ctx, w)
+    codes = w.synthetic_codes(12, frames)
+    hip = Hip()
+    n = dec.num_samples(frames)
+    dc, da = hip.malloc(codes.nbytes), hip.malloc(4 * n)
+    hip.h2d(dc, codes)
+    dec.decode_to_audio_device(dc, frames, frames, da, n)  # warmup (work buffers)
+    ctx.synchronize()
+    start, end = hip.event(), hip.event()
+    hip.record(start, ctx.stream)
+    for _ in range(reps):
+        dec.decode_to_audio_device(dc, frames, frames, da, n)
+    hip.record(end, ctx.stream)
+    avg_s = hip.elapsed_ms(start, end) / 1e3 / reps
+    hip.free(dc)
+    hip.free(da)
+    flops = decoder_flops(w.cfg, frames)
+    achieved = flops / avg_s / 1e12
+    out = {
+        "frames": frames, "samples": n, "ms": round(avg_s * 1e3, 2),
+        "audio_seconds_per_second": round(n / 24000.0 / avg_s, 1),
+        "roofline": {"bound": "fp32", "achieved": round(achieved, 2), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / FP32_PEAK_TFLOPS, 4), "algorithmic_flops": flops,
+                     "kernel": "whole decode (k_dec_gemm dominant)"},
+    }
+    if cpu_frames:
+        from oracle import oracle
+
+        small = w.synthetic_codes(13, cpu_frames)
+        t0 = time.perf_counter()
+        oracle.decode_to_audio(w, small)
+        dt = time.perf_counter() - t0
+        out["cpu_baseline"] = {"value": round(cpu_frames * 1920 / 24000.0 / dt, 4), "unit": "audio s/s",
+                               "cores": oracle.available_parallelism(), "kind": "port",
+                               "sample": f"{cpu_frames} frames (C oracle, convolutions split over output channels "
+                                         f"like the reference's threads)"}
+    return out
+
+
 def copy_calibration(ctx, nbytes=512 << 20):
     """One device-to-device copy of a known size: the plain copy kernel whose
     FETCH_SIZE / WRITE_SIZE counters calibrate the GEMV's."""
@@ -338,6 +408,8 @@ def main():
                           "timing": "HIP events around 5 prefill_talker_raw calls, host copies included",
                           "gemm": mfma_gemm_roofline(ctx)}
         log(f"prefill {out['prefill']}")
+        out["decoder"] = decoder_measure(ctx, args.steps, cpu_frames=0 if args.no_cpu else 2)
+        log(f"decoder {out['decoder']}")
     if not args.no_cpu:
         lh_np, lg_np = lh, lg
         kv_cpu, lh_np, lg_np = prefill()
