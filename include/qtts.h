@@ -243,6 +243,21 @@ qtts_status qtts_generate_codes(qtts_talker *t, qtts_predictor *p, qtts_kv *talk
                                 const qtts_loop_params *params, uint64_t seed, uint32_t *codes,
                                 int32_t *n_frames);
 
+/* `batch` independent loops of generate_speech (src/generate_new.rs:229-300)
+ * in lockstep over the shared weights -- the batched long-form case.  Stream
+ * b has its own prefilled talker cache talker_kvs[b] (all of one capacity),
+ * last_hidden + b*hidden, logits + b*vocab, positions[b], trailing text
+ * trailing_text + b*trailing_len*hidden and seeds[b]; its codes go to
+ * codes + b*16*max_codes ([16][max_codes] as above) and its frame count to
+ * n_frames[b].  The predictor caches are internal.  Every product runs on the
+ * matrix cores with one row per stream.  QTTS_ESHAPE when a weight cannot
+ * use them (a scale above 8188 in magnitude); at most 64 streams. */
+qtts_status qtts_generate_codes_batch(qtts_talker *t, qtts_predictor *p, int32_t batch, qtts_kv *const *talker_kvs,
+                                      const float *last_hidden, const float *logits, const int32_t *positions,
+                                      const float *trailing_text, int32_t trailing_len, const float *tts_pad_embed,
+                                      const qtts_loop_params *params, const uint64_t *seeds, uint32_t *codes,
+                                      int32_t *n_frames);
+
 #ifdef __cplusplus
 }
 #endif

@@ -365,7 +365,8 @@ qtts_status grow(qtts_ctx *c, T **buf, size_t *cap, size_t need) {
 // 8 (each wave keeps 8 steps of operand loads in flight; measured fastest at
 // every talker shape, 64 rows) unless K is short.
 qtts_status run_gemm_mfma(qtts_ctx *c, const DevQ4Mfma &w, const float *x, int M, int ldx, int mode,
-                          const uint16_t *gamma, float *y, int ldy, const float *bias, bool accumulate) {
+                          const uint16_t *gamma, float *y, int ldy, const float *bias, bool accumulate,
+                          float *norm_out = nullptr, int ldn = 0) {
     const int K = w.K, N = w.N, Ks = K / 16, panels = N / 32;
     if (K % 16 || N % 32 || K > kMfmaRowsMaxK || ldx % 4 || ((uintptr_t)x & 15))
         return fail(c, QTTS_ESHAPE, "MFMA GEMM: unsupported shape or unaligned rows");
@@ -389,6 +390,8 @@ qtts_status run_gemm_mfma(qtts_ctx *c, const DevQ4Mfma &w, const float *x, int M
         r.xh = c->mfma_x;
         r.xl = c->mfma_x + (size_t)Mpad * K;
         r.rexp = reinterpret_cast<int *>(c->mfma_x + (size_t)2 * 64 * K);
+        r.norm_out = norm_out ? norm_out + (size_t)r0 * ldn : nullptr;
+        r.ldn = ldn;
         launch_mfma_rows(c->stream, r);
         QTTS_TRY(check_launch(c, "k_mfma_rows"));
         GemmMfmaParams p{};
@@ -626,6 +629,8 @@ struct qtts_talker {
     // made by the first prefill of >= kMfmaMinRows rows
     std::vector<DevQ4Mfma> mfma;
     int mfma_state = 0;  // 0 not tried, 1 made, -1 some weight cannot use the matrix cores
+    DevQ4Mfma head_mfma{};  // codec head, for the batched loop
+    int head_mfma_state = 0;
     // loop buffers
     uint32_t *codes = nullptr;
     size_t codes_cap = 0;
@@ -660,6 +665,12 @@ struct qtts_predictor {
     int *status = nullptr;
     std::unique_ptr<EngProgram> prog;
     uint64_t prog_kv = 0;  // serial of the cache prog was built for
+    // MFMA operand copies for the batched loop: 4 per layer, the input
+    // projection, the heads (made by the first batched call)
+    std::vector<DevQ4Mfma> mfma;
+    DevQ4Mfma mfma_in{};
+    std::vector<DevQ4Mfma> mfma_heads;
+    int mfma_state = 0;  // 0 not tried, 1 made, -1 a weight cannot use the matrix cores
 };
 
 // ===========================================================================
@@ -2659,6 +2670,403 @@ qtts_status qtts_decode_to_audio(qtts_decoder *d, const uint32_t *codes, int32_t
     QTTS_TRY(dec_decode(d, d->codes, frames, frames, d->audio, need, n_samples));
     HIP_TRY(c, hipMemcpyAsync(audio, d->audio, (size_t)*n_samples * sizeof(float), hipMemcpyDeviceToHost, c->stream));
     return sync(c);
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------
+// Batched streams: `batch` independent generate_speech loops
+// (src/generate_new.rs:242-300) in lockstep over shared weights.  Every
+// product runs on the matrix cores with one row per stream (two per stream
+// in the predictor's first pass); attention and the K/V appends address each
+// row's own cache through per-row tables.
+// ---------------------------------------------------------------------------
+namespace {
+
+struct RowTab {
+    const float *const *k = nullptr, *const *v = nullptr;  // per-row layer-0 cache bases
+    const int *pos = nullptr, *kv = nullptr;               // per-row position / cache row (null: 0)
+    int stride = 1, pos0 = 0, kv0 = 0, cap = 0;
+};
+
+qtts_status make_stack_mfma(qtts_ctx *c, Owner &own, const Stack &st, std::vector<DevQ4Mfma> *out, bool *ok) {
+    std::vector<void *> mems;
+    *ok = true;
+    for (const DevLayer &Ly : st.L)
+        for (const DevQ4 *w : {&Ly.qkv, &Ly.o, &Ly.gu, &Ly.down}) {
+            DevQ4Mfma m{};
+            void *mem = nullptr;
+            bool one = false;
+            const qtts_status s = make_mfma_copy(c, *w, &mem, &m, &one);
+            if (s != QTTS_OK || !one) {
+                for (void *p : mems) (void)hipFree(p);
+                out->clear();
+                *ok = false;
+                return s;
+            }
+            mems.push_back(mem);
+            out->push_back(m);
+        }
+    for (void *p : mems) own.ptrs.push_back(p);
+    return QTTS_OK;
+}
+
+qtts_status make_head_mfma(qtts_talker *t) {
+    if (t->head_mfma_state != 0) return QTTS_OK;
+    void *mem = nullptr;
+    bool ok = false;
+    QTTS_TRY(make_mfma_copy(t->ctx, t->head, &mem, &t->head_mfma, &ok));
+    if (mem) t->own.ptrs.push_back(mem);
+    t->head_mfma_state = ok ? 1 : -1;
+    return QTTS_OK;
+}
+
+qtts_status make_predictor_mfma(qtts_predictor *p) {
+    qtts_ctx *c = p->ctx;
+    bool ok = false;
+    QTTS_TRY(make_stack_mfma(c, p->own, p->st, &p->mfma, &ok));
+    std::vector<void *> mems;
+    auto one = [&](const DevQ4 &w, DevQ4Mfma *m) -> qtts_status {
+        void *mem = nullptr;
+        bool good = false;
+        QTTS_TRY(make_mfma_copy(c, w, &mem, m, &good));
+        if (!good) ok = false;
+        if (mem) mems.push_back(mem);
+        return QTTS_OK;
+    };
+    if (ok && !p->identity_proj) QTTS_TRY(one(p->in_proj, &p->mfma_in));
+    p->mfma_heads.assign((size_t)p->groups, DevQ4Mfma{});
+    for (int g = 0; ok && g < p->groups; g++) QTTS_TRY(one(p->heads[g], &p->mfma_heads[(size_t)g]));
+    for (void *m : mems) p->own.ptrs.push_back(m);
+    p->mfma_state = ok ? 1 : -1;
+    return QTTS_OK;
+}
+
+// One layer stack over M independent rows (per-row caches from R).
+qtts_status layers_batched(qtts_ctx *c, const Stack &st, const DevQ4Mfma *W, const RowTab &R, float *x, int M,
+                           float *raw, float *q, float *a, int nsplit) {
+    const int hidden = st.hidden, qd = st.nq * st.hd, nqkv = qd + 2 * st.nkv * st.hd;
+    if ((size_t)M * st.nq * nsplit * (st.hd + 2) > kAttnPartFloats || M * st.nkv > kAttnCounters)
+        return fail(c, QTTS_ESHAPE, "batched attention: too many rows for the split buffers");
+    for (int l = 0; l < st.layers; l++) {
+        const DevLayer &Ly = st.L[l];
+        const DevQ4Mfma *Wl = W + (size_t)4 * l;
+        const long long layer_off = (long long)l * st.nkv * R.cap * st.hd;
+        QTTS_TRY(run_gemm_mfma(c, Wl[0], x, M, hidden, MFMA_ROWS_RMSNORM, Ly.in_g, raw, nqkv, nullptr, false));
+        QkvRowsParams qp{};
+        qp.raw = raw;
+        qp.ldr = nqkv;
+        qp.M = M;
+        qp.n_q_heads = st.nq;
+        qp.n_kv_heads = st.nkv;
+        qp.head_dim = st.hd;
+        qp.q_norm = Ly.q_norm;
+        qp.k_norm = Ly.k_norm;
+        qp.rope_cos = st.rope_cos;
+        qp.rope_sin = st.rope_sin;
+        qp.rope_rows = st.rope_rows;
+        qp.rope_skip_oob = st.rope_skip_oob;
+        qp.q = q;
+        qp.ldq = qd;
+        qp.kv_cap = R.cap;
+        qp.pos0 = R.pos0;
+        qp.row0 = R.kv0;
+        qp.row_k = R.k;
+        qp.row_v = R.v;
+        qp.row_pos = R.pos;
+        qp.row_kv = R.kv;
+        qp.row_stride = R.stride;
+        qp.layer_off = layer_off;
+        launch_qkv_rows(c->stream, qp);
+        QTTS_TRY(check_launch(c, "k_qkv_rows"));
+        AttnParams ap{};
+        ap.q = q;
+        ap.ldq = qd;
+        ap.kv_cap = R.cap;
+        ap.nq = st.nq;
+        ap.nkv = st.nkv;
+        ap.hd = st.hd;
+        ap.kvlen_const = R.kv0;
+        ap.nsplit = nsplit;
+        ap.scale = 1.0f / sqrtf((float)st.hd);  // src/talker.rs:305
+        ap.part = c->attn_part;
+        ap.counters = c->attn_counters;
+        ap.out = a;
+        ap.ldo = qd;
+        ap.row_k = R.k;
+        ap.row_v = R.v;
+        ap.row_kv = R.kv;
+        ap.row_stride = R.stride;
+        ap.layer_off = layer_off;
+        launch_attention(c->stream, ap, M);
+        QTTS_TRY(check_launch(c, "k_attn"));
+        QTTS_TRY(run_gemm_mfma(c, Wl[1], a, M, qd, MFMA_ROWS_PLAIN, nullptr, x, hidden, nullptr, true));
+        QTTS_TRY(run_gemm_mfma(c, Wl[2], x, M, hidden, MFMA_ROWS_RMSNORM, Ly.post_g, raw, 2 * st.inter, nullptr,
+                               false));
+        QTTS_TRY(run_gemm_mfma(c, Wl[3], raw, M, 2 * st.inter, MFMA_ROWS_SWIGLU, nullptr, x, hidden, nullptr, true));
+    }
+    return QTTS_OK;
+}
+
+// Device allocations of one batched call, freed on every return path.
+struct DevAllocs {
+    std::vector<void *> ptrs;
+    ~DevAllocs() {
+        for (void *p : ptrs) (void)hipFree(p);
+    }
+    template <class T>
+    qtts_status get(qtts_ctx *c, T **out, size_t count) {
+        void *p = nullptr;
+        if (hipMalloc(&p, (count ? count : 1) * sizeof(T)) != hipSuccess)
+            return fail(c, QTTS_ENOMEM, "batched loop buffers");
+        ptrs.push_back(p);
+        *out = reinterpret_cast<T *>(p);
+        return QTTS_OK;
+    }
+};
+
+}  // namespace
+
+extern "C" {
+
+qtts_status qtts_generate_codes_batch(qtts_talker *t, qtts_predictor *p, int32_t batch, qtts_kv *const *talker_kvs,
+                                      const float *last_hidden, const float *logits, const int32_t *positions,
+                                      const float *trailing_text, int32_t trailing_len, const float *tts_pad_embed,
+                                      const qtts_loop_params *params, const uint64_t *seeds, uint32_t *codes,
+                                      int32_t *n_frames) {
+    if (!t || batch < 1 || !talker_kvs || !last_hidden || !logits || !positions || !params || !seeds || !codes ||
+        !n_frames)
+        return QTTS_EINVAL;
+    qtts_ctx *c = t->ctx;
+    const bool talker_only = params->talker_only || !p;
+    if (!talker_only && (!tts_pad_embed || (trailing_len > 0 && !trailing_text)))
+        return fail(c, QTTS_EINVAL, "predictor loop needs tts_pad_embed and trailing text");
+    if (trailing_len < 0) return fail(c, QTTS_EINVAL, "trailing_len < 0");
+    if (batch > 64) return fail(c, QTTS_ERANGE, "at most 64 streams per batch");
+    const int B = batch, max_codes = params->max_codes;
+    for (int b = 0; b < B; b++) n_frames[b] = 0;
+    if (max_codes <= 0) return QTTS_OK;
+    const Stack &ts = t->st;
+    const int H = ts.hidden, V = t->vocab, cap = talker_kvs[0] ? talker_kvs[0]->cap : 0;
+    for (int b = 0; b < B; b++) {
+        qtts_kv *kv = talker_kvs[b];
+        if (!kv) return fail(c, QTTS_EINVAL, "null talker cache");
+        QTTS_TRY(check_kv(c, ts, kv));
+        if (kv->cap != cap) return fail(c, QTTS_ESHAPE, "batched talker caches must share one capacity");
+        if (kv->len + max_codes > kv->cap) return fail(c, QTTS_ERANGE, "talker cache too small");
+        if (positions[b] < 0 || positions[b] + max_codes > t->max_pos)
+            return fail(c, QTTS_ERANGE, "positions beyond the RoPE table");
+    }
+    if (!talker_only && p->talker_hidden != H) return fail(c, QTTS_ESHAPE, "predictor input width != talker hidden");
+    // matrix-core operand copies
+    if (t->mfma_state == 0) QTTS_TRY(make_talker_mfma(t));
+    QTTS_TRY(make_head_mfma(t));
+    if (t->mfma_state != 1 || t->head_mfma_state != 1)
+        return fail(c, QTTS_ESHAPE, "batched loop: a talker weight cannot use the matrix cores");
+    if (!talker_only) {
+        if (p->mfma_state == 0) QTTS_TRY(make_predictor_mfma(p));
+        if (p->mfma_state != 1) return fail(c, QTTS_ESHAPE, "batched loop: a predictor weight cannot use the matrix cores");
+    }
+    const Stack *ps = talker_only ? nullptr : &p->st;
+    const int hp = ps ? ps->hidden : 0, pcap = talker_only ? 0 : p->groups + 1, G = talker_only ? 0 : p->groups;
+    const int t_raw = std::max(ts.nq * ts.hd + 2 * ts.nkv * ts.hd, 2 * ts.inter);
+    const int p_raw = ps ? std::max(ps->nq * ps->hd + 2 * ps->nkv * ps->hd, 2 * ps->inter) : 0;
+    const int qd_max = std::max(ts.nq * ts.hd, ps ? ps->nq * ps->hd : 0);
+    const size_t ncodes = (size_t)16 * max_codes;
+
+    DevAllocs A;
+    LoopState *S = nullptr;
+    uint32_t *dcodes = nullptr;
+    float *trail = nullptr, *pad = nullptr, *x = nullptr, *in2 = nullptr, *lg = nullptr, *raw = nullptr, *q = nullptr;
+    float *att = nullptr, *xp = nullptr, *plog = nullptr, *pk = nullptr, *pv = nullptr;
+    const float **tab = nullptr;
+    int *pos2 = nullptr;
+    QTTS_TRY(A.get(c, &S, (size_t)B));
+    QTTS_TRY(A.get(c, &dcodes, (size_t)B * ncodes));
+    QTTS_TRY(A.get(c, &trail, (size_t)B * std::max(trailing_len, 1) * H));
+    QTTS_TRY(A.get(c, &pad, (size_t)H));
+    QTTS_TRY(A.get(c, &x, (size_t)B * H));
+    QTTS_TRY(A.get(c, &in2, (size_t)2 * B * H));
+    QTTS_TRY(A.get(c, &lg, (size_t)B * V));
+    QTTS_TRY(A.get(c, &raw, (size_t)2 * B * std::max(t_raw, p_raw)));
+    QTTS_TRY(A.get(c, &q, (size_t)2 * B * qd_max));
+    QTTS_TRY(A.get(c, &att, (size_t)2 * B * qd_max));
+    QTTS_TRY(A.get(c, &tab, (size_t)8 * B));
+    if (!talker_only) {
+        QTTS_TRY(A.get(c, &xp, (size_t)2 * B * hp));
+        QTTS_TRY(A.get(c, &plog, (size_t)B * p->vocab));
+        const size_t pstride = (size_t)ps->layers * ps->nkv * pcap * ps->hd;
+        QTTS_TRY(A.get(c, &pk, (size_t)B * pstride));
+        QTTS_TRY(A.get(c, &pv, (size_t)B * pstride));
+        QTTS_TRY(A.get(c, &pos2, (size_t)2 * B));
+    }
+    // row tables: talker caches [B]; predictor caches, two rows per stream
+    // for the first pass [2B] and one per stream after it [B]
+    std::vector<const float *> htab((size_t)8 * B, nullptr);
+    std::vector<int> hpos2((size_t)2 * B);
+    for (int b = 0; b < B; b++) {
+        htab[b] = talker_kvs[b]->k;
+        htab[B + b] = talker_kvs[b]->v;
+        if (!talker_only) {
+            const size_t pstride = (size_t)ps->layers * ps->nkv * pcap * ps->hd;
+            const float *kb = pk + b * pstride, *vb = pv + b * pstride;
+            htab[2 * B + 2 * b] = htab[2 * B + 2 * b + 1] = kb;  // [2B] K
+            htab[4 * B + 2 * b] = htab[4 * B + 2 * b + 1] = vb;  // [2B] V
+            htab[6 * B + b] = kb;                                // [B] K
+            htab[7 * B + b] = vb;                                // [B] V
+            hpos2[2 * b] = 0;
+            hpos2[2 * b + 1] = 1;
+        }
+    }
+    HIP_TRY(c, hipMemcpyAsync(tab, htab.data(), htab.size() * sizeof(float *), hipMemcpyHostToDevice, c->stream));
+    if (!talker_only)
+        HIP_TRY(c, hipMemcpyAsync(pos2, hpos2.data(), hpos2.size() * sizeof(int), hipMemcpyHostToDevice, c->stream));
+    const float *const *t_k = tab, *const *t_v = tab + B;
+    const float *const *p_k2 = tab + 2 * B, *const *p_v2 = tab + 4 * B;
+    const float *const *p_k1 = tab + 6 * B, *const *p_v1 = tab + 7 * B;
+    // initial state
+    std::vector<LoopState> init((size_t)B);
+    for (int b = 0; b < B; b++) {
+        init[b] = LoopState{};
+        init[b].pos = positions[b];
+        init[b].kvlen = talker_kvs[b]->len;
+        init[b].rng = seeds[b];
+    }
+    HIP_TRY(c, hipMemcpyAsync(S, init.data(), sizeof(LoopState) * B, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(c, hipMemsetAsync(dcodes, 0, (size_t)B * ncodes * sizeof(uint32_t), c->stream));
+    if (trailing_len > 0)
+        HIP_TRY(c, hipMemcpyAsync(trail, trailing_text, sizeof(float) * B * trailing_len * H, hipMemcpyHostToDevice,
+                                  c->stream));
+    if (tts_pad_embed)
+        HIP_TRY(c, hipMemcpyAsync(pad, tts_pad_embed, sizeof(float) * H, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(c, hipMemcpyAsync(lg, logits, sizeof(float) * B * V, hipMemcpyHostToDevice, c->stream));
+    if (!talker_only)
+        HIP_TRY(c, hipMemcpy2DAsync(in2, sizeof(float) * 2 * H, last_hidden, sizeof(float) * H, sizeof(float) * H, B,
+                                    hipMemcpyHostToDevice, c->stream));
+    const long long SS = (long long)sizeof(LoopState), SW = SS / 4;
+    const int tsplit = attn_nsplit(cap, 16);
+    RowTab TR;
+    TR.k = t_k;
+    TR.v = t_v;
+    TR.pos = &S[0].pos;
+    TR.kv = &S[0].kvlen;
+    TR.stride = (int)SW;
+    TR.cap = cap;
+
+    for (int f = 0; f < max_codes; f++) {
+        // 1. code 0 of every stream (sample_token, src/generate_new.rs:329-391)
+        SampleParams sp{};
+        sp.logits = lg;
+        sp.vocab = V;
+        sp.temperature = params->sampler.temperature;
+        sp.top_k = params->sampler.top_k;
+        sp.penalty = params->sampler.repetition_penalty;
+        sp.greedy = params->sampler.greedy;
+        sp.prev = S[0].prev;
+        sp.n_prev = 16;
+        sp.rng = &S[0].rng;
+        sp.token_out = &S[0].cur[0];
+        sp.status = &S[0].status;
+        sp.done = &S[0].done;
+        sp.stop_on_eos = params->stop_on_eos;
+        sp.eos = params->codec_eos_id;
+        sp.codes = dcodes;
+        sp.frame = &S[0].frame;
+        sp.max_codes = max_codes;
+        sp.prev_out = &S[0].prev[0];
+        sp.batch = B;
+        sp.state_stride = SS;
+        sp.logits_stride = V;
+        sp.codes_stride = (long long)ncodes;
+        launch_sample(c->stream, sp);
+        QTTS_TRY(check_launch(c, "k_sample"));
+        // 2. the predictor's 15 passes (generate_acoustic_codes, src/code_predictor.rs:218-273)
+        if (!talker_only) {
+            launch_embed_rows(c->stream, t->emb, &S[0].cur[0], SW, B, in2 + H, 2LL * H);
+            QTTS_TRY(check_launch(c, "k_embed_rows"));
+            for (int g = 0; g < G; g++) {
+                RowTab PR;
+                PR.cap = pcap;
+                int M;
+                if (g == 0) {
+                    M = 2 * B;
+                    if (p->identity_proj)
+                        HIP_TRY(c, hipMemcpyAsync(xp, in2, sizeof(float) * 2 * B * hp, hipMemcpyDeviceToDevice,
+                                                  c->stream));
+                    else
+                        QTTS_TRY(run_gemm_mfma(c, p->mfma_in, in2, M, H, MFMA_ROWS_PLAIN, nullptr, xp, hp, p->bias,
+                                               false));
+                    PR.k = p_k2;
+                    PR.v = p_v2;
+                    PR.pos = pos2;
+                    PR.kv = pos2;
+                    PR.stride = 1;
+                } else {
+                    M = B;
+                    float *dst = p->identity_proj ? xp : in2;
+                    launch_embed_rows(c->stream, p->emb[g - 1], &S[0].cur[g], SW, B, dst, p->identity_proj ? hp : H);
+                    QTTS_TRY(check_launch(c, "k_embed_rows"));
+                    if (!p->identity_proj)
+                        QTTS_TRY(run_gemm_mfma(c, p->mfma_in, in2, M, H, MFMA_ROWS_PLAIN, nullptr, xp, hp, p->bias,
+                                               false));
+                    PR.k = p_k1;
+                    PR.v = p_v1;
+                    PR.pos0 = g + 1;
+                    PR.kv0 = g + 1;
+                }
+                QTTS_TRY(layers_batched(c, *ps, p->mfma.data(), PR, xp, M, raw, q, att, 1));
+                // head g on the last row of each stream
+                const float *hx = g == 0 ? xp + hp : xp;
+                const int hld = g == 0 ? 2 * hp : hp;
+                QTTS_TRY(run_gemm_mfma(c, p->mfma_heads[(size_t)g], hx, B, hld, MFMA_ROWS_RMSNORM, ps->final_g, plog,
+                                       p->vocab, nullptr, false));
+                launch_argmax_rows(c->stream, plog, B, p->vocab, &S[0].cur[1 + g], SW, &S[0].status, SS);
+                QTTS_TRY(check_launch(c, "k_argmax_rows"));
+            }
+        }
+        // 3. the next talker input (src/generate_new.rs:270-286)
+        EmbSumParams e{};
+        e.mode = 0;  // talker-only: num_groups 0 gives codec_emb[code0] alone
+        e.codec_emb = t->emb;
+        if (!talker_only)
+            for (int g = 0; g < G; g++) e.group_emb[g] = p->emb[g];
+        e.num_groups = G;
+        e.cur = S[0].cur;
+        e.trailing = trail;
+        e.trailing_len = trailing_len;
+        e.pad = pad;
+        e.frame = &S[0].frame;
+        e.out = x;
+        e.hidden = H;
+        e.d_done = &S[0].done;
+        e.codes = dcodes;
+        e.max_codes = max_codes;
+        e.prev = S[0].prev;
+        e.batch = B;
+        e.state_stride = SS;
+        e.trailing_stride = (long long)trailing_len * H;
+        e.out_stride = H;
+        e.codes_stride = (long long)ncodes;
+        launch_embed_sum(c->stream, e);
+        QTTS_TRY(check_launch(c, "k_embed_sum"));
+        // 4. talker step for every stream, then the codec head
+        QTTS_TRY(layers_batched(c, ts, t->mfma.data(), TR, x, B, raw, q, att, tsplit));
+        QTTS_TRY(run_gemm_mfma(c, t->head_mfma, x, B, H, MFMA_ROWS_RMSNORM, ts.final_g, lg, V, nullptr, false,
+                               talker_only ? nullptr : in2, 2 * H));
+        launch_advance(c->stream, S, 1, B);
+        QTTS_TRY(check_launch(c, "k_advance"));
+    }
+    QTTS_TRY(sync(c));
+    std::vector<LoopState> fin((size_t)B);
+    HIP_TRY(c, hipMemcpy(fin.data(), S, sizeof(LoopState) * B, hipMemcpyDeviceToHost));
+    for (int b = 0; b < B; b++)
+        if (fin[b].status != 0) return fail(c, (qtts_status)fin[b].status, "NaN logits during generation");
+    HIP_TRY(c, hipMemcpy(codes, dcodes, (size_t)B * ncodes * sizeof(uint32_t), hipMemcpyDeviceToHost));
+    for (int b = 0; b < B; b++) {
+        n_frames[b] = fin[b].frame;
+        talker_kvs[b]->len += fin[b].frame;
+    }
+    return QTTS_OK;
 }
 
 }  // extern "C"

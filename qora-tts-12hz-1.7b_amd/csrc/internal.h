@@ -49,6 +49,8 @@ struct MfmaRowsParams {
     const uint16_t *gamma;  // RMSNORM weight (binary16 bits)
     _Float16 *xh, *xl;      // [Mpad / 32][K / 16][64][8], the MFMA A-operand order
     int *rexp;              // [Mpad] row exponents
+    float *norm_out;        // optional: the prologue's rows (f32) at norm_out[m * ldn + k]
+    int ldn;
 };
 
 // apply_qk_norm + RoPE + KV append over M rows of a fused QKV projection
@@ -65,6 +67,14 @@ struct QkvRowsParams {
     float *kcache, *vcache;  // [n_kv_heads][kv_cap][head_dim]
     int kv_cap;
     int pos0, row0;  // RoPE position and cache row of row 0
+    // independent rows (batched streams): with row_k set, row m's layer-0
+    // K/V bases are row_k[m] / row_v[m] (this layer at + layer_off), its
+    // position pos0 + row_pos[m * row_stride] and cache row
+    // row0 + row_kv[m * row_stride] (a null table counts as zeros)
+    const float *const *row_k, *const *row_v;
+    const int *row_pos, *row_kv;
+    int row_stride;
+    long long layer_off;
 };
 
 // ---- speech decoder (csrc/decoder.hip) ----
@@ -207,6 +217,13 @@ struct AttnParams {
     float *out;          // [M][nq*hd]
     int ldo;
     const int *d_done;
+    // independent rows (batched streams): with row_k set, row m attends to
+    // its own cache (row_k[m] / row_v[m] + layer_off) over
+    // kvlen_const + row_kv[m * row_stride] + 1 positions
+    const float *const *row_k, *const *row_v;
+    const int *row_kv;
+    int row_stride;
+    long long layer_off;
 };
 
 // Device-resident state of one generation loop (one per talker).
@@ -242,6 +259,11 @@ struct SampleParams {
     const int *frame;
     int max_codes;
     uint32_t *prev_out;  // prev_tokens[0] = token
+    // batched streams: block b works on stream b; every pointer above into a
+    // LoopState moves by b * state_stride bytes, logits by b * logits_stride
+    // floats, codes by b * codes_stride words
+    int batch;
+    long long state_stride, logits_stride, codes_stride;
 };
 
 struct EmbSumParams {
@@ -261,6 +283,12 @@ struct EmbSumParams {
     uint32_t *codes;
     int max_codes;
     uint32_t *prev;
+    // batched streams (grid.y = batch): LoopState pointers (cur, frame,
+    // d_done, prev) move by y * state_stride bytes, trailing by
+    // y * trailing_stride floats, out by y * out_stride floats, codes by
+    // y * codes_stride words
+    int batch;
+    long long state_stride, trailing_stride, out_stride, codes_stride;
 };
 
 // Launchers (kernels.hip).
@@ -286,7 +314,11 @@ void launch_dec_snake(hipStream_t st, const float *x, const float *alpha, const 
                       float *out);
 void launch_gemm_mfma(hipStream_t st, const GemmMfmaParams &p, int mt, int sw, int kc);
 void launch_embed_sum(hipStream_t st, const EmbSumParams &p);
-void launch_advance(hipStream_t st, LoopState *s, int frame_step);
+void launch_advance(hipStream_t st, LoopState *s, int frame_step, int batch = 1);
+void launch_embed_rows(hipStream_t st, const DevQ4 &w, const uint32_t *tok, long long tok_stride, int rows, float *out,
+                       long long out_stride);
+void launch_argmax_rows(hipStream_t st, const float *logits, int rows, int n, uint32_t *out, long long out_stride,
+                        int *status, long long status_stride);
 void launch_repack_q4(hipStream_t st, const uint8_t *packed, const uint16_t *scales, int K, int N, int col0,
                       int Ntot, uint4 *wq, uint16_t *ws);
 

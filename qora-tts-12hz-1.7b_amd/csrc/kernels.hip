@@ -12,6 +12,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cfloat>
+#include <type_traits>
 #include <cmath>
 
 #include "../../include/qtts.h"
@@ -369,7 +370,14 @@ __global__ __launch_bounds__(256) void k_qkv_rows(QkvRowsParams P) {
     const int hd = P.head_dim, half = hd / 2;
     const bool is_q = head < P.n_q_heads;
     const bool is_k = !is_q && head < P.n_q_heads + P.n_kv_heads;
-    const int pos = P.pos0 + m, row = P.row0 + m;
+    int pos = P.pos0 + m, row = P.row0 + m;
+    float *kcache = P.kcache, *vcache = P.vcache;
+    if (P.row_k) {
+        pos = P.pos0 + (P.row_pos ? P.row_pos[(size_t)m * P.row_stride] : 0);
+        row = P.row0 + (P.row_kv ? P.row_kv[(size_t)m * P.row_stride] : 0);
+        kcache = const_cast<float *>(P.row_k[m]) + P.layer_off;
+        vcache = const_cast<float *>(P.row_v[m]) + P.layer_off;
+    }
     const float *src = P.raw + (size_t)m * P.ldr + (size_t)head * hd;
     if (is_q || is_k) {
         const float v = tid < hd ? src[tid] : 0.0f;
@@ -393,14 +401,14 @@ __global__ __launch_bounds__(256) void k_qkv_rows(QkvRowsParams P) {
                 dst = P.q + (size_t)m * P.ldq + (size_t)head * hd;
             } else {
                 const int kh = head - P.n_q_heads;
-                dst = P.kcache + ((size_t)kh * P.kv_cap + row) * hd;
+                dst = kcache + ((size_t)kh * P.kv_cap + row) * hd;
             }
             dst[tid] = o1;
             dst[tid + half] = o2;
         }
     } else {
         const int vh = head - P.n_q_heads - P.n_kv_heads;
-        if (tid < hd) P.vcache[((size_t)vh * P.kv_cap + row) * hd + tid] = src[tid];
+        if (tid < hd) vcache[((size_t)vh * P.kv_cap + row) * hd + tid] = src[tid];
     }
 }
 
@@ -428,7 +436,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams P) {
     const int m = blockIdx.y;
     const int kvh = blockIdx.x / P.nsplit, sp = blockIdx.x - kvh * P.nsplit;
     const int G = P.nq / P.nkv;
-    const int L = (P.d_kvlen ? *P.d_kvlen : P.kvlen_const) + m + 1;
+    const int L = P.row_k ? P.kvlen_const + (P.row_kv ? P.row_kv[(size_t)m * P.row_stride] : 0) + 1
+                          : (P.d_kvlen ? *P.d_kvlen : P.kvlen_const) + m + 1;
     const int chunk = (L + P.nsplit - 1) / P.nsplit;
     const int t0 = sp * chunk;
     const int t1 = min(L, t0 + chunk);
@@ -440,8 +449,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams P) {
     }
     __syncthreads();
 
-    const float *Kb = P.kcache + (size_t)kvh * P.kv_cap * HD;
-    const float *Vb = P.vcache + (size_t)kvh * P.kv_cap * HD;
+    const float *Kb = (P.row_k ? P.row_k[m] + P.layer_off : P.kcache) + (size_t)kvh * P.kv_cap * HD;
+    const float *Vb = (P.row_v ? P.row_v[m] + P.layer_off : P.vcache) + (size_t)kvh * P.kv_cap * HD;
 
     // scores: 16 lanes per position, 8 dims per lane.
     {
@@ -566,7 +575,27 @@ __device__ int block_exscan_1024(int v, int *wsum /* >= 16 */, int *total) {
 
 }  // namespace
 
-__global__ __launch_bounds__(kSampleThreads) void k_sample(SampleParams P) {
+template <class T>
+__device__ __forceinline__ T *byte_off(T *p, long long bytes) {
+    return p ? reinterpret_cast<T *>(reinterpret_cast<char *>(const_cast<typename std::remove_const<T>::type *>(p)) +
+                                     bytes)
+             : p;
+}
+
+__global__ __launch_bounds__(kSampleThreads) void k_sample(SampleParams Pin) {
+    SampleParams P = Pin;
+    if (Pin.batch > 1) {
+        const long long b = blockIdx.x, so = b * Pin.state_stride;
+        P.logits += b * Pin.logits_stride;
+        P.prev = byte_off(P.prev, so);
+        P.rng = byte_off(P.rng, so);
+        P.token_out = byte_off(P.token_out, so);
+        P.status = byte_off(P.status, so);
+        P.done = byte_off(P.done, so);
+        P.frame = byte_off(P.frame, so);
+        P.prev_out = byte_off(P.prev_out, so);
+        if (P.codes) P.codes += b * Pin.codes_stride;
+    }
     if (P.done && *P.done) return;
     extern __shared__ unsigned char smem_raw[];
     float *s = reinterpret_cast<float *>(smem_raw);
@@ -798,7 +827,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleParams P) {
 
 void launch_sample(hipStream_t st, const SampleParams &p) {
     const size_t smem = (size_t)p.vocab * (sizeof(float) + sizeof(int));
-    hipLaunchKernelGGL(k_sample, dim3(1), dim3(kSampleThreads), smem, st, p);
+    hipLaunchKernelGGL(k_sample, dim3((unsigned)(p.batch > 1 ? p.batch : 1)), dim3(kSampleThreads), smem, st, p);
 }
 
 // ---------------------------------------------------------------------------
@@ -819,7 +848,18 @@ void launch_embed_row(hipStream_t st, const DevQ4 &w, const uint32_t *d_token, f
 // Next talker input: codec_emb[code0] + sum_g group_emb[g][code_g] + text row
 // (src/generate_new.rs:270-286, src/code_predictor.rs:280-293), in the
 // reference's order of additions; the frame's codes are filed here too.
-__global__ void k_embed_sum(EmbSumParams P) {
+__global__ void k_embed_sum(EmbSumParams Pin) {
+    EmbSumParams P = Pin;
+    if (Pin.batch > 1) {
+        const long long b = blockIdx.y, so = b * Pin.state_stride;
+        P.cur = byte_off(P.cur, so);
+        P.frame = byte_off(P.frame, so);
+        P.d_done = byte_off(P.d_done, so);
+        P.prev = byte_off(P.prev, so);
+        if (P.trailing) P.trailing += b * Pin.trailing_stride;
+        P.out += b * Pin.out_stride;
+        if (P.codes) P.codes += b * Pin.codes_stride;
+    }
     if (P.d_done && *P.d_done) return;
     const int j = blockIdx.x * blockDim.x + threadIdx.x;
     const int frame = P.frame ? *P.frame : 0;
@@ -854,18 +894,90 @@ __global__ void k_embed_sum(EmbSumParams P) {
 }
 
 void launch_embed_sum(hipStream_t st, const EmbSumParams &p) {
-    hipLaunchKernelGGL(k_embed_sum, dim3((unsigned)((p.hidden + 255) / 256)), dim3(256), 0, st, p);
+    hipLaunchKernelGGL(k_embed_sum, dim3((unsigned)((p.hidden + 255) / 256), (unsigned)(p.batch > 1 ? p.batch : 1)),
+                       dim3(256), 0, st, p);
 }
 
-__global__ void k_advance(LoopState *s, int frame_step) {
+__global__ void k_advance(LoopState *states, int frame_step, int batch) {
+    const int b = threadIdx.x;
+    if (b >= batch) return;
+    LoopState *s = states + b;
     if (s->done) return;
     s->pos += 1;
     s->kvlen += 1;
     s->frame += frame_step;
 }
 
-void launch_advance(hipStream_t st, LoopState *s, int frame_step) {
-    hipLaunchKernelGGL(k_advance, dim3(1), dim3(1), 0, st, s, frame_step);
+void launch_advance(hipStream_t st, LoopState *s, int frame_step, int batch) {
+    hipLaunchKernelGGL(k_advance, dim3(1), dim3((unsigned)((batch + 63) / 64 * 64)), 0, st, s, frame_step, batch);
+}
+
+// Row r = embedding row tok[r * tok_stride] of w (embed_lookup_q4,
+// src/gemv.rs:377-400, exact), at out + r * out_stride.
+__global__ void k_embed_rows(DevQ4 w, const uint32_t *tok, long long tok_stride, float *out, long long out_stride) {
+    const int j = blockIdx.x * blockDim.x + threadIdx.x, r = blockIdx.y;
+    if (j >= w.N) return;
+    const uint32_t t = tok[(size_t)r * tok_stride];
+    out[(size_t)r * out_stride + j] = t < (uint32_t)w.K ? q4_element(w, t, j) : 0.0f;
+}
+
+void launch_embed_rows(hipStream_t st, const DevQ4 &w, const uint32_t *tok, long long tok_stride, int rows, float *out,
+                       long long out_stride) {
+    hipLaunchKernelGGL(k_embed_rows, dim3((unsigned)((w.N + 255) / 256), (unsigned)rows), dim3(256), 0, st, w, tok,
+                       tok_stride, out, out_stride);
+}
+
+// sample_argmax (src/code_predictor.rs:328-334) of each row: the last index
+// of the maximum; a NaN sets *status (per row) to QTTS_ENAN and gives 0.
+__global__ __launch_bounds__(256) void k_argmax_rows(const float *logits, int n, uint32_t *out, long long out_stride,
+                                                     int *status, long long status_stride) {
+    __shared__ float sv[256];
+    __shared__ int si[256];
+    __shared__ int snan;
+    const int r = blockIdx.x, tid = threadIdx.x;
+    const float *row = logits + (size_t)r * n;
+    if (tid == 0) snan = 0;
+    __syncthreads();
+    float bv = -INFINITY;
+    int bi = -1, nan = 0;
+    for (int i = tid; i < n; i += 256) {
+        const float v = row[i];
+        if (v != v)
+            nan = 1;
+        else if (bi < 0 || v >= bv) {
+            bv = v;
+            bi = i;
+        }
+    }
+    if (nan) atomicOr(&snan, 1);
+    sv[tid] = bv;
+    si[tid] = bi;
+    __syncthreads();
+    for (int stp = 128; stp > 0; stp >>= 1) {
+        if (tid < stp) {
+            const float ov = sv[tid + stp];
+            const int oi = si[tid + stp];
+            if (oi >= 0 && (si[tid] < 0 || ov > sv[tid] || (ov == sv[tid] && oi > si[tid]))) {
+                sv[tid] = ov;
+                si[tid] = oi;
+            }
+        }
+        __syncthreads();
+    }
+    if (tid == 0) {
+        if (snan) {
+            out[(size_t)r * out_stride] = 0u;
+            if (status) *byte_off(status, (long long)r * status_stride) = QTTS_ENAN;
+        } else {
+            out[(size_t)r * out_stride] = (uint32_t)(si[0] < 0 ? 0 : si[0]);
+        }
+    }
+}
+
+void launch_argmax_rows(hipStream_t st, const float *logits, int rows, int n, uint32_t *out, long long out_stride,
+                        int *status, long long status_stride) {
+    hipLaunchKernelGGL(k_argmax_rows, dim3((unsigned)rows), dim3(256), 0, st, logits, n, out, out_stride, status,
+                       status_stride);
 }
 
 // ---------------------------------------------------------------------------

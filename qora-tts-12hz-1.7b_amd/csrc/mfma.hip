@@ -150,6 +150,16 @@ __global__ __launch_bounds__(256) void k_mfma_rows(MfmaRowsParams P) {
         e = min(15 - E, 126);
     }
     if (tid == 0) P.rexp[m] = e;
+    if (P.norm_out) {
+#pragma unroll
+        for (int j = 0; j < G; j++) {
+            const int g = tid + 256 * j;
+            if (g >= ng) continue;
+            float *dst = P.norm_out + (size_t)m * P.ldn + 8 * g;
+#pragma unroll
+            for (int i = 0; i < 8; i++) dst[i] = v[j][i];
+        }
+    }
     // 3. the binary16 hi + lo split
 #pragma unroll
     for (int j = 0; j < G; j++) {

@@ -235,6 +235,8 @@ def load_library(path: str = LIB_PATH):
         "qtts_f32_to_f16": ([C.c_float], C.c_uint16),
         "qtts_f16_to_f32": ([C.c_uint16], C.c_float),
         "qtts_quantize_f32_to_q4": ([vp, i32, i32, vp, vp], None),
+        "qtts_generate_codes_batch": (
+            [vp, vp, i32, C.POINTER(vp), f32p, f32p, vp, f32p, i32, f32p, C.POINTER(LoopParams), vp, vp, vp], i32),
         "qtts_model_file_open": ([C.c_char_p, C.POINTER(vp)], i32),
         "qtts_model_file_error": ([], C.c_char_p),
         "qtts_model_file_close": ([vp], None),
@@ -268,7 +270,7 @@ def exported_symbols() -> List[str]:
         "qtts_embed_codec_token", "qtts_predictor_upload", "qtts_predictor_free", "qtts_generate_acoustic_codes",
         "qtts_get_acoustic_embeddings_sum", "qtts_sample_token", "qtts_generate_codes", "qtts_synth_u64",
         "qtts_synth_q4", "qtts_synth_normal_f32", "qtts_synth_normal_f16", "qtts_f32_to_f16", "qtts_f16_to_f32",
-        "qtts_quantize_f32_to_q4", "qtts_model_file_open", "qtts_model_file_error", "qtts_model_file_close",
+        "qtts_quantize_f32_to_q4", "qtts_generate_codes_batch", "qtts_model_file_open", "qtts_model_file_error", "qtts_model_file_close",
         "qtts_model_file_talker", "qtts_model_file_predictor", "qtts_model_file_text", "qtts_model_file_info",
         "qtts_model_file_decoder", "qtts_decoder_upload", "qtts_decoder_free", "qtts_decoder_num_samples",
         "qtts_decode_to_audio", "qtts_decode_to_audio_device",
@@ -979,3 +981,29 @@ def generate_codes(talker: Talker, predictor: Optional[CodePredictor], talker_kv
                                           position, _ptr(tt), tl, _ptr(pad), C.byref(params), seed, _ptr(codes),
                                           C.byref(n)))
     return codes[:, : n.value].copy()
+
+
+def generate_codes_batch(talker: Talker, predictor: Optional[CodePredictor], talker_kvs, last_hidden, logits,
+                         positions, trailing_text: Optional[np.ndarray], tts_pad_embed: Optional[np.ndarray],
+                         params: LoopParams, seeds) -> list:
+    """len(talker_kvs) independent frame loops in lockstep (one row per
+    stream on the matrix cores).  last_hidden [B][hidden], logits [B][vocab],
+    trailing_text [B][n][hidden] or None.  Returns each stream's codes as
+    [16][n_frames] uint32."""
+    ctx = talker.ctx
+    B, hidden, vocab = len(talker_kvs), talker.cfg.hidden, talker.cfg.vocab
+    lh = _f32(last_hidden, B * hidden)
+    lg = _f32(logits, B * vocab)
+    tt = None if trailing_text is None else _f32(trailing_text).reshape(B, -1, hidden)
+    tl = 0 if tt is None else tt.shape[1]
+    pad = None if tts_pad_embed is None else _f32(tts_pad_embed, hidden)
+    pos = np.ascontiguousarray(positions, dtype=np.int32)
+    sd = np.ascontiguousarray(seeds, dtype=np.uint64)
+    kvs = (C.c_void_p * B)(*[kv.h for kv in talker_kvs])
+    mc = max(params.max_codes, 1)
+    codes = np.zeros((B, 16, mc), dtype=np.uint32)
+    n = np.zeros(B, dtype=np.int32)
+    ctx.check(ctx.lib.qtts_generate_codes_batch(talker.h, predictor.h if predictor is not None else None, B, kvs,
+                                                _ptr(lh), _ptr(lg), _ptr(pos), _ptr(tt), tl, _ptr(pad),
+                                                C.byref(params), _ptr(sd), _ptr(codes), _ptr(n)))
+    return [codes[b, :, : n[b]].copy() for b in range(B)]

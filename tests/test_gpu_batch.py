@@ -1,0 +1,97 @@
+"""GPU parity of the batched loop (qtts_generate_codes_batch): several
+independent streams in lockstep -- each with its own prompt, cache, position,
+trailing text and seed -- give, stream by stream, the codes the oracle's
+single-stream loop gives (greedy and sampled, with and without the code
+predictor), and the caches are left where single-stream loops leave them."""
+import numpy as np
+import pytest
+
+import qtts
+from oracle import oracle
+from shapes import FULL_PREDICTOR, FULL_TALKER, TINY_PREDICTOR, TINY_TALKER
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def tiny(ctx):
+    tw = qtts.TalkerWeights(61, TINY_TALKER)
+    pw = qtts.CodePredictorWeights(61, TINY_PREDICTOR, talker_hidden=TINY_TALKER.hidden)
+    return (tw, pw, qtts.Talker(ctx, tw), qtts.CodePredictor(ctx, pw), oracle.Talker(tw, nthreads=1),
+            oracle.CodePredictor(pw, nthreads=1))
+
+
+def _streams(tw, t, ot, B, seed, prompt_lens, cap, trailing=3):
+    """Prefilled caches (GPU and oracle) and the loop inputs of B streams."""
+    H = tw.cfg.hidden
+    kvs, okvs, lhs, lgs, pos = [], [], [], [], []
+    for b in range(B):
+        n = prompt_lens[b]
+        x = qtts.synth_normal_f32(seed, f"batch.prompt.{b}", n * H)
+        kv, okv = t.new_kv(cap), ot.new_kv(cap)
+        t.prefill_talker_raw(x, n, kv)
+        lh = ot.prefill_talker_raw(x, n, okv)
+        kvs.append(kv)
+        okvs.append(okv)
+        lhs.append(lh)
+        lgs.append(ot.apply_codec_head(lh))
+        pos.append(n)
+    text = qtts.synth_normal_f32(seed, "batch.text", B * trailing * H, 0.0, 0.1).reshape(B, trailing, H)
+    pad = qtts.synth_normal_f32(seed, "batch.pad", H, 0.0, 0.1)
+    return kvs, okvs, np.stack(lhs), np.stack(lgs), pos, text, pad
+
+
+@pytest.mark.parametrize("greedy", [True, False])
+def test_batch_matches_oracle_streams(tiny, greedy):
+    tw, pw, t, p, ot, op = tiny
+    B, frames = 5, 24
+    lens = [10, 6, 13, 10, 9]
+    kvs, okvs, lh, lg, pos, text, pad = _streams(tw, t, ot, B, 62, lens, 64)
+    seeds = [1000 + 17 * b for b in range(B)]
+    params = qtts.loop_params(frames, greedy=greedy, stop_on_eos=False)
+    got = qtts.generate_codes_batch(t, p, kvs, lh, lg, pos, text, pad, params, seeds)
+    for b in range(B):
+        ref = oracle.generate_codes(ot, op, okvs[b], op.new_kv(), lh[b], lg[b], pos[b], text[b], pad, params,
+                                    seed=seeds[b])
+        assert got[b].shape == ref.shape == (16, frames)
+        assert np.array_equal(got[b], ref), (b, np.argwhere(got[b] != ref)[:5])
+        assert len(kvs[b]) == lens[b] + frames
+
+
+def test_batch_talker_only_and_eos(tiny):
+    """Talker-only loops; with EOS on, each stream stops on its own frame."""
+    tw, _, t, _, ot, _ = tiny
+    B, frames = 3, 20
+    kvs, okvs, lh, lg, pos, _, _ = _streams(tw, t, ot, B, 63, [8, 8, 8], 32)
+    params = qtts.loop_params(frames, greedy=True, stop_on_eos=False, talker_only=True)
+    got = qtts.generate_codes_batch(t, None, kvs, lh, lg, pos, None, None, params, [5, 6, 7])
+    refs = []
+    for b in range(B):
+        ref = oracle.generate_codes(ot, None, okvs[b], None, lh[b], lg[b], pos[b], None, None, params, seed=5 + b)
+        assert np.array_equal(got[b], ref)
+        refs.append(ref)
+    # make stream 1's 4th code EOS: stream 1 stops before that frame, the others run on
+    eos = int(refs[1][0, 3])
+    params = qtts.loop_params(frames, greedy=True, stop_on_eos=True, talker_only=True, codec_eos_id=eos)
+    kvs, okvs, lh, lg, pos, _, _ = _streams(tw, t, ot, B, 63, [8, 8, 8], 32)
+    got = qtts.generate_codes_batch(t, None, kvs, lh, lg, pos, None, None, params, [5, 6, 7])
+    for b in range(B):
+        ref = oracle.generate_codes(ot, None, okvs[b], None, lh[b], lg[b], pos[b], None, None, params, seed=5 + b)
+        assert got[b].shape == ref.shape and np.array_equal(got[b], ref), b
+    assert got[1].shape[1] == int(np.argmax(refs[1][0] == eos))
+
+
+def test_batch_full_model(ctx):
+    """The 1.7B talker and predictor, 4 streams x 3 sampled frames."""
+    tw = qtts.TalkerWeights(1, FULL_TALKER)
+    pw = qtts.CodePredictorWeights(1, FULL_PREDICTOR, talker_hidden=FULL_TALKER.hidden)
+    t, p = qtts.Talker(ctx, tw), qtts.CodePredictor(ctx, pw)
+    ot, op = oracle.Talker(tw), oracle.CodePredictor(pw)
+    B, frames = 4, 3
+    kvs, okvs, lh, lg, pos, text, pad = _streams(tw, t, ot, B, 64, [12, 12, 12, 12], 32, trailing=2)
+    params = qtts.loop_params(frames, temperature=0.8, top_k=50, repetition_penalty=1.05, stop_on_eos=False)
+    got = qtts.generate_codes_batch(t, p, kvs, lh, lg, pos, text, pad, params, [31, 32, 33, 34])
+    for b in range(B):
+        ref = oracle.generate_codes(ot, op, okvs[b], op.new_kv(), lh[b], lg[b], pos[b], text[b], pad, params,
+                                    seed=31 + b)
+        assert np.array_equal(got[b], ref), (b, np.argwhere(got[b] != ref)[:5])
