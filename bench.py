@@ -261,6 +261,46 @@ def decoder_measure(ctx, frames, cpu_frames=2, reps=3):
     return out
 
 
+def batch_measure(ctx, talker, pred, streams=16, kv_len=1064, frames=32):
+    """The batched long-form case: `streams` independent loops in lockstep
+    (qtts_generate_codes_batch), each prefilled to kv_len positions -- the
+    mean cache length of 64-token prompts followed by 2000 codes -- then
+    `frames` sampled frames; aggregate codes/s over the HIP-event-timed
+    frames, and bytes per frame (every Q4 weight once for all streams plus
+    each stream's K/V reads and appends)."""
+    H = talker.cfg.hidden
+    kvs, lhs, lgs = [], [], []
+    for b in range(streams):
+        x = qtts.synth_normal_f32(5, f"bench.batch.{b}", kv_len * H)
+        kv = talker.new_kv(kv_len + frames + 8)
+        lh = talker.prefill_talker_raw(x, kv_len, kv)
+        kvs.append(kv)
+        lhs.append(lh)
+        lgs.append(talker.apply_codec_head(lh))
+    text = qtts.synth_normal_f32(5, "bench.batch.text", streams * 8 * H, 0.0, 0.1).reshape(streams, 8, H)
+    pad = qtts.synth_normal_f32(5, "bench.batch.pad", H, 0.0, 0.1)
+    params = qtts.loop_params(frames, temperature=0.8, top_k=50, repetition_penalty=1.05, stop_on_eos=False)
+    hip = Hip()
+    ev0, ev1 = hip.event(), hip.event()
+    ctx.synchronize()
+    hip.record(ev0, ctx.stream)
+    qtts.generate_codes_batch(talker, pred, kvs, np.stack(lhs), np.stack(lgs), [kv_len] * streams, text, pad, params,
+                              list(range(streams)))
+    hip.record(ev1, ctx.stream)
+    ctx.synchronize()
+    s = hip.elapsed_ms(ev0, ev1) / 1e3
+    weights = frame_bytes(qtts.TALKER_1P7B, qtts.PREDICTOR_1P7B, qtts.NUM_GROUPS, 0)
+    kv_bytes = streams * 2 * 4 * qtts.TALKER_1P7B.layers * qtts.TALKER_1P7B.kv_heads * qtts.TALKER_1P7B.head_dim * (
+        kv_len + frames / 2.0)
+    per_frame = weights + kv_bytes
+    achieved = per_frame * frames / s / 1e9
+    return {"streams": streams, "kv_len": [kv_len, kv_len + frames], "frames": frames,
+            "codes_per_s": round(streams * frames / s, 1), "ms_per_frame": round(s * 1e3 / frames, 3),
+            "timing": "HIP events around qtts_generate_codes_batch (host copies of the prompt state included)",
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(achieved / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_frame": per_frame}}
+
+
 def copy_calibration(ctx, nbytes=512 << 20):
     """One device-to-device copy of a known size: the plain copy kernel whose
     FETCH_SIZE / WRITE_SIZE counters calibrate the GEMV's."""
@@ -410,6 +450,8 @@ def main():
         log(f"prefill {out['prefill']}")
         out["decoder"] = decoder_measure(ctx, args.steps, cpu_frames=0 if args.no_cpu else 2)
         log(f"decoder {out['decoder']}")
+        out["batch"] = batch_measure(ctx, talker, pred)
+        log(f"batch {out['batch']}")
     if not args.no_cpu:
         lh_np, lg_np = lh, lg
         kv_cpu, lh_np, lg_np = prefill()

@@ -358,6 +358,26 @@ qtts_status grow(qtts_ctx *c, T **buf, size_t *cap, size_t need) {
     return QTTS_OK;
 }
 
+// Steps per wave (sw) and K chunks (kc) of the MFMA GEMM for K rows.
+void mfma_plan(int K, int *sw, int *kc) {
+    const int Ks = K / 16;
+    int s = 8;
+    while (s > 1 && 4 * (s / 2) >= Ks) s /= 2;
+    *sw = s;
+    *kc = (Ks + 4 * s - 1) / (4 * s);
+}
+
+// Grows the MFMA GEMM scratch for a K x N weight at up to M rows, so that a
+// later call allocates nothing (e.g. under stream capture).
+qtts_status mfma_reserve(qtts_ctx *c, int K, int N, int M) {
+    int sw, kc;
+    mfma_plan(K, &sw, &kc);
+    const int Mpad = M > 32 ? 64 : 32;
+    QTTS_TRY(grow(c, &c->mfma_x, &c->mfma_x_cap, (size_t)2 * 64 * K + 2 * 64));
+    if (kc > 1) QTTS_TRY(grow(c, &c->mfma_part, &c->mfma_part_cap, (size_t)kc * Mpad * N));
+    return QTTS_OK;
+}
+
 // y[m] (+)= f(x[m]) . W (+ bias) for M rows on the matrix cores
 // (csrc/mfma.hip), f the row prologue (MfmaRowsMode), 64 rows per pass: the
 // prologue and binary16 split, then one block per (panel, K chunk) of
@@ -371,9 +391,8 @@ qtts_status run_gemm_mfma(qtts_ctx *c, const DevQ4Mfma &w, const float *x, int M
     if (K % 16 || N % 32 || K > kMfmaRowsMaxK || ldx % 4 || ((uintptr_t)x & 15))
         return fail(c, QTTS_ESHAPE, "MFMA GEMM: unsupported shape or unaligned rows");
     if (panels > kCounters) return fail(c, QTTS_ESHAPE, "MFMA GEMM: more panels than counters");
-    int sw = 8;
-    while (sw > 1 && 4 * (sw / 2) >= Ks) sw /= 2;
-    const int kc = (Ks + 4 * sw - 1) / (4 * sw);
+    int sw, kc;
+    mfma_plan(K, &sw, &kc);
     for (int r0 = 0; r0 < M; r0 += 64) {
         const int Mc = M - r0 < 64 ? M - r0 : 64;
         const int mt = Mc > 32 ? 2 : 1, Mpad = 32 * mt;
@@ -2953,7 +2972,9 @@ qtts_status qtts_generate_codes_batch(qtts_talker *t, qtts_predictor *p, int32_t
     TR.stride = (int)SW;
     TR.cap = cap;
 
-    for (int f = 0; f < max_codes; f++) {
+    // one frame for every stream; captured once into a HIP graph and
+    // replayed (QTTS_NO_GRAPH=1: enqueued eagerly every frame)
+    auto enqueue_frame_batch = [&]() -> qtts_status {
         // 1. code 0 of every stream (sample_token, src/generate_new.rs:329-391)
         SampleParams sp{};
         sp.logits = lg;
@@ -3055,8 +3076,52 @@ qtts_status qtts_generate_codes_batch(qtts_talker *t, qtts_predictor *p, int32_t
                                talker_only ? nullptr : in2, 2 * H));
         launch_advance(c->stream, S, 1, B);
         QTTS_TRY(check_launch(c, "k_advance"));
+            return QTTS_OK;
+    };
+    // every GEMM's scratch, reserved before capture
+    QTTS_TRY(mfma_reserve(c, H, ts.nq * ts.hd + 2 * ts.nkv * ts.hd, B));
+    QTTS_TRY(mfma_reserve(c, ts.nq * ts.hd, H, B));
+    QTTS_TRY(mfma_reserve(c, H, 2 * ts.inter, B));
+    QTTS_TRY(mfma_reserve(c, ts.inter, H, B));
+    QTTS_TRY(mfma_reserve(c, H, V, B));
+    if (!talker_only) {
+        if (!p->identity_proj) QTTS_TRY(mfma_reserve(c, H, hp, 2 * B));
+        QTTS_TRY(mfma_reserve(c, hp, ps->nq * ps->hd + 2 * ps->nkv * ps->hd, 2 * B));
+        QTTS_TRY(mfma_reserve(c, ps->nq * ps->hd, hp, 2 * B));
+        QTTS_TRY(mfma_reserve(c, hp, 2 * ps->inter, 2 * B));
+        QTTS_TRY(mfma_reserve(c, ps->inter, hp, 2 * B));
+        QTTS_TRY(mfma_reserve(c, hp, p->vocab, B));
     }
-    QTTS_TRY(sync(c));
+    const bool use_graph = std::getenv("QTTS_NO_GRAPH") == nullptr;
+    hipGraph_t graph = nullptr;
+    hipGraphExec_t exec = nullptr;
+    if (use_graph) {
+        HIP_TRY(c, hipStreamBeginCapture(c->stream, hipStreamCaptureModeThreadLocal));
+        const qtts_status st = enqueue_frame_batch();
+        hipError_t e = hipStreamEndCapture(c->stream, &graph);
+        if (st != QTTS_OK || e != hipSuccess) {
+            if (graph) (void)hipGraphDestroy(graph);
+            return st != QTTS_OK ? st : fail(c, QTTS_EDEVICE, std::string("graph capture: ") + hipGetErrorString(e));
+        }
+        e = hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0);
+        if (e != hipSuccess) {
+            (void)hipGraphDestroy(graph);
+            return fail(c, QTTS_EDEVICE, std::string("graph instantiate: ") + hipGetErrorString(e));
+        }
+    }
+    qtts_status rc = QTTS_OK;
+    for (int f = 0; f < max_codes && rc == QTTS_OK; f++) {
+        if (use_graph) {
+            const hipError_t e = hipGraphLaunch(exec, c->stream);
+            if (e != hipSuccess) rc = fail(c, QTTS_EDEVICE, std::string("graph launch: ") + hipGetErrorString(e));
+        } else {
+            rc = enqueue_frame_batch();
+        }
+    }
+    if (rc == QTTS_OK) rc = sync(c);
+    if (exec) (void)hipGraphExecDestroy(exec);
+    if (graph) (void)hipGraphDestroy(graph);
+    QTTS_TRY(rc);
     std::vector<LoopState> fin((size_t)B);
     HIP_TRY(c, hipMemcpy(fin.data(), S, sizeof(LoopState) * B, hipMemcpyDeviceToHost));
     for (int b = 0; b < B; b++)

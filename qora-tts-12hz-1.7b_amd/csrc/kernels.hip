@@ -501,7 +501,13 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams P) {
         if (hf == 1)
             for (int g = 0; g < G; g++) pv[g][d] = acc[g];
         __syncthreads();
-        if (hf == 0) {
+        if (hf == 0 && P.nsplit == 1) {
+            // one split: the combine below would give (1 * o) / (1 * l)
+            for (int g = 0; g < G; g++) {
+                const int h = kvh * G + g;
+                P.out[(size_t)m * P.ldo + (size_t)h * HD + d] = (acc[g] + pv[g][d]) / lloc[g];
+            }
+        } else if (hf == 0) {
             for (int g = 0; g < G; g++) {
                 const int h = kvh * G + g;
                 float *dst = P.part + (((size_t)m * P.nq + h) * P.nsplit + sp) * (HD + 2);
@@ -513,6 +519,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams P) {
             }
         }
     }
+    if (P.nsplit == 1) return;
     wait_stores();
     __syncthreads();
     if (tid == 0) s_last = arrive_dev(&P.counters[m * P.nkv + kvh]) == (unsigned)(P.nsplit - 1);
