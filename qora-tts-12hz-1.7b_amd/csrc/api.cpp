@@ -690,6 +690,11 @@ struct qtts_predictor {
     DevQ4Mfma mfma_in{};
     std::vector<DevQ4Mfma> mfma_heads;
     int mfma_state = 0;  // 0 not tried, 1 made, -1 a weight cannot use the matrix cores
+    // in_proj(emb[g][code]) + bias for every code of emb[0 .. groups-2]:
+    // [groups-1][tab_rows][hidden], the engine's pass inputs by code
+    float *tab = nullptr;
+    int tab_rows = 0;
+    int tab_state = 0;  // 0 not tried, 1 made, -1 not used
 };
 
 // ===========================================================================
@@ -719,6 +724,27 @@ EngInput in_embed(const DevQ4 &emb, const TvRef &tok) {
     return i;
 }
 
+// A layer input read from a per-code table at the argmax of a logits row:
+// table[argmax(logits)], the argmax step's own code published as `code`.
+struct TabIn {
+    TvRef logits;
+    int n = 0;
+    const float *table = nullptr;
+    int rows = 0;
+    TvRef code;
+};
+
+EngInput in_argtab(const TabIn &t) {
+    EngInput i{};
+    i.kind = EIN_ARGTAB;
+    i.tv = t.logits.p;
+    i.tag = t.logits.tag;
+    i.n = t.n;
+    i.table = t.table;
+    i.table_rows = t.rows;
+    return i;
+}
+
 struct GemvSpec {
     int M = 1;
     int epi = EEPI_STORE;
@@ -727,6 +753,7 @@ struct GemvSpec {
     EngInput in[kEngMaxM]{};
     const float *bias = nullptr;
     TvRef resid{};
+    const TabIn *resid_tab = nullptr;  // EEPI_RESID: the residual is the table row instead
     int kc = 0;  // 0: choose
     float *out_plain = nullptr;
     float *norm_plain = nullptr;
@@ -751,6 +778,10 @@ TvRef add_gemv(EngProgram &P, const DevQ4 &w, const GemvSpec &sp) {
     kchunk = (kchunk + kEngThreads - 1) / kEngThreads * kEngThreads;
     kc = (w.K + kchunk - 1) / kchunk;
     if (sp.norm && kc != 1) P.err = "engine GEMV shape not supported";
+    for (int m = 0; m < sp.M; m++)
+        if (sp.in[m].kind == EIN_ARGTAB && (sp.M != 1 || NP != 1 || !sp.norm || sp.in[m].n > kEngArgtabMax))
+            P.err = "engine table input not supported";
+    if (sp.resid_tab && sp.M != 1) P.err = "engine table residual not supported";
     g.w = w;
     g.M = sp.M;
     g.kc = kc;
@@ -764,6 +795,13 @@ TvRef add_gemv(EngProgram &P, const DevQ4 &w, const GemvSpec &sp) {
     g.resid = sp.resid.p;
     g.resid_tag = sp.resid.tag;
     g.ld_resid = sp.resid.ld;
+    if (sp.resid_tab) {
+        g.resid_table = sp.resid_tab->table;
+        g.resid_code = sp.resid_tab->code.p;
+        g.resid_tag = sp.resid_tab->code.tag;
+        g.resid_table_rows = sp.resid_tab->rows;
+        g.ld_resid = Nout;
+    }
     g.out = P.tv((size_t)sp.M * Nout);
     g.out_tag = P.tag();
     g.ld_out = Nout;
@@ -842,15 +880,16 @@ TvRef add_attention(EngProgram &P, const Stack &st, int l, qtts_kv *kv, int M, c
     return out;
 }
 
-// One transformer layer over M rows; returns the new residual stream.
+// One transformer layer over M rows; returns the new residual stream.  The
+// input is x, or (tin, M == 1) the table row at the argmax of a logits row.
 TvRef add_layer(EngProgram &P, const Stack &st, int l, qtts_kv *kv, int M, const TvRef &x, bool from_state,
-                int pos_const, int len_const, int nsplit) {
+                int pos_const, int len_const, int nsplit, const TabIn *tin = nullptr) {
     const DevLayer &L = st.L[l];
     GemvSpec q;
     q.M = M;
     q.norm = true;
     q.gamma = L.in_g;
-    for (int m = 0; m < M; m++) q.in[m] = in_tv(x, m);
+    for (int m = 0; m < M; m++) q.in[m] = tin ? in_argtab(*tin) : in_tv(x, m);
     const TvRef qkv = add_gemv(P, L.qkv, q);
     const TvRef att = add_attention(P, st, l, kv, M, qkv, from_state, pos_const, len_const, nsplit);
     GemvSpec o;
@@ -858,6 +897,7 @@ TvRef add_layer(EngProgram &P, const Stack &st, int l, qtts_kv *kv, int M, const
     for (int m = 0; m < M; m++) o.in[m] = in_tv(att, m);
     o.epi = EEPI_RESID;
     o.resid = x;
+    o.resid_tab = tin;
     const TvRef xm = add_gemv(P, L.o, o);
     GemvSpec gu;
     gu.M = M;
@@ -1050,13 +1090,62 @@ int eng_talker_nsplit(int cap) {
 }
 bool eng_talker_fits(int cap) { return (cap + kEngMaxSplit - 1) / kEngMaxSplit <= 256; }
 
+// Passes 2.. of generate_acoustic_codes (src/code_predictor.rs:218-273)
+// project the previous code's embedding, emb[g-1][code], to the predictor's
+// width.  That projection depends only on the code, so it is applied ahead of
+// time to every code of emb[0 .. groups-2] by the same GEMV the step would
+// run (in_proj(row) + bias), and a pass reads its input row by code.
+// QTTS_PREDICTOR_TABLE=0 keeps the projection as a step.
+qtts_status make_predictor_tables(qtts_predictor *p) {
+    if (p->tab_state != 0) return QTTS_OK;
+    p->tab_state = -1;
+    const char *e = std::getenv("QTTS_PREDICTOR_TABLE");
+    if ((e && std::strcmp(e, "0") == 0) || p->identity_proj || p->groups < 2) return QTTS_OK;
+    qtts_ctx *c = p->ctx;
+    const int rows = p->emb[0].K, th = p->talker_hidden, H = p->st.hidden, nt = p->groups - 1;
+    for (int g = 0; g < nt; g++)
+        if (p->emb[g].K != rows || p->emb[g].N != th) return QTTS_OK;
+    float *tab = nullptr;
+    QTTS_TRY(p->own.alloc(c, &tab, (size_t)nt * rows * H));
+    Owner tmp;  // freed on return (hipFree waits for the stream's work)
+    float *x = nullptr;
+    uint32_t *ids = nullptr;
+    QTTS_TRY(tmp.alloc(c, &x, (size_t)rows * th));
+    QTTS_TRY(tmp.alloc(c, &ids, (size_t)rows));
+    std::vector<uint32_t> h((size_t)rows);
+    for (int i = 0; i < rows; i++) h[(size_t)i] = (uint32_t)i;
+    HIP_TRY(c, hipMemcpyAsync(ids, h.data(), sizeof(uint32_t) * rows, hipMemcpyHostToDevice, c->stream));
+    for (int g = 0; g < nt; g++) {
+        launch_embed_rows(c->stream, p->emb[g], ids, 1, rows, x, th);
+        QTTS_TRY(check_launch(c, "k_embed_rows"));
+        for (int r0 = 0; r0 < rows; r0 += kMaxM) {
+            GemvParams q = gemv_base(c, p->in_proj, rows - r0 < kMaxM ? rows - r0 : kMaxM);
+            q.prologue = PRO_PLAIN;
+            q.x = x + (size_t)r0 * th;
+            q.ldx = th;
+            q.epilogue = EPI_STORE;
+            q.y = tab + ((size_t)g * rows + r0) * H;
+            q.ldy = H;
+            q.bias = p->bias;
+            QTTS_TRY(run_gemv(c, q));
+        }
+    }
+    QTTS_TRY(sync(c));
+    p->tab = tab;
+    p->tab_rows = rows;
+    p->tab_state = 1;
+    return QTTS_OK;
+}
+
 qtts_status build_predictor_passes(EngProgram &P, qtts_predictor *p, qtts_kv *kv, const EngInput &row0,
                                    const EngInput &row1, TvRef *codes) {
     const Stack &st = p->st;
+    QTTS_TRY(make_predictor_tables(p));
     // Every pass repeats the first pass's rotations, so a layer's attention
     // runs on the same blocks in all passes (its K/V rows stay in their LDS).
     std::vector<int> rots;
     P.rot_record = &rots;
+    const size_t first = P.ops.size();
     GemvSpec ip;
     ip.M = 2;
     ip.in[0] = row0;
@@ -1069,16 +1158,37 @@ qtts_status build_predictor_passes(EngProgram &P, qtts_predictor *p, qtts_kv *kv
     hd.gamma = st.final_g;
     hd.in[0] = in_tv(x, 1);
     TvRef lg = add_gemv(P, p->heads[0], hd);
+    const bool tab = p->tab_state == 1;
+    if (tab && P.ops.size() > first + 1 && P.ops[first + 1].ntasks < P.grid) {
+        // The argmax step's block runs no task of the next pass's first
+        // step, which computes the same argmax itself.
+        P.rot_next = (P.ops[first + 1].rot + P.ops[first + 1].ntasks) % P.grid;
+    }
     codes[0] = add_argmax(P, lg, p->vocab, 1);
     P.rot_record = nullptr;
     for (int g = 1; g < p->groups; g++) {
         P.rot_plan = &rots;
         P.plan_pos = 0;
-        GemvSpec e;
-        e.in[0] = in_embed(p->emb[g - 1], codes[g - 1]);
-        e.bias = p->bias;
-        x = add_gemv(P, p->in_proj, e);
-        for (int l = 0; l < st.layers; l++) x = add_layer(P, st, l, kv, 1, x, false, g + 1, g + 1, 1);
+        if (tab) {
+            // The input projection of the previous code is a table row: the
+            // first layer reads it at the argmax of the previous logits
+            // (the argmax step still files and publishes the code).
+            P.plan_pos = 1;
+            TabIn ti;
+            ti.logits = lg;
+            ti.n = p->vocab;
+            ti.table = p->tab + (size_t)(g - 1) * p->tab_rows * st.hidden;
+            ti.rows = p->tab_rows;
+            ti.code = codes[g - 1];
+            x = add_layer(P, st, 0, kv, 1, TvRef{}, false, g + 1, g + 1, 1, &ti);
+        } else {
+            GemvSpec e;
+            e.in[0] = in_embed(p->emb[g - 1], codes[g - 1]);
+            e.bias = p->bias;
+            x = add_gemv(P, p->in_proj, e);
+            x = add_layer(P, st, 0, kv, 1, x, false, g + 1, g + 1, 1);
+        }
+        for (int l = 1; l < st.layers; l++) x = add_layer(P, st, l, kv, 1, x, false, g + 1, g + 1, 1);
         hd.in[0] = in_tv(x, 0);
         lg = add_gemv(P, p->heads[g], hd);
         codes[g] = add_argmax(P, lg, p->vocab, g + 1);

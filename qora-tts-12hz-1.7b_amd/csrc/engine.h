@@ -34,9 +34,10 @@ constexpr uint32_t kTagStride = 8192;  // tags reserved per launch
 constexpr int kEngMaxSplit = 32;
 constexpr int kEngSmemFloats = 10240;
 constexpr int kEngLdsKvPos = 32;  // positions of an LDS-resident K/V cache (one kv head)
+constexpr int kEngArgtabMax = 256 * 8;  // logits of an EIN_ARGTAB input
 
 enum EngOpKind : int { EOP_GEMV = 1, EOP_ATTN = 2, EOP_COMBINE = 3, EOP_ARGMAX = 4, EOP_SAMPLE = 5, EOP_EMBSUM = 6 };
-enum EngIn : int { EIN_TV = 0, EIN_PLAIN = 1, EIN_EMBED = 2 };
+enum EngIn : int { EIN_TV = 0, EIN_PLAIN = 1, EIN_EMBED = 2, EIN_ARGTAB = 3 };
 enum EngEpi : int { EEPI_STORE = 0, EEPI_RESID = 1, EEPI_SWIGLU = 2 };
 
 struct EngInput {
@@ -46,6 +47,9 @@ struct EngInput {
     const float *plain;   // EIN_PLAIN: the row, written by an earlier launch or the host
     DevQ4 emb;            // EIN_EMBED: x = emb row at the token
     const tv_t *tok_tv;   // EIN_EMBED: the token (integer in the value bits)
+    const float *table;   // EIN_ARGTAB: x = table row at argmax(tv[0..n)) (a row of K floats;
+    int table_rows;       //   a code past the last row gives zeros)
+    int n;                // EIN_ARGTAB: logits in tv (<= kEngArgtabMax)
 };
 
 struct EngGemv {
@@ -62,6 +66,9 @@ struct EngGemv {
     const float *bias;
     const tv_t *resid;  // EEPI_RESID: y = resid + gemv
     int resid_tag, ld_resid;
+    const float *resid_table;  // EEPI_RESID, M == 1: the residual is resid_table[code][col] instead,
+    const tv_t *resid_code;    //   code a tagged integer (tag resid_tag), row stride ld_resid
+    int resid_table_rows;
     tv_t *out;
     int out_tag, ld_out;
     float *out_plain;  // optional plain copy of the output (read by a later launch)

@@ -114,6 +114,58 @@ __device__ __forceinline__ void put_tv_u32(tv_t *p, uint32_t x, uint32_t tag) {
     st_dev_u64(p, ((uint64_t)tag << 32) | (uint64_t)x);
 }
 
+// sample_argmax (src/code_predictor.rs:328-334) of n <= 256 * NA tagged
+// logits over the block: the last index of the maximum (-1 when every value
+// is NaN).  Every thread gets the result; *anynan says whether any logit was
+// NaN.  scr: 8 words of LDS that no thread touches again before the next
+// block barrier.
+template <int NA>
+__device__ __forceinline__ int block_argmax(const tv_t *logits, int n, uint32_t tag, Ctl &c, float *scr, int *anynan) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    float bv = -INFINITY;
+    int bi = -1, nan = 0;
+    float vals[NA];
+    const int cnt = n > tid ? (n - tid + kEngThreads - 1) / kEngThreads : 0;
+    wait_strided<NA>(logits + tid, kEngThreads, cnt, tag, vals, c);
+#pragma unroll
+    for (int k = 0; k < NA; k++) {
+        if (k >= cnt) continue;
+        const int i = tid + k * kEngThreads;
+        const float v = vals[k];
+        if (v != v)
+            nan = 1;
+        else if (bi < 0 || v >= bv) {
+            bv = v;
+            bi = i;
+        }
+    }
+    for (int off = 32; off >= 1; off >>= 1) {
+        const float ov = __shfl_xor(bv, off, 64);
+        const int oi = __shfl_xor(bi, off, 64);
+        if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi > bi))) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    int *si = reinterpret_cast<int *>(scr);
+    float *sv = scr + kEngThreads / 64;
+    *anynan = __syncthreads_or(nan);
+    if (lane == 0) {
+        sv[wave] = bv;
+        si[wave] = bi;
+    }
+    __syncthreads();
+    float b = -INFINITY;
+    int ix = -1;
+#pragma unroll
+    for (int w = 0; w < kEngThreads / 64; w++)
+        if (si[w] >= 0 && (ix < 0 || sv[w] > b || (sv[w] == b && si[w] > ix))) {
+            b = sv[w];
+            ix = si[w];
+        }
+    return ix;
+}
+
 // ---------------------------------------------------------------------------
 // GEMV task: a slice of C output columns (C = 32, 16, 8 or 4 of a 32-column
 // panel; for SwiGLU the same slice of the gate and the up panel) x one K
@@ -187,7 +239,7 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
     uint64_t e_res = 0;
     if (epi_lane && g.bias) e_bias = glb(g.bias)[col0 + (tid % C)];
     if (epi_lane && g.epi == EEPI_RESID)
-        e_res = ld_dev_u64(&g.resid[(size_t)(tid / C) * g.ld_resid + col0 + (tid % C)]);
+        e_res = ld_dev_u64(g.resid_table ? g.resid_code : &g.resid[(size_t)(tid / C) * g.ld_resid + col0 + (tid % C)]);
 
     stamp(c, 2);
     // 2. inputs of this thread's rows.
@@ -219,6 +271,34 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
             ssq[m] = ss;
 #pragma unroll
             for (int i = 0; i < R; i++) xv[i][m] = i < NR && i < nj ? row[i < NR ? i : 0] * f16_to_f32((uint16_t)gam[i]) : 0.0f;
+        } else if (in.kind == EIN_ARGTAB) {
+            if constexpr (M == 1 && NP == 1) {
+                // The row of a per-code table at the argmax of the logits:
+                // the previous step's code and the projection of its
+                // embedding in one step (the host builds the table and keeps
+                // such inputs normed, in one chunk, M == 1).
+                constexpr int NR = R < kEngNormRows ? R : kEngNormRows;
+#pragma unroll
+                for (int i = 0; i < R; i++) asm volatile("" : "+v"(gam[i]));
+                int anynan = 0;
+                const int ix = block_argmax<kEngArgtabMax / kEngThreads>(in.tv, in.n, tb + in.tag, c,
+                                                                        smem + kEngSmemFloats - 8, &anynan);
+                const uint32_t tok = (ix < 0 || anynan) ? 0u : (uint32_t)ix;  // the argmax step's code
+                const int nj = K > tid ? (K - tid + kEngThreads - 1) / kEngThreads : 0;  // <= NR
+                const auto *trow = glb(in.table) + (size_t)(tok < (uint32_t)in.table_rows ? tok : 0u) * K + tid;
+                const bool have = tok < (uint32_t)in.table_rows;
+                float row[NR];
+#pragma unroll
+                for (int j = 0; j < NR; j++) row[j] = j < nj && have ? trow[j * kEngThreads] : 0.0f;
+                float ss = 0.0f;
+#pragma unroll
+                for (int j = 0; j < NR; j++)
+                    if (j < nj) ss += row[j] * row[j];
+                ssq[m] = ss;
+#pragma unroll
+                for (int i = 0; i < R; i++)
+                    xv[i][m] = i < NR && i < nj ? row[i < NR ? i : 0] * f16_to_f32((uint16_t)gam[i]) : 0.0f;
+            }
         } else if (in.kind == EIN_TV) {
             const int cnt = k1 > k0 + tid ? (k1 - k0 - tid + kEngThreads - 1) / kEngThreads : 0;
             float row[R];
@@ -251,7 +331,12 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
         for (int m = 0; m < M; m++) asm volatile("" : "+v"(xv[i][m]));
     // A residual read before it was complete (a block that ran ahead) is
     // read again now; the load flies during the accumulation.
-    if (epi_lane && g.epi == EEPI_RESID && (uint32_t)(e_res >> 32) != tb + g.resid_tag)
+    float e_tab = 0.0f;  // the residual read from resid_table
+    if (epi_lane && g.epi == EEPI_RESID && g.resid_table) {
+        const uint32_t code = (uint32_t)(e_res >> 32) == tb + g.resid_tag ? (uint32_t)e_res
+                                                                           : wait_tv_u32(g.resid_code, tb + g.resid_tag, c);
+        if (code < (uint32_t)g.resid_table_rows) e_tab = glb(g.resid_table)[(size_t)code * g.ld_resid + col0 + (tid % C)];
+    } else if (epi_lane && g.epi == EEPI_RESID && (uint32_t)(e_res >> 32) != tb + g.resid_tag)
         e_res = ld_dev_u64(&g.resid[(size_t)(tid / C) * g.ld_resid + col0 + (tid % C)]);
     stamp(c, 4);
     // 3. accumulate the slice's columns per panel.
@@ -375,7 +460,8 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
             float v = y[0];
             if (g.bias) v += e_bias;
             if (g.epi == EEPI_RESID) {
-                const float r = (uint32_t)(e_res >> 32) == tb + g.resid_tag
+                const float r = g.resid_table ? e_tab
+                                : (uint32_t)(e_res >> 32) == tb + g.resid_tag
                                     ? __uint_as_float((uint32_t)e_res)
                                     : wait_tv(&g.resid[(size_t)m * g.ld_resid + col], tb + g.resid_tag, c);
                 v = r + v;
@@ -916,52 +1002,12 @@ __device__ __forceinline__ int eng_combine(const KCONST EngCombine &cb, int task
     return task;
 }
 
-// sample_argmax (src/code_predictor.rs:328-334): last index of the maximum.
+// The argmax step: files the code and publishes it as a tagged integer.
 __device__ __forceinline__ void eng_argmax(const KCONST EngArgmax &a, uint32_t tb, const EngState &st, Ctl &c, uint32_t *codes,
                            int max_codes, float *smem) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    float bv = -INFINITY;
-    int bi = -1, nan = 0;
-    constexpr int NA = 16;  // n <= 4096
-    float vals[NA];
-    const int cnt = a.n > tid ? (a.n - tid + kEngThreads - 1) / kEngThreads : 0;
-    wait_strided<NA>(a.logits + tid, kEngThreads, cnt, tb + a.logits_tag, vals, c);
-#pragma unroll
-    for (int k = 0; k < NA; k++) {
-        if (k >= cnt) continue;
-        const int i = tid + k * kEngThreads;
-        const float v = vals[k];
-        if (v != v)
-            nan = 1;
-        else if (bi < 0 || v >= bv) {
-            bv = v;
-            bi = i;
-        }
-    }
-    for (int off = 32; off >= 1; off >>= 1) {
-        const float ov = __shfl_xor(bv, off, 64);
-        const int oi = __shfl_xor(bi, off, 64);
-        if (oi >= 0 && (bi < 0 || ov > bv || (ov == bv && oi > bi))) {
-            bv = ov;
-            bi = oi;
-        }
-    }
-    int *si = reinterpret_cast<int *>(smem);
-    float *sv = smem + 8;
-    const int anynan = __syncthreads_or(nan);
-    if (lane == 0) {
-        sv[wave] = bv;
-        si[wave] = bi;
-    }
-    __syncthreads();
-    if (tid == 0) {
-        float b = -INFINITY;
-        int ix = -1;
-        for (int w = 0; w < kEngThreads / 64; w++)
-            if (si[w] >= 0 && (ix < 0 || sv[w] > b || (sv[w] == b && si[w] > ix))) {
-                b = sv[w];
-                ix = si[w];
-            }
+    int anynan = 0;
+    const int ix = block_argmax<16>(a.logits, a.n, tb + a.logits_tag, c, smem, &anynan);  // n <= 4096
+    if (threadIdx.x == 0) {
         uint32_t code = ix < 0 ? 0u : (uint32_t)ix;
         if (anynan) {
             code = 0u;
