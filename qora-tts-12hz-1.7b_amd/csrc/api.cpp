@@ -563,6 +563,7 @@ struct TvRef {
     tv_t *p = nullptr;
     int tag = 0;
     int ld = 0;       // row stride
+    int parts = 1;    // 2: each row is two parts of ld / 2 values to be added (a split_out GEMV)
 };
 
 // A program and its tagged-value arena.  Built twice: a sizing pass with null
@@ -707,6 +708,7 @@ EngInput in_tv(const TvRef &r, int row) {
     i.kind = EIN_TV;
     i.tv = r.p ? r.p + (size_t)row * r.ld : nullptr;
     i.tag = r.tag;
+    i.parts = r.parts;
     return i;
 }
 EngInput in_plain(const float *p) {
@@ -754,6 +756,7 @@ struct GemvSpec {
     const float *bias = nullptr;
     TvRef resid{};
     const TabIn *resid_tab = nullptr;  // EEPI_RESID: the residual is the table row instead
+    bool split_out = false;  // two K chunks publish as two output parts (when the shapes allow)
     int kc = 0;  // 0: choose
     float *out_plain = nullptr;
     float *norm_plain = nullptr;
@@ -782,6 +785,17 @@ TvRef add_gemv(EngProgram &P, const DevQ4 &w, const GemvSpec &sp) {
         if (sp.in[m].kind == EIN_ARGTAB && (sp.M != 1 || NP != 1 || !sp.norm || sp.in[m].n > kEngArgtabMax))
             P.err = "engine table input not supported";
     if (sp.resid_tab && sp.M != 1) P.err = "engine table residual not supported";
+    constexpr int kPartsMaxK = kEngThreads * kEngNormRows / 2;  // a normed input read in two parts
+    for (int m = 0; m < sp.M; m++)
+        if (sp.in[m].kind == EIN_TV && sp.in[m].parts == 2 && (!sp.norm || w.K > kPartsMaxK))
+            P.err = "engine two-part input not supported";
+    // Two K chunks publish their sums as two parts of the output (chunk 0
+    // with the residual), so no block waits for the other's partial; the
+    // consumers (normed GEMV inputs, residuals) add the parts.  (Three parts,
+    // for the talker's down projection, measured slower: the wider poll costs
+    // the whole kernel registers.)
+    const bool split = sp.split_out && kc == 2 && NP == 1 && !sp.out_plain && !sp.norm_plain &&
+                       Nout <= kPartsMaxK && sp.epi == EEPI_RESID && !sp.resid_tab;
     g.w = w;
     g.M = sp.M;
     g.kc = kc;
@@ -795,6 +809,7 @@ TvRef add_gemv(EngProgram &P, const DevQ4 &w, const GemvSpec &sp) {
     g.resid = sp.resid.p;
     g.resid_tag = sp.resid.tag;
     g.ld_resid = sp.resid.ld;
+    g.resid_parts = sp.resid.parts;
     if (sp.resid_tab) {
         g.resid_table = sp.resid_tab->table;
         g.resid_code = sp.resid_tab->code.p;
@@ -802,19 +817,20 @@ TvRef add_gemv(EngProgram &P, const DevQ4 &w, const GemvSpec &sp) {
         g.resid_table_rows = sp.resid_tab->rows;
         g.ld_resid = Nout;
     }
-    g.out = P.tv((size_t)sp.M * Nout);
+    g.split_out = split ? 1 : 0;
+    g.out = P.tv((size_t)sp.M * (split ? 2 : 1) * Nout);
     g.out_tag = P.tag();
-    g.ld_out = Nout;
+    g.ld_out = split ? 2 * Nout : Nout;
     g.out_plain = sp.out_plain;
     g.ld_plain = Nout;
     g.norm_plain = sp.norm_plain;
-    if (kc > 1) {
+    if (kc > 1 && !split) {
         g.part = P.tv((size_t)(kc - 1) * sp.M * w.N);
         g.part_tag = P.tag();
     }
-    op.ntasks = (Nout / C) * kc;
+    op.ntasks = (Nout / C) * kc * sp.M;  // one-row tasks for every row
     P.push(op);
-    return TvRef{g.out, g.out_tag, Nout};
+    return TvRef{g.out, g.out_tag, g.ld_out, split ? 2 : 1};
 }
 
 TvRef add_attention(EngProgram &P, const Stack &st, int l, qtts_kv *kv, int M, const TvRef &qkv, bool from_state,
@@ -910,6 +926,7 @@ TvRef add_layer(EngProgram &P, const Stack &st, int l, qtts_kv *kv, int M, const
     dn.M = M;
     dn.epi = EEPI_RESID;
     dn.resid = xm;
+    dn.split_out = true;
     for (int m = 0; m < M; m++) dn.in[m] = in_tv(h, m);
     return add_gemv(P, L.down, dn);
 }
@@ -1159,10 +1176,13 @@ qtts_status build_predictor_passes(EngProgram &P, qtts_predictor *p, qtts_kv *kv
     hd.in[0] = in_tv(x, 1);
     TvRef lg = add_gemv(P, p->heads[0], hd);
     const bool tab = p->tab_state == 1;
-    if (tab && P.ops.size() > first + 1 && P.ops[first + 1].ntasks < P.grid) {
+    if (tab && P.ops.size() > first + 1) {
         // The argmax step's block runs no task of the next pass's first
-        // step, which computes the same argmax itself.
-        P.rot_next = (P.ops[first + 1].rot + P.ops[first + 1].ntasks) % P.grid;
+        // step (the one-row version of this pass's), which computes the same
+        // argmax itself.
+        const EngOp &q = P.ops[first + 1];
+        const int n = q.ntasks / (q.kind == EOP_GEMV && q.gemv.M > 1 ? q.gemv.M : 1);
+        if (n < P.grid) P.rot_next = (q.rot + n) % P.grid;
     }
     codes[0] = add_argmax(P, lg, p->vocab, 1);
     P.rot_record = nullptr;

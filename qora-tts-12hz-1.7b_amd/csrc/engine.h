@@ -50,11 +50,13 @@ struct EngInput {
     const float *table;   // EIN_ARGTAB: x = table row at argmax(tv[0..n)) (a row of K floats;
     int table_rows;       //   a code past the last row gives zeros)
     int n;                // EIN_ARGTAB: logits in tv (<= kEngArgtabMax)
+    int parts;            // EIN_TV with norm: 2 = the row is tv[k] + tv[K + k] (a split_out GEMV's
+                          //   two chunks; K <= 128 * kEngNormRows)
 };
 
 struct EngGemv {
     DevQ4 w;
-    int M;       // rows (1 or 2)
+    int M;       // rows (1 or 2): each row's tasks run separately (M x the one-row tasks)
     int kc;      // K chunks; chunk 0 owns the epilogue
     int kchunk;  // rows per chunk (multiple of 256, <= 256 * eng_rows_per_thread(cols, panels))
     int cols;    // output columns per task: 32, 16, 8 or 4 (a slice of a 32-column panel);
@@ -69,6 +71,10 @@ struct EngGemv {
     const float *resid_table;  // EEPI_RESID, M == 1: the residual is resid_table[code][col] instead,
     const tv_t *resid_code;    //   code a tagged integer (tag resid_tag), row stride ld_resid
     int resid_table_rows;
+    int resid_parts;           // 2: the residual is resid[col] + resid[N + col]
+    int split_out;             // kc == 2, NP == 1: chunk 1 publishes its sums as the output's second
+                               //   part (out[m * ld_out + N + col]) and chunk 0 adds the residual and
+                               //   bias to its own: no split-K wait; the consumers add the parts
     tv_t *out;
     int out_tag, ld_out;
     float *out_plain;  // optional plain copy of the output (read by a later launch)

@@ -82,6 +82,33 @@ __device__ __forceinline__ void wait_strided(const tv_t *base, size_t stride, in
     for (int i = 0; i < N; i++) out[i] = __uint_as_float((uint32_t)v[i]);
 }
 
+// out[i] = a[i*stride] + b[i*stride] for i < count (<= N), one tag: all 2N
+// loads are issued before any tag is checked.
+template <int N>
+__device__ __forceinline__ void wait_pair(const tv_t *a, const tv_t *b, size_t stride, int count, uint32_t tag,
+                                          float (&out)[N], Ctl &c) {
+    uint64_t va[N], vb[N];
+#pragma unroll
+    for (int i = 0; i < N; i++) {
+        va[i] = i < count ? ld_dev_u64(a + i * stride) : ((uint64_t)tag << 32);
+        vb[i] = i < count ? ld_dev_u64(b + i * stride) : ((uint64_t)tag << 32);
+    }
+    for (;;) {
+        bool ok = true;
+#pragma unroll
+        for (int i = 0; i < N; i++) ok &= ((uint32_t)(va[i] >> 32) == tag) & ((uint32_t)(vb[i] >> 32) == tag);
+        if (ok || must_stop(c)) break;
+        __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+        for (int i = 0; i < N; i++) {
+            va[i] = i < count ? ld_dev_u64(a + i * stride) : va[i];
+            vb[i] = i < count ? ld_dev_u64(b + i * stride) : vb[i];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < N; i++) out[i] = __uint_as_float((uint32_t)va[i]) + __uint_as_float((uint32_t)vb[i]);
+}
+
 // Same for a list of words with their own tags.
 template <int N>
 __device__ __forceinline__ void wait_list(const tv_t *const (&p)[N], const uint32_t (&tag)[N], int count,
@@ -174,7 +201,7 @@ __device__ __forceinline__ int block_argmax(const tv_t *logits, int n, uint32_t 
 // Same arithmetic as k_gemv: acc += (scale * x) * nib - 8 * (scale * x), f32.
 // ---------------------------------------------------------------------------
 template <int M, int NP, int C, int R>
-__device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint32_t tb, Ctl &c, float *smem) {
+__device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint32_t tb, Ctl &c, float *smem, int row) {
     constexpr int DW = q4_slice_dwords<C>();
     float *red = smem;                  // [NP][M][4 waves][C]
     float *scr = red + NP * M * 4 * C;  // [M][4] block-sum partials
@@ -236,10 +263,11 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
     // input polls.
     const bool epi_lane = ch == 0 && NP == 1 && tid < M * C;
     float e_bias = 0.0f;
-    uint64_t e_res = 0;
+    uint64_t e_res = 0, e_res2 = 0;
+    const tv_t *res_at = g.resid + (size_t)(tid / C + row) * g.ld_resid + col0 + (tid % C);  // EEPI_RESID without a table
     if (epi_lane && g.bias) e_bias = glb(g.bias)[col0 + (tid % C)];
-    if (epi_lane && g.epi == EEPI_RESID)
-        e_res = ld_dev_u64(g.resid_table ? g.resid_code : &g.resid[(size_t)(tid / C) * g.ld_resid + col0 + (tid % C)]);
+    if (epi_lane && g.epi == EEPI_RESID) e_res = ld_dev_u64(g.resid_table ? g.resid_code : res_at);
+    if (epi_lane && g.epi == EEPI_RESID && g.resid_parts == 2) e_res2 = ld_dev_u64(res_at + N);
 
     stamp(c, 2);
     // 2. inputs of this thread's rows.
@@ -250,7 +278,7 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
     for (int m = 0; m < M; m++) ssq[m] = 0.0f;
 #pragma unroll
     for (int m = 0; m < M; m++) {
-        const KCONST EngInput &in = g.in[m];
+        const KCONST EngInput &in = g.in[m + row];
         if (in.kind == EIN_TV && g.norm) {
             // rms_norm_f16 (src/gemv.rs:406-417) over the full row, which is
             // this task's chunk (the host keeps normed GEMVs in one chunk of
@@ -260,7 +288,17 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
             for (int i = 0; i < R; i++) asm volatile("" : "+v"(gam[i]));
             const int nj = K > tid ? (K - tid + kEngThreads - 1) / kEngThreads : 0;  // <= NR
             float row[NR];
-            wait_strided<NR>(in.tv + tid, kEngThreads, nj, tb + in.tag, row, c);
+            if (in.parts == 2) {
+                // the two parts of a split_out output (nj <= NR / 2): a wider
+                // poll (three parts of 2048) costs the whole kernel registers
+                constexpr int H = NR / 2 > 0 ? NR / 2 : 1;
+                float two[H];
+                wait_pair<H>(in.tv + tid, in.tv + K + tid, kEngThreads, nj, tb + in.tag, two, c);
+#pragma unroll
+                for (int j = 0; j < NR; j++) row[j] = j < H ? two[j < H ? j : 0] : 0.0f;
+            } else {
+                wait_strided<NR>(in.tv + tid, kEngThreads, nj, tb + in.tag, row, c);
+            }
             float ss = 0.0f;
 #pragma unroll
             for (int j = 0; j < NR; j++)
@@ -336,8 +374,10 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
         const uint32_t code = (uint32_t)(e_res >> 32) == tb + g.resid_tag ? (uint32_t)e_res
                                                                            : wait_tv_u32(g.resid_code, tb + g.resid_tag, c);
         if (code < (uint32_t)g.resid_table_rows) e_tab = glb(g.resid_table)[(size_t)code * g.ld_resid + col0 + (tid % C)];
-    } else if (epi_lane && g.epi == EEPI_RESID && (uint32_t)(e_res >> 32) != tb + g.resid_tag)
-        e_res = ld_dev_u64(&g.resid[(size_t)(tid / C) * g.ld_resid + col0 + (tid % C)]);
+    } else if (epi_lane && g.epi == EEPI_RESID) {
+        if ((uint32_t)(e_res >> 32) != tb + g.resid_tag) e_res = ld_dev_u64(res_at);
+        if (g.resid_parts == 2 && (uint32_t)(e_res2 >> 32) != tb + g.resid_tag) e_res2 = ld_dev_u64(res_at + N);
+    }
     stamp(c, 4);
     // 3. accumulate the slice's columns per panel.
     float acc[NP][M][C];
@@ -413,7 +453,7 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
     for (int m = 0; m < M; m++)
         inv[m] = g.norm ? 1.0f / sqrtf(((scr[4 * m] + scr[4 * m + 1]) + (scr[4 * m + 2] + scr[4 * m + 3])) / (float)K + 1e-6f)
                         : 1.0f;
-    if (g.norm_plain && tt == 0 && ch == 0) {
+    if (g.norm_plain && tt == 0 && ch == 0 && row + M == g.M) {
         // the normed last row, for a later launch
 #pragma unroll
         for (int i = 0; i < R; i++) {
@@ -431,17 +471,22 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
             y[pp] = (rw[0] + rw[C]) + (rw[2 * C] + rw[3 * C]);
         }
         // 5. split-K: non-owners publish partials; the owner adds them in order.
+        if (ch > 0 && NP == 1 && g.split_out) {
+            put_tv(&g.out[(size_t)(m + row) * g.ld_out + N + col], y[0], tb + g.out_tag);
+            return -1;
+        }
         if (ch > 0) {
 #pragma unroll
             for (int pp = 0; pp < NP; pp++)
-                put_tv(&g.part[((size_t)(ch - 1) * M + m) * N + pp * Nout + col], y[pp], tb + g.part_tag);
+                put_tv(&g.part[((size_t)(ch - 1) * g.M + m + row) * N + pp * Nout + col], y[pp], tb + g.part_tag);
             return -1;
         }
-        if (g.kc > 1) {
+        if (g.kc > 1 && !(NP == 1 && g.split_out)) {
 #pragma unroll
             for (int pp = 0; pp < NP; pp++) {
                 float pv4[4];
-                wait_strided<4>(&g.part[(size_t)m * N + pp * Nout + col], (size_t)M * N, g.kc - 1, tb + g.part_tag, pv4, c);
+                wait_strided<4>(&g.part[(size_t)(m + row) * N + pp * Nout + col], (size_t)g.M * N, g.kc - 1,
+                                tb + g.part_tag, pv4, c);
 #pragma unroll
                 for (int cc = 0; cc < 4; cc++)
                     if (cc < g.kc - 1) y[pp] += pv4[cc];
@@ -455,19 +500,25 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
         if (NP == 2) {
             // silu(g) * u, src/talker.rs:342-345
             const float gt = y[0], up = y[NP - 1];
-            put_tv(&g.out[(size_t)m * g.ld_out + col], (gt / (1.0f + expf(-gt))) * up, tb + g.out_tag);
+            put_tv(&g.out[(size_t)(m + row) * g.ld_out + col], (gt / (1.0f + expf(-gt))) * up, tb + g.out_tag);
         } else {
             float v = y[0];
             if (g.bias) v += e_bias;
             if (g.epi == EEPI_RESID) {
-                const float r = g.resid_table ? e_tab
-                                : (uint32_t)(e_res >> 32) == tb + g.resid_tag
-                                    ? __uint_as_float((uint32_t)e_res)
-                                    : wait_tv(&g.resid[(size_t)m * g.ld_resid + col], tb + g.resid_tag, c);
+                float r;
+                if (g.resid_table) {
+                    r = e_tab;
+                } else {
+                    r = (uint32_t)(e_res >> 32) == tb + g.resid_tag ? __uint_as_float((uint32_t)e_res)
+                                                                    : wait_tv(res_at, tb + g.resid_tag, c);
+                    if (g.resid_parts == 2)
+                        r += (uint32_t)(e_res2 >> 32) == tb + g.resid_tag ? __uint_as_float((uint32_t)e_res2)
+                                                                          : wait_tv(res_at + N, tb + g.resid_tag, c);
+                }
                 v = r + v;
             }
-            put_tv(&g.out[(size_t)m * g.ld_out + col], v, tb + g.out_tag);
-            if (g.out_plain) st_dev(&g.out_plain[(size_t)m * g.ld_plain + col], v);
+            put_tv(&g.out[(size_t)(m + row) * g.ld_out + col], v, tb + g.out_tag);
+            if (g.out_plain) st_dev(&g.out_plain[(size_t)(m + row) * g.ld_plain + col], v);
         }
     }
     if (ch > 0) return -1;
@@ -476,12 +527,12 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
 }
 
 template <int M, int NP>
-__device__ __forceinline__ int eng_gemv_cols(const KCONST EngGemv &g, int task, uint32_t tb, Ctl &c, float *smem) {
+__device__ __forceinline__ int eng_gemv_cols(const KCONST EngGemv &g, int task, uint32_t tb, Ctl &c, float *smem, int row) {
     // Whole 32-column panels: narrower slices spread an op over more blocks
     // but leave fewer blocks idle to run ahead into the next op (issuing its
     // weight loads early), which costs more than the shorter accumulation
     // saves on this loop.
-    return eng_gemv<M, NP, 32, eng_rows_per_thread(32, NP)>(g, task, tb, c, smem);
+    return eng_gemv<M, NP, 32, eng_rows_per_thread(32, NP)>(g, task, tb, c, smem, row);
 }
 
 // ---------------------------------------------------------------------------
@@ -1413,18 +1464,28 @@ __global__ __launch_bounds__(kEngThreads) void k_engine(EngArgs A) {
             int fi = -1;  // flag this task sets, if any
             switch (op.kind) {
                 case EOP_GEMV: {
+                    // An op of M rows runs as M x its one-row tasks (one
+                    // instantiation per panel count keeps the kernel's
+                    // registers down); every row's split-K non-owners come
+                    // before all owners, so no block waits on a later task.
                     const KCONST EngGemv &g = op.gemv;
-                    if (g.M == 1) {
-                        if (g.epi == EEPI_SWIGLU)
-                            fi = eng_gemv_cols<1, 2>(g, t, A.tag_base, c, smem);
-                        else
-                            fi = eng_gemv_cols<1, 1>(g, t, A.tag_base, c, smem);
-                    } else {
-                        if (g.epi == EEPI_SWIGLU)
-                            fi = eng_gemv_cols<2, 2>(g, t, A.tag_base, c, smem);
-                        else
-                            fi = eng_gemv_cols<2, 1>(g, t, A.tag_base, c, smem);
+                    int row = 0, tt = t;
+                    if (g.M > 1) {
+                        const int per = g.w.N / (g.epi == EEPI_SWIGLU ? 64 : 32);  // tasks per K chunk
+                        const int non = per * (g.kc - 1);
+                        if (t < non * g.M) {
+                            row = t / non;
+                            tt = t - row * non;
+                        } else {
+                            const int t2 = t - non * g.M;
+                            row = t2 / per;
+                            tt = non + (t2 - row * per);
+                        }
                     }
+                    if (g.epi == EEPI_SWIGLU)
+                        fi = eng_gemv_cols<1, 2>(g, tt, A.tag_base, c, smem, row);
+                    else
+                        fi = eng_gemv_cols<1, 1>(g, tt, A.tag_base, c, smem, row);
                     break;
                 }
                 case EOP_ATTN: fi = eng_attn(op.attn, t, A.tag_base, st, c, smem, kvl); break;
