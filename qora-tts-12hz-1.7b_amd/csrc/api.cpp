@@ -3014,6 +3014,7 @@ qtts_status qtts_generate_codes_batch(qtts_talker *t, qtts_predictor *p, int32_t
         return fail(c, QTTS_ESHAPE, "batched loop: a talker weight cannot use the matrix cores");
     if (!talker_only) {
         if (p->mfma_state == 0) QTTS_TRY(make_predictor_mfma(p));
+        QTTS_TRY(make_predictor_tables(p));
         if (p->mfma_state != 1) return fail(c, QTTS_ESHAPE, "batched loop: a predictor weight cannot use the matrix cores");
     }
     const Stack *ps = talker_only ? nullptr : &p->st;
@@ -3104,6 +3105,7 @@ qtts_status qtts_generate_codes_batch(qtts_talker *t, qtts_predictor *p, int32_t
 
     // one frame for every stream; captured once into a HIP graph and
     // replayed (QTTS_NO_GRAPH=1: enqueued eagerly every frame)
+    const float *ptab = !talker_only && p->tab_state == 1 ? p->tab : nullptr;  // the predictor's input table
     auto enqueue_frame_batch = [&]() -> qtts_status {
         // 1. code 0 of every stream (sample_token, src/generate_new.rs:329-391)
         SampleParams sp{};
@@ -3154,12 +3156,15 @@ qtts_status qtts_generate_codes_batch(qtts_talker *t, qtts_predictor *p, int32_t
                     PR.stride = 1;
                 } else {
                     M = B;
-                    float *dst = p->identity_proj ? xp : in2;
-                    launch_embed_rows(c->stream, p->emb[g - 1], &S[0].cur[g], SW, B, dst, p->identity_proj ? hp : H);
-                    QTTS_TRY(check_launch(c, "k_embed_rows"));
-                    if (!p->identity_proj)
-                        QTTS_TRY(run_gemm_mfma(c, p->mfma_in, in2, M, H, MFMA_ROWS_PLAIN, nullptr, xp, hp, p->bias,
-                                               false));
+                    if (!ptab) {  // with the table, the previous argmax filled xp
+                        float *dst = p->identity_proj ? xp : in2;
+                        launch_embed_rows(c->stream, p->emb[g - 1], &S[0].cur[g], SW, B, dst,
+                                          p->identity_proj ? hp : H);
+                        QTTS_TRY(check_launch(c, "k_embed_rows"));
+                        if (!p->identity_proj)
+                            QTTS_TRY(run_gemm_mfma(c, p->mfma_in, in2, M, H, MFMA_ROWS_PLAIN, nullptr, xp, hp,
+                                                   p->bias, false));
+                    }
                     PR.k = p_k1;
                     PR.v = p_v1;
                     PR.pos0 = g + 1;
@@ -3171,7 +3176,11 @@ qtts_status qtts_generate_codes_batch(qtts_talker *t, qtts_predictor *p, int32_t
                 const int hld = g == 0 ? 2 * hp : hp;
                 QTTS_TRY(run_gemm_mfma(c, p->mfma_heads[(size_t)g], hx, B, hld, MFMA_ROWS_RMSNORM, ps->final_g, plog,
                                        p->vocab, nullptr, false));
-                launch_argmax_rows(c->stream, plog, B, p->vocab, &S[0].cur[1 + g], SW, &S[0].status, SS);
+                // with the table, the argmax also writes the next pass's
+                // input rows: the projected embedding of each stream's code
+                const float *nt = ptab && g + 1 < G ? ptab + (size_t)g * p->tab_rows * hp : nullptr;
+                launch_argmax_rows(c->stream, plog, B, p->vocab, &S[0].cur[1 + g], SW, &S[0].status, SS, nt,
+                                   p->tab_rows, hp, xp, hp);
                 QTTS_TRY(check_launch(c, "k_argmax_rows"));
             }
         }

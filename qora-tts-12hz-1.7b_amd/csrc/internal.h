@@ -318,7 +318,8 @@ void launch_advance(hipStream_t st, LoopState *s, int frame_step, int batch = 1)
 void launch_embed_rows(hipStream_t st, const DevQ4 &w, const uint32_t *tok, long long tok_stride, int rows, float *out,
                        long long out_stride);
 void launch_argmax_rows(hipStream_t st, const float *logits, int rows, int n, uint32_t *out, long long out_stride,
-                        int *status, long long status_stride);
+                        int *status, long long status_stride, const float *table = nullptr, int table_rows = 0,
+                        int width = 0, float *rows_out = nullptr, long long rows_ld = 0);
 void launch_repack_q4(hipStream_t st, const uint8_t *packed, const uint16_t *scales, int K, int N, int col0,
                       int Ntot, uint4 *wq, uint16_t *ws);
 

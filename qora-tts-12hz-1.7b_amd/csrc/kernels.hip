@@ -428,7 +428,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams P) {
     constexpr int GMAX = 4;
     __shared__ float qs[GMAX][HD];
     __shared__ float sc[GMAX][kAttnMaxChunk];
-    __shared__ float pv[GMAX][HD];
+    __shared__ __align__(16) float pv[4 * GMAX][HD];  // P.V partials of the 4 waves
     __shared__ float mloc[GMAX], lloc[GMAX];
     __shared__ int s_last;
 
@@ -452,22 +452,34 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams P) {
     const float *Kb = (P.row_k ? P.row_k[m] + P.layer_off : P.kcache) + (size_t)kvh * P.kv_cap * HD;
     const float *Vb = (P.row_v ? P.row_v[m] + P.layer_off : P.vcache) + (size_t)kvh * P.kv_cap * HD;
 
-    // scores: 16 lanes per position, 8 dims per lane.
-    {
+    // scores: 16 lanes per position, 8 dims per lane; SU positions per
+    // thread are loaded before any is used (clamped to the split, masked
+    // after), so their loads are in flight together.
+    if (nt > 0) {
+        constexpr int SU = 4;
         const int l16 = tid & 15, slot = tid >> 4;
-        for (int tt = slot; tt < nt; tt += kAttnThreads / 16) {
-            const float *kr = Kb + (size_t)(t0 + tt) * HD + l16 * 8;
-            const float4 a = *reinterpret_cast<const float4 *>(kr);
-            const float4 b = *reinterpret_cast<const float4 *>(kr + 4);
-            for (int g = 0; g < G; g++) {
-                const float *qq = &qs[g][l16 * 8];
-                float dot = qq[0] * a.x + qq[1] * a.y + qq[2] * a.z + qq[3] * a.w + qq[4] * b.x + qq[5] * b.y +
-                            qq[6] * b.z + qq[7] * b.w;
-                dot += __shfl_xor(dot, 8, 16);
-                dot += __shfl_xor(dot, 4, 16);
-                dot += __shfl_xor(dot, 2, 16);
-                dot += __shfl_xor(dot, 1, 16);
-                if (l16 == 0) sc[g][tt] = dot * P.scale;
+        for (int b0 = 0; b0 < nt; b0 += 16 * SU) {
+            float4 ka[SU], kb[SU];
+#pragma unroll
+            for (int u = 0; u < SU; u++) {
+                const int tt = min(b0 + slot + 16 * u, nt - 1);
+                const float *kr = Kb + (size_t)(t0 + tt) * HD + l16 * 8;
+                ka[u] = *reinterpret_cast<const float4 *>(kr);
+                kb[u] = *reinterpret_cast<const float4 *>(kr + 4);
+            }
+#pragma unroll
+            for (int u = 0; u < SU; u++) {
+                const int tt = b0 + slot + 16 * u;
+                for (int g = 0; g < G; g++) {
+                    const float *qq = &qs[g][l16 * 8];
+                    float dot = qq[0] * ka[u].x + qq[1] * ka[u].y + qq[2] * ka[u].z + qq[3] * ka[u].w +
+                                qq[4] * kb[u].x + qq[5] * kb[u].y + qq[6] * kb[u].z + qq[7] * kb[u].w;
+                    dot += __shfl_xor(dot, 8, 16);
+                    dot += __shfl_xor(dot, 4, 16);
+                    dot += __shfl_xor(dot, 2, 16);
+                    dot += __shfl_xor(dot, 1, 16);
+                    if (l16 == 0 && tt < nt) sc[g][tt] = dot * P.scale;
+                }
             }
         }
     }
@@ -490,28 +502,59 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams P) {
         }
     }
     __syncthreads();
-    // P.V: thread (d, half) walks every other position.
+    // P.V: thread (d4, r8) holds dims 4*d4..4*d4+3 of every 8th position
+    // from r8, VU rows loaded together; the two halves of a wave are added
+    // by a lane exchange and the 4 waves through LDS.
     {
-        const int d = tid & (HD - 1), hf = tid >> 7;
-        float acc[GMAX] = {0.0f, 0.0f, 0.0f, 0.0f};
-        for (int tt = hf; tt < nt; tt += 2) {
-            const float v = Vb[(size_t)(t0 + tt) * HD + d];
-            for (int g = 0; g < G; g++) acc[g] += sc[g][tt] * v;
-        }
-        if (hf == 1)
-            for (int g = 0; g < G; g++) pv[g][d] = acc[g];
-        __syncthreads();
-        if (hf == 0 && P.nsplit == 1) {
-            // one split: the combine below would give (1 * o) / (1 * l)
-            for (int g = 0; g < G; g++) {
-                const int h = kvh * G + g;
-                P.out[(size_t)m * P.ldo + (size_t)h * HD + d] = (acc[g] + pv[g][d]) / lloc[g];
+        constexpr int VU = 4;
+        const int d4 = tid & 31, r8 = tid >> 5;
+        float4 acc[GMAX];
+#pragma unroll
+        for (int g = 0; g < GMAX; g++) acc[g] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        for (int b0 = 0; b0 < nt; b0 += 8 * VU) {
+            float4 v[VU];
+#pragma unroll
+            for (int u = 0; u < VU; u++) {
+                const int tt = min(b0 + r8 + 8 * u, nt - 1);
+                v[u] = *reinterpret_cast<const float4 *>(Vb + (size_t)(t0 + tt) * HD + 4 * d4);
             }
-        } else if (hf == 0) {
-            for (int g = 0; g < G; g++) {
-                const int h = kvh * G + g;
+#pragma unroll
+            for (int u = 0; u < VU; u++) {
+                const int tt = b0 + r8 + 8 * u;
+                if (tt >= nt) continue;
+#pragma unroll
+                for (int g = 0; g < GMAX; g++) {
+                    if (g >= G) continue;
+                    const float pr = sc[g][tt];
+                    acc[g].x += pr * v[u].x;
+                    acc[g].y += pr * v[u].y;
+                    acc[g].z += pr * v[u].z;
+                    acc[g].w += pr * v[u].w;
+                }
+            }
+        }
+        float *red = &pv[0][0];  // [4 waves][GMAX][HD]
+#pragma unroll
+        for (int g = 0; g < GMAX; g++) {
+            acc[g].x += __shfl_xor(acc[g].x, 32);
+            acc[g].y += __shfl_xor(acc[g].y, 32);
+            acc[g].z += __shfl_xor(acc[g].z, 32);
+            acc[g].w += __shfl_xor(acc[g].w, 32);
+            if (lane < 32 && g < G)
+                *reinterpret_cast<float4 *>(&red[(wave * GMAX + g) * HD + 4 * d4]) = acc[g];
+        }
+        __syncthreads();
+        for (int idx = tid; idx < G * HD; idx += kAttnThreads) {
+            const int g = idx / HD, d = idx - g * HD;
+            const float o = (red[g * HD + d] + red[(GMAX + g) * HD + d]) +
+                            (red[(2 * GMAX + g) * HD + d] + red[(3 * GMAX + g) * HD + d]);
+            const int h = kvh * G + g;
+            if (P.nsplit == 1) {
+                // one split: the combine below would give (1 * o) / (1 * l)
+                P.out[(size_t)m * P.ldo + (size_t)h * HD + d] = o / lloc[g];
+            } else {
                 float *dst = P.part + (((size_t)m * P.nq + h) * P.nsplit + sp) * (HD + 2);
-                st_dev(&dst[2 + d], acc[g] + pv[g][d]);
+                st_dev(&dst[2 + d], o);
                 if (d == 0) {
                     st_dev(&dst[0], mloc[g]);
                     st_dev(&dst[1], lloc[g]);
@@ -526,19 +569,44 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams P) {
     __syncthreads();
     if (!s_last) return;
     if (tid == 0) reset_dev(&P.counters[m * P.nkv + kvh]);
+    // Combine the splits (flash-decode merge, in split order).  The splits'
+    // (max, sum) pairs are staged in LDS and each thread's P.V partials are
+    // read CB at a time, so the device-coherent loads overlap.
+    const int ns = P.nsplit;
+    const bool staged = G * ns <= GMAX * kAttnMaxChunk / 2;
+    float *sm = &sc[0][0], *sl = sm + GMAX * kAttnMaxChunk / 2;  // [G][ns] each
+    if (staged) {
+        for (int i = tid; i < G * ns; i += kAttnThreads) {
+            const int g = i / ns, s2 = i - g * ns;
+            const float *src = P.part + (((size_t)m * P.nq + kvh * G + g) * ns + s2) * (HD + 2);
+            sm[i] = ld_dev(&src[0]);
+            sl[i] = ld_dev(&src[1]);
+        }
+    }
+    __syncthreads();
     for (int idx = tid; idx < G * HD; idx += kAttnThreads) {
         const int g = idx / HD, d = idx - g * HD;
         const int h = kvh * G + g;
-        const float *base = P.part + ((size_t)m * P.nq + h) * P.nsplit * (HD + 2);
+        const float *base = P.part + ((size_t)m * P.nq + h) * ns * (HD + 2);
+        auto mval = [&](int s2) { return staged ? sm[g * ns + s2] : ld_dev(&base[s2 * (HD + 2)]); };
+        auto lval = [&](int s2) { return staged ? sl[g * ns + s2] : ld_dev(&base[s2 * (HD + 2) + 1]); };
         float mx = -INFINITY;
-        for (int s = 0; s < P.nsplit; s++) mx = fmaxf(mx, ld_dev(&base[s * (HD + 2)]));
+        for (int s2 = 0; s2 < ns; s2++) mx = fmaxf(mx, mval(s2));
         float o = 0.0f, l = 0.0f;
-        for (int s = 0; s < P.nsplit; s++) {
-            const float ms = ld_dev(&base[s * (HD + 2)]);
-            if (ms == -INFINITY) continue;
-            const float w = expf(ms - mx);
-            o += w * ld_dev(&base[s * (HD + 2) + 2 + d]);
-            l += w * ld_dev(&base[s * (HD + 2) + 1]);
+        constexpr int CB = 8;
+        for (int s0 = 0; s0 < ns; s0 += CB) {
+            float ov[CB];
+#pragma unroll
+            for (int u = 0; u < CB; u++) ov[u] = s0 + u < ns ? ld_dev(&base[(s0 + u) * (HD + 2) + 2 + d]) : 0.0f;
+#pragma unroll
+            for (int u = 0; u < CB; u++) {
+                if (s0 + u >= ns) continue;
+                const float ms = mval(s0 + u);
+                if (ms == -INFINITY) continue;
+                const float w = expf(ms - mx);
+                o += w * ov[u];
+                l += w * lval(s0 + u);
+            }
         }
         P.out[(size_t)m * P.ldo + (size_t)h * HD + d] = o / l;
     }
@@ -936,8 +1004,11 @@ void launch_embed_rows(hipStream_t st, const DevQ4 &w, const uint32_t *tok, long
 
 // sample_argmax (src/code_predictor.rs:328-334) of each row: the last index
 // of the maximum; a NaN sets *status (per row) to QTTS_ENAN and gives 0.
+// With a table, the row also copies table[code] (width floats; zeros past
+// table_rows) to rows_out + r * rows_ld.
 __global__ __launch_bounds__(256) void k_argmax_rows(const float *logits, int n, uint32_t *out, long long out_stride,
-                                                     int *status, long long status_stride) {
+                                                     int *status, long long status_stride, const float *table,
+                                                     int table_rows, int width, float *rows_out, long long rows_ld) {
     __shared__ float sv[256];
     __shared__ int si[256];
     __shared__ int snan;
@@ -971,20 +1042,23 @@ __global__ __launch_bounds__(256) void k_argmax_rows(const float *logits, int n,
         }
         __syncthreads();
     }
+    const uint32_t code = snan ? 0u : (uint32_t)(si[0] < 0 ? 0 : si[0]);
     if (tid == 0) {
-        if (snan) {
-            out[(size_t)r * out_stride] = 0u;
-            if (status) *byte_off(status, (long long)r * status_stride) = QTTS_ENAN;
-        } else {
-            out[(size_t)r * out_stride] = (uint32_t)(si[0] < 0 ? 0 : si[0]);
-        }
+        out[(size_t)r * out_stride] = code;
+        if (snan && status) *byte_off(status, (long long)r * status_stride) = QTTS_ENAN;
+    }
+    if (table) {
+        const float *src = table + (size_t)code * width;
+        for (int j = tid; j < width; j += 256)
+            rows_out[(size_t)r * rows_ld + j] = code < (uint32_t)table_rows ? src[j] : 0.0f;
     }
 }
 
 void launch_argmax_rows(hipStream_t st, const float *logits, int rows, int n, uint32_t *out, long long out_stride,
-                        int *status, long long status_stride) {
+                        int *status, long long status_stride, const float *table, int table_rows, int width,
+                        float *rows_out, long long rows_ld) {
     hipLaunchKernelGGL(k_argmax_rows, dim3((unsigned)rows), dim3(256), 0, st, logits, n, out, out_stride, status,
-                       status_stride);
+                       status_stride, table, table_rows, width, rows_out, rows_ld);
 }
 
 // ---------------------------------------------------------------------------
