@@ -152,6 +152,26 @@ def test_predictor_full(full):
         assert np.array_equal(got, ref), (got, ref)
 
 
+def test_predictor_input_table_on_and_off(ctx, full, monkeypatch):
+    """Passes 2-15 read their input row from the per-code table of projected
+    embeddings (the default); QTTS_PREDICTOR_TABLE=0, read when a predictor
+    first runs, keeps the projection as a step of its own.  Both give the
+    oracle's codes, and their caches agree."""
+    tw, pw, t, p, ot, op = full
+    monkeypatch.setenv("QTTS_PREDICTOR_TABLE", "0")
+    p_off = qtts.CodePredictor(ctx, pw)
+    for i in range(2):
+        h = qtts.synth_normal_f32(8, f"tab.{i}", tw.cfg.hidden)
+        sem = ot.embed_codec_token(11 + 500 * i)
+        kv_on, kv_off = p.new_kv(), p_off.new_kv()
+        on = p.generate_acoustic_codes(h, sem, kv_on)
+        off = p_off.generate_acoustic_codes(h, sem, kv_off)
+        ref = op.generate_acoustic_codes(h, sem, op.new_kv())
+        assert np.array_equal(on, ref) and np.array_equal(off, ref), (on, off, ref)
+        (k1, v1), (k0, v0) = kv_on.store(), kv_off.store()
+        assert rel_err(k1, k0) < REL_TOL and rel_err(v1, v0) < REL_TOL
+
+
 def _loop_inputs(tw, seed, trailing=3):
     hidden = tw.cfg.hidden
     last_hidden = qtts.synth_normal_f32(seed, "loop.h", hidden)
