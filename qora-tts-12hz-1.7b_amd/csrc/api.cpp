@@ -696,6 +696,9 @@ struct qtts_predictor {
     float *tab = nullptr;
     int tab_rows = 0;
     int tab_state = 0;  // 0 not tried, 1 made, -1 not used
+    // layer 0's raw q|k|v of every tab row, rms_norm_f16 with its input gamma
+    // first: [groups-1][tab_rows][nq*hd + 2*nkv*hd] (with tab_state == 1)
+    float *qkv_tab = nullptr;
 };
 
 // ===========================================================================
@@ -734,6 +737,7 @@ struct TabIn {
     const float *table = nullptr;
     int rows = 0;
     TvRef code;
+    const float *qkv_table = nullptr;  // with it, the layer's raw q|k|v row by code too (no QKV step)
 };
 
 EngInput in_argtab(const TabIn &t) {
@@ -834,7 +838,7 @@ TvRef add_gemv(EngProgram &P, const DevQ4 &w, const GemvSpec &sp) {
 }
 
 TvRef add_attention(EngProgram &P, const Stack &st, int l, qtts_kv *kv, int M, const TvRef &qkv, bool from_state,
-                    int pos_const, int len_const, int nsplit) {
+                    int pos_const, int len_const, int nsplit, const TabIn *qtab = nullptr) {
     EngOp op{};
     op.kind = EOP_ATTN;
     EngAttn &a = op.attn;
@@ -864,6 +868,16 @@ TvRef add_attention(EngProgram &P, const Stack &st, int l, qtts_kv *kv, int M, c
     const bool lds_kv = !from_state && nsplit == 1 && st.hd == 128 && M * (st.nq / st.nkv) <= 4 &&
                         kv->cap <= kEngLdsKvPos && P.claim_lds(P.next_rot(), st.nkv, l);
     a.lds_kv = lds_kv ? 1 : 0;
+    if (qtab) {
+        if (!lds_kv || M != 1 || qtab->n > kEngArgtabMax) P.err = "engine q|k|v table needs the LDS-resident attention";
+        a.qkv = nullptr;
+        a.ld_qkv = st.nq * st.hd + 2 * st.nkv * st.hd;
+        a.qkv_table = qtab->qkv_table;
+        a.qkv_table_rows = qtab->rows;
+        a.logits = qtab->logits.p;
+        a.logits_tag = qtab->logits.tag;
+        a.logits_n = qtab->n;
+    }
     a.scale = 1.0f / sqrtf((float)st.hd);  // src/talker.rs:305
     const int qd = st.nq * st.hd;
     TvRef out{};
@@ -906,8 +920,9 @@ TvRef add_layer(EngProgram &P, const Stack &st, int l, qtts_kv *kv, int M, const
     q.norm = true;
     q.gamma = L.in_g;
     for (int m = 0; m < M; m++) q.in[m] = tin ? in_argtab(*tin) : in_tv(x, m);
-    const TvRef qkv = add_gemv(P, L.qkv, q);
-    const TvRef att = add_attention(P, st, l, kv, M, qkv, from_state, pos_const, len_const, nsplit);
+    const bool qtab = tin && tin->qkv_table;  // the q|k|v row by code: no QKV step
+    const TvRef qkv = qtab ? TvRef{} : add_gemv(P, L.qkv, q);
+    const TvRef att = add_attention(P, st, l, kv, M, qkv, from_state, pos_const, len_const, nsplit, qtab ? tin : nullptr);
     GemvSpec o;
     o.M = M;
     for (int m = 0; m < M; m++) o.in[m] = in_tv(att, m);
@@ -1147,8 +1162,27 @@ qtts_status make_predictor_tables(qtts_predictor *p) {
             QTTS_TRY(run_gemv(c, q));
         }
     }
+    // layer 0's q|k|v projection of every row, RMSNorm first (the first
+    // step of such a pass, also a function of the code alone)
+    const Stack &st = p->st;
+    const int nqkv = st.nq * st.hd + 2 * st.nkv * st.hd;
+    float *qkv = nullptr;
+    QTTS_TRY(p->own.alloc(c, &qkv, (size_t)nt * rows * nqkv));
+    for (int g = 0; g < nt; g++)
+        for (int r0 = 0; r0 < rows; r0 += kMaxM) {
+            GemvParams q = gemv_base(c, st.L[0].qkv, rows - r0 < kMaxM ? rows - r0 : kMaxM);
+            q.prologue = PRO_RMSNORM;
+            q.x = tab + ((size_t)g * rows + r0) * H;
+            q.ldx = H;
+            q.gamma = st.L[0].in_g;
+            q.epilogue = EPI_STORE;
+            q.y = qkv + ((size_t)g * rows + r0) * nqkv;
+            q.ldy = nqkv;
+            QTTS_TRY(run_gemv(c, q));
+        }
     QTTS_TRY(sync(c));
     p->tab = tab;
+    p->qkv_tab = qkv;
     p->tab_rows = rows;
     p->tab_state = 1;
     return QTTS_OK;
@@ -1176,11 +1210,15 @@ qtts_status build_predictor_passes(EngProgram &P, qtts_predictor *p, qtts_kv *kv
     hd.in[0] = in_tv(x, 1);
     TvRef lg = add_gemv(P, p->heads[0], hd);
     const bool tab = p->tab_state == 1;
-    if (tab && P.ops.size() > first + 1) {
+    // With the q|k|v table the later passes start at layer 0's attention,
+    // which must keep its rows in LDS (as this pass's does).
+    const bool qtab = tab && P.ops.size() > first + 2 && P.ops[first + 2].kind == EOP_ATTN &&
+                      P.ops[first + 2].attn.lds_kv == 1;
+    if (tab && P.ops.size() > first + 2) {
         // The argmax step's block runs no task of the next pass's first
-        // step (the one-row version of this pass's), which computes the same
-        // argmax itself.
-        const EngOp &q = P.ops[first + 1];
+        // step (the one-row version of this pass's QKV step, or the
+        // attention), which computes the same argmax itself.
+        const EngOp &q = P.ops[first + (qtab ? 2 : 1)];
         const int n = q.ntasks / (q.kind == EOP_GEMV && q.gemv.M > 1 ? q.gemv.M : 1);
         if (n < P.grid) P.rot_next = (q.rot + n) % P.grid;
     }
@@ -1193,13 +1231,14 @@ qtts_status build_predictor_passes(EngProgram &P, qtts_predictor *p, qtts_kv *kv
             // The input projection of the previous code is a table row: the
             // first layer reads it at the argmax of the previous logits
             // (the argmax step still files and publishes the code).
-            P.plan_pos = 1;
+            P.plan_pos = qtab ? 2 : 1;
             TabIn ti;
             ti.logits = lg;
             ti.n = p->vocab;
             ti.table = p->tab + (size_t)(g - 1) * p->tab_rows * st.hidden;
             ti.rows = p->tab_rows;
             ti.code = codes[g - 1];
+            if (qtab) ti.qkv_table = p->qkv_tab + (size_t)(g - 1) * p->tab_rows * (st.nq * st.hd + 2 * st.nkv * st.hd);
             x = add_layer(P, st, 0, kv, 1, TvRef{}, false, g + 1, g + 1, 1, &ti);
         } else {
             GemvSpec e;

@@ -100,6 +100,12 @@ struct EngAttn {
                              // of this layer runs task h on the same block (the host pins the
                              // rotation), which keeps kv head h's rows [0, len) there
     float scale;
+    // lds_kv, M == 1: the raw q/k/v row is qkv_table[argmax(logits[0..logits_n))] (ld_qkv
+    // floats; a code past the last row gives zeros) instead of the tagged qkv
+    const float *qkv_table;
+    int qkv_table_rows;
+    const tv_t *logits;
+    int logits_tag, logits_n;
     tv_t *part;  // nsplit > 1: [M][nq][nsplit][hd + 2]
     int part_tag;
     tv_t *out;   // nsplit == 1: [M][nq*hd]

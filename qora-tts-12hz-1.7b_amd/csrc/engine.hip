@@ -871,6 +871,13 @@ __device__ __forceinline__ int eng_attn_lean(const KCONST EngAttn &a, int task, 
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: scalar branches below
     const int G = a.nq / a.nkv;
     const int M = a.M;
+    uint32_t tcode = 0;  // qkv_table: the previous step's code, taken by the whole block
+    if (a.qkv_table) {
+        int anynan = 0;
+        const int ix = block_argmax<kEngArgtabMax / kEngThreads>(a.logits, a.logits_n, tb + a.logits_tag, c,
+                                                                smem + kEngSmemFloats - 8, &anynan);
+        tcode = (ix < 0 || anynan) ? 0u : (uint32_t)ix;
+    }
     if (wave >= M * G) return task;
     const int m = wave / G, gq = wave - m * G, kvh = task, h = kvh * G + gq;
     const int base = a.len_const, pos0 = a.pos_const;
@@ -921,7 +928,22 @@ __device__ __forceinline__ int eng_attn_lean(const KCONST EngAttn &a, int task, 
         ptr[4 + 4 * r] = &a.qkv[(size_t)r * a.ld_qkv + voff];
         ptr[5 + 4 * r] = ptr[4 + 4 * r] + 1;
     }
-    wait_list<NW>(ptr, tg, 2 + 4 * M, val, c);
+    if (a.qkv_table) {
+        // one new row (M == 1): its raw q, k, v from the table row at the code
+        const bool have = tcode < (uint32_t)a.qkv_table_rows;
+        const float *row = a.qkv_table + (size_t)(have ? tcode : 0u) * a.ld_qkv;
+        const uint64_t qb = glb(reinterpret_cast<const uint64_t *>(row + qoff))[0];
+        const uint64_t kb = glb(reinterpret_cast<const uint64_t *>(row + koff))[0];
+        const uint64_t vb = glb(reinterpret_cast<const uint64_t *>(row + voff))[0];
+        val[0] = have ? __uint_as_float((uint32_t)qb) : 0.0f;
+        val[1] = have ? __uint_as_float((uint32_t)(qb >> 32)) : 0.0f;
+        val[2] = have ? __uint_as_float((uint32_t)kb) : 0.0f;
+        val[3] = have ? __uint_as_float((uint32_t)(kb >> 32)) : 0.0f;
+        val[4] = have ? __uint_as_float((uint32_t)vb) : 0.0f;
+        val[5] = have ? __uint_as_float((uint32_t)(vb >> 32)) : 0.0f;
+    } else {
+        wait_list<NW>(ptr, tg, 2 + 4 * M, val, c);
+    }
     stamp(c, 3);
 
     // 2. QK-norm + RoPE of q and of the new k rows
