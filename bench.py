@@ -86,10 +86,11 @@ def q4_bytes(k, n):
 def frame_bytes(tc, pc, groups, kv_len):
     """Algorithmic bytes one engine launch (one code) moves: every weight it
     applies once (talker layers + codec head; the predictor's input
-    projection in the first pass, 5 layers and one head per pass), the
-    projected input row each later pass reads from the per-code table, the
-    talker K/V rows it reads at kv_len positions and writes once, and the
-    predictor's K/V rows."""
+    projection in the first pass, 5 layers and one head per pass, less
+    layer 0's q|k|v projection in the later passes), the rows each later
+    pass reads from the per-code tables instead (its projected input and
+    layer 0's q|k|v), the talker K/V rows it reads at kv_len positions and
+    writes once, and the predictor's K/V rows."""
     def layer(c):
         qd, kd = c.heads * c.head_dim, c.kv_heads * c.head_dim
         return (q4_bytes(c.hidden, qd + 2 * kd) + q4_bytes(qd, c.hidden) + q4_bytes(c.hidden, 2 * c.inter)
@@ -98,7 +99,9 @@ def frame_bytes(tc, pc, groups, kv_len):
     kv_row = tc.kv_heads * tc.head_dim * 4
     talker_kv = tc.layers * 2 * kv_row * (kv_len + 1)
     pred_pass = pc.layers * layer(pc) + q4_bytes(pc.hidden, pc.vocab)
-    pred_in = q4_bytes(tc.hidden, pc.hidden) + (groups - 1) * 4 * pc.hidden
+    p_qkv = pc.heads * pc.head_dim + 2 * pc.kv_heads * pc.head_dim
+    pred_in = (q4_bytes(tc.hidden, pc.hidden) + (groups - 1) * 4 * (pc.hidden + p_qkv)
+               - (groups - 1) * q4_bytes(pc.hidden, p_qkv))
     pred_kv = sum(pc.layers * 2 * pc.kv_heads * pc.head_dim * 4 * (g + 2) for g in range(groups))
     return talker + talker_kv + groups * pred_pass + pred_in + pred_kv
 

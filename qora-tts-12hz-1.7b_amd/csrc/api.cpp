@@ -1147,39 +1147,58 @@ qtts_status make_predictor_tables(qtts_predictor *p) {
     std::vector<uint32_t> h((size_t)rows);
     for (int i = 0; i < rows; i++) h[(size_t)i] = (uint32_t)i;
     HIP_TRY(c, hipMemcpyAsync(ids, h.data(), sizeof(uint32_t) * rows, hipMemcpyHostToDevice, c->stream));
-    for (int g = 0; g < nt; g++) {
-        launch_embed_rows(c->stream, p->emb[g], ids, 1, rows, x, th);
-        QTTS_TRY(check_launch(c, "k_embed_rows"));
-        for (int r0 = 0; r0 < rows; r0 += kMaxM) {
-            GemvParams q = gemv_base(c, p->in_proj, rows - r0 < kMaxM ? rows - r0 : kMaxM);
-            q.prologue = PRO_PLAIN;
-            q.x = x + (size_t)r0 * th;
-            q.ldx = th;
-            q.epilogue = EPI_STORE;
-            q.y = tab + ((size_t)g * rows + r0) * H;
-            q.ldy = H;
-            q.bias = p->bias;
-            QTTS_TRY(run_gemv(c, q));
-        }
-    }
-    // layer 0's q|k|v projection of every row, RMSNorm first (the first
-    // step of such a pass, also a function of the code alone)
+    // Matrix-core copies of the two weights (one GEMM per table), else GEMV
+    // launches of kMaxM rows.
     const Stack &st = p->st;
     const int nqkv = st.nq * st.hd + 2 * st.nkv * st.hd;
+    DevQ4Mfma m_in{}, m_qkv{};
+    bool ok_in = false, ok_qkv = false;
+    void *mem = nullptr;
+    if (rows >= kMfmaMinRows) {
+        QTTS_TRY(make_mfma_copy(c, p->in_proj, &mem, &m_in, &ok_in));
+        if (mem) tmp.ptrs.push_back(mem);
+        QTTS_TRY(make_mfma_copy(c, st.L[0].qkv, &mem, &m_qkv, &ok_qkv));
+        if (mem) tmp.ptrs.push_back(mem);
+    }
     float *qkv = nullptr;
     QTTS_TRY(p->own.alloc(c, &qkv, (size_t)nt * rows * nqkv));
-    for (int g = 0; g < nt; g++)
-        for (int r0 = 0; r0 < rows; r0 += kMaxM) {
-            GemvParams q = gemv_base(c, st.L[0].qkv, rows - r0 < kMaxM ? rows - r0 : kMaxM);
-            q.prologue = PRO_RMSNORM;
-            q.x = tab + ((size_t)g * rows + r0) * H;
-            q.ldx = H;
-            q.gamma = st.L[0].in_g;
-            q.epilogue = EPI_STORE;
-            q.y = qkv + ((size_t)g * rows + r0) * nqkv;
-            q.ldy = nqkv;
-            QTTS_TRY(run_gemv(c, q));
+    for (int g = 0; g < nt; g++) {
+        float *tg = tab + (size_t)g * rows * H, *qg = qkv + (size_t)g * rows * nqkv;
+        launch_embed_rows(c->stream, p->emb[g], ids, 1, rows, x, th);
+        QTTS_TRY(check_launch(c, "k_embed_rows"));
+        if (ok_in) {
+            QTTS_TRY(run_gemm_mfma(c, m_in, x, rows, th, MFMA_ROWS_PLAIN, nullptr, tg, H, p->bias, false));
+        } else {
+            for (int r0 = 0; r0 < rows; r0 += kMaxM) {
+                GemvParams q = gemv_base(c, p->in_proj, rows - r0 < kMaxM ? rows - r0 : kMaxM);
+                q.prologue = PRO_PLAIN;
+                q.x = x + (size_t)r0 * th;
+                q.ldx = th;
+                q.epilogue = EPI_STORE;
+                q.y = tg + (size_t)r0 * H;
+                q.ldy = H;
+                q.bias = p->bias;
+                QTTS_TRY(run_gemv(c, q));
+            }
         }
+        // layer 0's q|k|v projection of every row, RMSNorm first (the first
+        // step of such a pass, also a function of the code alone)
+        if (ok_qkv) {
+            QTTS_TRY(run_gemm_mfma(c, m_qkv, tg, rows, H, MFMA_ROWS_RMSNORM, st.L[0].in_g, qg, nqkv, nullptr, false));
+        } else {
+            for (int r0 = 0; r0 < rows; r0 += kMaxM) {
+                GemvParams q = gemv_base(c, st.L[0].qkv, rows - r0 < kMaxM ? rows - r0 : kMaxM);
+                q.prologue = PRO_RMSNORM;
+                q.x = tg + (size_t)r0 * H;
+                q.ldx = H;
+                q.gamma = st.L[0].in_g;
+                q.epilogue = EPI_STORE;
+                q.y = qg + (size_t)r0 * nqkv;
+                q.ldy = nqkv;
+                QTTS_TRY(run_gemv(c, q));
+            }
+        }
+    }
     QTTS_TRY(sync(c));
     p->tab = tab;
     p->qkv_tab = qkv;
