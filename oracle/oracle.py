@@ -1,8 +1,8 @@
 """ctypes binding of the CPU oracle (oracle/liboracle.so).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, __graft_entry__.smoke() and
-bench.py's CPU-baseline leg, always as the checker or the timed CPU
-baseline, never as a product path.  Function names follow the reference's
+bench.py's CPU-baseline leg, always as the reference the results are
+compared with or the timed CPU baseline, never as a product path.  Function names follow the reference's
 (src/gemv.rs, src/talker.rs, src/code_predictor.rs, src/generate_new.rs).
 """
 

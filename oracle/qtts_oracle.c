@@ -1,7 +1,8 @@
 /*
  * qtts_oracle.c — CPU restatement of the reference's per-code loop.
  *
- * TEST INFRASTRUCTURE ONLY (the parity checker and the timed CPU baseline);
+ * TEST INFRASTRUCTURE ONLY (what the parity tests compare with, and the
+ * timed CPU baseline);
  * the product library never links or calls it.  Every function cites the
  * reference lines whose arithmetic order it follows.  Compile with
  * -O3 -ffp-contract=off and no -march flag (Cargo.toml:20-23 release profile,

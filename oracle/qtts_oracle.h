@@ -1,8 +1,8 @@
 /*
  * qtts_oracle.h — CPU restatement of the reference's per-code loop.
  *
- * TEST INFRASTRUCTURE ONLY.  This is the checker the parity tests compare
- * the HIP library against, and the CPU baseline bench.py times.  Nothing in
+ * TEST INFRASTRUCTURE ONLY.  This is what the parity tests compare the HIP
+ * library against, and the CPU baseline bench.py times.  Nothing in
  * the product library links, loads or calls it.
  *
  * It restates the arithmetic ORDER of the reference Rust crate (qora-tts

@@ -2,7 +2,7 @@
  * qtts_oracle_decoder.c — CPU restatement of the speech decoder
  * (src/decoder.rs, src/conv.rs).
  *
- * TEST INFRASTRUCTURE ONLY: the checker the decoder's parity tests compare
+ * TEST INFRASTRUCTURE ONLY: the reference the decoder's parity tests compare
  * the HIP library against.  Nothing in the product library links it.
  *
  * Every sum keeps the reference's order: the f32 GEMVs accumulate over k

@@ -1,4 +1,4 @@
-"""CPU tests that pin the oracle (the parity checker) and the library's host
+"""CPU tests that pin the oracle (what the parity tests compare with) and the library's host
 logic.  Each check is chosen so that a plausible mistake fails it: closed
 forms (binary16, xorshift, RoPE, RMSNorm of a constant), invariants (one-hot
 GEMV, thread-split invariance, prefill == sequential decode, RoPE norm
