@@ -2952,8 +2952,10 @@ qtts_status make_predictor_mfma(qtts_predictor *p) {
 }
 
 // One layer stack over M independent rows (per-row caches from R).
+// fused: every row is its stream's only new row, so the attention kernel
+// does k_qkv_rows' work itself (no row attends to another row's new K/V).
 qtts_status layers_batched(qtts_ctx *c, const Stack &st, const DevQ4Mfma *W, const RowTab &R, float *x, int M,
-                           float *raw, float *q, float *a, int nsplit) {
+                           float *raw, float *q, float *a, int nsplit, bool fused) {
     const int hidden = st.hidden, qd = st.nq * st.hd, nqkv = qd + 2 * st.nkv * st.hd;
     if ((size_t)M * st.nq * nsplit * (st.hd + 2) > kAttnPartFloats || M * st.nkv > kAttnCounters)
         return fail(c, QTTS_ESHAPE, "batched attention: too many rows for the split buffers");
@@ -2986,8 +2988,10 @@ qtts_status layers_batched(qtts_ctx *c, const Stack &st, const DevQ4Mfma *W, con
         qp.row_kv = R.kv;
         qp.row_stride = R.stride;
         qp.layer_off = layer_off;
-        launch_qkv_rows(c->stream, qp);
-        QTTS_TRY(check_launch(c, "k_qkv_rows"));
+        if (!fused) {
+            launch_qkv_rows(c->stream, qp);
+            QTTS_TRY(check_launch(c, "k_qkv_rows"));
+        }
         AttnParams ap{};
         ap.q = q;
         ap.ldq = qd;
@@ -3007,6 +3011,18 @@ qtts_status layers_batched(qtts_ctx *c, const Stack &st, const DevQ4Mfma *W, con
         ap.row_kv = R.kv;
         ap.row_stride = R.stride;
         ap.layer_off = layer_off;
+        if (fused) {
+            ap.raw = raw;
+            ap.ldr = nqkv;
+            ap.q_norm = Ly.q_norm;
+            ap.k_norm = Ly.k_norm;
+            ap.rope_cos = st.rope_cos;
+            ap.rope_sin = st.rope_sin;
+            ap.rope_rows = st.rope_rows;
+            ap.rope_skip_oob = st.rope_skip_oob;
+            ap.row_pos = R.pos;
+            ap.pos0 = R.pos0;
+        }
         launch_attention(c->stream, ap, M);
         QTTS_TRY(check_launch(c, "k_attn"));
         QTTS_TRY(run_gemm_mfma(c, Wl[1], a, M, qd, MFMA_ROWS_PLAIN, nullptr, x, hidden, nullptr, true));
@@ -3230,7 +3246,7 @@ qtts_status qtts_generate_codes_batch(qtts_talker *t, qtts_predictor *p, int32_t
                     PR.pos0 = g + 1;
                     PR.kv0 = g + 1;
                 }
-                QTTS_TRY(layers_batched(c, *ps, p->mfma.data(), PR, xp, M, raw, q, att, 1));
+                QTTS_TRY(layers_batched(c, *ps, p->mfma.data(), PR, xp, M, raw, q, att, 1, g > 0));
                 // head g on the last row of each stream
                 const float *hx = g == 0 ? xp + hp : xp;
                 const int hld = g == 0 ? 2 * hp : hp;
@@ -3270,7 +3286,7 @@ qtts_status qtts_generate_codes_batch(qtts_talker *t, qtts_predictor *p, int32_t
         launch_embed_sum(c->stream, e);
         QTTS_TRY(check_launch(c, "k_embed_sum"));
         // 4. talker step for every stream, then the codec head
-        QTTS_TRY(layers_batched(c, ts, t->mfma.data(), TR, x, B, raw, q, att, tsplit));
+        QTTS_TRY(layers_batched(c, ts, t->mfma.data(), TR, x, B, raw, q, att, tsplit, true));
         QTTS_TRY(run_gemm_mfma(c, t->head_mfma, x, B, H, MFMA_ROWS_RMSNORM, ts.final_g, lg, V, nullptr, false,
                                talker_only ? nullptr : in2, 2 * H));
         launch_advance(c->stream, S, 1, B);

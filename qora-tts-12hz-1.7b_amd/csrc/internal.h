@@ -224,6 +224,19 @@ struct AttnParams {
     const int *row_kv;
     int row_stride;
     long long layer_off;
+    // one new row per stream (batched decode): with raw set, q is not read;
+    // every block QK-norms and rotates its kv head's query heads from the
+    // raw GEMM output (row m at raw + m * ldr, [q | k | v] heads x hd), and
+    // the block whose split holds the new position (kvlen_const +
+    // row_kv[m * row_stride]) does the same for k, appends k and v to the
+    // cache there and uses them from LDS -- the work of k_qkv_rows
+    const float *raw;
+    int ldr;
+    const uint16_t *q_norm, *k_norm;
+    const float *rope_cos, *rope_sin;
+    int rope_rows, rope_skip_oob;
+    const int *row_pos;  // RoPE position pos0 + row_pos[m * row_stride]
+    int pos0;
 };
 
 // Device-resident state of one generation loop (one per talker).

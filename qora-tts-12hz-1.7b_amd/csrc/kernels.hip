@@ -443,14 +443,62 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams P) {
     const int t1 = min(L, t0 + chunk);
     const int nt = max(0, t1 - t0);
 
-    for (int idx = tid; idx < G * HD; idx += kAttnThreads) {
-        const int g = idx / HD, d = idx - g * HD;
-        qs[g][d] = P.q[(size_t)m * P.ldq + (size_t)(kvh * G + g) * HD + d];
-    }
-    __syncthreads();
-
     const float *Kb = (P.row_k ? P.row_k[m] + P.layer_off : P.kcache) + (size_t)kvh * P.kv_cap * HD;
     const float *Vb = (P.row_v ? P.row_v[m] + P.layer_off : P.vcache) + (size_t)kvh * P.kv_cap * HD;
+    __shared__ __align__(16) float kn[HD], vn[HD];  // raw mode: the new row's k and v
+    const int tnew = P.raw ? L - 1 : -1;            // its position (raw mode)
+    if (P.raw) {
+        // QK-norm (src/talker.rs:86-99) and split-half RoPE (src/rope.rs:79-92)
+        // of this kv head's query heads and, in the split holding the new
+        // position, of its k; two heads per round, 128 threads each
+        __shared__ float hn[2][HD];
+        __shared__ float hs2[4];
+        const bool last = nt > 0 && t1 == L;
+        const int nh = G + (last ? 1 : 0);
+        const int pos = P.pos0 + (P.row_pos ? P.row_pos[(size_t)m * P.row_stride] : 0);
+        const bool rotate = !(P.rope_skip_oob && pos >= P.rope_rows);
+        const float *rs = P.raw + (size_t)m * P.ldr;
+        const int hh0 = tid >> 7, d = tid & (HD - 1);
+        for (int h0 = 0; h0 < nh; h0 += 2) {
+            const int hh = h0 + hh0;
+            const bool isk = hh == G;
+            const float v = hh < nh ? rs[(size_t)(isk ? P.nq + kvh : kvh * G + hh) * HD + d] : 0.0f;
+            const float w = wave_sum(v * v);
+            if (lane == 0) hs2[wave] = w;
+            __syncthreads();
+            const float inv = 1.0f / sqrtf((hs2[2 * hh0] + hs2[2 * hh0 + 1]) / (float)HD + 1e-6f);
+            if (hh < nh) hn[hh0][d] = v * inv * f16_to_f32((isk ? P.k_norm : P.q_norm)[d]);
+            __syncthreads();
+            if (hh < nh && d < HD / 2) {
+                const float x1 = hn[hh0][d], x2 = hn[hh0][d + HD / 2];
+                float o1 = x1, o2 = x2;
+                if (rotate) {
+                    const float cs = P.rope_cos[(size_t)pos * (HD / 2) + d];
+                    const float sn = P.rope_sin[(size_t)pos * (HD / 2) + d];
+                    o1 = x1 * cs - x2 * sn;
+                    o2 = x2 * cs + x1 * sn;
+                }
+                float *dst = isk ? kn : qs[hh < GMAX ? hh : 0];
+                dst[d] = o1;
+                dst[d + HD / 2] = o2;
+            }
+            __syncthreads();
+        }
+        if (last && tid < HD) {
+            // the new row: v as is; k and v appended to the stream's cache
+            // (src/talker.rs:299-302) for later steps; this step reads them
+            // from LDS
+            vn[tid] = rs[(size_t)(P.nq + P.nkv + kvh) * HD + tid];
+            const_cast<float *>(Kb)[(size_t)tnew * HD + tid] = kn[tid];
+            const_cast<float *>(Vb)[(size_t)tnew * HD + tid] = vn[tid];
+        }
+    } else {
+        for (int idx = tid; idx < G * HD; idx += kAttnThreads) {
+            const int g = idx / HD, dd = idx - g * HD;
+            qs[g][dd] = P.q[(size_t)m * P.ldq + (size_t)(kvh * G + g) * HD + dd];
+        }
+    }
+    __syncthreads();
 
     // scores: 16 lanes per position, 8 dims per lane; SU positions per
     // thread are loaded before any is used (clamped to the split, masked
@@ -466,6 +514,14 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams P) {
                 const float *kr = Kb + (size_t)(t0 + tt) * HD + l16 * 8;
                 ka[u] = *reinterpret_cast<const float4 *>(kr);
                 kb[u] = *reinterpret_cast<const float4 *>(kr + 4);
+            }
+#pragma unroll
+            for (int u = 0; u < SU; u++) {
+                const int tt = min(b0 + slot + 16 * u, nt - 1);
+                if (t0 + tt == tnew) {
+                    ka[u] = *reinterpret_cast<const float4 *>(&kn[l16 * 8]);
+                    kb[u] = *reinterpret_cast<const float4 *>(&kn[l16 * 8 + 4]);
+                }
             }
 #pragma unroll
             for (int u = 0; u < SU; u++) {
@@ -517,6 +573,11 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams P) {
             for (int u = 0; u < VU; u++) {
                 const int tt = min(b0 + r8 + 8 * u, nt - 1);
                 v[u] = *reinterpret_cast<const float4 *>(Vb + (size_t)(t0 + tt) * HD + 4 * d4);
+            }
+#pragma unroll
+            for (int u = 0; u < VU; u++) {
+                const int tt = min(b0 + r8 + 8 * u, nt - 1);
+                if (t0 + tt == tnew) v[u] = *reinterpret_cast<const float4 *>(&vn[4 * d4]);
             }
 #pragma unroll
             for (int u = 0; u < VU; u++) {
