@@ -387,7 +387,7 @@ qtts_status mfma_reserve(qtts_ctx *c, int K, int N, int M) {
 qtts_status run_gemm_mfma(qtts_ctx *c, const DevQ4Mfma &w, const float *x, int M, int ldx, int mode,
                           const uint16_t *gamma, float *y, int ldy, const float *bias, bool accumulate,
                           float *norm_out = nullptr, int ldn = 0) {
-    const int K = w.K, N = w.N, Ks = K / 16, panels = N / 32;
+    const int K = w.K, N = w.N, panels = N / 32;
     if (K % 16 || N % 32 || K > kMfmaRowsMaxK || ldx % 4 || ((uintptr_t)x & 15))
         return fail(c, QTTS_ESHAPE, "MFMA GEMM: unsupported shape or unaligned rows");
     if (panels > kCounters) return fail(c, QTTS_ESHAPE, "MFMA GEMM: more panels than counters");
