@@ -8,7 +8,7 @@ import pytest
 
 import qtts
 from oracle import oracle
-from shapes import FULL_PREDICTOR, FULL_TALKER, TINY_PREDICTOR, TINY_TALKER
+from shapes import FULL_PREDICTOR, FULL_TALKER, TINY_PREDICTOR, TINY_TALKER, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -56,6 +56,11 @@ def test_batch_matches_oracle_streams(tiny, greedy):
         assert got[b].shape == ref.shape == (16, frames)
         assert np.array_equal(got[b], ref), (b, np.argwhere(got[b] != ref)[:5])
         assert len(kvs[b]) == lens[b] + frames
+        # the rows the loop appended (QK-normed, rotated K and raw V, written
+        # by the attention kernel itself) match the oracle's cache
+        (gk, gv), (rk, rv) = kvs[b].store(), okvs[b].store()
+        assert gk.shape == rk.shape
+        assert rel_err(gk, rk) < 1e-3 and rel_err(gv, rv) < 1e-3, b
 
 
 def test_batch_talker_only_and_eos(tiny):
