@@ -63,6 +63,25 @@ def test_batch_matches_oracle_streams(tiny, greedy):
         assert rel_err(gk, rk) < 1e-3 and rel_err(gv, rv) < 1e-3, b
 
 
+def test_batch_long_caches(tiny):
+    """Streams deep into long caches (700-900 prompt rows of a 1000-row
+    capacity): every talker attention split spans dozens of positions and
+    the new row lands in the last one, which appends it; codes and caches
+    match the oracle's."""
+    tw, pw, t, p, ot, op = tiny
+    B, frames = 2, 4
+    lens = [700, 900]
+    kvs, okvs, lh, lg, pos, text, pad = _streams(tw, t, ot, B, 65, lens, 1000)
+    params = qtts.loop_params(frames, greedy=True, stop_on_eos=False)
+    got = qtts.generate_codes_batch(t, p, kvs, lh, lg, pos, text, pad, params, [3, 4])
+    for b in range(B):
+        ref = oracle.generate_codes(ot, op, okvs[b], op.new_kv(), lh[b], lg[b], pos[b], text[b], pad, params, seed=3 + b)
+        assert np.array_equal(got[b], ref), (b, np.argwhere(got[b] != ref)[:5])
+        (gk, gv), (rk, rv) = kvs[b].store(), okvs[b].store()
+        assert gk.shape == rk.shape
+        assert rel_err(gk, rk) < 1e-3 and rel_err(gv, rv) < 1e-3, b
+
+
 def test_batch_talker_only_and_eos(tiny):
     """Talker-only loops; with EOS on, each stream stops on its own frame."""
     tw, _, t, _, ot, _ = tiny
