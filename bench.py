@@ -83,27 +83,35 @@ def q4_bytes(k, n):
     return k * n // 2 + k * (n // 32) * 2
 
 
-def frame_bytes(tc, pc, groups, kv_len):
-    """Algorithmic bytes one engine launch (one code) moves: every weight it
-    applies once (talker layers + codec head; the predictor's input
-    projection in the first pass, 5 layers and one head per pass, less
-    layer 0's q|k|v projection in the later passes), the rows each later
-    pass reads from the per-code tables instead (its projected input and
-    layer 0's q|k|v), the talker K/V rows it reads at kv_len positions and
-    writes once, and the predictor's K/V rows."""
-    def layer(c):
-        qd, kd = c.heads * c.head_dim, c.kv_heads * c.head_dim
-        return (q4_bytes(c.hidden, qd + 2 * kd) + q4_bytes(qd, c.hidden) + q4_bytes(c.hidden, 2 * c.inter)
-                + q4_bytes(c.inter, c.hidden) + 4 * c.hidden + 4 * c.head_dim)
-    talker = tc.layers * layer(tc) + q4_bytes(tc.hidden, tc.vocab) + 2 * tc.hidden
+def _layer_bytes(c):
+    """One layer's Q4 weights (q|k|v, o, gate|up, down) and f16 norm gammas."""
+    qd, kd = c.heads * c.head_dim, c.kv_heads * c.head_dim
+    return (q4_bytes(c.hidden, qd + 2 * kd) + q4_bytes(qd, c.hidden) + q4_bytes(c.hidden, 2 * c.inter)
+            + q4_bytes(c.inter, c.hidden) + 4 * c.hidden + 4 * c.head_dim)
+
+
+def talker_step_bytes(tc, kv_len):
+    """Algorithmic bytes of one talker decode step at a cache of kv_len rows:
+    every layer weight once, the codec head, the final gamma, and the K/V rows
+    read (kv_len + 1 positions, the new one included) -- 855,459,840 B at
+    kv_len 256."""
     kv_row = tc.kv_heads * tc.head_dim * 4
-    talker_kv = tc.layers * 2 * kv_row * (kv_len + 1)
-    pred_pass = pc.layers * layer(pc) + q4_bytes(pc.hidden, pc.vocab)
+    return (tc.layers * _layer_bytes(tc) + q4_bytes(tc.hidden, tc.vocab) + 2 * tc.hidden
+            + tc.layers * 2 * kv_row * (kv_len + 1))
+
+
+def frame_bytes(tc, pc, groups, kv_len):
+    """Algorithmic bytes one engine launch (one code) moves: the talker step
+    (above); the predictor's input projection in the first pass, 5 layers and
+    one head per pass, less layer 0's q|k|v projection in the later passes;
+    the rows each later pass reads from the per-code tables instead (its
+    projected input and layer 0's q|k|v); and the predictor's K/V rows."""
+    pred_pass = pc.layers * _layer_bytes(pc) + q4_bytes(pc.hidden, pc.vocab)
     p_qkv = pc.heads * pc.head_dim + 2 * pc.kv_heads * pc.head_dim
     pred_in = (q4_bytes(tc.hidden, pc.hidden) + (groups - 1) * 4 * (pc.hidden + p_qkv)
                - (groups - 1) * q4_bytes(pc.hidden, p_qkv))
     pred_kv = sum(pc.layers * 2 * pc.kv_heads * pc.head_dim * 4 * (g + 2) for g in range(groups))
-    return talker + talker_kv + groups * pred_pass + pred_in + pred_kv
+    return talker_step_bytes(tc, kv_len) + groups * pred_pass + pred_in + pred_kv
 
 
 def engine_roofline(frames, gpu_s, kv_len_mean):
@@ -126,14 +134,15 @@ def engine_roofline(frames, gpu_s, kv_len_mean):
     }
 
 
-def gemv_roofline(ctx, iters=256, copies=64):
-    """Average duration of the talker's gate|up Q4 GEMV shape (K=2048 ->
-    N=2*6144 in one launch) over `copies` distinct weights (a 0.9 GB working
-    set, larger than the 256 MB last-level cache), timed with HIP events on
-    the context's stream, the stream the kernels run on."""
-    K, N = 2048, 12288
+def gemv_roofline(ctx, K=2048, N=12288, iters=256, copies=64, traffic_file=None, label=None):
+    """Average duration of one stand-alone Q4 GEMV launch (qtts_gemv_device)
+    of shape K -> N over `copies` distinct weights (a working set above the
+    256 MB last-level cache from 2048 x 4096 up), timed with HIP events on
+    the context's stream, the stream the kernels run on.  Algorithmic bytes
+    per launch: K*N/2 nibble bytes + 2*K*N/32 scale bytes + 4K input + 4N
+    output."""
     hip = Hip()
-    ws = [qtts.DeviceQ4(ctx, qtts.Q4Weight.synthetic(99, f"roof.{i}", K, N)) for i in range(copies)]
+    ws = [qtts.DeviceQ4(ctx, qtts.Q4Weight.synthetic(99, f"roof.{K}.{N}.{i}", K, N)) for i in range(copies)]
     dx, dy = hip.malloc(4 * K), hip.malloc(4 * N)
     hip.h2d(dx, qtts.synth_normal_f32(99, "roof.x", K))
     for i in range(copies):
@@ -147,19 +156,67 @@ def gemv_roofline(ctx, iters=256, copies=64):
     avg_s = hip.elapsed_ms(start, end) / 1e3 / iters
     hip.free(dx)
     hip.free(dy)
+    for w in ws:
+        w.close()
     algo_bytes = K * N // 2 + K * (N // 32) * 2 + 4 * K + 4 * N
     achieved = algo_bytes / avg_s / 1e9
     return {
+        "shape": f"{K}->{N}",
         "bound": "hbm",
         "achieved": round(achieved, 1),
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
-        "traffic": read_traffic("q4_gemv_2048x12288_counters.md"),
-        "kernel": "k_gemv<1,4> (stand-alone Q4 GEMV 2048->12288, talker gate|up, launch gaps included)",
+        "traffic": read_traffic(traffic_file) if traffic_file else None,
+        "kernel": label or f"Q4 GEMV {K}->{N} (qtts_gemv_device, launch gaps included)",
         "algorithmic_bytes_per_launch": algo_bytes,
         "avg_launch_us": round(avg_s * 1e6, 3),
+        "roofline_us": round(algo_bytes / (HBM_PEAK_GBS * 1e3), 3),
+        "weights_rotated": copies,
     }
+
+
+def gemv_shapes(ctx):
+    """The three isolated Q4 GEMV shapes (gate/up 2048->6144, down 6144->2048,
+    fused q|k|v 2048->4096) and the fused gate|up launch the talker runs
+    (2048->12288)."""
+    out = [gemv_roofline(ctx, K, N) for (K, N) in ((2048, 6144), (6144, 2048), (2048, 4096))]
+    out.append(gemv_roofline(ctx, 2048, 12288, traffic_file="q4_gemv_2048x12288_counters.md",
+                             label="Q4 GEMV 2048->12288 (talker gate|up fused, qtts_gemv_device)"))
+    return out
+
+
+def talker_step_measure(ctx, talker, steps=64, L=256):
+    """A single talker decode step: 28 layers, KV pre-filled to L positions
+    with N(0,1), one N(0,1) embedding per step at positions L, L+1, ...
+    (qtts_forward_with_embedding, host input and output copies of 8 KB and
+    20 KB included), HIP events on the context's stream.  Algorithmic bytes
+    per step: every talker Q4 weight once, the codec head, the norm gammas
+    and the K/V rows read (L+1 positions) and written."""
+    c = talker.cfg
+    shape = (c.layers, L, c.kv_heads, c.head_dim)
+    k = qtts.synth_normal_f32(3, "kv.k", int(np.prod(shape))).reshape(shape)
+    v = qtts.synth_normal_f32(3, "kv.v", int(np.prod(shape))).reshape(shape)
+    kv = talker.new_kv(L + steps + 8)
+    kv.load(k, v, L)
+    emb = qtts.synth_normal_f32(3, "step.emb", c.hidden)
+    talker.forward_with_embedding(emb, kv, L)  # program build, untimed
+    hip = Hip()
+    e0, e1 = hip.event(), hip.event()
+    ctx.synchronize()
+    hip.record(e0, ctx.stream)
+    for i in range(steps):
+        talker.forward_with_embedding(emb, kv, L + 1 + i)
+    hip.record(e1, ctx.stream)
+    s = hip.elapsed_ms(e0, e1) / 1e3 / steps
+    kv.close()
+    per = talker_step_bytes(qtts.TALKER_1P7B, L + (steps + 1) / 2.0)
+    achieved = per / s / 1e9
+    return {"kv_len": [L + 1, L + steps + 1], "steps": steps, "us_per_step": round(s * 1e6, 1),
+            "timing": "HIP events around forward_with_embedding calls (host copies of the embedding and outputs "
+                      "included)",
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(achieved / HBM_PEAK_GBS, 4), "algorithmic_bytes_per_step": per}}
 
 
 def mfma_gemm_roofline(ctx, rows=64, iters=128, copies=32):
@@ -295,6 +352,8 @@ def batch_measure(ctx, talker, pred, streams=16, kv_len=1064, frames=32):
     hip.record(ev1, ctx.stream)
     ctx.synchronize()
     s = hip.elapsed_ms(ev0, ev1) / 1e3
+    for kv in kvs:
+        kv.close()
     weights = frame_bytes(qtts.TALKER_1P7B, qtts.PREDICTOR_1P7B, qtts.NUM_GROUPS, 0)
     kv_bytes = streams * 2 * 4 * qtts.TALKER_1P7B.layers * qtts.TALKER_1P7B.kv_heads * qtts.TALKER_1P7B.head_dim * (
         kv_len + frames / 2.0)
@@ -332,38 +391,95 @@ def read_traffic(name):
     return None
 
 
-def cpu_baseline(tw, pw, gpu_kv, last_hidden, logits, text, pad, frames):
-    """The oracle's frame loop on this host, from the GPU's prefilled cache."""
+def host_info():
+    """CPU model, the C library and the cores this process may run on."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        libc = os.confstr("CS_GNU_LIBC_VERSION")
+    except (ValueError, OSError):
+        libc = "unknown"
+    aff = sorted(os.sched_getaffinity(0))
+    return {"cpu": model, "libc": libc, "affinity_cpus": len(aff),
+            "affinity": f"{aff[0]}-{aff[-1]}" if aff else ""}
+
+
+def cpu_baseline(tw, pw, gpu_kv, start, last_hidden, logits, text, pad, frames):
+    """The oracle's frame loop on this host, from a copy of the GPU's cache at
+    the timed window's first position."""
     from oracle import oracle
 
     ot, op = oracle.Talker(tw), oracle.CodePredictor(pw)
-    okv = ot.new_kv(PROMPT + frames + 8)
+    okv = ot.new_kv(start + frames + 8)
     k, v = gpu_kv.store()
-    okv.load(k, v, k.shape[1])
+    okv.load(np.ascontiguousarray(k[:, :start]), np.ascontiguousarray(v[:, :start]), start)
+    del k, v
     params = qtts.loop_params(frames, temperature=0.8, top_k=50, repetition_penalty=1.05, stop_on_eos=False)
     t0 = time.perf_counter()
-    codes = oracle.generate_codes(ot, op, okv, op.new_kv(), last_hidden, logits, PROMPT, text, pad, params, seed=42)
+    codes = oracle.generate_codes(ot, op, okv, op.new_kv(), last_hidden, logits, start, text, pad, params, seed=42)
     dt = time.perf_counter() - t0
+    threads = oracle.available_parallelism()
+    info = host_info()
     return {
         "value": round(codes.shape[1] / dt, 4),
         "unit": "codes/s",
-        "cores": oracle.available_parallelism(),
+        "cores": threads,
         "kind": "port",
-        "sample": f"{codes.shape[1]} codes of the same loop from the same 64-token prefilled cache "
-                  f"(C oracle, -O3, split-K threads = cores when k*n >= 4e6, predictor single-threaded)",
+        "sample": f"{codes.shape[1]} codes of the same loop at KV {start + 1}..{start + codes.shape[1]} "
+                  f"(C oracle, -O3, no -march; talker GEMVs with k*n >= 4e6 split over {threads} threads as "
+                  f"the reference's gemv_q4 spawns; the predictor single-threaded, as in the reference)",
+        "host": info,
     }
+
+
+def attention_only(ctx, talker, L, steps=8):
+    """Multi-kernel talker steps (QTTS_ENGINE=ops) at a cache of L N(0,1)
+    rows, so that the talker attention runs as its own launches (k_attn, one
+    per layer): the command the attention kernel's counter and trace runs
+    profile.  Prints the per-step time; algorithmic attention bytes per
+    launch are 2 * (L + 1) * kv_heads * head_dim * 4."""
+    os.environ["QTTS_ENGINE"] = "ops"
+    c = talker.cfg
+    shape = (c.layers, L, c.kv_heads, c.head_dim)
+    k = qtts.synth_normal_f32(3, "attn.k", int(np.prod(shape))).reshape(shape)
+    v = qtts.synth_normal_f32(3, "attn.v", int(np.prod(shape))).reshape(shape)
+    kv = talker.new_kv(L + steps + 8)
+    kv.load(k, v, L)
+    del k, v
+    emb = qtts.synth_normal_f32(3, "attn.emb", c.hidden)
+    t0 = time.perf_counter()
+    for i in range(steps):
+        talker.forward_with_embedding(emb, kv, L + i)
+    dt = (time.perf_counter() - t0) / steps
+    per_launch = 2 * (L + steps / 2.0) * c.kv_heads * c.head_dim * 4
+    kv.close()
+    return {"L": L, "steps": steps, "ms_per_step": round(dt * 1e3, 3), "attn_bytes_per_launch": per_launch}
+
+
+# The loop the headline is quoted on: 500 codes after a 64-token prefill,
+# cache lengths 65..564 (mean 314.5).  A shorter --steps run times a window
+# of the same loop centred on that mean.
+CONFIG_CODES = 500
 
 
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=500)
+    ap.add_argument("--steps", type=int, default=CONFIG_CODES)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--cpu-frames", type=int, default=12)
+    ap.add_argument("--cpu-frames", type=int, default=32)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--no-roofline", action="store_true", help="skip the stand-alone GEMV timing")
+    ap.add_argument("--no-roofline", action="store_true", help="skip the stand-alone timings")
     ap.add_argument("--roofline-only", action="store_true",
-                    help="only the GEMV timing and the copy-kernel calibration (for counter runs)")
+                    help="only the GEMV timings and the copy-kernel calibration (for counter runs)")
+    ap.add_argument("--attention-only", type=int, default=0, metavar="L",
+                    help="only multi-kernel talker steps at a cache of L rows (for attention counter runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for {args.gpus}); the per-code loop at batch 1 is a serial "
@@ -372,9 +488,10 @@ def main():
 
     if args.roofline_only:
         ctx = qtts.Context(0)
-        roof = gemv_roofline(ctx)
+        roof = gemv_shapes(ctx)
         copied = copy_calibration(ctx)
-        print(json.dumps({"roofline": roof, "copy_bytes": copied}), flush=True)
+        print(json.dumps({"gemv": roof, "copy_bytes": copied}), flush=True)
+        ctx.close()
         return
 
     t0 = time.time()
@@ -382,13 +499,22 @@ def main():
     pw = qtts.CodePredictorWeights(1, qtts.PREDICTOR_1P7B, talker_hidden=qtts.TALKER_1P7B.hidden)
     log(f"synthetic weights {time.time() - t0:.1f}s")
     ctx = qtts.Context(0)
-    talker, pred = qtts.Talker(ctx, tw), qtts.CodePredictor(ctx, pw)
+    talker = qtts.Talker(ctx, tw)
+    if args.attention_only:
+        out = attention_only(ctx, talker, args.attention_only)
+        print(json.dumps({"attention_only": out}), flush=True)
+        ctx.close()
+        return
+    pred = qtts.CodePredictor(ctx, pw)
     log(f"uploaded {time.time() - t0:.1f}s")
     hidden = tw.cfg.hidden
     prompt = qtts.synth_normal_f32(2, "bench.prompt", PROMPT * hidden)
     text = qtts.synth_normal_f32(2, "bench.text", 8 * hidden, 0.0, 0.1).reshape(8, hidden)
     pad = qtts.synth_normal_f32(2, "bench.pad", hidden, 0.0, 0.1)
-    cap = PROMPT + max(args.steps, args.warmup) + 8
+    # codes before the timed window (untimed, the same loop): the window's
+    # mean cache length is the 500-code loop's, 314.5
+    lead = max(0, int(round(PROMPT + 1 + (CONFIG_CODES - 1) / 2.0 - (args.steps - 1) / 2.0)) - (PROMPT + 1))
+    cap = PROMPT + lead + max(args.steps, args.warmup) + 8
 
     def prefill():
         kv = talker.new_kv(cap)
@@ -400,21 +526,26 @@ def main():
     if args.warmup > 0:
         kv, lh, lg = prefill()
         qtts.generate_codes(talker, pred, kv, pkv, lh, lg, PROMPT, text, pad, params(args.warmup), seed=41)
+        kv.close()
         log(f"warmup {args.warmup} codes done")
     kv, lh, lg = prefill()
+    if lead:
+        qtts.generate_codes(talker, pred, kv, pkv, lh, lg, PROMPT, text, pad, params(lead), seed=40)
+    start = PROMPT + lead  # cache length before the first timed code
+    assert len(kv) == start
     hip = Hip()
     ev0, ev1 = hip.event(), hip.event()
     ctx.synchronize()
     t1 = time.perf_counter()
     hip.record(ev0, ctx.stream)
-    codes = qtts.generate_codes(talker, pred, kv, pkv, lh, lg, PROMPT, text, pad, params(args.steps), seed=42)
+    codes = qtts.generate_codes(talker, pred, kv, pkv, lh, lg, start, text, pad, params(args.steps), seed=42)
     hip.record(ev1, ctx.stream)
     ctx.synchronize()
     dt = time.perf_counter() - t1
     gpu_s = hip.elapsed_ms(ev0, ev1) / 1e3
     assert codes.shape == (16, args.steps), codes.shape
     cps = args.steps / dt
-    log(f"{args.steps} codes in {dt * 1e3:.1f} ms -> {cps:.1f} codes/s")
+    log(f"{args.steps} codes (KV {start + 1}..{start + args.steps}) in {dt * 1e3:.1f} ms -> {cps:.1f} codes/s")
 
     out = {
         "metric": "codes/sec, 1.7B talker+predictor bs=1; Q4 GEMV HBM GB/s vs peak",
@@ -431,22 +562,28 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": "talker (28 layers, hidden 2048, 16/8 heads, SwiGLU 6144, vocab 3072) + code predictor "
-                        "(5 layers, hidden 1024, 15 argmax heads of 2048) per code, Q4 g=32 weights, batch 1",
+                        "(5 layers, hidden 1024, 15 argmax heads of 2048) per code, Q4 g=32 weights, batch 1; "
+                        "500-code loop after a 64-token prefill (KV 65..564)",
             "prompt_tokens": PROMPT,
-            "kv_len": [PROMPT + 1, PROMPT + args.steps],
+            "kv_len": [start + 1, start + args.steps],
+            "kv_len_mean": start + (args.steps + 1) / 2.0,
+            "untimed_lead_codes": lead,
             "sampler": "top-k 50, temperature 0.8, repetition penalty 1.05",
         },
     }
-    out["roofline"] = engine_roofline(args.steps, gpu_s, PROMPT + (args.steps - 1) / 2)
+    out["roofline"] = engine_roofline(args.steps, gpu_s, start + (args.steps - 1) / 2.0)
     log(f"roofline {out['roofline']}")
     if not args.no_roofline:
-        out["gemv"] = gemv_roofline(ctx)
-        log(f"stand-alone gemv {out['gemv']}")
+        out["gemv"] = gemv_shapes(ctx)
+        for g in out["gemv"]:
+            log(f"stand-alone gemv {g}")
+        out["talker_step"] = talker_step_measure(ctx, talker)
+        log(f"talker step {out['talker_step']}")
         # the 64-token prompt prefill (matrix-core path), HIP events
         ctx.synchronize()
         hip.record(ev0, ctx.stream)
         for _ in range(5):
-            prefill()
+            prefill()[0].close()
         hip.record(ev1, ctx.stream)
         ctx.synchronize()
         pf_s = hip.elapsed_ms(ev0, ev1) / 1e3 / 5
@@ -454,16 +591,15 @@ def main():
                           "timing": "HIP events around 5 prefill_talker_raw calls, host copies included",
                           "gemm": mfma_gemm_roofline(ctx)}
         log(f"prefill {out['prefill']}")
-        out["decoder"] = decoder_measure(ctx, args.steps, cpu_frames=0 if args.no_cpu else 2)
+        out["decoder"] = decoder_measure(ctx, CONFIG_CODES, cpu_frames=0 if args.no_cpu else 2)
         log(f"decoder {out['decoder']}")
         out["batch"] = batch_measure(ctx, talker, pred)
         log(f"batch {out['batch']}")
     if not args.no_cpu:
-        lh_np, lg_np = lh, lg
-        kv_cpu, lh_np, lg_np = prefill()
-        out["cpu_baseline"] = cpu_baseline(tw, pw, kv_cpu, lh_np, lg_np, text, pad, args.cpu_frames)
+        out["cpu_baseline"] = cpu_baseline(tw, pw, kv, start, lh, lg, text, pad, args.cpu_frames)
         log(f"cpu baseline {out['cpu_baseline']}")
     print(json.dumps(out), flush=True)
+    ctx.close()
 
 
 if __name__ == "__main__":

@@ -236,7 +236,12 @@ qtts_status qtts_sample_token(qtts_ctx *ctx, const float *logits, int32_t vocab,
  * the device from the prefill outputs (last_hidden, logits) at `position`.
  * trailing_text is [trailing_len][hidden] (build_trailing_text, 314-326),
  * tts_pad_embed is [hidden].  codes is [16][max_codes] (group-major, as
- * all_codes); *n_frames receives the number of frames produced. */
+ * all_codes); *n_frames receives the number of frames produced.
+ * Failures: QTTS_ERANGE before anything runs when position + max_codes passes
+ * the RoPE table or the cache cannot take max_codes more rows; QTTS_ENAN when
+ * a NaN reaches the code-0 sampler or a predictor argmax (where the reference
+ * panics).  After a failure *n_frames is 0 and both caches keep the length
+ * they had (rows past it may have been written). */
 qtts_status qtts_generate_codes(qtts_talker *t, qtts_predictor *p, qtts_kv *talker_kv, qtts_kv *predictor_kv,
                                 const float *last_hidden, const float *logits, int32_t position,
                                 const float *trailing_text, int32_t trailing_len, const float *tts_pad_embed,
@@ -251,7 +256,9 @@ qtts_status qtts_generate_codes(qtts_talker *t, qtts_predictor *p, qtts_kv *talk
  * codes + b*16*max_codes ([16][max_codes] as above) and its frame count to
  * n_frames[b].  The predictor caches are internal.  Every product runs on the
  * matrix cores with one row per stream.  QTTS_ESHAPE when a weight cannot
- * use them (a scale above 8188 in magnitude); at most 64 streams. */
+ * use them (a scale above 8188 in magnitude); at most 64 streams.  Failures
+ * as for qtts_generate_codes: QTTS_ENAN when any stream meets a NaN, and then
+ * no stream's n_frames or cache length moves. */
 qtts_status qtts_generate_codes_batch(qtts_talker *t, qtts_predictor *p, int32_t batch, qtts_kv *const *talker_kvs,
                                       const float *last_hidden, const float *logits, const int32_t *positions,
                                       const float *trailing_text, int32_t trailing_len, const float *tts_pad_embed,

@@ -72,6 +72,16 @@ def load():
         "qor_decode_to_audio": ([C.POINTER(qtts.DecoderView), vp, i32, i32, vp, C.c_int64, C.POINTER(C.c_int64), i32],
                                 i32),
         "qor_argmax": ([vp, i32, C.POINTER(u32)], i32),
+        "qor_dec_causal_conv": ([vp, i32, C.POINTER(qtts.ConvView), vp, i32], None),
+        "qor_dec_transposed_conv": ([vp, i32, C.POINTER(qtts.ConvView), vp, i32], i32),
+        "qor_dec_depthwise_conv": ([vp, i32, C.POINTER(qtts.ConvView), vp, i32], None),
+        "qor_dec_snake": ([vp, i32, i32, vp, vp, vp, i32], None),
+        "qor_dec_gelu": ([C.c_float], C.c_float),
+        "qor_dec_layer_norm_cf": ([vp, vp, vp, i32, i32, C.c_float, vp], None),
+        "qor_dec_rms_norm": ([vp, vp, C.c_float, i32, vp], None),
+        "qor_dec_rope": ([vp, i32, i32, i32, vp, vp, i32], None),
+        "qor_dec_window_attention": ([vp, vp, vp, i32, i32, i32, i32, vp], None),
+        "qor_dec_codebook_lookup": ([C.POINTER(qtts.DecoderView), vp, i32, i32, vp], None),
         "qor_sample_token": ([vp, i32, C.POINTER(qtts.SamplerParams), vp, i32, C.POINTER(C.c_uint64),
                               C.POINTER(u32)], i32),
         "qor_generate_codes": ([vp, vp, vp, vp, vp, vp, i32, vp, i32, vp, C.POINTER(qtts.LoopParams), C.c_uint64,
@@ -326,3 +336,90 @@ def decode_to_audio(w, codes, nthreads: int = 0) -> np.ndarray:
     _check(load().qor_decode_to_audio(C.byref(view), _p(codes), frames, frames, _p(out), out.size, C.byref(n),
                                       nthreads))
     return out[: n.value]
+
+
+# --- decoder primitives (test hooks of qtts_oracle_decoder.c) ---------------
+class dec:
+    """The decoder oracle's primitives one by one, for the CPU checks that pin
+    them.  Signals are channel-first [C][L] float32 arrays."""
+
+    @staticmethod
+    def _cv(weight, bias, cin, cout, k, stride=1, pad=0, dil=1):
+        w, b = f32(weight), f32(bias)
+        return qtts.ConvView(w.ctypes.data, b.ctypes.data, cin, cout, k, stride, pad, dil), (w, b)
+
+    @staticmethod
+    def causal_conv(x, w, b, dilation=1, nthreads=0):
+        cout, cin, k = w.shape
+        x = f32(x)
+        view, keep = dec._cv(w, b, cin, cout, k, 1, 0, dilation)
+        out = np.empty((cout, x.shape[1]), dtype=np.float32)
+        load().qor_dec_causal_conv(_p(x), x.shape[1], C.byref(view), _p(out), nthreads)
+        return out
+
+    @staticmethod
+    def transposed_conv(x, w, b, stride, padding=0, nthreads=0):
+        cin, cout, k = w.shape
+        x = f32(x)
+        L = x.shape[1]
+        view, keep = dec._cv(w, b, cin, cout, k, stride, padding, 1)
+        out = np.empty(cout * ((L - 1) * stride - 2 * padding + k), dtype=np.float32)
+        n = load().qor_dec_transposed_conv(_p(x), L, C.byref(view), _p(out), nthreads)
+        return out[: cout * n].reshape(cout, n)
+
+    @staticmethod
+    def depthwise_conv(x, w, b, padding=0, nthreads=0):
+        c, k = w.shape
+        x = f32(x)
+        view, keep = dec._cv(w, b, c, c, k, 1, padding, 1)
+        out = np.empty_like(x)
+        load().qor_dec_depthwise_conv(_p(x), x.shape[1], C.byref(view), _p(out), nthreads)
+        return out
+
+    @staticmethod
+    def snake(x, alpha, beta, nthreads=0):
+        x, a, b = f32(x), f32(alpha), f32(beta)
+        out = np.empty_like(x)
+        load().qor_dec_snake(_p(x), x.shape[0], x.shape[1], _p(a), _p(b), _p(out), nthreads)
+        return out
+
+    @staticmethod
+    def gelu(x):
+        return float(load().qor_dec_gelu(x))
+
+    @staticmethod
+    def layer_norm_cf(x, g, b, eps=1e-5):
+        x = f32(x)
+        out = np.empty_like(x)
+        load().qor_dec_layer_norm_cf(_p(x), _p(f32(g)), _p(f32(b)), x.shape[0], x.shape[1], eps, _p(out))
+        return out
+
+    @staticmethod
+    def rms_norm(x, g, eps=1e-5):
+        x = f32(x)
+        out = np.empty_like(x)
+        load().qor_dec_rms_norm(_p(x), _p(f32(g)), eps, x.size, _p(out))
+        return out
+
+    @staticmethod
+    def rope(x, heads, hd, pos, cos_t, sin_t):
+        d = f32(x).copy()
+        c = f32(cos_t)
+        load().qor_dec_rope(_p(d), heads, hd, pos, _p(c), _p(f32(sin_t)), c.size // (hd // 2))
+        return d
+
+    @staticmethod
+    def window_attention(q, k, v, heads, hd, window):
+        q, k, v = f32(q), f32(k), f32(v)
+        out = np.empty_like(q)
+        load().qor_dec_window_attention(_p(q), _p(k), _p(v), q.shape[0], heads, hd, window, _p(out))
+        return out
+
+    @staticmethod
+    def codebook_lookup(w, codes):
+        codes = np.ascontiguousarray(codes, dtype=np.uint32)
+        T = codes.shape[1]
+        view = w.view()
+        out = np.empty((w.cfg.vq_dim, T), dtype=np.float32)
+        load().qor_dec_codebook_lookup(C.byref(view), _p(codes), T, T, _p(out))
+        return out

@@ -116,6 +116,22 @@ int64_t qor_decoder_num_samples(const qtts_decoder_view *w, int32_t frames);
  * for a code past the codebook or too small an output buffer. */
 int32_t qor_decode_to_audio(const qtts_decoder_view *w, const uint32_t *codes, int32_t frames, int32_t ld,
                             float *audio, int64_t capacity, int64_t *n_samples, int32_t nthreads);
+/* Test hooks: the decoder's primitives (qtts_oracle_decoder.c), for CPU
+ * checks against closed forms and float64 brute force. */
+void qor_dec_causal_conv(const float *in, int32_t len, const qtts_conv_view *w, float *out, int32_t nt);
+int32_t qor_dec_transposed_conv(const float *in, int32_t len, const qtts_conv_view *w, float *out, int32_t nt);
+void qor_dec_depthwise_conv(const float *in, int32_t len, const qtts_conv_view *w, float *out, int32_t nt);
+void qor_dec_snake(const float *in, int32_t ch, int32_t len, const float *alpha, const float *beta, float *out,
+                   int32_t nt);
+float qor_dec_gelu(float x);
+void qor_dec_layer_norm_cf(const float *in, const float *g, const float *b, int32_t ch, int32_t len, float eps,
+                           float *out);
+void qor_dec_rms_norm(const float *x, const float *gamma, float eps, int32_t n, float *out);
+void qor_dec_rope(float *data, int32_t heads, int32_t hd, int32_t pos, const float *cs, const float *sn,
+                  int32_t rows);
+void qor_dec_window_attention(const float *q, const float *k, const float *v, int32_t T, int32_t heads, int32_t hd,
+                              int32_t window, float *out);
+void qor_dec_codebook_lookup(const qtts_decoder_view *w, const uint32_t *codes, int32_t T, int32_t ld, float *out);
 
 #ifdef __cplusplus
 }

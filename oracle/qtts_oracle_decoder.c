@@ -258,6 +258,32 @@ static float *codebook_lookup(const qtts_decoder_view *w, const uint32_t *codes,
     return out;
 }
 
+/* Causal sliding-window attention of row t (src/decoder.rs:262-300): each
+ * head attends to positions max(0, t+1-window) .. t; scores q.k * scale in
+ * dimension order, softmax_raw, then sum_s p_s v_s in position order.  q, k,
+ * v are [T][heads*hd]; sc holds window+1 floats; ao receives [heads*hd]. */
+static void window_attention_row(const float *q, const float *k, const float *v, int32_t t, int32_t heads,
+                                 int32_t hd, int32_t window, float scale, float *sc, float *ao) {
+    const int32_t ad = heads * hd;
+    const int32_t start = t + 1 > window ? t + 1 - window : 0;
+    const int32_t n = t + 1 - start;
+    for (int32_t i = 0; i < ad; i++) ao[i] = 0.0f;
+    for (int32_t h = 0; h < heads; h++) {
+        const float *qh = q + (size_t)t * ad + (size_t)h * hd;
+        for (int32_t s = 0; s < n; s++) {
+            const float *kh = k + (size_t)(start + s) * ad + (size_t)h * hd;
+            float dot = 0.0f;
+            for (int32_t d = 0; d < hd; d++) dot += qh[d] * kh[d];
+            sc[s] = dot * scale;
+        }
+        qor_softmax_raw(sc, n);
+        for (int32_t s = 0; s < n; s++) {
+            const float *vh = v + (size_t)(start + s) * ad + (size_t)h * hd;
+            for (int32_t d = 0; d < hd; d++) ao[(size_t)h * hd + d] += sc[s] * vh[d];
+        }
+    }
+}
+
 /* decoder_transformer, src/decoder.rs:195-330: [latent][T] -> [latent][T]. */
 static float *decoder_transformer(const qtts_decoder_view *w, const float *x_ch, int32_t T) {
     const int32_t hid = w->hidden_size, ad = w->num_heads * w->head_dim, in_dim = w->pre_conv.out_channels;
@@ -290,23 +316,7 @@ static float *decoder_transformer(const qtts_decoder_view *w, const float *x_ch,
             rope_split_half(k + (size_t)t * ad, w->num_heads, hd, t, w->rope_cos, w->rope_sin, w->rope_rows);
         }
         for (int32_t t = 0; t < T; t++) {
-            const int32_t start = t + 1 > w->sliding_window ? t + 1 - w->sliding_window : 0;
-            const int32_t n = t + 1 - start;
-            for (int32_t i = 0; i < ad; i++) ao[i] = 0.0f;
-            for (int32_t h = 0; h < w->num_heads; h++) {
-                const float *qh = q + (size_t)t * ad + (size_t)h * hd;
-                for (int32_t s = 0; s < n; s++) {
-                    const float *kh = k + (size_t)(start + s) * ad + (size_t)h * hd;
-                    float dot = 0.0f;
-                    for (int32_t d = 0; d < hd; d++) dot += qh[d] * kh[d];
-                    sc[s] = dot * scale;
-                }
-                qor_softmax_raw(sc, n);
-                for (int32_t s = 0; s < n; s++) {
-                    const float *vh = v + (size_t)(start + s) * ad + (size_t)h * hd;
-                    for (int32_t d = 0; d < hd; d++) ao[(size_t)h * hd + d] += sc[s] * vh[d];
-                }
-            }
+            window_attention_row(q, k, v, t, w->num_heads, hd, w->sliding_window, scale, sc, ao);
             f32_gemv(ao, L->o_proj, ad, hid, NULL, tmp);
             for (int32_t j = 0; j < hid; j++) x[(size_t)t * hid + j] += tmp[j] * L->attn_scale[j];
         }
@@ -447,4 +457,65 @@ int32_t qor_decode_to_audio(const qtts_decoder_view *w, const uint32_t *codes, i
     free(o);
     *n_samples = n;
     return QTTS_OK;
+}
+
+/* ---- Test hooks ----------------------------------------------------------
+ * The decoder's primitives above, exported so that CPU tests can check each
+ * against a closed form or a float64 brute force.  Layouts are the ones the
+ * primitives use: channel-first [ch][len] signals, token-major [T][D] rows. */
+void qor_dec_causal_conv(const float *in, int32_t len, const qtts_conv_view *w, float *out, int32_t nt) {
+    float *o = causal_conv(in, len, w, nt);
+    memcpy(out, o, (size_t)w->out_channels * len * sizeof(float));
+    free(o);
+}
+
+int32_t qor_dec_transposed_conv(const float *in, int32_t len, const qtts_conv_view *w, float *out, int32_t nt) {
+    int32_t ol = 0;
+    float *o = transposed_conv_cropped(in, len, w, &ol, nt);
+    memcpy(out, o, (size_t)w->out_channels * ol * sizeof(float));
+    free(o);
+    return ol;
+}
+
+void qor_dec_depthwise_conv(const float *in, int32_t len, const qtts_conv_view *w, float *out, int32_t nt) {
+    conv_job j = {2, in, w, NULL, NULL, len, len, 0, 0, out};
+    run_channels(j, w->out_channels, nt);
+}
+
+void qor_dec_snake(const float *in, int32_t ch, int32_t len, const float *alpha, const float *beta, float *out,
+                   int32_t nt) {
+    float *o = snake(in, ch, len, alpha, beta, nt);
+    memcpy(out, o, (size_t)ch * len * sizeof(float));
+    free(o);
+}
+
+float qor_dec_gelu(float x) { return gelu(x); }
+
+void qor_dec_layer_norm_cf(const float *in, const float *g, const float *b, int32_t ch, int32_t len, float eps,
+                           float *out) {
+    layer_norm_cf(in, g, b, ch, len, eps, out);
+}
+
+void qor_dec_rms_norm(const float *x, const float *gamma, float eps, int32_t n, float *out) {
+    rms_norm_f32(x, gamma, eps, n, out);
+}
+
+void qor_dec_rope(float *data, int32_t heads, int32_t hd, int32_t pos, const float *cs, const float *sn,
+                  int32_t rows) {
+    rope_split_half(data, heads, hd, pos, cs, sn, rows);
+}
+
+void qor_dec_window_attention(const float *q, const float *k, const float *v, int32_t T, int32_t heads, int32_t hd,
+                              int32_t window, float *out) {
+    float *sc = (float *)dcalloc((size_t)(window > 0 ? window : 1) + (size_t)T, sizeof(float));
+    const float scale = 1.0f / sqrtf((float)hd);
+    for (int32_t t = 0; t < T; t++)
+        window_attention_row(q, k, v, t, heads, hd, window, scale, sc, out + (size_t)t * heads * hd);
+    free(sc);
+}
+
+void qor_dec_codebook_lookup(const qtts_decoder_view *w, const uint32_t *codes, int32_t T, int32_t ld, float *out) {
+    float *o = codebook_lookup(w, codes, T, ld);
+    memcpy(out, o, (size_t)w->vq_dim * T * sizeof(float));
+    free(o);
 }

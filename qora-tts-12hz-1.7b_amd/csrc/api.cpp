@@ -1127,8 +1127,10 @@ bool eng_talker_fits(int cap) { return (cap + kEngMaxSplit - 1) / kEngMaxSplit <
 // Passes 2.. of generate_acoustic_codes (src/code_predictor.rs:218-273)
 // project the previous code's embedding, emb[g-1][code], to the predictor's
 // width.  That projection depends only on the code, so it is applied ahead of
-// time to every code of emb[0 .. groups-2] by the same GEMV the step would
-// run (in_proj(row) + bias), and a pass reads its input row by code.
+// time to every code of emb[0 .. groups-2] (in_proj(row) + bias), and a pass
+// reads its input row by code.  The table is made by the matrix-core GEMM
+// when the weight allows it (the same f32 products, summed in another order,
+// so a row may differ from the step's GEMV by rounding), else by the GEMV.
 // QTTS_PREDICTOR_TABLE=0 keeps the projection as a step.
 qtts_status make_predictor_tables(qtts_predictor *p) {
     if (p->tab_state != 0) return QTTS_OK;
@@ -2351,15 +2353,19 @@ qtts_status qtts_generate_codes(qtts_talker *t, qtts_predictor *p, qtts_kv *talk
         }
         if (fin.done) break;
     }
+    // No replay may still be in flight when the executable graph goes away.
+    if (rc != QTTS_OK) (void)hipStreamSynchronize(c->stream);
     if (exec) (void)hipGraphExecDestroy(exec);
     if (graph) (void)hipGraphDestroy(graph);
     QTTS_TRY(rc);
     QTTS_TRY(sync(c));
+    // A failed loop (NaN logits: the reference panics) leaves the caches'
+    // lengths and *n_frames as they were, as the frame engine does.
+    if (fin.status != 0) return fail(c, (qtts_status)fin.status, "generate_codes: NaN logits (the reference panics)");
     HIP_TRY(c, hipMemcpy(codes, t->codes, ncodes * sizeof(uint32_t), hipMemcpyDeviceToHost));
     *n_frames = fin.frame;
     talker_kv->len += fin.frame;
     if (!talker_only && fin.frame > 0) predictor_kv->len = p->groups + 1;
-    if (fin.status != 0) return fail(c, (qtts_status)fin.status, "NaN logits during generation");
     return QTTS_OK;
 }
 
@@ -3333,7 +3339,9 @@ qtts_status qtts_generate_codes_batch(qtts_talker *t, qtts_predictor *p, int32_t
             rc = enqueue_frame_batch();
         }
     }
+    // No replay may still be in flight when the executable graph goes away.
     if (rc == QTTS_OK) rc = sync(c);
+    else (void)hipStreamSynchronize(c->stream);
     if (exec) (void)hipGraphExecDestroy(exec);
     if (graph) (void)hipGraphDestroy(graph);
     QTTS_TRY(rc);

@@ -18,6 +18,7 @@ from __future__ import annotations
 import ctypes as C
 import dataclasses
 import os
+import weakref
 from typing import List, Optional, Sequence
 
 import numpy as np
@@ -37,6 +38,29 @@ class QttsError(RuntimeError):
         self.status = status
         name = STATUS_NAMES[status] if 0 <= status < len(STATUS_NAMES) else str(status)
         super().__init__(f"qtts {name}: {message}")
+
+
+class _DeviceObject:
+    """A handle owned by a Context: close() frees it once (the context's
+    close() calls it for every object still open)."""
+
+    _free_fn = ""
+
+    def _register(self, ctx: "Context", h):
+        self.ctx, self.h = ctx, h
+        ctx._children.add(self)
+
+    def close(self):
+        h = getattr(self, "h", None)
+        if h:
+            self.h = None
+            getattr(self.ctx.lib, self._free_fn)(h)
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
 
 
 # ---------------------------------------------------------------------------
@@ -640,15 +664,17 @@ class DecoderWeights:
         return u.astype(np.uint32).reshape(self.cfg.num_rest + 1, frames)
 
 
-class SpeechDecoder:
+class SpeechDecoder(_DeviceObject):
     """SpeechDecoderWeights in HBM with decode_to_audio."""
 
+    _free_fn = "qtts_decoder_free"
+
     def __init__(self, ctx: "Context", w):
-        self.ctx, self.cfg = ctx, getattr(w, "cfg", None)
+        self.cfg = getattr(w, "cfg", None)
         h = C.c_void_p()
         self._view = w.view()
         ctx.check(ctx.lib.qtts_decoder_upload(ctx.h, C.byref(self._view), C.byref(h)))
-        self.h = h
+        self._register(ctx, h)
 
     def num_samples(self, frames: int) -> int:
         return int(self.ctx.lib.qtts_decoder_num_samples(self.h, frames))
@@ -668,17 +694,6 @@ class SpeechDecoder:
         self.ctx.check(self.ctx.lib.qtts_decode_to_audio_device(self.h, C.c_void_p(d_codes), frames, ld,
                                                                 C.c_void_p(d_audio), capacity, C.byref(n)))
         return n.value
-
-    def close(self):
-        if getattr(self, "h", None):
-            self.ctx.lib.qtts_decoder_free(self.h)
-            self.h = None
-
-    def __del__(self):
-        try:
-            self.close()
-        except Exception:
-            pass
 
 
 # ---------------------------------------------------------------------------
@@ -746,6 +761,7 @@ class Context:
 
     def __init__(self, device: int = 0):
         self.lib = load_library()
+        self._children = weakref.WeakSet()  # device objects made from this context
         h = C.c_void_p()
         st = self.lib.qtts_ctx_create(device, C.byref(h))
         if st != QTTS_OK:
@@ -764,7 +780,16 @@ class Context:
         self.check(self.lib.qtts_ctx_synchronize(self.h))
 
     def close(self):
-        if self.h:
+        """Frees every object made from this context that is still open, then
+        the context: all device memory and the stream are released here, while
+        the HIP runtime is up, rather than by finalizers at interpreter exit."""
+        if getattr(self, "h", None):
+            try:
+                self.synchronize()
+            except QttsError:
+                pass  # the objects are freed all the same
+            for obj in list(self._children):
+                obj.close()
             self.lib.qtts_ctx_destroy(self.h)
             self.h = None
 
@@ -788,15 +813,17 @@ class Context:
         return int(tok.value), int(state.value)
 
 
-class DeviceQ4:
+class DeviceQ4(_DeviceObject):
     """A Weight::Q4 resident in HBM with gemv/gemm/embed_lookup (src/gemv.rs:148-176)."""
 
+    _free_fn = "qtts_q4_free"
+
     def __init__(self, ctx: Context, w: Q4Weight):
-        self.ctx, self.k, self.n = ctx, w.k, w.n
+        self.k, self.n = w.k, w.n
         h = C.c_void_p()
         v = w.view()
         ctx.check(ctx.lib.qtts_q4_upload(ctx.h, C.byref(v), C.byref(h)))
-        self.h = h
+        self._register(ctx, h)
 
     def gemv(self, x) -> np.ndarray:
         x = _f32(x, self.k)
@@ -826,22 +853,17 @@ class DeviceQ4:
     def memory_bytes(self) -> int:
         return int(self.ctx.lib.qtts_q4_bytes(self.h))
 
-    def __del__(self):
-        try:
-            self.ctx.lib.qtts_q4_free(self.h)
-        except Exception:
-            pass
 
-
-class KvCache:
+class KvCache(_DeviceObject):
     """RawKvCache (src/gemv.rs:75-86) in HBM, fixed capacity."""
 
+    _free_fn = "qtts_kv_free"
+
     def __init__(self, ctx: Context, num_layers: int, num_kv_heads: int, head_dim: int, capacity: int):
-        self.ctx = ctx
         self.shape = (num_layers, num_kv_heads, head_dim)
         h = C.c_void_p()
         ctx.check(ctx.lib.qtts_kv_create(ctx.h, num_layers, num_kv_heads, head_dim, capacity, C.byref(h)))
-        self.h = h
+        self._register(ctx, h)
 
     def __len__(self) -> int:
         return int(self.ctx.lib.qtts_kv_len(self.h))
@@ -862,22 +884,18 @@ class KvCache:
         self.ctx.check(self.ctx.lib.qtts_kv_store(self.h, _ptr(k), _ptr(v)))
         return k, v
 
-    def __del__(self):
-        try:
-            self.ctx.lib.qtts_kv_free(self.h)
-        except Exception:
-            pass
 
-
-class Talker:
+class Talker(_DeviceObject):
     """TalkerWeights in HBM with the reference's talker functions."""
 
+    _free_fn = "qtts_talker_free"
+
     def __init__(self, ctx: Context, w: TalkerWeights):
-        self.ctx, self.cfg = ctx, w.cfg
+        self.cfg = w.cfg
         h = C.c_void_p()
         v = w.view()
         ctx.check(ctx.lib.qtts_talker_upload(ctx.h, C.byref(v), C.byref(h)))
-        self.h = h
+        self._register(ctx, h)
 
     def new_kv(self, capacity: int) -> KvCache:
         c = self.cfg
@@ -910,23 +928,19 @@ class Talker:
         self.ctx.check(self.ctx.lib.qtts_embed_codec_token(self.h, int(token), _ptr(out)))
         return out
 
-    def __del__(self):
-        try:
-            self.ctx.lib.qtts_talker_free(self.h)
-        except Exception:
-            pass
 
-
-class CodePredictor:
+class CodePredictor(_DeviceObject):
     """CodePredictorWeights in HBM with generate_acoustic_codes."""
 
+    _free_fn = "qtts_predictor_free"
+
     def __init__(self, ctx: Context, w: CodePredictorWeights):
-        self.ctx, self.cfg, self.num_groups = ctx, w.cfg, w.num_groups
+        self.cfg, self.num_groups = w.cfg, w.num_groups
         self.talker_hidden = w.talker_hidden
         h = C.c_void_p()
         v = w.view()
         ctx.check(ctx.lib.qtts_predictor_upload(ctx.h, C.byref(v), C.byref(h)))
-        self.h = h
+        self._register(ctx, h)
 
     def new_kv(self, capacity: int = 16) -> KvCache:
         c = self.cfg
@@ -946,12 +960,6 @@ class CodePredictor:
         out = np.empty(self.talker_hidden, dtype=np.float32)
         self.ctx.check(self.ctx.lib.qtts_get_acoustic_embeddings_sum(self.h, _ptr(cs), _ptr(out)))
         return out
-
-    def __del__(self):
-        try:
-            self.ctx.lib.qtts_predictor_free(self.h)
-        except Exception:
-            pass
 
 
 def loop_params(max_codes: int, temperature: float = 0.8, top_k: int = 50, repetition_penalty: float = 1.05,

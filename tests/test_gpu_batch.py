@@ -119,3 +119,21 @@ def test_batch_full_model(ctx):
         ref = oracle.generate_codes(ot, op, okvs[b], op.new_kv(), lh[b], lg[b], pos[b], text[b], pad, params,
                                     seed=31 + b)
         assert np.array_equal(got[b], ref), (b, np.argwhere(got[b] != ref)[:5])
+
+
+def test_batch_without_predictor_tables(ctx, tiny, monkeypatch):
+    """QTTS_PREDICTOR_TABLE=0 (read when a predictor first runs): passes
+    2-15 of the batched loop gather the previous code's embedding and run the
+    input projection as a GEMM of their own instead of reading the per-code
+    table.  Codes still match the oracle's single-stream loops."""
+    tw, pw, t, _, ot, op = tiny
+    monkeypatch.setenv("QTTS_PREDICTOR_TABLE", "0")
+    p_off = qtts.CodePredictor(ctx, pw)
+    B, frames = 3, 8
+    kvs, okvs, lh, lg, pos, text, pad = _streams(tw, t, ot, B, 66, [9, 12, 7], 32)
+    params = qtts.loop_params(frames, temperature=0.8, top_k=50, repetition_penalty=1.05, stop_on_eos=False)
+    got = qtts.generate_codes_batch(t, p_off, kvs, lh, lg, pos, text, pad, params, [41, 42, 43])
+    for b in range(B):
+        ref = oracle.generate_codes(ot, op, okvs[b], op.new_kv(), lh[b], lg[b], pos[b], text[b], pad, params,
+                                    seed=41 + b)
+        assert np.array_equal(got[b], ref), (b, np.argwhere(got[b] != ref)[:5])

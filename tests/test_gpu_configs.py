@@ -1,0 +1,205 @@
+"""GPU parity at the full 1.7B shapes of the loop workloads, against the
+oracle on the same seeded random-init weights and inputs:
+
+- the talker-only loop (the legacy feedback, codec_embedding[code0] as the
+  next input, src/generate.rs:225-227): a 64-token prefill, then 64 greedy
+  and 64 sampled steps (top-k 50, T 0.8, penalty 1.05); and 64 sampled steps
+  from a cache loaded to 500 N(0,1) rows, through position 564;
+- the talker + code predictor loop (src/generate_new.rs:242-300) after a
+  64-token prefill: 64 greedy and 64 sampled frames;
+- 16 batched streams (qtts_generate_codes_batch) in 2064-row caches loaded
+  to 2000 N(0,1) rows: 3 sampled frames, every stream's codes, frame count,
+  cache length and appended cache rows.
+
+Bars: codes identical; hidden states and cache rows within 1e-3 relative.
+The oracle loops run in worker threads (ctypes releases the GIL), the
+predictor being single-threaded as in the reference.
+"""
+import time
+from concurrent.futures import ThreadPoolExecutor
+
+import numpy as np
+import pytest
+
+import qtts
+from oracle import oracle
+from shapes import FULL_PREDICTOR, FULL_TALKER, rel_err
+
+pytestmark = pytest.mark.gpu
+
+REL_TOL = 1e-3
+PROMPT = 64
+
+
+@pytest.fixture(scope="module")
+def full(ctx):
+    t0 = time.time()
+    tw = qtts.TalkerWeights(1, FULL_TALKER)
+    pw = qtts.CodePredictorWeights(1, FULL_PREDICTOR, talker_hidden=FULL_TALKER.hidden)
+    objs = (tw, pw, qtts.Talker(ctx, tw), qtts.CodePredictor(ctx, pw), oracle.Talker(tw), oracle.CodePredictor(pw))
+    print(f"1.7B weights synthesised and uploaded in {time.time() - t0:.1f}s", flush=True)
+    return objs
+
+
+@pytest.fixture(scope="module")
+def prompt64(full):
+    """A 64-token N(0,1) prompt prefilled on both sides; returns each side's
+    cache contents and the oracle's last hidden state and logits (the loop
+    inputs both sides start from)."""
+    tw, _, t, _, ot, _ = full
+    H = tw.cfg.hidden
+    x = qtts.synth_normal_f32(40, "cfg3.prompt", PROMPT * H)
+    kv, okv = t.new_kv(PROMPT + 8), ot.new_kv(PROMPT + 8)
+    lh = t.prefill_talker_raw(x, PROMPT, kv)
+    olh = ot.prefill_talker_raw(x, PROMPT, okv)
+    e = rel_err(lh, olh)
+    print(f"64-token prefill: last hidden rel err {e:.2e}", flush=True)
+    assert e < REL_TOL
+    gk, gv = kv.store()
+    rk, rv = okv.store()
+    assert rel_err(gk, rk) < REL_TOL and rel_err(gv, rv) < REL_TOL
+    return {"gpu": (gk, gv), "oracle": (rk, rv), "last_hidden": olh, "logits": ot.apply_codec_head(olh)}
+
+
+def _caches(t, ot, cap, gpu_kv, oracle_kv, length):
+    kv, okv = t.new_kv(cap), ot.new_kv(cap)
+    kv.load(gpu_kv[0], gpu_kv[1], length)
+    okv.load(oracle_kv[0], oracle_kv[1], length)
+    return kv, okv
+
+
+def _check_appended(kv, okv, start, count):
+    """The rows the loop appended to both caches agree."""
+    (gk, gv), (rk, rv) = kv.store(), okv.store()
+    assert gk.shape == rk.shape
+    sl = slice(start, start + count)
+    assert rel_err(gk[:, sl], rk[:, sl]) < REL_TOL and rel_err(gv[:, sl], rv[:, sl]) < REL_TOL
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("greedy", [True, False], ids=["greedy", "sampled"])
+def test_config3_talker_only_after_prefill(full, prompt64, greedy):
+    """64 talker-only steps after the 64-token prefill (KV 65 -> 128)."""
+    tw, _, t, _, ot, _ = full
+    steps = 64
+    params = qtts.loop_params(steps, temperature=0.8, top_k=50, repetition_penalty=1.05, greedy=greedy,
+                              stop_on_eos=False, talker_only=True)
+    kv, okv = _caches(t, ot, PROMPT + steps + 8, prompt64["gpu"], prompt64["oracle"], PROMPT)
+    lh, lg = prompt64["last_hidden"], prompt64["logits"]
+    t0 = time.time()
+    got = qtts.generate_codes(t, None, kv, None, lh, lg, PROMPT, None, None, params, seed=2024)
+    ref = oracle.generate_codes(ot, None, okv, None, lh, lg, PROMPT, None, None, params, seed=2024)
+    print(f"talker-only {steps} steps ({'greedy' if greedy else 'sampled'}): oracle+gpu {time.time() - t0:.1f}s",
+          flush=True)
+    assert got.shape == ref.shape == (16, steps)
+    assert np.array_equal(got[0], ref[0]), np.argwhere(got[0] != ref[0])[:5]
+    assert len(kv) == len(okv) == PROMPT + steps
+    _check_appended(kv, okv, PROMPT, steps)
+
+
+@pytest.mark.timeout(600)
+def test_config3_talker_only_to_564(full):
+    """64 sampled talker-only steps from a cache loaded to 500 N(0,1) rows:
+    the last steps of the 500-step loop, through KV length 564."""
+    tw, _, t, _, ot, _ = full
+    c = tw.cfg
+    L, steps = 500, 64
+    shape = (c.layers, L, c.kv_heads, c.head_dim)
+    k = qtts.synth_normal_f32(41, "cfg3.k", int(np.prod(shape))).reshape(shape)
+    v = qtts.synth_normal_f32(41, "cfg3.v", int(np.prod(shape))).reshape(shape)
+    kv, okv = _caches(t, ot, L + steps, (k, v), (k, v), L)
+    del k, v
+    lh = qtts.synth_normal_f32(41, "cfg3.h", c.hidden)
+    lg = ot.apply_codec_head(lh)
+    params = qtts.loop_params(steps, temperature=0.8, top_k=50, repetition_penalty=1.05, stop_on_eos=False,
+                              talker_only=True)
+    got = qtts.generate_codes(t, None, kv, None, lh, lg, L, None, None, params, seed=77)
+    ref = oracle.generate_codes(ot, None, okv, None, lh, lg, L, None, None, params, seed=77)
+    assert got.shape == ref.shape == (16, steps)
+    assert np.array_equal(got[0], ref[0]), np.argwhere(got[0] != ref[0])[:5]
+    assert len(kv) == len(okv) == L + steps == 564
+    _check_appended(kv, okv, L, steps)
+
+
+@pytest.mark.timeout(900)
+def test_full_loop_64_frames_after_prefill(full, prompt64):
+    """The talker + predictor loop, 64 frames after the 64-token prefill,
+    greedy and sampled: codes identical for every frame and group."""
+    tw, pw, t, p, ot, op = full
+    H, frames = tw.cfg.hidden, 64
+    lh, lg = prompt64["last_hidden"], prompt64["logits"]
+    text = qtts.synth_normal_f32(42, "full.text", 5 * H, 0.0, 0.1).reshape(5, H)
+    pad = qtts.synth_normal_f32(42, "full.pad", H, 0.0, 0.1)
+    modes = {"greedy": qtts.loop_params(frames, greedy=True, repetition_penalty=1.05, stop_on_eos=False),
+             "sampled": qtts.loop_params(frames, temperature=0.8, top_k=50, repetition_penalty=1.05,
+                                         stop_on_eos=False)}
+    runs = {}
+    for name in modes:
+        kv, okv = _caches(t, ot, PROMPT + frames + 8, prompt64["gpu"], prompt64["oracle"], PROMPT)
+        runs[name] = (kv, okv)
+
+    def oracle_loop(name):
+        okv = runs[name][1]
+        return oracle.generate_codes(ot, op, okv, op.new_kv(), lh, lg, PROMPT, text, pad, modes[name], seed=555)
+
+    t0 = time.time()
+    with ThreadPoolExecutor(max_workers=2) as pool:
+        futs = {name: pool.submit(oracle_loop, name) for name in modes}
+        got = {name: qtts.generate_codes(t, p, runs[name][0], p.new_kv(), lh, lg, PROMPT, text, pad, modes[name],
+                                         seed=555) for name in modes}
+        refs = {name: f.result() for name, f in futs.items()}
+    print(f"full loop 2 x {frames} frames: {time.time() - t0:.1f}s", flush=True)
+    for name in modes:
+        assert got[name].shape == refs[name].shape == (16, frames), name
+        assert np.array_equal(got[name], refs[name]), (name, np.argwhere(got[name] != refs[name])[:5])
+        kv, okv = runs[name]
+        assert len(kv) == len(okv) == PROMPT + frames
+        _check_appended(kv, okv, PROMPT, frames)
+
+
+@pytest.mark.timeout(900)
+def test_batch_config5_16_streams_2000_rows(full):
+    """16 streams of the talker + predictor in 2064-row caches (the talker
+    attention then runs more splits per kv head than at 1000 rows), each
+    loaded to 2000 N(0,1) rows of its own, with its own last hidden state,
+    trailing text and seed: 3 sampled frames.  Every stream's codes, frame
+    count, cache length and appended rows match the oracle's single-stream
+    loop."""
+    tw, pw, t, p, ot, op = full
+    c = tw.cfg
+    B, L, cap, frames = 16, 2000, 2064, 3
+    H = c.hidden
+    shape = (c.layers, L, c.kv_heads, c.head_dim)
+    kvs, okvs = [], []
+    t0 = time.time()
+    for b in range(B):
+        k = qtts.synth_normal_f32(43, f"cfg5.k.{b}", int(np.prod(shape))).reshape(shape)
+        v = qtts.synth_normal_f32(43, f"cfg5.v.{b}", int(np.prod(shape))).reshape(shape)
+        kv, okv = _caches(t, ot, cap, (k, v), (k, v), L)
+        kvs.append(kv)
+        okvs.append(okv)
+        del k, v
+    print(f"16 caches of {L} rows loaded in {time.time() - t0:.1f}s", flush=True)
+    lh = qtts.synth_normal_f32(43, "cfg5.h", B * H).reshape(B, H)
+    lg = np.stack([ot.apply_codec_head(lh[b]) for b in range(B)])
+    text = qtts.synth_normal_f32(43, "cfg5.text", B * 2 * H, 0.0, 0.1).reshape(B, 2, H)
+    pad = qtts.synth_normal_f32(43, "cfg5.pad", H, 0.0, 0.1)
+    seeds = [9000 + 7 * b for b in range(B)]
+    params = qtts.loop_params(frames, temperature=0.8, top_k=50, repetition_penalty=1.05, stop_on_eos=False)
+    pos = [L] * B
+
+    def oracle_loop(b):
+        return oracle.generate_codes(ot, op, okvs[b], op.new_kv(), lh[b], lg[b], L, text[b], pad, params,
+                                     seed=seeds[b])
+
+    t0 = time.time()
+    with ThreadPoolExecutor(max_workers=8) as pool:
+        futs = [pool.submit(oracle_loop, b) for b in range(B)]
+        got = qtts.generate_codes_batch(t, p, kvs, lh, lg, pos, text, pad, params, seeds)
+        refs = [f.result() for f in futs]
+    print(f"batch of {B} x {frames} frames and the oracle's streams: {time.time() - t0:.1f}s", flush=True)
+    for b in range(B):
+        assert got[b].shape == refs[b].shape == (16, frames), b
+        assert np.array_equal(got[b], refs[b]), (b, np.argwhere(got[b] != refs[b])[:5])
+        assert len(kvs[b]) == len(okvs[b]) == L + frames, b
+        _check_appended(kvs[b], okvs[b], L, frames)

@@ -424,3 +424,30 @@ def test_loop_frame_matches_manual_composition(tiny):
     prev = np.concatenate([[tok], ac]).astype(np.uint32)
     tok2, _ = oracle.sample_token(out[H:], 0.8, 50, 1.05, prev, st)
     assert codes[0, 1] == tok2
+
+
+@pytest.mark.parametrize("greedy", [True, False])
+def test_loop_talker_only_matches_manual_composition(tiny, greedy):
+    """The talker-only branch (the legacy feedback, src/generate.rs:225-227):
+    each frame samples code 0 with prev_tokens = [previous code 0, 0 x 15],
+    then feeds embed_codec_token(code 0) alone to forward_with_embedding at
+    the next position; groups 1-15 stay 0.  Composed by hand for 6 frames."""
+    tw, pw, ot, op = tiny
+    H = TINY_TALKER.hidden
+    lh = GOLDEN["talker_step0"][:H].astype(np.float32)
+    logits = GOLDEN["talker_step0"][H:].astype(np.float32)
+    frames, pos0, seed = 6, 2, 31
+    params = qtts.loop_params(frames, greedy=greedy, stop_on_eos=False, talker_only=True)
+    kv = ot.new_kv(16)
+    codes = oracle.generate_codes(ot, None, kv, None, lh, logits, pos0, None, None, params, seed=seed)
+    assert codes.shape == (16, frames) and len(kv) == frames
+    assert not codes[1:].any()
+    hkv, lg, st, prev = ot.new_kv(16), logits, seed, np.zeros(16, np.uint32)
+    for f in range(frames):
+        tok, st = oracle.sample_token(lg, 0.8, 50, 1.05, prev, st, greedy=greedy)
+        assert codes[0, f] == tok, f
+        prev[0] = tok
+        lg = ot.forward_with_embedding(ot.embed_codec_token(tok), hkv, pos0 + f)[H:]
+    k1, v1 = kv.store()
+    k2, v2 = hkv.store()
+    assert np.array_equal(k1, k2) and np.array_equal(v1, v2)
