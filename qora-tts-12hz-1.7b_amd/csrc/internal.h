@@ -339,4 +339,5 @@ void launch_repack_q4(hipStream_t st, const uint8_t *packed, const uint16_t *sca
 // GEMV launch plan for a [K -> N] weight at M rows.
 void plan_gemv(int K, int N, int M, int *kc, int *rpt);
 
+
 }  // namespace qtts

@@ -57,22 +57,9 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvParams P) {
     const int c = blockIdx.x - p * P.kc;
     const int k0 = c * (kGemvThreads * RPT);
 
-    // 1. weight rows of this chunk: one 128-bit load + one scale per row,
-    //    issued back to back with no branch between them.  A thread past the
-    //    last row (only in the last chunk) re-reads that row, and its input
-    //    is zero; the raw scale bits stay opaque until the accumulation so
-    //    that no load result is waited for while the others are issued.
-    const int nit = min(RPT, (K - k0 + kGemvThreads - 1) / kGemvThreads);
-    u32x4 wv[RPT];
-    uint32_t sv[RPT];
-#pragma unroll
-    for (int i = 0; i < RPT; i++) {
-        const int k = min(k0 + tid + i * kGemvThreads, K - 1);
-        wv[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4 *>(P.w.wq) + (size_t)p * K + k);
-        sv[i] = __builtin_nontemporal_load(P.w.ws + (size_t)p * K + k);
-    }
-
-    // 2. input values of those rows.
+    // 1. input values of this thread's rows, issued first: the loads retire
+    //    in order, so the accumulation below can then take each weight row
+    //    as it lands instead of waiting for the last one.
     float xv[RPT][M];
     if (P.prologue == PRO_RMSNORM) {
         // rms_norm_f16 (src/gemv.rs:406-417); each wave computes the full
@@ -117,12 +104,39 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvParams P) {
 #pragma unroll
             for (int m = 0; m < M; m++) xv[i][m] = ev[i];
     } else {
+        // branch-free: a row past K reads row K-1 and is zeroed
 #pragma unroll
         for (int i = 0; i < RPT; i++) {
             const int k = k0 + tid + i * kGemvThreads;
+            const int kc = min(k, K - 1);
 #pragma unroll
-            for (int m = 0; m < M; m++) xv[i][m] = k < K ? P.x[(size_t)m * P.ldx + k] : 0.0f;
+            for (int m = 0; m < M; m++) xv[i][m] = glb(P.x)[(size_t)m * P.ldx + kc];
+#pragma unroll
+            for (int m = 0; m < M; m++) xv[i][m] = k < K ? xv[i][m] : 0.0f;
         }
+    }
+
+    // 2. weight rows of this chunk: one 128-bit load + one scale per row,
+    //    issued back to back with no branch between them.  A thread past the
+    //    last row (only in the last chunk) re-reads that row, and its input
+    //    is zero; the raw scale bits stay opaque until the accumulation so
+    //    that no load result is waited for while the others are issued.
+    //    The scales go first and a scheduling barrier keeps the weight rows
+    //    after them in issue order, so row i is complete once the loads
+    //    issued after it (rows i+1..) are all that is outstanding.
+    u32x4 wv[RPT];
+    uint32_t sv[RPT];
+#pragma unroll
+    for (int i = 0; i < RPT; i++) {
+        const int k = min(k0 + tid + i * kGemvThreads, K - 1);
+        sv[i] = __builtin_nontemporal_load(glb(P.w.ws) + (size_t)p * K + k);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < RPT; i++) {
+        const int k = min(k0 + tid + i * kGemvThreads, K - 1);
+        wv[i] = __builtin_nontemporal_load(glb(reinterpret_cast<const u32x4 *>(P.w.wq)) + (size_t)p * K + k);
+        __builtin_amdgcn_sched_barrier(0);
     }
 
     // 3. accumulate 32 columns per thread: (scale * x) * nib, minus
@@ -135,11 +149,12 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvParams P) {
 #pragma unroll
         for (int j = 0; j < 32; j++) acc[m][j] = 0.0f;
     }
-#pragma unroll
-    for (int i = 0; i < RPT; i++) asm volatile("" : "+v"(sv[i]), "+v"(wv[i]));
+    // Rows past K (last chunk only) carry a zero input and add nothing.
 #pragma unroll
     for (int i = 0; i < RPT; i++) {
-        if (i >= nit) continue;
+        // row i's weights become visible to the compiler only here, so the
+        // wait before its FMAs is for row i alone
+        asm volatile("" : "+v"(sv[i]), "+v"(wv[i]));
         const float s = f16_to_f32((uint16_t)sv[i]);
         // sa = (scale * x) * 2^24, sb = (scale * x) * 2^20 (exact scalings;
         // the sums carry sum(scale * x) * 2^24)
@@ -161,15 +176,6 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvParams P) {
     // 4. block reduction -> this chunk's partial for the panel's 32 columns.
 #pragma unroll
     for (int m = 0; m < M; m++) dpp_reduce<32>(acc[m], &red[m * 4 * 32]);
-    __syncthreads();
-    if (tid < M * 32) {
-        const int m = tid >> 5, col = tid & 31;
-        const float *rw = &red[m * 4 * 32 + col];
-        const float s = (rw[0] + rw[32]) + (rw[64] + rw[96]);
-        st_dev(&P.partial[((size_t)c * M + m) * N + p * 32 + col], s);
-    }
-
-    // 5. the last block of an output group sums the chunks in order.
     int gp, group;
     if (P.epilogue == EPI_SWIGLU) {
         const int half = N / 64;
@@ -182,24 +188,40 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvParams P) {
         gp = 1;
         group = p;
     }
-    wait_stores();
+    // A block that alone makes its output group (one K chunk, one panel per
+    // group) finishes it from LDS: no partial round trip through memory.
+    const bool solo = P.kc == 1 && gp == 1;
     __syncthreads();
-    if (tid == 0) s_last = arrive_dev(&P.counters[group]) == (unsigned)(gp * P.kc - 1);
-    __syncthreads();
-    if (!s_last) return;
-    if (tid == 0) reset_dev(&P.counters[group]);
-
-    const int gcols = gp * 32;
-    for (int idx = tid; idx < M * gcols; idx += kGemvThreads) {
-        const int m = idx / gcols, j = idx - m * gcols;
-        int col;
-        if (P.epilogue == EPI_SWIGLU)
-            col = (j < 32) ? group * 32 + j : N / 2 + group * 32 + (j - 32);
+    if (tid < M * 32) {
+        const int m = tid >> 5, col = tid & 31;
+        const float *rw = &red[m * 4 * 32 + col];
+        const float s = (rw[0] + rw[32]) + (rw[64] + rw[96]);
+        if (solo)
+            ybuf[m * 32 + col] = s;
         else
-            col = group * gcols + j;
-        float s = 0.0f;
-        for (int cc = 0; cc < P.kc; cc++) s += ld_dev(&P.partial[((size_t)cc * M + m) * N + col]);
-        ybuf[m * gcols + j] = s;
+            st_dev(&P.partial[((size_t)c * M + m) * N + p * 32 + col], s);
+    }
+
+    // 5. the last block of an output group sums the chunks in order.
+    const int gcols = gp * 32;
+    if (!solo) {
+        wait_stores();
+        __syncthreads();
+        if (tid == 0) s_last = arrive_dev(&P.counters[group]) == (unsigned)(gp * P.kc - 1);
+        __syncthreads();
+        if (!s_last) return;
+        if (tid == 0) reset_dev(&P.counters[group]);
+        for (int idx = tid; idx < M * gcols; idx += kGemvThreads) {
+            const int m = idx / gcols, j = idx - m * gcols;
+            int col;
+            if (P.epilogue == EPI_SWIGLU)
+                col = (j < 32) ? group * 32 + j : N / 2 + group * 32 + (j - 32);
+            else
+                col = group * gcols + j;
+            float s = 0.0f;
+            for (int cc = 0; cc < P.kc; cc++) s += ld_dev(&P.partial[((size_t)cc * M + m) * N + col]);
+            ybuf[m * gcols + j] = s;
+        }
     }
     __syncthreads();
 
@@ -327,16 +349,69 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvParams P) {
     }
 }
 
-void plan_gemv(int K, int N, int M, int *kc, int *rpt) {
-    const int panels = N / 32;
-    int r = 1;
-    const int cands[3] = {4, 2, 1};
-    for (int ci = 0; ci < 3; ci++) {
-        r = cands[ci];
-        const int c = (K + kGemvThreads * r - 1) / (kGemvThreads * r);
-        if (panels * c >= 512) break;
+// The plain single-row GEMV (gemv_q4, src/gemv.rs:263-309) with K <= 2048:
+// one block per 32-column panel over its whole K.  The input rows go first,
+// then the scales, then the weight rows one by one (scheduling barriers keep
+// that issue order), so each row's FMAs wait for that row alone while the
+// later rows are still in flight; the 32 column sums are finished in LDS and
+// stored directly.  Same arithmetic as k_gemv.
+template <int RPT>
+__global__ __launch_bounds__(kGemvThreads) void k_gemv_plain(DevQ4 w, const float *x, float *y, const float *bias) {
+    __shared__ float red[4 * 32];
+    const int p = blockIdx.x, tid = threadIdx.x, K = w.K;
+    float xv[RPT];
+#pragma unroll
+    for (int i = 0; i < RPT; i++) {
+        const int k = tid + i * kGemvThreads;
+        xv[i] = glb(x)[min(k, K - 1)];
+        xv[i] = k < K ? xv[i] : 0.0f;
     }
+    uint32_t sv[RPT];
+    u32x4 wv[RPT];
+#pragma unroll
+    for (int i = 0; i < RPT; i++) sv[i] = __builtin_nontemporal_load(glb(w.ws) + (size_t)p * K + min(tid + i * kGemvThreads, K - 1));
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < RPT; i++) {
+        wv[i] = __builtin_nontemporal_load(glb(reinterpret_cast<const u32x4 *>(w.wq)) + (size_t)p * K +
+                                           min(tid + i * kGemvThreads, K - 1));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    float acc[1][32];
+#pragma unroll
+    for (int j = 0; j < 32; j++) acc[0][j] = 0.0f;
+    float sxsum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < RPT; i++) {
+        asm volatile("" : "+v"(sv[i]), "+v"(wv[i]));
+        const float s = f16_to_f32((uint16_t)sv[i]);
+        float sa[1], sb[1];
+        sa[0] = s * (xv[i] * 16777216.0f);
+        sb[0] = sa[0] * 0.0625f;
+        sxsum += sa[0];
+        const uint32_t wd[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
+        q4_mix_row<1, 32>(wd, sa, sb, acc);
+    }
+#pragma unroll
+    for (int j = 0; j < 32; j++) acc[0][j] = fmaf(-0x1p-21f, sxsum, acc[0][j]);
+    dpp_reduce<32>(acc[0], red);
+    __syncthreads();
+    if (tid < 32) {
+        float v = (red[tid] + red[32 + tid]) + (red[64 + tid] + red[96 + tid]);
+        if (bias) v += bias[p * 32 + tid];
+        y[p * 32 + tid] = v;
+    }
+}
+
+// Rows per thread and K chunks of a launch.  Up to 2048 rows a block takes
+// its panel's whole K (8 rows per thread at 2048): every weight load of the
+// launch is in flight at once and no partial sums go through memory.  Longer
+// K is split into chunks of 2048 rows, summed in chunk order.
+void plan_gemv(int K, int N, int M, int *kc, int *rpt) {
+    (void)N;
     (void)M;
+    int r = (K + kGemvThreads - 1) / kGemvThreads;
+    r = r <= 1 ? 1 : r <= 2 ? 2 : r <= 4 ? 4 : 8;
     *rpt = r;
     *kc = (K + kGemvThreads * r - 1) / (kGemvThreads * r);
 }
@@ -345,6 +420,7 @@ template <int M>
 static void launch_gemv_m(hipStream_t st, const GemvParams &p) {
     const dim3 grid((unsigned)((p.w.N / 32) * p.kc));
     switch (p.rpt) {
+        case 8: hipLaunchKernelGGL((k_gemv<M, 8>), grid, dim3(kGemvThreads), 0, st, p); break;
         case 4: hipLaunchKernelGGL((k_gemv<M, 4>), grid, dim3(kGemvThreads), 0, st, p); break;
         case 2: hipLaunchKernelGGL((k_gemv<M, 2>), grid, dim3(kGemvThreads), 0, st, p); break;
         default: hipLaunchKernelGGL((k_gemv<M, 1>), grid, dim3(kGemvThreads), 0, st, p); break;
@@ -352,6 +428,16 @@ static void launch_gemv_m(hipStream_t st, const GemvParams &p) {
 }
 
 void launch_gemv(hipStream_t st, const GemvParams &p) {
+    if (p.M == 1 && p.kc == 1 && p.prologue == PRO_PLAIN && p.epilogue == EPI_STORE && p.fin == FIN_NONE &&
+        !p.d_done) {
+        const dim3 grid((unsigned)(p.w.N / 32));
+        switch (p.rpt) {
+            case 8: hipLaunchKernelGGL((k_gemv_plain<8>), grid, dim3(kGemvThreads), 0, st, p.w, p.x, p.y, p.bias); return;
+            case 4: hipLaunchKernelGGL((k_gemv_plain<4>), grid, dim3(kGemvThreads), 0, st, p.w, p.x, p.y, p.bias); return;
+            case 2: hipLaunchKernelGGL((k_gemv_plain<2>), grid, dim3(kGemvThreads), 0, st, p.w, p.x, p.y, p.bias); return;
+            default: hipLaunchKernelGGL((k_gemv_plain<1>), grid, dim3(kGemvThreads), 0, st, p.w, p.x, p.y, p.bias); return;
+        }
+    }
     switch (p.M) {
         case 1: launch_gemv_m<1>(st, p); break;
         case 2: launch_gemv_m<2>(st, p); break;
