@@ -170,6 +170,15 @@ qtts_status qtts_embed_lookup(qtts_ctx *ctx, const qtts_q4 *w, int32_t token_id,
 /* Same operators on device buffers, enqueued on the context stream. */
 qtts_status qtts_gemv_device(qtts_ctx *ctx, const qtts_q4 *w, const float *d_input, float *d_output);
 qtts_status qtts_gemm_device(qtts_ctx *ctx, const qtts_q4 *w, const float *d_x, int32_t seq_len, float *d_output);
+/* No counterpart in the reference: qtts_gemm_device for 1..4 rows that
+ * allocates nothing, for callers that cannot allocate device memory (code
+ * under HIP graph capture, tight serving loops).  Enqueued on `stream` (a
+ * hipStream_t; NULL: the weight's context stream), no synchronisation.  Its
+ * split-K partials and counters live in one module-scope device array per
+ * device (1 MiB), shared by every call on that device: calls that overlap on
+ * one GPU race.  QTTS_ERANGE for rows outside 1..4, K above 8192 or N above
+ * 16384.  Same kernels and results as qtts_gemm_device for those shapes. */
+qtts_status qtts_gemv_device_static(const qtts_q4 *w, const float *d_x, int32_t rows, float *d_output, void *stream);
 
 /* ------------------------------------------------------------------------ */
 /* KV cache (RawKvCache, src/gemv.rs:75-86)                                  */

@@ -1323,6 +1323,7 @@ qtts_status qtts_ctx_create(int32_t device, qtts_ctx **out) {
     if (bad(hipMalloc(&c->d_small, 256))) return QTTS_ENOMEM;
     if (bad(hipMemset(c->counters, 0, kCounters * sizeof(unsigned)))) return QTTS_EDEVICE;
     if (bad(hipMemset(c->attn_counters, 0, kAttnCounters * sizeof(unsigned)))) return QTTS_EDEVICE;
+    if (bad(static_scratch_setup(device))) return QTTS_EDEVICE;
     if (bad(hipDeviceSynchronize())) return QTTS_EDEVICE;
     *out = c;
     return QTTS_OK;
@@ -1411,6 +1412,31 @@ qtts_status qtts_gemm_device(qtts_ctx *c, const qtts_q4 *w, const float *d_x, in
 
 qtts_status qtts_gemv_device(qtts_ctx *c, const qtts_q4 *w, const float *d_x, float *d_out) {
     return qtts_gemm_device(c, w, d_x, 1, d_out);
+}
+
+qtts_status qtts_gemv_device_static(const qtts_q4 *w, const float *d_x, int32_t rows, float *d_out, void *stream) {
+    if (!w || !d_x || !d_out) return QTTS_EINVAL;
+    qtts_ctx *c = w->ctx;
+    if (rows < 1 || rows > kMaxM) return fail(c, QTTS_ERANGE, "gemv_device_static: rows must be 1..4");
+    if (w->d.K > kStaticMaxK || w->d.N > kStaticMaxN)
+        return fail(c, QTTS_ERANGE, "gemv_device_static: K above 8192 or N above 16384");
+    float *scr = static_cast<float *>(static_scratch(c->device));
+    if (!scr) return fail(c, QTTS_ESTATE, "gemv_device_static: no scratch on this device");
+    GemvParams p{};
+    p.w = w->d;
+    p.M = rows;
+    plan_gemv(w->d.K, w->d.N, rows, &p.kc, &p.rpt);
+    if (p.kc > kStaticMaxChunks) return fail(c, QTTS_ERANGE, "gemv_device_static: too many K chunks");
+    p.prologue = PRO_PLAIN;
+    p.x = d_x;
+    p.ldx = w->d.K;
+    p.epilogue = EPI_STORE;
+    p.y = d_out;
+    p.ldy = w->d.N;
+    p.partial = scr;
+    p.counters = reinterpret_cast<unsigned *>(scr + kStaticPartialFloats);
+    launch_gemv(stream ? static_cast<hipStream_t>(stream) : c->stream, p);
+    return check_launch(c, "k_gemv");
 }
 
 qtts_status qtts_gemm(qtts_ctx *c, const qtts_q4 *w, const float *x, int32_t seq_len, float *out) {

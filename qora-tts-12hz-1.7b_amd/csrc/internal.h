@@ -339,5 +339,18 @@ void launch_repack_q4(hipStream_t st, const uint8_t *packed, const uint16_t *sca
 // GEMV launch plan for a [K -> N] weight at M rows.
 void plan_gemv(int K, int N, int M, int *kc, int *rpt);
 
+// Limits of the allocation-free GEMV (qtts_gemv_device_static), whose split-K
+// partials [chunks][rows][N] and arrival counters [N/32 + 1] live in a
+// module-scope device array (kernels.hip), one per device.
+constexpr int kStaticMaxK = 8192;  // <= 4 chunks of 2048 rows
+constexpr int kStaticMaxN = 16384;
+constexpr int kStaticMaxChunks = 4;
+constexpr size_t kStaticPartialFloats = (size_t)kStaticMaxChunks * kMaxM * kStaticMaxN;
+constexpr size_t kStaticCounterWords = kStaticMaxN / 32 + 64;
+// Looks up (once per device, with that device current) and zeroes the
+// device's copy of that array.
+hipError_t static_scratch_setup(int device);
+// Its device address for `device`, or null before setup.
+void *static_scratch(int device);
 
 }  // namespace qtts

@@ -12,6 +12,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cfloat>
+#include <mutex>
 #include <type_traits>
 #include <cmath>
 
@@ -401,6 +402,39 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv_plain(DevQ4 w, const floa
         if (bias) v += bias[p * 32 + tid];
         y[p * 32 + tid] = v;
     }
+}
+
+// Scratch of the allocation-free GEMV entry point: split-K partials
+// [chunks <= 4][rows <= 4][N <= 16384] f32, then the arrival counters
+// [N/32 + 1] (1 MiB + 2.3 KiB).  Each device holds its own copy while the
+// library is loaded.  In host code the name is a stand-in, not a device
+// address: kernels get the address hipGetSymbolAddress returns.
+static __device__ __align__(256) float scratch[kStaticPartialFloats + kStaticCounterWords];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void *g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+hipError_t static_scratch_setup(int device) {
+    if (device < 0 || device >= kMaxDevices) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (g_scratch_ptr[device]) return hipSuccess;
+    void *ptr = nullptr;
+    hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    // the counters must start at zero (every launch leaves them so)
+    e = hipMemset(ptr, 0, sizeof(scratch));
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e == hipSuccess) g_scratch_ptr[device] = ptr;
+    return e;
+}
+
+void *static_scratch(int device) {
+    if (device < 0 || device >= kMaxDevices) return nullptr;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    return g_scratch_ptr[device];
 }
 
 // Rows per thread and K chunks of a launch.  Up to 2048 rows a block takes

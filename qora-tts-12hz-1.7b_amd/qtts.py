@@ -231,6 +231,7 @@ def load_library(path: str = LIB_PATH):
         "qtts_embed_lookup": ([vp, vp, i32, f32p], i32),
         "qtts_gemv_device": ([vp, vp, vp, vp], i32),
         "qtts_gemm_device": ([vp, vp, vp, i32, vp], i32),
+        "qtts_gemv_device_static": ([vp, vp, i32, vp, vp], i32),
         "qtts_kv_create": ([vp, i32, i32, i32, i32, C.POINTER(vp)], i32),
         "qtts_kv_free": ([vp], None),
         "qtts_kv_len": ([vp], i32),
@@ -288,7 +289,7 @@ def exported_symbols() -> List[str]:
     return [
         "qtts_version", "qtts_ctx_create", "qtts_ctx_destroy", "qtts_last_error", "qtts_ctx_stream",
         "qtts_ctx_synchronize", "qtts_q4_upload", "qtts_q4_free", "qtts_q4_bytes", "qtts_gemv", "qtts_gemm",
-        "qtts_embed_lookup", "qtts_gemv_device", "qtts_gemm_device", "qtts_kv_create", "qtts_kv_free",
+        "qtts_embed_lookup", "qtts_gemv_device", "qtts_gemm_device", "qtts_gemv_device_static", "qtts_kv_create", "qtts_kv_free",
         "qtts_kv_len", "qtts_kv_clear", "qtts_kv_load", "qtts_kv_store", "qtts_talker_upload", "qtts_talker_free",
         "qtts_forward_with_embedding", "qtts_prefill_talker_raw", "qtts_apply_codec_head",
         "qtts_embed_codec_token", "qtts_predictor_upload", "qtts_predictor_free", "qtts_generate_acoustic_codes",
