@@ -106,6 +106,17 @@ typedef struct qtts_predictor_view {
     const float *rope_sin;
 } qtts_predictor_view;
 
+/* The prompt-assembly part of TalkerWeights (src/talker.rs:33-56; saved at
+ * src/save.rs:76-81): the text embedding and the two-layer text projection. */
+typedef struct qtts_text_view {
+    qtts_q4_view text_embedding;     /* [text_vocab][text_hidden] */
+    qtts_q4_view text_proj_fc1;      /* [text_hidden][fc1_out] */
+    const float *text_proj_fc1_bias; /* [fc1_out] */
+    qtts_q4_view text_proj_fc2;      /* [fc1_out][hidden] */
+    const float *text_proj_fc2_bias; /* [hidden] */
+    int32_t text_hidden_size;
+} qtts_text_view;
+
 /* sample_token parameters, src/generate_new.rs:38-45,329-391. */
 typedef struct qtts_sampler {
     float temperature;        /* divides the scores unless == 1.0 */
@@ -217,6 +228,44 @@ qtts_status qtts_prefill_talker_raw(qtts_talker *t, const float *x, int32_t seq_
 qtts_status qtts_apply_codec_head(qtts_talker *t, const float *hidden, float *logits);
 /* embed_codec_token(weights, token) -> [hidden]; src/talker.rs:152-154. */
 qtts_status qtts_embed_codec_token(qtts_talker *t, uint32_t token_id, float *out);
+
+/* Prompt assembly (src/talker.rs:105-116, src/generate_new.rs:60-326).  The
+ * text weights ride with the talker; every step below runs on the device.  */
+
+/* Uploads TalkerWeights' text embedding and text projection (src/talker.rs:
+ * 33-56) to the talker.  The text vocab must cover the TTS special tokens
+ * (src/generate_new.rs:28-30); QTTS_ESTATE on a second upload. */
+qtts_status qtts_talker_text_upload(qtts_talker *t, const qtts_text_view *w);
+/* embed_text_token(weights, token) -> [hidden]; src/talker.rs:105-116:
+ * fc2(silu(fc1(text_embedding[token]) + b1)) + b2. */
+qtts_status qtts_embed_text_token(qtts_talker *t, uint32_t token_id, float *out);
+/* The input rows prefill_custom_voice runs, src/generate_new.rs:60-177: the
+ * role prefix, the codec prefix with the TTS pad/BOS overlay (the built-in
+ * speaker path, voice_embedding NULL) or with the raw voice embedding row
+ * (voice_embedding [hidden]), and BOS + the first text token.  rows receives
+ * *seq_len (9, or 10 with text) rows of hidden floats. */
+qtts_status qtts_build_custom_voice_prompt(qtts_talker *t, const uint32_t *text_tokens, int32_t n_text,
+                                           uint32_t speaker_id, uint32_t language_id, const float *voice_embedding,
+                                           float *rows, int32_t *seq_len);
+/* prefill_custom_voice(...) -> (last_hidden, logits); src/generate_new.rs:
+ * 84-188.  The cache must be empty; *position receives the next position
+ * (9, or 10 with text; src/generate_new.rs:216). */
+qtts_status qtts_prefill_custom_voice(qtts_talker *t, const uint32_t *text_tokens, int32_t n_text, uint32_t speaker_id,
+                                      uint32_t language_id, const float *voice_embedding, qtts_kv *kv,
+                                      float *last_hidden, float *logits, int32_t *position);
+/* build_trailing_text(weights, tokens) -> rows; src/generate_new.rs:314-326:
+ * the text projection of tokens[1..] then of TTS_EOS, *n_rows = max(n_text, 1)
+ * rows of hidden floats. */
+qtts_status qtts_build_trailing_text(qtts_talker *t, const uint32_t *text_tokens, int32_t n_text, float *rows,
+                                     int32_t *n_rows);
+/* generate_speech (src/generate_new.rs:191-300) from token ids to codes:
+ * prefill_custom_voice, build_trailing_text, the TTS_PAD row and the frame
+ * loop (qtts_generate_codes).  The tokenizer and the speech decoder are not
+ * part of it.  codes / *n_frames as for qtts_generate_codes. */
+qtts_status qtts_generate_speech_codes(qtts_talker *t, qtts_predictor *p, const uint32_t *text_tokens, int32_t n_text,
+                                       uint32_t speaker_id, uint32_t language_id, const float *voice_embedding,
+                                       qtts_kv *talker_kv, qtts_kv *predictor_kv, const qtts_loop_params *params,
+                                       uint64_t seed, uint32_t *codes, int32_t *n_frames);
 
 /* ------------------------------------------------------------------------ */
 /* Code Predictor (src/code_predictor.rs)                                    */

@@ -31,17 +31,6 @@ extern "C" {
 
 typedef struct qtts_model_file qtts_model_file;
 
-/* The prompt-assembly part of TalkerWeights (src/talker.rs:33-56; saved at
- * src/save.rs:76-81): the text embedding and the two-layer text projection. */
-typedef struct qtts_text_view {
-    qtts_q4_view text_embedding;     /* [text_vocab][text_hidden] */
-    qtts_q4_view text_proj_fc1;      /* [text_hidden][fc1_out] */
-    const float *text_proj_fc1_bias; /* [fc1_out] */
-    qtts_q4_view text_proj_fc2;      /* [fc1_out][hidden] */
-    const float *text_proj_fc2_bias; /* [hidden] */
-    int32_t text_hidden_size;
-} qtts_text_view;
-
 /* Header fields and section layout. */
 typedef struct qtts_file_info {
     uint32_t version;      /* 1 */

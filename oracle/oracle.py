@@ -72,6 +72,14 @@ def load():
         "qor_decode_to_audio": ([C.POINTER(qtts.DecoderView), vp, i32, i32, vp, C.c_int64, C.POINTER(C.c_int64), i32],
                                 i32),
         "qor_argmax": ([vp, i32, C.POINTER(u32)], i32),
+        "qor_text_new": ([C.POINTER(qtts.TextView)], vp),
+        "qor_text_free": ([vp], None),
+        "qor_embed_text_token": ([vp, u32, vp, i32], i32),
+        "qor_build_custom_voice_prompt": ([vp, vp, i32, vp, i32, u32, u32, vp, vp, C.POINTER(i32), i32], i32),
+        "qor_prefill_custom_voice": ([vp, vp, i32, vp, i32, u32, u32, vp, vp, vp, vp, C.POINTER(i32), i32], i32),
+        "qor_build_trailing_text": ([vp, vp, i32, vp, C.POINTER(i32), i32], i32),
+        "qor_generate_speech_codes": ([vp, vp, vp, i32, vp, i32, u32, u32, vp, vp, vp, C.POINTER(qtts.LoopParams),
+                                       C.c_uint64, vp, C.POINTER(i32), i32], i32),
         "qor_dec_causal_conv": ([vp, i32, C.POINTER(qtts.ConvView), vp, i32], None),
         "qor_dec_transposed_conv": ([vp, i32, C.POINTER(qtts.ConvView), vp, i32], i32),
         "qor_dec_depthwise_conv": ([vp, i32, C.POINTER(qtts.ConvView), vp, i32], None),
@@ -322,6 +330,75 @@ def generate_codes(talker: Talker, predictor: Optional[CodePredictor], talker_kv
                                      position, _p(tt), tl, _p(pad), C.byref(params), seed, _p(codes), C.byref(n),
                                      nthreads))
     return codes[:, : n.value].copy()
+
+
+# --- prompt assembly (qtts_oracle_prompt.c) ---------------------------------
+class Text:
+    """The text embedding and projection for a talker (src/talker.rs:33-56)."""
+
+    def __init__(self, talker: Talker, w: "qtts.TextWeights", nthreads: int = 0):
+        self.talker, self.w, self.nthreads = talker, w, nthreads
+        self._view = w.view()
+        self.h = load().qor_text_new(C.byref(self._view))
+
+    @property
+    def hidden(self):
+        return self.talker.cfg.hidden
+
+    def embed_text_token(self, token: int) -> np.ndarray:
+        out = np.empty(self.hidden, dtype=np.float32)
+        _check(load().qor_embed_text_token(self.h, token, _p(out), self.nthreads))
+        return out
+
+    def _tok(self, tokens):
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        return t, (_p(t) if t.size else None)
+
+    def build_custom_voice_prompt(self, tokens, speaker_id, language_id, voice=None) -> np.ndarray:
+        t, tp = self._tok(tokens)
+        rows = np.empty((10, self.hidden), dtype=np.float32)
+        n = C.c_int32(0)
+        v = None if voice is None else f32(voice)
+        _check(load().qor_build_custom_voice_prompt(self.talker.h, self.h, self.talker.cfg.vocab, tp, t.size,
+                                                    speaker_id, language_id, _p(v), _p(rows), C.byref(n),
+                                                    self.nthreads))
+        return rows[: n.value].copy()
+
+    def prefill_custom_voice(self, tokens, speaker_id, language_id, kv: Kv, voice=None):
+        t, tp = self._tok(tokens)
+        lh = np.empty(self.hidden, dtype=np.float32)
+        lg = np.empty(self.talker.cfg.vocab, dtype=np.float32)
+        pos = C.c_int32(0)
+        v = None if voice is None else f32(voice)
+        _check(load().qor_prefill_custom_voice(self.talker.h, self.h, self.talker.cfg.vocab, tp, t.size, speaker_id,
+                                               language_id, _p(v), kv.h, _p(lh), _p(lg), C.byref(pos),
+                                               self.nthreads))
+        return lh, lg, pos.value
+
+    def build_trailing_text(self, tokens) -> np.ndarray:
+        t, tp = self._tok(tokens)
+        rows = np.empty((max(t.size, 1), self.hidden), dtype=np.float32)
+        n = C.c_int32(0)
+        _check(load().qor_build_trailing_text(self.h, tp, t.size, _p(rows), C.byref(n), self.nthreads))
+        return rows[: n.value].copy()
+
+    def generate_speech_codes(self, predictor, tokens, speaker_id, language_id, talker_kv: Kv, predictor_kv,
+                              params: "qtts.LoopParams", seed: int, voice=None) -> np.ndarray:
+        t, tp = self._tok(tokens)
+        codes = np.zeros((16, max(params.max_codes, 1)), dtype=np.uint32)
+        n = C.c_int32(0)
+        v = None if voice is None else f32(voice)
+        _check(load().qor_generate_speech_codes(self.talker.h, predictor.h if predictor is not None else None, self.h,
+                                                self.talker.cfg.vocab, tp, t.size, speaker_id, language_id, _p(v),
+                                                talker_kv.h, predictor_kv.h if predictor_kv is not None else None,
+                                                C.byref(params), seed, _p(codes), C.byref(n), self.nthreads))
+        return codes[:, : n.value].copy()
+
+    def __del__(self):
+        try:
+            load().qor_text_free(self.h)
+        except Exception:
+            pass
 
 
 def decode_to_audio(w, codes, nthreads: int = 0) -> np.ndarray:

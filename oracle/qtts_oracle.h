@@ -116,6 +116,33 @@ int64_t qor_decoder_num_samples(const qtts_decoder_view *w, int32_t frames);
  * for a code past the codebook or too small an output buffer. */
 int32_t qor_decode_to_audio(const qtts_decoder_view *w, const uint32_t *codes, int32_t frames, int32_t ld,
                             float *audio, int64_t capacity, int64_t *n_samples, int32_t nthreads);
+/* --- prompt assembly (qtts_oracle_prompt.c) ------------------------------ */
+typedef struct qor_text qor_text;
+/* The text embedding and projection of TalkerWeights (src/talker.rs:33-56). */
+qor_text *qor_text_new(const qtts_text_view *w);
+void qor_text_free(qor_text *x);
+/* embed_text_token, src/talker.rs:105-116.  QTTS_ERANGE past the text vocab. */
+int32_t qor_embed_text_token(const qor_text *x, uint32_t token, float *out, int32_t nthreads);
+/* The prompt rows of prefill_custom_voice (src/generate_new.rs:60-177):
+ * rows [10][hidden], *L = 9 or 10; voice NULL for the built-in speaker path. */
+int32_t qor_build_custom_voice_prompt(const qor_talker *t, const qor_text *x, int32_t codec_vocab,
+                                      const uint32_t *tokens, int32_t n_text, uint32_t speaker_id,
+                                      uint32_t language_id, const float *voice, float *rows, int32_t *L,
+                                      int32_t nthreads);
+/* prefill_custom_voice, src/generate_new.rs:84-188. */
+int32_t qor_prefill_custom_voice(const qor_talker *t, const qor_text *x, int32_t codec_vocab, const uint32_t *tokens,
+                                 int32_t n_text, uint32_t speaker_id, uint32_t language_id, const float *voice,
+                                 qor_kv *kv, float *last_hidden, float *logits, int32_t *position, int32_t nthreads);
+/* build_trailing_text, src/generate_new.rs:314-326: out [max(n_text,1)][hidden]. */
+int32_t qor_build_trailing_text(const qor_text *x, const uint32_t *tokens, int32_t n_text, float *out, int32_t *rows,
+                                int32_t nthreads);
+/* generate_speech from token ids to codes, src/generate_new.rs:191-300. */
+int32_t qor_generate_speech_codes(const qor_talker *t, const qor_predictor *p, const qor_text *x, int32_t codec_vocab,
+                                  const uint32_t *tokens, int32_t n_text, uint32_t speaker_id, uint32_t language_id,
+                                  const float *voice, qor_kv *talker_kv, qor_kv *predictor_kv,
+                                  const qtts_loop_params *params, uint64_t seed, uint32_t *codes, int32_t *n_frames,
+                                  int32_t nthreads);
+
 /* Test hooks: the decoder's primitives (qtts_oracle_decoder.c), for CPU
  * checks against closed forms and float64 brute force. */
 void qor_dec_causal_conv(const float *in, int32_t len, const qtts_conv_view *w, float *out, int32_t nt);

@@ -657,6 +657,15 @@ struct qtts_talker {
     float *trailing = nullptr;
     size_t trailing_cap = 0;
     float *pad = nullptr;
+    // prompt assembly (qtts_talker_text_upload): text embedding and the
+    // two-layer text projection, and their work rows
+    DevQ4 text_emb{}, fc1{}, fc2{};
+    float *fc1_b = nullptr, *fc2_b = nullptr;
+    int text_hidden = 0, has_text = 0;
+    float *tx_raw = nullptr, *tx_h = nullptr, *tx_rows = nullptr;
+    float *pr_codec = nullptr;  // [8][hidden]: the prompt's codec rows and the voice row
+    uint32_t *tx_tok = nullptr;
+    int tx_cap = 0;
     // engine programs (built lazily, cached per cache object)
     std::unique_ptr<EngProgram> step_prog, frame_prog;
     uint64_t step_kv = 0;  // serial of the cache step_prog was built for
@@ -665,6 +674,8 @@ struct qtts_talker {
         for (void *p : prefill_bufs) (void)hipFree(p);
         if (codes) (void)hipFree(codes);
         if (trailing) (void)hipFree(trailing);
+        for (void *p : {(void *)tx_raw, (void *)tx_h, (void *)tx_rows, (void *)tx_tok})
+            if (p) (void)hipFree(p);
     }
 };
 
@@ -1810,14 +1821,24 @@ static qtts_status prefill_layers_mfma(qtts_talker *t, qtts_kv *kv, int seq_len)
     return QTTS_OK;
 }
 
-qtts_status qtts_prefill_talker_raw(qtts_talker *t, const float *x, int32_t seq_len, qtts_kv *kv, float *last_hidden) {
-    if (!t || !x || !last_hidden) return QTTS_EINVAL;
+namespace {
+
+qtts_status prefill_buffers(qtts_talker *t, int32_t seq_len);
+
+// Checks a prefill of seq_len rows into kv and sizes the prefill work buffers.
+qtts_status prefill_prepare(qtts_talker *t, int32_t seq_len, qtts_kv *kv) {
     qtts_ctx *c = t->ctx;
     QTTS_TRY(check_kv(c, t->st, kv));
     if (kv->len != 0) return fail(c, QTTS_ESTATE, "prefill needs an empty cache (src/talker.rs:405-408)");
     if (seq_len < 1) return fail(c, QTTS_EINVAL, "seq_len < 1");
     if (seq_len > kv->cap) return fail(c, QTTS_ERANGE, "prefill longer than the cache");
     if (seq_len > t->max_pos) return fail(c, QTTS_ERANGE, "prefill longer than the RoPE table");
+    return prefill_buffers(t, seq_len);
+}
+
+// Sizes the prefill work buffers (t->xp and the per-row scratch) for seq_len rows.
+qtts_status prefill_buffers(qtts_talker *t, int32_t seq_len) {
+    qtts_ctx *c = t->ctx;
     const Stack &st = t->st;
     const int hidden = st.hidden, qd = st.nq * st.hd;
     if (seq_len > t->prefill_cap) {
@@ -1837,8 +1858,17 @@ qtts_status qtts_prefill_talker_raw(qtts_talker *t, const float *x, int32_t seq_
         t->prefill_bufs.push_back(t->rawp);
         t->prefill_cap = seq_len;
     }
+    return QTTS_OK;
+}
+
+// prefill_talker_raw (src/talker.rs:364-462) of the seq_len rows already in
+// t->xp.  Leaves the final-normed last row in t->out[0, hidden) and its
+// logits, apply_codec_head (src/talker.rs:627-629), in t->out + hidden.
+qtts_status prefill_from_xp(qtts_talker *t, int32_t seq_len, qtts_kv *kv) {
+    qtts_ctx *c = t->ctx;
+    const Stack &st = t->st;
+    const int hidden = st.hidden;
     t->nsplit = attn_nsplit(kv->cap, 16);
-    HIP_TRY(c, hipMemcpyAsync(t->xp, x, sizeof(float) * seq_len * hidden, hipMemcpyHostToDevice, c->stream));
     if (seq_len >= kMfmaMinRows && t->mfma_state == 0) QTTS_TRY(make_talker_mfma(t));
     if (seq_len >= kMfmaMinRows && t->mfma_state == 1) {
         QTTS_TRY(prefill_layers_mfma(t, kv, seq_len));
@@ -1846,7 +1876,7 @@ qtts_status qtts_prefill_talker_raw(qtts_talker *t, const float *x, int32_t seq_
         QTTS_TRY(prefill_layers_rows(t, kv, seq_len));
     }
     // final norm of the last row (src/talker.rs:460-461) via the head GEMV's
-    // normalising prologue; the logits it also produces are discarded.
+    // normalising prologue, which also forms the logits of that normed row
     GemvParams p = gemv_base(c, t->head, 1);
     p.prologue = PRO_RMSNORM;
     p.x = t->xp;
@@ -1859,10 +1889,24 @@ qtts_status qtts_prefill_talker_raw(qtts_talker *t, const float *x, int32_t seq_
     p.y = t->out + hidden;
     p.ldy = t->vocab;
     QTTS_TRY(run_gemv(c, p));
-    HIP_TRY(c, hipMemcpyAsync(last_hidden, t->out, sizeof(float) * hidden, hipMemcpyDeviceToHost, c->stream));
-    QTTS_TRY(sync(c));
     kv->len = seq_len;
     return QTTS_OK;
+}
+
+}  // namespace
+
+qtts_status qtts_prefill_talker_raw(qtts_talker *t, const float *x, int32_t seq_len, qtts_kv *kv, float *last_hidden) {
+    if (!t || !x || !last_hidden) return QTTS_EINVAL;
+    qtts_ctx *c = t->ctx;
+    QTTS_TRY(prefill_prepare(t, seq_len, kv));
+    HIP_TRY(c, hipMemcpyAsync(t->xp, x, sizeof(float) * seq_len * t->st.hidden, hipMemcpyHostToDevice, c->stream));
+    qtts_status s = prefill_from_xp(t, seq_len, kv);
+    if (s != QTTS_OK) {
+        kv->len = 0;
+        return s;
+    }
+    HIP_TRY(c, hipMemcpyAsync(last_hidden, t->out, sizeof(float) * t->st.hidden, hipMemcpyDeviceToHost, c->stream));
+    return sync(c);
 }
 
 qtts_status qtts_apply_codec_head(qtts_talker *t, const float *hidden, float *logits) {
@@ -1891,6 +1935,250 @@ qtts_status qtts_embed_codec_token(qtts_talker *t, uint32_t token_id, float *out
     QTTS_TRY(check_launch(c, "k_embed_row"));
     HIP_TRY(c, hipMemcpyAsync(out, t->out, sizeof(float) * t->st.hidden, hipMemcpyDeviceToHost, c->stream));
     return sync(c);
+}
+
+// ---------------------------------------------------------------------------
+// Prompt assembly: embed_text_token (src/talker.rs:105-116),
+// prefill_custom_voice (src/generate_new.rs:60-188) and build_trailing_text
+// (src/generate_new.rs:314-326) on the device.
+// ---------------------------------------------------------------------------
+namespace {
+
+// Special tokens, src/generate_new.rs:24-36.
+constexpr uint32_t kImStart = 151644, kAssistant = 77091, kNewline = 198;
+constexpr uint32_t kTtsPad = 151671, kTtsBos = 151672, kTtsEos = 151673;
+constexpr uint32_t kCodecThink = 2154, kCodecThinkBos = 2156, kCodecThinkEos = 2157, kCodecPad = 2148,
+                   kCodecBos = 2149;
+constexpr int kPromptMaxRows = 10;
+
+qtts_status text_reserve(qtts_talker *t, int n) {
+    if (n <= t->tx_cap) return QTTS_OK;
+    qtts_ctx *c = t->ctx;
+    for (void *p : {(void *)t->tx_raw, (void *)t->tx_h, (void *)t->tx_rows, (void *)t->tx_tok})
+        if (p) (void)hipFree(p);
+    t->tx_raw = t->tx_h = t->tx_rows = nullptr;
+    t->tx_tok = nullptr;
+    t->tx_cap = 0;
+    HIP_TRY(c, hipMalloc(&t->tx_raw, sizeof(float) * n * t->text_hidden));
+    HIP_TRY(c, hipMalloc(&t->tx_h, sizeof(float) * n * t->fc1.N));
+    HIP_TRY(c, hipMalloc(&t->tx_rows, sizeof(float) * n * t->st.hidden));
+    HIP_TRY(c, hipMalloc(&t->tx_tok, sizeof(uint32_t) * n));
+    t->tx_cap = n;
+    return QTTS_OK;
+}
+
+// One layer of the text projection over n rows: y = gemv(x, w) + bias, the
+// GEMV with rows of up to kMaxM per launch.
+qtts_status text_layer(qtts_talker *t, const DevQ4 &w, const float *x, int n, const float *bias, float *y) {
+    for (int r0 = 0; r0 < n; r0 += kMaxM) {
+        const int M = n - r0 < kMaxM ? n - r0 : kMaxM;
+        GemvParams p = gemv_base(t->ctx, w, M);
+        p.prologue = PRO_PLAIN;
+        p.x = x + (size_t)r0 * w.K;
+        p.ldx = w.K;
+        p.epilogue = EPI_STORE;
+        p.y = y + (size_t)r0 * w.N;
+        p.ldy = w.N;
+        p.bias = bias;
+        QTTS_TRY(run_gemv(t->ctx, p));
+    }
+    return QTTS_OK;
+}
+
+// embed_text_token of the n host tokens, rows [n][hidden] to `out` (device).
+qtts_status text_project(qtts_talker *t, const uint32_t *tokens, int n, float *out) {
+    qtts_ctx *c = t->ctx;
+    if (!t->has_text) return fail(c, QTTS_ESTATE, "no text weights: call qtts_talker_text_upload first");
+    for (int i = 0; i < n; i++)
+        if (tokens[i] >= (uint32_t)t->text_emb.K) return fail(c, QTTS_ERANGE, "text token id out of range");
+    QTTS_TRY(text_reserve(t, n));
+    HIP_TRY(c, hipMemcpyAsync(t->tx_tok, tokens, sizeof(uint32_t) * n, hipMemcpyHostToDevice, c->stream));
+    launch_embed_rows(c->stream, t->text_emb, t->tx_tok, 1, n, t->tx_raw, t->text_hidden);
+    QTTS_TRY(check_launch(c, "k_embed_rows"));
+    QTTS_TRY(text_layer(t, t->fc1, t->tx_raw, n, t->fc1_b, t->tx_h));
+    launch_silu(c->stream, t->tx_h, (long long)n * t->fc1.N);
+    QTTS_TRY(check_launch(c, "k_silu"));
+    return text_layer(t, t->fc2, t->tx_h, n, t->fc2_b, out);
+}
+
+// The rows of prefill_custom_voice into t->xp (sized for kPromptMaxRows);
+// *L = 9 or 10.
+qtts_status build_prompt(qtts_talker *t, const uint32_t *text_tokens, int32_t n_text, uint32_t speaker_id,
+                         uint32_t language_id, const float *voice, int *L) {
+    qtts_ctx *c = t->ctx;
+    const int H = t->st.hidden;
+    if (n_text < 0 || (n_text > 0 && !text_tokens)) return fail(c, QTTS_EINVAL, "text tokens");
+    // text rows: role prefix, TTS_PAD, TTS_BOS, the first text token
+    uint32_t tt[6] = {kImStart, kAssistant, kNewline, kTtsPad, kTtsBos, n_text > 0 ? text_tokens[0] : 0u};
+    const int nt = n_text > 0 ? 6 : 5;
+    // codec rows
+    uint32_t ct[7];
+    int nc = 0;
+    if (voice) {
+        const uint32_t v[6] = {kCodecThink, kCodecThinkBos, language_id, kCodecThinkEos, kCodecPad, kCodecBos};
+        for (uint32_t x : v) ct[nc++] = x;
+    } else {
+        const uint32_t v[7] = {kCodecThink, kCodecThinkBos, language_id, kCodecThinkEos, speaker_id, kCodecPad, kCodecBos};
+        for (uint32_t x : v) ct[nc++] = x;
+    }
+    if (n_text == 0) nc--;  // no BOS + first text row
+    for (int i = 0; i < nc; i++)
+        if (ct[i] >= (uint32_t)t->emb.K) return fail(c, QTTS_ERANGE, "codec token id out of range");
+    QTTS_TRY(text_reserve(t, 8));
+    float *T = t->tx_rows;  // [TTS role x3, TTS_PAD, TTS_BOS, text[0]]
+    QTTS_TRY(text_project(t, tt, nt, T));
+    // codec rows (the token buffer is reused in stream order)
+    float *codec = t->pr_codec;
+    HIP_TRY(c, hipMemcpyAsync(t->tx_tok, ct, sizeof(uint32_t) * nc, hipMemcpyHostToDevice, c->stream));
+    launch_embed_rows(c->stream, t->emb, t->tx_tok, 1, nc, codec, H);
+    QTTS_TRY(check_launch(c, "k_embed_rows"));
+    const float *voice_row = nullptr;
+    if (voice) {
+        float *vr = codec + (size_t)7 * H;
+        HIP_TRY(c, hipMemcpyAsync(vr, voice, sizeof(float) * H, hipMemcpyHostToDevice, c->stream));
+        voice_row = vr;
+    }
+    PromptRowsParams P{};
+    int r = 0;
+    for (int i = 0; i < 3; i++) P.a[r++] = T + (size_t)i * H;  // role prefix
+    const float *pad = T + (size_t)3 * H, *bos = T + (size_t)4 * H;
+    if (voice) {
+        for (int i = 0; i < 4; i++, r++) {
+            P.a[r] = codec + (size_t)i * H;
+            P.b[r] = pad;
+        }
+        P.a[r++] = voice_row;
+        P.a[r] = codec + (size_t)4 * H;  // CODEC_PAD
+        P.b[r++] = bos;
+        if (n_text > 0) {
+            P.a[r] = codec + (size_t)5 * H;  // CODEC_BOS
+            P.b[r++] = T + (size_t)5 * H;
+        }
+    } else {
+        for (int i = 0; i < 6; i++, r++) {
+            P.a[r] = codec + (size_t)i * H;
+            P.b[r] = i < 5 ? pad : bos;
+        }
+        if (n_text > 0) {
+            P.a[r] = codec + (size_t)6 * H;  // CODEC_BOS
+            P.b[r++] = T + (size_t)5 * H;
+        }
+    }
+    P.L = r;
+    P.H = H;
+    P.out = t->xp;
+    launch_prompt_rows(c->stream, P);
+    QTTS_TRY(check_launch(c, "k_prompt_rows"));
+    *L = r;
+    return QTTS_OK;
+}
+
+}  // namespace
+
+qtts_status qtts_talker_text_upload(qtts_talker *t, const qtts_text_view *v) {
+    if (!t || !v) return QTTS_EINVAL;
+    qtts_ctx *c = t->ctx;
+    if (t->has_text) return fail(c, QTTS_ESTATE, "text weights already uploaded");
+    const int th = v->text_hidden_size, H = t->st.hidden;
+    if (th <= 0) return fail(c, QTTS_ESHAPE, "text_hidden_size must be positive");
+    QTTS_TRY(check_view(c, &v->text_embedding, v->text_embedding.k, th, "text_embedding"));
+    QTTS_TRY(check_view(c, &v->text_proj_fc1, th, v->text_proj_fc1.n, "text_proj_fc1"));
+    QTTS_TRY(check_view(c, &v->text_proj_fc2, v->text_proj_fc1.n, H, "text_proj_fc2"));
+    if (v->text_embedding.k <= (int)kTtsEos) return fail(c, QTTS_ESHAPE, "text vocab below the TTS special tokens");
+    QTTS_TRY(alloc_q4(c, t->own, v->text_embedding.k, th, &t->text_emb));
+    QTTS_TRY(upload_part(c, &v->text_embedding, t->text_emb, 0));
+    QTTS_TRY(alloc_q4(c, t->own, th, v->text_proj_fc1.n, &t->fc1));
+    QTTS_TRY(upload_part(c, &v->text_proj_fc1, t->fc1, 0));
+    QTTS_TRY(alloc_q4(c, t->own, v->text_proj_fc1.n, H, &t->fc2));
+    QTTS_TRY(upload_part(c, &v->text_proj_fc2, t->fc2, 0));
+    QTTS_TRY(upload_array(c, t->own, v->text_proj_fc1_bias, (size_t)v->text_proj_fc1.n, &t->fc1_b, "text_proj_fc1_bias"));
+    QTTS_TRY(upload_array(c, t->own, v->text_proj_fc2_bias, (size_t)H, &t->fc2_b, "text_proj_fc2_bias"));
+    QTTS_TRY(t->own.alloc(c, &t->pr_codec, (size_t)8 * H));
+    t->text_hidden = th;
+    t->has_text = 1;
+    return QTTS_OK;
+}
+
+qtts_status qtts_embed_text_token(qtts_talker *t, uint32_t token_id, float *out) {
+    if (!t || !out) return QTTS_EINVAL;
+    qtts_ctx *c = t->ctx;
+    QTTS_TRY(text_reserve(t, 1));
+    QTTS_TRY(text_project(t, &token_id, 1, t->tx_rows));
+    HIP_TRY(c, hipMemcpyAsync(out, t->tx_rows, sizeof(float) * t->st.hidden, hipMemcpyDeviceToHost, c->stream));
+    return sync(c);
+}
+
+qtts_status qtts_build_custom_voice_prompt(qtts_talker *t, const uint32_t *text_tokens, int32_t n_text,
+                                           uint32_t speaker_id, uint32_t language_id, const float *voice_embedding,
+                                           float *rows, int32_t *seq_len) {
+    if (!t || !rows || !seq_len) return QTTS_EINVAL;
+    qtts_ctx *c = t->ctx;
+    *seq_len = 0;
+    QTTS_TRY(prefill_buffers(t, kPromptMaxRows));
+    int L = 0;
+    QTTS_TRY(build_prompt(t, text_tokens, n_text, speaker_id, language_id, voice_embedding, &L));
+    HIP_TRY(c, hipMemcpyAsync(rows, t->xp, sizeof(float) * L * t->st.hidden, hipMemcpyDeviceToHost, c->stream));
+    QTTS_TRY(sync(c));
+    *seq_len = L;
+    return QTTS_OK;
+}
+
+qtts_status qtts_prefill_custom_voice(qtts_talker *t, const uint32_t *text_tokens, int32_t n_text, uint32_t speaker_id,
+                                      uint32_t language_id, const float *voice_embedding, qtts_kv *kv,
+                                      float *last_hidden, float *logits, int32_t *position) {
+    if (!t || !kv || !last_hidden || !logits || !position) return QTTS_EINVAL;
+    qtts_ctx *c = t->ctx;
+    *position = 0;
+    const int L = (n_text > 0 ? 1 : 0) + 9;
+    QTTS_TRY(prefill_prepare(t, L, kv));
+    int built = 0;
+    QTTS_TRY(build_prompt(t, text_tokens, n_text, speaker_id, language_id, voice_embedding, &built));
+    qtts_status s = prefill_from_xp(t, built, kv);
+    if (s != QTTS_OK) {
+        kv->len = 0;
+        return s;
+    }
+    const int H = t->st.hidden;
+    HIP_TRY(c, hipMemcpyAsync(last_hidden, t->out, sizeof(float) * H, hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(c, hipMemcpyAsync(logits, t->out + H, sizeof(float) * t->vocab, hipMemcpyDeviceToHost, c->stream));
+    QTTS_TRY(sync(c));
+    *position = built;  // src/generate_new.rs:216
+    return QTTS_OK;
+}
+
+qtts_status qtts_build_trailing_text(qtts_talker *t, const uint32_t *text_tokens, int32_t n_text, float *rows,
+                                     int32_t *n_rows) {
+    if (!t || !rows || !n_rows || n_text < 0 || (n_text > 0 && !text_tokens)) return QTTS_EINVAL;
+    qtts_ctx *c = t->ctx;
+    *n_rows = 0;
+    std::vector<uint32_t> tok;
+    for (int i = 1; i < n_text; i++) tok.push_back(text_tokens[i]);
+    tok.push_back(kTtsEos);
+    const int n = (int)tok.size();
+    QTTS_TRY(text_reserve(t, n));
+    QTTS_TRY(text_project(t, tok.data(), n, t->tx_rows));
+    HIP_TRY(c, hipMemcpyAsync(rows, t->tx_rows, sizeof(float) * n * t->st.hidden, hipMemcpyDeviceToHost, c->stream));
+    QTTS_TRY(sync(c));
+    *n_rows = n;
+    return QTTS_OK;
+}
+
+qtts_status qtts_generate_speech_codes(qtts_talker *t, qtts_predictor *p, const uint32_t *text_tokens, int32_t n_text,
+                                       uint32_t speaker_id, uint32_t language_id, const float *voice_embedding,
+                                       qtts_kv *talker_kv, qtts_kv *predictor_kv, const qtts_loop_params *params,
+                                       uint64_t seed, uint32_t *codes, int32_t *n_frames) {
+    if (!t || !talker_kv || !params || !codes || !n_frames) return QTTS_EINVAL;
+    *n_frames = 0;
+    const int H = t->st.hidden;
+    std::vector<float> last_hidden(H), logits(t->vocab), pad(H);
+    std::vector<float> trailing((size_t)(n_text > 1 ? n_text : 1) * H);
+    int32_t position = 0, rows = 0;
+    QTTS_TRY(qtts_prefill_custom_voice(t, text_tokens, n_text, speaker_id, language_id, voice_embedding, talker_kv,
+                                       last_hidden.data(), logits.data(), &position));
+    QTTS_TRY(qtts_build_trailing_text(t, text_tokens, n_text, trailing.data(), &rows));
+    QTTS_TRY(qtts_embed_text_token(t, kTtsPad, pad.data()));
+    return qtts_generate_codes(t, p, talker_kv, predictor_kv, last_hidden.data(), logits.data(), position,
+                               trailing.data(), rows, pad.data(), params, seed, codes, n_frames);
 }
 
 // ---------------------------------------------------------------------------

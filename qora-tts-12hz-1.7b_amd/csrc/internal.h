@@ -328,6 +328,17 @@ void launch_dec_snake(hipStream_t st, const float *x, const float *alpha, const 
 void launch_gemm_mfma(hipStream_t st, const GemmMfmaParams &p, int mt, int sw, int kc);
 void launch_embed_sum(hipStream_t st, const EmbSumParams &p);
 void launch_advance(hipStream_t st, LoopState *s, int frame_step, int batch = 1);
+// Prompt rows of prefill_custom_voice: out[r] = a[r] (+ b[r] when b[r] is
+// set), H floats per row, r < L <= 10.
+struct PromptRowsParams {
+    const float *a[10];
+    const float *b[10];
+    int L, H;
+    float *out;
+};
+void launch_prompt_rows(hipStream_t st, const PromptRowsParams &p);
+// x[i] = silu(x[i]) = x / (1 + exp(-x)) for i < n (src/gemv.rs:447-451).
+void launch_silu(hipStream_t st, float *x, long long n);
 void launch_embed_rows(hipStream_t st, const DevQ4 &w, const uint32_t *tok, long long tok_stride, int rows, float *out,
                        long long out_stride);
 void launch_argmax_rows(hipStream_t st, const float *logits, int rows, int n, uint32_t *out, long long out_stride,

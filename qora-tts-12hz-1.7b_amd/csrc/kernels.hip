@@ -1168,6 +1168,32 @@ void launch_advance(hipStream_t st, LoopState *s, int frame_step, int batch) {
     hipLaunchKernelGGL(k_advance, dim3(1), dim3((unsigned)((batch + 63) / 64 * 64)), 0, st, s, frame_step, batch);
 }
 
+// The prompt rows of prefill_custom_voice (src/generate_new.rs:84-177): a
+// codec embedding row plus a text-projection row, added element by element
+// in that order, or one row copied as it is.
+__global__ void k_prompt_rows(PromptRowsParams P) {
+    const int j = blockIdx.x * blockDim.x + threadIdx.x, r = blockIdx.y;
+    if (j >= P.H || r >= P.L) return;
+    const float v = P.a[r][j];
+    P.out[(size_t)r * P.H + j] = P.b[r] ? v + P.b[r][j] : v;
+}
+
+void launch_prompt_rows(hipStream_t st, const PromptRowsParams &p) {
+    hipLaunchKernelGGL(k_prompt_rows, dim3((unsigned)((p.H + 255) / 256), (unsigned)p.L), dim3(256), 0, st, p);
+}
+
+// silu between the two text-projection layers (src/talker.rs:111-112).
+__global__ void k_silu(float *x, long long n) {
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    const float v = x[i];
+    x[i] = v / (1.0f + expf(-v));
+}
+
+void launch_silu(hipStream_t st, float *x, long long n) {
+    hipLaunchKernelGGL(k_silu, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, n);
+}
+
 // Row r = embedding row tok[r * tok_stride] of w (embed_lookup_q4,
 // src/gemv.rs:377-400, exact), at out + r * out_stride.
 __global__ void k_embed_rows(DevQ4 w, const uint32_t *tok, long long tok_stride, float *out, long long out_stride) {

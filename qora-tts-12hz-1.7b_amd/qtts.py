@@ -232,6 +232,13 @@ def load_library(path: str = LIB_PATH):
         "qtts_gemv_device": ([vp, vp, vp, vp], i32),
         "qtts_gemm_device": ([vp, vp, vp, i32, vp], i32),
         "qtts_gemv_device_static": ([vp, vp, i32, vp, vp], i32),
+        "qtts_talker_text_upload": ([vp, C.POINTER(TextView)], i32),
+        "qtts_embed_text_token": ([vp, u32, vp], i32),
+        "qtts_build_custom_voice_prompt": ([vp, vp, i32, u32, u32, vp, vp, C.POINTER(i32)], i32),
+        "qtts_prefill_custom_voice": ([vp, vp, i32, u32, u32, vp, vp, vp, vp, C.POINTER(i32)], i32),
+        "qtts_build_trailing_text": ([vp, vp, i32, vp, C.POINTER(i32)], i32),
+        "qtts_generate_speech_codes": ([vp, vp, vp, i32, u32, u32, vp, vp, vp, C.POINTER(LoopParams), C.c_uint64,
+                                        vp, C.POINTER(i32)], i32),
         "qtts_kv_create": ([vp, i32, i32, i32, i32, C.POINTER(vp)], i32),
         "qtts_kv_free": ([vp], None),
         "qtts_kv_len": ([vp], i32),
@@ -289,7 +296,9 @@ def exported_symbols() -> List[str]:
     return [
         "qtts_version", "qtts_ctx_create", "qtts_ctx_destroy", "qtts_last_error", "qtts_ctx_stream",
         "qtts_ctx_synchronize", "qtts_q4_upload", "qtts_q4_free", "qtts_q4_bytes", "qtts_gemv", "qtts_gemm",
-        "qtts_embed_lookup", "qtts_gemv_device", "qtts_gemm_device", "qtts_gemv_device_static", "qtts_kv_create", "qtts_kv_free",
+        "qtts_embed_lookup", "qtts_gemv_device", "qtts_gemm_device", "qtts_gemv_device_static",
+        "qtts_talker_text_upload", "qtts_embed_text_token", "qtts_build_custom_voice_prompt", "qtts_prefill_custom_voice",
+        "qtts_build_trailing_text", "qtts_generate_speech_codes", "qtts_kv_create", "qtts_kv_free",
         "qtts_kv_len", "qtts_kv_clear", "qtts_kv_load", "qtts_kv_store", "qtts_talker_upload", "qtts_talker_free",
         "qtts_forward_with_embedding", "qtts_prefill_talker_raw", "qtts_apply_codec_head",
         "qtts_embed_codec_token", "qtts_predictor_upload", "qtts_predictor_free", "qtts_generate_acoustic_codes",
@@ -494,6 +503,33 @@ class CodePredictorWeights:
 # ---------------------------------------------------------------------------
 # Device objects
 # ---------------------------------------------------------------------------
+TEXT_VOCAB_1P7B = 151936  # Qwen3 text vocab: covers the TTS special tokens (151671-151673)
+
+# Special tokens, src/generate_new.rs:24-36.
+IM_START, ASSISTANT, NEWLINE = 151644, 77091, 198
+TTS_PAD, TTS_BOS, TTS_EOS = 151671, 151672, 151673
+CODEC_THINK, CODEC_THINK_BOS, CODEC_THINK_EOS = 2154, 2156, 2157
+
+
+class TextWeights:
+    """Seeded random-init text embedding + two-layer text projection of
+    TalkerWeights (src/talker.rs:33-56): text_embedding [text_vocab]
+    [text_hidden], fc1 [text_hidden][text_hidden] + bias, fc2 [text_hidden]
+    [hidden] + bias, Q4 like the other weights."""
+
+    def __init__(self, seed: int, text_vocab: int = TEXT_VOCAB_1P7B, text_hidden: int = 2048, hidden: int = 2048):
+        self.text_vocab, self.text_hidden, self.hidden = text_vocab, text_hidden, hidden
+        self.text_embedding = Q4Weight.synthetic(seed, "text.embedding", text_vocab, text_hidden)
+        self.fc1 = Q4Weight.synthetic(seed, "text.fc1", text_hidden, text_hidden)
+        self.fc1_bias = synth_normal_f32(seed, "text.fc1_bias", text_hidden, 0.0, 0.02)
+        self.fc2 = Q4Weight.synthetic(seed, "text.fc2", text_hidden, hidden)
+        self.fc2_bias = synth_normal_f32(seed, "text.fc2_bias", hidden, 0.0, 0.02)
+
+    def view(self) -> "TextView":
+        return TextView(self.text_embedding.view(), self.fc1.view(), self.fc1_bias.ctypes.data, self.fc2.view(),
+                        self.fc2_bias.ctypes.data, self.text_hidden)
+
+
 def _f32(a, n: Optional[int] = None) -> np.ndarray:
     a = np.ascontiguousarray(a, dtype=np.float32)
     if n is not None and a.size < n:
@@ -929,6 +965,51 @@ class Talker(_DeviceObject):
         self.ctx.check(self.ctx.lib.qtts_embed_codec_token(self.h, int(token), _ptr(out)))
         return out
 
+    def attach_text(self, text: "TextWeights"):
+        """Uploads the text embedding and projection (qtts_talker_text_upload)."""
+        self._text_view = text.view()
+        self.ctx.check(self.ctx.lib.qtts_talker_text_upload(self.h, C.byref(self._text_view)))
+
+    # embed_text_token, src/talker.rs:105-116
+    def embed_text_token(self, token: int) -> np.ndarray:
+        out = np.empty(self.cfg.hidden, dtype=np.float32)
+        self.ctx.check(self.ctx.lib.qtts_embed_text_token(self.h, int(token), _ptr(out)))
+        return out
+
+    def build_custom_voice_prompt(self, text_tokens, speaker_id: int, language_id: int, voice_embedding=None):
+        """The rows prefill_custom_voice runs (src/generate_new.rs:60-177), [L][hidden]."""
+        tok = np.ascontiguousarray(text_tokens, dtype=np.uint32)
+        voice = None if voice_embedding is None else _f32(voice_embedding, self.cfg.hidden)
+        rows = np.empty((10, self.cfg.hidden), dtype=np.float32)
+        n = C.c_int32(0)
+        self.ctx.check(self.ctx.lib.qtts_build_custom_voice_prompt(self.h, _ptr(tok) if tok.size else None, tok.size,
+                                                                    speaker_id, language_id, _ptr(voice), _ptr(rows),
+                                                                    C.byref(n)))
+        return rows[: n.value].copy()
+
+    # prefill_custom_voice, src/generate_new.rs:84-188
+    def prefill_custom_voice(self, text_tokens, speaker_id: int, language_id: int, kv: "KvCache",
+                             voice_embedding=None):
+        """Returns (last_hidden, logits, position)."""
+        tok = np.ascontiguousarray(text_tokens, dtype=np.uint32)
+        voice = None if voice_embedding is None else _f32(voice_embedding, self.cfg.hidden)
+        lh = np.empty(self.cfg.hidden, dtype=np.float32)
+        lg = np.empty(self.cfg.vocab, dtype=np.float32)
+        pos = C.c_int32(0)
+        self.ctx.check(self.ctx.lib.qtts_prefill_custom_voice(self.h, _ptr(tok) if tok.size else None, tok.size,
+                                                               speaker_id, language_id, _ptr(voice), kv.h, _ptr(lh),
+                                                               _ptr(lg), C.byref(pos)))
+        return lh, lg, pos.value
+
+    # build_trailing_text, src/generate_new.rs:314-326
+    def build_trailing_text(self, text_tokens) -> np.ndarray:
+        tok = np.ascontiguousarray(text_tokens, dtype=np.uint32)
+        rows = np.empty((max(tok.size, 1), self.cfg.hidden), dtype=np.float32)
+        n = C.c_int32(0)
+        self.ctx.check(self.ctx.lib.qtts_build_trailing_text(self.h, _ptr(tok) if tok.size else None, tok.size,
+                                                              _ptr(rows), C.byref(n)))
+        return rows[: n.value].copy()
+
 
 class CodePredictor(_DeviceObject):
     """CodePredictorWeights in HBM with generate_acoustic_codes."""
@@ -989,6 +1070,25 @@ def generate_codes(talker: Talker, predictor: Optional[CodePredictor], talker_kv
                                           talker_kv.h, predictor_kv.h if predictor_kv is not None else None, _ptr(lh), _ptr(lg),
                                           position, _ptr(tt), tl, _ptr(pad), C.byref(params), seed, _ptr(codes),
                                           C.byref(n)))
+    return codes[:, : n.value].copy()
+
+
+def generate_speech_codes(talker: Talker, predictor: Optional[CodePredictor], text_tokens, speaker_id: int,
+                          language_id: int, talker_kv: KvCache, predictor_kv: Optional[KvCache], params: LoopParams,
+                          seed: int, voice_embedding=None) -> np.ndarray:
+    """generate_speech (src/generate_new.rs:191-300) from token ids to codes on
+    the device: prefill_custom_voice, build_trailing_text, the frame loop.
+    Returns all_codes as [16][n_frames] uint32."""
+    ctx = talker.ctx
+    tok = np.ascontiguousarray(text_tokens, dtype=np.uint32)
+    voice = None if voice_embedding is None else _f32(voice_embedding, talker.cfg.hidden)
+    codes = np.zeros((16, max(params.max_codes, 1)), dtype=np.uint32)
+    n = C.c_int32(0)
+    ctx.check(ctx.lib.qtts_generate_speech_codes(talker.h, predictor.h if predictor is not None else None,
+                                                 _ptr(tok) if tok.size else None, tok.size, speaker_id, language_id,
+                                                 _ptr(voice), talker_kv.h,
+                                                 predictor_kv.h if predictor_kv is not None else None,
+                                                 C.byref(params), seed, _ptr(codes), C.byref(n)))
     return codes[:, : n.value].copy()
 
 

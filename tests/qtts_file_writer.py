@@ -47,16 +47,12 @@ class _Out:
         self.f16v(w.scales)
 
 
-class TextWeights:
-    """Synthetic text embedding + two-layer text projection."""
+class TextWeights(qtts.TextWeights):
+    """Synthetic text embedding + two-layer text projection (fc1 text_hidden ->
+    text_hidden, fc2 text_hidden -> hidden)."""
 
     def __init__(self, seed, text_vocab, text_hidden, hidden):
-        self.text_hidden = text_hidden
-        self.text_embedding = qtts.Q4Weight.synthetic(seed, "text.embedding", text_vocab, text_hidden)
-        self.fc1 = qtts.Q4Weight.synthetic(seed, "text.fc1", text_hidden, text_hidden)
-        self.fc1_bias = qtts.synth_normal_f32(seed, "text.fc1_bias", text_hidden, 0.0, 0.02)
-        self.fc2 = qtts.Q4Weight.synthetic(seed, "text.fc2", text_hidden, hidden)
-        self.fc2_bias = qtts.synth_normal_f32(seed, "text.fc2_bias", hidden, 0.0, 0.02)
+        super().__init__(seed, text_vocab, text_hidden, hidden)
 
 
 def _layer(o, L):  # src/save.rs:61-72
