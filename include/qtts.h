@@ -228,6 +228,13 @@ qtts_status qtts_prefill_talker_raw(qtts_talker *t, const float *x, int32_t seq_
 qtts_status qtts_apply_codec_head(qtts_talker *t, const float *hidden, float *logits);
 /* embed_codec_token(weights, token) -> [hidden]; src/talker.rs:152-154. */
 qtts_status qtts_embed_codec_token(qtts_talker *t, uint32_t token_id, float *out);
+/* forward_talker_decode(weights, token, is_text, kv, position) -> the
+ * final-normed hidden [hidden_size]; src/talker.rs:161-258 (the legacy decode
+ * step).  The row fed is embed_text_token(token) when is_text (text weights
+ * uploaded, else QTTS_ESTATE) and embed_codec_token(token) otherwise; a token
+ * past its table is QTTS_ERANGE.  The cache gains one row. */
+qtts_status qtts_forward_talker_decode(qtts_talker *t, uint32_t token_id, int32_t is_text, qtts_kv *kv,
+                                       int32_t position, float *hidden);
 
 /* Prompt assembly (src/talker.rs:105-116, src/generate_new.rs:60-326).  The
  * text weights ride with the talker; every step below runs on the device.  */
@@ -280,6 +287,14 @@ qtts_status qtts_generate_acoustic_codes(qtts_predictor *p, const float *talker_
 /* get_acoustic_embeddings_sum(weights, codes) -> [embed_dim];
  * src/code_predictor.rs:280-293.  codes holds num_groups entries. */
 qtts_status qtts_get_acoustic_embeddings_sum(qtts_predictor *p, const uint32_t *codes, float *out);
+/* predict_codes(weights, talker_hidden, kv, _position) -> num_groups rows
+ * of logits; src/code_predictor.rs:126-213 (the legacy single step): the
+ * projected talker_hidden goes through the stack at the cache offset (RoPE
+ * at that offset) and every head reads the final-normed row.  logits is
+ * [num_groups][cp_vocab].  The cache is NOT cleared and gains one row;
+ * QTTS_ERANGE when it is full or the offset passes the device RoPE table
+ * (4096 rows, fewer when max_position is smaller). */
+qtts_status qtts_predict_codes(qtts_predictor *p, const float *talker_hidden, qtts_kv *kv, float *logits);
 
 /* ------------------------------------------------------------------------ */
 /* Sampler and frame loop (src/generate_new.rs)                              */
@@ -289,6 +304,17 @@ qtts_status qtts_get_acoustic_embeddings_sum(qtts_predictor *p, const uint32_t *
  * src/generate_new.rs:329-391 with simple_rand 17-22.  *rng is updated. */
 qtts_status qtts_sample_token(qtts_ctx *ctx, const float *logits, int32_t vocab, const qtts_sampler *params,
                               const uint32_t *prev_tokens, int32_t n_prev, uint64_t *rng, uint32_t *token);
+/* sample_top_k(logits, temperature, top_k, rng) of the legacy generator,
+ * src/generate.rs:50-84, on the device: temperature <= 0 is the argmax (the
+ * last index of the maximum); otherwise the top_k largest logits, sorted
+ * descending (ties, which the reference leaves unspecified, by ascending
+ * index), p_i = exp((l_i - l_0) / temperature) normalised and summed in
+ * that order against simple_rand, falling back to the k-th.  vocab is
+ * 1..4096 (QTTS_ESHAPE); top_k < 1 with temperature > 0 is QTTS_EINVAL and
+ * a NaN logit QTTS_ENAN (the reference panics on both).  *rng advances
+ * only when sampling. */
+qtts_status qtts_sample_top_k(qtts_ctx *ctx, const float *logits, int32_t vocab, float temperature, int32_t top_k,
+                              uint64_t *rng, uint32_t *token);
 
 /* The per-frame loop of generate_speech, src/generate_new.rs:229-300, run on
  * the device from the prefill outputs (last_hidden, logits) at `position`.

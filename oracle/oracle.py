@@ -27,7 +27,9 @@ _lib = None
 
 
 def _p(a):
-    return None if a is None else C.c_void_p(a.ctypes.data)
+    # data_as keeps a reference to the array, so a temporary (a contiguous
+    # copy made in the argument list) lives until the foreign call returns
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
 
 
 def load():
@@ -94,6 +96,9 @@ def load():
                               C.POINTER(u32)], i32),
         "qor_generate_codes": ([vp, vp, vp, vp, vp, vp, i32, vp, i32, vp, C.POINTER(qtts.LoopParams), C.c_uint64,
                                 vp, C.POINTER(i32), i32], i32),
+        "qor_sample_top_k": ([vp, i32, C.c_float, i32, C.POINTER(C.c_uint64), C.POINTER(u32)], i32),
+        "qor_predict_codes": ([vp, vp, vp, vp, i32], i32),
+        "qor_forward_talker_decode": ([vp, vp, u32, i32, vp, i32, vp, i32], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -217,6 +222,16 @@ def sample_token(logits, temperature=0.8, top_k=50, repetition_penalty=1.05, pre
     return int(tok.value), int(st.value)
 
 
+def sample_top_k(logits, temperature, top_k, rng=0):
+    """sample_top_k of the legacy generator (src/generate.rs:50-84):
+    (token, new_rng_state)."""
+    lg = f32(logits)
+    st = C.c_uint64(rng)
+    tok = C.c_uint32(0)
+    _check(load().qor_sample_top_k(_p(lg), lg.size, float(temperature), int(top_k), C.byref(st), C.byref(tok)))
+    return int(tok.value), int(st.value)
+
+
 # --- KV, talker, predictor --------------------------------------------------
 class Kv:
     def __init__(self, num_layers, num_kv_heads, head_dim, capacity):
@@ -230,7 +245,8 @@ class Kv:
         load().qor_kv_clear(self.h)
 
     def load(self, k, v, length):
-        _check(load().qor_kv_load(self.h, _p(f32(k)), _p(f32(v)), length))
+        k, v = f32(k), f32(v)  # keep the contiguous copies alive over the call
+        _check(load().qor_kv_load(self.h, _p(k), _p(v), length))
 
     def store(self):
         L, H, D = self.shape
@@ -309,6 +325,13 @@ class CodePredictor:
         load().qor_get_acoustic_embeddings_sum(self.h, _p(cs), _p(out))
         return out
 
+    def predict_codes(self, talker_hidden, kv: Kv) -> np.ndarray:
+        """predict_codes (src/code_predictor.rs:126-213): [num_groups][vocab]."""
+        out = np.empty((self.num_groups, self.cfg.vocab), dtype=np.float32)
+        _check(load().qor_predict_codes(self.h, _p(f32(talker_hidden, self.talker_hidden)), kv.h, _p(out),
+                                        self.nthreads))
+        return out
+
     def __del__(self):
         try:
             load().qor_predictor_free(self.h)
@@ -374,6 +397,13 @@ class Text:
                                                language_id, _p(v), kv.h, _p(lh), _p(lg), C.byref(pos),
                                                self.nthreads))
         return lh, lg, pos.value
+
+    def forward_talker_decode(self, token: int, is_text: bool, kv: Kv, position: int) -> np.ndarray:
+        """forward_talker_decode (src/talker.rs:161-258): the final-normed hidden."""
+        out = np.empty(self.hidden, dtype=np.float32)
+        _check(load().qor_forward_talker_decode(self.talker.h, self.h, token, 1 if is_text else 0, kv.h, position,
+                                                _p(out), self.nthreads))
+        return out
 
     def build_trailing_text(self, tokens) -> np.ndarray:
         t, tp = self._tok(tokens)

@@ -557,6 +557,10 @@ int32_t qor_prefill_talker_raw(const qor_talker *t, const float *x_in, int32_t s
     return rc;
 }
 
+int32_t qor_talker_hidden(const qor_talker *t) { return t->w.hidden_size; }
+int32_t qor_talker_vocab(const qor_talker *t) { return t->w.codec_head.n; }
+int32_t qor_talker_codec_rows(const qor_talker *t) { return t->w.codec_embedding.k; }
+
 void qor_apply_codec_head(const qor_talker *t, const float *hidden, float *logits, int32_t nthreads) {
     qor_gemv(hidden, &t->w.codec_head, logits, nthreads);
 }
@@ -580,7 +584,11 @@ qor_predictor *qor_predictor_new(const qtts_predictor_view *w) {
      * reference's formula, built for the positions that exist
      * (src/loader.rs:859-874 builds 65536). */
     const int32_t half = w->head_dim / 2;
-    int32_t rows = w->num_groups + 2;
+    /* generate_acoustic_codes restarts the cache every frame (positions
+     * 0..num_groups); predict_codes keeps appending, so the table covers
+     * 4096 positions (past them the oracle refuses: it would skip the
+     * rotation where the reference's 65536-row table does not). */
+    int32_t rows = 4096;
     if (rows > w->max_position) rows = w->max_position;
     p->st.num_layers = w->num_layers;
     p->st.layers = w->layers;
@@ -670,6 +678,30 @@ int32_t qor_generate_acoustic_codes(const qor_predictor *p, const float *talker_
     free(emb);
     free(logits);
     free(h);
+    free(x);
+    return rc;
+}
+
+/* predict_codes, src/code_predictor.rs:126-213: project_input, one decode
+ * step at the cache offset (RoPE at the offset), the final norm, then every
+ * lm_head on the same row. */
+int32_t qor_predict_codes(const qor_predictor *p, const float *talker_hidden, qor_kv *kv, float *logits,
+                          int32_t nthreads) {
+    const int32_t hidden = p->w.hidden_size;
+    if (kv->len >= p->st.max_pos && kv->len < p->w.max_position) return QTTS_ERANGE;
+    float *x = (float *)xcalloc((size_t)hidden, sizeof(float));
+    project_input(p, talker_hidden, x, nthreads);
+    int32_t rc = stack_decode(&p->st, x, kv, -1, nthreads);
+    if (rc == QTTS_OK) {
+        float *h = (float *)xcalloc((size_t)hidden, sizeof(float));
+        qor_rms_norm_f16(x, p->w.final_norm_gamma, hidden, h);
+        size_t off = 0;
+        for (int32_t g = 0; g < p->w.num_groups; g++) {
+            qor_gemv(h, &p->w.lm_heads[g], logits + off, nthreads);
+            off += (size_t)p->w.lm_heads[g].n;
+        }
+        free(h);
+    }
     free(x);
     return rc;
 }
@@ -774,6 +806,48 @@ int32_t qor_sample_token(const float *logits, int32_t vocab, const qtts_sampler 
         }
     }
     free(s);
+    return QTTS_OK;
+}
+
+/* generate::sample_top_k, src/generate.rs:50-84 (the legacy loop's sampler):
+ * greedy (last of equal maxima) when temperature <= 0; else the top_k
+ * logits in descending order (the reference's sort_unstable_by leaves equal
+ * logits in no fixed order: here equal logits go by ascending index),
+ * p_i = expf((l_i - l_0) / T) summed in that order, divided by the sum, and
+ * the first i in that order with r < cumsum, else the k-th index.  NaN is
+ * QTTS_ENAN (partial_cmp().unwrap()); top_k < 1 is QTTS_EINVAL (an empty
+ * top list panics at indices[0]). */
+int32_t qor_sample_top_k(const float *logits, int32_t vocab, float temperature, int32_t top_k, uint64_t *rng,
+                         uint32_t *token) {
+    for (int32_t i = 0; i < vocab; i++)
+        if (logits[i] != logits[i]) return QTTS_ENAN;
+    if (temperature <= 0.0f) return qor_argmax(logits, vocab, token);
+    if (top_k < 1 || vocab < 1) return QTTS_EINVAL;
+    const int32_t k = top_k < vocab ? top_k : vocab;
+    scored *idx = (scored *)xcalloc((size_t)vocab, sizeof(scored));
+    for (int32_t i = 0; i < vocab; i++) {
+        idx[i].v = logits[i];
+        idx[i].i = i;
+    }
+    qsort(idx, (size_t)vocab, sizeof(scored), scored_cmp);
+    float *probs = (float *)xcalloc((size_t)k, sizeof(float));
+    const float max_logit = idx[0].v;
+    float sum = 0.0f;
+    for (int32_t i = 0; i < k; i++) probs[i] = expf((idx[i].v - max_logit) / temperature);
+    for (int32_t i = 0; i < k; i++) sum += probs[i];
+    for (int32_t i = 0; i < k; i++) probs[i] /= sum;
+    const float r = qor_simple_rand(rng);
+    float cumsum = 0.0f;
+    *token = (uint32_t)idx[k - 1].i;
+    for (int32_t i = 0; i < k; i++) {
+        cumsum += probs[i];
+        if (r < cumsum) {
+            *token = (uint32_t)idx[i].i;
+            break;
+        }
+    }
+    free(probs);
+    free(idx);
     return QTTS_OK;
 }
 

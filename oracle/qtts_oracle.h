@@ -72,6 +72,10 @@ typedef struct qor_talker qor_talker;
  * builds the RoPE table, as load_talker does (src/loader.rs:768-775). */
 qor_talker *qor_talker_new(const qtts_talker_view *w);
 void qor_talker_free(qor_talker *t);
+/* hidden_size, codec vocab and codec embedding rows of the talker. */
+int32_t qor_talker_hidden(const qor_talker *t);
+int32_t qor_talker_vocab(const qor_talker *t);
+int32_t qor_talker_codec_rows(const qor_talker *t);
 /* forward_with_embedding, src/talker.rs:263-360.  out = [hidden ++ logits]. */
 int32_t qor_forward_with_embedding(const qor_talker *t, const float *embedding, qor_kv *kv, int32_t position,
                                    float *out, int32_t nthreads);
@@ -85,6 +89,7 @@ void qor_embed_codec_token(const qor_talker *t, uint32_t token_id, float *out);
 
 /* --- src/code_predictor.rs ----------------------------------------------- */
 typedef struct qor_predictor qor_predictor;
+typedef struct qor_text qor_text;
 qor_predictor *qor_predictor_new(const qtts_predictor_view *w);
 void qor_predictor_free(qor_predictor *p);
 /* generate_acoustic_codes, src/code_predictor.rs:218-273. */
@@ -116,8 +121,20 @@ int64_t qor_decoder_num_samples(const qtts_decoder_view *w, int32_t frames);
  * for a code past the codebook or too small an output buffer. */
 int32_t qor_decode_to_audio(const qtts_decoder_view *w, const uint32_t *codes, int32_t frames, int32_t ld,
                             float *audio, int64_t capacity, int64_t *n_samples, int32_t nthreads);
+/* generate::sample_top_k, src/generate.rs:50-84 (equal logits by index). */
+int32_t qor_sample_top_k(const float *logits, int32_t vocab, float temperature, int32_t top_k, uint64_t *rng,
+                         uint32_t *token);
+/* predict_codes, src/code_predictor.rs:126-213: one step of talker_hidden
+ * through the predictor at the cache offset, then all num_groups heads on the
+ * final-normed row: logits [num_groups][vocab]. */
+int32_t qor_predict_codes(const qor_predictor *p, const float *talker_hidden, qor_kv *kv, float *logits,
+                          int32_t nthreads);
+/* forward_talker_decode, src/talker.rs:161-258: the final-normed hidden of
+ * one step fed embed_text_token (is_text) or embed_codec_token. */
+int32_t qor_forward_talker_decode(const qor_talker *t, const qor_text *x, uint32_t token, int32_t is_text,
+                                  qor_kv *kv, int32_t position, float *hidden, int32_t nthreads);
+
 /* --- prompt assembly (qtts_oracle_prompt.c) ------------------------------ */
-typedef struct qor_text qor_text;
 /* The text embedding and projection of TalkerWeights (src/talker.rs:33-56). */
 qor_text *qor_text_new(const qtts_text_view *w);
 void qor_text_free(qor_text *x);

@@ -192,3 +192,28 @@ int32_t qor_generate_speech_codes(const qor_talker *t, const qor_predictor *p, c
     free(pad);
     return rc;
 }
+
+/* forward_talker_decode, src/talker.rs:161-258: embed_text_token (is_text)
+ * or embed_codec_token, then forward_with_embedding's step; the final-normed
+ * hidden state (the first hidden values forward_with_embedding returns). */
+int32_t qor_forward_talker_decode(const qor_talker *t, const qor_text *x, uint32_t token, int32_t is_text,
+                                  qor_kv *kv, int32_t position, float *hidden, int32_t nthreads) {
+    if (is_text && !x) return QTTS_EINVAL;
+    const int32_t hid = qor_talker_hidden(t), vocab = qor_talker_vocab(t);
+    float *emb = (float *)calloc((size_t)hid, sizeof(float));
+    float *out = (float *)calloc((size_t)hid + vocab, sizeof(float));
+    if (!emb || !out) abort();
+    int32_t rc = QTTS_OK;
+    if (is_text) {
+        rc = qor_embed_text_token(x, token, emb, nthreads);
+    } else if (token >= (uint32_t)qor_talker_codec_rows(t)) {
+        rc = QTTS_ERANGE;
+    } else {
+        qor_embed_codec_token(t, token, emb);
+    }
+    if (rc == QTTS_OK) rc = qor_forward_with_embedding(t, emb, kv, position, out, nthreads);
+    if (rc == QTTS_OK) memcpy(hidden, out, sizeof(float) * hid);
+    free(emb);
+    free(out);
+    return rc;
+}

@@ -29,6 +29,7 @@ constexpr size_t kPartialFloats = (size_t)1 << 20;  // split-K partials
 constexpr int kCounters = 8192;
 constexpr size_t kAttnPartFloats = (size_t)4 << 20;
 constexpr int kAttnCounters = 1024;
+constexpr int kPredictorRopeRows = 4096;
 
 }  // namespace
 
@@ -684,7 +685,7 @@ struct qtts_predictor {
     uint64_t serial = ++g_serial;
     Owner own;
     Stack st;
-    int talker_hidden = 0, groups = 0, vocab = 0, embed_dim = 0;
+    int talker_hidden = 0, groups = 0, vocab = 0, embed_dim = 0, max_pos = 0;
     bool identity_proj = false;
     DevQ4 in_proj{};
     float *bias = nullptr;
@@ -1654,13 +1655,21 @@ qtts_status enqueue_talker_step(qtts_talker *t, qtts_kv *kv, float *hidden_out, 
 
 }  // namespace
 
-qtts_status qtts_forward_with_embedding(qtts_talker *t, const float *embedding, qtts_kv *kv, int32_t position,
-                                        float *out) {
-    if (!t || !embedding || !out) return QTTS_EINVAL;
+namespace {
+
+qtts_status talker_step_check(qtts_talker *t, qtts_kv *kv, int32_t position) {
     qtts_ctx *c = t->ctx;
     QTTS_TRY(check_kv(c, t->st, kv));
     if (position < 0 || position >= t->max_pos) return fail(c, QTTS_ERANGE, "position beyond the RoPE table");
     if (kv->len + 1 > kv->cap) return fail(c, QTTS_ERANGE, "kv cache full");
+    return QTTS_OK;
+}
+
+// forward_with_embedding (src/talker.rs:263-360) of the embedding already in
+// t->x (enqueued before this call); [hidden ++ logits] to the host `out`
+// (out_n floats of it).
+qtts_status talker_step_x(qtts_talker *t, qtts_kv *kv, int32_t position, float *out, int out_n) {
+    qtts_ctx *c = t->ctx;
     const int hidden = t->st.hidden;
     if (engine_enabled() && eng_talker_fits(kv->cap)) {
         QTTS_TRY(eng_init(c));
@@ -1673,23 +1682,32 @@ qtts_status qtts_forward_with_embedding(qtts_talker *t, const float *embedding, 
             }));
             t->step_kv = kv->serial;
         }
-        HIP_TRY(c, hipMemcpyAsync(t->x, embedding, sizeof(float) * hidden, hipMemcpyHostToDevice, c->stream));
         QTTS_TRY(eng_reset(c, position, kv->len, 0));
         QTTS_TRY(eng_launch(c, *t->step_prog, 0, c->d_small, 1));
-        HIP_TRY(c, hipMemcpyAsync(out, t->out, sizeof(float) * (hidden + t->vocab), hipMemcpyDeviceToHost, c->stream));
+        HIP_TRY(c, hipMemcpyAsync(out, t->out, sizeof(float) * out_n, hipMemcpyDeviceToHost, c->stream));
         QTTS_TRY(sync(c));
         QTTS_TRY(eng_status_check(c, "forward_with_embedding"));
         kv->len += 1;
         return QTTS_OK;
     }
     t->nsplit = attn_nsplit(kv->cap, 16);
-    HIP_TRY(c, hipMemcpyAsync(t->x, embedding, sizeof(float) * hidden, hipMemcpyHostToDevice, c->stream));
     QTTS_TRY(set_state(t, position, kv->len));
     QTTS_TRY(enqueue_talker_step(t, kv, t->out, t->out + hidden, nullptr, 0));
-    HIP_TRY(c, hipMemcpyAsync(out, t->out, sizeof(float) * (hidden + t->vocab), hipMemcpyDeviceToHost, c->stream));
+    HIP_TRY(c, hipMemcpyAsync(out, t->out, sizeof(float) * out_n, hipMemcpyDeviceToHost, c->stream));
     QTTS_TRY(sync(c));
     kv->len += 1;
     return QTTS_OK;
+}
+
+}  // namespace
+
+qtts_status qtts_forward_with_embedding(qtts_talker *t, const float *embedding, qtts_kv *kv, int32_t position,
+                                        float *out) {
+    if (!t || !embedding || !out) return QTTS_EINVAL;
+    qtts_ctx *c = t->ctx;
+    QTTS_TRY(talker_step_check(t, kv, position));
+    HIP_TRY(c, hipMemcpyAsync(t->x, embedding, sizeof(float) * t->st.hidden, hipMemcpyHostToDevice, c->stream));
+    return talker_step_x(t, kv, position, out, t->st.hidden + t->vocab);
 }
 
 // Prefill layers on the GEMV path: row chunks of up to kMaxM tokens, in
@@ -1952,8 +1970,9 @@ constexpr uint32_t kCodecThink = 2154, kCodecThinkBos = 2156, kCodecThinkEos = 2
 constexpr int kPromptMaxRows = 10;
 
 qtts_status text_reserve(qtts_talker *t, int n) {
-    if (n <= t->tx_cap) return QTTS_OK;
     qtts_ctx *c = t->ctx;
+    if (!t->has_text) return fail(c, QTTS_ESTATE, "no text weights: call qtts_talker_text_upload first");
+    if (n <= t->tx_cap) return QTTS_OK;
     for (void *p : {(void *)t->tx_raw, (void *)t->tx_h, (void *)t->tx_rows, (void *)t->tx_tok})
         if (p) (void)hipFree(p);
     t->tx_raw = t->tx_h = t->tx_rows = nullptr;
@@ -2181,6 +2200,22 @@ qtts_status qtts_generate_speech_codes(qtts_talker *t, qtts_predictor *p, const 
                                trailing.data(), rows, pad.data(), params, seed, codes, n_frames);
 }
 
+qtts_status qtts_forward_talker_decode(qtts_talker *t, uint32_t token_id, int32_t is_text, qtts_kv *kv,
+                                       int32_t position, float *hidden) {
+    if (!t || !hidden) return QTTS_EINVAL;
+    qtts_ctx *c = t->ctx;
+    QTTS_TRY(talker_step_check(t, kv, position));
+    if (is_text) {
+        QTTS_TRY(text_project(t, &token_id, 1, t->x));
+    } else {
+        if (token_id >= (uint32_t)t->emb.K) return fail(c, QTTS_ERANGE, "token id out of range");
+        HIP_TRY(c, hipMemcpyAsync(c->d_small, &token_id, 4, hipMemcpyHostToDevice, c->stream));
+        launch_embed_row(c->stream, t->emb, c->d_small, t->x, nullptr);
+        QTTS_TRY(check_launch(c, "k_embed_row"));
+    }
+    return talker_step_x(t, kv, position, hidden, t->st.hidden);
+}
+
 // ---------------------------------------------------------------------------
 qtts_status qtts_predictor_upload(qtts_ctx *c, const qtts_predictor_view *v, qtts_predictor **out) {
     if (!c || !v || !out) return QTTS_EINVAL;
@@ -2225,10 +2260,13 @@ qtts_status qtts_predictor_upload(qtts_ctx *c, const qtts_predictor_view *v, qtt
     if ((s = upload_array(c, p->own, v->final_norm_gamma, (size_t)hidden, &p->st.final_g, "final_norm_gamma")) !=
         QTTS_OK)
         return bail(s);
-    // Positions 0..num_groups occur (the cache restarts every frame); rows
-    // past max_position skip the rotation as src/code_predictor.rs:107 does.
-    int rows = p->groups + 2;
+    // generate_acoustic_codes restarts its cache every frame (positions
+    // 0..num_groups); predict_codes keeps appending, so the table covers 4096
+    // positions (qtts_predict_codes refuses later ones).  Rows past
+    // max_position skip the rotation as src/code_predictor.rs:107 does.
+    int rows = kPredictorRopeRows;
     if (rows > v->max_position) rows = v->max_position;
+    p->max_pos = v->max_position;
     if (rows < 1) return bail(fail(c, QTTS_EINVAL, "max_position must be positive"));
     if ((s = upload_rope(c, p->own, v->head_dim, rows, v->rope_theta, v->rope_cos, v->rope_sin, &p->st)) != QTTS_OK) return bail(s);
     p->st.rope_skip_oob = 1;
@@ -2363,6 +2401,53 @@ qtts_status qtts_generate_acoustic_codes(qtts_predictor *p, const float *talker_
     return QTTS_OK;
 }
 
+qtts_status qtts_predict_codes(qtts_predictor *p, const float *talker_hidden, qtts_kv *kv, float *logits) {
+    if (!p || !talker_hidden || !logits) return QTTS_EINVAL;
+    qtts_ctx *c = p->ctx;
+    QTTS_TRY(check_kv(c, p->st, kv));
+    const int offset = kv->len, H = p->st.hidden;
+    if (offset + 1 > kv->cap) return fail(c, QTTS_ERANGE, "predictor cache full");
+    if (offset >= p->st.rope_rows && offset < p->max_pos)
+        return fail(c, QTTS_ERANGE, "predict_codes: position past the 4096-row RoPE table");
+    const size_t nlog = (size_t)p->groups * p->vocab;
+    QTTS_TRY(ensure_staging(c, 0, nlog));
+    HIP_TRY(c, hipMemcpyAsync(p->in2, talker_hidden, sizeof(float) * p->talker_hidden, hipMemcpyHostToDevice,
+                              c->stream));
+    // project_input (src/code_predictor.rs:51-61)
+    if (p->identity_proj) {
+        HIP_TRY(c, hipMemcpyAsync(p->x2, p->in2, sizeof(float) * H, hipMemcpyDeviceToDevice, c->stream));
+    } else {
+        GemvParams g = gemv_base(c, p->in_proj, 1);
+        g.prologue = PRO_PLAIN;
+        g.x = p->in2;
+        g.ldx = p->talker_hidden;
+        g.epilogue = EPI_STORE;
+        g.y = p->x2;
+        g.ldy = H;
+        g.bias = p->bias;
+        QTTS_TRY(run_gemv(c, g));
+    }
+    // one decode step at the cache offset (RoPE at the offset,
+    // src/code_predictor.rs:147-156), then every head on the final-normed row
+    QTTS_TRY(enqueue_layers(c, p->st, kv, p->x2, p->q2, p->a2, p->h2, 1, nullptr, offset, nullptr, offset,
+                            attn_nsplit(kv->cap, 1), nullptr));
+    for (int g = 0; g < p->groups; g++) {
+        GemvParams q = gemv_base(c, p->heads[g], 1);
+        q.prologue = PRO_RMSNORM;
+        q.x = p->x2;
+        q.ldx = H;
+        q.gamma = p->st.final_g;
+        q.epilogue = EPI_STORE;
+        q.y = c->d_out + (size_t)g * p->vocab;
+        q.ldy = p->vocab;
+        QTTS_TRY(run_gemv(c, q));
+    }
+    HIP_TRY(c, hipMemcpyAsync(logits, c->d_out, sizeof(float) * nlog, hipMemcpyDeviceToHost, c->stream));
+    QTTS_TRY(sync(c));
+    kv->len = offset + 1;
+    return QTTS_OK;
+}
+
 qtts_status qtts_get_acoustic_embeddings_sum(qtts_predictor *p, const uint32_t *codes, float *out) {
     if (!p || !codes || !out) return QTTS_EINVAL;
     qtts_ctx *c = p->ctx;
@@ -2417,6 +2502,35 @@ qtts_status qtts_sample_token(qtts_ctx *c, const float *logits, int32_t vocab, c
     *token = small[0];
     std::memcpy(rng, &small[2], 8);
     if (small[1] != 0) return fail(c, (qtts_status)small[1], "NaN in the sampler (src/generate_new.rs:365)");
+    return QTTS_OK;
+}
+
+qtts_status qtts_sample_top_k(qtts_ctx *c, const float *logits, int32_t vocab, float temperature, int32_t top_k,
+                              uint64_t *rng, uint32_t *token) {
+    if (!c || !logits || !rng || !token) return QTTS_EINVAL;
+    if (vocab <= 0 || vocab > kTopKMaxVocab) return fail(c, QTTS_ESHAPE, "sample_top_k: vocab must be 1..4096");
+    if (temperature > 0.0f && top_k < 1) return fail(c, QTTS_EINVAL, "sample_top_k: top_k < 1 (the reference panics)");
+    QTTS_TRY(ensure_staging(c, (size_t)vocab, 0));
+    // d_small: [0] token, [1] status, [2..3] rng
+    uint32_t small[4] = {0, 0, 0, 0};
+    std::memcpy(&small[2], rng, 8);
+    HIP_TRY(c, hipMemcpyAsync(c->d_in, logits, sizeof(float) * vocab, hipMemcpyHostToDevice, c->stream));
+    HIP_TRY(c, hipMemcpyAsync(c->d_small, small, sizeof(small), hipMemcpyHostToDevice, c->stream));
+    TopKParams P{};
+    P.logits = c->d_in;
+    P.vocab = vocab;
+    P.temperature = temperature;
+    P.top_k = top_k;
+    P.rng = reinterpret_cast<uint64_t *>(c->d_small + 2);
+    P.token_out = c->d_small;
+    P.status = reinterpret_cast<int *>(c->d_small + 1);
+    launch_sample_top_k(c->stream, P);
+    QTTS_TRY(check_launch(c, "k_sample_top_k"));
+    HIP_TRY(c, hipMemcpyAsync(small, c->d_small, sizeof(small), hipMemcpyDeviceToHost, c->stream));
+    QTTS_TRY(sync(c));
+    if (small[1] != 0) return fail(c, (qtts_status)small[1], "sample_top_k: NaN logits (the reference panics)");
+    *token = small[0];
+    std::memcpy(rng, &small[2], 8);
     return QTTS_OK;
 }
 

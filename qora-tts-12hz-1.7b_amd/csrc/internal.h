@@ -339,6 +339,18 @@ struct PromptRowsParams {
 void launch_prompt_rows(hipStream_t st, const PromptRowsParams &p);
 // x[i] = silu(x[i]) = x / (1 + exp(-x)) for i < n (src/gemv.rs:447-451).
 void launch_silu(hipStream_t st, float *x, long long n);
+// generate::sample_top_k (src/generate.rs:50-84) on one workgroup, vocab <= 4096.
+struct TopKParams {
+    const float *logits;
+    int vocab;
+    float temperature;
+    int top_k;
+    uint64_t *rng;
+    uint32_t *token_out;
+    int *status;
+};
+constexpr int kTopKMaxVocab = 4096;
+void launch_sample_top_k(hipStream_t st, const TopKParams &p);
 void launch_embed_rows(hipStream_t st, const DevQ4 &w, const uint32_t *tok, long long tok_stride, int rows, float *out,
                        long long out_stride);
 void launch_argmax_rows(hipStream_t st, const float *logits, int rows, int n, uint32_t *out, long long out_stride,

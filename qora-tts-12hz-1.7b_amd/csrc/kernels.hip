@@ -1194,6 +1194,104 @@ void launch_silu(hipStream_t st, float *x, long long n) {
     hipLaunchKernelGGL(k_silu, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st, x, n);
 }
 
+// generate::sample_top_k (src/generate.rs:50-84), the legacy sampler:
+//  - temperature <= 0: greedy, the last of equal maxima (Iterator::max_by);
+//  - else the top_k largest logits in descending order (the reference's
+//    sort_unstable_by leaves equal logits in an unspecified order; here they
+//    go by ascending index), p_i = exp((l_i - l_0) / T) summed in that
+//    order, each divided by the sum, then the first i in that order with
+//    r < cumsum, else the k-th index.
+// A NaN logit (partial_cmp().unwrap() panics) sets *status = QTTS_ENAN.  The
+// sort is a bitonic sort of (logit, index) pairs in LDS; the sums run on one
+// thread in the reference's order.
+__global__ __launch_bounds__(1024) void k_sample_top_k(TopKParams P) {
+    __shared__ float key[kTopKMaxVocab];
+    __shared__ int idx[kTopKMaxVocab];
+    __shared__ int s_nan;
+    const int tid = threadIdx.x, V = P.vocab;
+    int n2 = 1;
+    while (n2 < V) n2 <<= 1;
+    if (tid == 0) s_nan = 0;
+    __syncthreads();
+    int nan = 0;
+    for (int i = tid; i < n2; i += blockDim.x) {
+        const float v = i < V ? P.logits[i] : -INFINITY;
+        if (v != v) nan = 1;
+        key[i] = v;
+        idx[i] = i < V ? i : 0x7fffffff;
+    }
+    if (nan) atomicOr(&s_nan, 1);
+    __syncthreads();
+    if (s_nan) {
+        if (tid == 0) {
+            *P.status = QTTS_ENAN;
+            *P.token_out = 0u;
+        }
+        return;
+    }
+    if (P.temperature <= 0.0f) {
+        // the last index of the maximum: thread 0 scans in index order
+        if (tid == 0) {
+            int best = 0;
+            for (int i = 1; i < V; i++)
+                if (key[i] >= key[best]) best = i;
+            *P.token_out = (uint32_t)best;
+            *P.status = 0;
+        }
+        return;
+    }
+    // bitonic sort, descending by logit, ascending index among equals
+    for (int size = 2; size <= n2; size <<= 1) {
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            for (int i = tid; i < n2; i += blockDim.x) {
+                const int j = i ^ stride;
+                if (j > i) {
+                    const bool desc = (i & size) == 0;
+                    const float ki = key[i], kj = key[j];
+                    const int ii = idx[i], ij = idx[j];
+                    const bool i_first = ki > kj || (ki == kj && ii < ij);
+                    if (desc != i_first) {
+                        key[i] = kj;
+                        key[j] = ki;
+                        idx[i] = ij;
+                        idx[j] = ii;
+                    }
+                }
+            }
+            __syncthreads();
+        }
+    }
+    if (tid == 0) {
+        const int k = P.top_k < V ? P.top_k : V;
+        const float maxv = key[0];
+        float sum = 0.0f;
+        for (int i = 0; i < k; i++) {
+            const float p = (float)exp((double)((key[i] - maxv) / P.temperature));
+            key[i] = p;
+            sum += p;
+        }
+        for (int i = 0; i < k; i++) key[i] /= sum;
+        uint64_t st = *P.rng;
+        const float r = simple_rand_dev(&st);
+        *P.rng = st;
+        uint32_t tok = (uint32_t)idx[k - 1];
+        float cumsum = 0.0f;
+        for (int i = 0; i < k; i++) {
+            cumsum += key[i];
+            if (r < cumsum) {
+                tok = (uint32_t)idx[i];
+                break;
+            }
+        }
+        *P.token_out = tok;
+        *P.status = 0;
+    }
+}
+
+void launch_sample_top_k(hipStream_t st, const TopKParams &p) {
+    hipLaunchKernelGGL(k_sample_top_k, dim3(1), dim3(1024), 0, st, p);
+}
+
 // Row r = embedding row tok[r * tok_stride] of w (embed_lookup_q4,
 // src/gemv.rs:377-400, exact), at out + r * out_stride.
 __global__ void k_embed_rows(DevQ4 w, const uint32_t *tok, long long tok_stride, float *out, long long out_stride) {

@@ -204,7 +204,9 @@ _lib = None
 
 
 def _ptr(a: Optional[np.ndarray]):
-    return None if a is None else C.c_void_p(a.ctypes.data)
+    # data_as keeps a reference to the array, so a temporary (a contiguous
+    # copy made in the argument list) lives until the foreign call returns
+    return None if a is None else a.ctypes.data_as(C.c_void_p)
 
 
 def load_library(path: str = LIB_PATH):
@@ -256,6 +258,9 @@ def load_library(path: str = LIB_PATH):
         "qtts_generate_acoustic_codes": ([vp, f32p, f32p, vp, vp], i32),
         "qtts_get_acoustic_embeddings_sum": ([vp, vp, f32p], i32),
         "qtts_sample_token": ([vp, f32p, i32, C.POINTER(SamplerParams), vp, i32, C.POINTER(u64), C.POINTER(u32)], i32),
+        "qtts_sample_top_k": ([vp, f32p, i32, C.c_float, i32, C.POINTER(u64), C.POINTER(u32)], i32),
+        "qtts_predict_codes": ([vp, f32p, vp, f32p], i32),
+        "qtts_forward_talker_decode": ([vp, u32, i32, vp, i32, f32p], i32),
         "qtts_generate_codes": (
             [vp, vp, vp, vp, f32p, f32p, i32, f32p, i32, f32p, C.POINTER(LoopParams), u64, vp, C.POINTER(i32)],
             i32,
@@ -302,7 +307,8 @@ def exported_symbols() -> List[str]:
         "qtts_kv_len", "qtts_kv_clear", "qtts_kv_load", "qtts_kv_store", "qtts_talker_upload", "qtts_talker_free",
         "qtts_forward_with_embedding", "qtts_prefill_talker_raw", "qtts_apply_codec_head",
         "qtts_embed_codec_token", "qtts_predictor_upload", "qtts_predictor_free", "qtts_generate_acoustic_codes",
-        "qtts_get_acoustic_embeddings_sum", "qtts_sample_token", "qtts_generate_codes", "qtts_synth_u64",
+        "qtts_get_acoustic_embeddings_sum", "qtts_sample_token", "qtts_sample_top_k", "qtts_predict_codes",
+        "qtts_forward_talker_decode", "qtts_generate_codes", "qtts_synth_u64",
         "qtts_synth_q4", "qtts_synth_normal_f32", "qtts_synth_normal_f16", "qtts_f32_to_f16", "qtts_f16_to_f32",
         "qtts_quantize_f32_to_q4", "qtts_generate_codes_batch", "qtts_model_file_open", "qtts_model_file_error", "qtts_model_file_close",
         "qtts_model_file_talker", "qtts_model_file_predictor", "qtts_model_file_text", "qtts_model_file_info",
@@ -849,6 +855,16 @@ class Context:
                                               C.byref(state), C.byref(tok)))
         return int(tok.value), int(state.value)
 
+    # sample_top_k of the legacy generator, src/generate.rs:50-84
+    def sample_top_k(self, logits, temperature: float, top_k: int, rng: int = 0):
+        """Returns (token, new_rng_state)."""
+        lg = _f32(logits)
+        state = C.c_uint64(rng)
+        tok = C.c_uint32(0)
+        self.check(self.lib.qtts_sample_top_k(self.h, _ptr(lg), lg.size, float(temperature), int(top_k),
+                                              C.byref(state), C.byref(tok)))
+        return int(tok.value), int(state.value)
+
 
 class DeviceQ4(_DeviceObject):
     """A Weight::Q4 resident in HBM with gemv/gemm/embed_lookup (src/gemv.rs:148-176)."""
@@ -965,6 +981,13 @@ class Talker(_DeviceObject):
         self.ctx.check(self.ctx.lib.qtts_embed_codec_token(self.h, int(token), _ptr(out)))
         return out
 
+    # forward_talker_decode, src/talker.rs:161-258
+    def forward_talker_decode(self, token: int, is_text: bool, kv: KvCache, position: int) -> np.ndarray:
+        out = np.empty(self.cfg.hidden, dtype=np.float32)
+        self.ctx.check(self.ctx.lib.qtts_forward_talker_decode(self.h, int(token), 1 if is_text else 0, kv.h,
+                                                                int(position), _ptr(out)))
+        return out
+
     def attach_text(self, text: "TextWeights"):
         """Uploads the text embedding and projection (qtts_talker_text_upload)."""
         self._text_view = text.view()
@@ -1041,6 +1064,13 @@ class CodePredictor(_DeviceObject):
         cs = np.ascontiguousarray(codes, dtype=np.uint32)
         out = np.empty(self.talker_hidden, dtype=np.float32)
         self.ctx.check(self.ctx.lib.qtts_get_acoustic_embeddings_sum(self.h, _ptr(cs), _ptr(out)))
+        return out
+
+    # predict_codes, src/code_predictor.rs:126-213
+    def predict_codes(self, talker_hidden, kv: KvCache) -> np.ndarray:
+        th = _f32(talker_hidden, self.talker_hidden)
+        out = np.empty((self.num_groups, self.cfg.vocab), dtype=np.float32)
+        self.ctx.check(self.ctx.lib.qtts_predict_codes(self.h, _ptr(th), kv.h, _ptr(out)))
         return out
 
 
