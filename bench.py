@@ -167,7 +167,7 @@ def gemv_roofline(ctx, K=2048, N=12288, iters=256, copies=64, traffic_file=None,
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
-        "traffic": read_traffic(traffic_file) if traffic_file else None,
+        "traffic": read_traffic(traffic_file, f"{K}x{N}") if traffic_file else None,
         "kernel": label or f"Q4 GEMV {K}->{N} (qtts_gemv_device, launch gaps included)",
         "algorithmic_bytes_per_launch": algo_bytes,
         "avg_launch_us": round(avg_s * 1e6, 3),
@@ -176,13 +176,51 @@ def gemv_roofline(ctx, K=2048, N=12288, iters=256, copies=64, traffic_file=None,
     }
 
 
+GEMV_PROFILE = "q4_gemv_shapes_counters.md"
+
+
 def gemv_shapes(ctx):
     """The three isolated Q4 GEMV shapes (gate/up 2048->6144, down 6144->2048,
     fused q|k|v 2048->4096) and the fused gate|up launch the talker runs
     (2048->12288)."""
-    out = [gemv_roofline(ctx, K, N) for (K, N) in ((2048, 6144), (6144, 2048), (2048, 4096))]
-    out.append(gemv_roofline(ctx, 2048, 12288, traffic_file="q4_gemv_2048x12288_counters.md",
+    out = [gemv_roofline(ctx, K, N, traffic_file=GEMV_PROFILE) for (K, N) in ((2048, 6144), (6144, 2048), (2048, 4096))]
+    out.append(gemv_roofline(ctx, 2048, 12288, traffic_file=GEMV_PROFILE,
                              label="Q4 GEMV 2048->12288 (talker gate|up fused, qtts_gemv_device)"))
+    return out
+
+
+def copy_floor(ctx, sizes=(4743168, 7110656, 14213120), iters=256, copies=64):
+    """Device-to-device copies that move as many HBM bytes per launch as the
+    GEMV shapes (size / 2 read + size / 2 written), over `copies` buffer
+    pairs, HIP events on the context's stream: the duration a plain copy
+    kernel of that size needs, the fixed-cost floor a single launch of the
+    GEMV sits above."""
+    hip = Hip()
+    out = []
+    st = hip.C.c_void_p(ctx.stream)
+    for size in sizes:
+        half = size // 2
+        bufs = [(hip.malloc(half), hip.malloc(half)) for _ in range(copies)]
+
+        def cp(i):
+            a, b = bufs[i % copies]
+            hip._ok(hip.lib.hipMemcpyDtoDAsync(hip.C.c_void_p(b), hip.C.c_void_p(a), hip.C.c_size_t(half), st),
+                    "hipMemcpyDtoDAsync")
+
+        for i in range(copies):
+            cp(i)
+        ctx.synchronize()
+        e0, e1 = hip.event(), hip.event()
+        hip.record(e0, ctx.stream)
+        for i in range(iters):
+            cp(i)
+        hip.record(e1, ctx.stream)
+        s = hip.elapsed_ms(e0, e1) / 1e3 / iters
+        for a, b in bufs:
+            hip.free(a)
+            hip.free(b)
+        out.append({"bytes_moved": 2 * half, "avg_launch_us": round(s * 1e6, 3),
+                    "GBps": round(2 * half / s / 1e9, 1), "frac": round(2 * half / s / 1e9 / HBM_PEAK_GBS, 4)})
     return out
 
 
@@ -379,14 +417,16 @@ def copy_calibration(ctx, nbytes=512 << 20):
     return nbytes
 
 
-def read_traffic(name):
+def read_traffic(name, key=None):
     """HBM bytes per launch measured by the rocprofv3 counter runs
-    (profiles/<name>), if present."""
+    (profiles/<name>), if present: the line `traffic_bytes_per_launch:` or,
+    with a key, `traffic_bytes_per_launch[key]:`."""
     path = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(path):
         return None
+    tag = "traffic_bytes_per_launch" + (f"[{key}]" if key else "") + ":"
     for line in open(path):
-        if line.startswith("traffic_bytes_per_launch:"):
+        if line.startswith(tag):
             return int(float(line.split(":")[1]))
     return None
 
@@ -443,7 +483,8 @@ def attention_only(ctx, talker, L, steps=8):
     rows, so that the talker attention runs as its own launches (k_attn, one
     per layer): the command the attention kernel's counter and trace runs
     profile.  Prints the per-step time; algorithmic attention bytes per
-    launch are 2 * (L + 1) * kv_heads * head_dim * 4."""
+    launch are the K and V rows read, 2 * rows * kv_heads * head_dim * 4,
+    with rows = L + 1 .. L + steps (mean L + (steps + 1) / 2)."""
     os.environ["QTTS_ENGINE"] = "ops"
     c = talker.cfg
     shape = (c.layers, L, c.kv_heads, c.head_dim)
@@ -457,9 +498,79 @@ def attention_only(ctx, talker, L, steps=8):
     for i in range(steps):
         talker.forward_with_embedding(emb, kv, L + i)
     dt = (time.perf_counter() - t0) / steps
-    per_launch = 2 * (L + steps / 2.0) * c.kv_heads * c.head_dim * 4
+    per_launch = 2 * (L + (steps + 1) / 2.0) * c.kv_heads * c.head_dim * 4  # mean rows read: L + 4.5
     kv.close()
     return {"L": L, "steps": steps, "ms_per_step": round(dt * 1e3, 3), "attn_bytes_per_launch": per_launch}
+
+
+ENGINE_OP_KINDS = {1: "GEMV", 2: "ATTN", 3: "COMB", 4: "AMAX", 5: "SAMP", 6: "EMB"}
+
+
+def engine_trace_summary(path):
+    """Critical-path attribution of the last k_engine launch in a
+    QTTS_ENGINE_TRACE file ({nops, grid, kind[nops], ntasks[nops], u64
+    stamps[nops][grid][10]}, slot 0 = a block's op start and slot 1 its op
+    end on the 100 MHz wall clock).  Each op is charged the time by which it
+    moves the end of the chain (its last block's end past every earlier op's
+    end); ops before the embedding-sum op are the sampler and the 15
+    predictor passes, ops after it the talker step."""
+    data = open(path, "rb").read()
+    off, last = 0, None
+    while off < len(data):
+        nops, grid = np.frombuffer(data, np.int32, 2, off)
+        off += 8
+        kinds = np.frombuffer(data, np.int32, nops, off)
+        off += 4 * nops
+        ntasks = np.frombuffer(data, np.int32, nops, off)
+        off += 4 * nops
+        st = np.frombuffer(data, np.uint64, nops * grid * 10, off).reshape(nops, grid, 10).astype(np.int64)
+        off += 8 * nops * grid * 10
+        last = (kinds, ntasks, st)
+    kinds, ntasks, st = last
+    valid = st[:, :, 0] > 0
+    t0 = st[:, :, 0][valid].min()
+    ends = np.array([st[i, valid[i], 1].max() if valid[i].any() else 0 for i in range(len(kinds))])
+    emb = [i for i, k in enumerate(kinds) if k == 6]
+    e = emb[0] if emb else len(kinds)
+    groups, prev, sections = {}, t0, {"predictor": 0.0, "embedding sum": 0.0, "talker": 0.0}
+    for i in range(len(kinds)):
+        inc = (ends[i] - prev) * 0.01 if ends[i] > 0 else 0.0
+        inc = max(inc, 0.0)
+        prev = max(prev, ends[i])
+        sec = "predictor" if i < e else ("embedding sum" if i == e else "talker")
+        key = f"{sec} {ENGINE_OP_KINDS.get(int(kinds[i]), '?')} tasks={int(ntasks[i])}"
+        n, tot = groups.get(key, (0, 0.0))
+        groups[key] = (n + 1, tot + inc)
+        sections[sec] += inc
+    return {"ops": int(len(kinds)), "grid": int(st.shape[1]), "launch_us": round((ends.max() - t0) * 0.01, 1),
+            "sections_us": {k: round(v, 1) for k, v in sections.items()},
+            "by_op": {k: {"n": n, "us": round(t, 1), "us_per_op": round(t / n, 2)} for k, (n, t) in groups.items()}}
+
+
+def engine_trace(ctx, talker, pred, path, codes=3):
+    """Traces `codes` frames of the loop at cache lengths 315.. (the 500-code
+    loop's mean, 314.5) after a 64-token prompt and 250 untimed codes."""
+    hidden = talker.cfg.hidden
+    prompt = qtts.synth_normal_f32(2, "bench.prompt", PROMPT * hidden)
+    text = qtts.synth_normal_f32(2, "bench.text", 8 * hidden, 0.0, 0.1).reshape(8, hidden)
+    pad = qtts.synth_normal_f32(2, "bench.pad", hidden, 0.0, 0.1)
+    lead = 250
+    kv = talker.new_kv(PROMPT + lead + codes + 8)
+    lh = talker.prefill_talker_raw(prompt, PROMPT, kv)
+    lg = talker.apply_codec_head(lh)
+    pkv = pred.new_kv()
+    params = lambda n: qtts.loop_params(n, temperature=0.8, top_k=50, repetition_penalty=1.05, stop_on_eos=False)
+    qtts.generate_codes(talker, pred, kv, pkv, lh, lg, PROMPT, text, pad, params(lead), seed=40)
+    if os.path.exists(path):
+        os.remove(path)
+    os.environ["QTTS_ENGINE_TRACE"] = path
+    os.environ["QTTS_ENGINE_TRACE_FROM"] = "0"
+    qtts.generate_codes(talker, pred, kv, pkv, lh, lg, PROMPT + lead, text, pad, params(codes), seed=42)
+    del os.environ["QTTS_ENGINE_TRACE"]
+    out = engine_trace_summary(path)
+    out["kv_len"] = [PROMPT + lead + 1, PROMPT + lead + codes]
+    kv.close()
+    return out
 
 
 # The loop the headline is quoted on: 500 codes after a 64-token prefill,
@@ -480,6 +591,9 @@ def main():
                     help="only the GEMV timings and the copy-kernel calibration (for counter runs)")
     ap.add_argument("--attention-only", type=int, default=0, metavar="L",
                     help="only multi-kernel talker steps at a cache of L rows (for attention counter runs)")
+    ap.add_argument("--engine-trace", default="", metavar="FILE",
+                    help="only a per-op trace of 3 frames at cache lengths 315..317 (written to FILE) and its "
+                         "critical-path summary")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for {args.gpus}); the per-code loop at batch 1 is a serial "
@@ -489,8 +603,9 @@ def main():
     if args.roofline_only:
         ctx = qtts.Context(0)
         roof = gemv_shapes(ctx)
+        floor = copy_floor(ctx)
         copied = copy_calibration(ctx)
-        print(json.dumps({"gemv": roof, "copy_bytes": copied}), flush=True)
+        print(json.dumps({"gemv": roof, "copy_floor": floor, "copy_bytes": copied}), flush=True)
         ctx.close()
         return
 
@@ -507,6 +622,10 @@ def main():
         return
     pred = qtts.CodePredictor(ctx, pw)
     log(f"uploaded {time.time() - t0:.1f}s")
+    if args.engine_trace:
+        print(json.dumps({"engine_trace": engine_trace(ctx, talker, pred, args.engine_trace)}), flush=True)
+        ctx.close()
+        return
     hidden = tw.cfg.hidden
     prompt = qtts.synth_normal_f32(2, "bench.prompt", PROMPT * hidden)
     text = qtts.synth_normal_f32(2, "bench.text", 8 * hidden, 0.0, 0.1).reshape(8, hidden)

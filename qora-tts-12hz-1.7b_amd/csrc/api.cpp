@@ -438,6 +438,15 @@ int attn_nsplit(int cap, int min_split) {
     return n;
 }
 
+// Splits of a one-row talker attention (k_attn): at least 16, and enough
+// that a split holds <= 64 positions (its K and V rows then come in one
+// round trip) up to 64 splits.
+int attn_nsplit_row(int cap) {
+    int n = (cap + 63) / 64;
+    if (n > 64) n = 64;
+    return n < 16 ? 16 : n;
+}
+
 // One layer stack over M rows: QKV (RMSNorm prologue; QK-norm, RoPE and KV
 // append epilogue) -> attention -> O (+residual) -> gate|up (RMSNorm
 // prologue, SiLU*up epilogue) -> down (+residual).  Positions and cache rows
@@ -1690,7 +1699,7 @@ qtts_status talker_step_x(qtts_talker *t, qtts_kv *kv, int32_t position, float *
         kv->len += 1;
         return QTTS_OK;
     }
-    t->nsplit = attn_nsplit(kv->cap, 16);
+    t->nsplit = attn_nsplit_row(kv->cap);
     QTTS_TRY(set_state(t, position, kv->len));
     QTTS_TRY(enqueue_talker_step(t, kv, t->out, t->out + hidden, nullptr, 0));
     HIP_TRY(c, hipMemcpyAsync(out, t->out, sizeof(float) * out_n, hipMemcpyDeviceToHost, c->stream));
@@ -1886,7 +1895,7 @@ qtts_status prefill_from_xp(qtts_talker *t, int32_t seq_len, qtts_kv *kv) {
     qtts_ctx *c = t->ctx;
     const Stack &st = t->st;
     const int hidden = st.hidden;
-    t->nsplit = attn_nsplit(kv->cap, 16);
+    t->nsplit = attn_nsplit_row(kv->cap);
     if (seq_len >= kMfmaMinRows && t->mfma_state == 0) QTTS_TRY(make_talker_mfma(t));
     if (seq_len >= kMfmaMinRows && t->mfma_state == 1) {
         QTTS_TRY(prefill_layers_mfma(t, kv, seq_len));
@@ -2628,7 +2637,7 @@ qtts_status qtts_generate_codes(qtts_talker *t, qtts_predictor *p, qtts_kv *talk
     if (position < 0 || position + max_codes > t->max_pos) return fail(c, QTTS_ERANGE, "positions beyond the RoPE table");
     if (talker_kv->len + max_codes > talker_kv->cap) return fail(c, QTTS_ERANGE, "talker cache too small");
     const int hidden = t->st.hidden;
-    t->nsplit = attn_nsplit(talker_kv->cap, 16);
+    t->nsplit = attn_nsplit_row(talker_kv->cap);
     // device buffers
     const size_t ncodes = (size_t)16 * max_codes;
     if (ncodes > t->codes_cap) {

@@ -579,22 +579,40 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams P) {
         const bool rotate = !(P.rope_skip_oob && pos >= P.rope_rows);
         const float *rs = P.raw + (size_t)m * P.ldr;
         const int hh0 = tid >> 7, d = tid & (HD - 1);
-        for (int h0 = 0; h0 < nh; h0 += 2) {
-            const int hh = h0 + hh0;
+        // Every global read of this prologue is issued first (one round
+        // trip): the raw rows and gammas of each round's two heads, this
+        // thread's RoPE pair and the new row's v.
+        constexpr int NR = (GMAX + 2) / 2;  // rounds of two heads: G query heads and k
+        float vr[NR], gr[NR];
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            const int hh = 2 * r + hh0;
             const bool isk = hh == G;
-            const float v = hh < nh ? rs[(size_t)(isk ? P.nq + kvh : kvh * G + hh) * HD + d] : 0.0f;
+            vr[r] = hh < nh ? rs[(size_t)(isk ? P.nq + kvh : kvh * G + hh) * HD + d] : 0.0f;
+            gr[r] = hh < nh ? f16_to_f32((isk ? P.k_norm : P.q_norm)[d]) : 0.0f;
+        }
+        float cs = 1.0f, sn = 0.0f;
+        if (rotate && d < HD / 2) {
+            cs = P.rope_cos[(size_t)pos * (HD / 2) + d];
+            sn = P.rope_sin[(size_t)pos * (HD / 2) + d];
+        }
+        const float vnew = last && tid < HD ? rs[(size_t)(P.nq + P.nkv + kvh) * HD + tid] : 0.0f;
+#pragma unroll
+        for (int r = 0; r < NR; r++) {
+            if (2 * r >= nh) break;  // uniform
+            const int hh = 2 * r + hh0;
+            const bool isk = hh == G;
+            const float v = vr[r];
             const float w = wave_sum(v * v);
             if (lane == 0) hs2[wave] = w;
             __syncthreads();
             const float inv = 1.0f / sqrtf((hs2[2 * hh0] + hs2[2 * hh0 + 1]) / (float)HD + 1e-6f);
-            if (hh < nh) hn[hh0][d] = v * inv * f16_to_f32((isk ? P.k_norm : P.q_norm)[d]);
+            if (hh < nh) hn[hh0][d] = v * inv * gr[r];
             __syncthreads();
             if (hh < nh && d < HD / 2) {
                 const float x1 = hn[hh0][d], x2 = hn[hh0][d + HD / 2];
                 float o1 = x1, o2 = x2;
                 if (rotate) {
-                    const float cs = P.rope_cos[(size_t)pos * (HD / 2) + d];
-                    const float sn = P.rope_sin[(size_t)pos * (HD / 2) + d];
                     o1 = x1 * cs - x2 * sn;
                     o2 = x2 * cs + x1 * sn;
                 }
@@ -608,7 +626,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams P) {
             // the new row: v as is; k and v appended to the stream's cache
             // (src/talker.rs:299-302) for later steps; this step reads them
             // from LDS
-            vn[tid] = rs[(size_t)(P.nq + P.nkv + kvh) * HD + tid];
+            vn[tid] = vnew;
             const_cast<float *>(Kb)[(size_t)tnew * HD + tid] = kn[tid];
             const_cast<float *>(Vb)[(size_t)tnew * HD + tid] = vn[tid];
         }
@@ -620,6 +638,19 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams P) {
     }
     __syncthreads();
 
+    // The first VU * 8 V rows of the split are loaded now, so they are in
+    // flight with the K rows (a split of <= 64 positions makes one round
+    // trip for K and V together).
+    constexpr int VU = 8;
+    const int d4 = tid & 31, r8 = tid >> 5;
+    float4 v_first[VU];
+    if (nt > 0) {
+#pragma unroll
+        for (int u = 0; u < VU; u++) {
+            const int tt = min(r8 + 8 * u, nt - 1);
+            v_first[u] = *reinterpret_cast<const float4 *>(Vb + (size_t)(t0 + tt) * HD + 4 * d4);
+        }
+    }
     // scores: 16 lanes per position, 8 dims per lane; SU positions per
     // thread are loaded before any is used (clamped to the split, masked
     // after), so their loads are in flight together.
@@ -679,11 +710,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams P) {
     }
     __syncthreads();
     // P.V: thread (d4, r8) holds dims 4*d4..4*d4+3 of every 8th position
-    // from r8, VU rows loaded together; the two halves of a wave are added
-    // by a lane exchange and the 4 waves through LDS.
+    // from r8, VU rows loaded together (the first VU above); the two halves
+    // of a wave are added by a lane exchange and the 4 waves through LDS.
     {
-        constexpr int VU = 4;
-        const int d4 = tid & 31, r8 = tid >> 5;
         float4 acc[GMAX];
 #pragma unroll
         for (int g = 0; g < GMAX; g++) acc[g] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
@@ -692,7 +721,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams P) {
 #pragma unroll
             for (int u = 0; u < VU; u++) {
                 const int tt = min(b0 + r8 + 8 * u, nt - 1);
-                v[u] = *reinterpret_cast<const float4 *>(Vb + (size_t)(t0 + tt) * HD + 4 * d4);
+                v[u] = b0 == 0 ? v_first[u] : *reinterpret_cast<const float4 *>(Vb + (size_t)(t0 + tt) * HD + 4 * d4);
             }
 #pragma unroll
             for (int u = 0; u < VU; u++) {
@@ -774,7 +803,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn(AttnParams P) {
         float mx = -INFINITY;
         for (int s2 = 0; s2 < ns; s2++) mx = fmaxf(mx, mval(s2));
         float o = 0.0f, l = 0.0f;
-        constexpr int CB = 8;
+        constexpr int CB = 32;
         for (int s0 = 0; s0 < ns; s0 += CB) {
             float ov[CB];
 #pragma unroll

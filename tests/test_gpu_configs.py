@@ -7,6 +7,8 @@ oracle on the same seeded random-init weights and inputs:
   from a cache loaded to 500 N(0,1) rows, through position 564;
 - the talker + code predictor loop (src/generate_new.rs:242-300) after a
   64-token prefill: 64 greedy and 64 sampled frames;
+- two talker steps from caches loaded to 564 and 2064 N(0,1) rows, on the
+  frame engine and on the multi-kernel path (k_attn);
 - 16 batched streams (qtts_generate_codes_batch) in 2064-row caches loaded
   to 2000 N(0,1) rows: 3 sampled frames, every stream's codes, frame count,
   cache length and appended cache rows.
@@ -203,3 +205,35 @@ def test_batch_config5_16_streams_2000_rows(full):
         assert np.array_equal(got[b], refs[b]), (b, np.argwhere(got[b] != refs[b])[:5])
         assert len(kvs[b]) == len(okvs[b]) == L + frames, b
         _check_appended(kvs[b], okvs[b], L, frames)
+
+
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("L", [564, 2064])
+@pytest.mark.parametrize("engine", ["frame", "ops"])
+def test_talker_steps_long_cache(full, monkeypatch, L, engine):
+    """Two talker steps (forward_with_embedding) from a cache loaded to L
+    N(0,1) rows, on the frame engine and on the multi-kernel path (k_attn,
+    up to 64 position splits): hidden, logits and the two appended cache rows
+    against the oracle."""
+    tw, _, t, _, ot, _ = full
+    if engine == "ops":
+        monkeypatch.setenv("QTTS_ENGINE", "ops")
+    c = tw.cfg
+    shape = (c.layers, L, c.kv_heads, c.head_dim)
+    k = qtts.synth_normal_f32(50 + L, "long.k", int(np.prod(shape))).reshape(shape)
+    v = qtts.synth_normal_f32(50 + L, "long.v", int(np.prod(shape))).reshape(shape)
+    kv, okv = t.new_kv(L + 8), ot.new_kv(L + 8)
+    kv.load(k, v, L)
+    okv.load(k, v, L)
+    del k, v
+    for i in range(2):
+        emb = qtts.synth_normal_f32(60 + i, "long.emb", c.hidden)
+        got = t.forward_with_embedding(emb, kv, L + i)
+        ref = ot.forward_with_embedding(emb, okv, L + i)
+        e = rel_err(got[: c.hidden], ref[: c.hidden])
+        print(f"L={L} {engine} step {i}: hidden rel err {e:.2e}", flush=True)
+        assert e < REL_TOL and rel_err(got[c.hidden:], ref[c.hidden:]) < REL_TOL
+    gk, gv = kv.store()
+    rk, rv = okv.store()
+    assert rel_err(gk[:, L:], rk[:, L:]) < REL_TOL and rel_err(gv[:, L:], rv[:, L:]) < REL_TOL
+    kv.close()
