@@ -136,6 +136,7 @@ struct GemmMfmaParams {
 };
 
 constexpr int kGemvThreads = 256;
+constexpr int kGemvWideThreads = 1024;  // the one-row GEMV's block for 2048 < K <= 8192
 constexpr int kMaxM = 4;          // rows per GEMV launch (prefill chunks)
 constexpr int kMfmaMinRows = 8;   // GEMMs of at least this many rows run on the matrix cores
 constexpr int kMaxGroups = 15;    // predictor code groups

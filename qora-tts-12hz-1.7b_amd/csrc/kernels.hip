@@ -350,57 +350,80 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvParams P) {
     }
 }
 
-// The plain single-row GEMV (gemv_q4, src/gemv.rs:263-309) with K <= 2048:
-// one block per 32-column panel over its whole K.  The input rows go first,
-// then the scales, then the weight rows one by one (scheduling barriers keep
-// that issue order), so each row's FMAs wait for that row alone while the
-// later rows are still in flight; the 32 column sums are finished in LDS and
-// stored directly.  Same arithmetic as k_gemv.
-template <int RPT>
-__global__ __launch_bounds__(kGemvThreads) void k_gemv_plain(DevQ4 w, const float *x, float *y, const float *bias) {
-    __shared__ float red[4 * 32];
-    const int p = blockIdx.x, tid = threadIdx.x, K = w.K;
+// The plain single-row GEMV (gemv_q4, src/gemv.rs:263-309): one block of NT
+// threads per C-column slice of a 32-column panel, over its whole K (K <= NT *
+// RPT; 256 threads up to 2048 rows, 1024 threads up to 8192).  With C < 32
+// the S = 32 / C slices of a panel run on blocks 8 apart -- one XCD, as blocks
+// are dealt to the 8 XCDs round-robin -- so each panel row comes from HBM once
+// into that XCD's L2 (the host uses C < 32 only when the panels are a multiple
+// of 8).  The input rows go first, then the scales, then the weight rows one
+// by one (scheduling barriers keep that issue order), so each row's FMAs wait
+// for that row alone while the later rows are still in flight; the column
+// sums are finished in LDS and stored directly.  Same arithmetic as k_gemv.
+template <int RPT, int NT, int C>
+__global__ __launch_bounds__(NT) void k_gemv_plain(DevQ4 w, const float *x, float *y, const float *bias) {
+    constexpr int NW = NT / 64, S = 32 / C, DW = q4_slice_dwords<C>();
+    __shared__ float red[NW * C];
+    const int tid = threadIdx.x, K = w.K;
+    const int b = blockIdx.x;
+    const int p = S == 1 ? b : (b / (8 * S)) * 8 + (b % 8);  // panel
+    const int sl = S == 1 ? 0 : (b % (8 * S)) / 8;           // slice of the panel
     float xv[RPT];
 #pragma unroll
     for (int i = 0; i < RPT; i++) {
-        const int k = tid + i * kGemvThreads;
+        const int k = tid + i * NT;
         xv[i] = glb(x)[min(k, K - 1)];
         xv[i] = k < K ? xv[i] : 0.0f;
     }
     uint32_t sv[RPT];
-    u32x4 wv[RPT];
+    uint32_t wv[RPT][DW];
 #pragma unroll
-    for (int i = 0; i < RPT; i++) sv[i] = __builtin_nontemporal_load(glb(w.ws) + (size_t)p * K + min(tid + i * kGemvThreads, K - 1));
+    for (int i = 0; i < RPT; i++) sv[i] = __builtin_nontemporal_load(glb(w.ws) + (size_t)p * K + min(tid + i * NT, K - 1));
     __builtin_amdgcn_sched_barrier(0);
+    const uint8_t *wq = reinterpret_cast<const uint8_t *>(w.wq) + sl * (C / 2);
 #pragma unroll
     for (int i = 0; i < RPT; i++) {
-        wv[i] = __builtin_nontemporal_load(glb(reinterpret_cast<const u32x4 *>(w.wq)) + (size_t)p * K +
-                                           min(tid + i * kGemvThreads, K - 1));
+        q4_slice_load<C>(wq + ((size_t)p * K + min(tid + i * NT, K - 1)) * 16, wv[i]);
         __builtin_amdgcn_sched_barrier(0);
     }
-    float acc[1][32];
+    float acc[1][C];
 #pragma unroll
-    for (int j = 0; j < 32; j++) acc[0][j] = 0.0f;
+    for (int j = 0; j < C; j++) acc[0][j] = 0.0f;
     float sxsum = 0.0f;
 #pragma unroll
     for (int i = 0; i < RPT; i++) {
-        asm volatile("" : "+v"(sv[i]), "+v"(wv[i]));
+        asm volatile("" : "+v"(sv[i]));
+#pragma unroll
+        for (int d = 0; d < DW; d++) asm volatile("" : "+v"(wv[i][d]));
         const float s = f16_to_f32((uint16_t)sv[i]);
         float sa[1], sb[1];
         sa[0] = s * (xv[i] * 16777216.0f);
         sb[0] = sa[0] * 0.0625f;
         sxsum += sa[0];
-        const uint32_t wd[4] = {wv[i].x, wv[i].y, wv[i].z, wv[i].w};
-        q4_mix_row<1, 32>(wd, sa, sb, acc);
+        q4_mix_row<1, C>(wv[i], sa, sb, acc);
     }
 #pragma unroll
-    for (int j = 0; j < 32; j++) acc[0][j] = fmaf(-0x1p-21f, sxsum, acc[0][j]);
-    dpp_reduce<32>(acc[0], red);
+    for (int j = 0; j < C; j++) acc[0][j] = fmaf(-0x1p-21f, sxsum, acc[0][j]);
+    dpp_reduce<C>(acc[0], red);
     __syncthreads();
-    if (tid < 32) {
-        float v = (red[tid] + red[32 + tid]) + (red[64 + tid] + red[96 + tid]);
-        if (bias) v += bias[p * 32 + tid];
-        y[p * 32 + tid] = v;
+    if (tid < C) {
+        float v;
+        if constexpr (NW == 4) {
+            v = (red[tid] + red[C + tid]) + (red[2 * C + tid] + red[3 * C + tid]);
+        } else {
+            // the waves' sums pairwise, in wave order
+            float t[NW];
+#pragma unroll
+            for (int i = 0; i < NW; i++) t[i] = red[i * C + tid];
+#pragma unroll
+            for (int h = 1; h < NW; h *= 2)
+#pragma unroll
+                for (int i = 0; i + h < NW; i += 2 * h) t[i] += t[i + h];
+            v = t[0];
+        }
+        const int col = p * 32 + sl * C + tid;
+        if (bias) v += bias[col];
+        y[col] = v;
     }
 }
 
@@ -464,13 +487,49 @@ static void launch_gemv_m(hipStream_t st, const GemvParams &p) {
 void launch_gemv(hipStream_t st, const GemvParams &p) {
     if (p.M == 1 && p.kc == 1 && p.prologue == PRO_PLAIN && p.epilogue == EPI_STORE && p.fin == FIN_NONE &&
         !p.d_done) {
-        const dim3 grid((unsigned)(p.w.N / 32));
-        switch (p.rpt) {
-            case 8: hipLaunchKernelGGL((k_gemv_plain<8>), grid, dim3(kGemvThreads), 0, st, p.w, p.x, p.y, p.bias); return;
-            case 4: hipLaunchKernelGGL((k_gemv_plain<4>), grid, dim3(kGemvThreads), 0, st, p.w, p.x, p.y, p.bias); return;
-            case 2: hipLaunchKernelGGL((k_gemv_plain<2>), grid, dim3(kGemvThreads), 0, st, p.w, p.x, p.y, p.bias); return;
-            default: hipLaunchKernelGGL((k_gemv_plain<1>), grid, dim3(kGemvThreads), 0, st, p.w, p.x, p.y, p.bias); return;
+        // half-panel slices where the panels come in multiples of 8 (one
+        // XCD per panel's slices): twice the blocks, half the accumulation each
+        constexpr int T = kGemvThreads;
+        const bool half = (p.w.N / 32) % 8 == 0;
+        const dim3 grid((unsigned)(p.w.N / 32 * (half ? 2 : 1)));
+        if (half) {
+            switch (p.rpt) {
+                case 8: hipLaunchKernelGGL((k_gemv_plain<8, T, 16>), grid, dim3(T), 0, st, p.w, p.x, p.y, p.bias); return;
+                case 4: hipLaunchKernelGGL((k_gemv_plain<4, T, 16>), grid, dim3(T), 0, st, p.w, p.x, p.y, p.bias); return;
+                case 2: hipLaunchKernelGGL((k_gemv_plain<2, T, 16>), grid, dim3(T), 0, st, p.w, p.x, p.y, p.bias); return;
+                default: hipLaunchKernelGGL((k_gemv_plain<1, T, 16>), grid, dim3(T), 0, st, p.w, p.x, p.y, p.bias); return;
+            }
         }
+        switch (p.rpt) {
+            case 8: hipLaunchKernelGGL((k_gemv_plain<8, T, 32>), grid, dim3(T), 0, st, p.w, p.x, p.y, p.bias); return;
+            case 4: hipLaunchKernelGGL((k_gemv_plain<4, T, 32>), grid, dim3(T), 0, st, p.w, p.x, p.y, p.bias); return;
+            case 2: hipLaunchKernelGGL((k_gemv_plain<2, T, 32>), grid, dim3(T), 0, st, p.w, p.x, p.y, p.bias); return;
+            default: hipLaunchKernelGGL((k_gemv_plain<1, T, 32>), grid, dim3(T), 0, st, p.w, p.x, p.y, p.bias); return;
+        }
+    }
+    if (p.M == 1 && p.kc > 1 && p.w.K <= 8 * kGemvWideThreads && p.prologue == PRO_PLAIN &&
+        p.epilogue == EPI_STORE && p.fin == FIN_NONE && !p.d_done) {
+        // K > 2048: a 1024-thread block per panel instead of K chunks summed
+        // through memory (one CU per panel, 16 waves hiding the loads)
+        constexpr int T = kGemvWideThreads;
+        const int r = (p.w.K + T - 1) / T;
+        const bool half = (p.w.N / 32) % 8 == 0;
+        const dim3 grid((unsigned)(p.w.N / 32 * (half ? 2 : 1)));
+        if (half) {
+            if (r <= 4)
+                hipLaunchKernelGGL((k_gemv_plain<4, T, 16>), grid, dim3(T), 0, st, p.w, p.x, p.y, p.bias);
+            else if (r <= 6)
+                hipLaunchKernelGGL((k_gemv_plain<6, T, 16>), grid, dim3(T), 0, st, p.w, p.x, p.y, p.bias);
+            else
+                hipLaunchKernelGGL((k_gemv_plain<8, T, 16>), grid, dim3(T), 0, st, p.w, p.x, p.y, p.bias);
+        } else if (r <= 4) {
+            hipLaunchKernelGGL((k_gemv_plain<4, T, 32>), grid, dim3(T), 0, st, p.w, p.x, p.y, p.bias);
+        } else if (r <= 6) {
+            hipLaunchKernelGGL((k_gemv_plain<6, T, 32>), grid, dim3(T), 0, st, p.w, p.x, p.y, p.bias);
+        } else {
+            hipLaunchKernelGGL((k_gemv_plain<8, T, 32>), grid, dim3(T), 0, st, p.w, p.x, p.y, p.bias);
+        }
+        return;
     }
     switch (p.M) {
         case 1: launch_gemv_m<1>(st, p); break;
