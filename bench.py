@@ -31,6 +31,12 @@ HBM_PEAK_GBS = 8000.0
 MFMA_F16_PEAK_TFLOPS = 2500.0  # dense binary16 MFMA
 FP32_PEAK_TFLOPS = 157.3  # dense f32 MFMA
 PROMPT = 64
+# The loop the headline is quoted on: 500 codes after a 64-token prefill,
+# cache lengths 65..564 (mean 314.5).  A shorter --steps run times a window
+# of the same loop centred on that mean.  The talker-only loop (config 3)
+# runs as many steps.
+CONFIG_CODES = 500
+CONFIG_STEPS = 500
 
 
 def log(msg):
@@ -362,6 +368,94 @@ def decoder_measure(ctx, frames, cpu_frames=2, reps=3):
     return out
 
 
+def talker_only_measure(ctx, talker, prompt, steps=CONFIG_STEPS):
+    """Config 3: the talker-only loop (the legacy feedback,
+    codec_embedding[code0] as the next input, src/generate.rs:225-227) after
+    a 64-token prefill, `steps` sampled steps (top-k 50, T 0.8, penalty 1.05,
+    EOS ignored) at cache lengths 65..64+steps, HIP events on the context's
+    stream around the loop.  Algorithmic bytes: talker_step_bytes at each
+    step's cache length."""
+    params = lambda n: qtts.loop_params(n, temperature=0.8, top_k=50, repetition_penalty=1.05, stop_on_eos=False,
+                                        talker_only=True)
+
+    def run(n, seed, timed):
+        kv = talker.new_kv(PROMPT + steps + 8)
+        lh = talker.prefill_talker_raw(prompt, PROMPT, kv)
+        lg = talker.apply_codec_head(lh)
+        hip = Hip()
+        e0, e1 = hip.event(), hip.event()
+        ctx.synchronize()
+        hip.record(e0, ctx.stream)
+        codes = qtts.generate_codes(talker, None, kv, None, lh, lg, PROMPT, None, None, params(n), seed=seed)
+        hip.record(e1, ctx.stream)
+        s = hip.elapsed_ms(e0, e1) / 1e3
+        kv.close()
+        assert codes.shape[1] == n
+        return s
+
+    run(4, 3, False)  # program build, untimed
+    s = run(steps, 7, True)
+    tc = qtts.TALKER_1P7B
+    total = sum(talker_step_bytes(tc, PROMPT + i) for i in range(steps))
+    achieved = total / s / 1e9
+    return {"steps": steps, "kv_len": [PROMPT + 1, PROMPT + steps], "codes_per_s": round(steps / s, 1),
+            "ms_per_step": round(s * 1e3 / steps, 4),
+            "timing": "HIP events around one qtts_generate_codes call (talker_only)",
+            "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                         "frac": round(achieved / HBM_PEAK_GBS, 4), "algorithmic_bytes": total}}
+
+
+def cpu_side(tw, out, steps=16):
+    """The oracle (the C restatement of the reference's CPU path, threads as
+    the reference's gemv_q4 spawns them) on this host for the stand-alone
+    measurements: each GEMV shape (5 calls), the config-2 talker step (2
+    steps at a 256-row cache) and `steps` steps of the config-3 talker-only
+    loop after the 64-token prefill."""
+    from oracle import oracle
+
+    threads = oracle.available_parallelism()
+    for g in out.get("gemv", []):
+        K, N = map(int, g["shape"].split("->"))
+        w = qtts.Q4Weight.synthetic(99, f"roof.{K}.{N}.0", K, N)
+        x = qtts.synth_normal_f32(99, "roof.x", K)
+        oracle.gemv(x, w)
+        t0 = time.perf_counter()
+        for _ in range(5):
+            oracle.gemv(x, w)
+        g["cpu_us"] = round((time.perf_counter() - t0) / 5 * 1e6, 1)
+        g["cpu_threads"] = threads
+    ot = oracle.Talker(tw)
+    c = tw.cfg
+    if "talker_step" in out:
+        L = out["talker_step"]["kv_len"][0] - 1
+        shape = (c.layers, L, c.kv_heads, c.head_dim)
+        k = qtts.synth_normal_f32(3, "kv.k", int(np.prod(shape))).reshape(shape)
+        v = qtts.synth_normal_f32(3, "kv.v", int(np.prod(shape))).reshape(shape)
+        okv = ot.new_kv(L + 4)
+        okv.load(k, v, L)
+        del k, v
+        emb = qtts.synth_normal_f32(3, "step.emb", c.hidden)
+        ot.forward_with_embedding(emb, okv, L)
+        t0 = time.perf_counter()
+        for i in range(2):
+            ot.forward_with_embedding(emb, okv, L + 1 + i)
+        out["talker_step"]["cpu_us"] = round((time.perf_counter() - t0) / 2 * 1e6, 1)
+        out["talker_step"]["cpu_threads"] = threads
+        del okv
+    if "talker_only" in out:
+        prompt = qtts.synth_normal_f32(2, "bench.prompt", PROMPT * c.hidden)
+        okv = ot.new_kv(PROMPT + steps + 4)
+        lh = ot.prefill_talker_raw(prompt, PROMPT, okv)
+        lg = ot.apply_codec_head(lh)
+        params = qtts.loop_params(steps, temperature=0.8, top_k=50, repetition_penalty=1.05, stop_on_eos=False,
+                                  talker_only=True)
+        t0 = time.perf_counter()
+        codes = oracle.generate_codes(ot, None, okv, None, lh, lg, PROMPT, None, None, params, seed=7)
+        dt = time.perf_counter() - t0
+        out["talker_only"]["cpu"] = {"codes_per_s": round(codes.shape[1] / dt, 3), "threads": threads,
+                                     "sample": f"{codes.shape[1]} steps at KV {PROMPT + 1}..{PROMPT + codes.shape[1]}"}
+
+
 def batch_measure(ctx, talker, pred, streams=16, kv_len=1064, frames=32):
     """The batched long-form case: `streams` independent loops in lockstep
     (qtts_generate_codes_batch), each prefilled to kv_len positions -- the
@@ -573,10 +667,6 @@ def engine_trace(ctx, talker, pred, path, codes=3):
     return out
 
 
-# The loop the headline is quoted on: 500 codes after a 64-token prefill,
-# cache lengths 65..564 (mean 314.5).  A shorter --steps run times a window
-# of the same loop centred on that mean.
-CONFIG_CODES = 500
 
 
 def main():
@@ -698,6 +788,8 @@ def main():
             log(f"stand-alone gemv {g}")
         out["talker_step"] = talker_step_measure(ctx, talker)
         log(f"talker step {out['talker_step']}")
+        out["talker_only"] = talker_only_measure(ctx, talker, prompt)
+        log(f"talker-only loop {out['talker_only']}")
         # the 64-token prompt prefill (matrix-core path), HIP events
         ctx.synchronize()
         hip.record(ev0, ctx.stream)
@@ -717,6 +809,10 @@ def main():
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(tw, pw, kv, start, lh, lg, text, pad, args.cpu_frames)
         log(f"cpu baseline {out['cpu_baseline']}")
+        if not args.no_roofline:
+            cpu_side(tw, out)
+            log("cpu side: gemv " + str([g.get("cpu_us") for g in out["gemv"]]) +
+                f" talker step {out['talker_step'].get('cpu_us')} us, talker-only {out['talker_only'].get('cpu')}")
     print(json.dumps(out), flush=True)
     ctx.close()
 
