@@ -1455,6 +1455,22 @@ __device__ __forceinline__ int eng_embsum(const KCONST EngEmbSum &E, int task, u
     return task;
 }
 
+// Loads one dword of every 64-byte line of an op descriptor when a block
+// starts the op.  The compiler re-loads descriptor fields where they are used
+// rather than holding them in (spilled) registers; this way the fields the
+// epilogue reads after the accumulation hit the scalar cache instead of
+// waiting a memory round trip on the critical path.
+__device__ __forceinline__ void touch_desc(const KCONST EngOp *op) {
+    const KCONST uint32_t *p = reinterpret_cast<const KCONST uint32_t *>(op);
+    constexpr int kW = (int)(sizeof(EngOp) / 4);
+    uint32_t v[kW / 16 + 2];
+#pragma unroll
+    for (int i = 0; i < kW / 16 + 1; i++) v[i] = p[i * 16 < kW ? i * 16 : kW - 1];
+    v[kW / 16 + 1] = p[kW - 1];
+#pragma unroll
+    for (int i = 0; i < kW / 16 + 2; i++) asm volatile("" ::"s"(v[i]));
+}
+
 }  // namespace
 
 __global__ __launch_bounds__(kEngThreads) void k_engine(EngArgs A) {
@@ -1478,6 +1494,7 @@ __global__ __launch_bounds__(kEngThreads) void k_engine(EngArgs A) {
         if (t < 0) t += G;
         uint64_t *tr = (A.trace && t < op.ntasks) ? A.trace + ((size_t)oi * G + blockIdx.x) * kTraceSlots : nullptr;
         c.tr = tr;
+        if (t < op.ntasks) touch_desc(&op);
         if (tr && threadIdx.x == 0) {
             glb(tr)[0] = wall_clock64();
             glb(tr)[8] = clock64();
