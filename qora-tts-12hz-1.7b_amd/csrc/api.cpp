@@ -595,6 +595,8 @@ struct EngProgram {
     const std::vector<int> *rot_plan = nullptr;
     size_t plan_pos = 0;
     std::vector<int> lds_owner;  // block -> layer whose K/V rows it keeps in LDS (-1: none)
+    // an op the kernel does not run (the caller takes the multi-kernel path)
+    bool unsupported = false;
     ~EngProgram() {
         if (d_ops) (void)hipFree(d_ops);
         if (arena) (void)hipFree(arena);
@@ -605,6 +607,7 @@ struct EngProgram {
         rot_plan = nullptr;
         plan_pos = 0;
         lds_owner.assign((size_t)grid, -1);
+        unsupported = false;
         ops.clear();
         used = 0;
         next_tag = 1;
@@ -889,6 +892,10 @@ TvRef add_attention(EngProgram &P, const Stack &st, int l, qtts_kv *kv, int M, c
     const bool lds_kv = !from_state && nsplit == 1 && st.hd == 128 && M * (st.nq / st.nkv) <= 4 &&
                         kv->cap <= kEngLdsKvPos && P.claim_lds(P.next_rot(), st.nkv, l);
     a.lds_kv = lds_kv ? 1 : 0;
+    // outside LDS the kernel's attention serves at most two (row, q head)
+    // pairs per kv head: the talker step (one row, 16 / 8 heads) and the
+    // predictor's one-row steps; other shapes take the multi-kernel path
+    if (!lds_kv && M * (st.nq / st.nkv) > 2) P.unsupported = true;
     if (qtab) {
         if (!lds_kv || M != 1 || qtab->n > kEngArgtabMax) P.err = "engine q|k|v table needs the LDS-resident attention";
         a.qkv = nullptr;
@@ -1039,6 +1046,7 @@ qtts_status eng_build(qtts_ctx *c, EngProgram &P, const BuildFn &fn) {
     P.reset_build();
     QTTS_TRY(fn(P));
     if (P.err) return fail(c, QTTS_ESHAPE, P.err);
+    if (P.unsupported) return QTTS_OK;  // nothing allocated; the caller checks
     const size_t need = P.used;
     if (P.arena) (void)hipFree(P.arena);
     if (P.d_ops) (void)hipFree(P.d_ops);
@@ -1691,13 +1699,15 @@ qtts_status talker_step_x(qtts_talker *t, qtts_kv *kv, int32_t position, float *
             }));
             t->step_kv = kv->serial;
         }
-        QTTS_TRY(eng_reset(c, position, kv->len, 0));
-        QTTS_TRY(eng_launch(c, *t->step_prog, 0, c->d_small, 1));
-        HIP_TRY(c, hipMemcpyAsync(out, t->out, sizeof(float) * out_n, hipMemcpyDeviceToHost, c->stream));
-        QTTS_TRY(sync(c));
-        QTTS_TRY(eng_status_check(c, "forward_with_embedding"));
-        kv->len += 1;
-        return QTTS_OK;
+        if (!t->step_prog->unsupported) {
+            QTTS_TRY(eng_reset(c, position, kv->len, 0));
+            QTTS_TRY(eng_launch(c, *t->step_prog, 0, c->d_small, 1));
+            HIP_TRY(c, hipMemcpyAsync(out, t->out, sizeof(float) * out_n, hipMemcpyDeviceToHost, c->stream));
+            QTTS_TRY(sync(c));
+            QTTS_TRY(eng_status_check(c, "forward_with_embedding"));
+            kv->len += 1;
+            return QTTS_OK;
+        }
     }
     t->nsplit = attn_nsplit_row(kv->cap);
     QTTS_TRY(set_state(t, position, kv->len));
@@ -2389,15 +2399,17 @@ qtts_status qtts_generate_acoustic_codes(qtts_predictor *p, const float *talker_
             }));
             p->prog_kv = kv->serial;
         }
-        QTTS_TRY(eng_reset(c, 0, 0, 0));
-        QTTS_TRY(eng_launch(c, *p->prog, 0, p->codes, 1));
-        uint32_t all[16];
-        HIP_TRY(c, hipMemcpyAsync(all, p->codes, sizeof(all), hipMemcpyDeviceToHost, c->stream));
-        QTTS_TRY(sync(c));
-        QTTS_TRY(eng_status_check(c, "generate_acoustic_codes"));
-        for (int g = 0; g < p->groups; g++) codes[g] = all[1 + g];
-        kv->len = p->groups + 1;
-        return QTTS_OK;
+        if (!p->prog->unsupported) {
+            QTTS_TRY(eng_reset(c, 0, 0, 0));
+            QTTS_TRY(eng_launch(c, *p->prog, 0, p->codes, 1));
+            uint32_t all[16];
+            HIP_TRY(c, hipMemcpyAsync(all, p->codes, sizeof(all), hipMemcpyDeviceToHost, c->stream));
+            QTTS_TRY(sync(c));
+            QTTS_TRY(eng_status_check(c, "generate_acoustic_codes"));
+            for (int g = 0; g < p->groups; g++) codes[g] = all[1 + g];
+            kv->len = p->groups + 1;
+            return QTTS_OK;
+        }
     }
     HIP_TRY(c, hipMemsetAsync(p->status, 0, sizeof(int), c->stream));
     QTTS_TRY(enqueue_predictor(p, kv, p->codes, p->status, nullptr));
@@ -2671,6 +2683,7 @@ qtts_status qtts_generate_codes(qtts_talker *t, qtts_predictor *p, qtts_kv *talk
     HIP_TRY(c, hipMemcpyAsync(t->state, &init, sizeof(init), hipMemcpyHostToDevice, c->stream));
     QTTS_TRY(sync(c));
 
+    bool eng_ok = false;  // the frame program is built and runs in k_engine
     if (engine_enabled() && eng_talker_fits(talker_kv->cap) && (talker_only || !p->identity_proj) &&
         t->vocab <= 4096) {
         QTTS_TRY(eng_init(c));
@@ -2715,6 +2728,9 @@ qtts_status qtts_generate_codes(qtts_talker *t, qtts_predictor *p, qtts_kv *talk
             }));
             t->frame_key = key;
         }
+        eng_ok = !t->frame_prog->unsupported;
+    }
+    if (eng_ok) {
         // t->out holds [last_hidden | logits] for the first frame's sampler
         // and predictor input.
         HIP_TRY(c, hipMemcpyAsync(t->out, last_hidden, sizeof(float) * hidden, hipMemcpyHostToDevice, c->stream));

@@ -1028,9 +1028,11 @@ __device__ __forceinline__ int eng_attn(const KCONST EngAttn &a, int task, uint3
     const int npi = a.M * (a.nq / a.nkv);
     const int Lt = (a.from_state ? st.kvlen : a.len_const) + a.M;
     const bool small = (Lt + a.nsplit - 1) / a.nsplit <= 32;
+    // at most two (row, head) pairs (the host runs other shapes on the
+    // multi-kernel path; wider instantiations cost the whole kernel registers)
     if (npi <= 2) return small ? eng_attn_t<2, 2>(a, task, tb, st, c, smem) : eng_attn_t<2, 8>(a, task, tb, st, c, smem);
-    if (npi <= 4) return small ? eng_attn_t<4, 2>(a, task, tb, st, c, smem) : eng_attn_t<4, 8>(a, task, tb, st, c, smem);
-    return small ? eng_attn_t<8, 2>(a, task, tb, st, c, smem) : eng_attn_t<8, 8>(a, task, tb, st, c, smem);
+    fail_dev(c, QTTS_EDEVICE);
+    return task;
 }
 
 // Combine the splits of one (row, query head): flash-decode merge.  Threads

@@ -125,10 +125,12 @@ def test_predictor_tiny(tiny):
 
 @pytest.mark.parametrize("capacity", [16, 40])
 def test_predictor_cache_paths(tiny, capacity):
-    """Both predictor attention paths: cached rows kept in the LDS of the
-    blocks that run the layer (capacity <= 32) and rows read back from the
-    device cache (larger capacity).  Codes match, and so does the cache the
-    call leaves for the host."""
+    """Both predictor paths: the frame engine with the cached rows kept in
+    the LDS of the blocks that run the layer (capacity <= 32), and, for a
+    larger capacity (the first pass's two rows then exceed the engine's
+    attention outside LDS), the multi-kernel path reading the rows back from
+    the device cache.  Codes match, and so does the cache the call leaves for
+    the host."""
     tw, pw, t, p, ot, op = tiny
     for i in range(3):
         h = qtts.synth_normal_f32(31, f"pc.{i}", tw.cfg.hidden)
