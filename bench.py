@@ -230,6 +230,38 @@ def copy_floor(ctx, sizes=(4743168, 7110656, 14213120), iters=256, copies=64):
     return out
 
 
+def read_floor(ctx, sizes=(4743168, 7110656, 14213120), iters=256, copies=64):
+    """One launch that only reads: qtts_stream_read_device (every 16-byte
+    word once, one per thread, 256-thread blocks) over as many bytes as each
+    GEMV shape streams, `copies` buffers rotated, HIP events on the context's
+    stream.  The single-launch floor of streaming those bytes from HBM: a
+    GEMV of that size cannot take less."""
+    hip = Hip()
+    lib = qtts.load_library()
+    out = []
+    for size in sizes:
+        bufs = [hip.malloc(size) for _ in range(copies)]
+
+        def rd(i):
+            if lib.qtts_stream_read_device(hip.C.c_void_p(bufs[i % copies]), size, hip.C.c_void_p(ctx.stream)) != 0:
+                raise RuntimeError("qtts_stream_read_device failed")
+
+        for i in range(copies):
+            rd(i)
+        ctx.synchronize()
+        e0, e1 = hip.event(), hip.event()
+        hip.record(e0, ctx.stream)
+        for i in range(iters):
+            rd(i)
+        hip.record(e1, ctx.stream)
+        s = hip.elapsed_ms(e0, e1) / 1e3 / iters
+        for b in bufs:
+            hip.free(b)
+        out.append({"bytes_read": size, "blocks": (size // 16 + 255) // 256, "avg_launch_us": round(s * 1e6, 3),
+                    "GBps": round(size / s / 1e9, 1), "frac": round(size / s / 1e9 / HBM_PEAK_GBS, 4)})
+    return out
+
+
 def talker_step_measure(ctx, talker, steps=64, L=256):
     """A single talker decode step: 28 layers, KV pre-filled to L positions
     with N(0,1), one N(0,1) embedding per step at positions L, L+1, ...
@@ -694,8 +726,9 @@ def main():
         ctx = qtts.Context(0)
         roof = gemv_shapes(ctx)
         floor = copy_floor(ctx)
+        rfloor = read_floor(ctx)
         copied = copy_calibration(ctx)
-        print(json.dumps({"gemv": roof, "copy_floor": floor, "copy_bytes": copied}), flush=True)
+        print(json.dumps({"gemv": roof, "copy_floor": floor, "read_floor": rfloor, "copy_bytes": copied}), flush=True)
         ctx.close()
         return
 
@@ -786,6 +819,8 @@ def main():
         out["gemv"] = gemv_shapes(ctx)
         for g in out["gemv"]:
             log(f"stand-alone gemv {g}")
+        out["read_floor"] = read_floor(ctx)
+        log(f"single-launch read floor {out['read_floor']}")
         out["talker_step"] = talker_step_measure(ctx, talker)
         log(f"talker step {out['talker_step']}")
         out["talker_only"] = talker_only_measure(ctx, talker, prompt)

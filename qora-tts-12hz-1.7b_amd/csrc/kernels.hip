@@ -17,6 +17,7 @@
 #include <cmath>
 
 #include "../../include/qtts.h"
+#include "../../include/qtts_synth.h"
 #include "device_common.h"
 #include "internal.h"
 
@@ -425,6 +426,26 @@ __global__ __launch_bounds__(NT) void k_gemv_plain(DevQ4 w, const float *x, floa
         if (bias) v += bias[col];
         y[col] = v;
     }
+}
+
+// qtts_stream_read_device: every 16-byte word of a buffer read once (one
+// per thread) and XORed; an empty asm statement takes the result, so the
+// compiler keeps the loads (nothing is stored).
+__global__ __launch_bounds__(256) void k_stream_read(const u32x4 *p, uint64_t n16) {
+    const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n16) return;
+    const u32x4 v = __builtin_nontemporal_load(glb(p + i));
+    const unsigned x = v.x ^ v.y ^ v.z ^ v.w;
+    asm volatile("" ::"v"(x));
+}
+
+extern "C" int32_t qtts_stream_read_device(const void *d_buf, uint64_t bytes, void *stream) {
+    if (!d_buf || bytes == 0 || bytes % 16 != 0 || ((uintptr_t)d_buf & 15) || bytes / 16 > (uint64_t)256 * 0x7FFFFFFF)
+        return -1;
+    const uint64_t n16 = bytes / 16;
+    hipLaunchKernelGGL(k_stream_read, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
+                       static_cast<const u32x4 *>(d_buf), n16);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
 // Scratch of the allocation-free GEMV entry point: split-K partials

@@ -201,3 +201,24 @@ def test_sampler_greedy_last_max_and_nan(ctx):
     with pytest.raises(qtts.QttsError) as e:
         ctx.sample_token(logits, 0.8, 50, 1.0, (0,) * 16, 1, greedy=True)
     assert e.value.status == qtts.QTTS_ENAN
+
+
+def test_stream_read_device(ctx):
+    """qtts_stream_read_device (the GEMV shapes' single-launch read floor)
+    runs over a device buffer on the context's stream and leaves it intact."""
+    import ctypes as C
+
+    from bench import Hip
+
+    hip = Hip()
+    data = np.arange(1 << 16, dtype=np.uint32)
+    d = hip.malloc(data.nbytes)
+    try:
+        hip.h2d(d, data)
+        assert ctx.lib.qtts_stream_read_device(C.c_void_p(d), data.nbytes, C.c_void_p(ctx.stream)) == 0
+        ctx.synchronize()
+        back = np.empty_like(data)
+        assert hip.lib.hipMemcpy(C.c_void_p(back.ctypes.data), C.c_void_p(d), C.c_size_t(back.nbytes), 2) == 0
+        assert np.array_equal(back, data)
+    finally:
+        hip.free(d)
