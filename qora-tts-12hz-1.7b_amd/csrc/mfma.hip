@@ -68,10 +68,13 @@ __global__ void k_repack_mfma(DevQ4 w, uint32_t *wm, uint16_t *sa, uint16_t *sb,
 // src/talker.rs:342-345, with the same expression order as the GEMV path),
 // then v * 2^e split into binary16 hi + lo, with e the per-row exponent that
 // puts max|v| * 2^e in [2^14, 2^15) (no binary16 overflow; small entries keep
-// their relative precision).  rexp[m] = e; rows >= M are zero with e = 0.
-// xh and xl are stored in the MFMA A-operand order -- [M-tile][16-row step]
-// [lane][8] -- so that each wave's operand load of a step is one contiguous
-// KiB.
+// their relative precision).  With RMSNorm, max|v| is taken as
+// (1/rms) * max|x * gamma| from the same reduction as the sum of squares (one
+// block barrier, and the gammas load with the row), which can miss max|v| by
+// a few ulps: e is then one lower, putting max|v| * 2^e in [2^13, 2^15).
+// rexp[m] = e; rows >= M are zero with e = 0.  xh and xl are stored in the
+// MFMA A-operand order -- [M-tile][16-row step][lane][8] -- so that each
+// wave's operand load of a step is one contiguous KiB.
 template <int G>  // 8-value groups per thread: K <= 2048 * G
 __global__ __launch_bounds__(256) void k_mfma_rows(MfmaRowsParams P) {
     __shared__ float red[2][4];
@@ -90,9 +93,11 @@ __global__ __launch_bounds__(256) void k_mfma_rows(MfmaRowsParams P) {
         return;
     }
     const float *src = P.x + (size_t)m * P.ldx;
+    const bool norm = P.mode == MFMA_ROWS_RMSNORM;
     float v[G][8];
-    // 1. the row's values (all loads first), and the RMSNorm sum of squares
-    float ss = 0.0f;
+    uint32_t gw[G][4];
+    // 1. the row's values and gammas (all loads first); the sum of squares
+    //    and max|x * gamma| (RMSNorm) or max|v|
 #pragma unroll
     for (int j = 0; j < G; j++) {
         const int g = tid + 256 * j;
@@ -101,6 +106,10 @@ __global__ __launch_bounds__(256) void k_mfma_rows(MfmaRowsParams P) {
             const float4 b = *reinterpret_cast<const float4 *>(src + 8 * g + 4);
             v[j][0] = a.x, v[j][1] = a.y, v[j][2] = a.z, v[j][3] = a.w;
             v[j][4] = b.x, v[j][5] = b.y, v[j][6] = b.z, v[j][7] = b.w;
+            if (norm) {
+                const uint4 q = *reinterpret_cast<const uint4 *>(P.gamma + 8 * g);
+                gw[j][0] = q.x, gw[j][1] = q.y, gw[j][2] = q.z, gw[j][3] = q.w;
+            }
             if (P.mode == MFMA_ROWS_SWIGLU) {
                 const float4 c = *reinterpret_cast<const float4 *>(src + K + 8 * g);
                 const float4 d = *reinterpret_cast<const float4 *>(src + K + 8 * g + 4);
@@ -111,43 +120,42 @@ __global__ __launch_bounds__(256) void k_mfma_rows(MfmaRowsParams P) {
         } else {
 #pragma unroll
             for (int i = 0; i < 8; i++) v[j][i] = 0.0f;
-        }
 #pragma unroll
-        for (int i = 0; i < 8; i++) ss += v[j][i] * v[j][i];
-    }
-    if (P.mode == MFMA_ROWS_RMSNORM) {
-        ss = wave_sum(ss);
-        if (lane == 0) red[0][wave] = ss;
-        __syncthreads();
-        ss = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
-        const float inv = 1.0f / sqrtf(ss / (float)K + 1e-6f);
-#pragma unroll
-        for (int j = 0; j < G; j++) {
-            const int g = tid + 256 * j;
-            if (g < ng) {
-                const uint4 gw = *reinterpret_cast<const uint4 *>(P.gamma + 8 * g);
-                const uint32_t gp[4] = {gw.x, gw.y, gw.z, gw.w};
-#pragma unroll
-                for (int i = 0; i < 8; i++)
-                    v[j][i] = v[j][i] * inv * f16_to_f32((uint16_t)(gp[i / 2] >> (16 * (i & 1))));
-            }
+            for (int q = 0; q < 4; q++) gw[j][q] = 0u;
         }
     }
-    // 2. the row exponent
-    float mx = 0.0f;
+    float ss = 0.0f, mx = 0.0f;
 #pragma unroll
     for (int j = 0; j < G; j++)
 #pragma unroll
-        for (int i = 0; i < 8; i++) mx = fmaxf(mx, fabsf(v[j][i]));  // NaN entries drop out here and stay NaN below
+        for (int i = 0; i < 8; i++) {
+            ss += v[j][i] * v[j][i];
+            // NaN entries drop out of the max here and stay NaN below
+            mx = fmaxf(mx, fabsf(norm ? v[j][i] * f16_to_f32((uint16_t)(gw[j][i / 2] >> (16 * (i & 1)))) : v[j][i]));
+        }
+    ss = wave_sum(ss);
     mx = wave_max(mx);
-    if (lane == 0) red[1][wave] = mx;
+    if (lane == 0) {
+        red[0][wave] = ss;
+        red[1][wave] = mx;
+    }
     __syncthreads();
     mx = fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3]));
+    if (norm) {
+        ss = (red[0][0] + red[0][1]) + (red[0][2] + red[0][3]);
+        const float inv = 1.0f / sqrtf(ss / (float)K + 1e-6f);
+        mx *= inv;
+#pragma unroll
+        for (int j = 0; j < G; j++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) v[j][i] = v[j][i] * inv * f16_to_f32((uint16_t)(gw[j][i / 2] >> (16 * (i & 1))));
+    }
+    // 2. the row exponent
     int e = 0;
     if (mx > 0.0f && mx < INFINITY) {
         int E;
         (void)frexpf(mx, &E);  // mx = f * 2^E, f in [0.5, 1)
-        e = min(15 - E, 126);
+        e = min((norm ? 14 : 15) - E, 126);
     }
     if (tid == 0) P.rexp[m] = e;
     if (P.norm_out) {
