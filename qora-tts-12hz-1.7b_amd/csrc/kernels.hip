@@ -1234,26 +1234,55 @@ __global__ void k_embed_sum(EmbSumParams Pin) {
         if (P.prev) P.prev[1 + g] = P.cur[1 + g];
     }
     if (j >= P.hidden) return;
-    if (P.mode == 1) {  // get_acoustic_embeddings_sum alone
-        float acc = 0.0f;
-        for (int g = 0; g < P.num_groups; g++) {
-            const uint32_t c = P.cur[1 + g];
-            acc += c < (uint32_t)P.group_emb[g].K ? q4_element(P.group_emb[g], c, j) : 0.0f;
-        }
+    // Every code, then every element's byte and scale, are loaded before any
+    // is used (two memory round trips instead of two per group).  Slot 0 is
+    // code 0's codec_emb row (mode 0), slot 1 + g group g's row; a slot past
+    // the groups reads row 0 of a table this mode has (codec_emb in mode 0,
+    // group 0's in mode 1) and is not used.
+    constexpr int NG = kMaxGroups + 1;
+    const bool full = P.mode != 1;
+    const int ng = P.num_groups;
+    if (!full && ng <= 0) {  // an empty acoustic sum
+        P.out[j] = 0.0f;
+        return;
+    }
+    const bool text_in = full && ng > 0;
+    float text = 0.0f;
+    if (text_in) text = (frame < P.trailing_len ? P.trailing + (size_t)frame * P.hidden : P.pad)[j];
+    uint32_t code[NG];
+#pragma unroll
+    for (int g = 0; g < NG; g++) code[g] = g <= ng ? P.cur[g] : 0u;
+    uint32_t by[NG], sc[NG];
+    bool ok[NG];
+#pragma unroll
+    for (int g = 0; g < NG; g++) {
+        const bool used = g == 0 ? full : g - 1 < ng;
+        const DevQ4 &w = g > 0 && g - 1 < ng ? P.group_emb[g - 1] : (full ? P.codec_emb : P.group_emb[0]);
+        ok[g] = used && code[g] < (uint32_t)w.K;
+        const size_t r = (size_t)(j >> 5) * w.K + (ok[g] ? code[g] : 0u);
+        by[g] = glb(reinterpret_cast<const uint8_t *>(w.wq))[r * 16 + ((j & 31) >> 1)];
+        sc[g] = glb(w.ws)[r];
+    }
+#pragma unroll
+    for (int g = 0; g < NG; g++) asm volatile("" : "+v"(by[g]), "+v"(sc[g]));
+    // embed_lookup_q4 elements (src/gemv.rs:388-396), summed in the order of
+    // src/code_predictor.rs:280-293 and src/generate_new.rs:270-286
+    const auto elem = [&](int g) {
+        const int nib = (j & 1) ? (int)(by[g] >> 4) : (int)(by[g] & 15u);
+        return ok[g] ? f16_to_f32((uint16_t)sc[g]) * (float)(nib - 8) : 0.0f;
+    };
+    float acc = 0.0f;
+#pragma unroll
+    for (int g = 1; g < NG; g++)
+        if (g - 1 < ng) acc += elem(g);
+    if (!full) {  // get_acoustic_embeddings_sum alone
         P.out[j] = acc;
         return;
     }
-    const uint32_t c0 = P.cur[0];
-    float v = c0 < (uint32_t)P.codec_emb.K ? q4_element(P.codec_emb, c0, j) : 0.0f;
-    if (P.num_groups > 0) {
-        float acc = 0.0f;
-        for (int g = 0; g < P.num_groups; g++) {
-            const uint32_t c = P.cur[1 + g];
-            acc += c < (uint32_t)P.group_emb[g].K ? q4_element(P.group_emb[g], c, j) : 0.0f;
-        }
+    float v = elem(0);
+    if (ng > 0) {
         v += acc;
-        const float *text = frame < P.trailing_len ? P.trailing + (size_t)frame * P.hidden : P.pad;
-        v += text[j];
+        v += text;
     }
     P.out[j] = v;
 }
