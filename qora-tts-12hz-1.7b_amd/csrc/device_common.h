@@ -268,6 +268,28 @@ __device__ __forceinline__ void dpp_reduce(const float (&acc)[C], float *red) {
     }
 }
 
+// f32 sum of s[0..n) in index order by one thread (the order the reference
+// sums in).  The LDS reads are issued 32 at a time so the add chain, not the
+// read latency, sets the pace.  s is 16-byte aligned.
+__device__ __forceinline__ float seq_sum(const float *s, int n) {
+    float sum = 0.0f;
+    int i = 0;
+    for (; i + 32 <= n; i += 32) {
+        float4 v[8];
+#pragma unroll
+        for (int q = 0; q < 8; q++) v[q] = *reinterpret_cast<const float4 *>(&s[i + 4 * q]);
+#pragma unroll
+        for (int q = 0; q < 8; q++) {
+            sum += v[q].x;
+            sum += v[q].y;
+            sum += v[q].z;
+            sum += v[q].w;
+        }
+    }
+    for (; i < n; i++) sum += s[i];
+    return sum;
+}
+
 // out[i] = element (row, col0 + i * stride) of a panel-major Q4 weight for
 // columns < ncol, else 0 (row < w.K).  All loads are issued before any is
 // used, as in embed_lookup_q4 (src/gemv.rs:377-400) per element.

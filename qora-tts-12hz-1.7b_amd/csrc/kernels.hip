@@ -962,7 +962,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleParams Pin) {
         if (P.codes) P.codes += b * Pin.codes_stride;
     }
     if (P.done && *P.done) return;
-    extern __shared__ unsigned char smem_raw[];
+    extern __shared__ __align__(16) unsigned char smem_raw[];
     float *s = reinterpret_cast<float *>(smem_raw);
     int *list = reinterpret_cast<int *>(s + P.vocab);
     __shared__ unsigned hist[256];
@@ -973,10 +973,12 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleParams Pin) {
     __shared__ unsigned s_prefix, s_mask;
     __shared__ int s_remaining, s_nan, s_count;
     __shared__ uint32_t s_token;
+    __shared__ uint32_t s_prev[32];  // n_prev <= 32
 
     const int V = P.vocab, tid = threadIdx.x, nthr = blockDim.x;
     const int lane = tid & 63, wave = tid >> 6, nwaves = nthr >> 6;
     for (int i = tid; i < V; i += nthr) s[i] = P.logits[i];
+    if (tid < P.n_prev) s_prev[tid] = P.prev[tid];  // loaded with the logits, not one by one below
     if (tid == 0) {
         s_nan = 0;
         s_token = 0;
@@ -984,7 +986,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleParams Pin) {
     __syncthreads();
     if (tid == 0 && P.penalty != 1.0f) {
         for (int j = 0; j < P.n_prev; j++) {
-            const uint32_t t = P.prev[j];
+            const uint32_t t = s_prev[j];
             if (t < (uint32_t)V) {
                 if (s[t] > 0.0f)
                     s[t] /= P.penalty;
@@ -1052,11 +1054,7 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleParams Pin) {
         const float maxv = s_max;
         for (int i = tid; i < V; i += nthr) s[i] = (float)exp((double)(s[i] - maxv));
         __syncthreads();
-        if (tid == 0) {
-            float sum = 0.0f;
-            for (int i = 0; i < V; i++) sum += s[i];
-            s_sum = sum;
-        }
+        if (tid == 0) s_sum = seq_sum(s, V);
         __syncthreads();
         const float sum = s_sum;
         for (int i = tid; i < V; i += nthr) s[i] = s[i] / sum;
@@ -1089,19 +1087,37 @@ __global__ __launch_bounds__(kSampleThreads) void k_sample(SampleParams Pin) {
                         if ((key & mask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
                     }
                     __syncthreads();
-                    if (tid == 0) {
-                        int cum = 0, sel = 0;
+                    if (wave == 0) {
+                        // the digit holding the rem-th largest key, as a wave
+                        // scan: lane l holds digits 255-4l .. 252-4l
                         const int rem = s_remaining;
-                        for (int d = 255; d >= 0; d--) {
-                            if (cum + (int)hist[d] >= rem) {
-                                sel = d;
-                                break;
-                            }
-                            cum += (int)hist[d];
+                        int h[4], loc = 0;
+#pragma unroll
+                        for (int q = 0; q < 4; q++) {
+                            h[q] = (int)hist[255 - 4 * lane - q];
+                            loc += h[q];
                         }
-                        s_remaining = rem - cum;
-                        s_prefix = prefix | ((unsigned)sel << shift);
-                        s_mask = mask | (255u << shift);
+                        int incl = loc;
+#pragma unroll
+                        for (int off = 1; off < 64; off <<= 1) {
+                            const int y = __shfl_up(incl, off, 64);
+                            if (lane >= off) incl += y;
+                        }
+                        const int excl = incl - loc;
+                        if (excl < rem && incl >= rem) {  // one lane: the count with the prefix is >= rem
+                            int cum = excl, sel = 255 - 4 * lane - 3;
+#pragma unroll
+                            for (int q = 0; q < 4; q++) {
+                                if (cum + h[q] >= rem) {
+                                    sel = 255 - 4 * lane - q;
+                                    break;
+                                }
+                                cum += h[q];
+                            }
+                            s_remaining = rem - cum;
+                            s_prefix = prefix | ((unsigned)sel << shift);
+                            s_mask = mask | (255u << shift);
+                        }
                     }
                     __syncthreads();
                 }
