@@ -1029,8 +1029,11 @@ __device__ __forceinline__ int eng_attn(const KCONST EngAttn &a, int task, uint3
     const int Lt = (a.from_state ? st.kvlen : a.len_const) + a.M;
     const bool small = (Lt + a.nsplit - 1) / a.nsplit <= 32;
     // at most two (row, head) pairs (the host runs other shapes on the
-    // multi-kernel path; wider instantiations cost the whole kernel registers)
-    if (npi <= 2) return small ? eng_attn_t<2, 2>(a, task, tb, st, c, smem) : eng_attn_t<2, 8>(a, task, tb, st, c, smem);
+    // multi-kernel path; wider instantiations cost the whole kernel registers).
+    // A register batch of 48 positions holds a talker split of capacity / 48
+    // rows whole; longer splits (over 32 splits' worth of cache) take more
+    // batches.
+    if (npi <= 2) return small ? eng_attn_t<2, 2>(a, task, tb, st, c, smem) : eng_attn_t<2, 3>(a, task, tb, st, c, smem);
     fail_dev(c, QTTS_EDEVICE);
     return task;
 }
