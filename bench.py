@@ -1,6 +1,6 @@
 """Benchmark: codes/s of the 1.7B talker + code-predictor per-code loop at
 batch 1 on one MI355X, with the achieved bandwidth of the kernel the loop
-runs (k_engine, one launch per code), the stand-alone Q4 GEMV's, and the
+runs (k_engine, one cooperative launch per 16 codes), the stand-alone Q4 GEMV's, and the
 oracle's codes/s on this host's CPU cores.
 
 Workload (one "step" = one code = one frame of generate_speech's loop,
@@ -121,9 +121,11 @@ def frame_bytes(tc, pc, groups, kv_len):
 
 
 def engine_roofline(frames, gpu_s, kv_len_mean):
-    """k_engine, the kernel the loop runs (one launch per code): algorithmic
-    bytes per launch over the average launch duration from HIP events on the
-    context's stream around the timed region."""
+    """k_engine, the kernel the loop runs (one cooperative launch runs up to
+    16 codes, a grid barrier between them): algorithmic bytes per code over
+    the average time per code from HIP events on the context's stream around
+    the timed region (a launch of n codes moves n times the bytes in n times
+    the time, so the ratio is the launch's)."""
     per = frame_bytes(qtts.TALKER_1P7B, qtts.PREDICTOR_1P7B, qtts.NUM_GROUPS, kv_len_mean)
     avg_s = gpu_s / frames
     achieved = per / avg_s / 1e9
@@ -133,10 +135,11 @@ def engine_roofline(frames, gpu_s, kv_len_mean):
         "peak": HBM_PEAK_GBS,
         "unit": "GB/s",
         "frac": round(achieved / HBM_PEAK_GBS, 4),
-        "traffic": read_traffic("k_engine_frame_counters.md"),
-        "kernel": "k_engine (one cooperative launch per code: sampler, 15 predictor passes, talker step)",
-        "algorithmic_bytes_per_launch": per,
-        "avg_launch_us": round(avg_s * 1e6, 2),
+        "traffic": read_traffic("k_engine_frame_counters.md", per="code"),
+        "kernel": "k_engine (one cooperative launch per 16 codes; per code: sampler, 15 predictor passes, talker step)",
+        "codes_per_launch": 16,
+        "algorithmic_bytes_per_code": per,
+        "avg_code_us": round(avg_s * 1e6, 2),
     }
 
 
@@ -543,14 +546,14 @@ def copy_calibration(ctx, nbytes=512 << 20):
     return nbytes
 
 
-def read_traffic(name, key=None):
-    """HBM bytes per launch measured by the rocprofv3 counter runs
-    (profiles/<name>), if present: the line `traffic_bytes_per_launch:` or,
-    with a key, `traffic_bytes_per_launch[key]:`."""
+def read_traffic(name, key=None, per="launch"):
+    """HBM bytes per launch (or per code) measured by the rocprofv3 counter
+    runs (profiles/<name>), if present: the line `traffic_bytes_per_launch:`
+    or, with a key, `traffic_bytes_per_launch[key]:`."""
     path = os.path.join(ROOT, "profiles", name)
     if not os.path.exists(path):
         return None
-    tag = "traffic_bytes_per_launch" + (f"[{key}]" if key else "") + ":"
+    tag = f"traffic_bytes_per_{per}" + (f"[{key}]" if key else "") + ":"
     for line in open(path):
         if line.startswith(tag):
             return int(float(line.split(":")[1]))

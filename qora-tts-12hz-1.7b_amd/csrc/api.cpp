@@ -50,8 +50,9 @@ struct qtts_ctx {
     // persistent-kernel engine
     EngState *eng_state = nullptr;  // [2]
     int *eng_done = nullptr;
+    tv_t *eng_bar = nullptr;  // [grid + 1] arrival words and the release word of the barrier between codes
     int *eng_status = nullptr;
-    uint32_t eng_tag = 0;  // tag base of the last launch
+    uint32_t eng_tag = 0;  // tag base of the last code launched
     int eng_grid = 0;
     uint64_t *eng_trace = nullptr;  // QTTS_ENGINE_TRACE: per-op block timestamps
     size_t eng_trace_cap = 0;
@@ -86,6 +87,7 @@ void ctx_release(qtts_ctx *c) {
     (void)hipFree(c->d_small);
     (void)hipFree(c->eng_state);
     (void)hipFree(c->eng_done);
+    (void)hipFree(c->eng_bar);
     (void)hipFree(c->eng_trace);
     (void)hipFree(c->mfma_x);
     (void)hipFree(c->mfma_part);
@@ -1034,6 +1036,8 @@ qtts_status eng_init(qtts_ctx *c) {
     HIP_TRY(c, hipMemset(c->eng_done, 0, 2 * sizeof(int)));
     c->eng_grid = engine_max_grid();
     if (c->eng_grid <= 0) return fail(c, QTTS_EDEVICE, "engine kernel cannot be resident on this device");
+    HIP_TRY(c, hipMalloc(&c->eng_bar, (size_t)(c->eng_grid + 1) * sizeof(tv_t)));
+    HIP_TRY(c, hipMemset(c->eng_bar, 0, (size_t)(c->eng_grid + 1) * sizeof(tv_t)));
     c->eng_tag = 0;
     return QTTS_OK;
 }
@@ -1078,19 +1082,34 @@ qtts_status eng_reset(qtts_ctx *c, int pos, int kvlen, uint64_t rng) {
     return QTTS_OK;
 }
 
-qtts_status eng_launch(qtts_ctx *c, EngProgram &P, int st_in, uint32_t *codes, int max_codes) {
-    if (c->eng_tag > 0xFFFFFFFFu - 2 * kTagStride) {
+// Runs `ncodes` codes of program P in one cooperative launch (a traced
+// launch runs one code); code f reads state copy (st_in + f) & 1.
+qtts_status eng_launch(qtts_ctx *c, EngProgram &P, int st_in, uint32_t *codes, int max_codes, int ncodes = 1) {
+    const char *trace_env = std::getenv("QTTS_ENGINE_TRACE");
+    const char *codes_env = std::getenv("QTTS_ENGINE_CODES");
+    // (the barrier between codes waits on at most 256 blocks' words)
+    const int per = P.grid > 256 ? 1 : codes_env ? std::max(1, std::atoi(codes_env)) : kEngCodesPerLaunch;
+    if (ncodes > 1 && ((trace_env && *trace_env) || per < ncodes)) {
+        const int step = (trace_env && *trace_env) ? 1 : per;
+        for (int f = 0; f < ncodes; f += step)
+            QTTS_TRY(eng_launch(c, P, (st_in + f) & 1, codes, max_codes, std::min(step, ncodes - f)));
+        return QTTS_OK;
+    }
+    if (ncodes < 1) return QTTS_OK;
+    if (c->eng_tag > 0xFFFFFFFFu - (uint32_t)(ncodes + 1) * kTagStride) {
         // Tags are about to wrap: restart them above zero-filled arenas.
         HIP_TRY(c, hipStreamSynchronize(c->stream));
         return fail(c, QTTS_ESTATE, "engine tag space exhausted; recreate the context");
     }
-    c->eng_tag += kTagStride;
     EngArgs a{};
     a.ops = P.d_ops;
     a.nops = (int)P.ops.size();
-    a.tag_base = c->eng_tag;
-    a.st_in = c->eng_state + st_in;
-    a.st_out = c->eng_state + (st_in ^ 1);
+    a.tag_base = c->eng_tag + kTagStride;
+    c->eng_tag += (uint32_t)ncodes * kTagStride;
+    a.st = c->eng_state;
+    a.st0 = st_in;
+    a.ncodes = ncodes;
+    a.bar = c->eng_bar;
     a.done = c->eng_done;
     a.status = c->eng_status;
     a.codes = codes;
@@ -2740,7 +2759,7 @@ qtts_status qtts_generate_codes(qtts_talker *t, qtts_predictor *p, qtts_kv *talk
         int done = 0;
         for (int f0 = 0; f0 < max_codes && rc == QTTS_OK && !done; f0 += batch) {
             const int nb = max_codes - f0 < batch ? max_codes - f0 : batch;
-            for (int i = 0; i < nb && rc == QTTS_OK; i++) rc = eng_launch(c, *t->frame_prog, (f0 + i) & 1, t->codes, max_codes);
+            rc = eng_launch(c, *t->frame_prog, f0 & 1, t->codes, max_codes, nb);
             if (rc != QTTS_OK) break;
             if (params->stop_on_eos && f0 + nb < max_codes) {
                 int d = 0;

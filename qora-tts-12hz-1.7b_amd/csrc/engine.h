@@ -30,7 +30,8 @@ constexpr int kEngThreads = 256;
 constexpr int eng_rows_per_thread(int cols, int np) { return np == 2 || cols == 32 ? 8 : cols == 4 ? 16 : 24; }
 constexpr int kEngNormRows = 8;  // an RMSNorm input row has <= 256 * 8 values
 constexpr int kEngMaxM = 2;    // rows per GEMV (the predictor's 2-token prefill)
-constexpr uint32_t kTagStride = 8192;  // tags reserved per launch
+constexpr uint32_t kTagStride = 8192;  // tags reserved per code
+constexpr int kEngCodesPerLaunch = 16;  // codes of the frame loop per cooperative launch
 constexpr int kEngMaxSplit = 32;
 constexpr int kEngSmemFloats = 10240;
 constexpr int kEngLdsKvPos = 32;  // positions of an LDS-resident K/V cache (one kv head)
@@ -189,8 +190,10 @@ struct EngArgs {
     const EngOp *ops;
     int nops;
     uint32_t tag_base;
-    const EngState *st_in;
-    EngState *st_out;
+    EngState *st;  // the two state copies: code f of the launch reads st[(st0 + f) & 1], its sampler
+    int st0;       //   writes the other one
+    int ncodes;    // codes (frames) run by this launch, one after another
+    tv_t *bar;     // [grid + 1]: arrival words of the barrier between codes, then its release word
     int *done;    // abort word: EOS, error or timeout
     int *status;  // qtts_status of the device side
     uint32_t *codes;  // [16][max_codes]

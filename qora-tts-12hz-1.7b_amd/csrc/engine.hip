@@ -1464,69 +1464,104 @@ __global__ __launch_bounds__(kEngThreads) void k_engine(EngArgs A) {
     if (threadIdx.x == 0) s_bad = 0;
     __syncthreads();
     Ctl c{A.done, A.status, 0u, false, nullptr};
-    EngState st;
-    st.pos = ld_dev_i32(&A.st_in->pos);
-    st.kvlen = ld_dev_i32(&A.st_in->kvlen);
-    st.frame = ld_dev_i32(&A.st_in->frame);
-    st.pad = 0;
-    st.rng = ld_dev_u64(&A.st_in->rng);
     const int G = gridDim.x;
-    for (int oi = 0; oi < A.nops; oi++) {
-        const KCONST EngOp &op = ((const KCONST EngOp *)A.ops)[oi];
-        int t = ((int)blockIdx.x - op.rot) % G;
-        if (t < 0) t += G;
-        uint64_t *tr = (A.trace && t < op.ntasks) ? A.trace + ((size_t)oi * G + blockIdx.x) * kTraceSlots : nullptr;
-        c.tr = tr;
-        if (t < op.ntasks) touch_desc(&op);
-        if (tr && threadIdx.x == 0) {
-            glb(tr)[0] = wall_clock64();
-            glb(tr)[8] = clock64();
-        }
-        for (; t < op.ntasks; t += G) {
-            int fi = -1;  // flag this task sets, if any
-            switch (op.kind) {
-                case EOP_GEMV: {
-                    // An op of M rows runs as M x its one-row tasks (one
-                    // instantiation per panel count keeps the kernel's
-                    // registers down); every row's split-K non-owners come
-                    // before all owners, so no block waits on a later task.
-                    const KCONST EngGemv &g = op.gemv;
-                    int row = 0, tt = t;
-                    if (g.M > 1) {
-                        const int per = g.w.N / (g.epi == EEPI_SWIGLU ? 64 : 32);  // tasks per K chunk
-                        const int non = per * (g.kc - 1);
-                        if (t < non * g.M) {
-                            row = t / non;
-                            tt = t - row * non;
-                        } else {
-                            const int t2 = t - non * g.M;
-                            row = t2 / per;
-                            tt = non + (t2 - row * per);
-                        }
-                    }
-                    if (g.epi == EEPI_SWIGLU)
-                        fi = eng_gemv_cols<1, 2>(g, tt, A.tag_base, c, smem, row);
-                    else
-                        fi = eng_gemv_cols<1, 1>(g, tt, A.tag_base, c, smem, row);
-                    break;
-                }
-                case EOP_ATTN: fi = eng_attn(op.attn, t, A.tag_base, st, c, smem, kvl); break;
-                case EOP_COMBINE: fi = eng_combine(op.comb, t, A.tag_base, c, smem); break;
-                case EOP_ARGMAX: eng_argmax(op.amax, A.tag_base, st, c, A.codes, A.max_codes, smem); break;
-                case EOP_SAMPLE: eng_sample(op.samp, A.tag_base, st, A.st_out, c, A.codes, A.max_codes, smem); break;
-                case EOP_EMBSUM: fi = eng_embsum(op.emb, t, A.tag_base, st, c); break;
-                default: break;
+    for (int f = 0; f < A.ncodes; f++) {
+        // Code f: its own tag space, and the state its predecessor's sampler wrote.
+        const uint32_t tag_base = A.tag_base + (uint32_t)f * kTagStride;
+        const EngState *st_in = A.st + ((A.st0 + f) & 1);
+        EngState *st_out = A.st + ((A.st0 + f + 1) & 1);
+        c.spins = 0u;
+        EngState st;
+        st.pos = ld_dev_i32(&st_in->pos);
+        st.kvlen = ld_dev_i32(&st_in->kvlen);
+        st.frame = ld_dev_i32(&st_in->frame);
+        st.pad = 0;
+        st.rng = ld_dev_u64(&st_in->rng);
+        for (int oi = 0; oi < A.nops; oi++) {
+            const KCONST EngOp &op = ((const KCONST EngOp *)A.ops)[oi];
+            int t = ((int)blockIdx.x - op.rot) % G;
+            if (t < 0) t += G;
+            uint64_t *tr = (A.trace && t < op.ntasks) ? A.trace + ((size_t)oi * G + blockIdx.x) * kTraceSlots : nullptr;
+            c.tr = tr;
+            if (t < op.ntasks) touch_desc(&op);
+            if (tr && threadIdx.x == 0) {
+                glb(tr)[0] = wall_clock64();
+                glb(tr)[8] = clock64();
             }
-            (void)fi;
-            // One barrier between tasks: LDS is reused by the next task, and
-            // the block leaves together once any thread has seen an abort.
+            for (; t < op.ntasks; t += G) {
+                int fi = -1;  // flag this task sets, if any
+                switch (op.kind) {
+                    case EOP_GEMV: {
+                        // An op of M rows runs as M x its one-row tasks (one
+                        // instantiation per panel count keeps the kernel's
+                        // registers down); every row's split-K non-owners come
+                        // before all owners, so no block waits on a later task.
+                        const KCONST EngGemv &g = op.gemv;
+                        int row = 0, tt = t;
+                        if (g.M > 1) {
+                            const int per = g.w.N / (g.epi == EEPI_SWIGLU ? 64 : 32);  // tasks per K chunk
+                            const int non = per * (g.kc - 1);
+                            if (t < non * g.M) {
+                                row = t / non;
+                                tt = t - row * non;
+                            } else {
+                                const int t2 = t - non * g.M;
+                                row = t2 / per;
+                                tt = non + (t2 - row * per);
+                            }
+                        }
+                        if (g.epi == EEPI_SWIGLU)
+                            fi = eng_gemv_cols<1, 2>(g, tt, tag_base, c, smem, row);
+                        else
+                            fi = eng_gemv_cols<1, 1>(g, tt, tag_base, c, smem, row);
+                        break;
+                    }
+                    case EOP_ATTN: fi = eng_attn(op.attn, t, tag_base, st, c, smem, kvl); break;
+                    case EOP_COMBINE: fi = eng_combine(op.comb, t, tag_base, c, smem); break;
+                    case EOP_ARGMAX: eng_argmax(op.amax, tag_base, st, c, A.codes, A.max_codes, smem); break;
+                    case EOP_SAMPLE: eng_sample(op.samp, tag_base, st, st_out, c, A.codes, A.max_codes, smem); break;
+                    case EOP_EMBSUM: fi = eng_embsum(op.emb, t, tag_base, st, c); break;
+                    default: break;
+                }
+                (void)fi;
+                // One barrier between tasks: LDS is reused by the next task, and
+                // the block leaves together once any thread has seen an abort.
+                if (c.bad) s_bad = 1;
+                __syncthreads();
+                if (s_bad) return;
+            }
+            if (tr && threadIdx.x == 0) {
+                glb(tr)[1] = wall_clock64();
+                glb(tr)[9] = clock64();
+            }
+        }
+        if (f + 1 < A.ncodes) {
+            // Code boundary: every value the next code reads from this one (the
+            // logits, the last hidden row, the appended K/V rows, the state) was
+            // stored device-coherently; once each thread's stores are complete,
+            // all blocks arrive, and no block starts the next code before every
+            // block has finished this one.  The next code's plain loads (cached
+            // K/V rows) touch only lines no block has read in this launch.
+            // Block 0 gathers the arrival words and publishes one release word,
+            // which the other blocks poll (one word each, not all G).
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+            const uint32_t btag = tag_base + kTagStride - 1u;
+            if (threadIdx.x == 0) put_tv_u32(A.bar + blockIdx.x, 1u, btag);
+            if (blockIdx.x == 0) {
+                if (threadIdx.x < 64) {
+                    const int lane = (int)threadIdx.x;
+                    const int cnt = G > lane ? (G - lane + 63) / 64 : 0;  // <= 4 (G <= 256)
+                    float arrived[4];
+                    wait_strided<4>(A.bar + lane, 64, cnt, btag, arrived, c);
+                    if (lane == 0) put_tv_u32(A.bar + G, 1u, btag);
+                }
+            } else if (threadIdx.x == 0) {
+                (void)wait_tv_u32(A.bar + G, btag, c);
+            }
             if (c.bad) s_bad = 1;
             __syncthreads();
             if (s_bad) return;
-        }
-        if (tr && threadIdx.x == 0) {
-            glb(tr)[1] = wall_clock64();
-            glb(tr)[9] = clock64();
         }
     }
 }
