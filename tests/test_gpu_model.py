@@ -202,6 +202,41 @@ def test_loop_tiny(tiny, greedy):
     assert rel_err(lh, olh) < REL_TOL
 
 
+@pytest.mark.parametrize("per_launch", ["1", "7", None])
+def test_loop_tiny_codes_per_launch(tiny, monkeypatch, per_launch):
+    """The frame engine runs up to 16 codes per cooperative launch with a grid
+    barrier between codes (QTTS_ENGINE_CODES overrides the count): 1, 7 and
+    the default give the oracle's codes, cache length and cache rows, and an
+    EOS that falls inside a launch stops the loop at the same frame."""
+    tw, pw, t, p, ot, op = tiny
+    if per_launch is None:
+        monkeypatch.delenv("QTTS_ENGINE_CODES", raising=False)
+    else:
+        monkeypatch.setenv("QTTS_ENGINE_CODES", per_launch)
+    last_hidden, text, pad = _loop_inputs(tw, 27)
+    logits = ot.apply_codec_head(last_hidden)
+    frames = 40
+    params = qtts.loop_params(frames, temperature=0.8, top_k=50, repetition_penalty=1.05, stop_on_eos=False)
+    kv, okv = t.new_kv(48), ot.new_kv(48)
+    got = qtts.generate_codes(t, p, kv, p.new_kv(), last_hidden, logits, 0, text, pad, params, seed=31)
+    ref = oracle.generate_codes(ot, op, okv, op.new_kv(), last_hidden, logits, 0, text, pad, params, seed=31)
+    assert got.shape == ref.shape == (16, frames)
+    assert np.array_equal(got, ref), np.argwhere(got != ref)[:5]
+    assert len(kv) == len(okv) == frames
+    (k, v), (ok, ov) = kv.store(), okv.store()
+    assert k.shape == ok.shape and rel_err(k, ok) < REL_TOL and rel_err(v, ov) < REL_TOL
+    # EOS at frame 20's code 0: inside the second launch of 16, the third of 7
+    eos = int(ref[0, 20])
+    first = int(np.argmax(ref[0] == eos))
+    params = qtts.loop_params(frames, temperature=0.8, top_k=50, repetition_penalty=1.05, stop_on_eos=True,
+                              codec_eos_id=eos)
+    kv = t.new_kv(48)
+    got = qtts.generate_codes(t, p, kv, p.new_kv(), last_hidden, logits, 0, text, pad, params, seed=31)
+    assert got.shape == (16, first)
+    assert np.array_equal(got, ref[:, :first])
+    assert len(kv) == first
+
+
 def test_loop_tiny_talker_only_and_eos(tiny):
     tw, _, t, _, ot, _ = tiny
     hidden = tw.cfg.hidden
