@@ -23,19 +23,25 @@ namespace qtts {
 
 using tv_t = uint64_t;  // float bits | tag << 32
 
-constexpr int kEngThreads = 256;
+// One 512-thread block per CU: two waves per SIMD, so a task's
+// accumulation is spread over twice the lanes and every wave has a partner
+// to issue while it waits.  The kernel must then fit 256 registers a wave
+// (VGPRs and AGPRs together).
+constexpr int kEngThreads = 512;
+constexpr int kEngWaves = kEngThreads / 64;
 // Rows per thread of a GEMV task over a slice of `cols` columns of `np`
-// panels (the K chunk is at most 256 times this): a task's weights stay in
-// registers from issue to use, cols / 8 dwords per row (one for 4 columns).
-constexpr int eng_rows_per_thread(int cols, int np) { return np == 2 || cols == 32 ? 8 : cols == 4 ? 16 : 24; }
-constexpr int kEngNormRows = 8;  // an RMSNorm input row has <= 256 * 8 values
+// panels (the K chunk is at most kEngThreads times this): a task's weights
+// stay in registers from issue to use, cols / 8 dwords per row (one for 4
+// columns).
+constexpr int eng_rows_per_thread(int cols, int np) { return np == 2 || cols == 32 ? 4 : cols == 4 ? 8 : 12; }
+constexpr int kEngNormRows = 4;  // an RMSNorm input row has <= kEngThreads * 4 values
 constexpr int kEngMaxM = 2;    // rows per GEMV (the predictor's 2-token prefill)
 constexpr uint32_t kTagStride = 8192;  // tags reserved per code
 constexpr int kEngCodesPerLaunch = 16;  // codes of the frame loop per cooperative launch
 constexpr int kEngMaxSplit = 32;
 constexpr int kEngSmemFloats = 10240;
 constexpr int kEngLdsKvPos = 32;  // positions of an LDS-resident K/V cache (one kv head)
-constexpr int kEngArgtabMax = 256 * 8;  // logits of an EIN_ARGTAB input
+constexpr int kEngArgtabMax = 2048;  // logits of an EIN_ARGTAB input
 
 enum EngOpKind : int { EOP_GEMV = 1, EOP_ATTN = 2, EOP_COMBINE = 3, EOP_ARGMAX = 4, EOP_SAMPLE = 5, EOP_EMBSUM = 6 };
 enum EngIn : int { EIN_TV = 0, EIN_PLAIN = 1, EIN_EMBED = 2, EIN_ARGTAB = 3 };
@@ -52,14 +58,14 @@ struct EngInput {
     int table_rows;       //   a code past the last row gives zeros)
     int n;                // EIN_ARGTAB: logits in tv (<= kEngArgtabMax)
     int parts;            // EIN_TV with norm: 2 = the row is tv[k] + tv[K + k] (a split_out GEMV's
-                          //   two chunks; K <= 128 * kEngNormRows)
+                          //   two chunks; K <= kEngThreads / 2 * kEngNormRows)
 };
 
 struct EngGemv {
     DevQ4 w;
     int M;       // rows (1 or 2): each row's tasks run separately (M x the one-row tasks)
     int kc;      // K chunks; chunk 0 owns the epilogue
-    int kchunk;  // rows per chunk (multiple of 256, <= 256 * eng_rows_per_thread(cols, panels))
+    int kchunk;  // rows per chunk (multiple of kEngThreads, <= kEngThreads * eng_rows_per_thread(cols, panels))
     int cols;    // output columns per task: 32, 16, 8 or 4 (a slice of a 32-column panel);
                  // 32 or 16 for SwiGLU
     int epi;

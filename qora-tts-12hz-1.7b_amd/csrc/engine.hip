@@ -141,11 +141,24 @@ __device__ __forceinline__ void put_tv_u32(tv_t *p, uint32_t x, uint32_t tag) {
     st_dev_u64(p, ((uint64_t)tag << 32) | (uint64_t)x);
 }
 
-// sample_argmax (src/code_predictor.rs:328-334) of n <= 256 * NA tagged
-// logits over the block: the last index of the maximum (-1 when every value
-// is NaN).  Every thread gets the result; *anynan says whether any logit was
-// NaN.  scr: 8 words of LDS that no thread touches again before the next
-// block barrier.
+// Sum of the block's kEngWaves per-wave values v[w * stride], as a pairwise
+// tree (fixed order: the result does not depend on timing).
+__device__ __forceinline__ float waves_sum(const float *v, int stride) {
+    float t[kEngWaves];
+#pragma unroll
+    for (int w = 0; w < kEngWaves; w++) t[w] = v[w * stride];
+#pragma unroll
+    for (int h = kEngWaves / 2; h >= 1; h /= 2)
+#pragma unroll
+        for (int w = 0; w < h; w++) t[w] = t[w] + t[w + h];
+    return t[0];
+}
+
+// sample_argmax (src/code_predictor.rs:328-334) of n <= kEngThreads * NA
+// tagged logits over the block: the last index of the maximum (-1 when every
+// value is NaN).  Every thread gets the result; *anynan says whether any
+// logit was NaN.  scr: 2 * kEngWaves words of LDS that no thread touches
+// again before the next block barrier.
 template <int NA>
 __device__ __forceinline__ int block_argmax(const tv_t *logits, int n, uint32_t tag, Ctl &c, float *scr, int *anynan) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -175,7 +188,7 @@ __device__ __forceinline__ int block_argmax(const tv_t *logits, int n, uint32_t 
         }
     }
     int *si = reinterpret_cast<int *>(scr);
-    float *sv = scr + kEngThreads / 64;
+    float *sv = scr + kEngWaves;
     *anynan = __syncthreads_or(nan);
     if (lane == 0) {
         sv[wave] = bv;
@@ -185,7 +198,7 @@ __device__ __forceinline__ int block_argmax(const tv_t *logits, int n, uint32_t 
     float b = -INFINITY;
     int ix = -1;
 #pragma unroll
-    for (int w = 0; w < kEngThreads / 64; w++)
+    for (int w = 0; w < kEngWaves; w++)
         if (si[w] >= 0 && (ix < 0 || sv[w] > b || (sv[w] == b && si[w] > ix))) {
             b = sv[w];
             ix = si[w];
@@ -203,8 +216,8 @@ __device__ __forceinline__ int block_argmax(const tv_t *logits, int n, uint32_t 
 template <int M, int NP, int C, int R>
 __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint32_t tb, Ctl &c, float *smem, int row) {
     constexpr int DW = q4_slice_dwords<C>();
-    float *red = smem;                  // [NP][M][4 waves][C]
-    float *scr = red + NP * M * 4 * C;  // [M][4] block-sum partials
+    float *red = smem;                          // [NP][M][kEngWaves][C]
+    float *scr = red + NP * M * kEngWaves * C;  // [M][kEngWaves] block-sum partials
     const int tid = threadIdx.x;
     const int N = g.w.N, K = g.w.K;
     const int Nout = N / NP;
@@ -320,7 +333,7 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
                 for (int i = 0; i < R; i++) asm volatile("" : "+v"(gam[i]));
                 int anynan = 0;
                 const int ix = block_argmax<kEngArgtabMax / kEngThreads>(in.tv, in.n, tb + in.tag, c,
-                                                                        smem + kEngSmemFloats - 8, &anynan);
+                                                                        smem + kEngSmemFloats - 2 * kEngWaves, &anynan);
                 const uint32_t tok = (ix < 0 || anynan) ? 0u : (uint32_t)ix;  // the argmax step's code
                 const int nj = K > tid ? (K - tid + kEngThreads - 1) / kEngThreads : 0;  // <= NR
                 const auto *trow = glb(in.table) + (size_t)(tok < (uint32_t)in.table_rows ? tok : 0u) * K + tid;
@@ -438,12 +451,12 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
 #pragma unroll
     for (int pp = 0; pp < NP; pp++)
 #pragma unroll
-        for (int m = 0; m < M; m++) dpp_reduce<C>(acc[pp][m], &red[(pp * M + m) * 4 * C]);
+        for (int m = 0; m < M; m++) dpp_reduce<C>(acc[pp][m], &red[(pp * M + m) * kEngWaves * C]);
     if (g.norm) {
 #pragma unroll
         for (int m = 0; m < M; m++) {
             const float w = wave_sum(ssq[m]);
-            if ((tid & 63) == 0) scr[4 * m + (tid >> 6)] = w;
+            if ((tid & 63) == 0) scr[kEngWaves * m + (tid >> 6)] = w;
         }
     }
     __syncthreads();
@@ -451,8 +464,7 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
     float inv[M];  // 1 / rms of each input row (rms_norm_f16, src/gemv.rs:406-417)
 #pragma unroll
     for (int m = 0; m < M; m++)
-        inv[m] = g.norm ? 1.0f / sqrtf(((scr[4 * m] + scr[4 * m + 1]) + (scr[4 * m + 2] + scr[4 * m + 3])) / (float)K + 1e-6f)
-                        : 1.0f;
+        inv[m] = g.norm ? 1.0f / sqrtf(waves_sum(&scr[kEngWaves * m], 1) / (float)K + 1e-6f) : 1.0f;
     if (g.norm_plain && tt == 0 && ch == 0 && row + M == g.M) {
         // the normed last row, for a later launch
 #pragma unroll
@@ -467,8 +479,7 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
         float y[NP];
 #pragma unroll
         for (int pp = 0; pp < NP; pp++) {
-            const float *rw = &red[(pp * M + m) * 4 * C + j];
-            y[pp] = (rw[0] + rw[C]) + (rw[2 * C] + rw[3 * C]);
+            y[pp] = waves_sum(&red[(pp * M + m) * kEngWaves * C + j], C);
         }
         // 5. split-K: non-owners publish partials; the owner adds them in order.
         if (ch > 0 && NP == 1 && g.split_out) {
@@ -542,14 +553,17 @@ __device__ __forceinline__ int eng_gemv_cols(const KCONST EngGemv &g, int task, 
 // over the split (src/talker.rs:304-331), causal across the M new rows.
 // ---------------------------------------------------------------------------
 // NPI: (row, head) pairs rounded up; KJ: positions per thread held in
-// registers for the scores (16 lanes each) -- a register batch covers
-// PB = 16 * KJ positions (talker splits are <= 128 long, predictor steps <= 32).
+// registers for the scores (16 lanes each, NSLOT = kEngThreads / 16 positions
+// at a time) -- a register batch covers PB = NSLOT * KJ positions.
 template <int NPI, int KJ>
 __device__ __forceinline__ int eng_attn_t(const KCONST EngAttn &a, int task, uint32_t tb, const EngState &st, Ctl &c,
                                           float *smem) {
     constexpr int HD = 128, HALF = 64, CH = 256;
-    constexpr int VJ = 2 * KJ;     // positions per thread for P.V (8 groups of 32 lanes)
-    constexpr int PB = 16 * KJ;    // positions per register batch
+    constexpr int NSLOT = kEngThreads / 16;  // positions per score round (16 lanes each)
+    constexpr int NR8 = kEngThreads / 32;    // P.V position groups (32 lanes of 4 dims each)
+    constexpr int PB = NSLOT * KJ;           // positions per register batch
+    constexpr int VJ = PB / NR8;             // positions per thread for P.V
+    static_assert(PB <= CH, "a register batch must fit the score buffer");
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int G = a.nq / a.nkv;
     const int M = a.M;
@@ -567,11 +581,11 @@ __device__ __forceinline__ int eng_attn_t(const KCONST EngAttn &a, int task, uin
     float *sc = vn + kEngMaxM * HD;      // [NPI][CH] scores
     float *pt = sc + kEngMaxM * 4 * CH;  // [CH][NPI] probabilities (position-major)
     float *ml = pt + kEngMaxM * 4 * CH;  // [NPI][2]
-    float *pvb = ml + 16;                // [4 waves][NPI][HD] P.V partials
+    float *pvb = ml + 16;                // [kEngWaves][NPI][HD] P.V partials
     float *Kb = a.kcache + (size_t)kvh * a.kv_cap * HD;
     float *Vb = a.vcache + (size_t)kvh * a.kv_cap * HD;
     const int l16 = tid & 15, slot = tid >> 4;  // scores: 16 lanes per position, 8 dims per lane
-    const int d4 = tid & 31, r8 = tid >> 5;     // P.V: 4 dims, every 8th position
+    const int d4 = tid & 31, r8 = tid >> 5;     // P.V: 4 dims, every NR8-th position
 
     // Cached rows [0, base) for the register batch starting at position b0.
     // from_state: the rows were written by earlier launches, so plain loads
@@ -591,7 +605,7 @@ __device__ __forceinline__ int eng_attn_t(const KCONST EngAttn &a, int task, uin
     auto load_k = [&](int b0) {
 #pragma unroll
         for (int j = 0; j < KJ; j++) {
-            const int tt = b0 + slot + 16 * j, t = t0 + tt;
+            const int tt = b0 + slot + NSLOT * j, t = t0 + tt;
             kr[j][0] = kr[j][1] = z4;
             if (tt < nt && t < base) {
                 const float *src = Kb + (size_t)t * HD + l16 * 8;
@@ -603,7 +617,7 @@ __device__ __forceinline__ int eng_attn_t(const KCONST EngAttn &a, int task, uin
     auto load_v = [&](int b0) {
 #pragma unroll
         for (int u = 0; u < VJ; u++) {
-            const int tt = b0 + r8 + 8 * u, t = t0 + tt;
+            const int tt = b0 + r8 + NR8 * u, t = t0 + tt;
             vr[u] = z4;
             if (tt < nt && t < base) vr[u] = load16(Vb + (size_t)t * HD + 4 * d4);
         }
@@ -612,7 +626,7 @@ __device__ __forceinline__ int eng_attn_t(const KCONST EngAttn &a, int task, uin
     auto patch_k = [&](int b0) {
 #pragma unroll
         for (int j = 0; j < KJ; j++) {
-            const int tt = b0 + slot + 16 * j, t = t0 + tt;
+            const int tt = b0 + slot + NSLOT * j, t = t0 + tt;
             if (tt < nt && t >= base) {
                 kr[j][0] = *reinterpret_cast<const u32x4 *>(&kn[(t - base) * HD + l16 * 8]);
                 kr[j][1] = *reinterpret_cast<const u32x4 *>(&kn[(t - base) * HD + l16 * 8 + 4]);
@@ -622,7 +636,7 @@ __device__ __forceinline__ int eng_attn_t(const KCONST EngAttn &a, int task, uin
     auto patch_v = [&](int b0) {
 #pragma unroll
         for (int u = 0; u < VJ; u++) {
-            const int tt = b0 + r8 + 8 * u, t = t0 + tt;
+            const int tt = b0 + r8 + NR8 * u, t = t0 + tt;
             if (tt < nt && t >= base) vr[u] = *reinterpret_cast<const u32x4 *>(&vn[(t - base) * HD + 4 * d4]);
         }
     };
@@ -693,7 +707,7 @@ __device__ __forceinline__ int eng_attn_t(const KCONST EngAttn &a, int task, uin
     __syncthreads();
     stamp(c, 3);
     // 2. QK-norm (src/talker.rs:86-99) + split-half RoPE (src/rope.rs:79-92), one wave per vector
-    for (int vi = wave; vi < M * (G + 1); vi += kEngThreads / 64) {
+    for (int vi = wave; vi < M * (G + 1); vi += kEngWaves) {
         const int m = vi / (G + 1), r = vi - m * (G + 1);
         float *vec = r < G ? &qs[(m * G + r) * HD] : &kn[m * HD];
         const float x1 = vec[lane], x2 = vec[lane + HALF];
@@ -729,7 +743,7 @@ __device__ __forceinline__ int eng_attn_t(const KCONST EngAttn &a, int task, uin
         patch_k(b0);
 #pragma unroll
         for (int j = 0; j < KJ; j++) {
-            const int tt = b0 + slot + 16 * j, t = t0 + tt;
+            const int tt = b0 + slot + NSLOT * j, t = t0 + tt;
             const float k8[8] = {__uint_as_float(kr[j][0].x), __uint_as_float(kr[j][0].y), __uint_as_float(kr[j][0].z),
                                  __uint_as_float(kr[j][0].w), __uint_as_float(kr[j][1].x), __uint_as_float(kr[j][1].y),
                                  __uint_as_float(kr[j][1].z), __uint_as_float(kr[j][1].w)};
@@ -750,7 +764,7 @@ __device__ __forceinline__ int eng_attn_t(const KCONST EngAttn &a, int task, uin
     // 5. local softmax statistics, one wave per (row, head) (src/talker.rs:319-326);
     //    the probabilities go to pt position-major, zero past the split.
     const int ntp = (nt + PB - 1) / PB * PB;  // P.V reads whole batches
-    for (int pi = wave; pi < NPI; pi += kEngThreads / 64) {
+    for (int pi = wave; pi < NPI; pi += kEngWaves) {
         if (pi >= npi) {
             for (int t = lane; t < ntp; t += 64) pt[t * NPI + pi] = 0.0f;
             continue;
@@ -777,7 +791,7 @@ __device__ __forceinline__ int eng_attn_t(const KCONST EngAttn &a, int task, uin
     __syncthreads();
     stamp(c, 7);
     // 6. P.V (src/talker.rs:327-331): thread (4 dims, position group) over
-    //    its positions; the 8 groups are added by a lane swap across the
+    //    its positions; the NR8 groups are added by a lane swap across the
     //    wave halves and then through LDS.
     {
         float acc[NPI][4];
@@ -790,7 +804,7 @@ __device__ __forceinline__ int eng_attn_t(const KCONST EngAttn &a, int task, uin
             patch_v(b0);
 #pragma unroll
             for (int u = 0; u < VJ; u++) {
-                const int tt = b0 + r8 + 8 * u;
+                const int tt = b0 + r8 + NR8 * u;
                 float p[NPI];
                 if (NPI == 2) {
                     const float2 q = *reinterpret_cast<const float2 *>(&pt[tt * NPI]);
@@ -832,8 +846,7 @@ __device__ __forceinline__ int eng_attn_t(const KCONST EngAttn &a, int task, uin
         for (int idx = tid; idx < npi * HD; idx += kEngThreads) {
             const int pi = idx / HD, d = idx - pi * HD;
             const int m = pi / G, g = pi - m * G, h = kvh * G + g;
-            const float o = (pvb[(0 * NPI + pi) * HD + d] + pvb[(1 * NPI + pi) * HD + d]) +
-                            (pvb[(2 * NPI + pi) * HD + d] + pvb[(3 * NPI + pi) * HD + d]);
+            const float o = waves_sum(&pvb[pi * HD + d], NPI * HD);
             if (a.nsplit == 1) {
                 const float l = ml[pi * 2 + 1];
                 put_tv(&a.out[(size_t)m * a.nq * HD + h * HD + d], o / l, tb + a.out_tag);
@@ -875,7 +888,7 @@ __device__ __forceinline__ int eng_attn_lean(const KCONST EngAttn &a, int task, 
     if (a.qkv_table) {
         int anynan = 0;
         const int ix = block_argmax<kEngArgtabMax / kEngThreads>(a.logits, a.logits_n, tb + a.logits_tag, c,
-                                                                smem + kEngSmemFloats - 8, &anynan);
+                                                                smem + kEngSmemFloats - 2 * kEngWaves, &anynan);
         tcode = (ix < 0 || anynan) ? 0u : (uint32_t)ix;
     }
     if (wave >= M * G) return task;
@@ -994,7 +1007,7 @@ __device__ __forceinline__ int eng_attn_lean(const KCONST EngAttn &a, int task, 
     float part[NP];
 #pragma unroll
     for (int t = 0; t < NP; t++) part[t] = qn0 * kr[t].x + qn1 * kr[t].y;
-    float *red = smem;  // [4 waves][NP]
+    float *red = smem;  // [M * G waves][NP]
     dpp_reduce<NP>(part, red);
     // 5. softmax across lanes, position t on lane t
     const float sc = lane < nvis ? red[wave * NP + lane] * a.scale : -INFINITY;
@@ -1027,55 +1040,71 @@ __device__ __forceinline__ int eng_attn(const KCONST EngAttn &a, int task, uint3
     if (a.lds_kv) return eng_attn_lean(a, task, tb, c, smem, kvl);
     const int npi = a.M * (a.nq / a.nkv);
     const int Lt = (a.from_state ? st.kvlen : a.len_const) + a.M;
-    const bool small = (Lt + a.nsplit - 1) / a.nsplit <= 32;
+    const bool small = (Lt + a.nsplit - 1) / a.nsplit <= kEngThreads / 16;
     // at most two (row, head) pairs (the host runs other shapes on the
     // multi-kernel path; wider instantiations cost the whole kernel registers).
-    // A register batch of 48 positions holds a talker split of capacity / 48
+    // A register batch of 64 positions holds a talker split of capacity / 48
     // rows whole; longer splits (over 32 splits' worth of cache) take more
     // batches.
-    if (npi <= 2) return small ? eng_attn_t<2, 2>(a, task, tb, st, c, smem) : eng_attn_t<2, 3>(a, task, tb, st, c, smem);
+    if (npi <= 2) return small ? eng_attn_t<2, 1>(a, task, tb, st, c, smem) : eng_attn_t<2, 2>(a, task, tb, st, c, smem);
     fail_dev(c, QTTS_EDEVICE);
     return task;
 }
 
-// Combine the splits of one (row, query head): flash-decode merge.  Threads
-// 0..127 load their dim of every split's P.V while threads 128.. load the
-// splits' (max, sum): one round trip for all of it.
+// Combine the splits of one (row, query head): flash-decode merge.  Thread
+// (dim d, quarter q) loads dim d of splits q, q + 4, ... (at most
+// kEngMaxSplit / 4) while threads 0.. also load the splits' (max, sum): one
+// round trip for all of it.  The quarters' weighted sums are added in
+// quarter order (a fixed order: the result does not depend on timing).
 __device__ __forceinline__ int eng_combine(const KCONST EngCombine &cb, int task, uint32_t tb, Ctl &c, float *smem) {
-    constexpr int HD = 128;
+    constexpr int HD = 128, NQ = kEngThreads / HD, NS = kEngMaxSplit / NQ;
+    static_assert(kEngThreads % HD == 0 && kEngMaxSplit % NQ == 0, "combine layout");
     const int m = task / cb.nq, h = task - m * cb.nq;
-    const int tid = threadIdx.x;
+    const int tid = threadIdx.x, d = tid % HD, q = tid / HD;
     const int ns = cb.nsplit;
     const tv_t *base = cb.part + ((size_t)m * cb.nq + h) * ns * (HD + 2);
     float *sm = smem;                   // [kEngMaxSplit] split max
     float *sl = smem + kEngMaxSplit;    // [kEngMaxSplit] split sum
-    float os[kEngMaxSplit];
-    if (tid < HD) {
-        wait_strided<kEngMaxSplit>(base + 2 + tid, HD + 2, ns, tb + cb.part_tag, os, c);
-    } else if (tid - HD < ns) {
-        const int sp = tid - HD;
-        const tv_t *ptr[2] = {base + (size_t)sp * (HD + 2), base + (size_t)sp * (HD + 2) + 1};
+    float *po = sl + kEngMaxSplit;      // [NQ][HD] weighted P.V sums of each quarter
+    float *pl = po + NQ * HD;           // [NQ][HD] weighted sums of each quarter
+    float os[NS];
+    const int cnt = ns > q ? (ns - q + NQ - 1) / NQ : 0;
+    float ml[2];
+    if (tid < ns) {
+        const tv_t *ptr[2] = {base + (size_t)tid * (HD + 2), base + (size_t)tid * (HD + 2) + 1};
         const uint32_t tg[2] = {tb + cb.part_tag, tb + cb.part_tag};
-        float ml[2];
         wait_list<2>(ptr, tg, 2, ml, c);
-        sm[sp] = ml[0];
-        sl[sp] = ml[1];
+    }
+    wait_strided<NS>(base + (size_t)q * (HD + 2) + 2 + d, (size_t)NQ * (HD + 2), cnt, tb + cb.part_tag, os, c);
+    if (tid < ns) {
+        sm[tid] = ml[0];
+        sl[tid] = ml[1];
     }
     __syncthreads();
+    float mx = -INFINITY;
+#pragma unroll
+    for (int sp = 0; sp < kEngMaxSplit; sp++)
+        if (sp < ns) mx = fmaxf(mx, sm[sp]);
+    float o = 0.0f, l = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NS; i++) {
+        const int sp = q + NQ * i;
+        if (i >= cnt || sm[sp] == -INFINITY) continue;
+        const float w = expf(sm[sp] - mx);
+        o += w * os[i];
+        l += w * sl[sp];
+    }
+    po[q * HD + d] = o;
+    pl[q * HD + d] = l;
+    __syncthreads();
     if (tid < HD) {
-        float mx = -INFINITY;
+        float ot = 0.0f, lt = 0.0f;
 #pragma unroll
-        for (int sp = 0; sp < kEngMaxSplit; sp++)
-            if (sp < ns) mx = fmaxf(mx, sm[sp]);
-        float o = 0.0f, l = 0.0f;
-#pragma unroll
-        for (int sp = 0; sp < kEngMaxSplit; sp++) {
-            if (sp >= ns || sm[sp] == -INFINITY) continue;
-            const float w = expf(sm[sp] - mx);
-            o += w * os[sp];
-            l += w * sl[sp];
+        for (int qq = 0; qq < NQ; qq++) {
+            ot += po[qq * HD + d];
+            lt += pl[qq * HD + d];
         }
-        put_tv(&cb.out[(size_t)m * cb.nq * HD + h * HD + tid], o / l, tb + cb.out_tag);
+        put_tv(&cb.out[(size_t)m * cb.nq * HD + h * HD + d], ot / lt, tb + cb.out_tag);
     }
     return task;
 }
@@ -1084,7 +1113,7 @@ __device__ __forceinline__ int eng_combine(const KCONST EngCombine &cb, int task
 __device__ __forceinline__ void eng_argmax(const KCONST EngArgmax &a, uint32_t tb, const EngState &st, Ctl &c, uint32_t *codes,
                            int max_codes, float *smem) {
     int anynan = 0;
-    const int ix = block_argmax<16>(a.logits, a.n, tb + a.logits_tag, c, smem, &anynan);  // n <= 4096
+    const int ix = block_argmax<4096 / kEngThreads>(a.logits, a.n, tb + a.logits_tag, c, smem, &anynan);  // n <= 4096
     if (threadIdx.x == 0) {
         uint32_t code = ix < 0 ? 0u : (uint32_t)ix;
         if (anynan) {
@@ -1125,7 +1154,7 @@ __device__ __forceinline__ int seq_find(const float *p, int n, float r) {
     return -1;
 }
 
-// Exclusive scan over the 256-thread block.
+// Exclusive scan over the block.
 __device__ int block_exscan(int v, int *wsum, int *total) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     int x = v;
@@ -1138,7 +1167,7 @@ __device__ int block_exscan(int v, int *wsum, int *total) {
     if (lane == 63) wsum[wave] = x;
     __syncthreads();
     int base = 0, tot = 0;
-    for (int w = 0; w < kEngThreads / 64; w++) {
+    for (int w = 0; w < kEngWaves; w++) {
         if (w < wave) base += wsum[w];
         tot += wsum[w];
     }
@@ -1164,7 +1193,7 @@ __device__ __forceinline__ void eng_sample(const KCONST EngSample &P, uint32_t t
     uint64_t rng = st.rng;
 
     {
-        constexpr int NS = 16;  // V <= 4096
+        constexpr int NS = 4096 / kEngThreads;  // V <= 4096
         float lv[NS];
 #pragma unroll
         for (int k = 0; k < NS; k++) {
@@ -1227,7 +1256,7 @@ __device__ __forceinline__ void eng_sample(const KCONST EngSample &P, uint32_t t
         if (tid == 0) {
             float b = -INFINITY;
             int ix = -1;
-            for (int w = 0; w < kEngThreads / 64; w++)
+            for (int w = 0; w < kEngWaves; w++)
                 if (ired[w] >= 0 && (ix < 0 || fred[w] > b || (fred[w] == b && ired[w] > ix))) {
                     b = fred[w];
                     ix = ired[w];
@@ -1247,7 +1276,7 @@ __device__ __forceinline__ void eng_sample(const KCONST EngSample &P, uint32_t t
         __syncthreads();
         if (tid == 0) {
             float t = -INFINITY;
-            for (int w = 0; w < kEngThreads / 64; w++) t = fmaxf(t, fred[w]);
+            for (int w = 0; w < kEngWaves; w++) t = fmaxf(t, fred[w]);
             fmisc[0] = t;
         }
         __syncthreads();
@@ -1344,7 +1373,7 @@ __device__ __forceinline__ void eng_sample(const KCONST EngSample &P, uint32_t t
                     if (keep_bits & (1u << (i - i0))) list[pos++] = i;
                 __syncthreads();
                 // compact the kept probabilities, in index order, into s[0..tot)
-                constexpr int NS = 16;  // V <= 4096
+                constexpr int NS = 4096 / kEngThreads;  // V <= 4096
                 float kv[NS];
 #pragma unroll
                 for (int k = 0; k < NS; k++) {
@@ -1403,7 +1432,7 @@ __device__ __forceinline__ void eng_sample(const KCONST EngSample &P, uint32_t t
     __syncthreads();
 }
 
-// Next talker input (src/generate_new.rs:270-286), 256 columns per task.
+// Next talker input (src/generate_new.rs:270-286), kEngThreads columns per task.
 __device__ __forceinline__ int eng_embsum(const KCONST EngEmbSum &E, int task, uint32_t tb, const EngState &st, Ctl &c) {
     const int j = task * kEngThreads + threadIdx.x;
     if (E.mode == 2) {  // publish a plain row (host input) as a tagged vector
