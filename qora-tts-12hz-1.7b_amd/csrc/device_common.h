@@ -268,6 +268,43 @@ __device__ __forceinline__ void dpp_reduce(const float (&acc)[C], float *red) {
     }
 }
 
+constexpr int kDppRowRor8 = 0x128;  // lane i <- (i + 8) mod 16: the partner i ^ 8 within each 16
+
+// Column sums of a block's acc[32] (one partial per column per lane), step
+// one: halving stages leave each lane with one column's sum over the 64 lanes
+// of its wave.  Lane bit 5 goes first, by v_permlane32_swap (the upper half
+// of one register swapped with the lower half of another: one swap and one
+// add per pair of columns), then bit 4 by v_permlane16_swap, bits 0-2 by DPP
+// within rows of 16 lanes, and bit 3 as a plain add of the value rotated by 8
+// in the row, so lanes l and l ^ 8 end with the same sum.  Lanes with bit 3
+// clear store it to red[wave * 32 + col].  After a barrier, red[w][c] summed
+// over the waves is column c.
+__device__ __forceinline__ void lane_reduce32(const float (&acc)[32], float *red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float v[32];
+#pragma unroll
+    for (int j = 0; j < 32; j++) v[j] = acc[j];
+    // bit 5: lanes < 32 keep columns 0..15, lanes >= 32 columns 16..31
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[j]), __float_as_uint(v[j + 16]), false, false);
+        v[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    // bit 4: rows 0 and 2 keep the first 8 of their 16, rows 1 and 3 the last 8
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[j]), __float_as_uint(v[j + 8]), false, false);
+        v[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    const bool b0 = lane & 1, b1 = lane & 2, b2 = lane & 4, b3 = lane & 8;
+    dpp_stage<8, 0>(v, b0);
+    dpp_stage<4, 1>(v, b1);
+    dpp_stage<2, 2>(v, b2);
+    v[0] += dpp<kDppRowRor8>(v[0]);
+    const int col = ((lane & 32) ? 16 : 0) + ((lane & 16) ? 8 : 0) + (b0 ? 4 : 0) + (b1 ? 2 : 0) + (b2 ? 1 : 0);
+    if (!b3) red[wave * 32 + col] = v[0];
+}
+
 // f32 sum of s[0..n) in index order by one thread (the order the reference
 // sums in).  The LDS reads are issued 32 at a time so the add chain, not the
 // read latency, sets the pace.  s is 16-byte aligned.

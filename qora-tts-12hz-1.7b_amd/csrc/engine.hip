@@ -217,7 +217,8 @@ template <int M, int NP, int C, int R>
 __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint32_t tb, Ctl &c, float *smem, int row) {
     constexpr int DW = q4_slice_dwords<C>();
     float *red = smem;                          // [NP][M][kEngWaves][C]
-    float *scr = red + NP * M * kEngWaves * C;  // [M][kEngWaves] block-sum partials
+    float *scr = red + NP * M * kEngWaves * C;  // [M][kEngWaves] per-wave sums of squares
+    float *sxr = scr + M * kEngWaves;           // [NP][M][kEngWaves] per-wave sums of scale * x
     const int tid = threadIdx.x;
     const int N = g.w.N, K = g.w.K;
     const int Nout = N / NP;
@@ -410,8 +411,8 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
             for (int d = 0; d < DW; d++) asm volatile("" : "+v"(wv[pp][i][d]));
         }
     // Each term is (scale * x) * nib - 8 * (scale * x): the offset is applied
-    // once per column from the running sum of scale * x, kept (like the
-    // products' operands) scaled by 2^24.
+    // once per column, after the reduction, from the block's sum of
+    // scale * x, kept (like the products' operands) scaled by 2^24.
     float sxsum[NP][M];
 #pragma unroll
     for (int pp = 0; pp < NP; pp++)
@@ -436,22 +437,23 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
             q4_mix_row<M, C>(wv[pp][i], sa, sb, acc[pp]);
         }
     }
-#pragma unroll
-    for (int pp = 0; pp < NP; pp++)
-#pragma unroll
-        for (int m = 0; m < M; m++)
-#pragma unroll
-            for (int j = 0; j < C; j++) acc[pp][m][j] = fmaf(-0x1p-21f, sxsum[pp][m], acc[pp][m][j]);
 
     stamp(c, 5);
-    // 4. block reduction (lane exchanges within each wave, then 4 waves
+    // 4. block reduction (lane exchanges within each wave, then the waves
     //    through LDS).  Thread (m, j) < M * C ends with column j of row m of
     //    every panel, so the split-K exchange and the epilogue stay in its
     //    registers.
 #pragma unroll
     for (int pp = 0; pp < NP; pp++)
 #pragma unroll
-        for (int m = 0; m < M; m++) dpp_reduce<C>(acc[pp][m], &red[(pp * M + m) * kEngWaves * C]);
+        for (int m = 0; m < M; m++) {
+            if constexpr (C == 32)
+                lane_reduce32(acc[pp][m], &red[(pp * M + m) * kEngWaves * C]);
+            else
+                dpp_reduce<C>(acc[pp][m], &red[(pp * M + m) * kEngWaves * C]);
+            const float w = wave_sum(sxsum[pp][m]);
+            if ((tid & 63) == 0) sxr[(pp * M + m) * kEngWaves + (tid >> 6)] = w;
+        }
     if (g.norm) {
 #pragma unroll
         for (int m = 0; m < M; m++) {
@@ -461,16 +463,16 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
     }
     __syncthreads();
     stamp(c, 6);
-    float inv[M];  // 1 / rms of each input row (rms_norm_f16, src/gemv.rs:406-417)
-#pragma unroll
-    for (int m = 0; m < M; m++)
-        inv[m] = g.norm ? 1.0f / sqrtf(waves_sum(&scr[kEngWaves * m], 1) / (float)K + 1e-6f) : 1.0f;
+    // 1 / rms of input row m (rms_norm_f16, src/gemv.rs:406-417), computed
+    // only by the lanes that use it
+    auto inv_of = [&](int m) { return 1.0f / sqrtf(waves_sum(&scr[kEngWaves * m], 1) / (float)K + 1e-6f); };
     if (g.norm_plain && tt == 0 && ch == 0 && row + M == g.M) {
         // the normed last row, for a later launch
+        const float iv = inv_of(M - 1);
 #pragma unroll
         for (int i = 0; i < R; i++) {
             const int k = k0 + tid + i * kEngThreads;
-            if (i < nit && k < k1) st_dev(&g.norm_plain[k], xv[i][M - 1] * inv[M - 1]);
+            if (i < nit && k < k1) st_dev(&g.norm_plain[k], xv[i][M - 1] * iv);
         }
     }
     if (tid < M * C) {
@@ -479,7 +481,8 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
         float y[NP];
 #pragma unroll
         for (int pp = 0; pp < NP; pp++) {
-            y[pp] = waves_sum(&red[(pp * M + m) * kEngWaves * C + j], C);
+            y[pp] = fmaf(-0x1p-21f, waves_sum(&sxr[(pp * M + m) * kEngWaves], 1),
+                         waves_sum(&red[(pp * M + m) * kEngWaves * C + j], C));
         }
         // 5. split-K: non-owners publish partials; the owner adds them in order.
         if (ch > 0 && NP == 1 && g.split_out) {
@@ -504,8 +507,9 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
             }
         }
         if (g.norm) {
+            const float iv = inv_of(m);
 #pragma unroll
-            for (int pp = 0; pp < NP; pp++) y[pp] *= inv[m];
+            for (int pp = 0; pp < NP; pp++) y[pp] *= iv;
         }
         // 6. epilogue
         if (NP == 2) {
