@@ -283,6 +283,34 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
     if (epi_lane && g.epi == EEPI_RESID) e_res = ld_dev_u64(g.resid_table ? g.resid_code : res_at);
     if (epi_lane && g.epi == EEPI_RESID && g.resid_parts == 2) e_res2 = ld_dev_u64(res_at + N);
 
+    // The epilogue's plan for this lane, read out of the descriptor now
+    // (while the loads fly) and held in vector registers: under SGPR
+    // pressure the compiler would otherwise re-read each field after the
+    // reduction, one dependent scalar-cache round trip per branch on the
+    // critical path.  Flags: 1 norm, 2 second part of a split_out output,
+    // 4 split-K partial, 8 owner waits for partials, 16 bias, 32 residual,
+    // 64 residual from the table, 128 two-part residual, 256 plain copy,
+    // 512 the normed input row is stored.
+    const int e_m = tid / C + row, e_col = col0 + (tid % C);
+    const bool e_second = ch > 0 && NP == 1 && g.split_out;
+    uint32_t e_flags = (g.norm ? 1u : 0u) | (e_second ? 2u : 0u) | (ch > 0 && !e_second ? 4u : 0u) |
+                       (ch == 0 && g.kc > 1 && !(NP == 1 && g.split_out) ? 8u : 0u) | (g.bias ? 16u : 0u) |
+                       (g.epi == EEPI_RESID ? 32u : 0u) | (g.resid_table ? 64u : 0u) |
+                       (g.resid_parts == 2 ? 128u : 0u) | (g.out_plain ? 256u : 0u) |
+                       (g.norm_plain && tt == 0 && ch == 0 && row + M == g.M ? 512u : 0u);
+    uint64_t e_dst = (uint64_t)(e_second ? g.out + (size_t)e_m * g.ld_out + N + e_col
+                                : ch > 0 ? g.part + ((size_t)(ch - 1) * g.M + e_m) * N + e_col
+                                         : g.out + (size_t)e_m * g.ld_out + e_col);
+    uint32_t e_tag = tb + (ch > 0 && !e_second ? g.part_tag : g.out_tag);
+    uint64_t e_part = (uint64_t)(g.part + (size_t)e_m * N + e_col);  // the owner's partials, stride M * N
+    uint32_t e_pstride = (uint32_t)(g.M * N), e_nparts = (uint32_t)(g.kc - 1), e_ptag = tb + g.part_tag;
+    uint64_t e_plain = (uint64_t)(g.out_plain + (size_t)e_m * g.ld_plain + e_col);
+    uint64_t e_nplain = (uint64_t)g.norm_plain;
+    uint32_t e_rtag = tb + g.resid_tag;
+    float e_K = (float)K;
+    asm volatile("" : "+v"(e_flags), "+v"(e_dst), "+v"(e_tag), "+v"(e_part), "+v"(e_pstride), "+v"(e_nparts));
+    asm volatile("" : "+v"(e_ptag), "+v"(e_plain), "+v"(e_nplain), "+v"(e_rtag), "+v"(e_K));
+
     stamp(c, 2);
     // 2. inputs of this thread's rows.
     stamp(c, 3);
@@ -385,12 +413,11 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
     // read again now; the load flies during the accumulation.
     float e_tab = 0.0f;  // the residual read from resid_table
     if (epi_lane && g.epi == EEPI_RESID && g.resid_table) {
-        const uint32_t code = (uint32_t)(e_res >> 32) == tb + g.resid_tag ? (uint32_t)e_res
-                                                                           : wait_tv_u32(g.resid_code, tb + g.resid_tag, c);
+        const uint32_t code = (uint32_t)(e_res >> 32) == e_rtag ? (uint32_t)e_res : wait_tv_u32(g.resid_code, e_rtag, c);
         if (code < (uint32_t)g.resid_table_rows) e_tab = glb(g.resid_table)[(size_t)code * g.ld_resid + col0 + (tid % C)];
     } else if (epi_lane && g.epi == EEPI_RESID) {
-        if ((uint32_t)(e_res >> 32) != tb + g.resid_tag) e_res = ld_dev_u64(res_at);
-        if (g.resid_parts == 2 && (uint32_t)(e_res2 >> 32) != tb + g.resid_tag) e_res2 = ld_dev_u64(res_at + N);
+        if ((uint32_t)(e_res >> 32) != e_rtag) e_res = ld_dev_u64(res_at);
+        if (g.resid_parts == 2 && (uint32_t)(e_res2 >> 32) != e_rtag) e_res2 = ld_dev_u64(res_at + N);
     }
     stamp(c, 4);
     // 3. accumulate the slice's columns per panel.
@@ -465,19 +492,20 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
     stamp(c, 6);
     // 1 / rms of input row m (rms_norm_f16, src/gemv.rs:406-417), computed
     // only by the lanes that use it
-    auto inv_of = [&](int m) { return 1.0f / sqrtf(waves_sum(&scr[kEngWaves * m], 1) / (float)K + 1e-6f); };
-    if (g.norm_plain && tt == 0 && ch == 0 && row + M == g.M) {
+    auto inv_of = [&](int m) { return 1.0f / sqrtf(waves_sum(&scr[kEngWaves * m], 1) / e_K + 1e-6f); };
+    const uint32_t fl = __builtin_amdgcn_readfirstlane(e_flags);  // uniform
+    if (fl & 512u) {
         // the normed last row, for a later launch
         const float iv = inv_of(M - 1);
+        float *np_row = reinterpret_cast<float *>(e_nplain);
 #pragma unroll
         for (int i = 0; i < R; i++) {
             const int k = k0 + tid + i * kEngThreads;
-            if (i < nit && k < k1) st_dev(&g.norm_plain[k], xv[i][M - 1] * iv);
+            if (i < nit && k < k1) st_dev(&np_row[k], xv[i][M - 1] * iv);
         }
     }
     if (tid < M * C) {
         const int m = tid / C, j = tid % C;
-        const int col = col0 + j;
         float y[NP];
 #pragma unroll
         for (int pp = 0; pp < NP; pp++) {
@@ -485,28 +513,28 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
                          waves_sum(&red[(pp * M + m) * kEngWaves * C + j], C));
         }
         // 5. split-K: non-owners publish partials; the owner adds them in order.
-        if (ch > 0 && NP == 1 && g.split_out) {
-            put_tv(&g.out[(size_t)(m + row) * g.ld_out + N + col], y[0], tb + g.out_tag);
+        tv_t *dst = reinterpret_cast<tv_t *>(e_dst);
+        if (fl & 2u) {  // the second part of a split_out output
+            put_tv(dst, y[0], e_tag);
             return -1;
         }
-        if (ch > 0) {
+        if (fl & 4u) {
 #pragma unroll
-            for (int pp = 0; pp < NP; pp++)
-                put_tv(&g.part[((size_t)(ch - 1) * g.M + m + row) * N + pp * Nout + col], y[pp], tb + g.part_tag);
+            for (int pp = 0; pp < NP; pp++) put_tv(dst + pp * Nout, y[pp], e_tag);
             return -1;
         }
-        if (g.kc > 1 && !(NP == 1 && g.split_out)) {
+        if (fl & 8u) {
 #pragma unroll
             for (int pp = 0; pp < NP; pp++) {
                 float pv4[4];
-                wait_strided<4>(&g.part[(size_t)(m + row) * N + pp * Nout + col], (size_t)g.M * N, g.kc - 1,
-                                tb + g.part_tag, pv4, c);
+                wait_strided<4>(reinterpret_cast<const tv_t *>(e_part) + pp * Nout, e_pstride, (int)e_nparts, e_ptag,
+                                pv4, c);
 #pragma unroll
                 for (int cc = 0; cc < 4; cc++)
-                    if (cc < g.kc - 1) y[pp] += pv4[cc];
+                    if (cc < (int)e_nparts) y[pp] += pv4[cc];
             }
         }
-        if (g.norm) {
+        if (fl & 1u) {
             const float iv = inv_of(m);
 #pragma unroll
             for (int pp = 0; pp < NP; pp++) y[pp] *= iv;
@@ -515,25 +543,24 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
         if (NP == 2) {
             // silu(g) * u, src/talker.rs:342-345
             const float gt = y[0], up = y[NP - 1];
-            put_tv(&g.out[(size_t)(m + row) * g.ld_out + col], (gt / (1.0f + expf(-gt))) * up, tb + g.out_tag);
+            put_tv(dst, (gt / (1.0f + expf(-gt))) * up, e_tag);
         } else {
             float v = y[0];
-            if (g.bias) v += e_bias;
-            if (g.epi == EEPI_RESID) {
+            if (fl & 16u) v += e_bias;
+            if (fl & 32u) {
                 float r;
-                if (g.resid_table) {
+                if (fl & 64u) {
                     r = e_tab;
                 } else {
-                    r = (uint32_t)(e_res >> 32) == tb + g.resid_tag ? __uint_as_float((uint32_t)e_res)
-                                                                    : wait_tv(res_at, tb + g.resid_tag, c);
-                    if (g.resid_parts == 2)
-                        r += (uint32_t)(e_res2 >> 32) == tb + g.resid_tag ? __uint_as_float((uint32_t)e_res2)
-                                                                          : wait_tv(res_at + N, tb + g.resid_tag, c);
+                    r = (uint32_t)(e_res >> 32) == e_rtag ? __uint_as_float((uint32_t)e_res) : wait_tv(res_at, e_rtag, c);
+                    if (fl & 128u)
+                        r += (uint32_t)(e_res2 >> 32) == e_rtag ? __uint_as_float((uint32_t)e_res2)
+                                                                : wait_tv(res_at + N, e_rtag, c);
                 }
                 v = r + v;
             }
-            put_tv(&g.out[(size_t)(m + row) * g.ld_out + col], v, tb + g.out_tag);
-            if (g.out_plain) st_dev(&g.out_plain[(size_t)(m + row) * g.ld_plain + col], v);
+            put_tv(dst, v, e_tag);
+            if (fl & 256u) st_dev(reinterpret_cast<float *>(e_plain), v);
         }
     }
     if (ch > 0) return -1;
@@ -1012,7 +1039,8 @@ __device__ __forceinline__ int eng_attn_lean(const KCONST EngAttn &a, int task, 
 #pragma unroll
     for (int t = 0; t < NP; t++) part[t] = qn0 * kr[t].x + qn1 * kr[t].y;
     float *red = smem;  // [M * G waves][NP]
-    dpp_reduce<NP>(part, red);
+    static_assert(NP == 32, "the lean attention reduces 32 positions");
+    lane_reduce32(part, red);
     // 5. softmax across lanes, position t on lane t
     const float sc = lane < nvis ? red[wave * NP + lane] * a.scale : -INFINITY;
     const float mx = wave_max(sc);
