@@ -952,6 +952,14 @@ TvRef add_layer(EngProgram &P, const Stack &st, int l, qtts_kv *kv, int M, const
     for (int m = 0; m < M; m++) q.in[m] = tin ? in_argtab(*tin) : in_tv(x, m);
     const bool qtab = tin && tin->qkv_table;  // the q|k|v row by code: no QKV step
     const TvRef qkv = qtab ? TvRef{} : add_gemv(P, L.qkv, q);
+    if (!qtab && M > 1 && P.rot_record && !P.rot_plan) {
+        // The predictor's first pass (two rows) records the rotations the
+        // one-row passes replay: the attention goes right after the blocks
+        // of the one-row QKV step, so in those passes its blocks have no
+        // task in that step and wait for its outputs from the start.
+        const EngOp &qop = P.ops.back();
+        P.rot_next = (qop.rot + qop.ntasks / M) % P.grid;
+    }
     const TvRef att = add_attention(P, st, l, kv, M, qkv, from_state, pos_const, len_const, nsplit, qtab ? tin : nullptr);
     GemvSpec o;
     o.M = M;
