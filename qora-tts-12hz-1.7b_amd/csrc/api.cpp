@@ -1176,13 +1176,13 @@ qtts_status eng_status_check(qtts_ctx *c, const char *what) {
     return QTTS_OK;
 }
 
-// Talker attention splits of ~48 positions of the cache capacity: a split's
+// Talker attention splits of ~64 positions of the cache capacity: a split's
 // K/V rows (1 KB per position) stream into one CU at ~25-30 GB/s, so short
 // splits keep the attention step near its hand-off latency at long contexts,
-// while fewer splits shorten the combine (48 measured ahead of 32 and 64 on
-// a 592-row cache).
+// while fewer splits shorten the combine (with 512-thread blocks, 64 measured
+// ahead of 48 and 96 on the 500-code loop's caches).
 int eng_talker_nsplit(int cap) {
-    int n = (cap + 47) / 48;
+    int n = (cap + 63) / 64;
     if (n < 1) n = 1;
     if (n > kEngMaxSplit) n = kEngMaxSplit;
     return n;
@@ -1296,6 +1296,27 @@ qtts_status build_predictor_passes(EngProgram &P, qtts_predictor *p, qtts_kv *kv
     hd.norm = true;
     hd.gamma = st.final_g;
     hd.in[0] = in_tv(x, 1);
+    if (p->tab_state == 1 && P.ops.size() > first + 2 && P.ops[first + 2].kind == EOP_ATTN) {
+        // Passes 2-15 run the head right before the next pass's layer-0
+        // attention: its blocks go where the one-row passes leave them free
+        // of that attention's blocks and of the last down step's.
+        const EngOp &dn = P.ops.back(), &a0 = P.ops[first + 2];
+        const int nd = dn.ntasks / (dn.kind == EOP_GEMV && dn.gemv.M > 1 ? dn.gemv.M : 1);
+        const int nh = p->heads[0].N / 32;
+        auto in_range = [&](int b, int r, int n) { return ((b - r) % P.grid + P.grid) % P.grid < n; };
+        for (int k = 0; k < P.grid; k++) {
+            const int r = (dn.rot + nd + k) % P.grid;
+            bool ok = nh + nd + a0.ntasks <= P.grid;
+            for (int i = 0; ok && i < nh; i++) {
+                const int b = (r + i) % P.grid;
+                ok = !in_range(b, dn.rot, nd) && !in_range(b, a0.rot, a0.ntasks);
+            }
+            if (ok) {
+                P.rot_next = r;
+                break;
+            }
+        }
+    }
     TvRef lg = add_gemv(P, p->heads[0], hd);
     const bool tab = p->tab_state == 1;
     // With the q|k|v table the later passes start at layer 0's attention,
