@@ -797,9 +797,17 @@ TvRef add_gemv(EngProgram &P, const DevQ4 &w, const GemvSpec &sp) {
     op.kind = EOP_GEMV;
     EngGemv &g = op.gemv;
     const int Nout = sp.epi == EEPI_SWIGLU ? w.N / 2 : w.N;
-    // Tasks of whole 32-column panels (the kernel's GEMV slice width).
+    // Tasks of whole 32-column panels (the kernel's GEMV slice width), or of
+    // half panels for a SwiGLU step whose half-panel tasks fit the grid.
     const int NP = sp.epi == EEPI_SWIGLU ? 2 : 1;
-    const int C = 32;
+    const char *half_env = std::getenv("QTTS_ENGINE_SWIGLU_COLS");
+    auto half_fits = [&](int rows) {
+        return NP == 2 && !(half_env && std::atoi(half_env) == 32) &&
+               (Nout / 16) * ((w.K + kEngThreads * eng_rows_per_thread(16, 2) - 1) /
+                              (kEngThreads * eng_rows_per_thread(16, 2))) * rows <= P.grid;
+    };
+    const bool half = half_fits(sp.M);
+    const int C = half ? 16 : 32;
     const int rpt = eng_rows_per_thread(C, NP);
     if (Nout % 32 != 0 || (sp.norm && w.K > kEngThreads * kEngNormRows)) P.err = "engine GEMV shape not supported";
     // One K chunk where the rows fit one task: a split-K owner waits a
@@ -860,6 +868,13 @@ TvRef add_gemv(EngProgram &P, const DevQ4 &w, const GemvSpec &sp) {
     }
     op.ntasks = (Nout / C) * kc * sp.M;  // one-row tasks for every row
     P.push(op);
+    if (sp.M > 1 && P.rot_record && !P.rot_plan) {
+        // The predictor's first pass (two rows) records the rotations its
+        // one-row passes replay: the next op goes right after the blocks
+        // this op has in those passes, so consecutive ops there run on
+        // disjoint blocks and wait for their inputs from the start.
+        P.rot_next = (op.rot + (Nout / (half_fits(1) ? 16 : 32)) * kc) % P.grid;
+    }
     return TvRef{g.out, g.out_tag, g.ld_out, split ? 2 : 1};
 }
 
@@ -952,14 +967,6 @@ TvRef add_layer(EngProgram &P, const Stack &st, int l, qtts_kv *kv, int M, const
     for (int m = 0; m < M; m++) q.in[m] = tin ? in_argtab(*tin) : in_tv(x, m);
     const bool qtab = tin && tin->qkv_table;  // the q|k|v row by code: no QKV step
     const TvRef qkv = qtab ? TvRef{} : add_gemv(P, L.qkv, q);
-    if (!qtab && M > 1 && P.rot_record && !P.rot_plan) {
-        // The predictor's first pass (two rows) records the rotations the
-        // one-row passes replay: the attention goes right after the blocks
-        // of the one-row QKV step, so in those passes its blocks have no
-        // task in that step and wait for its outputs from the start.
-        const EngOp &qop = P.ops.back();
-        P.rot_next = (qop.rot + qop.ntasks / M) % P.grid;
-    }
     const TvRef att = add_attention(P, st, l, kv, M, qkv, from_state, pos_const, len_const, nsplit, qtab ? tin : nullptr);
     GemvSpec o;
     o.M = M;

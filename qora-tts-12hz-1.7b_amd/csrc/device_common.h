@@ -305,6 +305,34 @@ __device__ __forceinline__ void lane_reduce32(const float (&acc)[32], float *red
     if (!b3) red[wave * 32 + col] = v[0];
 }
 
+// The same for acc[16] (half-panel tasks): bits 5 and 4 by lane swaps, bits
+// 0 and 1 by DPP halving, bits 2 and 3 as plain adds, so lanes that differ in
+// bits 2 and 3 hold the same column sum; lanes with both clear store it to
+// red[wave * 16 + col].
+__device__ __forceinline__ void lane_reduce16(const float (&acc)[16], float *red) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    float v[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) v[j] = acc[j];
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v[j]), __float_as_uint(v[j + 8]), false, false);
+        v[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v[j]), __float_as_uint(v[j + 4]), false, false);
+        v[j] = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+    }
+    const bool b0 = lane & 1, b1 = lane & 2, b2 = lane & 4;
+    dpp_stage<4, 0>(v, b0);
+    dpp_stage<2, 1>(v, b1);
+    v[0] += dpp_xchg<2>(b2, v[0]);
+    v[0] += dpp<kDppRowRor8>(v[0]);
+    const int col = ((lane & 32) ? 8 : 0) + ((lane & 16) ? 4 : 0) + (b0 ? 2 : 0) + (b1 ? 1 : 0);
+    if ((lane & 12) == 0) red[wave * 16 + col] = v[0];
+}
+
 // f32 sum of s[0..n) in index order by one thread (the order the reference
 // sums in).  The LDS reads are issued 32 at a time so the add chain, not the
 // read latency, sets the pace.  s is 16-byte aligned.

@@ -33,7 +33,7 @@ constexpr int kEngWaves = kEngThreads / 64;
 // panels (the K chunk is at most kEngThreads times this): a task's weights
 // stay in registers from issue to use, cols / 8 dwords per row (one for 4
 // columns).
-constexpr int eng_rows_per_thread(int cols, int np) { return np == 2 || cols == 32 ? 4 : cols == 4 ? 8 : 12; }
+constexpr int eng_rows_per_thread(int cols, int np) { return np == 2 || cols >= 16 ? 4 : cols == 4 ? 8 : 12; }
 constexpr int kEngNormRows = 4;  // an RMSNorm input row has <= kEngThreads * 4 values
 constexpr int kEngMaxM = 2;    // rows per GEMV (the predictor's 2-token prefill)
 constexpr uint32_t kTagStride = 8192;  // tags reserved per code

@@ -476,6 +476,8 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
         for (int m = 0; m < M; m++) {
             if constexpr (C == 32)
                 lane_reduce32(acc[pp][m], &red[(pp * M + m) * kEngWaves * C]);
+            else if constexpr (C == 16)
+                lane_reduce16(acc[pp][m], &red[(pp * M + m) * kEngWaves * C]);
             else
                 dpp_reduce<C>(acc[pp][m], &red[(pp * M + m) * kEngWaves * C]);
             const float w = wave_sum(sxsum[pp][m]);
@@ -573,7 +575,11 @@ __device__ __forceinline__ int eng_gemv_cols(const KCONST EngGemv &g, int task, 
     // Whole 32-column panels: narrower slices spread an op over more blocks
     // but leave fewer blocks idle to run ahead into the next op (issuing its
     // weight loads early), which costs more than the shorter accumulation
-    // saves on this loop.
+    // saves on this loop -- except for the SwiGLU step when its half-panel
+    // tasks still fit the grid (the host's choice): that task is the
+    // heaviest (two panels and two reductions).
+    if constexpr (NP == 2)
+        if (g.cols == 16) return eng_gemv<M, 2, 16, eng_rows_per_thread(16, 2)>(g, task, tb, c, smem, row);
     return eng_gemv<M, NP, 32, eng_rows_per_thread(32, NP)>(g, task, tb, c, smem, row);
 }
 
@@ -1560,7 +1566,7 @@ __global__ __launch_bounds__(kEngThreads) void k_engine(EngArgs A) {
                         const KCONST EngGemv &g = op.gemv;
                         int row = 0, tt = t;
                         if (g.M > 1) {
-                            const int per = g.w.N / (g.epi == EEPI_SWIGLU ? 64 : 32);  // tasks per K chunk
+                            const int per = g.w.N / (g.epi == EEPI_SWIGLU ? 2 * g.cols : g.cols);  // tasks per K chunk
                             const int non = per * (g.kc - 1);
                             if (t < non * g.M) {
                                 row = t / non;
