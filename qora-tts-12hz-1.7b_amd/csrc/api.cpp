@@ -1157,7 +1157,9 @@ qtts_status eng_launch(qtts_ctx *c, EngProgram &P, int st_in, uint32_t *codes, i
         HIP_TRY(c, hipMemsetAsync(c->eng_trace, 0, trace_n * sizeof(uint64_t), c->stream));
         a.trace = c->eng_trace;
     }
-    hipError_t e = launch_engine(c->stream, a, P.grid);
+    const char *launch_env = std::getenv("QTTS_ENGINE_LAUNCH");
+    const bool coop = !(launch_env && std::strcmp(launch_env, "plain") == 0);
+    hipError_t e = launch_engine(c->stream, a, P.grid, coop);
     if (e != hipSuccess) return fail(c, QTTS_EDEVICE, std::string("engine launch: ") + hipGetErrorString(e));
     if (a.trace) {
         std::vector<uint64_t> h(trace_n);

@@ -210,7 +210,11 @@ struct EngArgs {
 
 constexpr int kTraceSlots = 10;
 
-hipError_t launch_engine(hipStream_t st, const EngArgs &a, int grid);
+// cooperative: hipLaunchCooperativeKernel (the default, which guarantees
+// that the whole grid is resident); otherwise an ordinary launch of the same
+// grid (QTTS_ENGINE_LAUNCH=plain, for profiler runs: a process that made a
+// cooperative launch holds the runtime's cooperative queue until exit).
+hipError_t launch_engine(hipStream_t st, const EngArgs &a, int grid, bool cooperative);
 int engine_max_grid();
 
 }  // namespace qtts

@@ -1633,10 +1633,16 @@ __global__ __launch_bounds__(kEngThreads) void k_engine(EngArgs A) {
     }
 }
 
-hipError_t launch_engine(hipStream_t st, const EngArgs &a, int grid) {
+hipError_t launch_engine(hipStream_t st, const EngArgs &a, int grid, bool cooperative) {
     EngArgs args = a;
     void *kargs[] = {&args};
-    return hipLaunchCooperativeKernel((const void *)k_engine, dim3((unsigned)grid), dim3(kEngThreads), kargs, 0, st);
+    if (cooperative)
+        return hipLaunchCooperativeKernel((const void *)k_engine, dim3((unsigned)grid), dim3(kEngThreads), kargs, 0, st);
+    // The same grid through an ordinary launch: on an otherwise idle device
+    // every block of a grid of (CUs x resident blocks per CU) is resident at
+    // once; if one were not, the waits on its outputs time out (EDEVICE) and
+    // the grid drains.
+    return hipLaunchKernel((const void *)k_engine, dim3((unsigned)grid), dim3(kEngThreads), kargs, 0, st);
 }
 
 int engine_max_grid() {
