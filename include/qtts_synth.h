@@ -45,14 +45,21 @@ float qtts_f16_to_f32(uint16_t h);
  * with round half away from zero, nibble = q + 8. */
 void qtts_quantize_f32_to_q4(const float *data, int32_t k, int32_t n, uint8_t *packed, uint16_t *scales);
 
-/* Reads every 16-byte word of a device buffer once, in one launch of
- * 256-thread blocks with one word per thread, on `stream` (a hipStream_t; null
- * for the default stream): the single-launch time of streaming `bytes` from
- * HBM with nothing else to do, the floor the Q4 GEMV timings are compared
- * against.  bytes must be a positive multiple of 16 and d_buf 16-byte aligned.
- * Returns 0, or -1 for bad arguments or a failed launch.  No counterpart in the
- * reference (a measurement aid, like the synthetic weights above). */
+/* Reads every 16-byte word of a device buffer once, in one launch, on
+ * `stream` (a hipStream_t; null for the default stream): the single-launch
+ * time of streaming `bytes` from HBM with nothing else to do, the floor the Q4
+ * GEMV timings are compared against.  A grid of a few blocks per CU walks the
+ * buffer with several 16-byte loads in flight per thread (the fastest shape
+ * measured).  bytes must be a positive multiple of 16 and d_buf 16-byte
+ * aligned.  Returns 0, or -1 for bad arguments or a failed launch.  No
+ * counterpart in the reference (a measurement aid, like the synthetic weights
+ * above). */
 int32_t qtts_stream_read_device(const void *d_buf, uint64_t bytes, void *stream);
+
+/* The same with the launch shape given: `blocks` 256-thread blocks, each
+ * thread keeping `unroll` (1, 2, 4 or 8) loads in flight per grid-wide
+ * stride; blocks == 0 launches one block per 256 words, one word per thread. */
+int32_t qtts_stream_read_device_ex(const void *d_buf, uint64_t bytes, int32_t blocks, int32_t unroll, void *stream);
 
 #ifdef __cplusplus
 }

@@ -12,6 +12,8 @@
 #include <hip/hip_runtime.h>
 
 #include <cfloat>
+#include <cstdio>
+#include <cstdlib>
 #include <mutex>
 #include <type_traits>
 #include <cmath>
@@ -353,18 +355,21 @@ __global__ __launch_bounds__(kGemvThreads) void k_gemv(GemvParams P) {
 
 // The plain single-row GEMV (gemv_q4, src/gemv.rs:263-309): one block of NT
 // threads per C-column slice of a 32-column panel, over its whole K (K <= NT *
-// RPT; 256 threads up to 2048 rows, 1024 threads up to 8192).  With C < 32
-// the S = 32 / C slices of a panel run on blocks 8 apart -- one XCD, as blocks
-// are dealt to the 8 XCDs round-robin -- so each panel row comes from HBM once
-// into that XCD's L2 (the host uses C < 32 only when the panels are a multiple
-// of 8).  The input rows go first, then the scales, then the weight rows one
-// by one (scheduling barriers keep that issue order), so each row's FMAs wait
-// for that row alone while the later rows are still in flight; the column
-// sums are finished in LDS and stored directly.  Same arithmetic as k_gemv.
+// RPT).  With C < 32 the S = 32 / C slices of a panel run on blocks 8 apart --
+// one XCD, as blocks are dealt to the 8 XCDs round-robin -- so each panel row
+// comes from HBM once into that XCD's L2 (the host uses C < 32 only when the
+// panels are a multiple of 8).  The input rows go first, then the scales, then
+// the weight rows one by one (scheduling barriers keep that issue order), so
+// each row's FMAs wait for that row alone while the later rows are still in
+// flight.  The column sums are reduced across each wave's lanes by lane swaps
+// (lane_reduce32 / lane_reduce16), then across the waves in LDS, where the
+// -8 offset is applied once per column from the block's sum of scale * x.
+// Same products as k_gemv.
 template <int RPT, int NT, int C>
 __global__ __launch_bounds__(NT) void k_gemv_plain(DevQ4 w, const float *x, float *y, const float *bias) {
     constexpr int NW = NT / 64, S = 32 / C, DW = q4_slice_dwords<C>();
     __shared__ float red[NW * C];
+    __shared__ float sxr[NW];
     const int tid = threadIdx.x, K = w.K;
     const int b = blockIdx.x;
     const int p = S == 1 ? b : (b / (8 * S)) * 8 + (b % 8);  // panel
@@ -403,34 +408,62 @@ __global__ __launch_bounds__(NT) void k_gemv_plain(DevQ4 w, const float *x, floa
         sxsum += sa[0];
         q4_mix_row<1, C>(wv[i], sa, sb, acc);
     }
-#pragma unroll
-    for (int j = 0; j < C; j++) acc[0][j] = fmaf(-0x1p-21f, sxsum, acc[0][j]);
-    dpp_reduce<C>(acc[0], red);
+    if constexpr (C == 32)
+        lane_reduce32(acc[0], red);
+    else if constexpr (C == 16)
+        lane_reduce16(acc[0], red);
+    else
+        dpp_reduce<C>(acc[0], red);
+    const float sw = wave_sum(sxsum);
+    if ((tid & 63) == 0) sxr[tid >> 6] = sw;
     __syncthreads();
     if (tid < C) {
-        float v;
-        if constexpr (NW == 4) {
-            v = (red[tid] + red[C + tid]) + (red[2 * C + tid] + red[3 * C + tid]);
-        } else {
-            // the waves' sums pairwise, in wave order
-            float t[NW];
+        // the waves' sums pairwise, in wave order
+        float t[NW], u[NW];
 #pragma unroll
-            for (int i = 0; i < NW; i++) t[i] = red[i * C + tid];
-#pragma unroll
-            for (int h = 1; h < NW; h *= 2)
-#pragma unroll
-                for (int i = 0; i + h < NW; i += 2 * h) t[i] += t[i + h];
-            v = t[0];
+        for (int i = 0; i < NW; i++) {
+            t[i] = red[i * C + tid];
+            u[i] = sxr[i];
         }
+#pragma unroll
+        for (int h = 1; h < NW; h *= 2)
+#pragma unroll
+            for (int i = 0; i + h < NW; i += 2 * h) {
+                t[i] += t[i + h];
+                u[i] += u[i + h];
+            }
+        float v = fmaf(-0x1p-21f, u[0], t[0]);
         const int col = p * 32 + sl * C + tid;
         if (bias) v += bias[col];
         y[col] = v;
     }
 }
 
-// qtts_stream_read_device: every 16-byte word of a buffer read once (one
-// per thread) and XORed; an empty asm statement takes the result, so the
-// compiler keeps the loads (nothing is stored).
+// Best-effort streaming read (qtts_stream_read_device_ex): a grid of
+// `blocks` 256-thread blocks walks the buffer in grid-wide strides, each
+// thread keeping U 16-byte loads in flight per step; the words are XORed and
+// an empty asm statement takes the result, so the compiler keeps the loads
+// (nothing is stored).
+template <int U>
+__global__ __launch_bounds__(256) void k_stream_read_loop(const u32x4 *p, uint64_t n16) {
+    const uint64_t stride = (uint64_t)gridDim.x * 256;
+    uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
+    unsigned x = 0;
+    for (; i + (U - 1) * stride < n16; i += U * stride) {
+        u32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) v[u] = __builtin_nontemporal_load(glb(p + i + u * stride));
+#pragma unroll
+        for (int u = 0; u < U; u++) x ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    for (; i < n16; i += stride) {
+        const u32x4 v = __builtin_nontemporal_load(glb(p + i));
+        x ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    asm volatile("" ::"v"(x));
+}
+
+// The same with one word per thread and a block per 256 words.
 __global__ __launch_bounds__(256) void k_stream_read(const u32x4 *p, uint64_t n16) {
     const uint64_t i = (uint64_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n16) return;
@@ -439,13 +472,33 @@ __global__ __launch_bounds__(256) void k_stream_read(const u32x4 *p, uint64_t n1
     asm volatile("" ::"v"(x));
 }
 
-extern "C" int32_t qtts_stream_read_device(const void *d_buf, uint64_t bytes, void *stream) {
-    if (!d_buf || bytes == 0 || bytes % 16 != 0 || ((uintptr_t)d_buf & 15) || bytes / 16 > (uint64_t)256 * 0x7FFFFFFF)
+extern "C" int32_t qtts_stream_read_device_ex(const void *d_buf, uint64_t bytes, int32_t blocks, int32_t unroll,
+                                              void *stream) {
+    if (!d_buf || bytes == 0 || bytes % 16 != 0 || ((uintptr_t)d_buf & 15) || bytes / 16 > (uint64_t)256 * 0x7FFFFFFF ||
+        blocks < 0 || (blocks > 0 && unroll != 1 && unroll != 2 && unroll != 4 && unroll != 8))
         return -1;
     const uint64_t n16 = bytes / 16;
-    hipLaunchKernelGGL(k_stream_read, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
-                       static_cast<const u32x4 *>(d_buf), n16);
+    const hipStream_t st = (hipStream_t)stream;
+    const auto *buf = static_cast<const u32x4 *>(d_buf);
+    if (blocks == 0) {
+        hipLaunchKernelGGL(k_stream_read, dim3((unsigned)((n16 + 255) / 256)), dim3(256), 0, st, buf, n16);
+    } else {
+        const dim3 g((unsigned)blocks), t(256);
+        switch (unroll) {
+            case 1: hipLaunchKernelGGL(k_stream_read_loop<1>, g, t, 0, st, buf, n16); break;
+            case 2: hipLaunchKernelGGL(k_stream_read_loop<2>, g, t, 0, st, buf, n16); break;
+            case 4: hipLaunchKernelGGL(k_stream_read_loop<4>, g, t, 0, st, buf, n16); break;
+            default: hipLaunchKernelGGL(k_stream_read_loop<8>, g, t, 0, st, buf, n16); break;
+        }
+    }
     return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// The read floor: one word per thread and a block per 256 words measured as
+// fast as every persistent shape (1-8 blocks per CU, 1-8 loads in flight per
+// thread) in kernel-trace averages for 4.7, 7.1 and 14.2 MB.
+extern "C" int32_t qtts_stream_read_device(const void *d_buf, uint64_t bytes, void *stream) {
+    return qtts_stream_read_device_ex(d_buf, bytes, 0, 1, stream);
 }
 
 // Scratch of the allocation-free GEMV entry point: split-K partials
@@ -505,51 +558,77 @@ static void launch_gemv_m(hipStream_t st, const GemvParams &p) {
     }
 }
 
-void launch_gemv(hipStream_t st, const GemvParams &p) {
-    if (p.M == 1 && p.kc == 1 && p.prologue == PRO_PLAIN && p.epilogue == EPI_STORE && p.fin == FIN_NONE &&
-        !p.d_done) {
-        // half-panel slices where the panels come in multiples of 8 (one
-        // XCD per panel's slices): twice the blocks, half the accumulation each
-        constexpr int T = kGemvThreads;
-        const bool half = (p.w.N / 32) % 8 == 0;
-        const dim3 grid((unsigned)(p.w.N / 32 * (half ? 2 : 1)));
-        if (half) {
-            switch (p.rpt) {
-                case 8: hipLaunchKernelGGL((k_gemv_plain<8, T, 16>), grid, dim3(T), 0, st, p.w, p.x, p.y, p.bias); return;
-                case 4: hipLaunchKernelGGL((k_gemv_plain<4, T, 16>), grid, dim3(T), 0, st, p.w, p.x, p.y, p.bias); return;
-                case 2: hipLaunchKernelGGL((k_gemv_plain<2, T, 16>), grid, dim3(T), 0, st, p.w, p.x, p.y, p.bias); return;
-                default: hipLaunchKernelGGL((k_gemv_plain<1, T, 16>), grid, dim3(T), 0, st, p.w, p.x, p.y, p.bias); return;
-            }
-        }
-        switch (p.rpt) {
-            case 8: hipLaunchKernelGGL((k_gemv_plain<8, T, 32>), grid, dim3(T), 0, st, p.w, p.x, p.y, p.bias); return;
-            case 4: hipLaunchKernelGGL((k_gemv_plain<4, T, 32>), grid, dim3(T), 0, st, p.w, p.x, p.y, p.bias); return;
-            case 2: hipLaunchKernelGGL((k_gemv_plain<2, T, 32>), grid, dim3(T), 0, st, p.w, p.x, p.y, p.bias); return;
-            default: hipLaunchKernelGGL((k_gemv_plain<1, T, 32>), grid, dim3(T), 0, st, p.w, p.x, p.y, p.bias); return;
+template <int NT, int C>
+static void launch_plain_nc(hipStream_t st, const GemvParams &p, int rpt) {
+    const dim3 grid((unsigned)(p.w.N / C)), t(NT);
+    switch (rpt) {
+        case 1: hipLaunchKernelGGL((k_gemv_plain<1, NT, C>), grid, t, 0, st, p.w, p.x, p.y, p.bias); return;
+        case 2: hipLaunchKernelGGL((k_gemv_plain<2, NT, C>), grid, t, 0, st, p.w, p.x, p.y, p.bias); return;
+        case 4: hipLaunchKernelGGL((k_gemv_plain<4, NT, C>), grid, t, 0, st, p.w, p.x, p.y, p.bias); return;
+        case 6: hipLaunchKernelGGL((k_gemv_plain<6, NT, C>), grid, t, 0, st, p.w, p.x, p.y, p.bias); return;
+        default: hipLaunchKernelGGL((k_gemv_plain<8, NT, C>), grid, t, 0, st, p.w, p.x, p.y, p.bias); return;
+    }
+}
+
+// Block size and slice width of the plain GEMV for a K x N shape, from a
+// kernel-trace sweep of (256, 512, 1024 threads) x (32-, 16-, 8-column
+// slices) at the config-1 shapes: 256 threads up to K = 2048 (1024 above),
+// and 16-column slices when their blocks fill the CUs evenly (or number no
+// more than the CUs), else whole panels: 384 half-panel blocks of 2048 ->
+// 6144 leave half the CUs with twice the work (4.54 us against 4.39 for 192
+// whole panels).  The slices of a panel need the panels in multiples of 8.
+// QTTS_GEMV_PLAIN="threads,cols" overrides the choice (a measurement aid).
+static int device_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] <= 0) {
+        int n = 0;
+        cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+    }
+    return cus[dev];
+}
+
+static void plain_plan(int K, int N, int *nt, int *c) {
+    const bool slices = (N / 32) % 8 == 0;
+    const int cus = device_cus(), b16 = N / 16;
+    *nt = K <= 2048 ? 256 : 1024;
+    *c = slices && (b16 <= cus || b16 % cus == 0) ? 16 : 32;
+    static const char *env = std::getenv("QTTS_GEMV_PLAIN");
+    if (env) {
+        int a = 0, b = 0;
+        if (std::sscanf(env, "%d,%d", &a, &b) == 2 && (a == 256 || a == 512 || a == 1024) &&
+            (b == 32 || ((b == 16 || b == 8) && slices)) && K <= 8 * a) {
+            *nt = a;
+            *c = b;
         }
     }
-    if (p.M == 1 && p.kc > 1 && p.w.K <= 8 * kGemvWideThreads && p.prologue == PRO_PLAIN &&
-        p.epilogue == EPI_STORE && p.fin == FIN_NONE && !p.d_done) {
-        // K > 2048: a 1024-thread block per panel instead of K chunks summed
-        // through memory (one CU per panel, 16 waves hiding the loads)
-        constexpr int T = kGemvWideThreads;
-        const int r = (p.w.K + T - 1) / T;
-        const bool half = (p.w.N / 32) % 8 == 0;
-        const dim3 grid((unsigned)(p.w.N / 32 * (half ? 2 : 1)));
-        if (half) {
-            if (r <= 4)
-                hipLaunchKernelGGL((k_gemv_plain<4, T, 16>), grid, dim3(T), 0, st, p.w, p.x, p.y, p.bias);
-            else if (r <= 6)
-                hipLaunchKernelGGL((k_gemv_plain<6, T, 16>), grid, dim3(T), 0, st, p.w, p.x, p.y, p.bias);
-            else
-                hipLaunchKernelGGL((k_gemv_plain<8, T, 16>), grid, dim3(T), 0, st, p.w, p.x, p.y, p.bias);
-        } else if (r <= 4) {
-            hipLaunchKernelGGL((k_gemv_plain<4, T, 32>), grid, dim3(T), 0, st, p.w, p.x, p.y, p.bias);
-        } else if (r <= 6) {
-            hipLaunchKernelGGL((k_gemv_plain<6, T, 32>), grid, dim3(T), 0, st, p.w, p.x, p.y, p.bias);
-        } else {
-            hipLaunchKernelGGL((k_gemv_plain<8, T, 32>), grid, dim3(T), 0, st, p.w, p.x, p.y, p.bias);
-        }
+}
+
+static void launch_plain(hipStream_t st, const GemvParams &p) {
+    int nt = 256, c = 32;
+    plain_plan(p.w.K, p.w.N, &nt, &c);
+    int r = (p.w.K + nt - 1) / nt;
+    r = r <= 1 ? 1 : r <= 2 ? 2 : r <= 4 ? 4 : r <= 6 ? 6 : 8;
+    switch (nt * 100 + c) {
+        case 25632: launch_plain_nc<256, 32>(st, p, r); return;
+        case 25616: launch_plain_nc<256, 16>(st, p, r); return;
+        case 25608: launch_plain_nc<256, 8>(st, p, r); return;
+        case 51232: launch_plain_nc<512, 32>(st, p, r); return;
+        case 51216: launch_plain_nc<512, 16>(st, p, r); return;
+        case 51208: launch_plain_nc<512, 8>(st, p, r); return;
+        case 102432: launch_plain_nc<1024, 32>(st, p, r); return;
+        case 102416: launch_plain_nc<1024, 16>(st, p, r); return;
+        default: launch_plain_nc<1024, 8>(st, p, r); return;
+    }
+}
+
+void launch_gemv(hipStream_t st, const GemvParams &p) {
+    // One row, a plain input and a store, K <= 8192: one block per panel
+    // slice over the whole K (no partial sums through memory).
+    if (p.M == 1 && p.w.K <= 8 * kGemvWideThreads && p.prologue == PRO_PLAIN && p.epilogue == EPI_STORE &&
+        p.fin == FIN_NONE && !p.d_done && (p.kc == 1 || p.w.K > 8 * kGemvThreads)) {
+        launch_plain(st, p);
         return;
     }
     switch (p.M) {

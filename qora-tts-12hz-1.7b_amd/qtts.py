@@ -272,6 +272,7 @@ def load_library(path: str = LIB_PATH):
         "qtts_f32_to_f16": ([C.c_float], C.c_uint16),
         "qtts_f16_to_f32": ([C.c_uint16], C.c_float),
         "qtts_stream_read_device": ([vp, u64, vp], i32),
+        "qtts_stream_read_device_ex": ([vp, u64, i32, i32, vp], i32),
         "qtts_quantize_f32_to_q4": ([vp, i32, i32, vp, vp], None),
         "qtts_generate_codes_batch": (
             [vp, vp, i32, C.POINTER(vp), f32p, f32p, vp, f32p, i32, f32p, C.POINTER(LoopParams), vp, vp, vp], i32),
@@ -311,7 +312,7 @@ def exported_symbols() -> List[str]:
         "qtts_get_acoustic_embeddings_sum", "qtts_sample_token", "qtts_sample_top_k", "qtts_predict_codes",
         "qtts_forward_talker_decode", "qtts_generate_codes", "qtts_synth_u64",
         "qtts_synth_q4", "qtts_synth_normal_f32", "qtts_synth_normal_f16", "qtts_f32_to_f16", "qtts_f16_to_f32",
-        "qtts_stream_read_device",
+        "qtts_stream_read_device", "qtts_stream_read_device_ex",
         "qtts_quantize_f32_to_q4", "qtts_generate_codes_batch", "qtts_model_file_open", "qtts_model_file_error", "qtts_model_file_close",
         "qtts_model_file_talker", "qtts_model_file_predictor", "qtts_model_file_text", "qtts_model_file_info",
         "qtts_model_file_decoder", "qtts_decoder_upload", "qtts_decoder_free", "qtts_decoder_num_samples",

@@ -46,6 +46,9 @@ def test_null_arguments_are_rejected():
     assert lib.qtts_stream_read_device(None, 16, None) == -1
     assert lib.qtts_stream_read_device(C.c_void_p(4096), 24, None) == -1
     assert lib.qtts_stream_read_device(C.c_void_p(4100), 32, None) == -1
+    assert lib.qtts_stream_read_device_ex(None, 16, 0, 1, None) == -1
+    assert lib.qtts_stream_read_device_ex(C.c_void_p(4096), 32, 8, 3, None) == -1
+    assert lib.qtts_stream_read_device_ex(C.c_void_p(4096), 32, -1, 4, None) == -1
     assert lib.qtts_last_error(None) == b"null context"
     lib.qtts_ctx_destroy(None)
     lib.qtts_q4_free(None)
