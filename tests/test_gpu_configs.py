@@ -13,7 +13,9 @@ oracle on the same seeded random-init weights and inputs:
   to 2000 N(0,1) rows: 3 sampled frames, every stream's codes, frame count,
   cache length and appended cache rows.
 
-Bars: codes identical; hidden states and cache rows within 1e-3 relative.
+Bars: codes identical; hidden states and cache rows within 1e-3 relative
+and within the regression bar of tests/shapes.py (about ten times the
+measured error).
 The oracle loops run in worker threads (ctypes releases the GIL), the
 predictor being single-threaded as in the reference.
 """
@@ -25,7 +27,7 @@ import pytest
 
 import qtts
 from oracle import oracle
-from shapes import FULL_PREDICTOR, FULL_TALKER, rel_err
+from shapes import FULL_PREDICTOR, FULL_TALKER, rel_err, within
 
 pytestmark = pytest.mark.gpu
 
@@ -54,12 +56,11 @@ def prompt64(full):
     kv, okv = t.new_kv(PROMPT + 8), ot.new_kv(PROMPT + 8)
     lh = t.prefill_talker_raw(x, PROMPT, kv)
     olh = ot.prefill_talker_raw(x, PROMPT, okv)
-    e = rel_err(lh, olh)
-    print(f"64-token prefill: last hidden rel err {e:.2e}", flush=True)
-    assert e < REL_TOL
+    print(f"64-token prefill: last hidden rel err {rel_err(lh, olh):.2e}", flush=True)
+    assert within(lh, olh)
     gk, gv = kv.store()
     rk, rv = okv.store()
-    assert rel_err(gk, rk) < REL_TOL and rel_err(gv, rv) < REL_TOL
+    assert within(gk, rk) and within(gv, rv)
     return {"gpu": (gk, gv), "oracle": (rk, rv), "last_hidden": olh, "logits": ot.apply_codec_head(olh)}
 
 
@@ -75,7 +76,7 @@ def _check_appended(kv, okv, start, count):
     (gk, gv), (rk, rv) = kv.store(), okv.store()
     assert gk.shape == rk.shape
     sl = slice(start, start + count)
-    assert rel_err(gk[:, sl], rk[:, sl]) < REL_TOL and rel_err(gv[:, sl], rv[:, sl]) < REL_TOL
+    assert within(gk[:, sl], rk[:, sl]) and within(gv[:, sl], rv[:, sl])
 
 
 @pytest.mark.timeout(600)
@@ -159,6 +160,69 @@ def test_full_loop_64_frames_after_prefill(full, prompt64):
         _check_appended(kv, okv, PROMPT, frames)
 
 
+def _loaded_caches(t, ot, c, L, cap, seed, tag):
+    """Both sides' caches loaded to the same L N(0,1) rows."""
+    shape = (c.layers, L, c.kv_heads, c.head_dim)
+    k = qtts.synth_normal_f32(seed, f"{tag}.k", int(np.prod(shape))).reshape(shape)
+    v = qtts.synth_normal_f32(seed, f"{tag}.v", int(np.prod(shape))).reshape(shape)
+    return _caches(t, ot, cap, (k, v), (k, v), L)
+
+
+@pytest.mark.timeout(900)
+def test_config4_bench_window(full):
+    """The window bench.py times: the talker + predictor loop from a cache of
+    304 rows (N(0,1)), 20 sampled frames at cache lengths 305..324 (top-k 50,
+    T 0.8, penalty 1.05, trailing text then pad): codes identical, appended
+    cache rows within the bars."""
+    tw, pw, t, p, ot, op = full
+    c = tw.cfg
+    L, frames = 304, 20
+    kv, okv = _loaded_caches(t, ot, c, L, L + frames + 4, 44, "cfg4win")
+    lh = qtts.synth_normal_f32(44, "cfg4win.h", c.hidden)
+    lg = ot.apply_codec_head(lh)
+    text = qtts.synth_normal_f32(44, "cfg4win.text", 4 * c.hidden, 0.0, 0.1).reshape(4, c.hidden)
+    pad = qtts.synth_normal_f32(44, "cfg4win.pad", c.hidden, 0.0, 0.1)
+    params = qtts.loop_params(frames, temperature=0.8, top_k=50, repetition_penalty=1.05, stop_on_eos=False)
+    t0 = time.time()
+    with ThreadPoolExecutor(max_workers=1) as pool:
+        fut = pool.submit(oracle.generate_codes, ot, op, okv, op.new_kv(), lh, lg, L, text, pad, params, 4242)
+        got = qtts.generate_codes(t, p, kv, p.new_kv(), lh, lg, L, text, pad, params, seed=4242)
+        ref = fut.result()
+    print(f"config 4 at KV {L + 1}..{L + frames}: {time.time() - t0:.1f}s", flush=True)
+    assert got.shape == ref.shape == (16, frames)
+    assert np.array_equal(got, ref), np.argwhere(got != ref)[:5]
+    assert len(kv) == len(okv) == L + frames
+    _check_appended(kv, okv, L, frames)
+
+
+@pytest.mark.timeout(600)
+def test_loop_is_deterministic(full):
+    """The same loop twice on one context with the same seed and inputs
+    (talker + predictor, 24 sampled frames from a 304-row cache): codes, the
+    talker's appended cache rows and the predictor cache are identical bit
+    for bit."""
+    tw, pw, t, p, ot, _ = full
+    c = tw.cfg
+    L, frames = 304, 24
+    lh = qtts.synth_normal_f32(45, "det.h", c.hidden)
+    lg = ot.apply_codec_head(lh)
+    text = qtts.synth_normal_f32(45, "det.text", 3 * c.hidden, 0.0, 0.1).reshape(3, c.hidden)
+    pad = qtts.synth_normal_f32(45, "det.pad", c.hidden, 0.0, 0.1)
+    params = qtts.loop_params(frames, temperature=0.8, top_k=50, repetition_penalty=1.05, stop_on_eos=False)
+    runs = []
+    for _ in range(2):
+        kv, _okv = _loaded_caches(t, ot, c, L, L + frames + 4, 45, "det")
+        pkv = p.new_kv()
+        codes = qtts.generate_codes(t, p, kv, pkv, lh, lg, L, text, pad, params, seed=99)
+        k, v = kv.store()
+        runs.append((codes, k[:, L:], v[:, L:], pkv.store()))
+        kv.close()
+    (c0, k0, v0, p0), (c1, k1, v1, p1) = runs
+    assert np.array_equal(c0, c1)
+    assert np.array_equal(k0, k1) and np.array_equal(v0, v1)
+    assert all(np.array_equal(a, b) for a, b in zip(p0, p1))
+
+
 @pytest.mark.timeout(900)
 def test_batch_config5_16_streams_2000_rows(full):
     """16 streams of the talker + predictor in 2064-row caches (the talker
@@ -230,10 +294,11 @@ def test_talker_steps_long_cache(full, monkeypatch, L, engine):
         emb = qtts.synth_normal_f32(60 + i, "long.emb", c.hidden)
         got = t.forward_with_embedding(emb, kv, L + i)
         ref = ot.forward_with_embedding(emb, okv, L + i)
-        e = rel_err(got[: c.hidden], ref[: c.hidden])
-        print(f"L={L} {engine} step {i}: hidden rel err {e:.2e}", flush=True)
-        assert e < REL_TOL and rel_err(got[c.hidden:], ref[c.hidden:]) < REL_TOL
+        print(f"L={L} {engine} step {i}: hidden rel err {rel_err(got[: c.hidden], ref[: c.hidden]):.2e}", flush=True)
+        # measured up to 2.3e-5 at 2064 random rows (long softmax sums)
+        tight = 1e-4 if L > 1024 else None
+        assert within(got[: c.hidden], ref[: c.hidden], tight) and within(got[c.hidden:], ref[c.hidden:], tight)
     gk, gv = kv.store()
     rk, rv = okv.store()
-    assert rel_err(gk[:, L:], rk[:, L:]) < REL_TOL and rel_err(gv[:, L:], rv[:, L:]) < REL_TOL
+    assert within(gk[:, L:], rk[:, L:], tight) and within(gv[:, L:], rv[:, L:], tight)
     kv.close()

@@ -4,9 +4,9 @@ transformer's sliding window exceeded) over several lengths, the 1.7B model's
 decoder at full size, the strided-codes device entry point, a decoder read
 from a .qora-tts file, and the error cases.
 
-Bar: audio within REL_TOL = 1e-3 of the oracle's (max abs difference over
-max abs sample, f32 sums in a different order over ~40 dependent stages);
-lengths exact."""
+Bars: audio within REL_TOL = 1e-3 of the oracle's (max abs difference over
+max abs sample, f32 sums in a different order over ~40 dependent stages) and
+within DECODER_TIGHT, about ten times the measured error; lengths exact."""
 import ctypes as C
 
 import numpy as np
@@ -16,10 +16,14 @@ import qtts
 from bench import Hip
 from oracle import oracle
 from qtts_file_writer import SMALL_DECODER, TextWeights, write_model
-from shapes import TINY_PREDICTOR, TINY_TALKER, rel_err
+from shapes import TINY_PREDICTOR, TINY_TALKER, rel_err, within
 
 pytestmark = pytest.mark.gpu
 REL_TOL = 1e-3
+# The decoder's regression bar: its audio passes through ~40 f32 layers and
+# transposed convolutions (measured errors 2e-6 small, 2.3e-5 at the 1.7B
+# shapes), so its bar sits above the loop's.
+DECODER_TIGHT = float(__import__("os").environ.get("QTTS_TEST_TIGHT_DECODER", "2e-4"))
 
 
 @pytest.fixture(scope="module")
@@ -35,9 +39,8 @@ def test_small_decoder_matches_oracle(small, frames):
     got = dec.decode_to_audio(codes)
     ref = oracle.decode_to_audio(w, codes)
     assert got.shape == ref.shape == (dec.num_samples(frames),)
-    e = rel_err(got, ref)
-    print(f"small decoder, {frames} frames: {got.size} samples, rel err {e:.2e}")
-    assert e < REL_TOL
+    print(f"small decoder, {frames} frames: {got.size} samples, rel err {rel_err(got, ref):.2e}")
+    assert within(got, ref, tight=DECODER_TIGHT)
 
 
 def test_full_decoder_matches_oracle(ctx):
@@ -47,9 +50,8 @@ def test_full_decoder_matches_oracle(ctx):
     got = dec.decode_to_audio(codes)
     ref = oracle.decode_to_audio(w, codes)
     assert got.shape == ref.shape == (3 * 1920,)
-    e = rel_err(got, ref)
-    print(f"1.7B decoder, 3 frames: rel err {e:.2e}, audio std {np.std(ref):.3f}")
-    assert e < REL_TOL
+    print(f"1.7B decoder, 3 frames: rel err {rel_err(got, ref):.2e}, audio std {np.std(ref):.3f}")
+    assert within(got, ref, tight=DECODER_TIGHT)
 
 
 def test_device_entry_point_with_strided_codes(ctx, small):

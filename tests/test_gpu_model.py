@@ -3,7 +3,8 @@ predictor frame and the frame loop — against the oracle on the same seeded
 random-init weights and inputs.
 
 Bars: hidden states and logits within REL_TOL = 1e-3 relative (fp32
-accumulate); predictor codes and greedy loop codes identical.
+accumulate) and within the regression bar of tests/shapes.py (about ten
+times the measured error); predictor codes and greedy loop codes identical.
 """
 import time
 
@@ -12,7 +13,7 @@ import pytest
 
 import qtts
 from oracle import oracle
-from shapes import FULL_PREDICTOR, FULL_TALKER, TINY_PREDICTOR, TINY_TALKER, rel_err
+from shapes import FULL_PREDICTOR, FULL_TALKER, TINY_PREDICTOR, TINY_TALKER, rel_err, within
 
 pytestmark = pytest.mark.gpu
 
@@ -43,12 +44,12 @@ def test_talker_steps_tiny(tiny):
         emb = qtts.synth_normal_f32(22, f"tiny.emb.{step}", cfg.hidden)
         got = t.forward_with_embedding(emb, kv, step + 3)
         ref = ot.forward_with_embedding(emb, okv, step + 3)
-        assert rel_err(got[: cfg.hidden], ref[: cfg.hidden]) < REL_TOL
-        assert rel_err(got[cfg.hidden:], ref[cfg.hidden:]) < REL_TOL
+        assert within(got[: cfg.hidden], ref[: cfg.hidden])
+        assert within(got[cfg.hidden:], ref[cfg.hidden:])
     assert len(kv) == len(okv) == 20
     k, v = kv.store()
     ok, ov = okv.store()
-    assert rel_err(k, ok) < REL_TOL and rel_err(v, ov) < REL_TOL
+    assert within(k, ok) and within(v, ov)
 
 
 def test_talker_step_full_prefilled_kv(full):
@@ -68,7 +69,7 @@ def test_talker_step_full_prefilled_kv(full):
     ref = ot.forward_with_embedding(emb, okv, L)
     eh, el = rel_err(got[: cfg.hidden], ref[: cfg.hidden]), rel_err(got[cfg.hidden:], ref[cfg.hidden:])
     print(f"full talker step: hidden rel err {eh:.2e}, logits rel err {el:.2e}")
-    assert eh < REL_TOL and el < REL_TOL
+    assert within(got[: cfg.hidden], ref[: cfg.hidden]) and within(got[cfg.hidden:], ref[cfg.hidden:])
     assert int(np.argmax(got[cfg.hidden:])) == int(np.argmax(ref[cfg.hidden:]))
 
 
@@ -83,13 +84,13 @@ def test_prefill_tiny(tiny, seq_len):
     kv, okv = t.new_kv(cap), ot.new_kv(cap)
     got = t.prefill_talker_raw(x, seq_len, kv)
     ref = ot.prefill_talker_raw(x, seq_len, okv)
-    assert rel_err(got, ref) < REL_TOL
+    assert within(got, ref)
     k, v = kv.store()
     ok, ov = okv.store()
-    assert rel_err(k, ok) < REL_TOL and rel_err(v, ov) < REL_TOL
+    assert within(k, ok) and within(v, ov)
     # a decode step continues from the prefilled cache
     emb = qtts.synth_normal_f32(23, "prefill.next", cfg.hidden)
-    assert rel_err(t.forward_with_embedding(emb, kv, seq_len), ot.forward_with_embedding(emb, okv, seq_len)) < REL_TOL
+    assert within(t.forward_with_embedding(emb, kv, seq_len), ot.forward_with_embedding(emb, okv, seq_len))
 
 
 def test_prefill_nonempty_cache_rejected(tiny):
@@ -107,9 +108,8 @@ def test_prefill_full_64(full):
     kv, okv = t.new_kv(128), ot.new_kv(128)
     got = t.prefill_talker_raw(x, 64, kv)
     ref = ot.prefill_talker_raw(x, 64, okv)
-    e = rel_err(got, ref)
-    print(f"prefill 64 rel err {e:.2e}")
-    assert e < REL_TOL
+    print(f"prefill 64 rel err {rel_err(got, ref):.2e}")
+    assert within(got, ref)
 
 
 def test_predictor_tiny(tiny):
@@ -141,7 +141,7 @@ def test_predictor_cache_paths(tiny, capacity):
         assert np.array_equal(got, ref), (got, ref)
         (gk, gv), (rk, rv) = kv.store(), okv.store()
         assert gk.shape == rk.shape
-        assert rel_err(gk, rk) < REL_TOL and rel_err(gv, rv) < REL_TOL
+        assert within(gk, rk) and within(gv, rv)
 
 
 def test_predictor_full(full):
@@ -171,7 +171,7 @@ def test_predictor_input_table_on_and_off(ctx, full, monkeypatch):
         ref = op.generate_acoustic_codes(h, sem, op.new_kv())
         assert np.array_equal(on, ref) and np.array_equal(off, ref), (on, off, ref)
         (k1, v1), (k0, v0) = kv_on.store(), kv_off.store()
-        assert rel_err(k1, k0) < REL_TOL and rel_err(v1, v0) < REL_TOL
+        assert within(k1, k0) and within(v1, v0)
 
 
 def _loop_inputs(tw, seed, trailing=3):
@@ -199,7 +199,7 @@ def test_loop_tiny(tiny, greedy):
     assert got.shape == ref.shape == (16, frames)
     assert np.array_equal(got, ref), np.argwhere(got != ref)[:5]
     assert len(kv) == len(okv) == 10 + frames
-    assert rel_err(lh, olh) < REL_TOL
+    assert within(lh, olh)
 
 
 @pytest.mark.parametrize("per_launch", ["1", "7", None])
@@ -224,7 +224,7 @@ def test_loop_tiny_codes_per_launch(tiny, monkeypatch, per_launch):
     assert np.array_equal(got, ref), np.argwhere(got != ref)[:5]
     assert len(kv) == len(okv) == frames
     (k, v), (ok, ov) = kv.store(), okv.store()
-    assert k.shape == ok.shape and rel_err(k, ok) < REL_TOL and rel_err(v, ov) < REL_TOL
+    assert k.shape == ok.shape and within(k, ok) and within(v, ov)
     # EOS at frame 20's code 0: inside the second launch of 16, the third of 7
     eos = int(ref[0, 20])
     first = int(np.argmax(ref[0] == eos))

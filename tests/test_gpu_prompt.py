@@ -14,7 +14,7 @@ import pytest
 
 import qtts
 from oracle import oracle
-from shapes import FULL_PREDICTOR, FULL_TALKER, rel_err
+from shapes import FULL_PREDICTOR, FULL_TALKER, rel_err, within
 
 pytestmark = pytest.mark.gpu
 
@@ -63,9 +63,9 @@ def test_prompt_rows_and_prefill(small, voice, tokens):
     lh, lg, pos = t.prefill_custom_voice(tokens, SPEAKER, LANGUAGE, kv, v)
     olh, olg, opos = ox.prefill_custom_voice(tokens, SPEAKER, LANGUAGE, okv, v)
     assert pos == opos == ref.shape[0] and len(kv) == len(okv) == pos
-    assert rel_err(lh, olh) < TOL and rel_err(lg, olg) < TOL
+    assert within(lh, olh) and within(lg, olg)
     (gk, gv), (rk, rv) = kv.store(), okv.store()
-    assert rel_err(gk, rk) < TOL and rel_err(gv, rv) < TOL
+    assert within(gk, rk) and within(gv, rv)
 
 
 @pytest.mark.parametrize("voice", [False, True], ids=["speaker", "voice"])
