@@ -22,7 +22,9 @@ if _PKG not in sys.path:
 
 import qtts  # noqa: E402  (host weight containers and ctypes views)
 
-LIB_PATH = os.path.join(_HERE, "liboracle.so")
+# QTTS_ORACLE_LIB names another build of the same sources (the sanitizer
+# build of tests/sanitize.mk); the default is the -O3 build of oracle/Makefile.
+LIB_PATH = os.environ.get("QTTS_ORACLE_LIB") or os.path.join(_HERE, "liboracle.so")
 _lib = None
 
 

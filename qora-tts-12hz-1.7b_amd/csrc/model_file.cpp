@@ -22,6 +22,19 @@ namespace {
 
 thread_local std::string g_error;
 
+// The fewest file bytes an item of each structure count takes (its headers
+// and u64 array counts with empty arrays), so that a count can be bounded by
+// the bytes left: an array 8, a Q4 weight 32 (k, n and two counts), a layer
+// 7 weights and 4 norm vectors, an upsample stage its channel count, two
+// convolutions (5 and 3 dimensions, weight and bias each) and 7 vectors, a
+// vocos block 2 vectors, a convolution and its residual count, a residual 4
+// vectors and 2 convolutions of 6 dimensions.
+constexpr uint64_t kVecMinBytes = 8, kWeightMinBytes = 32;
+constexpr uint64_t kLayerMinBytes = 7 * kWeightMinBytes + 4 * kVecMinBytes;
+constexpr uint64_t kUpsampleMinBytes = 4 + (20 + 2 * kVecMinBytes) + (12 + 2 * kVecMinBytes) + 7 * kVecMinBytes;
+constexpr uint64_t kVocosBlockMinBytes = 2 * kVecMinBytes + (20 + 2 * kVecMinBytes) + 4;
+constexpr uint64_t kResidualMinBytes = 4 * kVecMinBytes + 2 * (24 + 2 * kVecMinBytes);
+
 struct FileReader {
     FILE *f = nullptr;
     int64_t pos = 0, size = 0;
@@ -57,6 +70,15 @@ struct FileReader {
         if (!u32(&u, what)) return false;
         if (u > 0x7FFFFFFFu) return fail(std::string(what) + " out of range");
         *v = (int32_t)u;
+        return true;
+    }
+    // A structure count (layers, weights, stages): items that each take at
+    // least `min_bytes` of the file, bounded by the bytes left before
+    // anything is sized by it.
+    bool items(int32_t *v, uint64_t min_bytes, const char *what) {
+        if (!dim(v, what)) return false;
+        if ((uint64_t)*v > (uint64_t)(size - pos) / min_bytes)
+            return fail(std::string(what) + ": more items than the bytes left");
         return true;
     }
     // u64 element count of `elem`-byte elements, bounded by the bytes left.
@@ -162,7 +184,7 @@ struct qtts_model_file {
     bool read_talker(FileReader &r) {
         qtts_talker_view &t = talker;
         int32_t layers, text_hidden, sec;
-        if (!r.dim(&layers, "talker num_layers") || !r.dim(&t.hidden_size, "talker hidden_size") ||
+        if (!r.items(&layers, kLayerMinBytes, "talker num_layers") || !r.dim(&t.hidden_size, "talker hidden_size") ||
             !r.dim(&text_hidden, "talker text_hidden_size") || !r.dim(&t.num_heads, "talker num_heads") ||
             !r.dim(&t.num_kv_heads, "talker num_kv_heads") || !r.dim(&t.head_dim, "talker head_dim") ||
             !r.dim(&info.talker_num_kv_groups, "talker num_kv_groups") || !r.dim(&sec, "mrope_section length"))
@@ -201,7 +223,7 @@ struct qtts_model_file {
         qtts_predictor_view &p = predictor;
         int32_t layers, groups, heads_lm;
         uint8_t has_proj;
-        if (!r.dim(&layers, "predictor num_layers") || !r.dim(&p.hidden_size, "predictor hidden_size") ||
+        if (!r.items(&layers, kLayerMinBytes, "predictor num_layers") || !r.dim(&p.hidden_size, "predictor hidden_size") ||
             !r.dim(&p.num_heads, "predictor num_heads") || !r.dim(&p.num_kv_heads, "predictor num_kv_heads") ||
             !r.dim(&p.head_dim, "predictor head_dim") ||
             !r.dim(&info.predictor_num_kv_groups, "predictor num_kv_groups") || !r.u8(&has_proj, "has_proj"))
@@ -215,7 +237,7 @@ struct qtts_model_file {
                 return false;
             if (len != (uint64_t)p.input_proj.n) return r.fail("predictor.input_proj_bias: length mismatch");
         }
-        if (!r.dim(&groups, "predictor codec embedding count")) return false;
+        if (!r.items(&groups, kWeightMinBytes, "predictor codec embedding count")) return false;
         codec_embeddings.resize((size_t)groups);
         for (int32_t g = 0; g < groups; g++)
             if (!q4(r, &codec_embeddings[(size_t)g], "predictor.codec_embeddings." + std::to_string(g))) return false;
@@ -224,7 +246,7 @@ struct qtts_model_file {
             if (!layer(r, &predictor_layers[(size_t)l], p.hidden_size, p.head_dim,
                        "predictor.layers." + std::to_string(l)))
                 return false;
-        if (!r.dim(&heads_lm, "predictor lm head count")) return false;
+        if (!r.items(&heads_lm, kWeightMinBytes, "predictor lm head count")) return false;
         lm_heads.resize((size_t)heads_lm);
         for (int32_t g = 0; g < heads_lm; g++)
             if (!q4(r, &lm_heads[(size_t)g], "predictor.lm_heads." + std::to_string(g))) return false;
@@ -306,7 +328,7 @@ struct qtts_model_file {
         if (!vec(r, &w.first_output_proj, 0, "decoder.first_output_proj", &n)) return false;
         if (n % cd) return r.fail("decoder.first_output_proj: not whole rows of codebook_dim");
         w.vq_dim = (int32_t)(n / cd);
-        if (!r.dim(&d.decoder_rest_codebooks, "decoder codebook count")) return false;
+        if (!r.items(&d.decoder_rest_codebooks, kVecMinBytes, "decoder codebook count")) return false;
         w.num_rest = d.decoder_rest_codebooks;
         rest_codebooks.resize((size_t)w.num_rest);
         for (int32_t g = 0; g < w.num_rest; g++)
@@ -319,7 +341,7 @@ struct qtts_model_file {
             return false;
         const uint64_t lat = (uint64_t)w.pre_conv.out_channels;
         if (!vec(r, &w.tf_input_w, lat * hid, "decoder.tf_input_w") || !vec(r, &w.tf_input_b, hid, "decoder.tf_input_b") ||
-            !r.dim(&d.decoder_layers, "decoder layer count"))
+            !r.items(&d.decoder_layers, 11 * kVecMinBytes, "decoder layer count"))
             return false;
         w.num_layers = d.decoder_layers;
         dec_layers.resize((size_t)w.num_layers);
@@ -337,7 +359,7 @@ struct qtts_model_file {
         w.layers = dec_layers.data();
         if (!vec(r, &w.tf_norm, hid, "decoder.tf_norm") || !vec(r, &w.tf_output_w, hid * lat, "decoder.tf_output_w") ||
             !vec(r, &w.tf_output_b, lat, "decoder.tf_output_b") ||
-            !r.dim(&d.decoder_upsample_stages, "decoder upsample count"))
+            !r.items(&d.decoder_upsample_stages, kUpsampleMinBytes, "decoder upsample count"))
             return false;
         w.num_upsample = d.decoder_upsample_stages;
         dec_upsample.resize((size_t)w.num_upsample);
@@ -359,7 +381,7 @@ struct qtts_model_file {
                 return false;
         }
         w.upsample = dec_upsample.data();
-        if (!conv(r, &w.vocos_init, 0, "decoder.vocos_init") || !r.dim(&d.decoder_vocos_blocks, "vocos block count"))
+        if (!conv(r, &w.vocos_init, 0, "decoder.vocos_init") || !r.items(&d.decoder_vocos_blocks, kVocosBlockMinBytes, "vocos block count"))
             return false;
         w.num_vocos_blocks = d.decoder_vocos_blocks;
         dec_blocks.resize((size_t)w.num_vocos_blocks);
@@ -370,17 +392,24 @@ struct qtts_model_file {
             int32_t nres;
             if (!vec(r, &B.pre_snake_alpha, 0, p + ".pre_snake_alpha", &na) ||
                 !vec(r, &B.pre_snake_beta, na, p + ".pre_snake_beta") || !conv(r, &B.upsample, 1, p + ".upsample") ||
-                !r.dim(&nres, "vocos residual count"))
+                !r.items(&nres, kResidualMinBytes, "vocos residual count"))
                 return false;
+            // a SnakeBeta has one (alpha, beta) per channel of the
+            // convolution it feeds (src/conv.rs:347-372)
+            if (na != (uint64_t)B.upsample.in_channels)
+                return r.fail(p + ".pre_snake_alpha: length is not the upsample's input channels");
             dec_residuals.emplace_back((size_t)nres);
             std::vector<qtts_vocos_residual_view> &res = dec_residuals.back();
             for (int32_t i = 0; i < nres; i++) {
                 qtts_vocos_residual_view &R = res[(size_t)i];
                 const std::string q = p + ".residuals." + std::to_string(i);
+                uint64_t na2;
                 if (!vec(r, &R.act1_alpha, 0, q + ".act1_alpha", &na) || !vec(r, &R.act1_beta, na, q + ".act1_beta") ||
-                    !conv(r, &R.conv1, 0, q + ".conv1") || !vec(r, &R.act2_alpha, 0, q + ".act2_alpha", &na) ||
-                    !vec(r, &R.act2_beta, na, q + ".act2_beta") || !conv(r, &R.conv2, 0, q + ".conv2"))
+                    !conv(r, &R.conv1, 0, q + ".conv1") || !vec(r, &R.act2_alpha, 0, q + ".act2_alpha", &na2) ||
+                    !vec(r, &R.act2_beta, na2, q + ".act2_beta") || !conv(r, &R.conv2, 0, q + ".conv2"))
                     return false;
+                if (na != (uint64_t)R.conv1.in_channels || na2 != (uint64_t)R.conv2.in_channels)
+                    return r.fail(q + ": a SnakeBeta's length is not its convolution's input channels");
             }
             B.num_residuals = nres;
             B.residuals = res.data();
@@ -392,6 +421,8 @@ struct qtts_model_file {
             !conv(r, &w.output_conv, 0, "decoder.output_conv") || !vec(r, &w.rope_cos, 0, "decoder.rope_cos", &nc) ||
             !vec(r, &w.rope_sin, nc, "decoder.rope_sin"))
             return false;
+        if (na != (uint64_t)w.output_conv.in_channels)
+            return r.fail("decoder.final_snake_alpha: length is not output_conv's input channels");
         const uint64_t half = (uint64_t)w.head_dim / 2;
         if (half == 0 || nc % half) return r.fail("decoder rope tables: not whole rows of head_dim/2");
         w.rope_rows = (int32_t)(nc / half);

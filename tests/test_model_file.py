@@ -238,3 +238,40 @@ def test_inconsistent_weight_lengths_are_rejected(tmp_path, model):
     p.write_bytes(bytes(data))
     rc, msg = _open_status(str(p))
     assert rc == qtts.QTTS_EINVAL and "packed length" in msg, msg
+
+
+def test_snake_lengths_must_match_their_convolutions(tmp_path, model):
+    """A SnakeBeta with fewer entries than the channels of the convolution it
+    feeds (found by the sanitized fuzz pass of tests/fuzz_model_file.cpp: the
+    reader accepted it and the decoder upload then read past the array)."""
+    from qtts_file_writer import SMALL_DECODER
+
+    for where in ("final", "pre", "act1"):
+        dw = qtts.DecoderWeights(5, SMALL_DECODER)
+        if where == "final":
+            dw.final_snake_alpha = dw.final_snake_alpha[:-1]
+            dw.final_snake_beta = dw.final_snake_beta[:-1]
+        elif where == "pre":
+            dw.blocks[0]["pre_snake_alpha"] = dw.blocks[0]["pre_snake_alpha"][:-1]
+            dw.blocks[0]["pre_snake_beta"] = dw.blocks[0]["pre_snake_beta"][:-1]
+        else:
+            r = dw.blocks[-1]["residuals"][0]
+            r["act1_alpha"], r["act1_beta"] = r["act1_alpha"][:-1], r["act1_beta"][:-1]
+        path, _ = _write(tmp_path, model, name=f"snake_{where}.qora-tts", decoder=dw)
+        rc, msg = _open_status(path)
+        assert rc == qtts.QTTS_EINVAL and "input channels" in msg, (where, msg)
+
+
+def test_structure_counts_are_bounded_by_the_file(tmp_path, model):
+    """A layer count of 2^31 - 1 (found by the fuzz pass: the reader sized its
+    layer list from the count before reading any layer) is refused before
+    anything is allocated."""
+    path, meta = _write(tmp_path, model)
+    data = bytearray(open(path, "rb").read())
+    for off in (meta["talker_offset"], meta["predictor_offset"]):  # num_layers, the first u32 of each section
+        bad = bytearray(data)
+        bad[off:off + 4] = (0x7FFFFFFF).to_bytes(4, "little")
+        p = tmp_path / f"count{off}"
+        p.write_bytes(bytes(bad))
+        rc, msg = _open_status(str(p))
+        assert rc == qtts.QTTS_EINVAL and "more items than the bytes left" in msg, msg
