@@ -235,6 +235,16 @@ qtts_status qtts_embed_codec_token(qtts_talker *t, uint32_t token_id, float *out
  * past its table is QTTS_ERANGE.  The cache gains one row. */
 qtts_status qtts_forward_talker_decode(qtts_talker *t, uint32_t token_id, int32_t is_text, qtts_kv *kv,
                                        int32_t position, float *hidden);
+/* prefill_talker(weights, tokens, kv) -> the final-normed last row
+ * [hidden_size]; src/talker.rs:467-488.  The reference's (token, is_text)
+ * pairs arrive as two arrays of seq_len entries: row i is
+ * embed_text_token(tokens[i]) when is_text[i] is nonzero (text weights
+ * uploaded, else QTTS_ESTATE) and embed_codec_token(tokens[i]) otherwise;
+ * the rows then go through prefill_talker_raw (src/talker.rs:364-462).
+ * Every id is checked before any work (QTTS_ERANGE past its table); the
+ * cache must be empty and gains seq_len rows. */
+qtts_status qtts_prefill_talker(qtts_talker *t, const uint32_t *tokens, const int32_t *is_text, int32_t seq_len,
+                                qtts_kv *kv, float *last_hidden);
 
 /* Prompt assembly (src/talker.rs:105-116, src/generate_new.rs:60-326).  The
  * text weights ride with the talker; every step below runs on the device.  */
@@ -292,8 +302,8 @@ qtts_status qtts_get_acoustic_embeddings_sum(qtts_predictor *p, const uint32_t *
  * projected talker_hidden goes through the stack at the cache offset (RoPE
  * at that offset) and every head reads the final-normed row.  logits is
  * [num_groups][cp_vocab].  The cache is NOT cleared and gains one row;
- * QTTS_ERANGE when it is full or the offset passes the device RoPE table
- * (4096 rows, fewer when max_position is smaller). */
+ * QTTS_ERANGE when it is full.  Offsets at or past max_position (the
+ * table's rows) skip the rotation, as src/code_predictor.rs:105-107 does. */
 qtts_status qtts_predict_codes(qtts_predictor *p, const float *talker_hidden, qtts_kv *kv, float *logits);
 
 /* ------------------------------------------------------------------------ */

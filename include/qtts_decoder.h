@@ -110,11 +110,28 @@ int64_t qtts_decoder_num_samples(const qtts_decoder *d, int32_t frames);
  * g's index at frame t, g < num_rest + 1, t < frames; audio receives
  * qtts_decoder_num_samples(d, frames) samples (QTTS_ERANGE if capacity is
  * smaller, or for a code >= codebook_size).  Host buffers; the _device form
- * takes device buffers and does not synchronise. */
+ * takes device buffers, does not synchronise and does not read the codes on
+ * the host: a code >= codebook_size there reads codebook row 0. */
 qtts_status qtts_decode_to_audio(qtts_decoder *d, const uint32_t *codes, int32_t frames, int32_t ld, float *audio,
                                  int64_t capacity, int64_t *n_samples);
 qtts_status qtts_decode_to_audio_device(qtts_decoder *d, const uint32_t *d_codes, int32_t frames, int32_t ld,
                                         float *d_audio, int64_t capacity, int64_t *n_samples);
+
+/* generate_speech (src/generate_new.rs:191-311) from token ids to audio:
+ * qtts_generate_speech_codes's steps, then decode_to_audio of the codes
+ * where the frame loop leaves them in device memory (they never cross to the
+ * host).  The tokenizer is not part of it.  audio (host) receives *n_samples
+ * = qtts_decoder_num_samples(d, *n_frames) floats; capacity must cover
+ * qtts_decoder_num_samples(d, params->max_codes), checked before any work
+ * (QTTS_ERANGE).  A generated code >= the decoder's codebook_size, where the
+ * reference's lookup would panic, is QTTS_ERANGE.  The decoder must be on
+ * the talker's device (QTTS_EINVAL) and read at most 16 code groups
+ * (QTTS_ESHAPE).  Caches and seed as for qtts_generate_speech_codes. */
+qtts_status qtts_generate_speech(qtts_talker *t, qtts_predictor *p, qtts_decoder *d, const uint32_t *text_tokens,
+                                 int32_t n_text, uint32_t speaker_id, uint32_t language_id,
+                                 const float *voice_embedding, qtts_kv *talker_kv, qtts_kv *predictor_kv,
+                                 const qtts_loop_params *params, uint64_t seed, float *audio, int64_t capacity,
+                                 int64_t *n_samples, int32_t *n_frames);
 
 #ifdef __cplusplus
 }

@@ -101,6 +101,7 @@ def load():
         "qor_sample_top_k": ([vp, i32, C.c_float, i32, C.POINTER(C.c_uint64), C.POINTER(u32)], i32),
         "qor_predict_codes": ([vp, vp, vp, vp, i32], i32),
         "qor_forward_talker_decode": ([vp, vp, u32, i32, vp, i32, vp, i32], i32),
+        "qor_prefill_talker": ([vp, vp, vp, vp, i32, vp, vp, i32], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -431,6 +432,19 @@ class Text:
             load().qor_text_free(self.h)
         except Exception:
             pass
+
+
+def prefill_talker(talker: Talker, text: Optional[Text], tokens, is_text, kv: Kv, nthreads: int = 0) -> np.ndarray:
+    """prefill_talker (src/talker.rs:467-488): the (token, is_text) rows
+    embedded by embed_text_token or embed_codec_token, then
+    prefill_talker_raw; returns the final-normed last row."""
+    t = np.ascontiguousarray(tokens, dtype=np.uint32)
+    f = np.ascontiguousarray(np.asarray(is_text, dtype=bool), dtype=np.int32)
+    assert t.shape == f.shape
+    out = np.empty(talker.cfg.hidden, dtype=np.float32)
+    _check(load().qor_prefill_talker(talker.h, text.h if text is not None else None, _p(t) if t.size else None,
+                                     _p(f) if f.size else None, t.size, kv.h, _p(out), nthreads))
+    return out
 
 
 def decode_to_audio(w, codes, nthreads: int = 0) -> np.ndarray:

@@ -580,16 +580,11 @@ struct qor_predictor {
 qor_predictor *qor_predictor_new(const qtts_predictor_view *w) {
     qor_predictor *p = (qor_predictor *)xcalloc(1, sizeof(qor_predictor));
     p->w = *w;
-    /* Positions never exceed num_groups+1 per frame; the table is the
-     * reference's formula, built for the positions that exist
-     * (src/loader.rs:859-874 builds 65536). */
+    /* The whole table, src/loader.rs:859-874 (max_position rows, 65536 for
+     * the 1.7B model); positions past it skip the rotation
+     * (src/code_predictor.rs:105-107). */
     const int32_t half = w->head_dim / 2;
-    /* generate_acoustic_codes restarts the cache every frame (positions
-     * 0..num_groups); predict_codes keeps appending, so the table covers
-     * 4096 positions (past them the oracle refuses: it would skip the
-     * rotation where the reference's 65536-row table does not). */
-    int32_t rows = 4096;
-    if (rows > w->max_position) rows = w->max_position;
+    const int32_t rows = w->max_position;
     p->st.num_layers = w->num_layers;
     p->st.layers = w->layers;
     p->st.final_norm_gamma = w->final_norm_gamma;
@@ -688,7 +683,6 @@ int32_t qor_generate_acoustic_codes(const qor_predictor *p, const float *talker_
 int32_t qor_predict_codes(const qor_predictor *p, const float *talker_hidden, qor_kv *kv, float *logits,
                           int32_t nthreads) {
     const int32_t hidden = p->w.hidden_size;
-    if (kv->len >= p->st.max_pos && kv->len < p->w.max_position) return QTTS_ERANGE;
     float *x = (float *)xcalloc((size_t)hidden, sizeof(float));
     project_input(p, talker_hidden, x, nthreads);
     int32_t rc = stack_decode(&p->st, x, kv, -1, nthreads);

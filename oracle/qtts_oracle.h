@@ -133,6 +133,10 @@ int32_t qor_predict_codes(const qor_predictor *p, const float *talker_hidden, qo
  * one step fed embed_text_token (is_text) or embed_codec_token. */
 int32_t qor_forward_talker_decode(const qor_talker *t, const qor_text *x, uint32_t token, int32_t is_text,
                                   qor_kv *kv, int32_t position, float *hidden, int32_t nthreads);
+/* prefill_talker, src/talker.rs:467-488: (token, is_text) rows through
+ * prefill_talker_raw.  x may be NULL when no row is text. */
+int32_t qor_prefill_talker(const qor_talker *t, const qor_text *x, const uint32_t *tokens, const int32_t *is_text,
+                           int32_t seq_len, qor_kv *kv, float *last_hidden, int32_t nthreads);
 
 /* --- prompt assembly (qtts_oracle_prompt.c) ------------------------------ */
 /* The text embedding and projection of TalkerWeights (src/talker.rs:33-56). */

@@ -193,6 +193,33 @@ int32_t qor_generate_speech_codes(const qor_talker *t, const qor_predictor *p, c
     return rc;
 }
 
+/* prefill_talker, src/talker.rs:467-488: row i is embed_text_token(tokens[i])
+ * when is_text[i] is nonzero, else embed_codec_token(tokens[i]); the rows in
+ * sequence order then go through prefill_talker_raw (src/talker.rs:364-462),
+ * which leaves the final-normed last row in last_hidden.  x may be NULL when
+ * no row is text. */
+int32_t qor_prefill_talker(const qor_talker *t, const qor_text *x, const uint32_t *tokens, const int32_t *is_text,
+                           int32_t seq_len, qor_kv *kv, float *last_hidden, int32_t nthreads) {
+    if (seq_len < 1) return QTTS_EINVAL;
+    const int32_t hid = qor_talker_hidden(t);
+    float *rows = (float *)calloc((size_t)seq_len * hid, sizeof(float));
+    if (!rows) abort();
+    int32_t rc = QTTS_OK;
+    for (int32_t i = 0; i < seq_len && rc == QTTS_OK; i++) {
+        float *row = rows + (size_t)i * hid;
+        if (is_text[i]) {
+            rc = x ? qor_embed_text_token(x, tokens[i], row, nthreads) : QTTS_ESTATE;
+        } else if (tokens[i] >= (uint32_t)qor_talker_codec_rows(t)) {
+            rc = QTTS_ERANGE;
+        } else {
+            qor_embed_codec_token(t, tokens[i], row);
+        }
+    }
+    if (rc == QTTS_OK) rc = qor_prefill_talker_raw(t, rows, seq_len, kv, last_hidden, nthreads);
+    free(rows);
+    return rc;
+}
+
 /* forward_talker_decode, src/talker.rs:161-258: embed_text_token (is_text)
  * or embed_codec_token, then forward_with_embedding's step; the final-normed
  * hidden state (the first hidden values forward_with_embedding returns). */

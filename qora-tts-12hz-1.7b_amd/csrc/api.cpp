@@ -29,7 +29,6 @@ constexpr size_t kPartialFloats = (size_t)1 << 20;  // split-K partials
 constexpr int kCounters = 8192;
 constexpr size_t kAttnPartFloats = (size_t)4 << 20;
 constexpr int kAttnCounters = 1024;
-constexpr int kPredictorRopeRows = 4096;
 
 }  // namespace
 
@@ -681,6 +680,9 @@ struct qtts_talker {
     float *pr_codec = nullptr;  // [8][hidden]: the prompt's codec rows and the voice row
     uint32_t *tx_tok = nullptr;
     int tx_cap = 0;
+    // prefill_talker's per-row token ids and text slots: [pf_cap] + [pf_cap]
+    uint32_t *pf_tok = nullptr;
+    int pf_cap = 0;
     // engine programs (built lazily, cached per cache object)
     std::unique_ptr<EngProgram> step_prog, frame_prog;
     uint64_t step_kv = 0;  // serial of the cache step_prog was built for
@@ -689,7 +691,7 @@ struct qtts_talker {
         for (void *p : prefill_bufs) (void)hipFree(p);
         if (codes) (void)hipFree(codes);
         if (trailing) (void)hipFree(trailing);
-        for (void *p : {(void *)tx_raw, (void *)tx_h, (void *)tx_rows, (void *)tx_tok})
+        for (void *p : {(void *)tx_raw, (void *)tx_h, (void *)tx_rows, (void *)tx_tok, (void *)pf_tok})
             if (p) (void)hipFree(p);
     }
 };
@@ -2250,6 +2252,55 @@ qtts_status qtts_prefill_custom_voice(qtts_talker *t, const uint32_t *text_token
     return QTTS_OK;
 }
 
+qtts_status qtts_prefill_talker(qtts_talker *t, const uint32_t *tokens, const int32_t *is_text, int32_t seq_len,
+                                qtts_kv *kv, float *last_hidden) {
+    if (!t || !last_hidden || (seq_len > 0 && (!tokens || !is_text))) return QTTS_EINVAL;
+    qtts_ctx *c = t->ctx;
+    if (seq_len < 1) return fail(c, QTTS_EINVAL, "seq_len < 1");
+    // every id checked before any work, so a bad one leaves the cache empty
+    std::vector<uint32_t> text_ids, ids((size_t)2 * seq_len);
+    int32_t *slot = reinterpret_cast<int32_t *>(ids.data() + seq_len);
+    for (int i = 0; i < seq_len; i++) {
+        ids[i] = tokens[i];
+        if (is_text[i]) {
+            if (!t->has_text) return fail(c, QTTS_ESTATE, "text token without text weights: call qtts_talker_text_upload");
+            if (tokens[i] >= (uint32_t)t->text_emb.K) return fail(c, QTTS_ERANGE, "text token id out of range");
+            slot[i] = (int32_t)text_ids.size();
+            text_ids.push_back(tokens[i]);
+        } else {
+            if (tokens[i] >= (uint32_t)t->emb.K) return fail(c, QTTS_ERANGE, "codec token id out of range");
+            slot[i] = -1;
+        }
+    }
+    QTTS_TRY(prefill_prepare(t, seq_len, kv));
+    if (seq_len > t->pf_cap) {
+        if (t->pf_tok) (void)hipFree(t->pf_tok);
+        t->pf_tok = nullptr;
+        t->pf_cap = 0;
+        HIP_TRY(c, hipMalloc(&t->pf_tok, sizeof(uint32_t) * 2 * seq_len));
+        t->pf_cap = seq_len;
+    }
+    // the text rows in one batch through the projection (embed_text_token,
+    // src/talker.rs:105-116), then every row into t->xp in sequence order
+    const int nt = (int)text_ids.size();
+    if (nt > 0) {
+        QTTS_TRY(text_reserve(t, nt));
+        QTTS_TRY(text_project(t, text_ids.data(), nt, t->tx_rows));
+    }
+    HIP_TRY(c, hipMemcpyAsync(t->pf_tok, ids.data(), sizeof(uint32_t) * 2 * seq_len, hipMemcpyHostToDevice, c->stream));
+    launch_token_rows(c->stream, t->emb, t->pf_tok, reinterpret_cast<const int *>(t->pf_tok + seq_len), t->tx_rows,
+                      seq_len, t->xp, t->st.hidden);
+    qtts_status s = check_launch(c, "k_token_rows");
+    if (s == QTTS_OK) s = prefill_from_xp(t, seq_len, kv);
+    if (s != QTTS_OK) {
+        (void)hipStreamSynchronize(c->stream);  // the ids copy reads `ids`
+        kv->len = 0;
+        return s;
+    }
+    HIP_TRY(c, hipMemcpyAsync(last_hidden, t->out, sizeof(float) * t->st.hidden, hipMemcpyDeviceToHost, c->stream));
+    return sync(c);
+}
+
 qtts_status qtts_build_trailing_text(qtts_talker *t, const uint32_t *text_tokens, int32_t n_text, float *rows,
                                      int32_t *n_rows) {
     if (!t || !rows || !n_rows || n_text < 0 || (n_text > 0 && !text_tokens)) return QTTS_EINVAL;
@@ -2267,11 +2318,19 @@ qtts_status qtts_build_trailing_text(qtts_talker *t, const uint32_t *text_tokens
     return QTTS_OK;
 }
 
-qtts_status qtts_generate_speech_codes(qtts_talker *t, qtts_predictor *p, const uint32_t *text_tokens, int32_t n_text,
-                                       uint32_t speaker_id, uint32_t language_id, const float *voice_embedding,
-                                       qtts_kv *talker_kv, qtts_kv *predictor_kv, const qtts_loop_params *params,
-                                       uint64_t seed, uint32_t *codes, int32_t *n_frames) {
-    if (!t || !talker_kv || !params || !codes || !n_frames) return QTTS_EINVAL;
+static qtts_status generate_codes_dev(qtts_talker *t, qtts_predictor *p, qtts_kv *talker_kv, qtts_kv *predictor_kv,
+                                      const float *last_hidden, const float *logits, int32_t position,
+                                      const float *trailing_text, int32_t trailing_len, const float *tts_pad_embed,
+                                      const qtts_loop_params *params, uint64_t seed, uint32_t *codes,
+                                      int32_t *n_frames);
+
+// generate_speech up to the codes (src/generate_new.rs:205-300).  With codes
+// NULL the codes stay in t->codes ([16][params->max_codes], frame-minor) only.
+static qtts_status speech_codes(qtts_talker *t, qtts_predictor *p, const uint32_t *text_tokens, int32_t n_text,
+                                uint32_t speaker_id, uint32_t language_id, const float *voice_embedding,
+                                qtts_kv *talker_kv, qtts_kv *predictor_kv, const qtts_loop_params *params,
+                                uint64_t seed, uint32_t *codes, int32_t *n_frames) {
+    if (!t || !talker_kv || !params || !n_frames) return QTTS_EINVAL;
     *n_frames = 0;
     const int H = t->st.hidden;
     std::vector<float> last_hidden(H), logits(t->vocab), pad(H);
@@ -2281,8 +2340,17 @@ qtts_status qtts_generate_speech_codes(qtts_talker *t, qtts_predictor *p, const 
                                        last_hidden.data(), logits.data(), &position));
     QTTS_TRY(qtts_build_trailing_text(t, text_tokens, n_text, trailing.data(), &rows));
     QTTS_TRY(qtts_embed_text_token(t, kTtsPad, pad.data()));
-    return qtts_generate_codes(t, p, talker_kv, predictor_kv, last_hidden.data(), logits.data(), position,
-                               trailing.data(), rows, pad.data(), params, seed, codes, n_frames);
+    return generate_codes_dev(t, p, talker_kv, predictor_kv, last_hidden.data(), logits.data(), position,
+                              trailing.data(), rows, pad.data(), params, seed, codes, n_frames);
+}
+
+qtts_status qtts_generate_speech_codes(qtts_talker *t, qtts_predictor *p, const uint32_t *text_tokens, int32_t n_text,
+                                       uint32_t speaker_id, uint32_t language_id, const float *voice_embedding,
+                                       qtts_kv *talker_kv, qtts_kv *predictor_kv, const qtts_loop_params *params,
+                                       uint64_t seed, uint32_t *codes, int32_t *n_frames) {
+    if (!codes) return QTTS_EINVAL;
+    return speech_codes(t, p, text_tokens, n_text, speaker_id, language_id, voice_embedding, talker_kv, predictor_kv,
+                        params, seed, codes, n_frames);
 }
 
 qtts_status qtts_forward_talker_decode(qtts_talker *t, uint32_t token_id, int32_t is_text, qtts_kv *kv,
@@ -2345,12 +2413,12 @@ qtts_status qtts_predictor_upload(qtts_ctx *c, const qtts_predictor_view *v, qtt
     if ((s = upload_array(c, p->own, v->final_norm_gamma, (size_t)hidden, &p->st.final_g, "final_norm_gamma")) !=
         QTTS_OK)
         return bail(s);
-    // generate_acoustic_codes restarts its cache every frame (positions
-    // 0..num_groups); predict_codes keeps appending, so the table covers 4096
-    // positions (qtts_predict_codes refuses later ones).  Rows past
-    // max_position skip the rotation as src/code_predictor.rs:107 does.
-    int rows = kPredictorRopeRows;
-    if (rows > v->max_position) rows = v->max_position;
+    // The whole table, as src/loader.rs:859-874 builds it (65536 rows for
+    // the 1.7B model, 32 MiB): generate_acoustic_codes only reaches
+    // positions 0..num_groups, but predict_codes keeps appending to its
+    // cache.  Positions past the table skip the rotation, as
+    // src/code_predictor.rs:107 does.
+    const int rows = v->max_position;
     p->max_pos = v->max_position;
     if (rows < 1) return bail(fail(c, QTTS_EINVAL, "max_position must be positive"));
     if ((s = upload_rope(c, p->own, v->head_dim, rows, v->rope_theta, v->rope_cos, v->rope_sin, &p->st)) != QTTS_OK) return bail(s);
@@ -2494,8 +2562,6 @@ qtts_status qtts_predict_codes(qtts_predictor *p, const float *talker_hidden, qt
     QTTS_TRY(check_kv(c, p->st, kv));
     const int offset = kv->len, H = p->st.hidden;
     if (offset + 1 > kv->cap) return fail(c, QTTS_ERANGE, "predictor cache full");
-    if (offset >= p->st.rope_rows && offset < p->max_pos)
-        return fail(c, QTTS_ERANGE, "predict_codes: position past the 4096-row RoPE table");
     const size_t nlog = (size_t)p->groups * p->vocab;
     QTTS_TRY(ensure_staging(c, 0, nlog));
     HIP_TRY(c, hipMemcpyAsync(p->in2, talker_hidden, sizeof(float) * p->talker_hidden, hipMemcpyHostToDevice,
@@ -2697,7 +2763,19 @@ qtts_status qtts_generate_codes(qtts_talker *t, qtts_predictor *p, qtts_kv *talk
                                 const float *last_hidden, const float *logits, int32_t position,
                                 const float *trailing_text, int32_t trailing_len, const float *tts_pad_embed,
                                 const qtts_loop_params *params, uint64_t seed, uint32_t *codes, int32_t *n_frames) {
-    if (!t || !last_hidden || !logits || !params || !codes || !n_frames) return QTTS_EINVAL;
+    if (!codes) return QTTS_EINVAL;
+    return generate_codes_dev(t, p, talker_kv, predictor_kv, last_hidden, logits, position, trailing_text,
+                              trailing_len, tts_pad_embed, params, seed, codes, n_frames);
+}
+
+// The frame loop of qtts_generate_codes; with codes NULL the codes stay in
+// t->codes ([16][params->max_codes], frame-minor) and are not copied out.
+static qtts_status generate_codes_dev(qtts_talker *t, qtts_predictor *p, qtts_kv *talker_kv, qtts_kv *predictor_kv,
+                                      const float *last_hidden, const float *logits, int32_t position,
+                                      const float *trailing_text, int32_t trailing_len, const float *tts_pad_embed,
+                                      const qtts_loop_params *params, uint64_t seed, uint32_t *codes,
+                                      int32_t *n_frames) {
+    if (!t || !last_hidden || !logits || !params || !n_frames) return QTTS_EINVAL;
     qtts_ctx *c = t->ctx;
     *n_frames = 0;
     const bool talker_only = params->talker_only || !p;
@@ -2821,7 +2899,7 @@ qtts_status qtts_generate_codes(qtts_talker *t, qtts_predictor *p, qtts_kv *talk
         QTTS_TRY(eng_status_check(c, "generate_codes"));
         EngState fin[2];
         HIP_TRY(c, hipMemcpy(fin, c->eng_state, sizeof(fin), hipMemcpyDeviceToHost));
-        HIP_TRY(c, hipMemcpy(codes, t->codes, ncodes * sizeof(uint32_t), hipMemcpyDeviceToHost));
+        if (codes) HIP_TRY(c, hipMemcpy(codes, t->codes, ncodes * sizeof(uint32_t), hipMemcpyDeviceToHost));
         const int nf = fin[0].frame > fin[1].frame ? fin[0].frame : fin[1].frame;
         *n_frames = nf;
         talker_kv->len += nf;
@@ -2881,7 +2959,7 @@ qtts_status qtts_generate_codes(qtts_talker *t, qtts_predictor *p, qtts_kv *talk
     // A failed loop (NaN logits: the reference panics) leaves the caches'
     // lengths and *n_frames as they were, as the frame engine does.
     if (fin.status != 0) return fail(c, (qtts_status)fin.status, "generate_codes: NaN logits (the reference panics)");
-    HIP_TRY(c, hipMemcpy(codes, t->codes, ncodes * sizeof(uint32_t), hipMemcpyDeviceToHost));
+    if (codes) HIP_TRY(c, hipMemcpy(codes, t->codes, ncodes * sizeof(uint32_t), hipMemcpyDeviceToHost));
     *n_frames = fin.frame;
     talker_kv->len += fin.frame;
     if (!talker_only && fin.frame > 0) predictor_kv->len = p->groups + 1;
@@ -3404,6 +3482,51 @@ qtts_status qtts_decode_to_audio(qtts_decoder *d, const uint32_t *codes, int32_t
     QTTS_TRY(dec_decode(d, d->codes, frames, frames, d->audio, need, n_samples));
     HIP_TRY(c, hipMemcpyAsync(audio, d->audio, (size_t)*n_samples * sizeof(float), hipMemcpyDeviceToHost, c->stream));
     return sync(c);
+}
+
+qtts_status qtts_generate_speech(qtts_talker *t, qtts_predictor *p, qtts_decoder *d, const uint32_t *text_tokens,
+                                 int32_t n_text, uint32_t speaker_id, uint32_t language_id,
+                                 const float *voice_embedding, qtts_kv *talker_kv, qtts_kv *predictor_kv,
+                                 const qtts_loop_params *params, uint64_t seed, float *audio, int64_t capacity,
+                                 int64_t *n_samples, int32_t *n_frames) {
+    if (!t || !d || !params || !n_samples || !n_frames) return QTTS_EINVAL;
+    *n_samples = 0;
+    *n_frames = 0;
+    qtts_ctx *c = t->ctx, *dc = d->ctx;
+    if (dc->device != c->device) return fail(c, QTTS_EINVAL, "the decoder is on another device than the talker");
+    if (d->w.num_rest + 1 > 16) return fail(c, QTTS_ESHAPE, "the decoder reads more than a frame's 16 code groups");
+    const int max_codes = params->max_codes > 0 ? params->max_codes : 0;
+    const int64_t most = qtts_decoder_num_samples(d, max_codes);
+    if (most > 0 && !audio) return QTTS_EINVAL;
+    if (most > capacity) return fail(c, QTTS_ERANGE, "audio buffer smaller than max_codes frames decode to");
+    int32_t nf = 0;
+    QTTS_TRY(speech_codes(t, p, text_tokens, n_text, speaker_id, language_id, voice_embedding, talker_kv, predictor_kv,
+                          params, seed, nullptr, &nf));
+    *n_frames = nf;
+    if (nf == 0) return QTTS_OK;
+    // decode_to_audio (src/generate_new.rs:304-306) of the codes where the
+    // frame loop left them: t->codes, [16][max_codes], complete (the loop
+    // ends with its stream synchronised).
+    const int64_t need = qtts_decoder_num_samples(d, nf);
+    if (d->audio_cap < (size_t)need) {
+        (void)hipFree(d->audio);
+        d->audio = nullptr;
+        d->audio_cap = 0;
+        HIP_TRY(dc, hipMalloc(&d->audio, (size_t)need * sizeof(float)));
+        d->audio_cap = (size_t)need;
+    }
+    HIP_TRY(dc, hipMemsetAsync(d->status, 0, sizeof(int), dc->stream));
+    int64_t n = 0;
+    QTTS_TRY(dec_decode(d, t->codes, nf, max_codes, d->audio, need, &n));
+    int bad = 0;
+    HIP_TRY(dc, hipMemcpyAsync(&bad, d->status, sizeof(int), hipMemcpyDeviceToHost, dc->stream));
+    HIP_TRY(dc, hipMemcpyAsync(audio, d->audio, (size_t)n * sizeof(float), hipMemcpyDeviceToHost, dc->stream));
+    QTTS_TRY(sync(dc));
+    // a semantic code past the decoder's codebook: the reference's lookup
+    // (src/decoder.rs:151-152) would index past the table and panic
+    if (bad) return fail(c, QTTS_ERANGE, "a generated code is beyond the decoder's codebook");
+    *n_samples = n;
+    return QTTS_OK;
 }
 
 }  // extern "C"

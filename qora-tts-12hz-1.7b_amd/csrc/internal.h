@@ -354,6 +354,10 @@ constexpr int kTopKMaxVocab = 4096;
 void launch_sample_top_k(hipStream_t st, const TopKParams &p);
 void launch_embed_rows(hipStream_t st, const DevQ4 &w, const uint32_t *tok, long long tok_stride, int rows, float *out,
                        long long out_stride);
+// prefill_talker's rows: out[r] = text[slot[r]] if slot[r] >= 0, else the
+// codec embedding of tok[r] (rows x H, H == w.N).
+void launch_token_rows(hipStream_t st, const DevQ4 &w, const uint32_t *tok, const int *slot, const float *text,
+                       int rows, float *out, int H);
 void launch_argmax_rows(hipStream_t st, const float *logits, int rows, int n, uint32_t *out, long long out_stride,
                         int *status, long long status_stride, const float *table = nullptr, int table_rows = 0,
                         int width = 0, float *rows_out = nullptr, long long rows_ld = 0);

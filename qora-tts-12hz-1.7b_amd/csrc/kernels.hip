@@ -1540,6 +1540,22 @@ void launch_embed_rows(hipStream_t st, const DevQ4 &w, const uint32_t *tok, long
                        tok_stride, out, out_stride);
 }
 
+// The rows of prefill_talker (src/talker.rs:475-484): row r is text row
+// slot[r] (already projected) when slot[r] >= 0, else the codec embedding
+// row of tok[r] (ids checked on the host).
+__global__ void k_token_rows(DevQ4 w, const uint32_t *tok, const int *slot, const float *text, float *out, int H) {
+    const int j = blockIdx.x * blockDim.x + threadIdx.x, r = blockIdx.y;
+    if (j >= H) return;
+    const int s = slot[r];
+    out[(size_t)r * H + j] = s >= 0 ? text[(size_t)s * H + j] : q4_element(w, tok[r], j);
+}
+
+void launch_token_rows(hipStream_t st, const DevQ4 &w, const uint32_t *tok, const int *slot, const float *text,
+                       int rows, float *out, int H) {
+    hipLaunchKernelGGL(k_token_rows, dim3((unsigned)((H + 255) / 256), (unsigned)rows), dim3(256), 0, st, w, tok, slot,
+                       text, out, H);
+}
+
 // sample_argmax (src/code_predictor.rs:328-334) of each row: the last index
 // of the maximum; a NaN sets *status (per row) to QTTS_ENAN and gives 0.
 // With a table, the row also copies table[code] (width floats; zeros past

@@ -289,6 +289,9 @@ def load_library(path: str = LIB_PATH):
         "qtts_decoder_num_samples": ([vp, i32], C.c_int64),
         "qtts_decode_to_audio": ([vp, vp, i32, i32, f32p, C.c_int64, C.POINTER(C.c_int64)], i32),
         "qtts_decode_to_audio_device": ([vp, vp, i32, i32, vp, C.c_int64, C.POINTER(C.c_int64)], i32),
+        "qtts_prefill_talker": ([vp, vp, vp, i32, vp, f32p], i32),
+        "qtts_generate_speech": ([vp, vp, vp, vp, i32, u32, u32, vp, vp, vp, C.POINTER(LoopParams), C.c_uint64, f32p,
+                                  C.c_int64, C.POINTER(C.c_int64), C.POINTER(i32)], i32),
     }
     for name, (args, res) in sig.items():
         fn = getattr(lib, name)
@@ -316,7 +319,7 @@ def exported_symbols() -> List[str]:
         "qtts_quantize_f32_to_q4", "qtts_generate_codes_batch", "qtts_model_file_open", "qtts_model_file_error", "qtts_model_file_close",
         "qtts_model_file_talker", "qtts_model_file_predictor", "qtts_model_file_text", "qtts_model_file_info",
         "qtts_model_file_decoder", "qtts_decoder_upload", "qtts_decoder_free", "qtts_decoder_num_samples",
-        "qtts_decode_to_audio", "qtts_decode_to_audio_device",
+        "qtts_decode_to_audio", "qtts_decode_to_audio_device", "qtts_prefill_talker", "qtts_generate_speech",
     ]
 
 
@@ -971,6 +974,17 @@ class Talker(_DeviceObject):
         self.ctx.check(self.ctx.lib.qtts_prefill_talker_raw(self.h, _ptr(x), seq_len, kv.h, _ptr(out)))
         return out
 
+    # prefill_talker, src/talker.rs:467-488: (token, is_text) rows
+    def prefill_talker(self, tokens, is_text, kv: KvCache) -> np.ndarray:
+        t = np.ascontiguousarray(tokens, dtype=np.uint32)
+        f = np.ascontiguousarray(np.asarray(is_text, dtype=bool), dtype=np.int32)
+        if t.shape != f.shape:
+            raise ValueError("tokens and is_text differ in length")
+        out = np.empty(self.cfg.hidden, dtype=np.float32)
+        self.ctx.check(self.ctx.lib.qtts_prefill_talker(self.h, _ptr(t) if t.size else None,
+                                                        _ptr(f) if f.size else None, t.size, kv.h, _ptr(out)))
+        return out
+
     # apply_codec_head, src/talker.rs:627-629
     def apply_codec_head(self, hidden) -> np.ndarray:
         hs = _f32(hidden, self.cfg.hidden)
@@ -1104,6 +1118,25 @@ def generate_codes(talker: Talker, predictor: Optional[CodePredictor], talker_kv
                                           position, _ptr(tt), tl, _ptr(pad), C.byref(params), seed, _ptr(codes),
                                           C.byref(n)))
     return codes[:, : n.value].copy()
+
+
+def generate_speech(talker: Talker, predictor: Optional[CodePredictor], decoder: SpeechDecoder, text_tokens,
+                    speaker_id: int, language_id: int, talker_kv: KvCache, predictor_kv: Optional[KvCache],
+                    params: LoopParams, seed: int, voice_embedding=None):
+    """generate_speech (src/generate_new.rs:191-311) from token ids to audio in
+    one call; the codes stay in device memory between the frame loop and the
+    decoder.  Returns (audio float32, n_frames)."""
+    ctx = talker.ctx
+    tok = np.ascontiguousarray(text_tokens, dtype=np.uint32)
+    voice = None if voice_embedding is None else _f32(voice_embedding, talker.cfg.hidden)
+    out = np.empty(max(1, decoder.num_samples(max(params.max_codes, 0))), dtype=np.float32)
+    n, nf = C.c_int64(0), C.c_int32(0)
+    ctx.check(ctx.lib.qtts_generate_speech(talker.h, predictor.h if predictor is not None else None, decoder.h,
+                                           _ptr(tok) if tok.size else None, tok.size, speaker_id, language_id,
+                                           _ptr(voice), talker_kv.h,
+                                           predictor_kv.h if predictor_kv is not None else None, C.byref(params),
+                                           seed, _ptr(out), out.size, C.byref(n), C.byref(nf)))
+    return out[: n.value].copy(), nf.value
 
 
 def generate_speech_codes(talker: Talker, predictor: Optional[CodePredictor], text_tokens, speaker_id: int,

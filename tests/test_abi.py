@@ -41,6 +41,9 @@ def test_null_arguments_are_rejected():
     assert lib.qtts_forward_with_embedding(None, None, None, 0, None) == qtts.QTTS_EINVAL
     assert lib.qtts_sample_token(None, None, 0, None, None, 0, None, None) == qtts.QTTS_EINVAL
     assert lib.qtts_kv_len(None) == -1
+    assert lib.qtts_prefill_talker(None, None, None, 1, None, None) == qtts.QTTS_EINVAL
+    assert lib.qtts_generate_speech(None, None, None, None, 0, 0, 0, None, None, None, None, 0, None, 0, None,
+                                    None) == qtts.QTTS_EINVAL
     # the read-floor aid refuses a null buffer, a size off the 16-byte grid
     # and an unaligned buffer before any device work
     assert lib.qtts_stream_read_device(None, 16, None) == -1

@@ -2,11 +2,14 @@
 sample_top_k (src/generate.rs:50-84) on the device, predict_codes
 (src/code_predictor.rs:126-213) appending to a persistent predictor cache,
 and forward_talker_decode (src/talker.rs:161-258) fed codec and text tokens,
-on small models and at the 1.7B shapes.
+on small models and at the 1.7B shapes; predict_codes past row 4096 of the
+65536-row RoPE table and past the end of an 8-row one.
 
 Bars: tokens and rng states identical (tie-free logits: the reference leaves
 the order of equal logits unspecified); hidden states, logits and cache rows
 within 1e-3 relative (the GEMVs sum in another order than the oracle's)."""
+import dataclasses
+
 import numpy as np
 import pytest
 
@@ -118,18 +121,43 @@ def test_predict_codes_limits(small):
     with pytest.raises(qtts.QttsError) as e:
         p.predict_codes(h, kv)
     assert e.value.status == qtts.QTTS_ERANGE and len(kv) == 2
+
+
+@pytest.mark.parametrize("offset", [4095, 4096, 5000])
+def test_predict_codes_whole_rope_table(small, offset):
+    """The device table holds all max_position = 65536 rows
+    (src/loader.rs:859-874): offsets past 4096 rotate like the oracle's."""
+    t, p, ot, op, ox = small
     c = PREDICTOR
-    big, obig = p.new_kv(4100), op.new_kv(4100)
-    z = qtts.synth_normal_f32(65, "legacy.kv", c.layers * 4096 * c.kv_heads * c.head_dim).reshape(
-        c.layers, 4096, c.kv_heads, c.head_dim)
-    big.load(z, z, 4096)
-    with pytest.raises(qtts.QttsError) as e:  # past the 4096-row RoPE table
-        p.predict_codes(h, big)
-    assert e.value.status == qtts.QTTS_ERANGE and len(big) == 4096
-    # the last row the table covers, after 4095 rows of history
-    big.load(z[:, :4095], z[:, :4095], 4095)
-    obig.load(z[:, :4095], z[:, :4095], 4095)
-    assert within(p.predict_codes(h, big), op.predict_codes(h, obig))
+    h = qtts.synth_normal_f32(64, "legacy.th", TALKER.hidden)
+    kv, okv = p.new_kv(offset + 1), op.new_kv(offset + 1)
+    z = qtts.synth_normal_f32(65, "legacy.kv", c.layers * offset * c.kv_heads * c.head_dim).reshape(
+        c.layers, offset, c.kv_heads, c.head_dim)
+    kv.load(z, z, offset)
+    okv.load(z, z, offset)
+    got, ref = p.predict_codes(h, kv), op.predict_codes(h, okv)
+    print(f"predict_codes at offset {offset}: rel err {rel_err(got, ref):.2e}")
+    assert within(got, ref) and len(kv) == offset + 1
+    (gk, gv), (rk, rv) = kv.store(), okv.store()
+    assert within(gk[:, offset], rk[:, offset]) and within(gv[:, offset], rv[:, offset])
+
+
+def test_predict_codes_skip_past_table(ctx):
+    """A predictor with an 8-row table: offsets 8 and 9 skip the rotation
+    (src/code_predictor.rs:105-107), offset 7 rotates; as the oracle does."""
+    c = dataclasses.replace(PREDICTOR, max_position=8)
+    pw = qtts.CodePredictorWeights(66, c, talker_hidden=TALKER.hidden)
+    p, op = qtts.CodePredictor(ctx, pw), oracle.CodePredictor(pw, nthreads=1)
+    z = qtts.synth_normal_f32(67, "legacy.kv", c.layers * 7 * c.kv_heads * c.head_dim).reshape(
+        c.layers, 7, c.kv_heads, c.head_dim)
+    kv, okv = p.new_kv(10), op.new_kv(10)
+    kv.load(z, z, 7)
+    okv.load(z, z, 7)
+    for offset in (7, 8, 9):
+        h = qtts.synth_normal_f32(68 + offset, "legacy.th", TALKER.hidden)
+        assert within(p.predict_codes(h, kv), op.predict_codes(h, okv)), offset
+    (gk, gv), (rk, rv) = kv.store(), okv.store()
+    assert within(gk, rk) and within(gv, rv)
 
 
 @pytest.mark.timeout(600)

@@ -7,8 +7,11 @@ last maximum, top-k truncation, the sorted-order inverse CDF, the k-th-entry
 fallback at r == 1.0, the rng advancing only when sampling) and by the
 empirical distribution of many draws against softmax(l / T) over the top k.
 predict_codes is pinned against the float64 numpy model (tests/numpy_model.py)
-over three appended steps, forward_talker_decode against the exact
+over three appended steps, at offsets past row 4096 of its 65536-row table,
+and past the end of a short table (no rotation); forward_talker_decode against the exact
 composition embed_*_token -> forward_with_embedding and the float64 model."""
+import dataclasses
+
 import numpy as np
 import pytest
 
@@ -167,7 +170,7 @@ def test_predict_codes_appends_vs_float64(tiny):
         assert rel_err(got, ref) < 1e-5, i
 
 
-def test_predict_codes_cache_and_rope_limits(tiny):
+def test_predict_codes_cache_limit(tiny):
     _, pw, _, _, op, _ = tiny
     kv = op.new_kv(2)
     h = qtts.synth_normal_f32(47, "legacy.th", TINY_TALKER.hidden)
@@ -176,16 +179,62 @@ def test_predict_codes_cache_and_rope_limits(tiny):
     with pytest.raises(oracle.OracleError) as e:
         op.predict_codes(h, kv)
     assert e.value.status == qtts.QTTS_ERANGE and len(kv) == 2
-    # offset 4096 is past the 4096-row RoPE table but inside max_position
+
+
+def _history(cfg, rows, seed):
+    """rows of seeded K/V history [layers][rows][kv_heads][head_dim] and the
+    float64 cache of the same values."""
+    k = qtts.synth_normal_f32(seed, "legacy.k", cfg.layers * rows * cfg.kv_heads * cfg.head_dim).reshape(
+        cfg.layers, rows, cfg.kv_heads, cfg.head_dim)
+    v = qtts.synth_normal_f32(seed, "legacy.v", k.size).reshape(k.shape)
+    return k, v, [(k[i].astype(np.float64), v[i].astype(np.float64)) for i in range(cfg.layers)]
+
+
+@pytest.mark.parametrize("offset", [4095, 4096, 5000])
+def test_predict_codes_whole_rope_table(tiny, offset):
+    """The table covers max_position rows (65536, src/loader.rs:859-874), so
+    offsets past 4096 rotate too: the oracle against the float64 model, whose
+    angles come from the formula directly."""
+    _, pw, _, _, op, _ = tiny
     c = TINY_PREDICTOR
-    big = op.new_kv(4100)
-    z = np.zeros((c.layers, 4096, c.kv_heads, c.head_dim), np.float32)
-    big.load(z, z, 4096)
-    with pytest.raises(oracle.OracleError) as e:
-        op.predict_codes(h, big)
-    assert e.value.status == qtts.QTTS_ERANGE and len(big) == 4096
-    big.load(z[:, :4095], z[:, :4095], 4095)
-    assert op.predict_codes(h, big).shape == (pw.num_groups, c.vocab) and len(big) == 4096
+    assert c.max_position == 65536
+    k, v, cache = _history(c, offset, 48)
+    kv = op.new_kv(offset + 1)
+    kv.load(k, v, offset)
+    h = qtts.synth_normal_f32(49, "legacy.th", TINY_TALKER.hidden)
+    got = op.predict_codes(h, kv)
+    model = nm.PredictorModel(pw)
+    normed = nm.rms_norm(model.stack.step(model.project(h), cache, offset), model.final)
+    ref = np.stack([normed @ hd for hd in model.heads])
+    assert len(kv) == offset + 1 and rel_err(got, ref) < 1e-5
+
+
+def test_predict_codes_skip_past_table(monkeypatch):
+    """A predictor whose table has 8 rows: offsets 8 and 9 skip the rotation
+    (src/code_predictor.rs:105-107) and offset 7 still rotates; the float64
+    model with its rotation switched off at those offsets."""
+    c = dataclasses.replace(TINY_PREDICTOR, max_position=8)
+    pw = qtts.CodePredictorWeights(51, c, talker_hidden=TINY_TALKER.hidden)
+    op = oracle.CodePredictor(pw, nthreads=1)
+    model = nm.PredictorModel(pw)
+    rotate = nm.rope
+    monkeypatch.setattr(nm, "rope", lambda x, pos, theta: x if pos >= 8 else rotate(x, pos, theta))
+    k, v, _ = _history(c, 7, 52)
+    kv = op.new_kv(10)
+    kv.load(k, v, 7)
+    cache = [(k[i].astype(np.float64), v[i].astype(np.float64)) for i in range(c.layers)]
+    for offset in (7, 8, 9):
+        h = qtts.synth_normal_f32(53 + offset, "legacy.th", TINY_TALKER.hidden)
+        got = op.predict_codes(h, kv)
+        normed = nm.rms_norm(model.stack.step(model.project(h), cache, offset), model.final)
+        ref = np.stack([normed @ hd for hd in model.heads])
+        assert rel_err(got, ref) < 1e-5, offset
+    # and the skip is visible: rotating offset 9 instead moves the result
+    monkeypatch.setattr(nm, "rope", rotate)
+    cache2 = [(a[:9], b[:9]) for a, b in cache]
+    h = qtts.synth_normal_f32(62, "legacy.th", TINY_TALKER.hidden)
+    normed = nm.rms_norm(model.stack.step(model.project(h), cache2, 9), model.final)
+    assert rel_err(got, np.stack([normed @ hd for hd in model.heads])) > 1e-3
 
 
 # ---------------------------------------------------------------- forward_talker_decode

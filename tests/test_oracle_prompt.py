@@ -127,6 +127,45 @@ def test_generate_speech_codes_composition(model, voice):
     assert np.array_equal(got, ref)
 
 
+@pytest.mark.parametrize("n", [1, 6, 13])
+def test_prefill_talker_composition(model, n):
+    """prefill_talker (src/talker.rs:467-488): row i from embed_text_token or
+    embed_codec_token by its flag, in sequence order, then prefill_talker_raw;
+    bit for bit, caches included (a swapped flag or row changes the bits)."""
+    tw, pw, text, ot, op, ox = model
+    rng = np.random.default_rng(n)
+    is_text = rng.integers(0, 2, n).astype(bool)
+    is_text[0] = True
+    tokens = np.where(is_text, rng.integers(0, qtts.TEXT_VOCAB_1P7B, n), rng.integers(0, TALKER.vocab, n))
+    tokens = tokens.astype(np.uint32)
+    kv, kv2 = ot.new_kv(16), ot.new_kv(16)
+    got = oracle.prefill_talker(ot, ox, tokens, is_text, kv)
+    rows = np.stack([ox.embed_text_token(t) if f else ot.embed_codec_token(t) for t, f in zip(tokens, is_text)])
+    ref = ot.prefill_talker_raw(rows, n, kv2)
+    assert np.array_equal(got, ref) and len(kv) == len(kv2) == n
+    (a, b), (c, d) = kv.store(), kv2.store()
+    assert np.array_equal(a, c) and np.array_equal(b, d)
+    if n > 1:  # the flags matter: all-codec rows of the same ids differ
+        assert not np.array_equal(oracle.prefill_talker(ot, None, tokens % TALKER.vocab, np.zeros(n, bool),
+                                                        ot.new_kv(16)), got)
+
+
+def test_prefill_talker_errors(model):
+    _, _, _, ot, _, ox = model
+    kv = ot.new_kv(8)
+    cases = (([TALKER.vocab], [False], qtts.QTTS_ERANGE), ([qtts.TEXT_VOCAB_1P7B], [True], qtts.QTTS_ERANGE),
+             ([], [], qtts.QTTS_EINVAL))
+    for toks, flags, status in cases:
+        with pytest.raises(oracle.OracleError) as e:
+            oracle.prefill_talker(ot, ox, toks, flags, kv)
+        assert e.value.status == status and len(kv) == 0
+    with pytest.raises(oracle.OracleError) as e:  # a text row and no text weights
+        oracle.prefill_talker(ot, None, [5, 9707], [False, True], kv)
+    assert e.value.status == qtts.QTTS_ESTATE and len(kv) == 0
+    oracle.prefill_talker(ot, None, [5, 2148], [False, False], kv)
+    assert len(kv) == 2
+
+
 def test_codec_token_range(model):
     _, _, _, ot, _, ox = model
     with pytest.raises(oracle.OracleError) as e:
