@@ -127,7 +127,10 @@ __device__ __forceinline__ void reset_dev(unsigned *ctr) {
     __hip_atomic_store(glb(ctr), 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 // Waits until this wave's earlier memory operations have completed.
-__device__ __forceinline__ void wait_stores() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup"); }
+// Waits until every memory operation this wave issued has completed (its
+// stores acknowledged), so a later store that other blocks poll is ordered
+// after them.  (A workgroup-scope release fence emits no wait on gfx950.)
+__device__ __forceinline__ void wait_stores() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
 // xorshift64 (13, 7, 17) and (state as f32) / (u64::MAX as f32), both
 // conversions rounding to nearest (src/generate_new.rs:17-22).
