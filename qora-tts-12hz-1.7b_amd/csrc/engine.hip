@@ -17,26 +17,34 @@ constexpr uint32_t kSpinLimit = 1u << 23;
 // past the limit, marks itself bad and keeps executing the task with zeros
 // (so every block barrier is still reached); the block leaves at the end of
 // the task.
+// TR: the traced kernel (QTTS_ENGINE_TRACE); the production kernel has no
+// stamps, branches or trace pointer in its ops (they cost it ~4 %).
+template <bool TR>
 struct Ctl {
+    static constexpr bool kTrace = TR;
     int *done;
     int *status;
     uint32_t spins;
     bool bad;
-    uint64_t *tr;  // trace slots of this (op, block), or null
+    uint64_t *tr;  // trace slots of this (op, block), or null (TR only)
 };
 
 // Trace stamp k (2..7) of the current task, thread 0 only.
-__device__ __forceinline__ void stamp(const Ctl &c, int k) {
-    if (c.tr && threadIdx.x == 0) glb(c.tr)[k] = wall_clock64();
+template <class CT>
+__device__ __forceinline__ void stamp(const CT &c, int k) {
+    if constexpr (CT::kTrace)
+        if (c.tr && threadIdx.x == 0) glb(c.tr)[k] = wall_clock64();
 }
 
-__device__ __forceinline__ void fail_dev(Ctl &c, int code) {
+template <class CT>
+__device__ __forceinline__ void fail_dev(CT &c, int code) {
     st_dev_i32(c.status, code);
     st_dev_i32(c.done, 1);
     c.bad = true;
 }
 
-__device__ __forceinline__ bool must_stop(Ctl &c) {
+template <class CT>
+__device__ __forceinline__ bool must_stop(CT &c) {
     if (c.bad) return true;
     if ((++c.spins & 127u) == 0u) {
         if (ld_dev_i32(c.done)) {
@@ -51,7 +59,8 @@ __device__ __forceinline__ bool must_stop(Ctl &c) {
     return false;
 }
 
-__device__ __forceinline__ float wait_tv(const tv_t *p, uint32_t tag, Ctl &c) {
+template <class CT>
+__device__ __forceinline__ float wait_tv(const tv_t *p, uint32_t tag, CT &c) {
     uint64_t v = ld_dev_u64(p);
     while ((uint32_t)(v >> 32) != tag) {
         if (must_stop(c)) return 0.0f;
@@ -63,9 +72,9 @@ __device__ __forceinline__ float wait_tv(const tv_t *p, uint32_t tag, Ctl &c) {
 
 // Waits for `count` (<= N) words base[i*stride]: all loads are issued
 // before any tag is checked, then only the stale ones are re-read.
-template <int N>
+template <int N, class CT>
 __device__ __forceinline__ void wait_strided(const tv_t *base, size_t stride, int count, uint32_t tag, float (&out)[N],
-                                             Ctl &c) {
+                                             CT &c) {
     uint64_t v[N];
 #pragma unroll
     for (int i = 0; i < N; i++) v[i] = i < count ? ld_dev_u64(base + i * stride) : ((uint64_t)tag << 32);
@@ -84,9 +93,9 @@ __device__ __forceinline__ void wait_strided(const tv_t *base, size_t stride, in
 
 // out[i] = a[i*stride] + b[i*stride] for i < count (<= N), one tag: all 2N
 // loads are issued before any tag is checked.
-template <int N>
+template <int N, class CT>
 __device__ __forceinline__ void wait_pair(const tv_t *a, const tv_t *b, size_t stride, int count, uint32_t tag,
-                                          float (&out)[N], Ctl &c) {
+                                          float (&out)[N], CT &c) {
     uint64_t va[N], vb[N];
 #pragma unroll
     for (int i = 0; i < N; i++) {
@@ -110,9 +119,9 @@ __device__ __forceinline__ void wait_pair(const tv_t *a, const tv_t *b, size_t s
 }
 
 // Same for a list of words with their own tags.
-template <int N>
+template <int N, class CT>
 __device__ __forceinline__ void wait_list(const tv_t *const (&p)[N], const uint32_t (&tag)[N], int count,
-                                          float (&out)[N], Ctl &c) {
+                                          float (&out)[N], CT &c) {
     uint64_t v[N];
 #pragma unroll
     for (int i = 0; i < N; i++) v[i] = i < count ? ld_dev_u64(p[i]) : ((uint64_t)tag[i] << 32);
@@ -129,7 +138,8 @@ __device__ __forceinline__ void wait_list(const tv_t *const (&p)[N], const uint3
     for (int i = 0; i < N; i++) out[i] = __uint_as_float((uint32_t)v[i]);
 }
 
-__device__ __forceinline__ uint32_t wait_tv_u32(const tv_t *p, uint32_t tag, Ctl &c) {
+template <class CT>
+__device__ __forceinline__ uint32_t wait_tv_u32(const tv_t *p, uint32_t tag, CT &c) {
     return __float_as_uint(wait_tv(p, tag, c));
 }
 
@@ -159,8 +169,8 @@ __device__ __forceinline__ float waves_sum(const float *v, int stride) {
 // value is NaN).  Every thread gets the result; *anynan says whether any
 // logit was NaN.  scr: 2 * kEngWaves words of LDS that no thread touches
 // again before the next block barrier.
-template <int NA>
-__device__ __forceinline__ int block_argmax(const tv_t *logits, int n, uint32_t tag, Ctl &c, float *scr, int *anynan) {
+template <int NA, class CT>
+__device__ __forceinline__ int block_argmax(const tv_t *logits, int n, uint32_t tag, CT &c, float *scr, int *anynan) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float bv = -INFINITY;
     int bi = -1, nan = 0;
@@ -213,8 +223,8 @@ __device__ __forceinline__ int block_argmax(const tv_t *logits, int n, uint32_t 
 // within one task per block, so every GEMV spreads over the whole grid.
 // Same arithmetic as k_gemv: acc += (scale * x) * nib - 8 * (scale * x), f32.
 // ---------------------------------------------------------------------------
-template <int M, int NP, int C, int R>
-__device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint32_t tb, Ctl &c, float *smem, int row) {
+template <int M, int NP, int C, int R, class CT>
+__device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint32_t tb, CT &c, float *smem, int row) {
     constexpr int DW = q4_slice_dwords<C>();
     float *red = smem;                          // [NP][M][kEngWaves][C]
     float *scr = red + NP * M * kEngWaves * C;  // [M][kEngWaves] per-wave sums of squares
@@ -570,8 +580,8 @@ __device__ __forceinline__ int eng_gemv(const KCONST EngGemv &g, int task, uint3
     return col0;
 }
 
-template <int M, int NP>
-__device__ __forceinline__ int eng_gemv_cols(const KCONST EngGemv &g, int task, uint32_t tb, Ctl &c, float *smem, int row) {
+template <int M, int NP, class CT>
+__device__ __forceinline__ int eng_gemv_cols(const KCONST EngGemv &g, int task, uint32_t tb, CT &c, float *smem, int row) {
     // Whole 32-column panels: narrower slices spread an op over more blocks
     // but leave fewer blocks idle to run ahead into the next op (issuing its
     // weight loads early), which costs more than the shorter accumulation
@@ -592,8 +602,8 @@ __device__ __forceinline__ int eng_gemv_cols(const KCONST EngGemv &g, int task, 
 // NPI: (row, head) pairs rounded up; KJ: positions per thread held in
 // registers for the scores (16 lanes each, NSLOT = kEngThreads / 16 positions
 // at a time) -- a register batch covers PB = NSLOT * KJ positions.
-template <int NPI, int KJ>
-__device__ __forceinline__ int eng_attn_t(const KCONST EngAttn &a, int task, uint32_t tb, const EngState &st, Ctl &c,
+template <int NPI, int KJ, class CT>
+__device__ __forceinline__ int eng_attn_t(const KCONST EngAttn &a, int task, uint32_t tb, const EngState &st, CT &c,
                                           float *smem) {
     constexpr int HD = 128, HALF = 64, CH = 256;
     constexpr int NSLOT = kEngThreads / 16;  // positions per score round (16 lanes each)
@@ -914,7 +924,8 @@ __device__ __forceinline__ int eng_attn_t(const KCONST EngAttn &a, int task, uin
 // the end (src/talker.rs:304-331), causal across the M new rows.  The rows
 // are also written to the device cache, for the host.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ int eng_attn_lean(const KCONST EngAttn &a, int task, uint32_t tb, Ctl &c, float *smem,
+template <class CT>
+__device__ __forceinline__ int eng_attn_lean(const KCONST EngAttn &a, int task, uint32_t tb, CT &c, float *smem,
                                              float *kvl) {
     constexpr int HD = 128, HALF = 64, NP = kEngLdsKvPos;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -1073,7 +1084,8 @@ __device__ __forceinline__ int eng_attn_lean(const KCONST EngAttn &a, int task, 
     return task;
 }
 
-__device__ __forceinline__ int eng_attn(const KCONST EngAttn &a, int task, uint32_t tb, const EngState &st, Ctl &c,
+template <class CT>
+__device__ __forceinline__ int eng_attn(const KCONST EngAttn &a, int task, uint32_t tb, const EngState &st, CT &c,
                                         float *smem, float *kvl) {
     if (a.lds_kv) return eng_attn_lean(a, task, tb, c, smem, kvl);
     const int npi = a.M * (a.nq / a.nkv);
@@ -1094,7 +1106,8 @@ __device__ __forceinline__ int eng_attn(const KCONST EngAttn &a, int task, uint3
 // kEngMaxSplit / 4) while threads 0.. also load the splits' (max, sum): one
 // round trip for all of it.  The quarters' weighted sums are added in
 // quarter order (a fixed order: the result does not depend on timing).
-__device__ __forceinline__ int eng_combine(const KCONST EngCombine &cb, int task, uint32_t tb, Ctl &c, float *smem) {
+template <class CT>
+__device__ __forceinline__ int eng_combine(const KCONST EngCombine &cb, int task, uint32_t tb, CT &c, float *smem) {
     constexpr int HD = 128, NQ = kEngThreads / HD, NS = kEngMaxSplit / NQ;
     static_assert(kEngThreads % HD == 0 && kEngMaxSplit % NQ == 0, "combine layout");
     const int m = task / cb.nq, h = task - m * cb.nq;
@@ -1148,7 +1161,8 @@ __device__ __forceinline__ int eng_combine(const KCONST EngCombine &cb, int task
 }
 
 // The argmax step: files the code and publishes it as a tagged integer.
-__device__ __forceinline__ void eng_argmax(const KCONST EngArgmax &a, uint32_t tb, const EngState &st, Ctl &c, uint32_t *codes,
+template <class CT>
+__device__ __forceinline__ void eng_argmax(const KCONST EngArgmax &a, uint32_t tb, const EngState &st, CT &c, uint32_t *codes,
                            int max_codes, float *smem) {
     int anynan = 0;
     const int ix = block_argmax<4096 / kEngThreads>(a.logits, a.n, tb + a.logits_tag, c, smem, &anynan);  // n <= 4096
@@ -1217,7 +1231,8 @@ __device__ int block_exscan(int v, int *wsum, int *total) {
 // sample_token (src/generate_new.rs:329-391), same schedule as k_sample:
 // the three order-dependent f32 sums on one lane in index order, the rest
 // in parallel; the stable top-k by radix select over the float bits.
-__device__ __forceinline__ void eng_sample(const KCONST EngSample &P, uint32_t tb, const EngState &st, EngState *st_out, Ctl &c,
+template <class CT>
+__device__ __forceinline__ void eng_sample(const KCONST EngSample &P, uint32_t tb, const EngState &st, EngState *st_out, CT &c,
                            uint32_t *codes, int max_codes, float *smem) {
     const int V = P.vocab, tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     float *s = smem;
@@ -1471,7 +1486,8 @@ __device__ __forceinline__ void eng_sample(const KCONST EngSample &P, uint32_t t
 }
 
 // Next talker input (src/generate_new.rs:270-286), kEngThreads columns per task.
-__device__ __forceinline__ int eng_embsum(const KCONST EngEmbSum &E, int task, uint32_t tb, const EngState &st, Ctl &c) {
+template <class CT>
+__device__ __forceinline__ int eng_embsum(const KCONST EngEmbSum &E, int task, uint32_t tb, const EngState &st, CT &c) {
     const int j = task * kEngThreads + threadIdx.x;
     if (E.mode == 2) {  // publish a plain row (host input) as a tagged vector
         if (j < E.hidden) put_tv(&E.out[j], ld_dev(&E.pad[j]), tb + E.out_tag);
@@ -1523,6 +1539,7 @@ __device__ __forceinline__ void touch_desc(const KCONST EngOp *op) {
 
 }  // namespace
 
+template <bool TR>
 __global__ __launch_bounds__(kEngThreads) void k_engine(EngArgs A) {
     __shared__ __align__(16) float smem[kEngSmemFloats];
     __shared__ __align__(16) float kvl[2 * kEngLdsKvPos * 128];  // lds_kv attention: this block's K/V rows
@@ -1530,7 +1547,7 @@ __global__ __launch_bounds__(kEngThreads) void k_engine(EngArgs A) {
     if (ld_dev_i32(A.done)) return;
     if (threadIdx.x == 0) s_bad = 0;
     __syncthreads();
-    Ctl c{A.done, A.status, 0u, false, nullptr};
+    Ctl<TR> c{A.done, A.status, 0u, false, nullptr};
     const int G = gridDim.x;
     for (int f = 0; f < A.ncodes; f++) {
         // Code f: its own tag space, and the state its predecessor's sampler wrote.
@@ -1548,10 +1565,12 @@ __global__ __launch_bounds__(kEngThreads) void k_engine(EngArgs A) {
             const KCONST EngOp &op = ((const KCONST EngOp *)A.ops)[oi];
             int t = ((int)blockIdx.x - op.rot) % G;
             if (t < 0) t += G;
-            uint64_t *tr = (A.trace && t < op.ntasks) ? A.trace + ((size_t)oi * G + blockIdx.x) * kTraceSlots : nullptr;
+            uint64_t *tr = nullptr;
+            if constexpr (TR)
+                if (A.trace && t < op.ntasks) tr = A.trace + ((size_t)oi * G + blockIdx.x) * kTraceSlots;
             c.tr = tr;
             if (t < op.ntasks) touch_desc(&op);
-            if (tr && threadIdx.x == 0) {
+            if (TR && tr && threadIdx.x == 0) {
                 glb(tr)[0] = wall_clock64();
                 glb(tr)[8] = clock64();
             }
@@ -1597,7 +1616,7 @@ __global__ __launch_bounds__(kEngThreads) void k_engine(EngArgs A) {
                 __syncthreads();
                 if (s_bad) return;
             }
-            if (tr && threadIdx.x == 0) {
+            if (TR && tr && threadIdx.x == 0) {
                 glb(tr)[1] = wall_clock64();
                 glb(tr)[9] = clock64();
             }
@@ -1636,22 +1655,24 @@ __global__ __launch_bounds__(kEngThreads) void k_engine(EngArgs A) {
 hipError_t launch_engine(hipStream_t st, const EngArgs &a, int grid, bool cooperative) {
     EngArgs args = a;
     void *kargs[] = {&args};
-    if (cooperative)
-        return hipLaunchCooperativeKernel((const void *)k_engine, dim3((unsigned)grid), dim3(kEngThreads), kargs, 0, st);
+    // the traced kernel only when trace slots are given
+    const void *fn = a.trace ? (const void *)k_engine<true> : (const void *)k_engine<false>;
+    if (cooperative) return hipLaunchCooperativeKernel(fn, dim3((unsigned)grid), dim3(kEngThreads), kargs, 0, st);
     // The same grid through an ordinary launch: on an otherwise idle device
     // every block of a grid of (CUs x resident blocks per CU) is resident at
     // once; if one were not, the waits on its outputs time out (EDEVICE) and
     // the grid drains.
-    return hipLaunchKernel((const void *)k_engine, dim3((unsigned)grid), dim3(kEngThreads), kargs, 0, st);
+    return hipLaunchKernel(fn, dim3((unsigned)grid), dim3(kEngThreads), kargs, 0, st);
 }
 
 int engine_max_grid() {
-    int dev = 0, ncu = 0, per = 0;
+    int dev = 0, ncu = 0, per = 0, per_tr = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 0;
     if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, (const void *)k_engine, kEngThreads, 0) != hipSuccess)
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, (const void *)k_engine<false>, kEngThreads, 0) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_tr, (const void *)k_engine<true>, kEngThreads, 0) != hipSuccess)
         return 0;
-    return ncu * (per < 1 ? 0 : 1);
+    return ncu * (per < 1 || per_tr < 1 ? 0 : 1);
 }
 
 }  // namespace qtts
