@@ -1563,7 +1563,7 @@ __global__ __launch_bounds__(kEngThreads) void k_engine(EngArgs A) {
         st.rng = ld_dev_u64(&st_in->rng);
         for (int oi = 0; oi < A.nops; oi++) {
             const KCONST EngOp &op = ((const KCONST EngOp *)A.ops)[oi];
-            int t = ((int)blockIdx.x - op.rot) % G;
+            int t = (int)blockIdx.x - op.rot;  // 0 <= rot < G
             if (t < 0) t += G;
             uint64_t *tr = nullptr;
             if constexpr (TR)
