@@ -8,6 +8,7 @@
 #include <cstdio>
 #include <cstdlib>
 #include <algorithm>
+#include <array>
 #include <atomic>
 #include <cstring>
 #include <functional>
@@ -2973,9 +2974,22 @@ static qtts_status generate_codes_dev(qtts_talker *t, qtts_predictor *p, qtts_kv
 // The weights keep the reference's layouts; every projection and convolution
 // is one k_dec_gemm launch (csrc/decoder.hip).
 // ---------------------------------------------------------------------------
+// A causal convolution's weights as binary16 hi + lo matrix-core operands
+// (DecConvMfmaParams); wh is null where the convolution runs on k_dec_gemm.
+struct DecConvMfma {
+    _Float16 *wh = nullptr, *wl = nullptr;
+    int ew = 0, mtiles = 0, ksteps = 0, cin16 = 0;
+};
+
 struct qtts_decoder {
     qtts_ctx *ctx = nullptr;
     Owner own;
+    // the Vocos convolutions on the matrix cores: [block][unit][conv1, conv2]
+    // and [block][output phase] of each block's transposed convolution
+    std::vector<std::vector<std::array<DecConvMfma, 2>>> res_mfma;
+    std::vector<std::vector<DecConvMfma>> up_mfma;
+    unsigned *amax = nullptr;  // [amax_slots][kDecMaxSlots]: max |x| of each such convolution's input, cleared per decode
+    int amax_slots = 0;
     qtts_decoder_view w{};  // device pointers
     std::vector<qtts_dec_layer_view> layers;
     std::vector<qtts_upsample_view> upsample;
@@ -3017,6 +3031,61 @@ qtts_status dec_conv(qtts_ctx *c, Owner &own, const qtts_conv_view &v, bool dept
                                 : (size_t)v.in_channels * v.out_channels * v.kernel_size;
     QTTS_TRY(dec_up(c, own, v.weight, wn, &d->weight, name));
     return dec_up(c, own, v.bias, (size_t)v.out_channels, &d->bias, name);
+}
+
+// The exponent ew that puts max |W| of a host weight array at
+// max |W| * 2^ew in [2^14, 2^15) (0 when every weight is zero).
+int dec_weight_exponent(const float *w, size_t n) {
+    float mx = 0.0f;
+    for (size_t i = 0; i < n; i++) {
+        const float a = std::fabs(w[i]);
+        if (a > mx) mx = a;  // NaN never compares greater
+    }
+    if (!(mx > 0.0f && std::isfinite(mx))) return 0;
+    int E;
+    (void)std::frexp(mx, &E);
+    return std::min(15 - E, 126);
+}
+
+// A matrix-core operand copy (k_dec_conv_repack) of the device weights dw:
+// element (m, ci, tap) at dw[m * sm + ci * sci + k0 + tap * kd], scaled by
+// 2^ew and split into binary16 hi + lo.
+qtts_status dec_mfma_copy(qtts_ctx *c, Owner &own, const float *dw, long long sm, long long sci, int k0, int kd,
+                          int M, int cin, int taps, int ew, DecConvMfma *out) {
+    DecConvMfma m;
+    m.ew = ew;
+    m.cin16 = (cin + 15) / 16 * 16;
+    m.mtiles = (M + 31) / 32;
+    m.ksteps = taps * m.cin16 / 16;
+    const size_t n = (size_t)m.mtiles * m.ksteps * 64 * 8;
+    QTTS_TRY(own.alloc(c, &m.wh, n));
+    QTTS_TRY(own.alloc(c, &m.wl, n));
+    launch_dec_conv_repack(c->stream, dw, sm, sci, k0, kd, M, cin, taps, m.cin16, m.mtiles, m.ksteps, ew, m.wh, m.wl);
+    QTTS_TRY(check_launch(c, "k_dec_conv_repack"));
+    *out = m;
+    return QTTS_OK;
+}
+
+// A causal convolution's copy (host view h for the weight maximum, device
+// view dv for the repack).
+qtts_status dec_conv_mfma(qtts_ctx *c, Owner &own, const qtts_conv_view &h, const qtts_conv_view &dv,
+                          DecConvMfma *out) {
+    const int ci = h.in_channels, co = h.out_channels, k = h.kernel_size;
+    const int ew = dec_weight_exponent(h.weight, (size_t)ci * co * k);
+    return dec_mfma_copy(c, own, dv.weight, (long long)ci * k, k, 0, 1, co, ci, k, ew, out);
+}
+
+// A transposed convolution's copy, one per output phase r: tap t of phase r
+// is kernel index r + (J - 1 - t) * stride (J = kernel / stride taps).
+qtts_status dec_convt_mfma(qtts_ctx *c, Owner &own, const qtts_conv_view &h, const qtts_conv_view &dv,
+                           std::vector<DecConvMfma> *out) {
+    const int ci = h.in_channels, co = h.out_channels, k = h.kernel_size, s = h.stride, J = k / s;
+    const int ew = dec_weight_exponent(h.weight, (size_t)ci * co * k);
+    out->assign((size_t)s, DecConvMfma{});
+    for (int r = 0; r < s; r++)
+        QTTS_TRY(dec_mfma_copy(c, own, dv.weight, k, (long long)co * k, r + (J - 1) * s, -s, co, ci, J, ew,
+                               &(*out)[(size_t)r]));
+    return QTTS_OK;
 }
 
 qtts_status dec_check_transposed(qtts_ctx *c, const qtts_conv_view &v, int in_ch, const char *name) {
@@ -3112,6 +3181,70 @@ qtts_status dec_causal(qtts_decoder *d, const qtts_conv_view &v, const float *x,
     p.resid = resid;
     launch_dec_gemm(d->ctx->stream, p);
     return check_launch(d->ctx, "k_dec_gemm");
+}
+
+// The same convolution on the matrix cores (k_dec_conv_mfma) from its
+// binary16 operand copy; xmax: kDecMaxSlots words whose maximum is the bits
+// of max |x|.
+qtts_status dec_causal_mfma(qtts_decoder *d, const qtts_conv_view &v, const DecConvMfma &m, const float *x,
+                            const unsigned *xmax, int len, float *c, int epi, const float *resid = nullptr) {
+    DecConvMfmaParams p{};
+    p.wh = m.wh;
+    p.wl = m.wl;
+    p.ew = m.ew;
+    p.M = v.out_channels;
+    p.mtiles = m.mtiles;
+    p.ksteps = m.ksteps;
+    p.cin = v.in_channels;
+    p.cin16 = m.cin16;
+    p.ksize = v.kernel_size;
+    p.dilation = v.dilation;
+    p.len = len;
+    p.x = x;
+    p.xmax = xmax;
+    p.bias = v.bias;
+    p.epi = epi;
+    p.c = c;
+    p.ldc = len;
+    p.out_stride = 1;
+    p.phase = 0;
+    p.resid = resid;
+    launch_dec_conv_mfma(d->ctx->stream, p);
+    return check_launch(d->ctx, "k_dec_conv_mfma");
+}
+
+// conv_transpose1d + the causal right crop on the matrix cores: output phase
+// r (out[q * stride + r], q < len) is a causal convolution of x with J taps
+// reaching J - 1 steps back, from the phase's operand copy.
+qtts_status dec_transposed_mfma(qtts_decoder *d, const qtts_conv_view &v, const std::vector<DecConvMfma> &ph,
+                                const float *x, const unsigned *xmax, int len, float *c) {
+    const int J = v.kernel_size / v.stride;
+    for (int r = 0; r < v.stride; r++) {
+        const DecConvMfma &m = ph[(size_t)r];
+        DecConvMfmaParams p{};
+        p.wh = m.wh;
+        p.wl = m.wl;
+        p.ew = m.ew;
+        p.M = v.out_channels;
+        p.mtiles = m.mtiles;
+        p.ksteps = m.ksteps;
+        p.cin = v.in_channels;
+        p.cin16 = m.cin16;
+        p.ksize = J;
+        p.dilation = 1;
+        p.len = len;
+        p.x = x;
+        p.xmax = xmax;
+        p.bias = v.bias;
+        p.epi = DEC_EPI_STORE;
+        p.c = c;
+        p.ldc = (long long)len * v.stride;
+        p.out_stride = v.stride;
+        p.phase = r;
+        launch_dec_conv_mfma(d->ctx->stream, p);
+        QTTS_TRY(check_launch(d->ctx, "k_dec_conv_mfma"));
+    }
+    return QTTS_OK;
 }
 
 // conv_transpose1d + the causal right crop (src/conv.rs:198-268,
@@ -3260,24 +3393,36 @@ qtts_status dec_decode(qtts_decoder *d, const uint32_t *d_codes, int T, int ld, 
         QTTS_TRY(dec_causal(d, w.vocos_init, sig, L, o, DEC_EPI_STORE));
         sig = o;
     }
-    for (const auto &b : d->blocks) {
+    // the residual convolutions' input maxima start at zero in every decode
+    if (d->amax_slots > 0) {
+        launch_dec_fill_u32(st, d->amax, d->amax_slots * kDecMaxSlots, 0u);
+        QTTS_TRY(check_launch(c, "k_dec_fill_u32"));
+    }
+    int slot = 0;
+    for (size_t bi = 0; bi < d->blocks.size(); bi++) {
+        const qtts_vocos_block_view &b = d->blocks[bi];
         const int cin = b.upsample.in_channels, cout = b.upsample.out_channels;
         float *t1 = other(sig), *nxt = other(sig, t1);
-        launch_dec_snake(st, sig, b.pre_snake_alpha, b.pre_snake_beta, cin, L, t1);
+        unsigned *m0 = d->amax + (size_t)slot * kDecMaxSlots;
+        slot += 1;
+        launch_dec_snake(st, sig, b.pre_snake_alpha, b.pre_snake_beta, cin, L, t1, m0);
         QTTS_TRY(check_launch(c, "k_dec_snake"));
-        QTTS_TRY(dec_transposed(d, b.upsample, t1, L, nxt));
+        QTTS_TRY(dec_transposed_mfma(d, b.upsample, d->up_mfma[bi], t1, m0, L, nxt));
         L *= b.upsample.stride;
         sig = nxt;
         float *t2 = other(sig, t1);
         for (int r = 0; r < b.num_residuals; r++) {
             const qtts_vocos_residual_view &rv = b.residuals[r];
-            launch_dec_snake(st, sig, rv.act1_alpha, rv.act1_beta, cout, L, t1);
+            const std::array<DecConvMfma, 2> &mc = d->res_mfma[bi][(size_t)r];
+            unsigned *m1 = d->amax + (size_t)slot * kDecMaxSlots, *m2 = m1 + kDecMaxSlots;
+            slot += 2;
+            launch_dec_snake(st, sig, rv.act1_alpha, rv.act1_beta, cout, L, t1, m1);
             QTTS_TRY(check_launch(c, "k_dec_snake"));
-            QTTS_TRY(dec_causal(d, rv.conv1, t1, L, t2, DEC_EPI_STORE));
-            launch_dec_snake(st, t2, rv.act2_alpha, rv.act2_beta, cout, L, t1);
+            QTTS_TRY(dec_causal_mfma(d, rv.conv1, mc[0], t1, m1, L, t2, DEC_EPI_STORE));
+            launch_dec_snake(st, t2, rv.act2_alpha, rv.act2_beta, cout, L, t1, m2);
             QTTS_TRY(check_launch(c, "k_dec_snake"));
             // signal = conv2 + residual, in place (each output reads its own residual first)
-            QTTS_TRY(dec_causal(d, rv.conv2, t1, L, sig, DEC_EPI_RESID_IN, sig));
+            QTTS_TRY(dec_causal_mfma(d, rv.conv2, mc[1], t1, m2, L, sig, DEC_EPI_RESID_IN, sig));
         }
     }
     float *t1 = other(sig);
@@ -3381,14 +3526,18 @@ qtts_status qtts_decoder_upload(qtts_ctx *c, const qtts_decoder_view *v, qtts_de
     if ((s = dec_conv(c, o, v->vocos_init, false, &w.vocos_init, "vocos_init")) != QTTS_OK) return bail(s);
     ch = v->vocos_init.out_channels;
     d->residuals.resize((size_t)std::max(v->num_vocos_blocks, 0));
+    d->res_mfma.resize(d->residuals.size());
+    d->up_mfma.resize(d->residuals.size());
     for (int b = 0; b < v->num_vocos_blocks; b++) {
         const qtts_vocos_block_view &B = v->vocos_blocks[b];
         qtts_vocos_block_view D = B;
         if ((s = dec_check_transposed(c, B.upsample, ch, "vocos upsample")) != QTTS_OK) return bail(s);
         if ((s = up(B.pre_snake_alpha, (size_t)ch, &D.pre_snake_alpha, "pre_snake_alpha")) != QTTS_OK ||
             (s = up(B.pre_snake_beta, (size_t)ch, &D.pre_snake_beta, "pre_snake_beta")) != QTTS_OK ||
-            (s = dec_conv(c, o, B.upsample, false, &D.upsample, "vocos upsample")) != QTTS_OK)
+            (s = dec_conv(c, o, B.upsample, false, &D.upsample, "vocos upsample")) != QTTS_OK ||
+            (s = dec_convt_mfma(c, o, B.upsample, D.upsample, &d->up_mfma[(size_t)b])) != QTTS_OK)
             return bail(s);
+        d->amax_slots += 1;
         ch = B.upsample.out_channels;
         for (int r = 0; r < B.num_residuals; r++) {
             const qtts_vocos_residual_view &R = B.residuals[r];
@@ -3403,6 +3552,12 @@ qtts_status qtts_decoder_upload(qtts_ctx *c, const qtts_decoder_view *v, qtts_de
                 (s = dec_conv(c, o, R.conv1, false, &E.conv1, "residual conv1")) != QTTS_OK ||
                 (s = dec_conv(c, o, R.conv2, false, &E.conv2, "residual conv2")) != QTTS_OK)
                 return bail(s);
+            std::array<DecConvMfma, 2> mc{};
+            if ((s = dec_conv_mfma(c, o, R.conv1, E.conv1, &mc[0])) != QTTS_OK ||
+                (s = dec_conv_mfma(c, o, R.conv2, E.conv2, &mc[1])) != QTTS_OK)
+                return bail(s);
+            d->res_mfma[b].push_back(mc);
+            d->amax_slots += 2;
             d->residuals[b].push_back(E);
         }
         D.residuals = d->residuals[b].data();
@@ -3422,6 +3577,8 @@ qtts_status qtts_decoder_upload(qtts_ctx *c, const qtts_decoder_view *v, qtts_de
     }
     if ((s = o.alloc(c, &d->status, 1)) != QTTS_OK) return bail(s);
     if (hipMemset(d->status, 0, sizeof(int)) != hipSuccess) return bail(fail(c, QTTS_EDEVICE, "hipMemset"));
+    if ((s = o.alloc(c, &d->amax, (size_t)std::max(d->amax_slots, 1) * kDecMaxSlots)) != QTTS_OK) return bail(s);
+    if (hipStreamSynchronize(c->stream) != hipSuccess) return bail(fail(c, QTTS_EDEVICE, "decoder weight repack"));
     *out = d;
     return QTTS_OK;
 }

@@ -15,9 +15,13 @@
 //  k_dec_dwconv   causal depthwise convolution (src/conv.rs:280-345)
 //  k_dec_lnorm    channel-first LayerNorm per time step, channels summed in
 //                 order (src/decoder.rs:580-602)
-//  k_dec_snake    SnakeBeta (src/conv.rs:347-400)
+//  k_dec_snake    SnakeBeta (src/conv.rs:347-400), optionally recording
+//                 max |out| for the convolution that reads it
+//  k_dec_conv_mfma  a causal convolution on the matrix cores
+//                 (v_mfma_f32_32x32x16_f16 with binary16 hi + lo operands)
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 
@@ -29,6 +33,11 @@ namespace qtts {
 namespace {
 
 constexpr int TM = 64, TN = 64, TK = 16;
+constexpr unsigned kSnakeBlocks = 8192;  // SnakeBeta grid cap (threads stride through the tensor)
+#ifndef QTTS_DEC_CONV_TILES
+#define QTTS_DEC_CONV_TILES 1
+#endif
+constexpr int kDecConvTiles = QTTS_DEC_CONV_TILES;  // 32-step output tiles per wave of k_dec_conv_mfma
 
 __global__ void k_dec_gather(DecGatherParams P) {
     const int t = blockIdx.x, cd = P.cd;
@@ -254,14 +263,194 @@ __global__ void k_dec_lnorm(const float *x, const float *g, const float *b, int 
     for (int c = 0; c < ch; c++) out[(size_t)c * len + t] = (x[(size_t)c * len + t] - mean) * inv * g[c] + b[c];
 }
 
-// x + exp(-beta) * sin(exp(alpha) * x)^2 per channel, channel-first.
-__global__ void k_dec_snake(const float *x, const float *alpha, const float *beta, int ch, int len, float *out) {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (size_t)ch * len) return;
-    const int c = (int)(i / len);
-    const float a = expf(alpha[c]), inv_b = expf(-beta[c]);
-    const float v = x[i], s = sinf(a * v);
-    out[i] = v + inv_b * s * s;
+// x + exp(-beta) * sin(exp(alpha) * x)^2 per channel, channel-first, over a
+// grid of at most kSnakeBlocks blocks (each thread strides through the
+// tensor).  With amax set, each block's largest |out| (NaN excluded) is
+// folded into amax[block % kMaxSlots] by an unsigned atomicMax of the float
+// bits, which orders non-negative floats as their values: the slots' maximum
+// does not depend on the order of the blocks, and 64 slots keep the atomics
+// from queueing on one address.
+__global__ __launch_bounds__(256) void k_dec_snake(const float *x, const float *alpha, const float *beta, int ch,
+                                                   int len, float *out, unsigned *amax) {
+    const size_t total = (size_t)ch * len, stride = (size_t)gridDim.x * blockDim.x;
+    float m = 0.0f;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
+        const int c = (int)(i / len);
+        const float a = expf(alpha[c]), inv_b = expf(-beta[c]);
+        const float v = x[i], s = sinf(a * v);
+        const float o = v + inv_b * s * s;
+        out[i] = o;
+        m = fmaxf(m, fabsf(o));  // a NaN o leaves m as it was
+    }
+    if (!amax) return;  // uniform
+    __shared__ float red[4];
+    m = wave_max(m);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        atomicMax(&amax[blockIdx.x % kDecMaxSlots], __float_as_uint(m));
+    }
+}
+
+__global__ void k_dec_fill_u32(unsigned *p, int n, unsigned v) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// The exponent e that puts a positive finite maximum m at m * 2^e in
+// [2^14, 2^15) (0 for zero, infinite or NaN).
+__device__ __forceinline__ int split_exponent(float m) {
+    if (!(m > 0.0f && m < INFINITY)) return 0;
+    int E;
+    (void)frexpf(m, &E);  // m = f * 2^E, f in [0.5, 1)
+    return min(15 - E, 126);
+}
+
+// A convolution's weights as binary16 hi + lo MFMA A operands, scaled by
+// 2^ew: thread (tile, step, lane) writes the 8 values of row
+// m = 32 * tile + lane % 32 at k' = 16 * step + 8 * (lane / 32) + i,
+// tap = k' / cin16, ci = k' % cin16 (zero past M or cin): the element
+// w[m * sm + ci * sci + k0 + tap * kd] -- for a causal convolution
+// W[m][ci][tap] (src/conv.rs:114-184: sm = cin * ksize, sci = ksize, k0 = 0,
+// kd = 1); for output phase r of a transposed one W[ci][m][r + (J-1-tap) s]
+// (src/conv.rs:198-268: sm = ksize, sci = M * ksize, k0 = r + (J - 1) s,
+// kd = -s), so that tap t reads the input J - 1 - t steps back.
+// hi = f16(w'), lo = f16(w' - hi).
+__global__ void k_dec_conv_repack(const float *w, long long sm, long long sci, int k0, int kd, int M, int cin,
+                                  int taps, int cin16, int mtiles, int ksteps, int ew, _Float16 *wh, _Float16 *wl) {
+    const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (size_t)mtiles * ksteps * 64) return;
+    const int lane = (int)(idx & 63);
+    const size_t ts = idx >> 6;
+    const int tile = (int)(ts / ksteps), step = (int)(ts - (size_t)tile * ksteps);
+    const int m = 32 * tile + (lane & 31), kb = 16 * step + 8 * (lane >> 5);
+    half8 h, l;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        const int kp = kb + i, tap = kp / cin16, ci = kp - tap * cin16;
+        const float v = (m < M && ci < cin && tap < taps)
+                            ? ldexpf(w[(long long)m * sm + (long long)ci * sci + k0 + (long long)tap * kd], ew)
+                            : 0.0f;
+        const _Float16 hv = (_Float16)v;
+        h[i] = hv;
+        l[i] = (_Float16)(v - (float)hv);
+    }
+    reinterpret_cast<half8 *>(wh)[idx] = h;
+    reinterpret_cast<half8 *>(wl)[idx] = l;
+}
+
+// A causal convolution c[m][n] = bias[m] + sum_{ci, tap} W[m][ci][tap] *
+// x[ci][n + (tap - (ksize - 1)) * dilation] (zero before the signal) as an
+// implicit GEMM on the matrix cores.  Each wave owns NT tiles of 32 output
+// steps n and the block's MT tiles of 32 channels, so each A operand it
+// loads serves NT tiles; per 16-row K step it gathers its own B operands --
+// lane l of tile j: step n0 + 32 j + l % 32, channels ci0 + 8 (l / 32) + i of
+// one tap (K is tap-major and the channels are padded to a multiple of 16,
+// so a step never straddles two taps) -- scales them by 2^ex (ex from the
+// producer's max |x|), splits them into binary16 hi + lo, and runs three
+// MFMAs per tile pair: wh * xh + wh * xl + wl * xh.  Every product of
+// binary16 values is exact in the f32 accumulator; the dropped wl * xl term
+// and the two splits leave a relative error of about 2^-21 per term, the
+// f32 level.  The next step's operands are loaded before the current
+// step's MFMAs.
+template <int MT, int NT>
+__global__ __launch_bounds__(256) void k_dec_conv_mfma(DecConvMfmaParams P) {
+    static_assert(kDecMaxSlots == 64, "one max slot per lane");
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = lane & 31, half = lane >> 5;
+    const int nb = (blockIdx.x * 4 + wave) * 32 * NT + col;  // this lane's step in tile 0
+    const int t0 = blockIdx.y * MT;
+    const int len = P.len, cin16 = P.cin16, ksteps = P.ksteps;
+    // max |x| over the producer's slots, one per lane
+    const int ex = split_exponent(wave_max(__uint_as_float(P.xmax[lane])));
+    const float xs = ldexpf(1.0f, ex);
+    const int cpl = P.cin - 8 * half;  // channels this lane's half may read at ci0 = 0
+
+    // operands of step s: A of every channel tile, the 8 raw x values of
+    // this lane in every step tile
+    auto load = [&](int s, half8 (&ah)[MT], half8 (&al)[MT], float (&xv)[NT][8]) {
+        const int kp = 16 * s;  // wave-uniform; cin16 % 16 == 0, so one tap per step
+        const int tap = kp / cin16, ci0 = kp - tap * cin16;
+        const int off = (tap - (P.ksize - 1)) * P.dilation;
+        const bool chan_ok = ci0 < cpl;  // the first of this lane's 8 channels
+#pragma unroll
+        for (int j = 0; j < NT; j++) {
+            const int n = nb + 32 * j, p = n + off;
+            const bool ok = n < len && p >= 0 && chan_ok;
+            const float *xp = P.x + (size_t)(ci0 + 8 * half) * len + (ok ? p : 0);
+#pragma unroll
+            for (int i = 0; i < 8; i++) xv[j][i] = ok && ci0 + i < cpl ? xp[(size_t)i * len] : 0.0f;
+        }
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            const size_t o = ((size_t)(t0 + t) * ksteps + s) * 64 + lane;
+            ah[t] = reinterpret_cast<const half8 *>(P.wh)[o];
+            al[t] = reinterpret_cast<const half8 *>(P.wl)[o];
+        }
+    };
+    f32x16 acc[MT][NT];
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int j = 0; j < NT; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[t][j][r] = 0.0f;
+    half8 ah[MT], al[MT];
+    float xv[NT][8];
+    load(0, ah, al, xv);
+    for (int s = 0; s < ksteps; s++) {
+        half8 nh[MT], nl[MT];
+        float nx[NT][8];
+        load(s + 1 < ksteps ? s + 1 : s, nh, nl, nx);
+#pragma unroll
+        for (int j = 0; j < NT; j++) {
+            half8 bh, bl;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float v = xv[j][i] * xs;
+                const _Float16 hv = (_Float16)v;
+                bh[i] = hv;
+                bl[i] = (_Float16)(v - (float)hv);
+            }
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                acc[t][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[t], bh, acc[t][j], 0, 0, 0);
+                acc[t][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[t], bl, acc[t][j], 0, 0, 0);
+                acc[t][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[t], bh, acc[t][j], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            ah[t] = nh[t];
+            al[t] = nl[t];
+        }
+#pragma unroll
+        for (int j = 0; j < NT; j++)
+#pragma unroll
+            for (int i = 0; i < 8; i++) xv[j][i] = nx[j][i];
+    }
+    // D layout: lane l, register r -> row (r / 4) * 8 + (l / 32) * 4 + r % 4,
+    // column l % 32
+    const int sc = -(ex + P.ew);
+#pragma unroll
+    for (int j = 0; j < NT; j++) {
+        const int n = nb + 32 * j;
+        if (n >= len) continue;
+#pragma unroll
+        for (int t = 0; t < MT; t++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int m = 32 * (t0 + t) + (r >> 2) * 8 + half * 4 + (r & 3);
+                if (m >= P.M) continue;
+                const float v = ldexpf(acc[t][j][r], sc) + P.bias[m];
+                const size_t o = (size_t)m * P.ldc + (size_t)n * P.out_stride + P.phase;
+                P.c[o] = P.epi == DEC_EPI_RESID_IN ? P.resid[o] + v : v;
+            }
+    }
 }
 
 unsigned blocks_for(size_t n, unsigned per) { return (unsigned)((n + per - 1) / per); }
@@ -307,9 +496,34 @@ void launch_dec_lnorm(hipStream_t st, const float *x, const float *g, const floa
 }
 
 void launch_dec_snake(hipStream_t st, const float *x, const float *alpha, const float *beta, int ch, int len,
-                      float *out) {
-    hipLaunchKernelGGL(k_dec_snake, dim3(blocks_for((size_t)ch * len, 256)), dim3(256), 0, st, x, alpha, beta, ch,
-                       len, out);
+                      float *out, unsigned *amax) {
+    const unsigned blocks = std::min<unsigned>(blocks_for((size_t)ch * len, 256), kSnakeBlocks);
+    hipLaunchKernelGGL(k_dec_snake, dim3(blocks), dim3(256), 0, st, x, alpha, beta, ch, len, out, amax);
+}
+
+void launch_dec_fill_u32(hipStream_t st, unsigned *p, int n, unsigned v) {
+    hipLaunchKernelGGL(k_dec_fill_u32, dim3(blocks_for((size_t)n, 256)), dim3(256), 0, st, p, n, v);
+}
+
+void launch_dec_conv_repack(hipStream_t st, const float *w, long long sm, long long sci, int k0, int kd, int M, int cin,
+                            int taps, int cin16, int mtiles, int ksteps, int ew, _Float16 *wh, _Float16 *wl) {
+    const size_t n = (size_t)mtiles * ksteps * 64;
+    hipLaunchKernelGGL(k_dec_conv_repack, dim3(blocks_for(n, 256)), dim3(256), 0, st, w, sm, sci, k0, kd, M, cin,
+                       taps, cin16, mtiles, ksteps, ew, wh, wl);
+}
+
+// MT: the largest of 4, 3, 2, 1 that divides the tile count (a block's
+// tiles share each gathered B operand).
+void launch_dec_conv_mfma(hipStream_t st, const DecConvMfmaParams &p) {
+    constexpr int NT = kDecConvTiles;
+    const int mt = p.mtiles % 4 == 0 ? 4 : p.mtiles % 3 == 0 ? 3 : p.mtiles % 2 == 0 ? 2 : 1;
+    const dim3 grid(blocks_for((size_t)p.len, 128 * NT), (unsigned)(p.mtiles / mt));
+    switch (mt) {
+        case 4: hipLaunchKernelGGL((k_dec_conv_mfma<4, NT>), grid, dim3(256), 0, st, p); break;
+        case 3: hipLaunchKernelGGL((k_dec_conv_mfma<3, NT>), grid, dim3(256), 0, st, p); break;
+        case 2: hipLaunchKernelGGL((k_dec_conv_mfma<2, NT>), grid, dim3(256), 0, st, p); break;
+        default: hipLaunchKernelGGL((k_dec_conv_mfma<1, NT>), grid, dim3(256), 0, st, p); break;
+    }
 }
 
 }  // namespace qtts

@@ -80,6 +80,7 @@ struct QkvRowsParams {
 // ---- speech decoder (csrc/decoder.hip) ----
 constexpr int kDecMaxWindow = 512;   // sliding window of the decoder attention
 constexpr int kDecMaxHeadDim = 256;
+constexpr int kDecMaxSlots = 64;  // slots of one tensor's max |x| (SnakeBeta -> k_dec_conv_mfma)
 
 struct DecGatherParams {
     const uint32_t *codes;  // [groups][ld]
@@ -114,6 +115,25 @@ struct DecGemmParams {
     int out_stride;
     const float *scale_n;  // DEC_EPI_SCALED_RESID / DEC_EPI_RESID_IN
     const float *resid;    // DEC_EPI_RESID_IN (same addressing as c)
+};
+
+// A causal convolution (implicit GEMM, as DEC_B_CONV) on the matrix cores:
+// weights pre-split into binary16 hi + lo in the MFMA A-operand order with
+// K ordered tap-major (k' = tap * cin16 + ci, the channels padded to a
+// multiple of 16 with zero weights), activations split on the fly.
+struct DecConvMfmaParams {
+    const _Float16 *wh, *wl;  // [mtiles][ksteps][64][8]; row m = 32 * tile + lane % 32
+    int ew;                   // the weights were scaled by 2^ew
+    int M, mtiles, ksteps;    // output channels, 32-row tiles, 16-row K steps (ksize * cin16 / 16)
+    int cin, cin16, ksize, dilation, len;
+    const float *x;           // [cin][len]
+    const unsigned *xmax;     // [kDecMaxSlots]: bits of max |x| over the slots (a producer's atomicMax)
+    const float *bias;        // [M]
+    int epi;                  // DEC_EPI_STORE or DEC_EPI_RESID_IN
+    float *c;                 // output (m, n) at c[m * ldc + n * out_stride + phase]
+    long long ldc;
+    int out_stride, phase;    // 1, 0; or one output phase of a transposed convolution
+    const float *resid;       // DEC_EPI_RESID_IN: at the output's index (may be c)
 };
 
 struct DecAttnParams {
@@ -325,7 +345,11 @@ void launch_dec_dwconv(hipStream_t st, const float *x, const float *w, const flo
 void launch_dec_lnorm(hipStream_t st, const float *x, const float *g, const float *b, int ch, int len, float eps,
                       float *out);
 void launch_dec_snake(hipStream_t st, const float *x, const float *alpha, const float *beta, int ch, int len,
-                      float *out);
+                      float *out, unsigned *amax = nullptr);
+void launch_dec_fill_u32(hipStream_t st, unsigned *p, int n, unsigned v);
+void launch_dec_conv_repack(hipStream_t st, const float *w, long long sm, long long sci, int k0, int kd, int M, int cin,
+                            int taps, int cin16, int mtiles, int ksteps, int ew, _Float16 *wh, _Float16 *wl);
+void launch_dec_conv_mfma(hipStream_t st, const DecConvMfmaParams &p);
 void launch_gemm_mfma(hipStream_t st, const GemmMfmaParams &p, int mt, int sw, int kc);
 void launch_embed_sum(hipStream_t st, const EmbSumParams &p);
 void launch_advance(hipStream_t st, LoopState *s, int frame_step, int batch = 1);
