@@ -385,9 +385,12 @@ def decoder_measure(ctx, frames, cpu_frames=2, reps=3):
     out = {
         "frames": frames, "samples": n, "ms": round(avg_s * 1e3, 2),
         "audio_seconds_per_second": round(n / 24000.0 / avg_s, 1),
-        "roofline": {"bound": "fp32", "achieved": round(achieved, 2), "peak": FP32_PEAK_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(achieved / FP32_PEAK_TFLOPS, 4), "algorithmic_flops": flops,
-                     "kernel": "whole decode (k_dec_gemm dominant)"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": MFMA_F16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / MFMA_F16_PEAK_TFLOPS, 4), "algorithmic_flops": flops,
+                     "issued_f16_TFLOPs": round(3 * achieved, 1),
+                     "frac_of_f32_peak": round(achieved / FP32_PEAK_TFLOPS, 4),
+                     "kernel": "whole decode (k_dec_conv_mfma dominant: every projection and convolution as "
+                               "three binary16 MFMAs per f32 product term)"},
     }
     if cpu_frames:
         from oracle import oracle
@@ -716,6 +719,8 @@ def main():
                     help="only the GEMV timings and the copy-kernel calibration (for counter runs)")
     ap.add_argument("--attention-only", type=int, default=0, metavar="L",
                     help="only multi-kernel talker steps at a cache of L rows (for attention counter runs)")
+    ap.add_argument("--decoder-only", type=int, default=0, metavar="FRAMES",
+                    help="only the speech decoder's decode of FRAMES frames (for decoder kernel traces)")
     ap.add_argument("--engine-trace", default="", metavar="FILE",
                     help="only a per-op trace of 3 frames at cache lengths 315..317 (written to FILE) and its "
                          "critical-path summary")
@@ -732,6 +737,12 @@ def main():
         rfloor = read_floor(ctx)
         copied = copy_calibration(ctx)
         print(json.dumps({"gemv": roof, "copy_floor": floor, "read_floor": rfloor, "copy_bytes": copied}), flush=True)
+        ctx.close()
+        return
+
+    if args.decoder_only:
+        ctx = qtts.Context(0)
+        print(json.dumps({"decoder": decoder_measure(ctx, args.decoder_only, cpu_frames=0)}), flush=True)
         ctx.close()
         return
 

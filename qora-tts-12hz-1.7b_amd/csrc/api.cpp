@@ -2972,10 +2972,11 @@ static qtts_status generate_codes_dev(qtts_talker *t, qtts_predictor *p, qtts_kv
 // ---------------------------------------------------------------------------
 // Speech decoder: decode_to_audio (src/decoder.rs:394-509) on the device.
 // The weights keep the reference's layouts; every projection and convolution
-// is one k_dec_gemm launch (csrc/decoder.hip).
+// runs on the matrix cores (k_dec_conv_mfma, csrc/decoder.hip) from a
+// binary16 hi + lo operand copy made at upload.
 // ---------------------------------------------------------------------------
-// A causal convolution's weights as binary16 hi + lo matrix-core operands
-// (DecConvMfmaParams); wh is null where the convolution runs on k_dec_gemm.
+// A convolution's or linear layer's weights as binary16 hi + lo
+// matrix-core operands (DecConvMfmaParams).
 struct DecConvMfma {
     _Float16 *wh = nullptr, *wl = nullptr;
     int ew = 0, mtiles = 0, ksteps = 0, cin16 = 0;
@@ -2988,6 +2989,14 @@ struct qtts_decoder {
     // and [block][output phase] of each block's transposed convolution
     std::vector<std::vector<std::array<DecConvMfma, 2>>> res_mfma;
     std::vector<std::vector<DecConvMfma>> up_mfma;
+    // the other matrix-core layers: codebook projections, pre-conv, the
+    // transformer's input / output and per-layer q, k, v, o, gate, up, down,
+    // each ConvNeXt stage's transposed convolution (per phase) and pw1, pw2,
+    // the Vocos input and output convolutions
+    DecConvMfma proj0, proj_rest, pre_conv, tf_in, tf_out, vocos_init, out_conv;
+    std::vector<std::array<DecConvMfma, 7>> layer_mfma;
+    std::vector<std::vector<DecConvMfma>> cnx_up_mfma;
+    std::vector<std::array<DecConvMfma, 2>> pw_mfma;
     unsigned *amax = nullptr;  // [amax_slots][kDecMaxSlots]: max |x| of each such convolution's input, cleared per decode
     int amax_slots = 0;
     qtts_decoder_view w{};  // device pointers
@@ -3088,6 +3097,13 @@ qtts_status dec_convt_mfma(qtts_ctx *c, Owner &own, const qtts_conv_view &h, con
     return QTTS_OK;
 }
 
+// A linear layer's copy: W [K][N] (in-major, as dec_linear reads it), output
+// feature m = n of W, channel ci = k.
+qtts_status dec_lin_mfma(qtts_ctx *c, Owner &own, const float *hw, const float *dw, int K, int N, DecConvMfma *out) {
+    const int ew = dec_weight_exponent(hw, (size_t)K * N);
+    return dec_mfma_copy(c, own, dw, 1, N, 0, 0, N, K, 1, ew, out);
+}
+
 qtts_status dec_check_transposed(qtts_ctx *c, const qtts_conv_view &v, int in_ch, const char *name) {
     if (v.in_channels != in_ch || v.stride <= 0 || v.padding != 0 || v.kernel_size < v.stride ||
         v.kernel_size % v.stride != 0)
@@ -3122,70 +3138,10 @@ int64_t dec_len_after(const qtts_conv_view &v, int64_t len) {
     return crop > 0 ? full - crop : full;
 }
 
-DecGemmParams dec_gemm_base(int M, int N, int K) {
-    DecGemmParams p{};
-    p.M = M;
-    p.N = N;
-    p.K = K;
-    p.epi = DEC_EPI_STORE;
-    return p;
-}
-
-// Y(m = row, n) = X[rows][K] . W[K][N] with X token-major: the transformer's
-// and ConvNeXt's projections.  Output at c[m * scm + n * scn].
-qtts_status dec_linear(qtts_decoder *d, const float *x, long long sxm, long long sxk, int rows, const float *w, int K,
-                       int N, const float *bias_n, float *c, long long scm, long long scn, int epi,
-                       const float *scale_n = nullptr, const float *resid = nullptr, int act = DEC_ACT_NONE) {
-    DecGemmParams p = dec_gemm_base(rows, N, K);
-    p.a_mode = DEC_A_STRIDED;
-    p.a = x;
-    p.sam = sxm;
-    p.sak = sxk;
-    p.a_kfast = sxk == 1;
-    p.b_mode = DEC_B_STRIDED;
-    p.b = w;
-    p.sbk = N;
-    p.sbn = 1;
-    p.bias_n = bias_n;
-    p.act = act;
-    p.epi = epi;
-    p.c = c;
-    p.scm = scm;
-    p.scn = scn;
-    p.scale_n = scale_n;
-    p.resid = resid;
-    launch_dec_gemm(d->ctx->stream, p);
-    return check_launch(d->ctx, "k_dec_gemm");
-}
-
 // Causal convolution (causal_conv1d, src/conv.rs:114-184) of x [in][len]
-// into c [out][len].
-qtts_status dec_causal(qtts_decoder *d, const qtts_conv_view &v, const float *x, int len, float *c, int epi,
-                       const float *resid = nullptr) {
-    DecGemmParams p = dec_gemm_base(v.out_channels, len, v.in_channels * v.kernel_size);
-    p.a_mode = DEC_A_STRIDED;
-    p.a = v.weight;
-    p.sam = (long long)v.in_channels * v.kernel_size;
-    p.sak = 1;
-    p.a_kfast = 1;
-    p.b_mode = DEC_B_CONV;
-    p.b = x;
-    p.ksize = v.kernel_size;
-    p.dilation = v.dilation;
-    p.in_len = len;
-    p.bias_m = v.bias;
-    p.epi = epi;
-    p.c = c;
-    p.scm = len;
-    p.scn = 1;
-    p.resid = resid;
-    launch_dec_gemm(d->ctx->stream, p);
-    return check_launch(d->ctx, "k_dec_gemm");
-}
-
-// The same convolution on the matrix cores (k_dec_conv_mfma) from its
-// binary16 operand copy; xmax: kDecMaxSlots words whose maximum is the bits
-// of max |x|.
+// into c [out][len] on the matrix cores (k_dec_conv_mfma), from the
+// weights' binary16 operand copy; xmax: kDecMaxSlots words whose maximum is
+// the bits of max |x|.
 qtts_status dec_causal_mfma(qtts_decoder *d, const qtts_conv_view &v, const DecConvMfma &m, const float *x,
                             const unsigned *xmax, int len, float *c, int epi, const float *resid = nullptr) {
     DecConvMfmaParams p{};
@@ -3201,6 +3157,8 @@ qtts_status dec_causal_mfma(qtts_decoder *d, const qtts_conv_view &v, const DecC
     p.dilation = v.dilation;
     p.len = len;
     p.x = x;
+    p.sxc = len;
+    p.sxn = 1;
     p.xmax = xmax;
     p.bias = v.bias;
     p.epi = epi;
@@ -3213,9 +3171,49 @@ qtts_status dec_causal_mfma(qtts_decoder *d, const qtts_conv_view &v, const DecC
     return check_launch(d->ctx, "k_dec_conv_mfma");
 }
 
-// conv_transpose1d + the causal right crop on the matrix cores: output phase
-// r (out[q * stride + r], q < len) is a causal convolution of x with J taps
-// reaching J - 1 steps back, from the phase's operand copy.
+// Y(row, n) = X[rows][K] . W[K][N] (+ bias, act) with x(row, k) at
+// x[row * sxm + k * sxk] and the output at c[row * scm + n * scn]: the
+// transformer's and ConvNeXt's projections, on the matrix cores
+// (k_dec_conv_mfma with one tap: output feature n is channel m = n at
+// position row).
+qtts_status dec_linear_mfma(qtts_decoder *d, const DecConvMfma &m, const float *x, long long sxm, long long sxk,
+                            int rows, int K, int N, const unsigned *xmax, const float *bias, float *c, long long scm,
+                            long long scn, int epi, const float *scale = nullptr, const float *resid = nullptr,
+                            int act = DEC_ACT_NONE) {
+    DecConvMfmaParams p{};
+    p.wh = m.wh;
+    p.wl = m.wl;
+    p.ew = m.ew;
+    p.M = N;
+    p.mtiles = m.mtiles;
+    p.ksteps = m.ksteps;
+    p.cin = K;
+    p.cin16 = m.cin16;
+    p.ksize = 1;
+    p.dilation = 1;
+    p.len = rows;
+    p.x = x;
+    p.sxc = sxk;
+    p.sxn = sxm;
+    p.xmax = xmax;
+    p.bias = bias;
+    p.scale = scale;
+    p.act = act;
+    p.epi = epi;
+    p.c = c;
+    p.ldc = scn;
+    p.out_stride = scm;
+    p.phase = 0;
+    p.resid = resid;
+    launch_dec_conv_mfma(d->ctx->stream, p);
+    return check_launch(d->ctx, "k_dec_conv_mfma");
+}
+
+// conv_transpose1d + the causal right crop (src/conv.rs:198-268,
+// src/decoder.rs:430-444) on the matrix cores: output phase r
+// (out[q * stride + r], q < len) is a causal convolution of x with
+// J = kernel / stride taps reaching J - 1 steps back, from the phase's
+// operand copy.
 qtts_status dec_transposed_mfma(qtts_decoder *d, const qtts_conv_view &v, const std::vector<DecConvMfma> &ph,
                                 const float *x, const unsigned *xmax, int len, float *c) {
     const int J = v.kernel_size / v.stride;
@@ -3234,6 +3232,8 @@ qtts_status dec_transposed_mfma(qtts_decoder *d, const qtts_conv_view &v, const 
         p.dilation = 1;
         p.len = len;
         p.x = x;
+        p.sxc = len;
+        p.sxn = 1;
         p.xmax = xmax;
         p.bias = v.bias;
         p.epi = DEC_EPI_STORE;
@@ -3243,33 +3243,6 @@ qtts_status dec_transposed_mfma(qtts_decoder *d, const qtts_conv_view &v, const 
         p.phase = r;
         launch_dec_conv_mfma(d->ctx->stream, p);
         QTTS_TRY(check_launch(d->ctx, "k_dec_conv_mfma"));
-    }
-    return QTTS_OK;
-}
-
-// conv_transpose1d + the causal right crop (src/conv.rs:198-268,
-// src/decoder.rs:430-444): one launch per output phase r, out[o = q*s + r].
-qtts_status dec_transposed(qtts_decoder *d, const qtts_conv_view &v, const float *x, int len, float *c) {
-    const int J = v.kernel_size / v.stride, out_len = len * v.stride;
-    for (int r = 0; r < v.stride; r++) {
-        DecGemmParams p = dec_gemm_base(v.out_channels, len, v.in_channels * J);
-        p.a_mode = DEC_A_CONVT;
-        p.a = v.weight;
-        p.a_kfast = 0;
-        p.b_mode = DEC_B_CONVT;
-        p.b = x;
-        p.ksize = v.kernel_size;
-        p.taps = J;
-        p.stride = v.stride;
-        p.phase = r;
-        p.in_len = len;
-        p.bias_m = v.bias;
-        p.c = c;
-        p.scm = out_len;
-        p.scn = 1;
-        p.out_stride = v.stride;
-        launch_dec_gemm(d->ctx->stream, p);
-        QTTS_TRY(check_launch(d->ctx, "k_dec_gemm"));
     }
     return QTTS_OK;
 }
@@ -3309,6 +3282,21 @@ qtts_status dec_decode(qtts_decoder *d, const uint32_t *d_codes, int T, int ld, 
     float *P1 = dec_buf(d, 14, std::max<size_t>(inner_max, 1), &s);
     if (s != QTTS_OK) return s;
 
+    // Every matrix-core layer scales its input by a power of two from the
+    // input's max |x|, gathered into a fresh group of slots (cleared here).
+    launch_dec_fill_u32(st, d->amax, d->amax_slots * kDecMaxSlots, 0u);
+    QTTS_TRY(check_launch(c, "k_dec_fill_u32"));
+    int slot = 0;
+    auto take = [&]() -> unsigned * {
+        return slot < d->amax_slots ? d->amax + (size_t)(slot++) * kDecMaxSlots : nullptr;
+    };
+    auto maxof = [&](const float *x, size_t n, unsigned **out) -> qtts_status {
+        *out = take();
+        if (!*out) return fail(c, QTTS_EDEVICE, "decoder: more matrix-core inputs than max slots");
+        launch_dec_absmax(st, x, n, *out);
+        return check_launch(c, "k_dec_absmax");
+    };
+    unsigned *mx = nullptr, *mx2 = nullptr;
     // 1. codebook lookup -> S0 [vq][T] (src/decoder.rs:142-189)
     DecGatherParams g{};
     g.codes = d_codes;
@@ -3323,12 +3311,16 @@ qtts_status dec_decode(qtts_decoder *d, const uint32_t *d_codes, int T, int ld, 
     g.status = d->status;
     launch_dec_gather(st, g, T);
     QTTS_TRY(check_launch(c, "k_dec_gather"));
-    QTTS_TRY(dec_linear(d, E0, cd, 1, T, w.first_output_proj, cd, vq, nullptr, S0, 1, T, DEC_EPI_STORE));
-    QTTS_TRY(dec_linear(d, ES, cd, 1, T, w.rest_output_proj, cd, vq, nullptr, S0, 1, T, DEC_EPI_ACCUM));
+    QTTS_TRY(maxof(E0, (size_t)T * cd, &mx));
+    QTTS_TRY(maxof(ES, (size_t)T * cd, &mx2));
+    QTTS_TRY(dec_linear_mfma(d, d->proj0, E0, cd, 1, T, cd, vq, mx, nullptr, S0, 1, T, DEC_EPI_STORE));
+    QTTS_TRY(dec_linear_mfma(d, d->proj_rest, ES, cd, 1, T, cd, vq, mx2, nullptr, S0, 1, T, DEC_EPI_ACCUM));
     // 2. pre-conv -> S1 [lat][T]
-    QTTS_TRY(dec_causal(d, w.pre_conv, S0, T, S1, DEC_EPI_STORE));
+    QTTS_TRY(maxof(S0, (size_t)vq * T, &mx));
+    QTTS_TRY(dec_causal_mfma(d, w.pre_conv, d->pre_conv, S0, mx, T, S1, DEC_EPI_STORE));
     // 3. transformer (src/decoder.rs:195-330) -> S0 [lat][T]
-    QTTS_TRY(dec_linear(d, S1, 1, T, T, w.tf_input_w, lat, hid, w.tf_input_b, X, hid, 1, DEC_EPI_STORE));
+    QTTS_TRY(maxof(S1, (size_t)lat * T, &mx));
+    QTTS_TRY(dec_linear_mfma(d, d->tf_in, S1, 1, T, T, lat, hid, mx, w.tf_input_b, X, hid, 1, DEC_EPI_STORE));
     DecAttnParams a{};
     a.q = Q;
     a.k = K;
@@ -3339,30 +3331,37 @@ qtts_status dec_decode(qtts_decoder *d, const uint32_t *d_codes, int T, int ld, 
     a.hd = w.head_dim;
     a.window = w.sliding_window;
     a.scale = 1.0f / sqrtf((float)w.head_dim);
-    for (const auto &L : d->layers) {
+    for (size_t li = 0; li < d->layers.size(); li++) {
+        const qtts_dec_layer_view &L = d->layers[li];
+        const std::array<DecConvMfma, 7> &lm = d->layer_mfma[li];
         launch_dec_rmsnorm(st, X, L.input_norm, T, hid, 1e-5f, XN);
         QTTS_TRY(check_launch(c, "k_dec_rmsnorm"));
-        QTTS_TRY(dec_linear(d, XN, hid, 1, T, L.q_proj, hid, ad, nullptr, Q, ad, 1, DEC_EPI_STORE));
-        QTTS_TRY(dec_linear(d, XN, hid, 1, T, L.k_proj, hid, ad, nullptr, K, ad, 1, DEC_EPI_STORE));
-        QTTS_TRY(dec_linear(d, XN, hid, 1, T, L.v_proj, hid, ad, nullptr, V, ad, 1, DEC_EPI_STORE));
+        QTTS_TRY(maxof(XN, (size_t)T * hid, &mx));
+        QTTS_TRY(dec_linear_mfma(d, lm[0], XN, hid, 1, T, hid, ad, mx, nullptr, Q, ad, 1, DEC_EPI_STORE));
+        QTTS_TRY(dec_linear_mfma(d, lm[1], XN, hid, 1, T, hid, ad, mx, nullptr, K, ad, 1, DEC_EPI_STORE));
+        QTTS_TRY(dec_linear_mfma(d, lm[2], XN, hid, 1, T, hid, ad, mx, nullptr, V, ad, 1, DEC_EPI_STORE));
         launch_dec_rope(st, Q, K, T, w.num_heads, w.head_dim, w.rope_cos, w.rope_sin, w.rope_rows);
         QTTS_TRY(check_launch(c, "k_dec_rope"));
         launch_dec_attn(st, a);
         QTTS_TRY(check_launch(c, "k_dec_attn"));
-        QTTS_TRY(dec_linear(d, AO, ad, 1, T, L.o_proj, ad, hid, nullptr, X, hid, 1, DEC_EPI_SCALED_RESID,
-                            L.attn_scale));
+        QTTS_TRY(maxof(AO, (size_t)T * ad, &mx));
+        QTTS_TRY(dec_linear_mfma(d, lm[3], AO, ad, 1, T, ad, hid, mx, nullptr, X, hid, 1, DEC_EPI_SCALED_RESID,
+                                 L.attn_scale));
         launch_dec_rmsnorm(st, X, L.post_attn_norm, T, hid, 1e-5f, XN);
         QTTS_TRY(check_launch(c, "k_dec_rmsnorm"));
-        QTTS_TRY(dec_linear(d, XN, hid, 1, T, L.gate_proj, hid, inter, nullptr, G, inter, 1, DEC_EPI_STORE));
-        QTTS_TRY(dec_linear(d, XN, hid, 1, T, L.up_proj, hid, inter, nullptr, U, inter, 1, DEC_EPI_STORE));
+        QTTS_TRY(maxof(XN, (size_t)T * hid, &mx));
+        QTTS_TRY(dec_linear_mfma(d, lm[4], XN, hid, 1, T, hid, inter, mx, nullptr, G, inter, 1, DEC_EPI_STORE));
+        QTTS_TRY(dec_linear_mfma(d, lm[5], XN, hid, 1, T, hid, inter, mx, nullptr, U, inter, 1, DEC_EPI_STORE));
         launch_dec_swiglu(st, G, U, (size_t)T * inter, G);
         QTTS_TRY(check_launch(c, "k_dec_swiglu"));
-        QTTS_TRY(dec_linear(d, G, inter, 1, T, L.down_proj, inter, hid, nullptr, X, hid, 1, DEC_EPI_SCALED_RESID,
-                            L.mlp_scale));
+        QTTS_TRY(maxof(G, (size_t)T * inter, &mx));
+        QTTS_TRY(dec_linear_mfma(d, lm[6], G, inter, 1, T, inter, hid, mx, nullptr, X, hid, 1, DEC_EPI_SCALED_RESID,
+                                 L.mlp_scale));
     }
     launch_dec_rmsnorm(st, X, w.tf_norm, T, hid, 1e-5f, XN);
     QTTS_TRY(check_launch(c, "k_dec_rmsnorm"));
-    QTTS_TRY(dec_linear(d, XN, hid, 1, T, w.tf_output_w, hid, lat, w.tf_output_b, S0, 1, T, DEC_EPI_STORE));
+    QTTS_TRY(maxof(XN, (size_t)T * hid, &mx));
+    QTTS_TRY(dec_linear_mfma(d, d->tf_out, XN, hid, 1, T, hid, lat, mx, w.tf_output_b, S0, 1, T, DEC_EPI_STORE));
     // 4. upsample: transposed conv + ConvNeXt (src/decoder.rs:336-388, 424-448)
     float *const pool[4] = {S0, S1, S2, S3};
     auto other = [&](const float *a, const float *b = nullptr, const float *c3 = nullptr) {
@@ -3372,39 +3371,38 @@ qtts_status dec_decode(qtts_decoder *d, const uint32_t *d_codes, int T, int ld, 
     };
     float *sig = S0;
     int L = T;
-    for (const auto &u : d->upsample) {
+    for (size_t ui = 0; ui < d->upsample.size(); ui++) {
+        const qtts_upsample_view &u = d->upsample[ui];
         float *up = other(sig), *dw = other(sig, up), *nrm = other(sig, up, dw);
-        QTTS_TRY(dec_transposed(d, u.conv_t, sig, L, up));
+        QTTS_TRY(maxof(sig, (size_t)u.channels * L, &mx));
+        QTTS_TRY(dec_transposed_mfma(d, u.conv_t, d->cnx_up_mfma[ui], sig, mx, L, up));
         L *= u.conv_t.stride;
         launch_dec_dwconv(st, up, u.dw_conv.weight, u.dw_conv.bias, u.channels, L, u.dw_conv.kernel_size, dw);
         QTTS_TRY(check_launch(c, "k_dec_dwconv"));
         launch_dec_lnorm(st, dw, u.norm_w, u.norm_b, u.channels, L, 1e-5f, nrm);
         QTTS_TRY(check_launch(c, "k_dec_lnorm"));
-        QTTS_TRY(dec_linear(d, nrm, 1, L, L, u.pw1_w, u.channels, u.inner_dim, u.pw1_b, P1, u.inner_dim, 1,
-                            DEC_EPI_STORE, nullptr, nullptr, DEC_ACT_GELU));
+        QTTS_TRY(maxof(nrm, (size_t)u.channels * L, &mx));
+        QTTS_TRY(dec_linear_mfma(d, d->pw_mfma[ui][0], nrm, 1, L, L, u.channels, u.inner_dim, mx, u.pw1_b, P1,
+                                 u.inner_dim, 1, DEC_EPI_STORE, nullptr, nullptr, DEC_ACT_GELU));
         // out = residual + gamma * pw2 (the residual is the stage input `up`)
-        QTTS_TRY(dec_linear(d, P1, u.inner_dim, 1, L, u.pw2_w, u.inner_dim, u.channels, u.pw2_b, dw, 1, L,
-                            DEC_EPI_RESID_IN, u.gamma, up));
+        QTTS_TRY(maxof(P1, (size_t)L * u.inner_dim, &mx));
+        QTTS_TRY(dec_linear_mfma(d, d->pw_mfma[ui][1], P1, u.inner_dim, 1, L, u.inner_dim, u.channels, mx, u.pw2_b,
+                                 dw, 1, L, DEC_EPI_RESID_IN, u.gamma, up));
         sig = dw;
     }
     // 5. Vocos (src/decoder.rs:450-495)
     {
         float *o = other(sig);
-        QTTS_TRY(dec_causal(d, w.vocos_init, sig, L, o, DEC_EPI_STORE));
+        QTTS_TRY(maxof(sig, (size_t)w.vocos_init.in_channels * L, &mx));
+        QTTS_TRY(dec_causal_mfma(d, w.vocos_init, d->vocos_init, sig, mx, L, o, DEC_EPI_STORE));
         sig = o;
     }
-    // the residual convolutions' input maxima start at zero in every decode
-    if (d->amax_slots > 0) {
-        launch_dec_fill_u32(st, d->amax, d->amax_slots * kDecMaxSlots, 0u);
-        QTTS_TRY(check_launch(c, "k_dec_fill_u32"));
-    }
-    int slot = 0;
     for (size_t bi = 0; bi < d->blocks.size(); bi++) {
         const qtts_vocos_block_view &b = d->blocks[bi];
         const int cin = b.upsample.in_channels, cout = b.upsample.out_channels;
         float *t1 = other(sig), *nxt = other(sig, t1);
-        unsigned *m0 = d->amax + (size_t)slot * kDecMaxSlots;
-        slot += 1;
+        unsigned *m0 = take();
+        if (!m0) return fail(c, QTTS_EDEVICE, "decoder: more matrix-core inputs than max slots");
         launch_dec_snake(st, sig, b.pre_snake_alpha, b.pre_snake_beta, cin, L, t1, m0);
         QTTS_TRY(check_launch(c, "k_dec_snake"));
         QTTS_TRY(dec_transposed_mfma(d, b.upsample, d->up_mfma[bi], t1, m0, L, nxt));
@@ -3414,8 +3412,8 @@ qtts_status dec_decode(qtts_decoder *d, const uint32_t *d_codes, int T, int ld, 
         for (int r = 0; r < b.num_residuals; r++) {
             const qtts_vocos_residual_view &rv = b.residuals[r];
             const std::array<DecConvMfma, 2> &mc = d->res_mfma[bi][(size_t)r];
-            unsigned *m1 = d->amax + (size_t)slot * kDecMaxSlots, *m2 = m1 + kDecMaxSlots;
-            slot += 2;
+            unsigned *m1 = take(), *m2 = take();
+            if (!m1 || !m2) return fail(c, QTTS_EDEVICE, "decoder: more matrix-core inputs than max slots");
             launch_dec_snake(st, sig, rv.act1_alpha, rv.act1_beta, cout, L, t1, m1);
             QTTS_TRY(check_launch(c, "k_dec_snake"));
             QTTS_TRY(dec_causal_mfma(d, rv.conv1, mc[0], t1, m1, L, t2, DEC_EPI_STORE));
@@ -3427,9 +3425,11 @@ qtts_status dec_decode(qtts_decoder *d, const uint32_t *d_codes, int T, int ld, 
     }
     float *t1 = other(sig);
     // 6. final SnakeBeta, output conv, clamp to [-1, 1]
-    launch_dec_snake(st, sig, w.final_snake_alpha, w.final_snake_beta, w.output_conv.in_channels, L, t1);
+    unsigned *mf = take();
+    if (!mf) return fail(c, QTTS_EDEVICE, "decoder: more matrix-core inputs than max slots");
+    launch_dec_snake(st, sig, w.final_snake_alpha, w.final_snake_beta, w.output_conv.in_channels, L, t1, mf);
     QTTS_TRY(check_launch(c, "k_dec_snake"));
-    QTTS_TRY(dec_causal(d, w.output_conv, t1, L, d_audio, DEC_EPI_CLAMP));
+    QTTS_TRY(dec_causal_mfma(d, w.output_conv, d->out_conv, t1, mf, L, d_audio, DEC_EPI_CLAMP));
     *n_samples = (int64_t)L * w.output_conv.out_channels;
     return QTTS_OK;
 }
@@ -3469,6 +3469,9 @@ qtts_status qtts_decoder_upload(qtts_ctx *c, const qtts_decoder_view *v, qtts_de
         (s = up(v->first_output_proj, (size_t)cd * vq, &w.first_output_proj, "first_output_proj")) != QTTS_OK ||
         (s = up(v->rest_output_proj, (size_t)cd * vq, &w.rest_output_proj, "rest_output_proj")) != QTTS_OK)
         return bail(s);
+    if ((s = dec_lin_mfma(c, o, v->first_output_proj, w.first_output_proj, cd, vq, &d->proj0)) != QTTS_OK ||
+        (s = dec_lin_mfma(c, o, v->rest_output_proj, w.rest_output_proj, cd, vq, &d->proj_rest)) != QTTS_OK)
+        return bail(s);
     std::vector<const float *> rest((size_t)std::max(v->num_rest, 1), nullptr);
     for (int g = 0; g < v->num_rest; g++)
         if (!v->rest_codebooks || (s = up(v->rest_codebooks[g], cbn, &rest[g], "rest_codebook")) != QTTS_OK)
@@ -3477,12 +3480,16 @@ qtts_status qtts_decoder_upload(qtts_ctx *c, const qtts_decoder_view *v, qtts_de
     if (hipMemcpy(d->rest_dev, rest.data(), rest.size() * sizeof(float *), hipMemcpyHostToDevice) != hipSuccess)
         return bail(fail(c, QTTS_EDEVICE, "hipMemcpy"));
     w.rest_codebooks = nullptr;
-    if ((s = dec_conv(c, o, v->pre_conv, false, &w.pre_conv, "pre_conv")) != QTTS_OK) return bail(s);
+    if ((s = dec_conv(c, o, v->pre_conv, false, &w.pre_conv, "pre_conv")) != QTTS_OK ||
+        (s = dec_conv_mfma(c, o, v->pre_conv, w.pre_conv, &d->pre_conv)) != QTTS_OK)
+        return bail(s);
     if ((s = up(v->tf_input_w, (size_t)lat * hid, &w.tf_input_w, "tf_input_w")) != QTTS_OK ||
         (s = up(v->tf_input_b, (size_t)hid, &w.tf_input_b, "tf_input_b")) != QTTS_OK ||
         (s = up(v->tf_norm, (size_t)hid, &w.tf_norm, "tf_norm")) != QTTS_OK ||
         (s = up(v->tf_output_w, (size_t)hid * lat, &w.tf_output_w, "tf_output_w")) != QTTS_OK ||
-        (s = up(v->tf_output_b, (size_t)lat, &w.tf_output_b, "tf_output_b")) != QTTS_OK)
+        (s = up(v->tf_output_b, (size_t)lat, &w.tf_output_b, "tf_output_b")) != QTTS_OK ||
+        (s = dec_lin_mfma(c, o, v->tf_input_w, w.tf_input_w, lat, hid, &d->tf_in)) != QTTS_OK ||
+        (s = dec_lin_mfma(c, o, v->tf_output_w, w.tf_output_w, hid, lat, &d->tf_out)) != QTTS_OK)
         return bail(s);
     for (int l = 0; l < v->num_layers; l++) {
         const qtts_dec_layer_view &L = v->layers[l];
@@ -3499,6 +3506,17 @@ qtts_status qtts_decoder_upload(qtts_ctx *c, const qtts_decoder_view *v, qtts_de
             (s = up(L.attn_scale, (size_t)hid, &D.attn_scale, "attn_scale")) != QTTS_OK ||
             (s = up(L.mlp_scale, (size_t)hid, &D.mlp_scale, "mlp_scale")) != QTTS_OK)
             return bail(s);
+        std::array<DecConvMfma, 7> lm{};
+        if ((s = dec_lin_mfma(c, o, L.q_proj, D.q_proj, hid, ad, &lm[0])) != QTTS_OK ||
+            (s = dec_lin_mfma(c, o, L.k_proj, D.k_proj, hid, ad, &lm[1])) != QTTS_OK ||
+            (s = dec_lin_mfma(c, o, L.v_proj, D.v_proj, hid, ad, &lm[2])) != QTTS_OK ||
+            (s = dec_lin_mfma(c, o, L.o_proj, D.o_proj, ad, hid, &lm[3])) != QTTS_OK ||
+            (s = dec_lin_mfma(c, o, L.gate_proj, D.gate_proj, hid, inter, &lm[4])) != QTTS_OK ||
+            (s = dec_lin_mfma(c, o, L.up_proj, D.up_proj, hid, inter, &lm[5])) != QTTS_OK ||
+            (s = dec_lin_mfma(c, o, L.down_proj, D.down_proj, inter, hid, &lm[6])) != QTTS_OK)
+            return bail(s);
+        d->layer_mfma.push_back(lm);
+        d->amax_slots += 4;  // the normed rows twice, the attention output, SiLU(gate) * up
         d->layers.push_back(D);
     }
     w.layers = nullptr;
@@ -3519,11 +3537,22 @@ qtts_status qtts_decoder_upload(qtts_ctx *c, const qtts_decoder_view *v, qtts_de
             (s = up(U.pw2_b, (size_t)ch, &D.pw2_b, "pw2_b")) != QTTS_OK ||
             (s = up(U.gamma, (size_t)ch, &D.gamma, "gamma")) != QTTS_OK)
             return bail(s);
+        std::vector<DecConvMfma> ph;
+        std::array<DecConvMfma, 2> pw{};
+        if ((s = dec_convt_mfma(c, o, U.conv_t, D.conv_t, &ph)) != QTTS_OK ||
+            (s = dec_lin_mfma(c, o, U.pw1_w, D.pw1_w, ch, U.inner_dim, &pw[0])) != QTTS_OK ||
+            (s = dec_lin_mfma(c, o, U.pw2_w, D.pw2_w, U.inner_dim, ch, &pw[1])) != QTTS_OK)
+            return bail(s);
+        d->cnx_up_mfma.push_back(ph);
+        d->pw_mfma.push_back(pw);
+        d->amax_slots += 3;  // the stage input, the LayerNorm output, GELU(pw1)
         d->upsample.push_back(D);
     }
     w.upsample = nullptr;
     if (v->vocos_init.in_channels != ch) return bail(fail(c, QTTS_ESHAPE, "decoder: vocos_init input channels"));
-    if ((s = dec_conv(c, o, v->vocos_init, false, &w.vocos_init, "vocos_init")) != QTTS_OK) return bail(s);
+    if ((s = dec_conv(c, o, v->vocos_init, false, &w.vocos_init, "vocos_init")) != QTTS_OK ||
+        (s = dec_conv_mfma(c, o, v->vocos_init, w.vocos_init, &d->vocos_init)) != QTTS_OK)
+        return bail(s);
     ch = v->vocos_init.out_channels;
     d->residuals.resize((size_t)std::max(v->num_vocos_blocks, 0));
     d->res_mfma.resize(d->residuals.size());
@@ -3567,8 +3596,12 @@ qtts_status qtts_decoder_upload(qtts_ctx *c, const qtts_decoder_view *v, qtts_de
     if (v->output_conv.in_channels != ch) return bail(fail(c, QTTS_ESHAPE, "decoder: output_conv input channels"));
     if ((s = up(v->final_snake_alpha, (size_t)ch, &w.final_snake_alpha, "final_snake_alpha")) != QTTS_OK ||
         (s = up(v->final_snake_beta, (size_t)ch, &w.final_snake_beta, "final_snake_beta")) != QTTS_OK ||
-        (s = dec_conv(c, o, v->output_conv, false, &w.output_conv, "output_conv")) != QTTS_OK)
+        (s = dec_conv(c, o, v->output_conv, false, &w.output_conv, "output_conv")) != QTTS_OK ||
+        (s = dec_conv_mfma(c, o, v->output_conv, w.output_conv, &d->out_conv)) != QTTS_OK)
         return bail(s);
+    // the codebook rows (two), the pre-conv input and output, the
+    // transformer's output rows, the Vocos input and the final SnakeBeta
+    d->amax_slots += 7;
     const size_t rn = (size_t)v->rope_rows * (v->head_dim / 2);
     if (rn) {
         if ((s = up(v->rope_cos, rn, &w.rope_cos, "rope_cos")) != QTTS_OK ||

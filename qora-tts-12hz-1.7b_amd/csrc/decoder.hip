@@ -3,11 +3,6 @@
 //
 //  k_dec_gather   codebook rows of every frame: group 0's, and the sum of
 //                 the other groups' in group order (src/decoder.rs:142-189)
-//  k_dec_gemm     one f32 tile GEMM for every projection and convolution:
-//                 64 x 64 output tiles, 16-deep K slices staged in LDS, 4 x 4
-//                 outputs per thread; operands are strided views or gathers
-//                 (a causal convolution's shifted input rows; one output
-//                 phase of a transposed convolution), with fused epilogues
 //  k_dec_rmsnorm  rms_norm_f32 per frame (src/decoder.rs:515-525)
 //  k_dec_rope     apply_rope_split_half of q and k (src/decoder.rs:556-578)
 //  k_dec_attn     causal sliding-window attention, one wave per (frame, head)
@@ -17,8 +12,12 @@
 //                 order (src/decoder.rs:580-602)
 //  k_dec_snake    SnakeBeta (src/conv.rs:347-400), optionally recording
 //                 max |out| for the convolution that reads it
-//  k_dec_conv_mfma  a causal convolution on the matrix cores
-//                 (v_mfma_f32_32x32x16_f16 with binary16 hi + lo operands)
+//  k_dec_conv_mfma  every projection and convolution on the matrix cores
+//                 (v_mfma_f32_32x32x16_f16 with binary16 hi + lo operands):
+//                 causal convolutions as implicit GEMMs, one output phase
+//                 of a transposed convolution, linear layers as one tap;
+//                 fused epilogues
+//  k_dec_absmax   max |x| of a layer input (the operand scale)
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -32,7 +31,6 @@ namespace qtts {
 
 namespace {
 
-constexpr int TM = 64, TN = 64, TK = 16;
 constexpr unsigned kSnakeBlocks = 8192;  // SnakeBeta grid cap (threads stride through the tensor)
 #ifndef QTTS_DEC_CONV_TILES
 #define QTTS_DEC_CONV_TILES 1
@@ -61,96 +59,8 @@ __global__ void k_dec_gather(DecGatherParams P) {
     }
 }
 
-// A(m, k) and B(k, n) of the GEMM.
-__device__ __forceinline__ float dec_a(const DecGemmParams &P, int m, int k) {
-    if (m >= P.M || k >= P.K) return 0.0f;
-    if (P.a_mode == DEC_A_STRIDED) return P.a[(size_t)m * P.sam + (size_t)k * P.sak];
-    // DEC_A_CONVT: W[ci][m][phase + j * stride], k = ci * J + j
-    const int ci = k / P.taps, j = k - ci * P.taps;
-    return P.a[((size_t)ci * P.M + m) * P.ksize + P.phase + j * P.stride];
-}
-
-__device__ __forceinline__ float dec_b(const DecGemmParams &P, int k, int n) {
-    if (k >= P.K || n >= P.N) return 0.0f;
-    if (P.b_mode == DEC_B_STRIDED) return P.b[(size_t)k * P.sbk + (size_t)n * P.sbn];
-    if (P.b_mode == DEC_B_CONV) {
-        // causal convolution: x[ci][n + tap * dilation - (ksize - 1) * dilation]
-        const int ci = k / P.ksize, tap = k - ci * P.ksize;
-        const int p = n + (tap - (P.ksize - 1)) * P.dilation;
-        return p >= 0 ? P.b[(size_t)ci * P.in_len + p] : 0.0f;
-    }
-    // DEC_B_CONVT: x[ci][n - j], k = ci * J + j
-    const int ci = k / P.taps, j = k - ci * P.taps;
-    const int p = n - j;
-    return (p >= 0 && p < P.in_len) ? P.b[(size_t)ci * P.in_len + p] : 0.0f;
-}
-
+// GELU, the tanh form the reference uses.
 __device__ __forceinline__ float dec_gelu(float x) { return x * 0.5f * (1.0f + tanhf(x * 0.7071067811865476f)); }
-
-__global__ __launch_bounds__(256) void k_dec_gemm(DecGemmParams P) {
-    __shared__ float As[TK][TM + 4];
-    __shared__ float Bs[TK][TN + 4];
-    const int tid = threadIdx.x;
-    const int m0 = blockIdx.y * TM, n0 = blockIdx.x * TN;
-    const int tm = (tid >> 4) * 4, tn = (tid & 15) * 4;
-    float acc[4][4] = {};
-    for (int k0 = 0; k0 < P.K; k0 += TK) {
-        // 1024 A and 1024 B values per slice, 4 per thread; consecutive
-        // threads take consecutive addresses of the operand's fast index
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int e = tid + 256 * i;
-            int mm, kk;
-            if (P.a_kfast) {
-                kk = e & (TK - 1);
-                mm = e >> 4;
-            } else {
-                mm = e & (TM - 1);
-                kk = e >> 6;
-            }
-            As[kk][mm] = dec_a(P, m0 + mm, k0 + kk);
-            const int nn = e & (TN - 1), kb = e >> 6;
-            Bs[kb][nn] = dec_b(P, k0 + kb, n0 + nn);
-        }
-        __syncthreads();
-#pragma unroll
-        for (int kk = 0; kk < TK; kk++) {
-            const float4 a = *reinterpret_cast<const float4 *>(&As[kk][tm]);
-            const float4 b = *reinterpret_cast<const float4 *>(&Bs[kk][tn]);
-            const float av[4] = {a.x, a.y, a.z, a.w}, bv[4] = {b.x, b.y, b.z, b.w};
-#pragma unroll
-            for (int i = 0; i < 4; i++)
-#pragma unroll
-                for (int j = 0; j < 4; j++) acc[i][j] += av[i] * bv[j];
-        }
-        __syncthreads();
-    }
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        const int m = m0 + tm + i;
-        if (m >= P.M) continue;
-#pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int n = n0 + tn + j;
-            if (n >= P.N) continue;
-            float v = acc[i][j];
-            if (P.bias_m) v += P.bias_m[m];
-            if (P.bias_n) v += P.bias_n[n];
-            if (P.act == DEC_ACT_GELU) v = dec_gelu(v);
-            const int col = P.out_stride ? n * P.out_stride + P.phase : n;
-            float *dst = P.c + (size_t)m * P.scm + (size_t)col * P.scn;
-            switch (P.epi) {
-                case DEC_EPI_STORE: *dst = v; break;
-                case DEC_EPI_ACCUM: *dst += v; break;
-                case DEC_EPI_SCALED_RESID: *dst += P.scale_n[n] * v; break;
-                case DEC_EPI_RESID_IN:
-                    *dst = P.resid[(size_t)m * P.scm + (size_t)col * P.scn] + (P.scale_n ? P.scale_n[n] * v : v);
-                    break;
-                default: *dst = v < -1.0f ? -1.0f : (v > 1.0f ? 1.0f : v); break;  // DEC_EPI_CLAMP (NaN stays)
-            }
-        }
-    }
-}
 
 // rms_norm_f32 of each of `rows` rows of n values: one block per row.
 __global__ __launch_bounds__(256) void k_dec_rmsnorm(const float *x, const float *gamma, int n, float eps, float *out) {
@@ -247,20 +157,40 @@ __global__ void k_dec_dwconv(const float *x, const float *w, const float *b, int
 }
 
 // LayerNorm across channels at each time step (one thread per step; the
-// channel sums run in channel order).
-__global__ void k_dec_lnorm(const float *x, const float *g, const float *b, int ch, int len, float eps, float *out) {
+// channel sums run in channel order, 8 channels' loads issued together).
+__global__ __launch_bounds__(64) void k_dec_lnorm(const float *x, const float *g, const float *b, int ch, int len,
+                                                  float eps, float *out) {
     const int t = blockIdx.x * blockDim.x + threadIdx.x;
     if (t >= len) return;
+    const float *xt = x + t;
     float mean = 0.0f;
-    for (int c = 0; c < ch; c++) mean += x[(size_t)c * len + t];
+    int c = 0;
+    for (; c + 8 <= ch; c += 8) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = xt[(size_t)(c + i) * len];
+#pragma unroll
+        for (int i = 0; i < 8; i++) mean += v[i];
+    }
+    for (; c < ch; c++) mean += xt[(size_t)c * len];
     mean /= (float)ch;
     float var = 0.0f;
-    for (int c = 0; c < ch; c++) {
-        const float d = x[(size_t)c * len + t] - mean;
+    for (c = 0; c + 8 <= ch; c += 8) {
+        float v[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) v[i] = xt[(size_t)(c + i) * len];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const float d = v[i] - mean;
+            var += d * d;
+        }
+    }
+    for (; c < ch; c++) {
+        const float d = xt[(size_t)c * len] - mean;
         var += d * d;
     }
     const float inv = 1.0f / sqrtf(var / (float)ch + eps);
-    for (int c = 0; c < ch; c++) out[(size_t)c * len + t] = (x[(size_t)c * len + t] - mean) * inv * g[c] + b[c];
+    for (c = 0; c < ch; c++) out[(size_t)c * len + t] = (xt[(size_t)c * len] - mean) * inv * g[c] + b[c];
 }
 
 // x + exp(-beta) * sin(exp(alpha) * x)^2 per channel, channel-first, over a
@@ -296,6 +226,22 @@ __global__ __launch_bounds__(256) void k_dec_snake(const float *x, const float *
 __global__ void k_dec_fill_u32(unsigned *p, int n, unsigned v) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i < n) p[i] = v;
+}
+
+// max |x| of n values into the kDecMaxSlots slots of amax, as k_dec_snake
+// records it (for inputs of the matrix-core layers that no SnakeBeta makes).
+__global__ __launch_bounds__(256) void k_dec_absmax(const float *x, size_t n, unsigned *amax) {
+    float m = 0.0f;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        m = fmaxf(m, fabsf(x[i]));
+    __shared__ float red[4];
+    m = wave_max(m);
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        atomicMax(&amax[blockIdx.x % kDecMaxSlots], __float_as_uint(m));
+    }
 }
 
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
@@ -357,7 +303,7 @@ __global__ void k_dec_conv_repack(const float *w, long long sm, long long sci, i
 // and the two splits leave a relative error of about 2^-21 per term, the
 // f32 level.  The next step's operands are loaded before the current
 // step's MFMAs.
-template <int MT, int NT>
+template <int MT, int NT, bool KF>  // KF: channels contiguous (sxc == 1, cin % 8 == 0)
 __global__ __launch_bounds__(256) void k_dec_conv_mfma(DecConvMfmaParams P) {
     static_assert(kDecMaxSlots == 64, "one max slot per lane");
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -381,9 +327,17 @@ __global__ __launch_bounds__(256) void k_dec_conv_mfma(DecConvMfmaParams P) {
         for (int j = 0; j < NT; j++) {
             const int n = nb + 32 * j, p = n + off;
             const bool ok = n < len && p >= 0 && chan_ok;
-            const float *xp = P.x + (size_t)(ci0 + 8 * half) * len + (ok ? p : 0);
+            const float *xp = P.x + (long long)(ci0 + 8 * half) * P.sxc + (long long)(ok ? p : 0) * P.sxn;
+            if constexpr (KF) {
+                // all 8 channels exist (cin % 8 == 0): two 16-byte loads
+                const float4 a = ok ? *reinterpret_cast<const float4 *>(xp) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                const float4 b = ok ? *reinterpret_cast<const float4 *>(xp + 4) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                xv[j][0] = a.x, xv[j][1] = a.y, xv[j][2] = a.z, xv[j][3] = a.w;
+                xv[j][4] = b.x, xv[j][5] = b.y, xv[j][6] = b.z, xv[j][7] = b.w;
+            } else {
 #pragma unroll
-            for (int i = 0; i < 8; i++) xv[j][i] = ok && ci0 + i < cpl ? xp[(size_t)i * len] : 0.0f;
+                for (int i = 0; i < 8; i++) xv[j][i] = ok && ci0 + i < cpl ? xp[(long long)i * P.sxc] : 0.0f;
+            }
         }
 #pragma unroll
         for (int t = 0; t < MT; t++) {
@@ -446,9 +400,19 @@ __global__ __launch_bounds__(256) void k_dec_conv_mfma(DecConvMfmaParams P) {
             for (int r = 0; r < 16; r++) {
                 const int m = 32 * (t0 + t) + (r >> 2) * 8 + half * 4 + (r & 3);
                 if (m >= P.M) continue;
-                const float v = ldexpf(acc[t][j][r], sc) + P.bias[m];
-                const size_t o = (size_t)m * P.ldc + (size_t)n * P.out_stride + P.phase;
-                P.c[o] = P.epi == DEC_EPI_RESID_IN ? P.resid[o] + v : v;
+                float v = ldexpf(acc[t][j][r], sc);
+                if (P.bias) v += P.bias[m];
+                if (P.act == DEC_ACT_GELU) v = dec_gelu(v);
+                float *dst = P.c + (long long)m * P.ldc + (long long)n * P.out_stride + P.phase;
+                switch (P.epi) {
+                    case DEC_EPI_STORE: *dst = v; break;
+                    case DEC_EPI_ACCUM: *dst += v; break;
+                    case DEC_EPI_SCALED_RESID: *dst += P.scale[m] * v; break;
+                    case DEC_EPI_RESID_IN:
+                        *dst = P.resid[dst - P.c] + (P.scale ? P.scale[m] * v : v);
+                        break;
+                    default: *dst = v < -1.0f ? -1.0f : (v > 1.0f ? 1.0f : v); break;  // DEC_EPI_CLAMP (NaN stays)
+                }
             }
     }
 }
@@ -459,11 +423,6 @@ unsigned blocks_for(size_t n, unsigned per) { return (unsigned)((n + per - 1) / 
 
 void launch_dec_gather(hipStream_t st, const DecGatherParams &p, int frames) {
     hipLaunchKernelGGL(k_dec_gather, dim3((unsigned)frames), dim3(256), 0, st, p);
-}
-
-void launch_dec_gemm(hipStream_t st, const DecGemmParams &p) {
-    const dim3 grid(blocks_for((size_t)p.N, TN), blocks_for((size_t)p.M, TM));
-    hipLaunchKernelGGL(k_dec_gemm, grid, dim3(256), 0, st, p);
 }
 
 void launch_dec_rmsnorm(hipStream_t st, const float *x, const float *gamma, int rows, int n, float eps, float *out) {
@@ -492,7 +451,7 @@ void launch_dec_dwconv(hipStream_t st, const float *x, const float *w, const flo
 
 void launch_dec_lnorm(hipStream_t st, const float *x, const float *g, const float *b, int ch, int len, float eps,
                       float *out) {
-    hipLaunchKernelGGL(k_dec_lnorm, dim3(blocks_for((size_t)len, 256)), dim3(256), 0, st, x, g, b, ch, len, eps, out);
+    hipLaunchKernelGGL(k_dec_lnorm, dim3(blocks_for((size_t)len, 64)), dim3(64), 0, st, x, g, b, ch, len, eps, out);
 }
 
 void launch_dec_snake(hipStream_t st, const float *x, const float *alpha, const float *beta, int ch, int len,
@@ -512,18 +471,33 @@ void launch_dec_conv_repack(hipStream_t st, const float *w, long long sm, long l
                        taps, cin16, mtiles, ksteps, ew, wh, wl);
 }
 
-// MT: the largest of 4, 3, 2, 1 that divides the tile count (a block's
-// tiles share each gathered B operand).
-void launch_dec_conv_mfma(hipStream_t st, const DecConvMfmaParams &p) {
+template <bool KF>
+static void launch_conv_mfma_kf(hipStream_t st, const DecConvMfmaParams &p, int mt) {
     constexpr int NT = kDecConvTiles;
-    const int mt = p.mtiles % 4 == 0 ? 4 : p.mtiles % 3 == 0 ? 3 : p.mtiles % 2 == 0 ? 2 : 1;
     const dim3 grid(blocks_for((size_t)p.len, 128 * NT), (unsigned)(p.mtiles / mt));
     switch (mt) {
-        case 4: hipLaunchKernelGGL((k_dec_conv_mfma<4, NT>), grid, dim3(256), 0, st, p); break;
-        case 3: hipLaunchKernelGGL((k_dec_conv_mfma<3, NT>), grid, dim3(256), 0, st, p); break;
-        case 2: hipLaunchKernelGGL((k_dec_conv_mfma<2, NT>), grid, dim3(256), 0, st, p); break;
-        default: hipLaunchKernelGGL((k_dec_conv_mfma<1, NT>), grid, dim3(256), 0, st, p); break;
+        case 4: hipLaunchKernelGGL((k_dec_conv_mfma<4, NT, KF>), grid, dim3(256), 0, st, p); break;
+        case 3: hipLaunchKernelGGL((k_dec_conv_mfma<3, NT, KF>), grid, dim3(256), 0, st, p); break;
+        case 2: hipLaunchKernelGGL((k_dec_conv_mfma<2, NT, KF>), grid, dim3(256), 0, st, p); break;
+        default: hipLaunchKernelGGL((k_dec_conv_mfma<1, NT, KF>), grid, dim3(256), 0, st, p); break;
     }
+}
+
+// MT: the largest of 4, 3, 2, 1 that divides the tile count (a block's
+// tiles share each gathered B operand), or 1 when fewer than 256 blocks
+// would fill the GPU otherwise.
+void launch_dec_conv_mfma(hipStream_t st, const DecConvMfmaParams &p) {
+    int mt = p.mtiles % 4 == 0 ? 4 : p.mtiles % 3 == 0 ? 3 : p.mtiles % 2 == 0 ? 2 : 1;
+    if ((size_t)blocks_for((size_t)p.len, 128 * kDecConvTiles) * (size_t)(p.mtiles / mt) < 256) mt = 1;
+    if (p.sxc == 1 && p.cin % 8 == 0 && p.sxn % 4 == 0 && ((uintptr_t)p.x & 15) == 0)
+        launch_conv_mfma_kf<true>(st, p, mt);
+    else
+        launch_conv_mfma_kf<false>(st, p, mt);
+}
+
+void launch_dec_absmax(hipStream_t st, const float *x, size_t n, unsigned *amax) {
+    const unsigned blocks = std::min<unsigned>(blocks_for(n, 256), 2048u);
+    hipLaunchKernelGGL(k_dec_absmax, dim3(blocks), dim3(256), 0, st, x, n, amax);
 }
 
 }  // namespace qtts

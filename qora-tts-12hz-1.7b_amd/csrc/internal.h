@@ -91,48 +91,33 @@ struct DecGatherParams {
     int *status;                 // set to 1 for a code >= cb_size
 };
 
-enum DecAMode { DEC_A_STRIDED = 0, DEC_A_CONVT = 1 };
-enum DecBMode { DEC_B_STRIDED = 0, DEC_B_CONV = 1, DEC_B_CONVT = 2 };
 enum DecAct { DEC_ACT_NONE = 0, DEC_ACT_GELU = 1 };
 enum DecEpi { DEC_EPI_STORE = 0, DEC_EPI_ACCUM = 1, DEC_EPI_SCALED_RESID = 2, DEC_EPI_RESID_IN = 3, DEC_EPI_CLAMP = 4 };
 
-// C(m, n) (epi)= act(sum_k A(m, k) B(k, n) + bias), C(m, n) at
-// c[m * scm + col * scn] with col = n, or n * out_stride + phase when
-// out_stride != 0 (one output phase of a transposed convolution).
-struct DecGemmParams {
-    int M, N, K;
-    int a_mode, b_mode, a_kfast;
-    const float *a;
-    long long sam, sak;  // DEC_A_STRIDED
-    const float *b;
-    long long sbk, sbn;  // DEC_B_STRIDED
-    int ksize, dilation, in_len;  // DEC_B_CONV: causal taps; DEC_*_CONVT: kernel size, input length
-    int taps, stride, phase;      // DEC_*_CONVT: taps per phase (ksize / stride), stride, output phase
-    const float *bias_m, *bias_n;
-    int act, epi;
-    float *c;
-    long long scm, scn;
-    int out_stride;
-    const float *scale_n;  // DEC_EPI_SCALED_RESID / DEC_EPI_RESID_IN
-    const float *resid;    // DEC_EPI_RESID_IN (same addressing as c)
-};
-
-// A causal convolution (implicit GEMM, as DEC_B_CONV) on the matrix cores:
-// weights pre-split into binary16 hi + lo in the MFMA A-operand order with
-// K ordered tap-major (k' = tap * cin16 + ci, the channels padded to a
-// multiple of 16 with zero weights), activations split on the fly.
+// A convolution or linear layer on the matrix cores (k_dec_conv_mfma) as a
+// causal convolution: output (m, n) = act(sum_{tap, ci} A(m, ci, tap) *
+// x(ci, n + (tap - (ksize - 1)) * dilation) + bias[m]) (x zero before n = 0),
+// combined into c by `epi` (STORE: =, ACCUM: +=, SCALED_RESID: += scale[m] *,
+// RESID_IN: = resid + scale[m] *, CLAMP: = clamp to [-1, 1]).  A: weights pre-split into
+// binary16 hi + lo in the MFMA A-operand order with K ordered tap-major
+// (k' = tap * cin16 + ci, the channels padded to a multiple of 16 with zero
+// weights); x(ci, p) = x[ci * sxc + p * sxn], split on the fly.  A linear
+// layer is the case ksize = 1 with m the output feature and n the row.
 struct DecConvMfmaParams {
     const _Float16 *wh, *wl;  // [mtiles][ksteps][64][8]; row m = 32 * tile + lane % 32
     int ew;                   // the weights were scaled by 2^ew
     int M, mtiles, ksteps;    // output channels, 32-row tiles, 16-row K steps (ksize * cin16 / 16)
-    int cin, cin16, ksize, dilation, len;
-    const float *x;           // [cin][len]
-    const unsigned *xmax;     // [kDecMaxSlots]: bits of max |x| over the slots (a producer's atomicMax)
-    const float *bias;        // [M]
-    int epi;                  // DEC_EPI_STORE or DEC_EPI_RESID_IN
+    int cin, cin16, ksize, dilation, len;  // len: output positions n
+    const float *x;
+    long long sxc, sxn;       // x strides of a channel and a position
+    const unsigned *xmax;     // [kDecMaxSlots]: bits of max |x| over the slots
+    const float *bias;        // [M] or null
+    const float *scale;       // [M]: DEC_EPI_SCALED_RESID / DEC_EPI_RESID_IN (null: 1)
+    int act, epi;             // DecAct, DecEpi
     float *c;                 // output (m, n) at c[m * ldc + n * out_stride + phase]
     long long ldc;
-    int out_stride, phase;    // 1, 0; or one output phase of a transposed convolution
+    long long out_stride;
+    int phase;
     const float *resid;       // DEC_EPI_RESID_IN: at the output's index (may be c)
 };
 
@@ -334,7 +319,6 @@ void launch_repack_mfma(hipStream_t st, const DevQ4 &w, uint32_t *wm, uint16_t *
 void launch_mfma_rows(hipStream_t st, const MfmaRowsParams &p);
 void launch_qkv_rows(hipStream_t st, const QkvRowsParams &p);
 void launch_dec_gather(hipStream_t st, const DecGatherParams &p, int frames);
-void launch_dec_gemm(hipStream_t st, const DecGemmParams &p);
 void launch_dec_rmsnorm(hipStream_t st, const float *x, const float *gamma, int rows, int n, float eps, float *out);
 void launch_dec_rope(hipStream_t st, float *q, float *k, int T, int heads, int hd, const float *cs, const float *sn,
                      int rows);
@@ -347,6 +331,7 @@ void launch_dec_lnorm(hipStream_t st, const float *x, const float *g, const floa
 void launch_dec_snake(hipStream_t st, const float *x, const float *alpha, const float *beta, int ch, int len,
                       float *out, unsigned *amax = nullptr);
 void launch_dec_fill_u32(hipStream_t st, unsigned *p, int n, unsigned v);
+void launch_dec_absmax(hipStream_t st, const float *x, size_t n, unsigned *amax);
 void launch_dec_conv_repack(hipStream_t st, const float *w, long long sm, long long sci, int k0, int kd, int M, int cin,
                             int taps, int cin16, int mtiles, int ksteps, int ew, _Float16 *wh, _Float16 *wl);
 void launch_dec_conv_mfma(hipStream_t st, const DecConvMfmaParams &p);
