@@ -3065,7 +3065,7 @@ qtts_status dec_mfma_copy(qtts_ctx *c, Owner &own, const float *dw, long long sm
     m.ew = ew;
     m.cin16 = (cin + 15) / 16 * 16;
     m.mtiles = (M + 31) / 32;
-    m.ksteps = taps * m.cin16 / 16;
+    m.ksteps = (taps * m.cin16 / 16 + kConvStage - 1) / kConvStage * kConvStage;
     const size_t n = (size_t)m.mtiles * m.ksteps * 64 * 8;
     QTTS_TRY(own.alloc(c, &m.wh, n));
     QTTS_TRY(own.alloc(c, &m.wl, n));

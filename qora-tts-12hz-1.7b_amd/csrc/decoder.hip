@@ -32,10 +32,7 @@ namespace qtts {
 namespace {
 
 constexpr unsigned kSnakeBlocks = 8192;  // SnakeBeta grid cap (threads stride through the tensor)
-#ifndef QTTS_DEC_CONV_TILES
-#define QTTS_DEC_CONV_TILES 1
-#endif
-constexpr int kDecConvTiles = QTTS_DEC_CONV_TILES;  // 32-step output tiles per wave of k_dec_conv_mfma
+
 
 __global__ void k_dec_gather(DecGatherParams P) {
     const int t = blockIdx.x, cd = P.cd;
@@ -291,130 +288,140 @@ __global__ void k_dec_conv_repack(const float *w, long long sm, long long sci, i
 
 // A causal convolution c[m][n] = bias[m] + sum_{ci, tap} W[m][ci][tap] *
 // x[ci][n + (tap - (ksize - 1)) * dilation] (zero before the signal) as an
-// implicit GEMM on the matrix cores.  Each wave owns NT tiles of 32 output
-// steps n and the block's MT tiles of 32 channels, so each A operand it
-// loads serves NT tiles; per 16-row K step it gathers its own B operands --
-// lane l of tile j: step n0 + 32 j + l % 32, channels ci0 + 8 (l / 32) + i of
-// one tap (K is tap-major and the channels are padded to a multiple of 16,
-// so a step never straddles two taps) -- scales them by 2^ex (ex from the
-// producer's max |x|), splits them into binary16 hi + lo, and runs three
-// MFMAs per tile pair: wh * xh + wh * xl + wl * xh.  Every product of
-// binary16 values is exact in the f32 accumulator; the dropped wl * xl term
-// and the two splits leave a relative error of about 2^-21 per term, the
-// f32 level.  The next step's operands are loaded before the current
-// step's MFMAs.
-template <int MT, int NT, bool KF>  // KF: channels contiguous (sxc == 1, cin % 8 == 0)
+// implicit GEMM on the matrix cores.  Each wave owns 32 output steps n and
+// the block's MT tiles of 32 channels.  The A operands of a stage of
+// kConvStage 16-row K steps are loaded once per block -- each wave loads a
+// quarter of the (tile, step, hi/lo) units -- and staged in LDS (double
+// buffered, one barrier per stage), so the four waves share them.  Per step
+// each wave gathers its own B operand -- lane l: step n0 + l % 32, channels
+// ci0 + 8 (l / 32) + i of one tap (K is tap-major and the channels are
+// padded to a multiple of 16, so a step never straddles two taps) -- scales
+// it by 2^ex (ex from the producer's max |x|), splits it into binary16 hi +
+// lo, and runs three MFMAs per tile: wh * xh + wh * xl + wl * xh.  Every
+// product of binary16 values is exact in the f32 accumulator; the dropped
+// wl * xl term and the two splits leave a relative error of about 2^-21 per
+// term, the f32 level.  The next stage's operands are loaded before the
+// current stage's MFMAs.
+template <int MT, bool KF>  // KF: channels contiguous (sxc == 1, cin % 8 == 0)
 __global__ __launch_bounds__(256) void k_dec_conv_mfma(DecConvMfmaParams P) {
     static_assert(kDecMaxSlots == 64, "one max slot per lane");
+    constexpr int G = kConvStage;
+    constexpr int UNITS = 2 * MT * G;  // 1-KiB operand units per stage: (step, tile, hi/lo)
+    constexpr int UPW = UNITS / 4;     // per wave
+    static_assert(UNITS % 4 == 0, "units split evenly over the 4 waves");
+    __shared__ half8 As[2][UNITS][64];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int col = lane & 31, half = lane >> 5;
-    const int nb = (blockIdx.x * 4 + wave) * 32 * NT + col;  // this lane's step in tile 0
+    const int n = (blockIdx.x * 4 + wave) * 32 + col;  // this lane's output step
     const int t0 = blockIdx.y * MT;
-    const int len = P.len, cin16 = P.cin16, ksteps = P.ksteps;
+    const int len = P.len, cin16 = P.cin16, ksteps = P.ksteps, nstage = ksteps / G;
     // max |x| over the producer's slots, one per lane
     const int ex = split_exponent(wave_max(__uint_as_float(P.xmax[lane])));
     const float xs = ldexpf(1.0f, ex);
     const int cpl = P.cin - 8 * half;  // channels this lane's half may read at ci0 = 0
 
-    // operands of step s: A of every channel tile, the 8 raw x values of
-    // this lane in every step tile
-    auto load = [&](int s, half8 (&ah)[MT], half8 (&al)[MT], float (&xv)[NT][8]) {
-        const int kp = 16 * s;  // wave-uniform; cin16 % 16 == 0, so one tap per step
-        const int tap = kp / cin16, ci0 = kp - tap * cin16;
-        const int off = (tap - (P.ksize - 1)) * P.dilation;
-        const bool chan_ok = ci0 < cpl;  // the first of this lane's 8 channels
+    // this wave's A units of stage g: unit u = (gs * MT + t) * 2 + hl
+    auto load_a = [&](int g, half8 (&ua)[UPW]) {
 #pragma unroll
-        for (int j = 0; j < NT; j++) {
-            const int n = nb + 32 * j, p = n + off;
-            const bool ok = n < len && p >= 0 && chan_ok;
-            const float *xp = P.x + (long long)(ci0 + 8 * half) * P.sxc + (long long)(ok ? p : 0) * P.sxn;
-            if constexpr (KF) {
-                // all 8 channels exist (cin % 8 == 0): two 16-byte loads
-                const float4 a = ok ? *reinterpret_cast<const float4 *>(xp) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                const float4 b = ok ? *reinterpret_cast<const float4 *>(xp + 4) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-                xv[j][0] = a.x, xv[j][1] = a.y, xv[j][2] = a.z, xv[j][3] = a.w;
-                xv[j][4] = b.x, xv[j][5] = b.y, xv[j][6] = b.z, xv[j][7] = b.w;
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; i++) xv[j][i] = ok && ci0 + i < cpl ? xp[(long long)i * P.sxc] : 0.0f;
-            }
-        }
-#pragma unroll
-        for (int t = 0; t < MT; t++) {
-            const size_t o = ((size_t)(t0 + t) * ksteps + s) * 64 + lane;
-            ah[t] = reinterpret_cast<const half8 *>(P.wh)[o];
-            al[t] = reinterpret_cast<const half8 *>(P.wl)[o];
+        for (int k = 0; k < UPW; k++) {
+            const int u = wave + 4 * k, hl = u & 1, t = (u >> 1) % MT, gs = (u >> 1) / MT;
+            const size_t o = ((size_t)(t0 + t) * ksteps + g * G + gs) * 64 + lane;
+            ua[k] = reinterpret_cast<const half8 *>(hl ? P.wl : P.wh)[o];
         }
     };
-    f32x16 acc[MT][NT];
+    // the 8 raw x values of this lane at step s (zero past the taps of a
+    // padded last stage)
+    auto load_b = [&](int s, float (&xv)[8]) {
+        const int kp = 16 * s;  // wave-uniform; cin16 % 16 == 0, so one tap per step
+        const int tap = kp / cin16, ci0 = kp - tap * cin16;
+        const int p = n + (tap - (P.ksize - 1)) * P.dilation;
+        const bool ok = n < len && p >= 0 && tap < P.ksize && ci0 < cpl;
+        const float *xp = P.x + (long long)(ci0 + 8 * half) * P.sxc + (long long)(ok ? p : 0) * P.sxn;
+        if constexpr (KF) {
+            // all 8 channels exist (cin % 8 == 0): two 16-byte loads
+            const float4 a = ok ? *reinterpret_cast<const float4 *>(xp) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const float4 b = ok ? *reinterpret_cast<const float4 *>(xp + 4) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            xv[0] = a.x, xv[1] = a.y, xv[2] = a.z, xv[3] = a.w;
+            xv[4] = b.x, xv[5] = b.y, xv[6] = b.z, xv[7] = b.w;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++) xv[i] = ok && ci0 + i < cpl ? xp[(long long)i * P.sxc] : 0.0f;
+        }
+    };
+    f32x16 acc[MT];
 #pragma unroll
     for (int t = 0; t < MT; t++)
 #pragma unroll
-        for (int j = 0; j < NT; j++)
+        for (int r = 0; r < 16; r++) acc[t][r] = 0.0f;
+    half8 ua[UPW];
+    float xv[G][8];
+    load_a(0, ua);
 #pragma unroll
-            for (int r = 0; r < 16; r++) acc[t][j][r] = 0.0f;
-    half8 ah[MT], al[MT];
-    float xv[NT][8];
-    load(0, ah, al, xv);
-    for (int s = 0; s < ksteps; s++) {
-        half8 nh[MT], nl[MT];
-        float nx[NT][8];
-        load(s + 1 < ksteps ? s + 1 : s, nh, nl, nx);
+    for (int gs = 0; gs < G; gs++) load_b(gs, xv[gs]);
 #pragma unroll
-        for (int j = 0; j < NT; j++) {
+    for (int k = 0; k < UPW; k++) As[0][wave + 4 * k][lane] = ua[k];
+    __syncthreads();
+    for (int g = 0; g < nstage; g++) {
+        const int buf = g & 1;
+        const bool more = g + 1 < nstage;  // uniform
+        half8 na[UPW];
+        float nx[G][8];
+        if (more) {
+            load_a(g + 1, na);
+#pragma unroll
+            for (int gs = 0; gs < G; gs++) load_b((g + 1) * G + gs, nx[gs]);
+        }
+#pragma unroll
+        for (int gs = 0; gs < G; gs++) {
             half8 bh, bl;
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                const float v = xv[j][i] * xs;
+                const float v = xv[gs][i] * xs;
                 const _Float16 hv = (_Float16)v;
                 bh[i] = hv;
                 bl[i] = (_Float16)(v - (float)hv);
             }
 #pragma unroll
             for (int t = 0; t < MT; t++) {
-                acc[t][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[t], bh, acc[t][j], 0, 0, 0);
-                acc[t][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[t], bl, acc[t][j], 0, 0, 0);
-                acc[t][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[t], bh, acc[t][j], 0, 0, 0);
+                const half8 ah = As[buf][(gs * MT + t) * 2][lane], al = As[buf][(gs * MT + t) * 2 + 1][lane];
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bh, acc[t], 0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bl, acc[t], 0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bh, acc[t], 0, 0, 0);
             }
         }
+        if (more) {
+            // buf ^ 1 was last read in stage g - 1, before the last barrier
 #pragma unroll
-        for (int t = 0; t < MT; t++) {
-            ah[t] = nh[t];
-            al[t] = nl[t];
+            for (int k = 0; k < UPW; k++) As[buf ^ 1][wave + 4 * k][lane] = na[k];
+#pragma unroll
+            for (int gs = 0; gs < G; gs++)
+#pragma unroll
+                for (int i = 0; i < 8; i++) xv[gs][i] = nx[gs][i];
         }
-#pragma unroll
-        for (int j = 0; j < NT; j++)
-#pragma unroll
-            for (int i = 0; i < 8; i++) xv[j][i] = nx[j][i];
+        __syncthreads();
     }
     // D layout: lane l, register r -> row (r / 4) * 8 + (l / 32) * 4 + r % 4,
     // column l % 32
+    if (n >= len) return;
     const int sc = -(ex + P.ew);
 #pragma unroll
-    for (int j = 0; j < NT; j++) {
-        const int n = nb + 32 * j;
-        if (n >= len) continue;
+    for (int t = 0; t < MT; t++)
 #pragma unroll
-        for (int t = 0; t < MT; t++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int m = 32 * (t0 + t) + (r >> 2) * 8 + half * 4 + (r & 3);
-                if (m >= P.M) continue;
-                float v = ldexpf(acc[t][j][r], sc);
-                if (P.bias) v += P.bias[m];
-                if (P.act == DEC_ACT_GELU) v = dec_gelu(v);
-                float *dst = P.c + (long long)m * P.ldc + (long long)n * P.out_stride + P.phase;
-                switch (P.epi) {
-                    case DEC_EPI_STORE: *dst = v; break;
-                    case DEC_EPI_ACCUM: *dst += v; break;
-                    case DEC_EPI_SCALED_RESID: *dst += P.scale[m] * v; break;
-                    case DEC_EPI_RESID_IN:
-                        *dst = P.resid[dst - P.c] + (P.scale ? P.scale[m] * v : v);
-                        break;
-                    default: *dst = v < -1.0f ? -1.0f : (v > 1.0f ? 1.0f : v); break;  // DEC_EPI_CLAMP (NaN stays)
-                }
+        for (int r = 0; r < 16; r++) {
+            const int m = 32 * (t0 + t) + (r >> 2) * 8 + half * 4 + (r & 3);
+            if (m >= P.M) continue;
+            float v = ldexpf(acc[t][r], sc);
+            if (P.bias) v += P.bias[m];
+            if (P.act == DEC_ACT_GELU) v = dec_gelu(v);
+            float *dst = P.c + (long long)m * P.ldc + (long long)n * P.out_stride + P.phase;
+            switch (P.epi) {
+                case DEC_EPI_STORE: *dst = v; break;
+                case DEC_EPI_ACCUM: *dst += v; break;
+                case DEC_EPI_SCALED_RESID: *dst += P.scale[m] * v; break;
+                case DEC_EPI_RESID_IN: *dst = P.resid[dst - P.c] + (P.scale ? P.scale[m] * v : v); break;
+                default: *dst = v < -1.0f ? -1.0f : (v > 1.0f ? 1.0f : v); break;  // DEC_EPI_CLAMP (NaN stays)
             }
-    }
+        }
 }
 
 unsigned blocks_for(size_t n, unsigned per) { return (unsigned)((n + per - 1) / per); }
@@ -473,13 +480,12 @@ void launch_dec_conv_repack(hipStream_t st, const float *w, long long sm, long l
 
 template <bool KF>
 static void launch_conv_mfma_kf(hipStream_t st, const DecConvMfmaParams &p, int mt) {
-    constexpr int NT = kDecConvTiles;
-    const dim3 grid(blocks_for((size_t)p.len, 128 * NT), (unsigned)(p.mtiles / mt));
+    const dim3 grid(blocks_for((size_t)p.len, 128), (unsigned)(p.mtiles / mt));
     switch (mt) {
-        case 4: hipLaunchKernelGGL((k_dec_conv_mfma<4, NT, KF>), grid, dim3(256), 0, st, p); break;
-        case 3: hipLaunchKernelGGL((k_dec_conv_mfma<3, NT, KF>), grid, dim3(256), 0, st, p); break;
-        case 2: hipLaunchKernelGGL((k_dec_conv_mfma<2, NT, KF>), grid, dim3(256), 0, st, p); break;
-        default: hipLaunchKernelGGL((k_dec_conv_mfma<1, NT, KF>), grid, dim3(256), 0, st, p); break;
+        case 4: hipLaunchKernelGGL((k_dec_conv_mfma<4, KF>), grid, dim3(256), 0, st, p); break;
+        case 3: hipLaunchKernelGGL((k_dec_conv_mfma<3, KF>), grid, dim3(256), 0, st, p); break;
+        case 2: hipLaunchKernelGGL((k_dec_conv_mfma<2, KF>), grid, dim3(256), 0, st, p); break;
+        default: hipLaunchKernelGGL((k_dec_conv_mfma<1, KF>), grid, dim3(256), 0, st, p); break;
     }
 }
 
@@ -488,7 +494,7 @@ static void launch_conv_mfma_kf(hipStream_t st, const DecConvMfmaParams &p, int 
 // would fill the GPU otherwise.
 void launch_dec_conv_mfma(hipStream_t st, const DecConvMfmaParams &p) {
     int mt = p.mtiles % 4 == 0 ? 4 : p.mtiles % 3 == 0 ? 3 : p.mtiles % 2 == 0 ? 2 : 1;
-    if ((size_t)blocks_for((size_t)p.len, 128 * kDecConvTiles) * (size_t)(p.mtiles / mt) < 256) mt = 1;
+    if ((size_t)blocks_for((size_t)p.len, 128) * (size_t)(p.mtiles / mt) < 256) mt = 1;
     if (p.sxc == 1 && p.cin % 8 == 0 && p.sxn % 4 == 0 && ((uintptr_t)p.x & 15) == 0)
         launch_conv_mfma_kf<true>(st, p, mt);
     else

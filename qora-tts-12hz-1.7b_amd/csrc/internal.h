@@ -81,6 +81,7 @@ struct QkvRowsParams {
 constexpr int kDecMaxWindow = 512;   // sliding window of the decoder attention
 constexpr int kDecMaxHeadDim = 256;
 constexpr int kDecMaxSlots = 64;  // slots of one tensor's max |x| (SnakeBeta -> k_dec_conv_mfma)
+constexpr int kConvStage = 2;     // 16-row K steps per LDS stage of k_dec_conv_mfma (ksteps is a multiple)
 
 struct DecGatherParams {
     const uint32_t *codes;  // [groups][ld]
@@ -106,7 +107,8 @@ enum DecEpi { DEC_EPI_STORE = 0, DEC_EPI_ACCUM = 1, DEC_EPI_SCALED_RESID = 2, DE
 struct DecConvMfmaParams {
     const _Float16 *wh, *wl;  // [mtiles][ksteps][64][8]; row m = 32 * tile + lane % 32
     int ew;                   // the weights were scaled by 2^ew
-    int M, mtiles, ksteps;    // output channels, 32-row tiles, 16-row K steps (ksize * cin16 / 16)
+    int M, mtiles, ksteps;    // output channels, 32-row tiles, 16-row K steps (ksize * cin16 / 16,
+                              // rounded up to a multiple of kConvStage with zero weights)
     int cin, cin16, ksize, dilation, len;  // len: output positions n
     const float *x;
     long long sxc, sxn;       // x strides of a channel and a position
