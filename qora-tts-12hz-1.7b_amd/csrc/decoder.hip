@@ -255,8 +255,9 @@ __device__ __forceinline__ int split_exponent(float m) {
 
 // A convolution's weights as binary16 hi + lo MFMA A operands, scaled by
 // 2^ew: thread (tile, step, lane) writes the 8 values of row
-// m = 32 * tile + lane % 32 at k' = 16 * step + 8 * (lane / 32) + i,
-// tap = k' / cin16, ci = k' % cin16 (zero past M or cin): the element
+// m = 32 * tile + lane % 32 for step = (16-channel block cb, tap) with the
+// taps inner (cb = step / taps, tap = step % taps), channels
+// ci = 16 cb + 8 (lane / 32) + i (zero past M or cin): the element
 // w[m * sm + ci * sci + k0 + tap * kd] -- for a causal convolution
 // W[m][ci][tap] (src/conv.rs:114-184: sm = cin * ksize, sci = ksize, k0 = 0,
 // kd = 1); for output phase r of a transposed one W[ci][m][r + (J-1-tap) s]
@@ -271,10 +272,11 @@ __global__ void k_dec_conv_repack(const float *w, long long sm, long long sci, i
     const size_t ts = idx >> 6;
     const int tile = (int)(ts / ksteps), step = (int)(ts - (size_t)tile * ksteps);
     const int m = 32 * tile + (lane & 31), kb = 16 * step + 8 * (lane >> 5);
+    const int cb = step / taps, tap = step - cb * taps;  // step = (16-channel block, tap), taps inner
     half8 h, l;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        const int kp = kb + i, tap = kp / cin16, ci = kp - tap * cin16;
+        const int ci = 16 * cb + (kb & 15) + i;
         const float v = (m < M && ci < cin && tap < taps)
                             ? ldexpf(w[(long long)m * sm + (long long)ci * sci + k0 + (long long)tap * kd], ew)
                             : 0.0f;
@@ -294,8 +296,9 @@ __global__ void k_dec_conv_repack(const float *w, long long sm, long long sci, i
 // quarter of the (tile, step, hi/lo) units -- and staged in LDS (double
 // buffered, one barrier per stage), so the four waves share them.  Per step
 // each wave gathers its own B operand -- lane l: step n0 + l % 32, channels
-// ci0 + 8 (l / 32) + i of one tap (K is tap-major and the channels are
-// padded to a multiple of 16, so a step never straddles two taps) -- scales
+// ci0 + 8 (l / 32) + i of one tap (a step is one tap of one block of 16
+// channels, the taps of a block consecutive, so a tap re-reads the lines
+// the previous step gathered, shifted by the dilation) -- scales
 // it by 2^ex (ex from the producer's max |x|), splits it into binary16 hi +
 // lo, and runs three MFMAs per tile: wh * xh + wh * xl + wl * xh.  Every
 // product of binary16 values is exact in the f32 accumulator; the dropped
@@ -332,8 +335,7 @@ __global__ __launch_bounds__(256) void k_dec_conv_mfma(DecConvMfmaParams P) {
     // the 8 raw x values of this lane at step s (zero past the taps of a
     // padded last stage)
     auto load_b = [&](int s, float (&xv)[8]) {
-        const int kp = 16 * s;  // wave-uniform; cin16 % 16 == 0, so one tap per step
-        const int tap = kp / cin16, ci0 = kp - tap * cin16;
+        const int cb = s / P.ksize, tap = s - cb * P.ksize, ci0 = 16 * cb;  // wave-uniform
         const int p = n + (tap - (P.ksize - 1)) * P.dilation;
         const bool ok = n < len && p >= 0 && tap < P.ksize && ci0 < cpl;
         const float *xp = P.x + (long long)(ci0 + 8 * half) * P.sxc + (long long)(ok ? p : 0) * P.sxn;

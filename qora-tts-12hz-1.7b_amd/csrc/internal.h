@@ -100,9 +100,10 @@ enum DecEpi { DEC_EPI_STORE = 0, DEC_EPI_ACCUM = 1, DEC_EPI_SCALED_RESID = 2, DE
 // x(ci, n + (tap - (ksize - 1)) * dilation) + bias[m]) (x zero before n = 0),
 // combined into c by `epi` (STORE: =, ACCUM: +=, SCALED_RESID: += scale[m] *,
 // RESID_IN: = resid + scale[m] *, CLAMP: = clamp to [-1, 1]).  A: weights pre-split into
-// binary16 hi + lo in the MFMA A-operand order with K ordered tap-major
-// (k' = tap * cin16 + ci, the channels padded to a multiple of 16 with zero
-// weights); x(ci, p) = x[ci * sxc + p * sxn], split on the fly.  A linear
+// binary16 hi + lo in the MFMA A-operand order, one 16-row K step per
+// (16-channel block, tap) with the taps inner (the channels padded to a
+// multiple of 16 with zero weights); x(ci, p) = x[ci * sxc + p * sxn],
+// split on the fly.  A linear
 // layer is the case ksize = 1 with m the output feature and n the row.
 struct DecConvMfmaParams {
     const _Float16 *wh, *wl;  // [mtiles][ksteps][64][8]; row m = 32 * tile + lane % 32
