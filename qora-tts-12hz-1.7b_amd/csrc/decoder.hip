@@ -31,7 +31,7 @@ namespace qtts {
 
 namespace {
 
-constexpr unsigned kSnakeBlocks = 8192;  // SnakeBeta grid cap (threads stride through the tensor)
+constexpr unsigned kSnakeBlocks = 8192;  // SnakeBeta grid size target (threads stride through their channel)
 
 
 __global__ void k_dec_gather(DecGatherParams P) {
@@ -190,23 +190,24 @@ __global__ __launch_bounds__(64) void k_dec_lnorm(const float *x, const float *g
     for (c = 0; c < ch; c++) out[(size_t)c * len + t] = (xt[(size_t)c * len] - mean) * inv * g[c] + b[c];
 }
 
-// x + exp(-beta) * sin(exp(alpha) * x)^2 per channel, channel-first, over a
-// grid of at most kSnakeBlocks blocks (each thread strides through the
-// tensor).  With amax set, each block's largest |out| (NaN excluded) is
-// folded into amax[block % kMaxSlots] by an unsigned atomicMax of the float
-// bits, which orders non-negative floats as their values: the slots' maximum
-// does not depend on the order of the blocks, and 64 slots keep the atomics
-// from queueing on one address.
+// x + exp(-beta) * sin(exp(alpha) * x)^2 per channel, channel-first: block
+// row y is channel y (its two exponentials computed once per thread, no
+// division per element), and the blocks of a row stride through its
+// samples.  With amax set, each block's largest |out| (NaN excluded) is
+// folded into amax[block % kDecMaxSlots] by an unsigned atomicMax of the
+// float bits, which orders non-negative floats as their values: the slots'
+// maximum does not depend on the order of the blocks, and 64 slots keep the
+// atomics from queueing on one address.
 __global__ __launch_bounds__(256) void k_dec_snake(const float *x, const float *alpha, const float *beta, int ch,
                                                    int len, float *out, unsigned *amax) {
-    const size_t total = (size_t)ch * len, stride = (size_t)gridDim.x * blockDim.x;
+    const int c = blockIdx.y;
+    const float a = expf(alpha[c]), inv_b = expf(-beta[c]);
+    const size_t base = (size_t)c * len;
     float m = 0.0f;
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < total; i += stride) {
-        const int c = (int)(i / len);
-        const float a = expf(alpha[c]), inv_b = expf(-beta[c]);
-        const float v = x[i], s = sinf(a * v);
+    for (int t = blockIdx.x * blockDim.x + threadIdx.x; t < len; t += gridDim.x * blockDim.x) {
+        const float v = x[base + t], s = sinf(a * v);
         const float o = v + inv_b * s * s;
-        out[i] = o;
+        out[base + t] = o;
         m = fmaxf(m, fabsf(o));  // a NaN o leaves m as it was
     }
     if (!amax) return;  // uniform
@@ -216,7 +217,7 @@ __global__ __launch_bounds__(256) void k_dec_snake(const float *x, const float *
     __syncthreads();
     if (threadIdx.x == 0) {
         m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-        atomicMax(&amax[blockIdx.x % kDecMaxSlots], __float_as_uint(m));
+        atomicMax(&amax[(blockIdx.y * gridDim.x + blockIdx.x) % kDecMaxSlots], __float_as_uint(m));
     }
 }
 
@@ -465,8 +466,9 @@ void launch_dec_lnorm(hipStream_t st, const float *x, const float *g, const floa
 
 void launch_dec_snake(hipStream_t st, const float *x, const float *alpha, const float *beta, int ch, int len,
                       float *out, unsigned *amax) {
-    const unsigned blocks = std::min<unsigned>(blocks_for((size_t)ch * len, 256), kSnakeBlocks);
-    hipLaunchKernelGGL(k_dec_snake, dim3(blocks), dim3(256), 0, st, x, alpha, beta, ch, len, out, amax);
+    // about kSnakeBlocks blocks in all, at least one per channel
+    const unsigned per_row = std::max(1u, std::min<unsigned>(blocks_for((size_t)len, 256), kSnakeBlocks / (unsigned)ch));
+    hipLaunchKernelGGL(k_dec_snake, dim3(per_row, (unsigned)ch), dim3(256), 0, st, x, alpha, beta, ch, len, out, amax);
 }
 
 void launch_dec_fill_u32(hipStream_t st, unsigned *p, int n, unsigned v) {
