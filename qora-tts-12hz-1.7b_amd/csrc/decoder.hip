@@ -32,6 +32,10 @@ namespace qtts {
 namespace {
 
 constexpr unsigned kSnakeBlocks = 8192;  // SnakeBeta grid size target (threads stride through their channel)
+#ifndef QTTS_DEC_FILL_BLOCKS
+#define QTTS_DEC_FILL_BLOCKS 1024
+#endif
+constexpr size_t kDecFillBlocks = QTTS_DEC_FILL_BLOCKS;  // below: K split over a block's waves
 
 
 __global__ void k_dec_gather(DecGatherParams P) {
@@ -427,6 +431,101 @@ __global__ __launch_bounds__(256) void k_dec_conv_mfma(DecConvMfmaParams P) {
         }
 }
 
+// The same product for launches too small to fill the GPU (the transformer's
+// linears at 500 rows, the first Vocos stages): one block per (32 output
+// steps, channel tile), its 4 waves splitting the K steps four ways (each
+// wave loads its own A operands and gathers its own B), the partial sums
+// added through LDS in wave order (deterministic) by wave 0, which runs the
+// epilogue.  A quarter of the dependent step chain per wave and four times
+// the blocks of k_dec_conv_mfma<1>.
+template <bool KF>
+__global__ __launch_bounds__(256) void k_dec_conv_mfma_ks(DecConvMfmaParams P) {
+    static_assert(kDecMaxSlots == 64, "one max slot per lane");
+    __shared__ float red[3][16][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int col = lane & 31, half = lane >> 5;
+    const int n = blockIdx.x * 32 + col;
+    const int tile = blockIdx.y;
+    const int len = P.len, ksteps = P.ksteps;
+    const int q = (ksteps + 3) / 4, s0 = wave * q, s1 = min(ksteps, s0 + q);
+    const int ex = split_exponent(wave_max(__uint_as_float(P.xmax[lane])));
+    const float xs = ldexpf(1.0f, ex);
+    const int cpl = P.cin - 8 * half;
+    auto load = [&](int s, half8 &ah, half8 &al, float (&xv)[8]) {
+        const int cb = s / P.ksize, tap = s - cb * P.ksize, ci0 = 16 * cb;  // wave-uniform
+        const int p = n + (tap - (P.ksize - 1)) * P.dilation;
+        const bool ok = n < len && p >= 0 && ci0 < cpl;
+        const float *xp = P.x + (long long)(ci0 + 8 * half) * P.sxc + (long long)(ok ? p : 0) * P.sxn;
+        if constexpr (KF) {
+            const float4 a = ok ? *reinterpret_cast<const float4 *>(xp) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            const float4 b = ok ? *reinterpret_cast<const float4 *>(xp + 4) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+            xv[0] = a.x, xv[1] = a.y, xv[2] = a.z, xv[3] = a.w;
+            xv[4] = b.x, xv[5] = b.y, xv[6] = b.z, xv[7] = b.w;
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; i++) xv[i] = ok && ci0 + i < cpl ? xp[(long long)i * P.sxc] : 0.0f;
+        }
+        const size_t o = ((size_t)tile * ksteps + s) * 64 + lane;
+        ah = reinterpret_cast<const half8 *>(P.wh)[o];
+        al = reinterpret_cast<const half8 *>(P.wl)[o];
+    };
+    f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[r] = 0.0f;
+    if (s0 < s1) {  // uniform
+        half8 ah, al;
+        float xv[8];
+        load(s0, ah, al, xv);
+        for (int s = s0; s < s1; s++) {
+            half8 nh, nl;
+            float nx[8];
+            load(s + 1 < s1 ? s + 1 : s, nh, nl, nx);
+            half8 bh, bl;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const float v = xv[i] * xs;
+                const _Float16 hv = (_Float16)v;
+                bh[i] = hv;
+                bl[i] = (_Float16)(v - (float)hv);
+            }
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bh, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bl, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bh, acc, 0, 0, 0);
+            ah = nh;
+            al = nl;
+#pragma unroll
+            for (int i = 0; i < 8; i++) xv[i] = nx[i];
+        }
+    }
+    if (wave > 0) {
+#pragma unroll
+        for (int r = 0; r < 16; r++) red[wave - 1][r][lane] = acc[r];
+    }
+    __syncthreads();
+    if (wave > 0 || n >= len) return;
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[r] = ((acc[r] + red[0][r][lane]) + red[1][r][lane]) + red[2][r][lane];
+    // D layout: lane l, register r -> row (r / 4) * 8 + (l / 32) * 4 + r % 4,
+    // column l % 32
+    const int sc = -(ex + P.ew);
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+        const int m = 32 * tile + (r >> 2) * 8 + half * 4 + (r & 3);
+        if (m >= P.M) continue;
+        float v = ldexpf(acc[r], sc);
+        if (P.bias) v += P.bias[m];
+        if (P.act == DEC_ACT_GELU) v = dec_gelu(v);
+        float *dst = P.c + (long long)m * P.ldc + (long long)n * P.out_stride + P.phase;
+        switch (P.epi) {
+            case DEC_EPI_STORE: *dst = v; break;
+            case DEC_EPI_ACCUM: *dst += v; break;
+            case DEC_EPI_SCALED_RESID: *dst += P.scale[m] * v; break;
+            case DEC_EPI_RESID_IN: *dst = P.resid[dst - P.c] + (P.scale ? P.scale[m] * v : v); break;
+            default: *dst = v < -1.0f ? -1.0f : (v > 1.0f ? 1.0f : v); break;  // DEC_EPI_CLAMP (NaN stays)
+        }
+    }
+}
+
 unsigned blocks_for(size_t n, unsigned per) { return (unsigned)((n + per - 1) / per); }
 
 }  // namespace
@@ -494,12 +593,22 @@ static void launch_conv_mfma_kf(hipStream_t st, const DecConvMfmaParams &p, int 
 }
 
 // MT: the largest of 4, 3, 2, 1 that divides the tile count (a block's
-// tiles share each gathered B operand), or 1 when fewer than 256 blocks
-// would fill the GPU otherwise.
+// tiles share each gathered B operand); a launch that would leave CUs idle
+// even at MT = 1 (fewer than kDecFillBlocks blocks) splits K over the
+// block's waves instead (k_dec_conv_mfma_ks).
 void launch_dec_conv_mfma(hipStream_t st, const DecConvMfmaParams &p) {
+    const bool kf = p.sxc == 1 && p.cin % 8 == 0 && p.sxn % 4 == 0 && ((uintptr_t)p.x & 15) == 0;
+    if ((size_t)blocks_for((size_t)p.len, 128) * (size_t)p.mtiles < kDecFillBlocks) {
+        const dim3 grid(blocks_for((size_t)p.len, 32), (unsigned)p.mtiles);
+        if (kf)
+            hipLaunchKernelGGL(k_dec_conv_mfma_ks<true>, grid, dim3(256), 0, st, p);
+        else
+            hipLaunchKernelGGL(k_dec_conv_mfma_ks<false>, grid, dim3(256), 0, st, p);
+        return;
+    }
     int mt = p.mtiles % 4 == 0 ? 4 : p.mtiles % 3 == 0 ? 3 : p.mtiles % 2 == 0 ? 2 : 1;
     if ((size_t)blocks_for((size_t)p.len, 128) * (size_t)(p.mtiles / mt) < 256) mt = 1;
-    if (p.sxc == 1 && p.cin % 8 == 0 && p.sxn % 4 == 0 && ((uintptr_t)p.x & 15) == 0)
+    if (kf)
         launch_conv_mfma_kf<true>(st, p, mt);
     else
         launch_conv_mfma_kf<false>(st, p, mt);
