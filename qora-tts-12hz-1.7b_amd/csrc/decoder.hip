@@ -22,6 +22,8 @@
 
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
+#include <cstring>
 #include <cstdint>
 
 #include "device_common.h"
@@ -595,10 +597,15 @@ static void launch_conv_mfma_kf(hipStream_t st, const DecConvMfmaParams &p, int 
 // MT: the largest of 4, 3, 2, 1 that divides the tile count (a block's
 // tiles share each gathered B operand); a launch that would leave CUs idle
 // even at MT = 1 (fewer than kDecFillBlocks blocks) splits K over the
-// block's waves instead (k_dec_conv_mfma_ks).
+// block's waves instead (k_dec_conv_mfma_ks).  QTTS_DEC_CONV=tiles or
+// =split forces one kernel for every launch (tiles: MT by divisibility
+// alone), so that short decodes can check both against a reference.
 void launch_dec_conv_mfma(hipStream_t st, const DecConvMfmaParams &p) {
+    const char *plan = std::getenv("QTTS_DEC_CONV");
+    const bool force_tiles = plan && std::strcmp(plan, "tiles") == 0, force_split = plan && std::strcmp(plan, "split") == 0;
     const bool kf = p.sxc == 1 && p.cin % 8 == 0 && p.sxn % 4 == 0 && ((uintptr_t)p.x & 15) == 0;
-    if ((size_t)blocks_for((size_t)p.len, 128) * (size_t)p.mtiles < kDecFillBlocks) {
+    if (force_split ||
+        (!force_tiles && (size_t)blocks_for((size_t)p.len, 128) * (size_t)p.mtiles < kDecFillBlocks)) {
         const dim3 grid(blocks_for((size_t)p.len, 32), (unsigned)p.mtiles);
         if (kf)
             hipLaunchKernelGGL(k_dec_conv_mfma_ks<true>, grid, dim3(256), 0, st, p);
@@ -607,7 +614,7 @@ void launch_dec_conv_mfma(hipStream_t st, const DecConvMfmaParams &p) {
         return;
     }
     int mt = p.mtiles % 4 == 0 ? 4 : p.mtiles % 3 == 0 ? 3 : p.mtiles % 2 == 0 ? 2 : 1;
-    if ((size_t)blocks_for((size_t)p.len, 128) * (size_t)(p.mtiles / mt) < 256) mt = 1;
+    if (!force_tiles && (size_t)blocks_for((size_t)p.len, 128) * (size_t)(p.mtiles / mt) < 256) mt = 1;
     if (kf)
         launch_conv_mfma_kf<true>(st, p, mt);
     else

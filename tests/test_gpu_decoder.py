@@ -54,6 +54,30 @@ def test_full_decoder_matches_oracle(ctx):
     assert within(got, ref, tight=DECODER_TIGHT)
 
 
+@pytest.mark.parametrize("plan", ["tiles", "split"])
+def test_decoder_conv_plans_match_oracle(ctx, small, monkeypatch, plan):
+    """Every projection and convolution forced through one matrix-core
+    kernel: `tiles` runs k_dec_conv_mfma with MT 1-4 channel tiles per block
+    (the 1.7B decoder's layers have 1 to 48 tiles), `split` the K-split
+    variant that short decodes otherwise use for every layer.  Both against
+    the oracle, small decoder and 1.7B."""
+    monkeypatch.setenv("QTTS_DEC_CONV", plan)
+    w, dec = small
+    codes = w.synthetic_codes(140, 17)
+    got = dec.decode_to_audio(codes)
+    ref = oracle.decode_to_audio(w, codes)
+    print(f"small decoder, {plan}: rel err {rel_err(got, ref):.2e}")
+    assert within(got, ref, tight=DECODER_TIGHT)
+    wf = qtts.DecoderWeights(9)
+    full = qtts.SpeechDecoder(ctx, wf)
+    codes = wf.synthetic_codes(11, 3)
+    got = full.decode_to_audio(codes)
+    ref = oracle.decode_to_audio(wf, codes)
+    full.close()
+    print(f"1.7B decoder, {plan}, 3 frames: rel err {rel_err(got, ref):.2e}")
+    assert within(got, ref, tight=DECODER_TIGHT)
+
+
 def test_device_entry_point_with_strided_codes(ctx, small):
     """codes[g * ld + t] with ld > frames, device buffers in and out."""
     w, dec = small
