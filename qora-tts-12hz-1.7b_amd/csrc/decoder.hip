@@ -16,7 +16,9 @@
 //                 (v_mfma_f32_32x32x16_f16 with binary16 hi + lo operands):
 //                 causal convolutions as implicit GEMMs, one output phase
 //                 of a transposed convolution, linear layers as one tap;
-//                 fused epilogues
+//                 fused epilogues; k_dec_conv_win for convolutions of 3+
+//                 taps (the input window split once into LDS),
+//                 k_dec_conv_mfma_ks for launches too small to fill the GPU
 //  k_dec_absmax   max |x| of a layer input (the operand scale)
 #include <hip/hip_runtime.h>
 
@@ -38,6 +40,10 @@ constexpr unsigned kSnakeBlocks = 8192;  // SnakeBeta grid size target (threads 
 #define QTTS_DEC_FILL_BLOCKS 1024
 #endif
 constexpr size_t kDecFillBlocks = QTTS_DEC_FILL_BLOCKS;  // below: K split over a block's waves
+#ifndef QTTS_DEC_CONV_WINDOW
+#define QTTS_DEC_CONV_WINDOW 1
+#endif
+constexpr bool kDecConvWindow = QTTS_DEC_CONV_WINDOW;  // convolutions of 3+ taps through k_dec_conv_win
 
 
 __global__ void k_dec_gather(DecGatherParams P) {
@@ -528,6 +534,124 @@ __global__ __launch_bounds__(256) void k_dec_conv_mfma_ks(DecConvMfmaParams P) {
     }
 }
 
+// A causal convolution with 3 or more taps over a channel-first input
+// (sxn == 1), its input window staged in LDS: per block of 16 input
+// channels, the block's window -- positions n0 - (ksize - 1) * dilation ..
+// n0 + 127 of those channels -- is loaded once (thread t: position t, the
+// 16 channels' values, each load coalesced over the threads), scaled by 2^ex
+// and split into binary16 hi + lo, and stored position-major ([position][16
+// channels], one 32-byte row per thread), so every tap's B operand is two
+// 16-byte LDS reads at position n - n0 + tap * dilation: each value is split
+// once instead of once per tap.  The next channel block's window is loaded
+// into registers during the current block's taps (double-buffered, one
+// barrier per channel block); A operands come from global memory one step
+// ahead.  Same operand order and products as k_dec_conv_mfma.
+template <int MT>
+__global__ __launch_bounds__(256) void k_dec_conv_win(DecConvMfmaParams P) {
+    static_assert(kDecMaxSlots == 64, "one max slot per lane");
+    constexpr int WMAX = 256;  // window positions: 128 + (ksize - 1) * dilation <= the block's threads
+    __shared__ __align__(16) _Float16 wh_s[2][WMAX][16], wl_s[2][WMAX][16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 31, half = lane >> 5;
+    const int n0 = blockIdx.x * 128, n = n0 + wave * 32 + col;
+    const int t0 = blockIdx.y * MT;
+    const int len = P.len, ks = P.ksize, dil = P.dilation, ksteps = P.ksteps;
+    const int W = 128 + (ks - 1) * dil, wpos = n0 - (ks - 1) * dil + tid;  // this thread's window position
+    const bool wok = tid < W && wpos >= 0 && wpos < len;
+    const int ncb = P.cin16 / 16;
+    const int ex = split_exponent(wave_max(__uint_as_float(P.xmax[lane])));
+    const float xs = ldexpf(1.0f, ex);
+    auto load_win = [&](int cb, float (&v)[16]) {
+        const float *xp = P.x + (size_t)(16 * cb) * len + (wok ? wpos : 0);
+#pragma unroll
+        for (int c = 0; c < 16; c++) v[c] = wok && 16 * cb + c < P.cin ? xp[(size_t)c * len] : 0.0f;
+    };
+    auto store_win = [&](int buf, const float (&v)[16]) {
+        if (tid >= W) return;
+        half8 h[2], l[2];
+#pragma unroll
+        for (int c = 0; c < 16; c++) {
+            const float x = v[c] * xs;
+            const _Float16 hv = (_Float16)x;
+            h[c >> 3][c & 7] = hv;
+            l[c >> 3][c & 7] = (_Float16)(x - (float)hv);
+        }
+        *reinterpret_cast<half8 *>(&wh_s[buf][tid][0]) = h[0];
+        *reinterpret_cast<half8 *>(&wh_s[buf][tid][8]) = h[1];
+        *reinterpret_cast<half8 *>(&wl_s[buf][tid][0]) = l[0];
+        *reinterpret_cast<half8 *>(&wl_s[buf][tid][8]) = l[1];
+    };
+    auto load_a = [&](int s, half8 (&ah)[MT], half8 (&al)[MT]) {
+#pragma unroll
+        for (int t = 0; t < MT; t++) {
+            const size_t o = ((size_t)(t0 + t) * ksteps + s) * 64 + lane;
+            ah[t] = reinterpret_cast<const half8 *>(P.wh)[o];
+            al[t] = reinterpret_cast<const half8 *>(P.wl)[o];
+        }
+    };
+    f32x16 acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[t][r] = 0.0f;
+    float wv[16];
+    load_win(0, wv);
+    store_win(0, wv);
+    half8 ah[MT], al[MT];
+    load_a(0, ah, al);
+    __syncthreads();
+    const int nsteps = ncb * ks;  // the steps past these (stage padding) hold zero weights
+    for (int cb = 0; cb < ncb; cb++) {
+        const int buf = cb & 1;
+        const bool more = cb + 1 < ncb;  // uniform
+        if (more) load_win(cb + 1, wv);
+        for (int tap = 0; tap < ks; tap++) {
+            const int s = cb * ks + tap;
+            half8 nh[MT], nl[MT];
+            load_a(s + 1 < nsteps ? s + 1 : s, nh, nl);
+            const int p = wave * 32 + col + tap * dil;
+            const half8 bh = *reinterpret_cast<const half8 *>(&wh_s[buf][p][8 * half]);
+            const half8 bl = *reinterpret_cast<const half8 *>(&wl_s[buf][p][8 * half]);
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[t], bh, acc[t], 0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[t], bl, acc[t], 0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al[t], bh, acc[t], 0, 0, 0);
+            }
+#pragma unroll
+            for (int t = 0; t < MT; t++) {
+                ah[t] = nh[t];
+                al[t] = nl[t];
+            }
+        }
+        // buf ^ 1 was last read in channel block cb - 1, before the last barrier
+        if (more) store_win(buf ^ 1, wv);
+        __syncthreads();
+    }
+    // D layout: lane l, register r -> row (r / 4) * 8 + (l / 32) * 4 + r % 4,
+    // column l % 32
+    if (n >= len) return;
+    const int sc = -(ex + P.ew);
+#pragma unroll
+    for (int t = 0; t < MT; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int m = 32 * (t0 + t) + (r >> 2) * 8 + half * 4 + (r & 3);
+            if (m >= P.M) continue;
+            float v = ldexpf(acc[t][r], sc);
+            if (P.bias) v += P.bias[m];
+            if (P.act == DEC_ACT_GELU) v = dec_gelu(v);
+            float *dst = P.c + (long long)m * P.ldc + (long long)n * P.out_stride + P.phase;
+            switch (P.epi) {
+                case DEC_EPI_STORE: *dst = v; break;
+                case DEC_EPI_ACCUM: *dst += v; break;
+                case DEC_EPI_SCALED_RESID: *dst += P.scale[m] * v; break;
+                case DEC_EPI_RESID_IN: *dst = P.resid[dst - P.c] + (P.scale ? P.scale[m] * v : v); break;
+                default: *dst = v < -1.0f ? -1.0f : (v > 1.0f ? 1.0f : v); break;  // DEC_EPI_CLAMP (NaN stays)
+            }
+        }
+}
+
 unsigned blocks_for(size_t n, unsigned per) { return (unsigned)((n + per - 1) / per); }
 
 }  // namespace
@@ -597,9 +721,10 @@ static void launch_conv_mfma_kf(hipStream_t st, const DecConvMfmaParams &p, int 
 // MT: the largest of 4, 3, 2, 1 that divides the tile count (a block's
 // tiles share each gathered B operand); a launch that would leave CUs idle
 // even at MT = 1 (fewer than kDecFillBlocks blocks) splits K over the
-// block's waves instead (k_dec_conv_mfma_ks).  QTTS_DEC_CONV=tiles or
-// =split forces one kernel for every launch (tiles: MT by divisibility
-// alone), so that short decodes can check both against a reference.
+// block's waves instead (k_dec_conv_mfma_ks); channel-first convolutions of
+// 3 or more taps take k_dec_conv_win.  QTTS_DEC_CONV=tiles or =split forces
+// the long-decode kernels (MT by divisibility alone) or the K split for
+// every launch, so that short decodes can check both against a reference.
 void launch_dec_conv_mfma(hipStream_t st, const DecConvMfmaParams &p) {
     const char *plan = std::getenv("QTTS_DEC_CONV");
     const bool force_tiles = plan && std::strcmp(plan, "tiles") == 0, force_split = plan && std::strcmp(plan, "split") == 0;
@@ -615,6 +740,17 @@ void launch_dec_conv_mfma(hipStream_t st, const DecConvMfmaParams &p) {
     }
     int mt = p.mtiles % 4 == 0 ? 4 : p.mtiles % 3 == 0 ? 3 : p.mtiles % 2 == 0 ? 2 : 1;
     if (!force_tiles && (size_t)blocks_for((size_t)p.len, 128) * (size_t)(p.mtiles / mt) < 256) mt = 1;
+    if (kDecConvWindow && p.ksize >= 3 && p.sxn == 1 && p.sxc == p.len && 128 + (p.ksize - 1) * p.dilation <= 256) {
+        // a channel-first convolution with 3 or more taps whose window fits the block's threads
+        const dim3 grid(blocks_for((size_t)p.len, 128), (unsigned)(p.mtiles / mt));
+        switch (mt) {
+            case 4: hipLaunchKernelGGL(k_dec_conv_win<4>, grid, dim3(256), 0, st, p); break;
+            case 3: hipLaunchKernelGGL(k_dec_conv_win<3>, grid, dim3(256), 0, st, p); break;
+            case 2: hipLaunchKernelGGL(k_dec_conv_win<2>, grid, dim3(256), 0, st, p); break;
+            default: hipLaunchKernelGGL(k_dec_conv_win<1>, grid, dim3(256), 0, st, p); break;
+        }
+        return;
+    }
     if (kf)
         launch_conv_mfma_kf<true>(st, p, mt);
     else

@@ -56,11 +56,12 @@ def test_full_decoder_matches_oracle(ctx):
 
 @pytest.mark.parametrize("plan", ["tiles", "split"])
 def test_decoder_conv_plans_match_oracle(ctx, small, monkeypatch, plan):
-    """Every projection and convolution forced through one matrix-core
-    kernel: `tiles` runs k_dec_conv_mfma with MT 1-4 channel tiles per block
-    (the 1.7B decoder's layers have 1 to 48 tiles), `split` the K-split
-    variant that short decodes otherwise use for every layer.  Both against
-    the oracle, small decoder and 1.7B."""
+    """Every projection and convolution forced through the kernels of long
+    decodes or through the K split: `tiles` runs the convolutions of 3 or
+    more taps on k_dec_conv_win and the rest on k_dec_conv_mfma, both with
+    1-4 channel tiles per block (the 1.7B decoder's layers have 1 to 48
+    tiles); `split` runs k_dec_conv_mfma_ks, which short decodes otherwise
+    use for every layer.  Both against the oracle, small decoder and 1.7B."""
     monkeypatch.setenv("QTTS_DEC_CONV", plan)
     w, dec = small
     codes = w.synthetic_codes(140, 17)
