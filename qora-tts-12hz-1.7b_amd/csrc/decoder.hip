@@ -36,14 +36,9 @@ namespace qtts {
 namespace {
 
 constexpr unsigned kSnakeBlocks = 8192;  // SnakeBeta grid size target (threads stride through their channel)
-#ifndef QTTS_DEC_FILL_BLOCKS
-#define QTTS_DEC_FILL_BLOCKS 1024
-#endif
-constexpr size_t kDecFillBlocks = QTTS_DEC_FILL_BLOCKS;  // below: K split over a block's waves
-#ifndef QTTS_DEC_CONV_WINDOW
-#define QTTS_DEC_CONV_WINDOW 1
-#endif
-constexpr bool kDecConvWindow = QTTS_DEC_CONV_WINDOW;  // convolutions of 3+ taps through k_dec_conv_win
+// Matrix-core launches of fewer blocks than this at one channel tile split
+// K over a block's waves instead (measured: 1,024 ahead of 0 and 4,096).
+constexpr size_t kDecFillBlocks = 1024;
 
 
 __global__ void k_dec_gather(DecGatherParams P) {
@@ -740,7 +735,7 @@ void launch_dec_conv_mfma(hipStream_t st, const DecConvMfmaParams &p) {
     }
     int mt = p.mtiles % 4 == 0 ? 4 : p.mtiles % 3 == 0 ? 3 : p.mtiles % 2 == 0 ? 2 : 1;
     if (!force_tiles && (size_t)blocks_for((size_t)p.len, 128) * (size_t)(p.mtiles / mt) < 256) mt = 1;
-    if (kDecConvWindow && p.ksize >= 3 && p.sxn == 1 && p.sxc == p.len && 128 + (p.ksize - 1) * p.dilation <= 256) {
+    if (p.ksize >= 3 && p.sxn == 1 && p.sxc == p.len && 128 + (p.ksize - 1) * p.dilation <= 256) {
         // a channel-first convolution with 3 or more taps whose window fits the block's threads
         const dim3 grid(blocks_for((size_t)p.len, 128), (unsigned)(p.mtiles / mt));
         switch (mt) {
