@@ -719,6 +719,9 @@ def main():
                     help="only the GEMV timings and the copy-kernel calibration (for counter runs)")
     ap.add_argument("--attention-only", type=int, default=0, metavar="L",
                     help="only multi-kernel talker steps at a cache of L rows (for attention counter runs)")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only the 64-token talker prefill (10 timed calls) and its stand-alone gate|up GEMM "
+                         "(for prefill kernel traces)")
     ap.add_argument("--decoder-only", type=int, default=0, metavar="FRAMES",
                     help="only the speech decoder's decode of FRAMES frames (for decoder kernel traces)")
     ap.add_argument("--engine-trace", default="", metavar="FILE",
@@ -755,6 +758,30 @@ def main():
     if args.attention_only:
         out = attention_only(ctx, talker, args.attention_only)
         print(json.dumps({"attention_only": out}), flush=True)
+        ctx.close()
+        return
+    if args.prefill_only:
+        hidden = tw.cfg.hidden
+        prompt = qtts.synth_normal_f32(2, "bench.prompt", PROMPT * hidden)
+        hip = Hip()
+        ev0, ev1 = hip.event(), hip.event()
+        def one_prefill():
+            kv = talker.new_kv(2 * PROMPT)
+            talker.prefill_talker_raw(prompt, PROMPT, kv)
+            kv.close()
+
+        for _ in range(2):
+            one_prefill()
+        ctx.synchronize()
+        hip.record(ev0, ctx.stream)
+        for _ in range(10):
+            one_prefill()
+        hip.record(ev1, ctx.stream)
+        ctx.synchronize()
+        pf_s = hip.elapsed_ms(ev0, ev1) / 1e3 / 10
+        print(json.dumps({"prefill": {"tokens": PROMPT, "ms": round(pf_s * 1e3, 3),
+                                      "timing": "HIP events around 10 prefill_talker_raw calls (cache creation "
+                                                "included)", "gemm": mfma_gemm_roofline(ctx)}}), flush=True)
         ctx.close()
         return
     pred = qtts.CodePredictor(ctx, pw)
