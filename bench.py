@@ -722,6 +722,8 @@ def main():
     ap.add_argument("--prefill-only", action="store_true",
                     help="only the 64-token talker prefill (10 timed calls) and its stand-alone gate|up GEMM "
                          "(for prefill kernel traces)")
+    ap.add_argument("--batch-only", action="store_true",
+                    help="only the 16-stream batched loop of the `batch` field (for batch kernel traces)")
     ap.add_argument("--decoder-only", type=int, default=0, metavar="FRAMES",
                     help="only the speech decoder's decode of FRAMES frames (for decoder kernel traces)")
     ap.add_argument("--engine-trace", default="", metavar="FILE",
@@ -786,6 +788,13 @@ def main():
         return
     pred = qtts.CodePredictor(ctx, pw)
     log(f"uploaded {time.time() - t0:.1f}s")
+    if args.batch_only:
+        # a 2-frame call first makes the one-time matrix-core operand copies
+        # and predictor tables, as the default run's earlier legs do
+        batch_measure(ctx, talker, pred, frames=2)
+        print(json.dumps({"batch": batch_measure(ctx, talker, pred)}), flush=True)
+        ctx.close()
+        return
     if args.engine_trace:
         print(json.dumps({"engine_trace": engine_trace(ctx, talker, pred, args.engine_trace)}), flush=True)
         ctx.close()
