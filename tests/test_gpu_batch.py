@@ -63,6 +63,32 @@ def test_batch_matches_oracle_streams(tiny, greedy):
         assert within(gk, rk) and within(gv, rv), b
 
 
+@pytest.mark.parametrize("B", [1, 20, 64])
+def test_batch_sizes(tiny, B):
+    """One stream, more streams than one 16-row tile (the first pass's 2B
+    rows then span two or more 32-row matrix-core tiles: 40 rows, and 128
+    rows in two 64-row chunks at the 64-stream maximum): sampled codes and
+    caches match the oracle's single-stream loops."""
+    tw, pw, t, p, ot, op = tiny
+    frames = 4
+    lens = [5 + (7 * b) % 10 for b in range(B)]
+    kvs, okvs, lh, lg, pos, text, pad = _streams(tw, t, ot, B, 67, lens, 24, trailing=2)
+    seeds = [3000 + 11 * b for b in range(B)]
+    params = qtts.loop_params(frames, temperature=0.8, top_k=50, repetition_penalty=1.05, stop_on_eos=False)
+    got = qtts.generate_codes_batch(t, p, kvs, lh, lg, pos, text, pad, params, seeds)
+    assert len(got) == B
+    for b in range(B):
+        ref = oracle.generate_codes(ot, op, okvs[b], op.new_kv(), lh[b], lg[b], pos[b], text[b], pad, params,
+                                    seed=seeds[b])
+        assert got[b].shape == ref.shape == (16, frames)
+        assert np.array_equal(got[b], ref), (b, np.argwhere(got[b] != ref)[:5])
+        (gk, gv), (rk, rv) = kvs[b].store(), okvs[b].store()
+        assert gk.shape == rk.shape
+        assert within(gk, rk) and within(gv, rv), b
+    for kv in kvs:
+        kv.close()
+
+
 def test_batch_is_deterministic(tiny):
     """The same 5-stream batch twice with the same seeds and inputs: every
     stream's codes and cache are identical bit for bit."""
