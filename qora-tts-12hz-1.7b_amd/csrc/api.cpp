@@ -442,12 +442,19 @@ int attn_nsplit(int cap, int min_split) {
 
 // Splits of a one-row talker attention (k_attn): at least 16, and enough
 // that a split holds <= 64 positions (its K and V rows then come in one
-// round trip) up to 64 splits.
+// round trip) up to 64 splits; past 64 * kAttnMaxChunk positions, as many
+// as keep every split within the block's kAttnMaxChunk-entry score buffer.
 int attn_nsplit_row(int cap) {
     int n = (cap + 63) / 64;
     if (n > 64) n = 64;
-    return n < 16 ? 16 : n;
+    if (n < 16) n = 16;
+    const int fit = (cap + kAttnMaxChunk - 1) / kAttnMaxChunk;
+    return n < fit ? fit : n;
 }
+
+// k_attn keeps a split's scores in a kAttnMaxChunk-entry LDS buffer per
+// query head: a split of a cache of `cap` rows must not hold more.
+bool attn_split_fits(int cap, int nsplit) { return nsplit > 0 && (cap + nsplit - 1) / nsplit <= kAttnMaxChunk; }
 
 // One layer stack over M rows: QKV (RMSNorm prologue; QK-norm, RoPE and KV
 // append epilogue) -> attention -> O (+residual) -> gate|up (RMSNorm
@@ -507,6 +514,7 @@ qtts_status enqueue_layers(qtts_ctx *c, const Stack &st, qtts_kv *kv, float *x, 
         a.d_done = d_done;
         if ((size_t)M * st.nq * nsplit * (st.hd + 2) > kAttnPartFloats || M * st.nkv > kAttnCounters)
             return fail(c, QTTS_ESHAPE, "attention split buffer too small");
+        if (!attn_split_fits(kv->cap, nsplit)) return fail(c, QTTS_ESHAPE, "attention: a split exceeds the score buffer");
         launch_attention(c->stream, a, M);
         QTTS_TRY(check_launch(c, "k_attn"));
 
@@ -3797,6 +3805,7 @@ qtts_status layers_batched(qtts_ctx *c, const Stack &st, const DevQ4Mfma *W, con
     const int hidden = st.hidden, qd = st.nq * st.hd, nqkv = qd + 2 * st.nkv * st.hd;
     if ((size_t)M * st.nq * nsplit * (st.hd + 2) > kAttnPartFloats || M * st.nkv > kAttnCounters)
         return fail(c, QTTS_ESHAPE, "batched attention: too many rows for the split buffers");
+    if (!attn_split_fits(R.cap, nsplit)) return fail(c, QTTS_ESHAPE, "batched attention: a split exceeds the score buffer");
     for (int l = 0; l < st.layers; l++) {
         const DevLayer &Ly = st.L[l];
         const DevQ4Mfma *Wl = W + (size_t)4 * l;

@@ -9,6 +9,8 @@ oracle on the same seeded random-init weights and inputs:
   64-token prefill: 64 greedy and 64 sampled frames;
 - two talker steps from caches loaded to 564 and 2064 N(0,1) rows, on the
   frame engine and on the multi-kernel path (k_attn);
+- two talker steps from caches loaded to 16384 and 32766 N(0,1) rows (the
+  latter at the last two positions of the 32768-row RoPE table);
 - 16 batched streams (qtts_generate_codes_batch) in 2064-row caches loaded
   to 2000 N(0,1) rows: 3 sampled frames, every stream's codes, frame count,
   cache length and appended cache rows.
@@ -301,4 +303,44 @@ def test_talker_steps_long_cache(full, monkeypatch, L, engine):
     gk, gv = kv.store()
     rk, rv = okv.store()
     assert within(gk[:, L:], rk[:, L:], tight) and within(gv[:, L:], rv[:, L:], tight)
+    kv.close()
+
+
+@pytest.mark.timeout(900)
+@pytest.mark.parametrize("L", [16384, 32766])
+def test_talker_steps_max_context(full, L):
+    """Caches past 16384 rows, up to the maximum: two talker steps at
+    positions L and L + 1 -- at L = 32766 the last rows of the 32768-row
+    RoPE table (src/rope.rs:11-41) -- from a cache loaded to L N(0,1) rows
+    in an (L + 2)-row capacity (7.5 GB of K/V at the maximum).  Past 8192
+    rows the multi-kernel path runs the step; its one-row attention then
+    needs more than 64 splits to keep every split within the 256-entry score
+    buffer of k_attn (65 and 128 splits here).  Hidden, logits and the two
+    appended cache rows against the oracle."""
+    tw, _, t, _, ot, _ = full
+    c = tw.cfg
+    cap = L + 2
+    assert cap <= c.max_position
+    shape = (c.layers, L, c.kv_heads, c.head_dim)
+    t0 = time.time()
+    kv, okv = t.new_kv(cap), ot.new_kv(cap)
+    k = qtts.synth_normal_f32(71 + L, "max.k", int(np.prod(shape))).reshape(shape)
+    v = qtts.synth_normal_f32(71 + L, "max.v", int(np.prod(shape))).reshape(shape)
+    kv.load(k, v, L)
+    okv.load(k, v, L)
+    del k, v
+    print(f"caches loaded in {time.time() - t0:.1f}s", flush=True)
+    for i in range(2):
+        emb = qtts.synth_normal_f32(72 + i, "max.emb", c.hidden)
+        got = t.forward_with_embedding(emb, kv, L + i)
+        ref = ot.forward_with_embedding(emb, okv, L + i)
+        eh, el = rel_err(got[: c.hidden], ref[: c.hidden]), rel_err(got[c.hidden:], ref[c.hidden:])
+        print(f"position {L + i}: hidden rel err {eh:.2e}, logits {el:.2e}", flush=True)
+        # measured <= 1.3e-6 (1.7e-3 while the 64-split cap let a split
+        # overrun the score buffer)
+        assert within(got[: c.hidden], ref[: c.hidden]) and within(got[c.hidden:], ref[c.hidden:])
+    assert len(kv) == len(okv) == cap
+    gk, gv = kv.store()
+    rk, rv = okv.store()
+    assert within(gk[:, L:], rk[:, L:]) and within(gv[:, L:], rv[:, L:])
     kv.close()
