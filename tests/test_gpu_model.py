@@ -73,10 +73,13 @@ def test_talker_step_full_prefilled_kv(full):
     assert int(np.argmax(got[cfg.hidden:])) == int(np.argmax(ref[cfg.hidden:]))
 
 
-@pytest.mark.parametrize("seq_len", [1, 5, 13, 70])
+@pytest.mark.parametrize("seq_len", [1, 5, 13, 70, 300, 700])
 def test_prefill_tiny(tiny, seq_len):
     """Below 8 rows the prefill runs on the GEMV path, from 8 rows on the
-    matrix cores (70 rows: two 64-row GEMM passes)."""
+    matrix cores (70 rows: two 64-row GEMM passes).  Past 256 rows the causal
+    attention splits each row's positions into 256-position pieces merged by
+    the last split (300 rows: 2 splits; 700 rows: 3, and the rows in two
+    attention launches of at most 512)."""
     tw, _, t, _, ot, _ = tiny
     cfg = tw.cfg
     x = qtts.synth_normal_f32(23, f"prefill.{seq_len}", seq_len * cfg.hidden)
