@@ -7,8 +7,8 @@ oracle on the same seeded random-init weights and inputs:
   from a cache loaded to 500 N(0,1) rows, through position 564;
 - the talker + code predictor loop (src/generate_new.rs:242-300) after a
   64-token prefill: 64 greedy and 64 sampled frames;
-- two talker steps from caches loaded to 564 and 2064 N(0,1) rows, on the
-  frame engine and on the multi-kernel path (k_attn);
+- two talker steps from caches loaded to 564, 2064 and 8184 N(0,1) rows, on
+  the frame engine and on the multi-kernel path (k_attn);
 - two talker steps from caches loaded to 16384 and 32766 N(0,1) rows (the
   latter at the last two positions of the 32768-row RoPE table);
 - 16 batched streams (qtts_generate_codes_batch) in 2064-row caches loaded
@@ -274,13 +274,14 @@ def test_batch_config5_16_streams_2000_rows(full):
 
 
 @pytest.mark.timeout(600)
-@pytest.mark.parametrize("L", [564, 2064])
+@pytest.mark.parametrize("L", [564, 2064, 8184])
 @pytest.mark.parametrize("engine", ["frame", "ops"])
 def test_talker_steps_long_cache(full, monkeypatch, L, engine):
     """Two talker steps (forward_with_embedding) from a cache loaded to L
     N(0,1) rows, on the frame engine and on the multi-kernel path (k_attn,
     up to 64 position splits): hidden, logits and the two appended cache rows
-    against the oracle."""
+    against the oracle.  L = 8184 fills the frame engine's largest cache
+    (8192 rows: 32 splits of 256 positions, its score buffer's size)."""
     tw, _, t, _, ot, _ = full
     if engine == "ops":
         monkeypatch.setenv("QTTS_ENGINE", "ops")
