@@ -54,6 +54,23 @@ def test_full_decoder_matches_oracle(ctx):
     assert within(got, ref, tight=DECODER_TIGHT)
 
 
+@pytest.mark.timeout(600)
+def test_full_decoder_long(ctx):
+    """The 1.7B decoder over 100 frames (8 s of audio, 192,000 samples): the
+    convolutions then run on the large-grid kernels the 500-frame bench
+    decode uses (the window kernel and multi-tile blocks instead of the K
+    split of short decodes), and the transformer's attention past its
+    sliding window."""
+    w = qtts.DecoderWeights(9)
+    dec = qtts.SpeechDecoder(ctx, w)
+    codes = w.synthetic_codes(12, 100)
+    got = dec.decode_to_audio(codes)
+    ref = oracle.decode_to_audio(w, codes)
+    assert got.shape == ref.shape == (100 * 1920,)
+    print(f"1.7B decoder, 100 frames: rel err {rel_err(got, ref):.2e}, audio std {np.std(ref):.3f}")
+    assert within(got, ref, tight=DECODER_TIGHT)
+
+
 @pytest.mark.parametrize("plan", ["tiles", "split"])
 def test_decoder_conv_plans_match_oracle(ctx, small, monkeypatch, plan):
     """Every projection and convolution forced through the kernels of long
