@@ -197,6 +197,35 @@ def test_config4_bench_window(full):
     _check_appended(kv, okv, L, frames)
 
 
+@pytest.mark.timeout(900)
+def test_loop_past_engine_cache(full):
+    """The talker + predictor loop from a cache loaded to 20000 rows
+    (N(0,1)), past the frame engine's 8192-row limit: the loop runs on the
+    multi-kernel path, whose one-row attention takes 79 splits of at most
+    256 positions.  4 sampled frames: codes identical, appended cache rows
+    within the bars."""
+    tw, pw, t, p, ot, op = full
+    c = tw.cfg
+    L, frames = 20000, 4
+    kv, okv = _loaded_caches(t, ot, c, L, L + frames + 4, 46, "past")
+    lh = qtts.synth_normal_f32(46, "past.h", c.hidden)
+    lg = ot.apply_codec_head(lh)
+    text = qtts.synth_normal_f32(46, "past.text", 2 * c.hidden, 0.0, 0.1).reshape(2, c.hidden)
+    pad = qtts.synth_normal_f32(46, "past.pad", c.hidden, 0.0, 0.1)
+    params = qtts.loop_params(frames, temperature=0.8, top_k=50, repetition_penalty=1.05, stop_on_eos=False)
+    t0 = time.time()
+    with ThreadPoolExecutor(max_workers=1) as pool:
+        fut = pool.submit(oracle.generate_codes, ot, op, okv, op.new_kv(), lh, lg, L, text, pad, params, 4343)
+        got = qtts.generate_codes(t, p, kv, p.new_kv(), lh, lg, L, text, pad, params, seed=4343)
+        ref = fut.result()
+    print(f"loop at KV {L + 1}..{L + frames}: {time.time() - t0:.1f}s", flush=True)
+    assert got.shape == ref.shape == (16, frames)
+    assert np.array_equal(got, ref), np.argwhere(got != ref)[:5]
+    assert len(kv) == len(okv) == L + frames
+    _check_appended(kv, okv, L, frames)
+    kv.close()
+
+
 @pytest.mark.timeout(600)
 def test_loop_is_deterministic(full):
     """The same loop twice on one context with the same seed and inputs
