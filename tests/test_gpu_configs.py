@@ -198,15 +198,16 @@ def test_config4_bench_window(full):
 
 
 @pytest.mark.timeout(900)
-def test_loop_past_engine_cache(full):
-    """The talker + predictor loop from a cache loaded to 20000 rows
-    (N(0,1)), past the frame engine's 8192-row limit: the loop runs on the
-    multi-kernel path, whose one-row attention takes 79 splits of at most
-    256 positions.  4 sampled frames: codes identical, appended cache rows
-    within the bars."""
+@pytest.mark.parametrize("L,frames", [(8172, 16), (20000, 4)])
+def test_loop_long_caches(full, L, frames):
+    """The talker + predictor loop from a cache loaded to L N(0,1) rows:
+    8172 rows in the frame engine's largest cache (8192 rows: one launch of
+    16 codes whose talker attention splits hold up to 256 positions), and
+    20000 rows, past that limit, where the loop runs on the multi-kernel
+    path and its one-row attention takes 79 splits of at most 256 positions.
+    Sampled frames: codes identical, appended cache rows within the bars."""
     tw, pw, t, p, ot, op = full
     c = tw.cfg
-    L, frames = 20000, 4
     kv, okv = _loaded_caches(t, ot, c, L, L + frames + 4, 46, "past")
     lh = qtts.synth_normal_f32(46, "past.h", c.hidden)
     lg = ot.apply_codec_head(lh)
