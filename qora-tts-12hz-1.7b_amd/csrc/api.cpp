@@ -53,6 +53,7 @@ struct qtts_ctx {
     tv_t *eng_bar = nullptr;  // [grid + 1] arrival words and the release word of the barrier between codes
     int *eng_status = nullptr;
     uint32_t eng_tag = 0;  // tag base of the last code launched
+    uint32_t eng_epoch = 0;  // bumped when the tag space restarts (a program's arena is cleared before its next launch)
     int eng_grid = 0;
     uint64_t *eng_trace = nullptr;  // QTTS_ENGINE_TRACE: per-op block timestamps
     size_t eng_trace_cap = 0;
@@ -593,6 +594,7 @@ struct EngProgram {
     EngOp *d_ops = nullptr;
     tv_t *arena = nullptr;
     size_t used = 0;
+    uint32_t epoch = 0;  // the context's tag epoch the arena was last cleared in
     bool sizing = true;
     int next_tag = 1;
     int rot_next = 0;
@@ -1074,6 +1076,12 @@ qtts_status eng_init(qtts_ctx *c) {
     HIP_TRY(c, hipMalloc(&c->eng_bar, (size_t)(c->eng_grid + 1) * sizeof(tv_t)));
     HIP_TRY(c, hipMemset(c->eng_bar, 0, (size_t)(c->eng_grid + 1) * sizeof(tv_t)));
     c->eng_tag = 0;
+    // QTTS_ENGINE_TAG_START=n (a test aid): the tag space starts at n, so that
+    // a short run reaches its restart
+    if (const char *e = std::getenv("QTTS_ENGINE_TAG_START")) {
+        const unsigned long long v = std::strtoull(e, nullptr, 0);
+        if (v < 0xFFFFFFFFull) c->eng_tag = (uint32_t)v;
+    }
     return QTTS_OK;
 }
 
@@ -1093,6 +1101,7 @@ qtts_status eng_build(qtts_ctx *c, EngProgram &P, const BuildFn &fn) {
     P.d_ops = nullptr;
     HIP_TRY(c, hipMalloc(&P.arena, (need ? need : 1) * sizeof(tv_t)));
     HIP_TRY(c, hipMemset(P.arena, 0, (need ? need : 1) * sizeof(tv_t)));
+    P.epoch = c->eng_epoch;
     P.sizing = false;
     P.reset_build();
     QTTS_TRY(fn(P));
@@ -1132,9 +1141,20 @@ qtts_status eng_launch(qtts_ctx *c, EngProgram &P, int st_in, uint32_t *codes, i
     }
     if (ncodes < 1) return QTTS_OK;
     if (c->eng_tag > 0xFFFFFFFFu - (uint32_t)(ncodes + 1) * kTagStride) {
-        // Tags are about to wrap: restart them above zero-filled arenas.
+        // The 32-bit tags are about to wrap (every 2^32 / kTagStride = 524,288
+        // codes): once every launch has finished, restart them at zero in a
+        // new epoch.  Every tagged word is cleared before the new tags are
+        // used -- the barrier's words here, each program's arena before its
+        // first launch of the epoch -- so no stale word carries a tag the new
+        // epoch will wait for.
         HIP_TRY(c, hipStreamSynchronize(c->stream));
-        return fail(c, QTTS_ESTATE, "engine tag space exhausted; recreate the context");
+        HIP_TRY(c, hipMemsetAsync(c->eng_bar, 0, (size_t)(c->eng_grid + 1) * sizeof(tv_t), c->stream));
+        c->eng_tag = 0;
+        c->eng_epoch++;
+    }
+    if (P.epoch != c->eng_epoch) {
+        HIP_TRY(c, hipMemsetAsync(P.arena, 0, (P.used ? P.used : 1) * sizeof(tv_t), c->stream));
+        P.epoch = c->eng_epoch;
     }
     EngArgs a{};
     a.ops = P.d_ops;

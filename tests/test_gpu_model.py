@@ -205,6 +205,43 @@ def test_loop_tiny(tiny, greedy):
     assert within(lh, olh)
 
 
+def test_engine_tag_restart(tiny, monkeypatch):
+    """The frame engine's 32-bit hand-off tags (8192 per code) run out every
+    524,288 codes of a context; it then restarts them in a new epoch after
+    clearing every tagged word.  A context whose tags start 40 codes before
+    the end runs a 64-frame loop across the restart (launches of 16 codes),
+    a talker step, and a second loop in the new epoch: codes, cache rows and
+    step outputs match the oracle's."""
+    tw, pw, _, _, ot, op = tiny
+    monkeypatch.setenv("QTTS_ENGINE_TAG_START", str(0xFFFFFFFF - 40 * 8192))
+    monkeypatch.delenv("QTTS_ENGINE_CODES", raising=False)
+    monkeypatch.delenv("QTTS_ENGINE", raising=False)
+    c = qtts.Context(0)
+    try:
+        t, p = qtts.Talker(c, tw), qtts.CodePredictor(c, pw)
+        last_hidden, text, pad = _loop_inputs(tw, 29)
+        logits = ot.apply_codec_head(last_hidden)
+        params = qtts.loop_params(64, temperature=0.8, top_k=50, repetition_penalty=1.05, stop_on_eos=False)
+        kv, okv = t.new_kv(96), ot.new_kv(96)
+        got = qtts.generate_codes(t, p, kv, p.new_kv(), last_hidden, logits, 0, text, pad, params, seed=41)
+        ref = oracle.generate_codes(ot, op, okv, op.new_kv(), last_hidden, logits, 0, text, pad, params, seed=41)
+        assert got.shape == ref.shape == (16, 64)
+        assert np.array_equal(got, ref), np.argwhere(got != ref)[:5]
+        (k, v), (ok, ov) = kv.store(), okv.store()
+        assert within(k, ok) and within(v, ov)
+        emb = qtts.synth_normal_f32(29, "restart.emb", tw.cfg.hidden)
+        assert within(t.forward_with_embedding(emb, kv, 64), ot.forward_with_embedding(emb, okv, 64))
+        params = qtts.loop_params(24, temperature=0.8, top_k=50, repetition_penalty=1.05, stop_on_eos=False)
+        kv2, okv2 = t.new_kv(32), ot.new_kv(32)
+        got = qtts.generate_codes(t, p, kv2, p.new_kv(), last_hidden, logits, 0, text, pad, params, seed=43)
+        ref = oracle.generate_codes(ot, op, okv2, op.new_kv(), last_hidden, logits, 0, text, pad, params, seed=43)
+        assert np.array_equal(got, ref), np.argwhere(got != ref)[:5]
+        for x in (kv, kv2):
+            x.close()
+    finally:
+        c.close()
+
+
 @pytest.mark.parametrize("per_launch", ["1", "7", None])
 def test_loop_tiny_codes_per_launch(tiny, monkeypatch, per_launch):
     """The frame engine runs up to 16 codes per cooperative launch with a grid
