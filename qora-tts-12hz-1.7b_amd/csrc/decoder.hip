@@ -9,7 +9,8 @@
 //  k_dec_swiglu   silu(gate) * up
 //  k_dec_dwconv   causal depthwise convolution (src/conv.rs:280-345)
 //  k_dec_lnorm    channel-first LayerNorm per time step, channels summed in
-//                 order (src/decoder.rs:580-602)
+//                 order (src/decoder.rs:580-602); k_dec_lnorm_tile the same
+//                 over an LDS tile of 16 or 8 time steps
 //  k_dec_snake    SnakeBeta (src/conv.rs:347-400), optionally recording
 //                 max |out| for the convolution that reads it
 //  k_dec_conv_mfma  every projection and convolution on the matrix cores
@@ -195,6 +196,55 @@ __global__ __launch_bounds__(64) void k_dec_lnorm(const float *x, const float *g
     }
     const float inv = 1.0f / sqrtf(var / (float)ch + eps);
     for (c = 0; c < ch; c++) out[(size_t)c * len + t] = (xt[(size_t)c * len] - mean) * inv * g[c] + b[c];
+}
+
+// The same LayerNorm with TS time steps per block: the block's [ch][TS]
+// input tile is loaded once into LDS (TS consecutive steps of a channel are
+// consecutive addresses, 16 loads per thread in flight), thread t < TS runs
+// step t's two channel sums in channel order from LDS -- the arithmetic of
+// k_dec_lnorm, so the output is the same bit for bit -- and every thread
+// writes the normalised tile.  One global round trip instead of one per 8
+// channels of each pass.
+template <int TS>
+__global__ __launch_bounds__(256) void k_dec_lnorm_tile(const float *x, const float *g, const float *b, int ch, int len,
+                                                        float eps, float *out) {
+    extern __shared__ float tile[];  // [ch][TS]
+    __shared__ float s_mean[TS], s_inv[TS];
+    constexpr int U = 16;
+    const int t0 = blockIdx.x * TS, tid = threadIdx.x;
+    const int n = min(TS, len - t0);
+    const int total = ch * TS;
+    for (int base = 0; base < total; base += 256 * U) {
+        float v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = base + u * 256 + tid, c = i / TS, j = i - c * TS;
+            v[u] = i < total && j < n ? x[(size_t)c * len + t0 + j] : 0.0f;
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int i = base + u * 256 + tid;
+            if (i < total) tile[i] = v[u];
+        }
+    }
+    __syncthreads();
+    if (tid < n) {
+        float mean = 0.0f;
+        for (int c = 0; c < ch; c++) mean += tile[c * TS + tid];
+        mean /= (float)ch;
+        float var = 0.0f;
+        for (int c = 0; c < ch; c++) {
+            const float d = tile[c * TS + tid] - mean;
+            var += d * d;
+        }
+        s_mean[tid] = mean;
+        s_inv[tid] = 1.0f / sqrtf(var / (float)ch + eps);
+    }
+    __syncthreads();
+    for (int i = tid; i < total; i += 256) {
+        const int c = i / TS, j = i - c * TS;
+        if (j < n) out[(size_t)c * len + t0 + j] = (tile[i] - s_mean[j]) * s_inv[j] * g[c] + b[c];
+    }
 }
 
 // x + exp(-beta) * sin(exp(alpha) * x)^2 per channel, channel-first: block
@@ -681,7 +731,16 @@ void launch_dec_dwconv(hipStream_t st, const float *x, const float *w, const flo
 
 void launch_dec_lnorm(hipStream_t st, const float *x, const float *g, const float *b, int ch, int len, float eps,
                       float *out) {
-    hipLaunchKernelGGL(k_dec_lnorm, dim3(blocks_for((size_t)len, 64)), dim3(64), 0, st, x, g, b, ch, len, eps, out);
+    // the tiled kernel while its [ch][TS] tile fits 64 KiB of LDS
+    const size_t lds16 = (size_t)ch * 16 * sizeof(float), lds8 = (size_t)ch * 8 * sizeof(float);
+    if (lds16 <= 65536)
+        hipLaunchKernelGGL(k_dec_lnorm_tile<16>, dim3((unsigned)((len + 15) / 16)), dim3(256), lds16, st, x, g, b, ch,
+                           len, eps, out);
+    else if (lds8 <= 65536)
+        hipLaunchKernelGGL(k_dec_lnorm_tile<8>, dim3((unsigned)((len + 7) / 8)), dim3(256), lds8, st, x, g, b, ch, len,
+                           eps, out);
+    else
+        hipLaunchKernelGGL(k_dec_lnorm, dim3(blocks_for((size_t)len, 64)), dim3(64), 0, st, x, g, b, ch, len, eps, out);
 }
 
 void launch_dec_snake(hipStream_t st, const float *x, const float *alpha, const float *beta, int ch, int len,
