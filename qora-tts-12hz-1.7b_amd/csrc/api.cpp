@@ -1221,13 +1221,18 @@ qtts_status eng_status_check(qtts_ctx *c, const char *what) {
 // splits keep the attention step near its hand-off latency at long contexts,
 // while fewer splits shorten the combine (with 512-thread blocks, 64 measured
 // ahead of 48 and 96 on the 500-code loop's caches).
+// Past 32 splits (8,192 rows), as many as keep a split within the attention
+// step's 256-position score buffer, up to kEngMaxSplit (32,768 rows; the
+// attention then runs several tasks per block).
 int eng_talker_nsplit(int cap) {
     int n = (cap + 63) / 64;
     if (n < 1) n = 1;
-    if (n > kEngMaxSplit) n = kEngMaxSplit;
-    return n;
+    if (n > 32) n = 32;
+    const int fit = (cap + 255) / 256;
+    if (n < fit) n = fit;
+    return n > kEngMaxSplit ? kEngMaxSplit : n;
 }
-bool eng_talker_fits(int cap) { return (cap + kEngMaxSplit - 1) / kEngMaxSplit <= 256; }
+bool eng_talker_fits(int cap) { return (cap + 255) / 256 <= kEngMaxSplit; }
 
 // Passes 2.. of generate_acoustic_codes (src/code_predictor.rs:218-273)
 // project the previous code's embedding, emb[g-1][code], to the predictor's

@@ -38,7 +38,7 @@ constexpr int kEngNormRows = 4;  // an RMSNorm input row has <= kEngThreads * 4 
 constexpr int kEngMaxM = 2;    // rows per GEMV (the predictor's 2-token prefill)
 constexpr uint32_t kTagStride = 8192;  // tags reserved per code
 constexpr int kEngCodesPerLaunch = 16;  // codes of the frame loop per cooperative launch
-constexpr int kEngMaxSplit = 32;
+constexpr int kEngMaxSplit = 128;  // talker attention splits (<= 256 positions each: 32,768 cache rows)
 constexpr int kEngSmemFloats = 10240;
 constexpr int kEngLdsKvPos = 32;  // positions of an LDS-resident K/V cache (one kv head)
 constexpr int kEngArgtabMax = 2048;  // logits of an EIN_ARGTAB input

@@ -1102,14 +1102,19 @@ __device__ __forceinline__ int eng_attn(const KCONST EngAttn &a, int task, uint3
 }
 
 // Combine the splits of one (row, query head): flash-decode merge.  Thread
-// (dim d, quarter q) loads dim d of splits q, q + 4, ... (at most
-// kEngMaxSplit / 4) while threads 0.. also load the splits' (max, sum): one
-// round trip for all of it.  The quarters' weighted sums are added in
-// quarter order (a fixed order: the result does not depend on timing).
+// (dim d, quarter q) loads dim d of splits q, q + 4, ... of the first 32
+// while threads 0.. also load every split's (max, sum): one round trip for
+// up to 32 splits, one more per further 32 (long caches).  The quarters'
+// weighted sums are added in quarter order (a fixed order: the result does
+// not depend on timing).
 template <class CT>
 __device__ __forceinline__ int eng_combine(const KCONST EngCombine &cb, int task, uint32_t tb, CT &c, float *smem) {
-    constexpr int HD = 128, NQ = kEngThreads / HD, NS = kEngMaxSplit / NQ;
-    static_assert(kEngThreads % HD == 0 && kEngMaxSplit % NQ == 0, "combine layout");
+    // Splits are read in rounds of kCombRound; thread (q, d) holds dim d of
+    // splits r0 + q + NQ i of a round, and adds them in split order.
+    constexpr int HD = 128, NQ = kEngThreads / HD, kCombRound = 32, NS = kCombRound / NQ;
+    static_assert(kEngThreads % HD == 0 && kCombRound % NQ == 0 && kEngMaxSplit % kCombRound == 0 &&
+                      kEngMaxSplit <= kEngThreads,
+                  "combine layout");
     const int m = task / cb.nq, h = task - m * cb.nq;
     const int tid = threadIdx.x, d = tid % HD, q = tid / HD;
     const int ns = cb.nsplit;
@@ -1119,14 +1124,19 @@ __device__ __forceinline__ int eng_combine(const KCONST EngCombine &cb, int task
     float *po = sl + kEngMaxSplit;      // [NQ][HD] weighted P.V sums of each quarter
     float *pl = po + NQ * HD;           // [NQ][HD] weighted sums of each quarter
     float os[NS];
-    const int cnt = ns > q ? (ns - q + NQ - 1) / NQ : 0;
+    auto round_cnt = [&](int r0) {
+        const int n = min(ns - r0, kCombRound);
+        return n > q ? (n - q + NQ - 1) / NQ : 0;
+    };
     float ml[2];
     if (tid < ns) {
         const tv_t *ptr[2] = {base + (size_t)tid * (HD + 2), base + (size_t)tid * (HD + 2) + 1};
         const uint32_t tg[2] = {tb + cb.part_tag, tb + cb.part_tag};
         wait_list<2>(ptr, tg, 2, ml, c);
     }
-    wait_strided<NS>(base + (size_t)q * (HD + 2) + 2 + d, (size_t)NQ * (HD + 2), cnt, tb + cb.part_tag, os, c);
+    // the first round's partials are polled with the (max, sum) pairs
+    wait_strided<NS>(base + (size_t)q * (HD + 2) + 2 + d, (size_t)NQ * (HD + 2), round_cnt(0), tb + cb.part_tag, os,
+                     c);
     if (tid < ns) {
         sm[tid] = ml[0];
         sl[tid] = ml[1];
@@ -1134,9 +1144,11 @@ __device__ __forceinline__ int eng_combine(const KCONST EngCombine &cb, int task
     __syncthreads();
     float mx = -INFINITY;
 #pragma unroll
-    for (int sp = 0; sp < kEngMaxSplit; sp++)
+    for (int sp = 0; sp < kCombRound; sp++)
         if (sp < ns) mx = fmaxf(mx, sm[sp]);
+    for (int sp = kCombRound; sp < ns; sp++) mx = fmaxf(mx, sm[sp]);
     float o = 0.0f, l = 0.0f;
+    const int cnt = round_cnt(0);
 #pragma unroll
     for (int i = 0; i < NS; i++) {
         const int sp = q + NQ * i;
@@ -1144,6 +1156,19 @@ __device__ __forceinline__ int eng_combine(const KCONST EngCombine &cb, int task
         const float w = expf(sm[sp] - mx);
         o += w * os[i];
         l += w * sl[sp];
+    }
+    for (int r0 = kCombRound; r0 < ns; r0 += kCombRound) {  // caches past 8,192 rows
+        const int rc = round_cnt(r0);
+        wait_strided<NS>(base + (size_t)(r0 + q) * (HD + 2) + 2 + d, (size_t)NQ * (HD + 2), rc, tb + cb.part_tag, os,
+                         c);
+#pragma unroll
+        for (int i = 0; i < NS; i++) {
+            const int sp = r0 + q + NQ * i;
+            if (i >= rc || sm[sp] == -INFINITY) continue;
+            const float w = expf(sm[sp] - mx);
+            o += w * os[i];
+            l += w * sl[sp];
+        }
     }
     po[q * HD + d] = o;
     pl[q * HD + d] = l;

@@ -10,7 +10,8 @@ oracle on the same seeded random-init weights and inputs:
 - two talker steps from caches loaded to 564, 2064 and 8184 N(0,1) rows, on
   the frame engine and on the multi-kernel path (k_attn);
 - two talker steps from caches loaded to 16384 and 32766 N(0,1) rows (the
-  latter at the last two positions of the 32768-row RoPE table);
+  latter at the last two positions of the 32768-row RoPE table), on both
+  paths;
 - 16 batched streams (qtts_generate_codes_batch) in 2064-row caches loaded
   to 2000 N(0,1) rows: 3 sampled frames, every stream's codes, frame count,
   cache length and appended cache rows.
@@ -198,15 +199,18 @@ def test_config4_bench_window(full):
 
 
 @pytest.mark.timeout(900)
-@pytest.mark.parametrize("L,frames", [(8172, 16), (20000, 4)])
-def test_loop_long_caches(full, L, frames):
+@pytest.mark.parametrize("L,frames,engine", [(8172, 16, "frame"), (20000, 4, "frame"), (20000, 4, "ops")])
+def test_loop_long_caches(full, monkeypatch, L, frames, engine):
     """The talker + predictor loop from a cache loaded to L N(0,1) rows:
-    8172 rows in the frame engine's largest cache (8192 rows: one launch of
-    16 codes whose talker attention splits hold up to 256 positions), and
-    20000 rows, past that limit, where the loop runs on the multi-kernel
-    path and its one-row attention takes 79 splits of at most 256 positions.
-    Sampled frames: codes identical, appended cache rows within the bars."""
+    8172 rows in an 8192-row cache (the frame engine's talker attention at
+    32 splits of up to 256 positions, one launch of 16 codes), and 20000 rows
+    (past 32 splits: 79 splits of at most 256 positions, several attention
+    tasks per block and a combine step in three rounds), on the frame engine
+    and on the multi-kernel path.  Sampled frames: codes identical, appended
+    cache rows within the bars."""
     tw, pw, t, p, ot, op = full
+    if engine == "ops":
+        monkeypatch.setenv("QTTS_ENGINE", "ops")
     c = tw.cfg
     kv, okv = _loaded_caches(t, ot, c, L, L + frames + 4, 46, "past")
     lh = qtts.synth_normal_f32(46, "past.h", c.hidden)
@@ -310,8 +314,9 @@ def test_talker_steps_long_cache(full, monkeypatch, L, engine):
     """Two talker steps (forward_with_embedding) from a cache loaded to L
     N(0,1) rows, on the frame engine and on the multi-kernel path (k_attn,
     up to 64 position splits): hidden, logits and the two appended cache rows
-    against the oracle.  L = 8184 fills the frame engine's largest cache
-    (8192 rows: 32 splits of 256 positions, its score buffer's size)."""
+    against the oracle.  L = 8184 fills the largest cache the frame engine
+    covers with 32 splits (8192 rows: 256 positions each, its score
+    buffer's size)."""
     tw, _, t, _, ot, _ = full
     if engine == "ops":
         monkeypatch.setenv("QTTS_ENGINE", "ops")
@@ -337,18 +342,29 @@ def test_talker_steps_long_cache(full, monkeypatch, L, engine):
     kv.close()
 
 
+# The appended rows of the later layers carry the error of softmax sums over
+# 16K-32K random positions taken in another order (measured up to 6.3e-5 on
+# the multi-kernel path and 4.4e-5 on the frame engine at 16384 rows, against
+# ~1e-6 in the hidden state).
+CACHE_ROWS_TIGHT = 5e-4
+
+
 @pytest.mark.timeout(900)
 @pytest.mark.parametrize("L", [16384, 32766])
-def test_talker_steps_max_context(full, L):
+@pytest.mark.parametrize("engine", ["frame", "ops"])
+def test_talker_steps_max_context(full, monkeypatch, L, engine):
     """Caches past 16384 rows, up to the maximum: two talker steps at
     positions L and L + 1 -- at L = 32766 the last rows of the 32768-row
     RoPE table (src/rope.rs:11-41) -- from a cache loaded to L N(0,1) rows
-    in an (L + 2)-row capacity (7.5 GB of K/V at the maximum).  Past 8192
-    rows the multi-kernel path runs the step; its one-row attention then
-    needs more than 64 splits to keep every split within the 256-entry score
-    buffer of k_attn (65 and 128 splits here).  Hidden, logits and the two
+    in an (L + 2)-row capacity (7.5 GB of K/V at the maximum).  Both paths
+    keep every attention split within 256 positions, their score buffers'
+    size: the frame engine with 65 and 128 splits (4 attention tasks per
+    block, the combine in rounds of 32 splits), the multi-kernel path's
+    one-row k_attn with 65 and 128 splits.  Hidden, logits and the two
     appended cache rows against the oracle."""
     tw, _, t, _, ot, _ = full
+    if engine == "ops":
+        monkeypatch.setenv("QTTS_ENGINE", "ops")
     c = tw.cfg
     cap = L + 2
     assert cap <= c.max_position
@@ -373,5 +389,7 @@ def test_talker_steps_max_context(full, L):
     assert len(kv) == len(okv) == cap
     gk, gv = kv.store()
     rk, rv = okv.store()
-    assert within(gk[:, L:], rk[:, L:]) and within(gv[:, L:], rv[:, L:])
+    ek, ev = rel_err(gk[:, L:], rk[:, L:]), rel_err(gv[:, L:], rv[:, L:])
+    print(f"appended rows: k rel err {ek:.2e}, v {ev:.2e}", flush=True)
+    assert within(gk[:, L:], rk[:, L:], CACHE_ROWS_TIGHT) and within(gv[:, L:], rv[:, L:], CACHE_ROWS_TIGHT)
     kv.close()
