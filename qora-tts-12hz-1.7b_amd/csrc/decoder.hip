@@ -261,11 +261,31 @@ __global__ __launch_bounds__(256) void k_dec_snake(const float *x, const float *
     const float a = expf(alpha[c]), inv_b = expf(-beta[c]);
     const size_t base = (size_t)c * len;
     float m = 0.0f;
-    for (int t = blockIdx.x * blockDim.x + threadIdx.x; t < len; t += gridDim.x * blockDim.x) {
-        const float v = x[base + t], s = sinf(a * v);
+    auto snake = [&](float v) {
+        const float s = sinf(a * v);
         const float o = v + inv_b * s * s;
-        out[base + t] = o;
         m = fmaxf(m, fabsf(o));  // a NaN o leaves m as it was
+        return o;
+    };
+    const int stride = gridDim.x * blockDim.x;
+    if ((len & 3) == 0) {
+        // rows of a multiple of 4 samples (every decoder stage): 16-byte
+        // loads and stores, two in flight per thread
+        const float4 *x4 = reinterpret_cast<const float4 *>(x + base);
+        float4 *o4 = reinterpret_cast<float4 *>(out + base);
+        const int n4 = len >> 2;
+        int t = blockIdx.x * blockDim.x + threadIdx.x;
+        for (; t + stride < n4; t += 2 * stride) {
+            const float4 v0 = x4[t], v1 = x4[t + stride];
+            o4[t] = make_float4(snake(v0.x), snake(v0.y), snake(v0.z), snake(v0.w));
+            o4[t + stride] = make_float4(snake(v1.x), snake(v1.y), snake(v1.z), snake(v1.w));
+        }
+        if (t < n4) {
+            const float4 v0 = x4[t];
+            o4[t] = make_float4(snake(v0.x), snake(v0.y), snake(v0.z), snake(v0.w));
+        }
+    } else {
+        for (int t = blockIdx.x * blockDim.x + threadIdx.x; t < len; t += stride) out[base + t] = snake(x[base + t]);
     }
     if (!amax) return;  // uniform
     __shared__ float red[4];
@@ -745,8 +765,10 @@ void launch_dec_lnorm(hipStream_t st, const float *x, const float *g, const floa
 
 void launch_dec_snake(hipStream_t st, const float *x, const float *alpha, const float *beta, int ch, int len,
                       float *out, unsigned *amax) {
-    // about kSnakeBlocks blocks in all, at least one per channel
-    const unsigned per_row = std::max(1u, std::min<unsigned>(blocks_for((size_t)len, 256), kSnakeBlocks / (unsigned)ch));
+    // about kSnakeBlocks blocks in all, at least one per channel (rows of a
+    // multiple of 4 samples take 4 per thread and iteration)
+    const size_t items = (len & 3) == 0 ? (size_t)len / 4 : (size_t)len;
+    const unsigned per_row = std::max(1u, std::min<unsigned>(blocks_for(items, 256), kSnakeBlocks / (unsigned)ch));
     hipLaunchKernelGGL(k_dec_snake, dim3(per_row, (unsigned)ch), dim3(256), 0, st, x, alpha, beta, ch, len, out, amax);
 }
 
