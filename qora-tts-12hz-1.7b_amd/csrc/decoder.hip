@@ -307,8 +307,19 @@ __global__ void k_dec_fill_u32(unsigned *p, int n, unsigned v) {
 // records it (for inputs of the matrix-core layers that no SnakeBeta makes).
 __global__ __launch_bounds__(256) void k_dec_absmax(const float *x, size_t n, unsigned *amax) {
     float m = 0.0f;
-    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
-        m = fmaxf(m, fabsf(x[i]));
+    const size_t stride = (size_t)gridDim.x * blockDim.x, t0 = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if ((n & 3) == 0 && ((uintptr_t)x & 15) == 0) {
+        // 16-byte loads, four in flight per thread
+        const float4 *x4 = reinterpret_cast<const float4 *>(x);
+        const size_t n4 = n >> 2;
+#pragma unroll 4
+        for (size_t i = t0; i < n4; i += stride) {
+            const float4 v = x4[i];
+            m = fmaxf(m, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
+    } else {
+        for (size_t i = t0; i < n; i += stride) m = fmaxf(m, fabsf(x[i]));
+    }
     __shared__ float red[4];
     m = wave_max(m);
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = m;
@@ -834,7 +845,9 @@ void launch_dec_conv_mfma(hipStream_t st, const DecConvMfmaParams &p) {
 }
 
 void launch_dec_absmax(hipStream_t st, const float *x, size_t n, unsigned *amax) {
-    const unsigned blocks = std::min<unsigned>(blocks_for(n, 256), 2048u);
+    // at most 512 blocks: each folds its maximum into one of the 64 slots
+    // with one atomic, so fewer blocks queue fewer atomics per slot
+    const unsigned blocks = std::min<unsigned>(blocks_for((n + 3) / 4, 256), 512u);
     hipLaunchKernelGGL(k_dec_absmax, dim3(blocks), dim3(256), 0, st, x, n, amax);
 }
 
