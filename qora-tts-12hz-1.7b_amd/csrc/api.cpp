@@ -3250,9 +3250,19 @@ qtts_status dec_linear_mfma(qtts_decoder *d, const DecConvMfma &m, const float *
 qtts_status dec_transposed_mfma(qtts_decoder *d, const qtts_conv_view &v, const std::vector<DecConvMfma> &ph,
                                 const float *x, const unsigned *xmax, int len, float *c) {
     const int J = v.kernel_size / v.stride;
+    // up to kDecMaxPhases output phases in one launch (grid z = phase): the
+    // phases share their input, shapes and weight exponent
+    const bool one = v.stride > 1 && v.stride <= kDecMaxPhases;
     for (int r = 0; r < v.stride; r++) {
         const DecConvMfma &m = ph[(size_t)r];
         DecConvMfmaParams p{};
+        if (one) {
+            p.nphase = v.stride;
+            for (int q = 0; q < v.stride; q++) {
+                p.ph_wh[q] = ph[(size_t)q].wh;
+                p.ph_wl[q] = ph[(size_t)q].wl;
+            }
+        }
         p.wh = m.wh;
         p.wl = m.wl;
         p.ew = m.ew;
@@ -3276,6 +3286,7 @@ qtts_status dec_transposed_mfma(qtts_decoder *d, const qtts_conv_view &v, const 
         p.phase = r;
         launch_dec_conv_mfma(d->ctx->stream, p);
         QTTS_TRY(check_launch(d->ctx, "k_dec_conv_mfma"));
+        if (one) break;  // the launch ran every phase
     }
     return QTTS_OK;
 }

@@ -407,6 +407,9 @@ __global__ __launch_bounds__(256) void k_dec_conv_mfma(DecConvMfmaParams P) {
     const int n = (blockIdx.x * 4 + wave) * 32 + col;  // this lane's output step
     const int t0 = blockIdx.y * MT;
     const int len = P.len, cin16 = P.cin16, ksteps = P.ksteps, nstage = ksteps / G;
+    const bool multi = P.nphase > 1;  // uniform
+    const _Float16 *wh = multi ? P.ph_wh[blockIdx.z] : P.wh, *wl = multi ? P.ph_wl[blockIdx.z] : P.wl;
+    const int phase = multi ? (int)blockIdx.z : P.phase;
     // max |x| over the producer's slots, one per lane
     const int ex = split_exponent(wave_max(__uint_as_float(P.xmax[lane])));
     const float xs = ldexpf(1.0f, ex);
@@ -418,7 +421,7 @@ __global__ __launch_bounds__(256) void k_dec_conv_mfma(DecConvMfmaParams P) {
         for (int k = 0; k < UPW; k++) {
             const int u = wave + 4 * k, hl = u & 1, t = (u >> 1) % MT, gs = (u >> 1) / MT;
             const size_t o = ((size_t)(t0 + t) * ksteps + g * G + gs) * 64 + lane;
-            ua[k] = reinterpret_cast<const half8 *>(hl ? P.wl : P.wh)[o];
+            ua[k] = reinterpret_cast<const half8 *>(hl ? wl : wh)[o];
         }
     };
     // the 8 raw x values of this lane at step s (zero past the taps of a
@@ -504,7 +507,7 @@ __global__ __launch_bounds__(256) void k_dec_conv_mfma(DecConvMfmaParams P) {
             float v = ldexpf(acc[t][r], sc);
             if (P.bias) v += P.bias[m];
             if (P.act == DEC_ACT_GELU) v = dec_gelu(v);
-            float *dst = P.c + (long long)m * P.ldc + (long long)n * P.out_stride + P.phase;
+            float *dst = P.c + (long long)m * P.ldc + (long long)n * P.out_stride + phase;
             switch (P.epi) {
                 case DEC_EPI_STORE: *dst = v; break;
                 case DEC_EPI_ACCUM: *dst += v; break;
@@ -531,6 +534,9 @@ __global__ __launch_bounds__(256) void k_dec_conv_mfma_ks(DecConvMfmaParams P) {
     const int n = blockIdx.x * 32 + col;
     const int tile = blockIdx.y;
     const int len = P.len, ksteps = P.ksteps;
+    const bool multi = P.nphase > 1;  // uniform
+    const _Float16 *wh = multi ? P.ph_wh[blockIdx.z] : P.wh, *wl = multi ? P.ph_wl[blockIdx.z] : P.wl;
+    const int phase = multi ? (int)blockIdx.z : P.phase;
     const int q = (ksteps + 3) / 4, s0 = wave * q, s1 = min(ksteps, s0 + q);
     const int ex = split_exponent(wave_max(__uint_as_float(P.xmax[lane])));
     const float xs = ldexpf(1.0f, ex);
@@ -550,8 +556,8 @@ __global__ __launch_bounds__(256) void k_dec_conv_mfma_ks(DecConvMfmaParams P) {
             for (int i = 0; i < 8; i++) xv[i] = ok && ci0 + i < cpl ? xp[(long long)i * P.sxc] : 0.0f;
         }
         const size_t o = ((size_t)tile * ksteps + s) * 64 + lane;
-        ah = reinterpret_cast<const half8 *>(P.wh)[o];
-        al = reinterpret_cast<const half8 *>(P.wl)[o];
+        ah = reinterpret_cast<const half8 *>(wh)[o];
+        al = reinterpret_cast<const half8 *>(wl)[o];
     };
     f32x16 acc;
 #pragma unroll
@@ -599,7 +605,7 @@ __global__ __launch_bounds__(256) void k_dec_conv_mfma_ks(DecConvMfmaParams P) {
         float v = ldexpf(acc[r], sc);
         if (P.bias) v += P.bias[m];
         if (P.act == DEC_ACT_GELU) v = dec_gelu(v);
-        float *dst = P.c + (long long)m * P.ldc + (long long)n * P.out_stride + P.phase;
+        float *dst = P.c + (long long)m * P.ldc + (long long)n * P.out_stride + phase;
         switch (P.epi) {
             case DEC_EPI_STORE: *dst = v; break;
             case DEC_EPI_ACCUM: *dst += v; break;
@@ -632,6 +638,9 @@ __global__ __launch_bounds__(256) void k_dec_conv_win(DecConvMfmaParams P) {
     const int n0 = blockIdx.x * 128, n = n0 + wave * 32 + col;
     const int t0 = blockIdx.y * MT;
     const int len = P.len, ks = P.ksize, dil = P.dilation, ksteps = P.ksteps;
+    const bool multi = P.nphase > 1;  // uniform
+    const _Float16 *wh = multi ? P.ph_wh[blockIdx.z] : P.wh, *wl = multi ? P.ph_wl[blockIdx.z] : P.wl;
+    const int phase = multi ? (int)blockIdx.z : P.phase;
     const int W = 128 + (ks - 1) * dil, wpos = n0 - (ks - 1) * dil + tid;  // this thread's window position
     const bool wok = tid < W && wpos >= 0 && wpos < len;
     const int ncb = P.cin16 / 16;
@@ -661,8 +670,8 @@ __global__ __launch_bounds__(256) void k_dec_conv_win(DecConvMfmaParams P) {
 #pragma unroll
         for (int t = 0; t < MT; t++) {
             const size_t o = ((size_t)(t0 + t) * ksteps + s) * 64 + lane;
-            ah[t] = reinterpret_cast<const half8 *>(P.wh)[o];
-            al[t] = reinterpret_cast<const half8 *>(P.wl)[o];
+            ah[t] = reinterpret_cast<const half8 *>(wh)[o];
+            al[t] = reinterpret_cast<const half8 *>(wl)[o];
         }
     };
     f32x16 acc[MT];
@@ -717,7 +726,7 @@ __global__ __launch_bounds__(256) void k_dec_conv_win(DecConvMfmaParams P) {
             float v = ldexpf(acc[t][r], sc);
             if (P.bias) v += P.bias[m];
             if (P.act == DEC_ACT_GELU) v = dec_gelu(v);
-            float *dst = P.c + (long long)m * P.ldc + (long long)n * P.out_stride + P.phase;
+            float *dst = P.c + (long long)m * P.ldc + (long long)n * P.out_stride + phase;
             switch (P.epi) {
                 case DEC_EPI_STORE: *dst = v; break;
                 case DEC_EPI_ACCUM: *dst += v; break;
@@ -796,7 +805,7 @@ void launch_dec_conv_repack(hipStream_t st, const float *w, long long sm, long l
 
 template <bool KF>
 static void launch_conv_mfma_kf(hipStream_t st, const DecConvMfmaParams &p, int mt) {
-    const dim3 grid(blocks_for((size_t)p.len, 128), (unsigned)(p.mtiles / mt));
+    const dim3 grid(blocks_for((size_t)p.len, 128), (unsigned)(p.mtiles / mt), (unsigned)std::max(1, p.nphase));
     switch (mt) {
         case 4: hipLaunchKernelGGL((k_dec_conv_mfma<4, KF>), grid, dim3(256), 0, st, p); break;
         case 3: hipLaunchKernelGGL((k_dec_conv_mfma<3, KF>), grid, dim3(256), 0, st, p); break;
@@ -816,9 +825,10 @@ void launch_dec_conv_mfma(hipStream_t st, const DecConvMfmaParams &p) {
     const char *plan = std::getenv("QTTS_DEC_CONV");
     const bool force_tiles = plan && std::strcmp(plan, "tiles") == 0, force_split = plan && std::strcmp(plan, "split") == 0;
     const bool kf = p.sxc == 1 && p.cin % 8 == 0 && p.sxn % 4 == 0 && ((uintptr_t)p.x & 15) == 0;
+    const size_t nph = (size_t)std::max(1, p.nphase);  // a transposed convolution's phases in one launch
     if (force_split ||
-        (!force_tiles && (size_t)blocks_for((size_t)p.len, 128) * (size_t)p.mtiles < kDecFillBlocks)) {
-        const dim3 grid(blocks_for((size_t)p.len, 32), (unsigned)p.mtiles);
+        (!force_tiles && (size_t)blocks_for((size_t)p.len, 128) * (size_t)p.mtiles * nph < kDecFillBlocks)) {
+        const dim3 grid(blocks_for((size_t)p.len, 32), (unsigned)p.mtiles, (unsigned)nph);
         if (kf)
             hipLaunchKernelGGL(k_dec_conv_mfma_ks<true>, grid, dim3(256), 0, st, p);
         else
@@ -826,10 +836,10 @@ void launch_dec_conv_mfma(hipStream_t st, const DecConvMfmaParams &p) {
         return;
     }
     int mt = p.mtiles % 4 == 0 ? 4 : p.mtiles % 3 == 0 ? 3 : p.mtiles % 2 == 0 ? 2 : 1;
-    if (!force_tiles && (size_t)blocks_for((size_t)p.len, 128) * (size_t)(p.mtiles / mt) < 256) mt = 1;
+    if (!force_tiles && (size_t)blocks_for((size_t)p.len, 128) * (size_t)(p.mtiles / mt) * nph < 256) mt = 1;
     if (p.ksize >= 3 && p.sxn == 1 && p.sxc == p.len && 128 + (p.ksize - 1) * p.dilation <= 256) {
         // a channel-first convolution with 3 or more taps whose window fits the block's threads
-        const dim3 grid(blocks_for((size_t)p.len, 128), (unsigned)(p.mtiles / mt));
+        const dim3 grid(blocks_for((size_t)p.len, 128), (unsigned)(p.mtiles / mt), (unsigned)nph);
         switch (mt) {
             case 4: hipLaunchKernelGGL(k_dec_conv_win<4>, grid, dim3(256), 0, st, p); break;
             case 3: hipLaunchKernelGGL(k_dec_conv_win<3>, grid, dim3(256), 0, st, p); break;

@@ -105,6 +105,8 @@ enum DecEpi { DEC_EPI_STORE = 0, DEC_EPI_ACCUM = 1, DEC_EPI_SCALED_RESID = 2, DE
 // multiple of 16 with zero weights); x(ci, p) = x[ci * sxc + p * sxn],
 // split on the fly.  A linear
 // layer is the case ksize = 1 with m the output feature and n the row.
+constexpr int kDecMaxPhases = 8;  // output phases of one transposed-convolution launch
+
 struct DecConvMfmaParams {
     const _Float16 *wh, *wl;  // [mtiles][ksteps][64][8]; row m = 32 * tile + lane % 32
     int ew;                   // the weights were scaled by 2^ew
@@ -122,6 +124,11 @@ struct DecConvMfmaParams {
     long long out_stride;
     int phase;
     const float *resid;       // DEC_EPI_RESID_IN: at the output's index (may be c)
+    // nphase > 1: one launch runs the output phases 0 .. nphase-1 of a
+    // transposed convolution (grid z = phase); phase p's weights are
+    // ph_wh[p] / ph_wl[p] (wh, wl and phase are then unused)
+    int nphase;
+    const _Float16 *ph_wh[kDecMaxPhases], *ph_wl[kDecMaxPhases];
 };
 
 struct DecAttnParams {
