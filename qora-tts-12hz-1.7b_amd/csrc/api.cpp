@@ -3028,6 +3028,10 @@ struct qtts_decoder {
     // the Vocos input and output convolutions
     DecConvMfma proj0, proj_rest, pre_conv, tf_in, tf_out, vocos_init, out_conv;
     std::vector<std::array<DecConvMfma, 7>> layer_mfma;
+    // per layer, q|k|v and gate|up as one copy each (the linears that share
+    // an input in one launch; when every part is a whole number of tiles)
+    std::vector<std::array<DecConvMfma, 2>> layer_cat;
+    bool cat = false;
     std::vector<std::vector<DecConvMfma>> cnx_up_mfma;
     std::vector<std::array<DecConvMfma, 2>> pw_mfma;
     unsigned *amax = nullptr;  // [amax_slots][kDecMaxSlots]: max |x| of each such convolution's input, cleared per decode
@@ -3135,6 +3139,35 @@ qtts_status dec_convt_mfma(qtts_ctx *c, Owner &own, const qtts_conv_view &h, con
 qtts_status dec_lin_mfma(qtts_ctx *c, Owner &own, const float *hw, const float *dw, int K, int N, DecConvMfma *out) {
     const int ew = dec_weight_exponent(hw, (size_t)K * N);
     return dec_mfma_copy(c, own, dw, 1, N, 0, 0, N, K, 1, ew, out);
+}
+
+// Linear layers that read one input, as one copy: part p's N output
+// features (a multiple of 32) are tiles p * N / 32 .., so the launch's
+// output row holds the parts side by side; one weight exponent for all
+// (the one of the largest max |W|).
+qtts_status dec_lin_mfma_cat(qtts_ctx *c, Owner &own, const float *const *hw, const float *const *dw, int parts,
+                             int K, int N, DecConvMfma *out) {
+    int ew = 0;
+    for (int q = 0; q < parts; q++) {
+        const int e = dec_weight_exponent(hw[q], (size_t)K * N);
+        ew = q == 0 ? e : std::min(ew, e);
+    }
+    DecConvMfma m;
+    m.ew = ew;
+    m.cin16 = (K + 15) / 16 * 16;
+    const int tiles = N / 32;
+    m.mtiles = parts * tiles;
+    m.ksteps = (m.cin16 / 16 + kConvStage - 1) / kConvStage * kConvStage;
+    const size_t per = (size_t)tiles * m.ksteps * 64 * 8;
+    QTTS_TRY(own.alloc(c, &m.wh, per * parts));
+    QTTS_TRY(own.alloc(c, &m.wl, per * parts));
+    for (int q = 0; q < parts; q++) {
+        launch_dec_conv_repack(c->stream, dw[q], 1, N, 0, 0, N, K, 1, m.cin16, tiles, m.ksteps, ew, m.wh + per * q,
+                               m.wl + per * q);
+        QTTS_TRY(check_launch(c, "k_dec_conv_repack"));
+    }
+    *out = m;
+    return QTTS_OK;
 }
 
 qtts_status dec_check_transposed(qtts_ctx *c, const qtts_conv_view &v, int in_ch, const char *name) {
@@ -3324,6 +3357,8 @@ qtts_status dec_decode(qtts_decoder *d, const uint32_t *d_codes, int T, int ld, 
     float *V = dec_buf(d, 10, (size_t)T * ad, &s), *AO = dec_buf(d, 11, (size_t)T * ad, &s);
     float *G = dec_buf(d, 12, (size_t)T * inter, &s), *U = dec_buf(d, 13, (size_t)T * inter, &s);
     float *P1 = dec_buf(d, 14, std::max<size_t>(inner_max, 1), &s);
+    float *QKV = d->cat ? dec_buf(d, 15, (size_t)T * 3 * ad, &s) : nullptr;
+    float *GU = d->cat ? dec_buf(d, 16, (size_t)T * 2 * inter, &s) : nullptr;
     if (s != QTTS_OK) return s;
 
     // Every matrix-core layer scales its input by a power of two from the
@@ -3369,6 +3404,7 @@ qtts_status dec_decode(qtts_decoder *d, const uint32_t *d_codes, int T, int ld, 
     a.q = Q;
     a.k = K;
     a.v = V;
+    a.ld = ad;
     a.out = AO;
     a.T = T;
     a.heads = w.num_heads;
@@ -3381,10 +3417,21 @@ qtts_status dec_decode(qtts_decoder *d, const uint32_t *d_codes, int T, int ld, 
         launch_dec_rmsnorm(st, X, L.input_norm, T, hid, 1e-5f, XN);
         QTTS_TRY(check_launch(c, "k_dec_rmsnorm"));
         QTTS_TRY(maxof(XN, (size_t)T * hid, &mx));
-        QTTS_TRY(dec_linear_mfma(d, lm[0], XN, hid, 1, T, hid, ad, mx, nullptr, Q, ad, 1, DEC_EPI_STORE));
-        QTTS_TRY(dec_linear_mfma(d, lm[1], XN, hid, 1, T, hid, ad, mx, nullptr, K, ad, 1, DEC_EPI_STORE));
-        QTTS_TRY(dec_linear_mfma(d, lm[2], XN, hid, 1, T, hid, ad, mx, nullptr, V, ad, 1, DEC_EPI_STORE));
-        launch_dec_rope(st, Q, K, T, w.num_heads, w.head_dim, w.rope_cos, w.rope_sin, w.rope_rows);
+        if (d->cat) {
+            // q|k|v in one launch: row t holds q, k, v side by side (3 * ad)
+            QTTS_TRY(dec_linear_mfma(d, d->layer_cat[li][0], XN, hid, 1, T, hid, 3 * ad, mx, nullptr, QKV, 3 * ad, 1,
+                                     DEC_EPI_STORE));
+            a.q = QKV;
+            a.k = QKV + ad;
+            a.v = QKV + 2 * ad;
+            a.ld = 3 * ad;
+        } else {
+            QTTS_TRY(dec_linear_mfma(d, lm[0], XN, hid, 1, T, hid, ad, mx, nullptr, Q, ad, 1, DEC_EPI_STORE));
+            QTTS_TRY(dec_linear_mfma(d, lm[1], XN, hid, 1, T, hid, ad, mx, nullptr, K, ad, 1, DEC_EPI_STORE));
+            QTTS_TRY(dec_linear_mfma(d, lm[2], XN, hid, 1, T, hid, ad, mx, nullptr, V, ad, 1, DEC_EPI_STORE));
+        }
+        launch_dec_rope(st, const_cast<float *>(a.q), const_cast<float *>(a.k), T, w.num_heads, w.head_dim, w.rope_cos,
+                        w.rope_sin, w.rope_rows, a.ld);
         QTTS_TRY(check_launch(c, "k_dec_rope"));
         launch_dec_attn(st, a);
         QTTS_TRY(check_launch(c, "k_dec_attn"));
@@ -3394,9 +3441,16 @@ qtts_status dec_decode(qtts_decoder *d, const uint32_t *d_codes, int T, int ld, 
         launch_dec_rmsnorm(st, X, L.post_attn_norm, T, hid, 1e-5f, XN);
         QTTS_TRY(check_launch(c, "k_dec_rmsnorm"));
         QTTS_TRY(maxof(XN, (size_t)T * hid, &mx));
-        QTTS_TRY(dec_linear_mfma(d, lm[4], XN, hid, 1, T, hid, inter, mx, nullptr, G, inter, 1, DEC_EPI_STORE));
-        QTTS_TRY(dec_linear_mfma(d, lm[5], XN, hid, 1, T, hid, inter, mx, nullptr, U, inter, 1, DEC_EPI_STORE));
-        launch_dec_swiglu(st, G, U, (size_t)T * inter, G);
+        if (d->cat) {
+            // gate|up in one launch (row t: gate then up), SiLU(gate) * up into G
+            QTTS_TRY(dec_linear_mfma(d, d->layer_cat[li][1], XN, hid, 1, T, hid, 2 * inter, mx, nullptr, GU, 2 * inter,
+                                     1, DEC_EPI_STORE));
+            launch_dec_swiglu(st, GU, GU + inter, T, inter, 2 * inter, G);
+        } else {
+            QTTS_TRY(dec_linear_mfma(d, lm[4], XN, hid, 1, T, hid, inter, mx, nullptr, G, inter, 1, DEC_EPI_STORE));
+            QTTS_TRY(dec_linear_mfma(d, lm[5], XN, hid, 1, T, hid, inter, mx, nullptr, U, inter, 1, DEC_EPI_STORE));
+            launch_dec_swiglu(st, G, U, T, inter, inter, G);
+        }
         QTTS_TRY(check_launch(c, "k_dec_swiglu"));
         QTTS_TRY(maxof(G, (size_t)T * inter, &mx));
         QTTS_TRY(dec_linear_mfma(d, lm[6], G, inter, 1, T, inter, hid, mx, nullptr, X, hid, 1, DEC_EPI_SCALED_RESID,
@@ -3560,6 +3614,16 @@ qtts_status qtts_decoder_upload(qtts_ctx *c, const qtts_decoder_view *v, qtts_de
             (s = dec_lin_mfma(c, o, L.down_proj, D.down_proj, inter, hid, &lm[6])) != QTTS_OK)
             return bail(s);
         d->layer_mfma.push_back(lm);
+        d->cat = ad % 32 == 0 && inter % 32 == 0;
+        if (d->cat) {
+            std::array<DecConvMfma, 2> lc{};
+            const float *hq[3] = {L.q_proj, L.k_proj, L.v_proj}, *dq[3] = {D.q_proj, D.k_proj, D.v_proj};
+            const float *hg[2] = {L.gate_proj, L.up_proj}, *dg[2] = {D.gate_proj, D.up_proj};
+            if ((s = dec_lin_mfma_cat(c, o, hq, dq, 3, hid, ad, &lc[0])) != QTTS_OK ||
+                (s = dec_lin_mfma_cat(c, o, hg, dg, 2, hid, inter, &lc[1])) != QTTS_OK)
+                return bail(s);
+            d->layer_cat.push_back(lc);
+        }
         d->amax_slots += 4;  // the normed rows twice, the attention output, SiLU(gate) * up
         d->layers.push_back(D);
     }

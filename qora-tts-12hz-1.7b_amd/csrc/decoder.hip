@@ -83,14 +83,15 @@ __global__ __launch_bounds__(256) void k_dec_rmsnorm(const float *x, const float
 
 // Split-half rotation of q and k at position = frame; no rotation past the
 // table.  One thread per (frame, head, pair).
-__global__ void k_dec_rope(float *q, float *k, int T, int heads, int hd, const float *cs, const float *sn, int rows) {
+__global__ void k_dec_rope(float *q, float *k, int T, int heads, int hd, const float *cs, const float *sn, int rows,
+                           int ld) {
     const int half = hd / 2;
     const size_t idx = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (idx >= (size_t)T * heads * half) return;
     const int i = (int)(idx % half), h = (int)(idx / half % heads), t = (int)(idx / half / heads);
     if (t >= rows) return;
     const float c = cs[(size_t)t * half + i], s = sn[(size_t)t * half + i];
-    float *qb = q + (size_t)t * heads * hd + (size_t)h * hd, *kb = k + (size_t)t * heads * hd + (size_t)h * hd;
+    float *qb = q + (size_t)t * ld + (size_t)h * hd, *kb = k + (size_t)t * ld + (size_t)h * hd;
     float x0 = qb[i], x1 = qb[half + i];
     qb[i] = x0 * c - x1 * s;
     qb[half + i] = x1 * c + x0 * s;
@@ -109,16 +110,16 @@ __global__ __launch_bounds__(256) void k_dec_attn(DecAttnParams P) {
     const int pair = blockIdx.x * 4 + wave;
     const bool valid = pair < P.T * P.heads;  // wave-uniform; every wave reaches both barriers
     const int t = valid ? pair / P.heads : 0, h = valid ? pair - t * P.heads : 0;
-    const int ad = P.heads * P.hd;
+    const int ad = P.heads * P.hd, ld = P.ld > 0 ? P.ld : ad;
     const int start = t + 1 > P.window ? t + 1 - P.window : 0, n = t + 1 - start;
     if (valid)
-        for (int d = lane; d < P.hd; d += 64) qs[wave][d] = P.q[(size_t)t * ad + (size_t)h * P.hd + d];
+        for (int d = lane; d < P.hd; d += 64) qs[wave][d] = P.q[(size_t)t * ld + (size_t)h * P.hd + d];
     __syncthreads();
     float inv = 0.0f;
     if (valid) {
         float mx = -INFINITY;
         for (int s = lane; s < n; s += 64) {
-            const float *k = P.k + (size_t)(start + s) * ad + (size_t)h * P.hd;
+            const float *k = P.k + (size_t)(start + s) * ld + (size_t)h * P.hd;
             float dot = 0.0f;
             for (int d = 0; d < P.hd; d++) dot += qs[wave][d] * k[d];
             dot *= P.scale;
@@ -138,14 +139,16 @@ __global__ __launch_bounds__(256) void k_dec_attn(DecAttnParams P) {
     if (valid)
         for (int d = lane; d < P.hd; d += 64) {
             float o = 0.0f;
-            for (int s = 0; s < n; s++) o += (ps[wave][s] * inv) * P.v[(size_t)(start + s) * ad + (size_t)h * P.hd + d];
+            for (int s = 0; s < n; s++) o += (ps[wave][s] * inv) * P.v[(size_t)(start + s) * ld + (size_t)h * P.hd + d];
             P.out[(size_t)t * ad + (size_t)h * P.hd + d] = o;
         }
 }
 
-__global__ void k_dec_swiglu(const float *g, const float *u, size_t n, float *out) {
+__global__ void k_dec_swiglu(const float *g, const float *u, int rows, int width, int ld, float *out) {
     const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) out[i] = (g[i] / (1.0f + expf(-g[i]))) * u[i];
+    if (i >= (size_t)rows * width) return;
+    const size_t t = i / width, j = i - t * width, a = t * ld + j;
+    out[i] = (g[a] / (1.0f + expf(-g[a]))) * u[a];
 }
 
 // Causal depthwise convolution (padding kernel_size - 1), channel-first.
@@ -750,17 +753,18 @@ void launch_dec_rmsnorm(hipStream_t st, const float *x, const float *gamma, int 
 }
 
 void launch_dec_rope(hipStream_t st, float *q, float *k, int T, int heads, int hd, const float *cs, const float *sn,
-                     int rows) {
+                     int rows, int ld) {
     const size_t n = (size_t)T * heads * (hd / 2);
-    hipLaunchKernelGGL(k_dec_rope, dim3(blocks_for(n, 256)), dim3(256), 0, st, q, k, T, heads, hd, cs, sn, rows);
+    hipLaunchKernelGGL(k_dec_rope, dim3(blocks_for(n, 256)), dim3(256), 0, st, q, k, T, heads, hd, cs, sn, rows, ld);
 }
 
 void launch_dec_attn(hipStream_t st, const DecAttnParams &p) {
     hipLaunchKernelGGL(k_dec_attn, dim3(blocks_for((size_t)p.T * p.heads, 4)), dim3(256), 0, st, p);
 }
 
-void launch_dec_swiglu(hipStream_t st, const float *g, const float *u, size_t n, float *out) {
-    hipLaunchKernelGGL(k_dec_swiglu, dim3(blocks_for(n, 256)), dim3(256), 0, st, g, u, n, out);
+void launch_dec_swiglu(hipStream_t st, const float *g, const float *u, int rows, int width, int ld, float *out) {
+    const size_t n = (size_t)rows * width;
+    hipLaunchKernelGGL(k_dec_swiglu, dim3(blocks_for(n, 256)), dim3(256), 0, st, g, u, rows, width, ld, out);
 }
 
 void launch_dec_dwconv(hipStream_t st, const float *x, const float *w, const float *b, int ch, int len, int ks,

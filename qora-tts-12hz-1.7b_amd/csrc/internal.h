@@ -132,7 +132,8 @@ struct DecConvMfmaParams {
 };
 
 struct DecAttnParams {
-    const float *q, *k, *v;  // [T][heads * hd]
+    const float *q, *k, *v;  // rows of heads * hd values, ld apart (0: heads * hd)
+    int ld;
     float *out;
     int T, heads, hd, window;
     float scale;
@@ -331,9 +332,10 @@ void launch_qkv_rows(hipStream_t st, const QkvRowsParams &p);
 void launch_dec_gather(hipStream_t st, const DecGatherParams &p, int frames);
 void launch_dec_rmsnorm(hipStream_t st, const float *x, const float *gamma, int rows, int n, float eps, float *out);
 void launch_dec_rope(hipStream_t st, float *q, float *k, int T, int heads, int hd, const float *cs, const float *sn,
-                     int rows);
+                     int rows, int ld);  // q, k rows ld apart
 void launch_dec_attn(hipStream_t st, const DecAttnParams &p);
-void launch_dec_swiglu(hipStream_t st, const float *g, const float *u, size_t n, float *out);
+// out[t][j] = silu(g[t * ld + j]) * u[t * ld + j] for rows t < rows, j < width (out rows width apart)
+void launch_dec_swiglu(hipStream_t st, const float *g, const float *u, int rows, int width, int ld, float *out);
 void launch_dec_dwconv(hipStream_t st, const float *x, const float *w, const float *b, int ch, int len, int ks,
                        float *out);
 void launch_dec_lnorm(hipStream_t st, const float *x, const float *g, const float *b, int ch, int len, float eps,
