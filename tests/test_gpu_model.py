@@ -205,6 +205,23 @@ def test_loop_tiny(tiny, greedy):
     assert within(lh, olh)
 
 
+def test_engine_swiglu_full_panels(ctx, tiny, monkeypatch):
+    """QTTS_ENGINE_SWIGLU_COLS=32 (read when a frame program is built) runs
+    the predictor's SwiGLU step in whole-panel tasks instead of half panels:
+    a predictor made with it gives the oracle's codes over a sampled loop."""
+    tw, pw, _, _, ot, op = tiny
+    monkeypatch.setenv("QTTS_ENGINE_SWIGLU_COLS", "32")
+    t, p = qtts.Talker(ctx, tw), qtts.CodePredictor(ctx, pw)
+    last_hidden, text, pad = _loop_inputs(tw, 33)
+    logits = ot.apply_codec_head(last_hidden)
+    params = qtts.loop_params(24, temperature=0.8, top_k=50, repetition_penalty=1.05, stop_on_eos=False)
+    kv, okv = t.new_kv(32), ot.new_kv(32)
+    got = qtts.generate_codes(t, p, kv, p.new_kv(), last_hidden, logits, 0, text, pad, params, seed=53)
+    ref = oracle.generate_codes(ot, op, okv, op.new_kv(), last_hidden, logits, 0, text, pad, params, seed=53)
+    assert np.array_equal(got, ref), np.argwhere(got != ref)[:5]
+    kv.close()
+
+
 def test_engine_tag_restart(tiny, monkeypatch):
     """The frame engine's 32-bit hand-off tags (8192 per code) run out every
     524,288 codes of a context; it then restarts them in a new epoch after
