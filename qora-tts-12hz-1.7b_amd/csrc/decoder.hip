@@ -18,7 +18,8 @@
 //                 causal convolutions as implicit GEMMs, one output phase
 //                 of a transposed convolution, linear layers as one tap;
 //                 fused epilogues; k_dec_conv_win for convolutions of 3+
-//                 taps (the input window split once into LDS),
+//                 taps (the input window split once into LDS; the variant
+//                 k_dec_conv_win_tw, one channel tile per wave, at 4 tiles),
 //                 k_dec_conv_mfma_ks for launches too small to fill the GPU
 //  k_dec_absmax   max |x| of a layer input (the operand scale)
 #include <hip/hip_runtime.h>
@@ -740,6 +741,117 @@ __global__ __launch_bounds__(256) void k_dec_conv_win(DecConvMfmaParams P) {
         }
 }
 
+// k_dec_conv_win with the waves' roles swapped, for 4 channel tiles per
+// block: wave w owns channel tile 4 * blockIdx.y + w -- its A operands
+// loaded by it alone, where every wave of k_dec_conv_win<4> loads all four
+// tiles' -- and all four 32-position tiles of the block, whose B operands it
+// reads from the staged window (LDS, twice L1's bandwidth).  Per step a CU
+// then reads 8 KiB of A operands through L1 instead of 32 KiB.  Same window,
+// operands and product order per output as k_dec_conv_win: the same bits.
+__global__ __launch_bounds__(256) void k_dec_conv_win_tw(DecConvMfmaParams P) {
+    static_assert(kDecMaxSlots == 64, "one max slot per lane");
+    constexpr int WMAX = 256, PT = 4;  // window positions; 32-position tiles per block
+    __shared__ __align__(16) _Float16 wh_s[2][WMAX][16], wl_s[2][WMAX][16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int col = lane & 31, half = lane >> 5;
+    const int n0 = blockIdx.x * 128;
+    const int tile = blockIdx.y * 4 + wave;  // < mtiles (the grid has mtiles / 4 rows)
+    const int len = P.len, ks = P.ksize, dil = P.dilation, ksteps = P.ksteps;
+    const bool multi = P.nphase > 1;  // uniform
+    const _Float16 *wh = multi ? P.ph_wh[blockIdx.z] : P.wh, *wl = multi ? P.ph_wl[blockIdx.z] : P.wl;
+    const int phase = multi ? (int)blockIdx.z : P.phase;
+    const int W = 128 + (ks - 1) * dil, wpos = n0 - (ks - 1) * dil + tid;  // this thread's window position
+    const bool wok = tid < W && wpos >= 0 && wpos < len;
+    const int ncb = P.cin16 / 16;
+    const int ex = split_exponent(wave_max(__uint_as_float(P.xmax[lane])));
+    const float xs = ldexpf(1.0f, ex);
+    auto load_win = [&](int cb, float (&v)[16]) {
+        const float *xp = P.x + (size_t)(16 * cb) * len + (wok ? wpos : 0);
+#pragma unroll
+        for (int c = 0; c < 16; c++) v[c] = wok && 16 * cb + c < P.cin ? xp[(size_t)c * len] : 0.0f;
+    };
+    auto store_win = [&](int buf, const float (&v)[16]) {
+        if (tid >= W) return;
+        half8 h[2], l[2];
+#pragma unroll
+        for (int c = 0; c < 16; c++) {
+            const float x = v[c] * xs;
+            const _Float16 hv = (_Float16)x;
+            h[c >> 3][c & 7] = hv;
+            l[c >> 3][c & 7] = (_Float16)(x - (float)hv);
+        }
+        *reinterpret_cast<half8 *>(&wh_s[buf][tid][0]) = h[0];
+        *reinterpret_cast<half8 *>(&wh_s[buf][tid][8]) = h[1];
+        *reinterpret_cast<half8 *>(&wl_s[buf][tid][0]) = l[0];
+        *reinterpret_cast<half8 *>(&wl_s[buf][tid][8]) = l[1];
+    };
+    auto load_a = [&](int s, half8 &ah, half8 &al) {
+        const size_t o = ((size_t)tile * ksteps + s) * 64 + lane;
+        ah = reinterpret_cast<const half8 *>(wh)[o];
+        al = reinterpret_cast<const half8 *>(wl)[o];
+    };
+    f32x16 acc[PT];
+#pragma unroll
+    for (int t = 0; t < PT; t++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[t][r] = 0.0f;
+    float wv[16];
+    load_win(0, wv);
+    store_win(0, wv);
+    half8 ah, al;
+    load_a(0, ah, al);
+    __syncthreads();
+    const int nsteps = ncb * ks;  // the steps past these (stage padding) hold zero weights
+    for (int cb = 0; cb < ncb; cb++) {
+        const int buf = cb & 1;
+        const bool more = cb + 1 < ncb;  // uniform
+        if (more) load_win(cb + 1, wv);
+        for (int tap = 0; tap < ks; tap++) {
+            const int s = cb * ks + tap;
+            half8 nh, nl;
+            load_a(s + 1 < nsteps ? s + 1 : s, nh, nl);
+#pragma unroll
+            for (int t = 0; t < PT; t++) {
+                const int p = t * 32 + col + tap * dil;
+                const half8 bh = *reinterpret_cast<const half8 *>(&wh_s[buf][p][8 * half]);
+                const half8 bl = *reinterpret_cast<const half8 *>(&wl_s[buf][p][8 * half]);
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bh, acc[t], 0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bl, acc[t], 0, 0, 0);
+                acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bh, acc[t], 0, 0, 0);
+            }
+            ah = nh;
+            al = nl;
+        }
+        // buf ^ 1 was last read in channel block cb - 1, before the last barrier
+        if (more) store_win(buf ^ 1, wv);
+        __syncthreads();
+    }
+    // D layout: lane l, register r -> row (r / 4) * 8 + (l / 32) * 4 + r % 4,
+    // column l % 32
+    const int sc = -(ex + P.ew);
+#pragma unroll
+    for (int t = 0; t < PT; t++) {
+        const int n = n0 + t * 32 + col;
+        if (n >= len) continue;
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            const int m = 32 * tile + (r >> 2) * 8 + half * 4 + (r & 3);
+            if (m >= P.M) continue;
+            float v = ldexpf(acc[t][r], sc);
+            if (P.bias) v += P.bias[m];
+            if (P.act == DEC_ACT_GELU) v = dec_gelu(v);
+            float *dst = P.c + (long long)m * P.ldc + (long long)n * P.out_stride + phase;
+            switch (P.epi) {
+                case DEC_EPI_STORE: *dst = v; break;
+                case DEC_EPI_ACCUM: *dst += v; break;
+                case DEC_EPI_SCALED_RESID: *dst += P.scale[m] * v; break;
+                case DEC_EPI_RESID_IN: *dst = P.resid[dst - P.c] + (P.scale ? P.scale[m] * v : v); break;
+                default: *dst = v < -1.0f ? -1.0f : (v > 1.0f ? 1.0f : v); break;  // DEC_EPI_CLAMP (NaN stays)
+            }
+        }
+    }
+}
+
 unsigned blocks_for(size_t n, unsigned per) { return (unsigned)((n + per - 1) / per); }
 
 }  // namespace
@@ -845,7 +957,7 @@ void launch_dec_conv_mfma(hipStream_t st, const DecConvMfmaParams &p) {
         // a channel-first convolution with 3 or more taps whose window fits the block's threads
         const dim3 grid(blocks_for((size_t)p.len, 128), (unsigned)(p.mtiles / mt), (unsigned)nph);
         switch (mt) {
-            case 4: hipLaunchKernelGGL(k_dec_conv_win<4>, grid, dim3(256), 0, st, p); break;
+            case 4: hipLaunchKernelGGL(k_dec_conv_win_tw, grid, dim3(256), 0, st, p); break;
             case 3: hipLaunchKernelGGL(k_dec_conv_win<3>, grid, dim3(256), 0, st, p); break;
             case 2: hipLaunchKernelGGL(k_dec_conv_win<2>, grid, dim3(256), 0, st, p); break;
             default: hipLaunchKernelGGL(k_dec_conv_win<1>, grid, dim3(256), 0, st, p); break;
