@@ -19,7 +19,8 @@
 //                 of a transposed convolution, linear layers as one tap;
 //                 fused epilogues; k_dec_conv_win for convolutions of 3+
 //                 taps (the input window split once into LDS; the variant
-//                 k_dec_conv_win_tw, one channel tile per wave, at 4 tiles),
+//                 k_dec_conv_win_tw, one channel tile per wave, at 3 and 4
+//                 tiles),
 //                 k_dec_conv_mfma_ks for launches too small to fill the GPU
 //  k_dec_absmax   max |x| of a layer input (the operand scale)
 #include <hip/hip_runtime.h>
@@ -625,18 +626,19 @@ __global__ __launch_bounds__(256) void k_dec_conv_mfma_ks(DecConvMfmaParams P) {
 // channels, the block's window -- positions n0 - (ksize - 1) * dilation ..
 // n0 + 127 of those channels -- is loaded once (thread t: position t, the
 // 16 channels' values, each load coalesced over the threads), scaled by 2^ex
-// and split into binary16 hi + lo, and stored position-major ([position][16
-// channels], one 32-byte row per thread), so every tap's B operand is two
-// 16-byte LDS reads at position n - n0 + tap * dilation: each value is split
-// once instead of once per tap.  The next channel block's window is loaded
-// into registers during the current block's taps (double-buffered, one
-// barrier per channel block); A operands come from global memory one step
-// ahead.  Same operand order and products as k_dec_conv_mfma.
+// and split into binary16 hi + lo, and stored position-major per half of the
+// channels ([8-channel half][position][8 channels], 16-byte rows, so the 16
+// lanes of a 16-byte LDS read hit 16 consecutive rows: no bank conflicts),
+// and every tap's B operand is two 16-byte LDS reads at position n - n0 +
+// tap * dilation: each value is split once instead of once per tap.  The
+// next channel block's window is loaded into registers during the current
+// block's taps (double-buffered, one barrier per channel block); A operands
+// come from global memory one step ahead.  Same operand order and products as k_dec_conv_mfma.
 template <int MT>
 __global__ __launch_bounds__(256) void k_dec_conv_win(DecConvMfmaParams P) {
     static_assert(kDecMaxSlots == 64, "one max slot per lane");
     constexpr int WMAX = 256;  // window positions: 128 + (ksize - 1) * dilation <= the block's threads
-    __shared__ __align__(16) _Float16 wh_s[2][WMAX][16], wl_s[2][WMAX][16];
+    __shared__ __align__(16) _Float16 wh_s[2][2][WMAX][8], wl_s[2][2][WMAX][8];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 31, half = lane >> 5;
     const int n0 = blockIdx.x * 128, n = n0 + wave * 32 + col;
@@ -665,10 +667,10 @@ __global__ __launch_bounds__(256) void k_dec_conv_win(DecConvMfmaParams P) {
             h[c >> 3][c & 7] = hv;
             l[c >> 3][c & 7] = (_Float16)(x - (float)hv);
         }
-        *reinterpret_cast<half8 *>(&wh_s[buf][tid][0]) = h[0];
-        *reinterpret_cast<half8 *>(&wh_s[buf][tid][8]) = h[1];
-        *reinterpret_cast<half8 *>(&wl_s[buf][tid][0]) = l[0];
-        *reinterpret_cast<half8 *>(&wl_s[buf][tid][8]) = l[1];
+        *reinterpret_cast<half8 *>(&wh_s[buf][0][tid][0]) = h[0];
+        *reinterpret_cast<half8 *>(&wh_s[buf][1][tid][0]) = h[1];
+        *reinterpret_cast<half8 *>(&wl_s[buf][0][tid][0]) = l[0];
+        *reinterpret_cast<half8 *>(&wl_s[buf][1][tid][0]) = l[1];
     };
     auto load_a = [&](int s, half8 (&ah)[MT], half8 (&al)[MT]) {
 #pragma unroll
@@ -699,8 +701,8 @@ __global__ __launch_bounds__(256) void k_dec_conv_win(DecConvMfmaParams P) {
             half8 nh[MT], nl[MT];
             load_a(s + 1 < nsteps ? s + 1 : s, nh, nl);
             const int p = wave * 32 + col + tap * dil;
-            const half8 bh = *reinterpret_cast<const half8 *>(&wh_s[buf][p][8 * half]);
-            const half8 bl = *reinterpret_cast<const half8 *>(&wl_s[buf][p][8 * half]);
+            const half8 bh = *reinterpret_cast<const half8 *>(&wh_s[buf][half][p][0]);
+            const half8 bl = *reinterpret_cast<const half8 *>(&wl_s[buf][half][p][0]);
 #pragma unroll
             for (int t = 0; t < MT; t++) {
                 acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah[t], bh, acc[t], 0, 0, 0);
@@ -741,49 +743,62 @@ __global__ __launch_bounds__(256) void k_dec_conv_win(DecConvMfmaParams P) {
         }
 }
 
-// k_dec_conv_win with the waves' roles swapped, for 4 channel tiles per
-// block: wave w owns channel tile 4 * blockIdx.y + w -- its A operands
-// loaded by it alone, where every wave of k_dec_conv_win<4> loads all four
-// tiles' -- and all four 32-position tiles of the block, whose B operands it
-// reads from the staged window (LDS, twice L1's bandwidth).  Per step a CU
-// then reads 8 KiB of A operands through L1 instead of 32 KiB.  Same window,
-// operands and product order per output as k_dec_conv_win: the same bits.
-__global__ __launch_bounds__(256) void k_dec_conv_win_tw(DecConvMfmaParams P) {
+// k_dec_conv_win with the waves' roles swapped, for NW (3 or 4) channel
+// tiles per block of NW waves: wave w owns channel tile NW * blockIdx.y + w
+// -- its A operands loaded by it alone, where every wave of
+// k_dec_conv_win<MT> loads all MT tiles' -- and all four 32-position tiles
+// of the block, whose B operands it reads from the staged window (LDS,
+// twice L1's bandwidth).  Per step a block reads NW * 2 KiB of A operands
+// through L1 instead of 4 * NW * 2 KiB.  The window (up to 256 positions)
+// is staged by the block's 64 * NW threads, position t + 64 * NW * q by
+// thread t in pass q.  Same window, operands and product order per output
+// as k_dec_conv_win: the same bits.
+template <int NW>
+__global__ __launch_bounds__(64 * NW) void k_dec_conv_win_tw(DecConvMfmaParams P) {
     static_assert(kDecMaxSlots == 64, "one max slot per lane");
     constexpr int WMAX = 256, PT = 4;  // window positions; 32-position tiles per block
-    __shared__ __align__(16) _Float16 wh_s[2][WMAX][16], wl_s[2][WMAX][16];
+    constexpr int NT = 64 * NW, NP = (WMAX + NT - 1) / NT;  // threads; staging passes
+    __shared__ __align__(16) _Float16 wh_s[2][2][WMAX][8], wl_s[2][2][WMAX][8];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int col = lane & 31, half = lane >> 5;
     const int n0 = blockIdx.x * 128;
-    const int tile = blockIdx.y * 4 + wave;  // < mtiles (the grid has mtiles / 4 rows)
+    const int tile = blockIdx.y * NW + wave;  // < mtiles (the grid has mtiles / NW rows)
     const int len = P.len, ks = P.ksize, dil = P.dilation, ksteps = P.ksteps;
     const bool multi = P.nphase > 1;  // uniform
     const _Float16 *wh = multi ? P.ph_wh[blockIdx.z] : P.wh, *wl = multi ? P.ph_wl[blockIdx.z] : P.wl;
     const int phase = multi ? (int)blockIdx.z : P.phase;
-    const int W = 128 + (ks - 1) * dil, wpos = n0 - (ks - 1) * dil + tid;  // this thread's window position
-    const bool wok = tid < W && wpos >= 0 && wpos < len;
+    const int W = 128 + (ks - 1) * dil;  // window positions n0 - (ks - 1) * dil .. n0 + 127
     const int ncb = P.cin16 / 16;
     const int ex = split_exponent(wave_max(__uint_as_float(P.xmax[lane])));
     const float xs = ldexpf(1.0f, ex);
-    auto load_win = [&](int cb, float (&v)[16]) {
-        const float *xp = P.x + (size_t)(16 * cb) * len + (wok ? wpos : 0);
+    auto load_win = [&](int cb, float (&v)[NP][16]) {
 #pragma unroll
-        for (int c = 0; c < 16; c++) v[c] = wok && 16 * cb + c < P.cin ? xp[(size_t)c * len] : 0.0f;
-    };
-    auto store_win = [&](int buf, const float (&v)[16]) {
-        if (tid >= W) return;
-        half8 h[2], l[2];
+        for (int q = 0; q < NP; q++) {
+            const int wi = tid + q * NT, wpos = n0 - (ks - 1) * dil + wi;
+            const bool wok = wi < W && wpos >= 0 && wpos < len;
+            const float *xp = P.x + (size_t)(16 * cb) * len + (wok ? wpos : 0);
 #pragma unroll
-        for (int c = 0; c < 16; c++) {
-            const float x = v[c] * xs;
-            const _Float16 hv = (_Float16)x;
-            h[c >> 3][c & 7] = hv;
-            l[c >> 3][c & 7] = (_Float16)(x - (float)hv);
+            for (int c = 0; c < 16; c++) v[q][c] = wok && 16 * cb + c < P.cin ? xp[(size_t)c * len] : 0.0f;
         }
-        *reinterpret_cast<half8 *>(&wh_s[buf][tid][0]) = h[0];
-        *reinterpret_cast<half8 *>(&wh_s[buf][tid][8]) = h[1];
-        *reinterpret_cast<half8 *>(&wl_s[buf][tid][0]) = l[0];
-        *reinterpret_cast<half8 *>(&wl_s[buf][tid][8]) = l[1];
+    };
+    auto store_win = [&](int buf, const float (&v)[NP][16]) {
+#pragma unroll
+        for (int q = 0; q < NP; q++) {
+            const int wi = tid + q * NT;
+            if (wi >= W) continue;
+            half8 h[2], l[2];
+#pragma unroll
+            for (int c = 0; c < 16; c++) {
+                const float x = v[q][c] * xs;
+                const _Float16 hv = (_Float16)x;
+                h[c >> 3][c & 7] = hv;
+                l[c >> 3][c & 7] = (_Float16)(x - (float)hv);
+            }
+            *reinterpret_cast<half8 *>(&wh_s[buf][0][wi][0]) = h[0];
+            *reinterpret_cast<half8 *>(&wh_s[buf][1][wi][0]) = h[1];
+            *reinterpret_cast<half8 *>(&wl_s[buf][0][wi][0]) = l[0];
+            *reinterpret_cast<half8 *>(&wl_s[buf][1][wi][0]) = l[1];
+        }
     };
     auto load_a = [&](int s, half8 &ah, half8 &al) {
         const size_t o = ((size_t)tile * ksteps + s) * 64 + lane;
@@ -795,7 +810,7 @@ __global__ __launch_bounds__(256) void k_dec_conv_win_tw(DecConvMfmaParams P) {
     for (int t = 0; t < PT; t++)
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[t][r] = 0.0f;
-    float wv[16];
+    float wv[NP][16];
     load_win(0, wv);
     store_win(0, wv);
     half8 ah, al;
@@ -813,8 +828,8 @@ __global__ __launch_bounds__(256) void k_dec_conv_win_tw(DecConvMfmaParams P) {
 #pragma unroll
             for (int t = 0; t < PT; t++) {
                 const int p = t * 32 + col + tap * dil;
-                const half8 bh = *reinterpret_cast<const half8 *>(&wh_s[buf][p][8 * half]);
-                const half8 bl = *reinterpret_cast<const half8 *>(&wl_s[buf][p][8 * half]);
+                const half8 bh = *reinterpret_cast<const half8 *>(&wh_s[buf][half][p][0]);
+                const half8 bl = *reinterpret_cast<const half8 *>(&wl_s[buf][half][p][0]);
                 acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bh, acc[t], 0, 0, 0);
                 acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(ah, bl, acc[t], 0, 0, 0);
                 acc[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(al, bh, acc[t], 0, 0, 0);
@@ -957,8 +972,8 @@ void launch_dec_conv_mfma(hipStream_t st, const DecConvMfmaParams &p) {
         // a channel-first convolution with 3 or more taps whose window fits the block's threads
         const dim3 grid(blocks_for((size_t)p.len, 128), (unsigned)(p.mtiles / mt), (unsigned)nph);
         switch (mt) {
-            case 4: hipLaunchKernelGGL(k_dec_conv_win_tw, grid, dim3(256), 0, st, p); break;
-            case 3: hipLaunchKernelGGL(k_dec_conv_win<3>, grid, dim3(256), 0, st, p); break;
+            case 4: hipLaunchKernelGGL(k_dec_conv_win_tw<4>, grid, dim3(256), 0, st, p); break;
+            case 3: hipLaunchKernelGGL(k_dec_conv_win_tw<3>, grid, dim3(192), 0, st, p); break;
             case 2: hipLaunchKernelGGL(k_dec_conv_win<2>, grid, dim3(256), 0, st, p); break;
             default: hipLaunchKernelGGL(k_dec_conv_win<1>, grid, dim3(256), 0, st, p); break;
         }
