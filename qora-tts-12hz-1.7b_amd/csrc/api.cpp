@@ -3495,13 +3495,18 @@ qtts_status dec_decode(qtts_decoder *d, const uint32_t *d_codes, int T, int ld, 
         QTTS_TRY(dec_causal_mfma(d, w.vocos_init, d->vocos_init, sig, mx, L, o, DEC_EPI_STORE));
         sig = o;
     }
+    // a residual unit's conv2 output still to be added to sig: the SnakeBeta
+    // that next reads sig adds it and stores the sum (faster than the conv2
+    // epilogue reading each residual), the same f32 addition
+    float *pend = nullptr;
     for (size_t bi = 0; bi < d->blocks.size(); bi++) {
         const qtts_vocos_block_view &b = d->blocks[bi];
         const int cin = b.upsample.in_channels, cout = b.upsample.out_channels;
         float *t1 = other(sig), *nxt = other(sig, t1);
         unsigned *m0 = take();
         if (!m0) return fail(c, QTTS_EDEVICE, "decoder: more matrix-core inputs than max slots");
-        launch_dec_snake(st, sig, b.pre_snake_alpha, b.pre_snake_beta, cin, L, t1, m0);
+        launch_dec_snake(st, sig, b.pre_snake_alpha, b.pre_snake_beta, cin, L, t1, m0, pend, pend ? sig : nullptr);
+        pend = nullptr;
         QTTS_TRY(check_launch(c, "k_dec_snake"));
         QTTS_TRY(dec_transposed_mfma(d, b.upsample, d->up_mfma[bi], t1, m0, L, nxt));
         L *= b.upsample.stride;
@@ -3512,20 +3517,23 @@ qtts_status dec_decode(qtts_decoder *d, const uint32_t *d_codes, int T, int ld, 
             const std::array<DecConvMfma, 2> &mc = d->res_mfma[bi][(size_t)r];
             unsigned *m1 = take(), *m2 = take();
             if (!m1 || !m2) return fail(c, QTTS_EDEVICE, "decoder: more matrix-core inputs than max slots");
-            launch_dec_snake(st, sig, rv.act1_alpha, rv.act1_beta, cout, L, t1, m1);
+            launch_dec_snake(st, sig, rv.act1_alpha, rv.act1_beta, cout, L, t1, m1, pend, pend ? sig : nullptr);
+            pend = nullptr;
             QTTS_TRY(check_launch(c, "k_dec_snake"));
             QTTS_TRY(dec_causal_mfma(d, rv.conv1, mc[0], t1, m1, L, t2, DEC_EPI_STORE));
             launch_dec_snake(st, t2, rv.act2_alpha, rv.act2_beta, cout, L, t1, m2);
             QTTS_TRY(check_launch(c, "k_dec_snake"));
-            // signal = conv2 + residual, in place (each output reads its own residual first)
-            QTTS_TRY(dec_causal_mfma(d, rv.conv2, mc[1], t1, m2, L, sig, DEC_EPI_RESID_IN, sig));
+            // signal = residual + conv2: conv2 into t2, added by the next SnakeBeta
+            QTTS_TRY(dec_causal_mfma(d, rv.conv2, mc[1], t1, m2, L, t2, DEC_EPI_STORE));
+            pend = t2;
         }
     }
     float *t1 = other(sig);
     // 6. final SnakeBeta, output conv, clamp to [-1, 1]
     unsigned *mf = take();
     if (!mf) return fail(c, QTTS_EDEVICE, "decoder: more matrix-core inputs than max slots");
-    launch_dec_snake(st, sig, w.final_snake_alpha, w.final_snake_beta, w.output_conv.in_channels, L, t1, mf);
+    launch_dec_snake(st, sig, w.final_snake_alpha, w.final_snake_beta, w.output_conv.in_channels, L, t1, mf, pend,
+                     pend ? sig : nullptr);
     QTTS_TRY(check_launch(c, "k_dec_snake"));
     QTTS_TRY(dec_causal_mfma(d, w.output_conv, d->out_conv, t1, mf, L, d_audio, DEC_EPI_CLAMP));
     *n_samples = (int64_t)L * w.output_conv.out_channels;

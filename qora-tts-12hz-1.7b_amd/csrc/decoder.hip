@@ -252,6 +252,9 @@ __global__ __launch_bounds__(256) void k_dec_lnorm_tile(const float *x, const fl
     }
 }
 
+// With add set, the input is x + add, stored to sum (which may be x: each
+// element is read before it is written, by the same thread) before the
+// activation: a residual sum made where it is next read.
 // x + exp(-beta) * sin(exp(alpha) * x)^2 per channel, channel-first: block
 // row y is channel y (its two exponentials computed once per thread, no
 // division per element), and the blocks of a row stride through its
@@ -261,7 +264,7 @@ __global__ __launch_bounds__(256) void k_dec_lnorm_tile(const float *x, const fl
 // maximum does not depend on the order of the blocks, and 64 slots keep the
 // atomics from queueing on one address.
 __global__ __launch_bounds__(256) void k_dec_snake(const float *x, const float *alpha, const float *beta, int ch,
-                                                   int len, float *out, unsigned *amax) {
+                                                   int len, float *out, unsigned *amax, const float *add, float *sum) {
     const int c = blockIdx.y;
     const float a = expf(alpha[c]), inv_b = expf(-beta[c]);
     const size_t base = (size_t)c * len;
@@ -278,19 +281,37 @@ __global__ __launch_bounds__(256) void k_dec_snake(const float *x, const float *
         // loads and stores, two in flight per thread
         const float4 *x4 = reinterpret_cast<const float4 *>(x + base);
         float4 *o4 = reinterpret_cast<float4 *>(out + base);
+        const float4 *a4 = reinterpret_cast<const float4 *>(add + base);
+        float4 *s4 = reinterpret_cast<float4 *>(sum + base);
+        auto in = [&](int i) {  // x, or x + add stored to sum first
+            float4 v = x4[i];
+            if (add) {
+                const float4 d = a4[i];
+                v = make_float4(v.x + d.x, v.y + d.y, v.z + d.z, v.w + d.w);
+                s4[i] = v;
+            }
+            return v;
+        };
         const int n4 = len >> 2;
         int t = blockIdx.x * blockDim.x + threadIdx.x;
         for (; t + stride < n4; t += 2 * stride) {
-            const float4 v0 = x4[t], v1 = x4[t + stride];
+            const float4 v0 = in(t), v1 = in(t + stride);
             o4[t] = make_float4(snake(v0.x), snake(v0.y), snake(v0.z), snake(v0.w));
             o4[t + stride] = make_float4(snake(v1.x), snake(v1.y), snake(v1.z), snake(v1.w));
         }
         if (t < n4) {
-            const float4 v0 = x4[t];
+            const float4 v0 = in(t);
             o4[t] = make_float4(snake(v0.x), snake(v0.y), snake(v0.z), snake(v0.w));
         }
     } else {
-        for (int t = blockIdx.x * blockDim.x + threadIdx.x; t < len; t += stride) out[base + t] = snake(x[base + t]);
+        for (int t = blockIdx.x * blockDim.x + threadIdx.x; t < len; t += stride) {
+            float v = x[base + t];
+            if (add) {
+                v += add[base + t];
+                sum[base + t] = v;
+            }
+            out[base + t] = snake(v);
+        }
     }
     if (!amax) return;  // uniform
     __shared__ float red[4];
@@ -915,12 +936,13 @@ void launch_dec_lnorm(hipStream_t st, const float *x, const float *g, const floa
 }
 
 void launch_dec_snake(hipStream_t st, const float *x, const float *alpha, const float *beta, int ch, int len,
-                      float *out, unsigned *amax) {
+                      float *out, unsigned *amax, const float *add, float *sum) {
     // about kSnakeBlocks blocks in all, at least one per channel (rows of a
     // multiple of 4 samples take 4 per thread and iteration)
     const size_t items = (len & 3) == 0 ? (size_t)len / 4 : (size_t)len;
     const unsigned per_row = std::max(1u, std::min<unsigned>(blocks_for(items, 256), kSnakeBlocks / (unsigned)ch));
-    hipLaunchKernelGGL(k_dec_snake, dim3(per_row, (unsigned)ch), dim3(256), 0, st, x, alpha, beta, ch, len, out, amax);
+    hipLaunchKernelGGL(k_dec_snake, dim3(per_row, (unsigned)ch), dim3(256), 0, st, x, alpha, beta, ch, len, out, amax,
+                       add, sum);
 }
 
 void launch_dec_fill_u32(hipStream_t st, unsigned *p, int n, unsigned v) {

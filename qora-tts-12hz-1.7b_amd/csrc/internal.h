@@ -341,7 +341,7 @@ void launch_dec_dwconv(hipStream_t st, const float *x, const float *w, const flo
 void launch_dec_lnorm(hipStream_t st, const float *x, const float *g, const float *b, int ch, int len, float eps,
                       float *out);
 void launch_dec_snake(hipStream_t st, const float *x, const float *alpha, const float *beta, int ch, int len,
-                      float *out, unsigned *amax = nullptr);
+                      float *out, unsigned *amax = nullptr, const float *add = nullptr, float *sum = nullptr);
 void launch_dec_fill_u32(hipStream_t st, unsigned *p, int n, unsigned v);
 void launch_dec_absmax(hipStream_t st, const float *x, size_t n, unsigned *amax);
 void launch_dec_conv_repack(hipStream_t st, const float *w, long long sm, long long sci, int k0, int kd, int M, int cin,
